@@ -1,0 +1,221 @@
+"""Benchmark: Qwen2.5-7B-shape batch-1 decode GEMV pass on one MI355X.
+
+One step = the exact group-128 int8 GEMVs of one 7B decode token over distinct weights resident in
+HBM: 28 layers x {q|k|v (4608 x 3584), o (3584 x 3584), gate|up (37888 x 3584), down (3584 x 18944)}
+plus lm_head (152064 x 3584) = 7.07 GB of int8 weights + 0.11 GB of int16 scales, x int8 uniform in
+[-127, 127] (A8), int64 outputs, captured in one HIP graph. value = steps per second (tok/s).
+Also reported: the pass's HBM rate, per-shape GEMV rates (HIP events on the launch stream), the
+prefill GEMM rate (M = 2048, K = 3584 -> N = 18944 and K = 18944 -> N = 3584) and the numpy oracle
+timed on the host cores as the CPU baseline.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "exact-llm_amd"))
+
+METRIC = "decode tok/s (7B-shape, bs1); GEMV HBM GB/s; prefill int8 MFMA TOPS"
+HBM_PEAK_GBPS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+
+def gemv_pass(args):
+    import numpy as np
+    import torch
+    from exact_amd import ops, synth
+    from exact_amd.ops import I8, I64, PackedLinear
+
+    cfg = synth.CONFIGS["qwen2.5-7b"]
+    dev = "cuda"
+    D, I, NL = cfg.D, cfg.I, cfg.NL
+    nqkv = (cfg.H + 2 * cfg.KV) * cfg.hd
+    thr = torch.tensor(synth.thresholds().astype(np.int64)).to(torch.int32).to(dev)
+    seed = 7
+
+    def lin(name, N, K):
+        wp, mp = PackedLinear.alloc(N, K, dev)
+        ops.synth_linear(wp, mp, N, K, synth.key(seed, name + ".w"), synth.key(seed, name + ".m"), synth.M_LO, synth.M_HI, thr)
+        return PackedLinear(wp, mp, N, K)
+
+    shapes = {"qkv": (nqkv, D), "o": (D, cfg.H * cfg.hd), "gateup": (2 * I, D), "down": (D, I)}
+    layers = [{k: lin(f"L{li}.{k}", *v) for k, v in shapes.items()} for li in range(NL)]
+    head = lin("head", cfg.V, D)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    x_d = torch.randint(-127, 128, (1, D), generator=g, dtype=torch.int8).to(dev)
+    x_i = torch.randint(-127, 128, (1, I), generator=g, dtype=torch.int8).to(dev)
+    x_a = torch.randint(-127, 128, (1, cfg.H * cfg.hd), generator=g, dtype=torch.int8).to(dev)
+    xin = {"qkv": x_d, "o": x_a, "gateup": x_d, "down": x_i}
+    outs = {k: torch.zeros((1, v[0]), dtype=I64, device=dev) for k, v in shapes.items()}
+    out_head = torch.zeros((1, cfg.V), dtype=I64, device=dev)
+
+    def nbytes(N, K, R=1):
+        return N * K + N * (K // 128) * 2 + R * K + R * N * 8
+
+    pass_bytes = sum(nbytes(*shapes[k]) for k in shapes) * NL + nbytes(cfg.V, D)
+
+    def step():
+        for L in layers:
+            for k in shapes:
+                ops.gemv_g128(xin[k], 7, L[k], outs[k])
+        ops.gemv_g128(x_d, 7, head, out_head)
+
+    torch.cuda.synchronize()
+    step()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(args.steps):
+        graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+
+    # per-shape launch durations: events around NL launches over distinct weights (no cache reuse)
+    per = {}
+    for k, (N, K) in list(shapes.items()) + [("head", (cfg.V, D))]:
+        reps = 3
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(st)
+        for _ in range(reps):
+            if k == "head":
+                ops.gemv_g128(x_d, 7, head, out_head)
+            else:
+                for L in layers:
+                    ops.gemv_g128(xin[k], 7, L[k], outs[k])
+        b.record(st)
+        torch.cuda.synchronize()
+        n = reps * (1 if k == "head" else NL)
+        us = a.elapsed_time(b) * 1000.0 / n
+        per[k] = dict(N=N, K=K, us=round(us, 2), GBps=round(nbytes(N, K) / us / 1e3, 1))
+    del layers, head
+    torch.cuda.empty_cache()
+    return dict(ms=ms, wall=wall, pass_bytes=pass_bytes, per=per)
+
+
+def prefill_gemm(args):
+    import torch
+    import numpy as np
+    from exact_amd import ops, synth
+    from exact_amd.ops import PackedLinear
+    dev = "cuda"
+    thr = torch.tensor(synth.thresholds().astype(np.int64)).to(torch.int32).to(dev)
+    res = {}
+    for name, (M, K, N) in {"gateup_K3584_N18944": (2048, 3584, 18944), "down_K18944_N3584": (2048, 18944, 3584)}.items():
+        wp, mp = PackedLinear.alloc(N, K, dev)
+        ops.synth_linear(wp, mp, N, K, synth.key(9, name + ".w"), synth.key(9, name + ".m"), synth.M_LO, synth.M_HI, thr)
+        lin = PackedLinear(wp, mp, N, K)
+        x = torch.randint(-127, 128, (M, K), dtype=torch.int8).to(dev)
+        out = torch.empty((M, N), dtype=torch.int64, device=dev)
+        ops.gemm_g128(x, 7, lin, out)
+        torch.cuda.synchronize()
+        st = torch.cuda.current_stream()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 3
+        a.record(st)
+        for _ in range(reps):
+            ops.gemm_g128(x, 7, lin, out)
+        b.record(st)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1000.0 / reps
+        res[name] = dict(us=round(us, 1), TOPS=round(2.0 * M * K * N / us / 1e6, 2))
+        del wp, mp, lin, x, out
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline():
+    """The oracle's group-128 linear (float64 BLAS per group + int64 rescale, the reference's CPU
+    algorithm) on one 7B layer's GEMVs + the head, bs1 A8, timed on this host; extrapolated to a token."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import exact_oracle as O
+    rng = np.random.default_rng(0)
+    shapes = {"q": (3584, 3584), "k": (512, 3584), "v": (512, 3584), "o": (3584, 3584), "gate": (18944, 3584),
+              "up": (18944, 3584), "down": (3584, 18944)}
+    t_layer = 0.0
+    for name, (N, K) in shapes.items():
+        w = rng.integers(-127, 128, (K, N), dtype=np.int8)
+        M = rng.integers(8192, 24576, (K // 128, N))
+        x = rng.integers(-127, 128, (1, K))
+        t0 = time.perf_counter()
+        O.linear_group_t(x, w, M, abits=7)
+        t_layer += time.perf_counter() - t0
+    N, K = 152064, 3584
+    w = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    M = rng.integers(8192, 24576, (K // 128, N))
+    x = rng.integers(-127, 128, (1, K))
+    t0 = time.perf_counter()
+    O.linear_group_t(x, w, M, abits=7)
+    t_head = time.perf_counter() - t0
+    tok_s = 1.0 / (28 * t_layer + t_head)
+    return {"value": round(tok_s, 4), "unit": "tok/s", "cores": os.cpu_count(), "kind": "port",
+            "sample": f"one 7B layer's 7 GEMVs ({t_layer:.2f} s) + lm_head ({t_head:.2f} s), bs1 A8, numpy oracle "
+                      "(float64 BLAS per group), extrapolated as 28 layers + head"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build runs the exact path on a single MI355X; "
+              "multi-GPU runs are not part of it (see DESIGN.md for how the path would shard).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    import exact_amd
+    exact_amd.load()
+    r = gemv_pass(args)
+    pre = {} if args.no_prefill else prefill_gemm(args)
+    cpu = None if args.no_cpu else cpu_baseline()
+    tok_s = 1000.0 / r["ms"]
+    pass_gbps = r["pass_bytes"] / (r["ms"] * 1e-3) / 1e9
+    dom = r["per"]["gateup"]
+    line = {
+        "metric": METRIC, "value": round(tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(r["ms"], 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "Qwen2.5-7B-shape bs1 decode GEMV pass: 28 x (q|k|v 4608x3584, o 3584x3584, "
+                               "gate|up 37888x3584, down 3584x18944) + lm_head 152064x3584, group-128 int16 scales, "
+                               "A8 x, int64 outputs, one HIP graph", "batch": 1, "abits": 7,
+                   "weights_GB": round(r["pass_bytes"] / 1e9, 3), "parallelism": "single GPU"},
+        "gemv_GBps": round(pass_gbps, 1),
+        "gemv_per_shape": r["per"],
+        "prefill_gemm": pre,
+        "prefill_TOPS": (round(min(v["TOPS"] for v in pre.values()), 2) if pre else None),
+        "roofline": {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(dom["GBps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "k_gemv_g128<7> on gate|up 37888x3584 (136 MB per launch)"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,153 @@
+// q/k/v epilogue with RoPE and KV-cache write, and exact integer attention.
+//
+// KV cache per layer: kq int16 [B][KV][Smax][hd] (qrow(k, 15) per position, exact_torch.py:147),
+// sk int32 [B][KV][Smax] (the per-position shifts), v int64 [B][KV][Smax][hd] (Q16, unquantised,
+// SPEC.md:24). Positions beyond pos[r] are never read, which equals the reference's masked static
+// cache (speed_fair_kaggle.py:588-589,611: masked slots get probability exactly 0).
+#include "exact_common.h"
+#include "abi_util.h"
+
+namespace exact {
+
+// grid (R, H + 2*KV), block 64 (one wave per head slot), hd <= 256
+__global__ void k_qkv_rope_cache(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
+                                 const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
+                                 const int64_t* __restrict__ sin_t, const int32_t* __restrict__ slot,
+                                 const int32_t* __restrict__ pos, int16_t* __restrict__ qq, int32_t* __restrict__ sq,
+                                 int16_t* __restrict__ kq, int32_t* __restrict__ sk, int64_t* __restrict__ v, int H,
+                                 int KV, int hd, int Smax) {
+  __shared__ int64_t y[256];
+  const int r = blockIdx.x, hs = blockIdx.y, lane = threadIdx.x;
+  const int N = (H + 2 * KV) * hd;
+  const int sh = 28 - s[r];
+  const int p = pos[r], sl = slot[r];
+  if (p < 0 || p >= Smax) return;   // the host keeps positions inside the cache; never write outside it
+  const int base = hs * hd;   // q heads, then k heads, then v heads, each hd wide
+  for (int j = lane; j < hd; j += 64) {
+    const int64_t val = shr64(t[(int64_t)r * N + base + j], sh);
+    y[j] = b ? val + b[base + j] : val;
+  }
+  __syncthreads();
+  if (hs >= H + KV) {   // v: stored unquantised
+    const int kh = hs - H - KV;
+    int64_t* dst = v + (((int64_t)sl * KV + kh) * Smax + p) * hd;
+    for (int j = lane; j < hd; j += 64) dst[j] = y[j];
+    return;
+  }
+  const int half = hd >> 1;
+  int64_t z[4];
+  int64_t m = 0;
+  int nz = 0;
+  for (int j = lane; j < hd; j += 64, ++nz) {
+    const int64_t rot = j < half ? -y[j + half] : y[j - half];
+    const int64_t val = shr64(y[j] * cos_t[(int64_t)p * hd + j] + rot * sin_t[(int64_t)p * hd + j], EXACT_F);
+    z[nz] = val;
+    const int64_t a = abs64(val);
+    m = a > m ? a : m;
+  }
+  m = wave_max64(m);
+  int q = bitlen64(m) - 15;
+  if (q < 0) q = 0;
+  nz = 0;
+  if (hs < H) {
+    int16_t* dst = qq + ((int64_t)r * H + hs) * hd;
+    for (int j = lane; j < hd; j += 64, ++nz) {
+      int64_t w = shr64(z[nz], q);
+      dst[j] = (int16_t)(w > 32767 ? 32767 : (w < -32767 ? -32767 : w));
+    }
+    if (lane == 0) sq[r * H + hs] = q;
+  } else {
+    const int kh = hs - H;
+    const int64_t row = ((int64_t)sl * KV + kh) * Smax + p;
+    int16_t* dst = kq + row * hd;
+    for (int j = lane; j < hd; j += 64, ++nz) {
+      int64_t w = shr64(z[nz], q);
+      dst[j] = (int16_t)(w > 32767 ? 32767 : (w < -32767 ? -32767 : w));
+    }
+    if (lane == 0) sk[row] = q;
+  }
+}
+
+// grid (R, H), block 256. Scores in LDS (Smax entries), then max, exp LUT, sum, Q20 p, and p.V.
+__global__ __launch_bounds__(256) void k_attention(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
+                                                   const int16_t* __restrict__ kq, const int32_t* __restrict__ sk,
+                                                   const int64_t* __restrict__ v, const int32_t* __restrict__ slot,
+                                                   const int32_t* __restrict__ pos, const int32_t* __restrict__ expt,
+                                                   int64_t* __restrict__ out, int H, int KV, int hd, int Smax, int INV) {
+  extern __shared__ int64_t sc[];   // Smax entries
+  __shared__ int32_t qs[256];
+  __shared__ int64_t red[16];
+  __shared__ int64_t part[256];
+  const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int kh = h / (H / KV);
+  const int S = min(pos[r] + 1, Smax), sl = slot[r];
+  const int sqv = sq[r * H + h];
+  for (int j = tid; j < hd; j += blockDim.x) qs[j] = qq[((int64_t)r * H + h) * hd + j];
+  __syncthreads();
+  const int64_t cbase = ((int64_t)sl * KV + kh) * Smax;
+  int64_t mx = INT64_MIN;
+  for (int si = tid; si < S; si += blockDim.x) {
+    const int16_t* kr = kq + (cbase + si) * hd;
+    int64_t dot = 0;
+    for (int j = 0; j < hd; j += 2) {
+      const int32_t kk = *reinterpret_cast<const int32_t*>(kr + j);
+      dot += (int64_t)qs[j] * (int16_t)(kk & 0xffff) + (int64_t)qs[j + 1] * (int16_t)(kk >> 16);
+    }
+    const int64_t val = shr64(dot * INV, 32 - sqv - sk[cbase + si]);
+    sc[si] = val;
+    mx = val > mx ? val : mx;
+  }
+  mx = block_max64(mx, red);
+  int64_t es = 0;
+  for (int si = tid; si < S; si += blockDim.x) {
+    const int64_t e = lut_exp(expt, mx - sc[si]);
+    sc[si] = e;
+    es += e;
+  }
+  es = block_sum64(es, red);
+  for (int si = tid; si < S; si += blockDim.x) sc[si] = floordiv64(shl64(sc[si], 20), es);
+  __syncthreads();
+  // p.V: thread (j, part) sums keys si = part, part + nparts, ...
+  const int nparts = blockDim.x / hd;   // hd divides 256
+  const int j = tid % hd, pp = tid / hd;
+  int64_t a = 0;
+  if (pp < nparts) {
+    const int64_t* vb = v + cbase * hd + j;
+    for (int si = pp; si < S; si += nparts) a = (int64_t)((uint64_t)a + (uint64_t)(sc[si] * vb[(int64_t)si * hd]));
+  }
+  part[tid] = a;
+  __syncthreads();
+  if (tid < hd) {
+    uint64_t tot = 0;
+    for (int k = 0; k < nparts; ++k) tot += (uint64_t)part[k * hd + tid];
+    out[((int64_t)r * H + h) * hd + tid] = shr64((int64_t)tot, 20);
+  }
+}
+
+}  // namespace exact
+
+using namespace exact;
+
+extern "C" int exact_qkv_rope_cache(const int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
+                                    const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* qq, int32_t* sq,
+                                    int16_t* kq, int32_t* sk, int64_t* v, int32_t R, int32_t H, int32_t KV, int32_t hd,
+                                    int32_t Smax, void* stream) {
+  if (!t || !s || !cos_t || !sin_t || !slot || !pos || !qq || !sq || !kq || !sk || !v) return EXACT_E_ARG;
+  if (R <= 0 || H <= 0 || KV <= 0 || H % KV || hd <= 0 || Smax <= 0) return EXACT_E_ARG;
+  if (hd > 256 || hd % 2) return EXACT_E_UNSUPPORTED;
+  hipLaunchKernelGGL(k_qkv_rope_cache, dim3(R, H + 2 * KV), dim3(64), 0, as_stream(stream), t, s, b, cos_t, sin_t, slot,
+                     pos, qq, sq, kq, sk, v, H, KV, hd, Smax);
+  return launch_status("qkv_rope_cache");
+}
+
+extern "C" int exact_attention(const int16_t* qq, const int32_t* sq, const int16_t* kq, const int32_t* sk,
+                               const int64_t* v, const int32_t* slot, const int32_t* pos, const int32_t* exp_t,
+                               int64_t* out, int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t Smax, int32_t INV,
+                               void* stream) {
+  if (!qq || !sq || !kq || !sk || !v || !slot || !pos || !exp_t || !out) return EXACT_E_ARG;
+  if (R <= 0 || H <= 0 || KV <= 0 || H % KV || hd <= 0 || Smax <= 0) return EXACT_E_ARG;
+  if (hd > 256 || 256 % hd || Smax > 8192) return EXACT_E_UNSUPPORTED;
+  hipLaunchKernelGGL(k_attention, dim3(R, H), dim3(256), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot, pos,
+                     exp_t, out, H, KV, hd, Smax, INV);
+  return launch_status("attention");
+}

@@ -1,0 +1,331 @@
+// Integer nonlinearities and epilogues (one workgroup per row where a row reduction is needed).
+// Each kernel restates one step of the reference's numeric program; see exact_common.h for the
+// primitives and exact_hip.h for the reference line each entry point replaces.
+#include "exact_common.h"
+#include "abi_util.h"
+
+namespace exact {
+
+static const char* g_err = "";
+static char g_errbuf[256];
+void set_error(const char* where, hipError_t e) {
+  snprintf(g_errbuf, sizeof(g_errbuf), "%s: %s", where, hipGetErrorString(e));
+  g_err = g_errbuf;
+}
+
+template <typename T>
+__device__ __forceinline__ void store_q(void* xq, int64_t i, int64_t v) {
+  reinterpret_cast<T*>(xq)[i] = (T)v;
+}
+
+// qrow of a row held in `buf` (length K), writes xq / s for row r
+__device__ __forceinline__ void qrow_store(const int64_t* buf, int K, int bits, void* xq, int32_t* s, int r,
+                                           int64_t* red) {
+  int64_t m = 0;
+  for (int i = threadIdx.x; i < K; i += blockDim.x) {
+    const int64_t a = abs64(buf[i]);
+    m = a > m ? a : m;
+  }
+  m = block_max64(m, red);
+  int sh = bitlen64(m) - bits;
+  if (sh < 0) sh = 0;
+  const int64_t lim = (1LL << bits) - 1;
+  for (int i = threadIdx.x; i < K; i += blockDim.x) {
+    int64_t q = shr64(buf[i], sh);
+    q = q > lim ? lim : (q < -lim ? -lim : q);
+    if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * K + i, q);
+    else store_q<int16_t>(xq, (int64_t)r * K + i, q);
+  }
+  if (threadIdx.x == 0) s[r] = sh;
+}
+
+// x (R, K) int64 -> qrow
+__global__ void k_qrow(const int64_t* __restrict__ x, int bits, void* xq, int32_t* s, int K) {
+  extern __shared__ int64_t buf[];
+  __shared__ int64_t red[16];
+  const int r = blockIdx.x;
+  for (int i = threadIdx.x; i < K; i += blockDim.x) buf[i] = x[(int64_t)r * K + i];
+  __syncthreads();
+  qrow_store(buf, K, bits, xq, s, r, red);
+}
+
+// irms of the row in buf (in place): exact_llm.py:100-106
+__device__ void irms_inplace(int64_t* buf, const int64_t* __restrict__ g, int D, int64_t* red) {
+  int64_t m = 0;
+  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+    const int64_t a = abs64(buf[i]);
+    m = a > m ? a : m;
+  }
+  m = block_max64(m, red);
+  int k = bitlen64(m) - 24;
+  if (k < 0) k = 0;
+  int64_t ss = 0;
+  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+    const int64_t xs = shr64(buf[i], k);
+    ss = (int64_t)((uint64_t)ss + (uint64_t)(xs * xs));
+  }
+  ss = block_sum64(ss, red);
+  const int64_t ms = floordiv64(ss, D) + 1;
+  int64_t rt = isqrt64(ms);
+  if (rt < 1) rt = 1;
+  const int64_t den = shl64(rt, k);
+  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+    const int64_t y = floordiv64(shl64(buf[i], EXACT_F), den);
+    buf[i] = shr64(y * g[i], EXACT_F);
+  }
+  __syncthreads();
+}
+
+__global__ void k_irms(const int64_t* __restrict__ x, const int64_t* __restrict__ g, int64_t* __restrict__ y, int D) {
+  extern __shared__ int64_t buf[];
+  __shared__ int64_t red[16];
+  const int r = blockIdx.x;
+  for (int i = threadIdx.x; i < D; i += blockDim.x) buf[i] = x[(int64_t)r * D + i];
+  __syncthreads();
+  irms_inplace(buf, g, D, red);
+  for (int i = threadIdx.x; i < D; i += blockDim.x) y[(int64_t)r * D + i] = buf[i];
+}
+
+__global__ void k_rmsnorm_qrow(int64_t* __restrict__ x, const int64_t* __restrict__ res_t,
+                               const int32_t* __restrict__ res_s, const int64_t* __restrict__ g, int bits, void* xq,
+                               int32_t* s, int D) {
+  extern __shared__ int64_t buf[];
+  __shared__ int64_t red[16];
+  const int r = blockIdx.x;
+  int64_t* xr = x + (int64_t)r * D;
+  if (res_t) {
+    const int sh = 28 - res_s[r];
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {
+      const int64_t v = (int64_t)((uint64_t)xr[i] + (uint64_t)shr64(res_t[(int64_t)r * D + i], sh));
+      buf[i] = v;
+      xr[i] = v;
+    }
+  } else {
+    for (int i = threadIdx.x; i < D; i += blockDim.x) buf[i] = xr[i];
+  }
+  __syncthreads();
+  irms_inplace(buf, g, D, red);
+  qrow_store(buf, D, bits, xq, s, r, red);
+}
+
+// gate|up total -> h = shr(isilu(g) * u, 16) (stored over the gate half) -> qrow
+__global__ void k_swiglu_qrow(int64_t* __restrict__ t, const int32_t* __restrict__ s, const int32_t* __restrict__ silu,
+                              int bits, void* xq, int32_t* sq, int I) {
+  __shared__ int64_t red[16];
+  const int r = blockIdx.x;
+  int64_t* tr = t + (int64_t)r * 2 * I;
+  const int sh = 28 - s[r];
+  int64_t m = 0;
+  for (int i = threadIdx.x; i < I; i += blockDim.x) {
+    const int64_t gv = shr64(tr[i], sh), uv = shr64(tr[I + i], sh);
+    const int64_t hv = shr64(lut16(silu, gv, false) * uv, EXACT_F);
+    tr[i] = hv;
+    const int64_t a = abs64(hv);
+    m = a > m ? a : m;
+  }
+  m = block_max64(m, red);
+  int q = bitlen64(m) - bits;
+  if (q < 0) q = 0;
+  const int64_t lim = (1LL << bits) - 1;
+  for (int i = threadIdx.x; i < I; i += blockDim.x) {
+    int64_t v = shr64(tr[i], q);
+    v = v > lim ? lim : (v < -lim ? -lim : v);
+    if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * I + i, v);
+    else store_q<int16_t>(xq, (int64_t)r * I + i, v);
+  }
+  if (threadIdx.x == 0) sq[r] = q;
+}
+
+__global__ void k_requant_group(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
+                                const int64_t* __restrict__ b, int64_t* __restrict__ y, int R, int N) {
+  const int64_t total = (int64_t)R * N;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int r = (int)(i / N);
+    const int n = (int)(i - (int64_t)r * N);
+    const int64_t v = shr64(t[i], 28 - s[r]);
+    y[i] = b ? v + b[n] : v;
+  }
+}
+
+__global__ void k_requant_channel(const int64_t* acc, const int32_t* __restrict__ s, const int64_t* __restrict__ M,
+                                  int Mbits, const int64_t* __restrict__ b, int64_t* y, int N) {
+  __shared__ int64_t red[16];
+  const int r = blockIdx.x;
+  const int64_t* ar = acc + (int64_t)r * N;
+  int64_t m = 0;
+  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+    const int64_t a = abs64(ar[i]);
+    m = a > m ? a : m;
+  }
+  m = block_max64(m, red);
+  int drop = bitlen64(m) + Mbits - 62;
+  if (drop < 0) drop = 0;
+  const int sh = 28 - s[r] - drop;
+  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+    const int64_t v = shr64(shr64(ar[i], drop) * M[i], sh);
+    y[(int64_t)r * N + i] = b ? v + b[i] : v;
+  }
+}
+
+__global__ void k_lut(const int64_t* __restrict__ x, const int32_t* __restrict__ T, int64_t* __restrict__ y, int64_t n,
+                      int sig) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    y[i] = lut16(T, x[i], sig != 0);
+}
+
+__global__ void k_isoftmax(const int64_t* __restrict__ sc, const int32_t* __restrict__ n_valid,
+                           const int32_t* __restrict__ T, int64_t* __restrict__ p, int N) {
+  __shared__ int64_t red[16];
+  const int r = blockIdx.x;
+  const int nv = n_valid ? n_valid[r] : N;
+  const int64_t* row = sc + (int64_t)r * N;
+  int64_t mx = INT64_MIN;
+  for (int i = threadIdx.x; i < nv; i += blockDim.x) mx = row[i] > mx ? row[i] : mx;
+  mx = block_max64(mx, red);
+  int64_t es = 0;
+  for (int i = threadIdx.x; i < nv; i += blockDim.x) es += lut_exp(T, mx - row[i]);
+  es = block_sum64(es, red);
+  for (int i = threadIdx.x; i < N; i += blockDim.x)
+    p[(int64_t)r * N + i] = i < nv ? floordiv64(shl64(lut_exp(T, mx - row[i]), 20), es) : 0;
+}
+
+__global__ void k_embed(const int32_t* __restrict__ ids, const int32_t* __restrict__ emb, int64_t* __restrict__ x,
+                        int D, int V) {
+  const int r = blockIdx.x;
+  int id = ids[r];
+  id = id < 0 ? 0 : (id >= V ? V - 1 : id);
+  for (int i = threadIdx.x; i < D; i += blockDim.x) x[(int64_t)r * D + i] = emb[(int64_t)id * D + i];
+}
+
+__global__ void k_logits_argmax(const int64_t* t, const int32_t* __restrict__ s, int64_t* lg, int32_t* ids, int N) {
+  __shared__ int64_t bv[16];
+  __shared__ int bi[16];
+  const int r = blockIdx.x;
+  const int sh = 28 - s[r];
+  int64_t best = INT64_MIN;
+  int bidx = 0x7fffffff;
+  for (int i = threadIdx.x; i < N; i += blockDim.x) {
+    const int64_t v = shr64(t[(int64_t)r * N + i], sh);
+    if (lg) lg[(int64_t)r * N + i] = v;
+    if (v > best) { best = v; bidx = i; }   // i increases per thread: keeps the first max
+  }
+  // wave reduction with lowest-index tie-break
+  for (int o = 32; o > 0; o >>= 1) {
+    const int64_t ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bidx, o, 64);
+    if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
+  }
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) { bv[w] = best; bi[w] = bidx; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < nw; ++i)
+      if (bv[i] > best || (bv[i] == best && bi[i] < bidx)) { best = bv[i]; bidx = bi[i]; }
+    if (ids) ids[r] = bidx;
+  }
+}
+
+__global__ void k_advance(int32_t* pos, int R) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < R) pos[i] += 1;
+}
+
+static inline int blk_for(int n) { return n >= 2048 ? 512 : 256; }
+
+}  // namespace exact
+
+using namespace exact;
+
+extern "C" int exact_version(void) { return 100; }
+extern "C" const char* exact_last_error(void) { return g_err; }
+
+#define SMEM_ROW_MAX 8192    // int64 entries staged per row in LDS (64 KiB)
+
+extern "C" int exact_qrow(const int64_t* x, int32_t bits, void* xq, int32_t* s, int32_t R, int32_t K, void* stream) {
+  if (!x || !xq || !s || R <= 0 || K <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
+  if (K > SMEM_ROW_MAX) return EXACT_E_UNSUPPORTED;
+  hipLaunchKernelGGL(k_qrow, dim3(R), dim3(blk_for(K)), K * 8, as_stream(stream), x, bits, xq, s, K);
+  return launch_status("qrow");
+}
+
+extern "C" int exact_irms(const int64_t* x, const int64_t* g, int64_t* y, int32_t R, int32_t D, void* stream) {
+  if (!x || !g || !y || R <= 0 || D <= 0) return EXACT_E_ARG;
+  if (D > SMEM_ROW_MAX) return EXACT_E_UNSUPPORTED;
+  hipLaunchKernelGGL(k_irms, dim3(R), dim3(blk_for(D)), D * 8, as_stream(stream), x, g, y, D);
+  return launch_status("irms");
+}
+
+extern "C" int exact_rmsnorm_qrow(int64_t* x, const int64_t* res_t, const int32_t* res_s, const int64_t* g, int32_t bits,
+                                  void* xq, int32_t* s, int32_t R, int32_t D, void* stream) {
+  if (!x || !g || !xq || !s || R <= 0 || D <= 0 || bits < 1 || bits > 15 || (res_t && !res_s)) return EXACT_E_ARG;
+  if (D > SMEM_ROW_MAX) return EXACT_E_UNSUPPORTED;
+  hipLaunchKernelGGL(k_rmsnorm_qrow, dim3(R), dim3(blk_for(D)), D * 8, as_stream(stream), x, res_t, res_s, g, bits, xq, s,
+                     D);
+  return launch_status("rmsnorm_qrow");
+}
+
+extern "C" int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq, int32_t* sq,
+                                 int32_t R, int32_t I, void* stream) {
+  if (!t || !s || !silu_t || !xq || !sq || R <= 0 || I <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
+  hipLaunchKernelGGL(k_swiglu_qrow, dim3(R), dim3(blk_for(I)), 0, as_stream(stream), t, s, silu_t, bits, xq, sq, I);
+  return launch_status("swiglu_qrow");
+}
+
+extern "C" int exact_requant_group(const int64_t* t, const int32_t* s, const int64_t* b, int64_t* y, int32_t R, int32_t N,
+                                   void* stream) {
+  if (!t || !s || !y || R <= 0 || N <= 0) return EXACT_E_ARG;
+  const int64_t total = (int64_t)R * N;
+  const int blocks = (int)std::min<int64_t>(cdiv(total, 256), 8192);
+  hipLaunchKernelGGL(k_requant_group, dim3(blocks), dim3(256), 0, as_stream(stream), t, s, b, y, R, N);
+  return launch_status("requant_group");
+}
+
+extern "C" int exact_requant_channel(const int64_t* acc, const int32_t* s, const int64_t* M, int32_t Mbits, const int64_t* b,
+                                     int64_t* y, int32_t R, int32_t N, void* stream) {
+  if (!acc || !s || !M || !y || R <= 0 || N <= 0 || Mbits < 0 || Mbits > 62) return EXACT_E_ARG;
+  hipLaunchKernelGGL(k_requant_channel, dim3(R), dim3(blk_for(N)), 0, as_stream(stream), acc, s, M, Mbits, b, y, N);
+  return launch_status("requant_channel");
+}
+
+extern "C" int exact_isilu(const int64_t* x, const int32_t* silu_t, int64_t* y, int64_t n, void* stream) {
+  if (!x || !silu_t || !y || n < 0) return EXACT_E_ARG;
+  if (n == 0) return EXACT_OK;
+  hipLaunchKernelGGL(k_lut, dim3((unsigned)std::min<int64_t>(cdiv(n, 256), 8192)), dim3(256), 0, as_stream(stream), x, silu_t, y,
+                     n, 0);
+  return launch_status("isilu");
+}
+
+extern "C" int exact_isig(const int64_t* x, const int32_t* sig_t, int64_t* y, int64_t n, void* stream) {
+  if (!x || !sig_t || !y || n < 0) return EXACT_E_ARG;
+  if (n == 0) return EXACT_OK;
+  hipLaunchKernelGGL(k_lut, dim3((unsigned)std::min<int64_t>(cdiv(n, 256), 8192)), dim3(256), 0, as_stream(stream), x, sig_t, y,
+                     n, 1);
+  return launch_status("isig");
+}
+
+extern "C" int exact_isoftmax(const int64_t* sc, const int32_t* n_valid, const int32_t* exp_t, int64_t* p, int32_t R,
+                              int32_t N, void* stream) {
+  if (!sc || !exp_t || !p || R <= 0 || N <= 0) return EXACT_E_ARG;
+  hipLaunchKernelGGL(k_isoftmax, dim3(R), dim3(256), 0, as_stream(stream), sc, n_valid, exp_t, p, N);
+  return launch_status("isoftmax");
+}
+
+extern "C" int exact_embed(const int32_t* ids, const int32_t* emb, int64_t* x, int32_t R, int32_t D, int32_t V,
+                           void* stream) {
+  if (!ids || !emb || !x || R <= 0 || D <= 0 || V <= 0) return EXACT_E_ARG;
+  hipLaunchKernelGGL(k_embed, dim3(R), dim3(256), 0, as_stream(stream), ids, emb, x, D, V);
+  return launch_status("embed");
+}
+
+extern "C" int exact_logits_argmax(const int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int32_t R, int32_t N,
+                                   void* stream) {
+  if (!t || !s || R <= 0 || N <= 0) return EXACT_E_ARG;
+  hipLaunchKernelGGL(k_logits_argmax, dim3(R), dim3(1024), 0, as_stream(stream), t, s, lg, ids, N);
+  return launch_status("logits_argmax");
+}
+
+extern "C" int exact_advance(int32_t* pos, int32_t R, void* stream) {
+  if (!pos || R <= 0) return EXACT_E_ARG;
+  hipLaunchKernelGGL(k_advance, dim3((R + 255) / 256), dim3(256), 0, as_stream(stream), pos, R);
+  return launch_status("advance");
+}

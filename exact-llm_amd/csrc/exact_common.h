@@ -1,0 +1,109 @@
+// Integer primitives of the exact program, device side (gfx950).
+// Every function reproduces numpy int64 semantics (two's-complement wrap; the library is built
+// with -fwrapv), so results are bit-identical to the CPU definitions:
+//   round_shift  exact_llm.py:25-34   (round half up; n <= 0 shifts left)
+//   bitlen       exact_llm.py:35-40
+//   floor div    numpy '//' (exact_llm.py:103,105,115)
+//   isqrt        exact_llm.py:97-99   (exact floor sqrt)
+//   LUT interpolation of EXP_T / SILU_T / SIG_T  exact_llm.py:112-113,119-121; moe_exact_kaggle.py:421-423
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define EXACT_F 16
+#define EXACT_ONE (1LL << 16)
+#define EXACT_EXP_N 10242     // 40*256 + 2 entries
+#define EXACT_LUT16_N 8194    // 32*256 + 2 entries
+
+namespace exact {
+
+__device__ __forceinline__ int64_t shl64(int64_t a, int m) {
+  return m >= 64 ? 0 : (int64_t)((uint64_t)a << m);
+}
+
+// numpy: (a + (1 << (n-1))) >> n for n > 0, a << -n otherwise; shifts >= 64 follow numpy's rules.
+__device__ __forceinline__ int64_t shr64(int64_t a, int n) {
+  if (n <= 0) return shl64(a, -n);
+  uint64_t half = (n - 1) < 64 ? (1ULL << (n - 1)) : 0ULL;
+  int64_t s = (int64_t)((uint64_t)a + half);
+  if (n >= 64) return s < 0 ? -1 : 0;
+  return s >> n;
+}
+
+__device__ __forceinline__ int bitlen64(int64_t m) { return m <= 0 ? 0 : 64 - __clzll(m); }
+
+__device__ __forceinline__ int64_t abs64(int64_t a) { return a < 0 ? (int64_t)(0 - (uint64_t)a) : a; }
+
+// floor division for b > 0 (numpy '//')
+__device__ __forceinline__ int64_t floordiv64(int64_t a, int64_t b) {
+  int64_t q = a / b;
+  int64_t r = a - q * b;
+  return (r != 0 && ((r < 0) != (b < 0))) ? q - 1 : q;
+}
+
+__device__ __forceinline__ int64_t isqrt64(int64_t n) {
+  if (n <= 0) return 0;
+  int64_t r = (int64_t)__builtin_sqrt((double)n);
+  while (r > 0 && r * r > n) --r;
+  while ((r + 1) * (r + 1) <= n) ++r;
+  return r;
+}
+
+// exp LUT (Q24), d >= 0 for valid entries: e = T[i] - shr((T[i] - T[i+1]) * fr, 8)
+__device__ __forceinline__ int64_t lut_exp(const int32_t* T, int64_t d) {
+  int64_t i = d >> 8;
+  if (i > EXACT_EXP_N - 2) i = EXACT_EXP_N - 2;
+  int64_t fr = d & 255;
+  int64_t a = T[i], b = T[i + 1];
+  int64_t e = a - shr64((a - b) * fr, 8);
+  return d < (40LL << EXACT_F) ? e : 0;
+}
+
+// SiLU (identity above 16) / sigmoid (1.0 above 16) tables on [-16, 16) at 1/256 steps
+__device__ __forceinline__ int64_t lut16(const int32_t* T, int64_t x, bool sig) {
+  if (x >= (16LL << EXACT_F)) return sig ? EXACT_ONE : x;
+  if (x < -(16LL << EXACT_F)) return 0;
+  int64_t t = x + (16LL << EXACT_F);
+  int64_t i = t >> 8, fr = t & 255;
+  int64_t a = T[i], b = T[i + 1];
+  return a + shr64((b - a) * fr, 8);
+}
+
+// ---- wave (64-lane) reductions
+__device__ __forceinline__ int64_t wave_max64(int64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    int64_t w = __shfl_xor(v, o, 64);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = (int64_t)((uint64_t)v + (uint64_t)__shfl_xor(v, o, 64));
+  return v;
+}
+
+// block reductions for blockDim.x a multiple of 64 (<= 1024); scratch holds >= 16 int64
+__device__ __forceinline__ int64_t block_max64(int64_t v, int64_t* scratch) {
+  v = wave_max64(v);
+  int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[w] = v;
+  __syncthreads();
+  int64_t r = scratch[0];
+  for (int i = 1; i < nw; ++i) r = scratch[i] > r ? scratch[i] : r;
+  return r;
+}
+__device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t* scratch) {
+  v = wave_sum64(v);
+  int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[w] = v;
+  __syncthreads();
+  uint64_t r = 0;
+  for (int i = 0; i < nw; ++i) r += (uint64_t)scratch[i];
+  return (int64_t)r;
+}
+
+}  // namespace exact

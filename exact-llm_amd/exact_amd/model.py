@@ -1,0 +1,324 @@
+"""Device model: the exact integer forward pass on one MI355X, driven from Python through the C ABI.
+
+Mirrors the reference's torch twin and speed engine:
+  TModel.forward(ids, cache, last_only) / new_cache()      exact_torch.py:126-193
+  GraphDecoder(model).load_prefix / capture / step(token)   experiments/speed_fair_kaggle.py:590-645
+with the layer order of IntModel.__call__ (exact_llm.py:161-180):
+  x = emb[ids]; per layer: a = irms(x, g1); q, k, v = linears(a); RoPE; per-head integer attention;
+  x += o(att); m = irms(x, g2); x += down(shr(isilu(gate(m)) * up(m), 16)); logits = head(irms(x, gf)).
+Every step runs in hand-written HIP kernels (libexact_hip.so); Python only allocates buffers and
+sequences launches on the current stream, so a whole decode step can be captured in a HIP graph.
+"""
+import numpy as np
+import torch
+
+from . import ops, synth
+from .ops import I8, I16, I32, I64, PackedLinear, ExactError
+from .tables import DeviceTables
+
+
+def _lin_keys(seed, name):
+    return synth.key(seed, name + ".w"), synth.key(seed, name + ".m"), synth.key(seed, name + ".b")
+
+
+class DeviceWeights:
+    """Packed device weights of one model. Layers hold fused q|k|v and gate|up linears (group mode) so
+    a decode step issues one GEMV per fused linear; per-channel models keep separate linears."""
+
+    def __init__(self, cfg, device):
+        self.cfg, self.device = cfg, device
+        self.layers = []
+        self.mode = "group"
+
+    # -- seeded synthetic model generated on the device
+    @classmethod
+    def synthetic(cls, cfg, seed, device, layers=None):
+        self = cls(cfg, device)
+        thr = torch.tensor(synth.thresholds().astype(np.int64), dtype=I64).to(torch.int32).to(device)
+        D, H, KV, hd = cfg.D, cfg.H, cfg.KV, cfg.hd
+        nl = cfg.NL if layers is None else layers
+
+        def fused(parts, K, bias):
+            N = sum(n for _, n in parts)
+            wp, mp = PackedLinear.alloc(N, K, device)
+            off, bs = 0, []
+            for name, n in parts:
+                kw, km, kb = _lin_keys(seed, name)
+                ops.synth_linear(wp, mp, n, K, kw, km, synth.M_LO, synth.M_HI, thr, n_off=off)
+                if bias:
+                    bs.append(ops.synth_vector(kb, synth.BIAS[0], synth.BIAS[1], n, device))
+                off += n
+            b = torch.cat(bs) if bias else None
+            return PackedLinear(wp, mp, N, K, b)
+
+        for li in range(nl):
+            L = dict(
+                g1=ops.synth_vector(synth.key(seed, f"L{li}.g1"), *synth.GAIN, D, device),
+                g2=ops.synth_vector(synth.key(seed, f"L{li}.g2"), *synth.GAIN, D, device),
+                qkv=fused([(f"L{li}.q", H * hd), (f"L{li}.k", KV * hd), (f"L{li}.v", KV * hd)], D, True),
+                o=fused([(f"L{li}.o", D)], H * hd, False))
+            if cfg.moe:
+                L["router"] = fused([(f"L{li}.router", cfg.NE)], D, False)
+                L["experts"] = [(fused([(f"L{li}.e{e}.gate", cfg.MI), (f"L{li}.e{e}.up", cfg.MI)], D, False),
+                                 fused([(f"L{li}.e{e}.down", D)], cfg.MI, False)) for e in range(cfg.NE)]
+                L["shared"] = (fused([(f"L{li}.sg", cfg.SI), (f"L{li}.su", cfg.SI)], D, False),
+                               fused([(f"L{li}.sd", D)], cfg.SI, False))
+                L["sgate"] = fused([(f"L{li}.sgate", 1)], D, False)
+            else:
+                L["gateup"] = fused([(f"L{li}.gate", cfg.I), (f"L{li}.up", cfg.I)], D, False)
+                L["down"] = fused([(f"L{li}.down", D)], cfg.I, False)
+            self.layers.append(L)
+        self.gf = ops.synth_vector(synth.key(seed, "gf"), *synth.GAIN, D, device)
+        emb = fused([("emb", cfg.V)], D, False)
+        self.emb = ops.embed_table(emb, cfg.V, D)
+        self.head = emb if cfg.tie else fused([("head", cfg.V)], D, False)
+        return self
+
+    # -- from integer arrays in the oracle's layout (w (K, N) int8; group M (G, N) or channel M (N,))
+    @classmethod
+    def from_arrays(cls, cfg, arrays, device, mode="group"):
+        """arrays: emb (V, D) Q16, gf, and per layer i: f'{i}.g1', f'{i}.g2', f'{i}.{name}.w' / '.M' / '.b'."""
+        self = cls(cfg, device)
+        self.mode = mode
+
+        def lin(pfx):
+            w = arrays[pfx + ".w"]
+            K, N = w.shape
+            M = np.asarray(arrays[pfx + ".M"], np.int64)
+            b = arrays.get(pfx + ".b")
+            bt = None if b is None else ops.np_to_dev(b, I64, device)
+            wd = ops.np_to_dev(w, I8, device)
+            if mode == "group":
+                if M.max() >= 1 << 15 or M.min() < 0:
+                    raise ExactError("group scales must fit int16")
+                wp, mp = ops.pack_linear(wd, ops.np_to_dev(M, I16, device))
+                return PackedLinear(wp, mp, N, K, bt)
+            ones = torch.ones((K // 128, N), dtype=I16, device=device)
+            wp, mp = ops.pack_linear(wd, ones)
+            Mbits = int(M.max()).bit_length()
+            return PackedLinear(wp, mp, N, K, bt, "channel", ops.np_to_dev(M, I64, device), Mbits)
+
+        for i in range(cfg.NL):
+            L = dict(g1=ops.np_to_dev(arrays[f"{i}.g1"], I64, device), g2=ops.np_to_dev(arrays[f"{i}.g2"], I64, device),
+                     q=lin(f"{i}.q"), k=lin(f"{i}.k"), v=lin(f"{i}.v"), o=lin(f"{i}.o"), gate=lin(f"{i}.gate"),
+                     up=lin(f"{i}.up"), down=lin(f"{i}.down"))
+            self.layers.append(L)
+        self.gf = ops.np_to_dev(arrays["gf"], I64, device)
+        emb = np.asarray(arrays["emb"], np.int64)
+        if np.abs(emb).max() >= 1 << 31:
+            raise ExactError("embedding rows must fit int32")
+        self.emb = ops.np_to_dev(emb, I32, device)
+        self.head = lin("head")
+        return self
+
+
+class Cache:
+    """Static KV cache: per layer kq int16 (B, KV, Smax, hd), sk int32 (B, KV, Smax), v int64 (B, KV, Smax, hd),
+    plus the filled length of every slot (host side)."""
+
+    def __init__(self, cfg, B, Smax, device, layers):
+        self.B, self.Smax = B, Smax
+        self.layers = [(torch.zeros((B, cfg.KV, Smax, cfg.hd), dtype=I16, device=device),
+                        torch.zeros((B, cfg.KV, Smax), dtype=I32, device=device),
+                        torch.zeros((B, cfg.KV, Smax, cfg.hd), dtype=I64, device=device)) for _ in range(layers)]
+        self.n = [0] * B
+
+
+class Workspace:
+    """Activation buffers for R rows (allocated once; reused by every step and by captured graphs)."""
+
+    def __init__(self, cfg, R, device, nq, I):
+        D, H, hd, V = cfg.D, cfg.H, cfg.hd, cfg.V
+        z = lambda *sh, dt=I64: torch.zeros(sh, dtype=dt, device=device)
+        self.R = R
+        self.x, self.xq, self.s = z(R, D), z(R, D, dt=I16), z(R, dt=I32)
+        self.t_qkv, self.qq, self.sq = z(R, nq), z(R, H, hd, dt=I16), z(R, H, dt=I32)
+        self.att, self.aq, self.sa = z(R, H * hd), z(R, H * hd, dt=I16), z(R, dt=I32)
+        self.t_o, self.t_gu, self.hq, self.sh = z(R, D), z(R, 2 * I), z(R, I, dt=I16), z(R, dt=I32)
+        self.t_d, self.t_head = z(R, D), z(R, V)
+        self.logits, self.next_ids = z(R, V), z(R, dt=I32)
+        self.s28 = torch.full((R,), 28, dtype=I32, device=device)
+        self.ids, self.slot, self.pos = z(R, dt=I32), z(R, dt=I32), z(R, dt=I32)
+
+
+class TModel:
+    """Exact integer model on the GPU (the reference's TModel + GraphDecoder engine, exact_torch.py:126-193)."""
+
+    def __init__(self, weights, Smax=512, batch=1, abits=15):
+        self.w = weights
+        self.cfg = c = weights.cfg
+        self.dev = weights.device
+        self.abits = abits
+        self.Smax, self.batch = Smax, batch
+        self.tab = DeviceTables(self.dev, Smax, c.hd, c.theta)
+        self.nl = len(weights.layers)
+        self.nq = (c.H + 2 * c.KV) * c.hd
+        self.I = c.I if not c.moe else max(c.MI, c.SI)
+        self._ws = {}
+
+    # ---------------------------------------------------------------- buffers
+    def new_cache(self, B=None):
+        return Cache(self.cfg, self.batch if B is None else B, self.Smax, self.dev, self.nl)
+
+    def workspace(self, R):
+        if R not in self._ws:
+            self._ws[R] = Workspace(self.cfg, R, self.dev, self.nq, self.I)
+        return self._ws[R]
+
+    # ---------------------------------------------------------------- linears
+    def _lin(self, x, lin, out):
+        """t for a group-mode linear (the caller applies shr(t, 28 - s) + b in the consumer kernel)."""
+        return ops.linear_t(x, self.abits, lin, out)
+
+    def _lin_channel(self, x, s, lin, out):
+        """channel mode: y = requant_channel(acc) written over out; the consumer then uses s = 28."""
+        acc = ops.linear_t(x, self.abits, lin)
+        ops.requant_channel(acc, s, lin.M, lin.Mbits, lin.bias, out=out)
+        return out
+
+    # ---------------------------------------------------------------- one pass over R rows
+    def forward_rows(self, ws, want_logits=True):
+        """Runs the model on ws.ids with (slot, pos) per row; KV of each row is written into the cache
+        at (slot, pos). Leaves logits in ws.logits and greedy ids in ws.next_ids."""
+        c, R, tab = self.cfg, ws.R, self.tab
+        H, KV, hd, D = c.H, c.KV, c.hd, c.D
+        group = self.w.mode == "group"
+        ops.embed(ws.ids, self.w.emb, ws.x)
+        res_t, res_s = None, None
+        for li, L in enumerate(self.w.layers):
+            cache = self._cache.layers[li]
+            ops.rmsnorm_qrow(ws.x, L["g1"], self.abits, res_t, res_s, ws.xq, ws.s)
+            if group:
+                self._lin(ws.xq, L["qkv"], ws.t_qkv)
+                s_qkv, b_qkv = ws.s, L["qkv"].bias
+            else:
+                off = 0
+                for part in ("q", "k", "v"):
+                    lin = L[part]
+                    y = self._lin_channel(ws.xq, ws.s, lin, torch.empty((R, lin.N), dtype=I64, device=self.dev))
+                    ws.t_qkv[:, off:off + lin.N].copy_(y)
+                    off += lin.N
+                s_qkv, b_qkv = ws.s28, None
+            ops.qkv_rope_cache(ws.t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache, ws.qq, ws.sq, H, KV, hd)
+            ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv)
+            ops.qrow(ws.att, self.abits, ws.aq, ws.sa)
+            if group:
+                self._lin(ws.aq, L["o"], ws.t_o)
+                ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.sa, ws.xq, ws.s)
+            else:
+                self._lin_channel(ws.aq, ws.sa, L["o"], ws.t_o)
+                ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.s28, ws.xq, ws.s)
+            if c.moe:
+                raise ExactError("MoE blocks run through MoEModel")
+            if group:
+                self._lin(ws.xq, L["gateup"], ws.t_gu)
+                ops.swiglu_qrow(ws.t_gu, ws.s, tab.silu, self.abits, ws.hq, ws.sh)
+                self._lin(ws.hq, L["down"], ws.t_d)
+                res_t, res_s = ws.t_d, ws.sh
+            else:
+                I = L["gate"].N
+                yg = self._lin_channel(ws.xq, ws.s, L["gate"], torch.empty((R, I), dtype=I64, device=self.dev))
+                yu = self._lin_channel(ws.xq, ws.s, L["up"], torch.empty((R, I), dtype=I64, device=self.dev))
+                ws.t_gu[:, :I].copy_(yg)
+                ws.t_gu[:, I:].copy_(yu)
+                ops.swiglu_qrow(ws.t_gu, ws.s28, tab.silu, self.abits, ws.hq, ws.sh)
+                self._lin_channel(ws.hq, ws.sh, L["down"], ws.t_d)
+                res_t, res_s = ws.t_d, ws.s28
+        ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s)
+        if group:
+            self._lin(ws.xq, self.w.head, ws.t_head)
+            ops.logits_argmax(ws.t_head, ws.s, ws.logits if want_logits else None, ws.next_ids)
+        else:
+            self._lin_channel(ws.xq, ws.s, self.w.head, ws.t_head)
+            ops.logits_argmax(ws.t_head, ws.s28, ws.logits if want_logits else None, ws.next_ids)
+        return ws
+
+    # ---------------------------------------------------------------- reference-shaped API
+    def forward(self, ids, cache=None, last_only=False, slot=0):
+        """int64 Q16 logits (T, V) of the new tokens ids (a list) for cache slot `slot` (exact_torch.py:171-193)."""
+        if cache is None:
+            cache = self.new_cache(B=1)
+            slot = 0
+        T = len(ids)
+        p0 = cache.n[slot]
+        if p0 + T > self.Smax:
+            raise ExactError(f"sequence of {p0 + T} positions exceeds the cache ({self.Smax})")
+        self._cache = cache
+        ws = self.workspace(T)
+        ws.ids.copy_(torch.tensor(ids, dtype=I32))
+        ws.slot.fill_(slot)
+        ws.pos.copy_(torch.arange(p0, p0 + T, dtype=I32))
+        self.forward_rows(ws)
+        cache.n[slot] = p0 + T
+        out = ws.logits.clone()
+        return out[-1:] if last_only else out
+
+    def decode_rows(self, tokens, cache):
+        """One decode step for B sequences (row r = cache slot r, at position cache.n[r])."""
+        B = len(tokens)
+        self._cache = cache
+        ws = self.workspace(B)
+        ws.ids.copy_(torch.tensor(tokens, dtype=I32))
+        ws.slot.copy_(torch.arange(B, dtype=I32))
+        ws.pos.copy_(torch.tensor(cache.n[:B], dtype=I32))
+        if max(cache.n[:B]) >= self.Smax:
+            raise ExactError("cache full")
+        self.forward_rows(ws)
+        for r in range(B):
+            cache.n[r] += 1
+        return ws.logits.clone(), ws.next_ids.clone()
+
+
+class GraphDecoder:
+    """HIP-graph decode step for B sequences (speed_fair_kaggle.py:590-645): ids, slots and positions
+    live on the device; one replay runs every kernel of a step, writes the logits and the greedy next
+    ids, and advances the positions. step() = copy tokens (optional) + replay."""
+
+    def __init__(self, tm, cache, B):
+        self.tm, self.cache, self.B = tm, cache, B
+        self.ws = tm.workspace(B)
+        self.graph = None
+
+    def load(self, tokens):
+        ws = self.ws
+        ws.ids.copy_(torch.tensor(tokens, dtype=I32))
+        ws.slot.copy_(torch.arange(self.B, dtype=I32))
+        ws.pos.copy_(torch.tensor(self.cache.n[:self.B], dtype=I32))
+
+    def _step(self):
+        self.tm._cache = self.cache
+        self.tm.forward_rows(self.ws)
+        ops.advance(self.ws.pos)
+
+    def capture(self):
+        """Warm up once outside the graph (restoring positions), then capture one step."""
+        ws = self.ws
+        pos0 = ws.pos.clone()
+        ids0 = ws.ids.clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self._step()
+        torch.cuda.current_stream().wait_stream(s)
+        ws.pos.copy_(pos0)
+        ws.ids.copy_(ids0)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+        torch.cuda.synchronize()
+
+    def step(self, feed_argmax=True):
+        """One decode step: returns (logits (B, V) view, next ids view). With feed_argmax the next step
+        consumes the greedy ids directly on the device."""
+        if max(self.cache.n[:self.B]) >= self.tm.Smax:
+            raise ExactError("cache full")
+        if self.graph is None:
+            self._step()
+        else:
+            self.graph.replay()
+        for r in range(self.B):
+            self.cache.n[r] += 1
+        if feed_argmax:
+            self.ws.ids.copy_(self.ws.next_ids)
+        return self.ws.logits, self.ws.next_ids

@@ -1,0 +1,268 @@
+"""Torch-facing wrappers of the C ABI: validate tensors on the host, pass raw device pointers and the
+current HIP stream, return or fill caller-visible tensors. Allocation (when an output is not given)
+happens here, on the host side of the ABI, never inside the library.
+
+The reference's single custom op is exact::gemv (experiments/speed_fair_kaggle.py:698-702); it is
+registered below under the same name with the same (x16, wT, Mg) -> int64 (N,) contract, where wT
+and Mg are this library's packed weight and scale buffers.
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import ExactError
+
+I8, I16, I32, I64 = torch.int8, torch.int16, torch.int32, torch.int64
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need(t, dtype, name, numel=None):
+    if not isinstance(t, torch.Tensor):
+        raise ExactError(f"{name}: expected a tensor")
+    if t.device.type != "cuda":
+        raise ExactError(f"{name}: expected a GPU tensor, got {t.device}")
+    if t.dtype != dtype:
+        raise ExactError(f"{name}: expected {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ExactError(f"{name}: expected a contiguous tensor")
+    if numel is not None and t.numel() < numel:
+        raise ExactError(f"{name}: expected at least {numel} elements, got {t.numel()}")
+    return t
+
+
+# ----------------------------------------------------------------------------- packed linears
+class PackedLinear:
+    """A linear in the packed device layout: wp int8 [Np/64][G][8][64][16], mp int16 [Np/64][G][64].
+    mode 'group': y = shr(t, 28 - s) + b; mode 'channel': M (N,) int64 with the per-row drop rule."""
+
+    def __init__(self, wp, mp, N, K, bias=None, mode="group", M=None, Mbits=None):
+        self.wp, self.mp, self.N, self.K = wp, mp, N, K
+        self.G = K // 128
+        self.bias, self.mode, self.M, self.Mbits = bias, mode, M, Mbits
+
+    @staticmethod
+    def alloc(N, K, device):
+        if K % 128:
+            raise ExactError(f"K = {K} is not a multiple of 128")
+        nb = (N + 63) // 64
+        G = K // 128
+        wp = torch.empty(nb * G * 8192, dtype=I8, device=device)
+        mp = torch.empty(nb * G * 64, dtype=I16, device=device)
+        return wp, mp
+
+    def part(self, n0, n1):
+        """View of output rows [n0, n1) (n0 % 64 == 0): shares the packed storage."""
+        if n0 % 64:
+            raise ExactError("sub-linear must start on a 64-row boundary")
+        nb0, nb1 = n0 // 64, (n1 + 63) // 64
+        b = None if self.bias is None else self.bias[n0:n1]
+        return PackedLinear(self.wp[nb0 * self.G * 8192: nb1 * self.G * 8192], self.mp[nb0 * self.G * 64: nb1 * self.G * 64],
+                            n1 - n0, self.K, b, self.mode)
+
+
+def synth_linear(wp, mp, N, K, kw, km, m_lo, m_hi, thr_dev, n_off=0):
+    """Generate an (N, K) synthetic linear into rows [n_off, n_off + N) of packed buffers."""
+    G = K // 128
+    nb0 = n_off // 64
+    if n_off % 64:
+        raise ExactError("parts of a fused linear must start on 64-row boundaries")
+    w = wp[nb0 * G * 8192:]
+    m = mp[nb0 * G * 64:]
+    _lib.call("exact_synth_linear", ctypes.c_uint64(kw), ctypes.c_uint64(km), m_lo, m_hi, _ptr(thr_dev), _ptr(w), _ptr(m),
+              N, K, _stream())
+
+
+def synth_vector(k, lo, hi, n, device):
+    out = torch.empty(n, dtype=I64, device=device)
+    _lib.call("exact_synth_vector", ctypes.c_uint64(k), lo, hi, _ptr(out), n, _stream())
+    return out
+
+
+def pack_linear(w_kn, m_gn, wp=None, mp=None, n_off=0):
+    """Pack a (K, N) int8 weight and (G, N) int16 scales (device tensors)."""
+    K, N = w_kn.shape
+    _need(w_kn, I8, "w_kn")
+    _need(m_gn, I16, "m_gn")
+    if wp is None:
+        wp, mp = PackedLinear.alloc(N, K, w_kn.device)
+    G = K // 128
+    nb0 = n_off // 64
+    _lib.call("exact_pack_linear", _ptr(w_kn), _ptr(m_gn), _ptr(wp[nb0 * G * 8192:]), _ptr(mp[nb0 * G * 64:]), N, K,
+              _stream())
+    return wp, mp
+
+
+# ----------------------------------------------------------------------------- linears
+def gemv_g128(x, abits, lin, out=None):
+    """t (R, N) int64 = sum_g acc_g * M_g for R <= 15 (abits 15) / 16 (abits 7) rows."""
+    return _linear("exact_gemv_g128", x, abits, lin, out)
+
+
+def gemm_g128(x, abits, lin, out=None):
+    return _linear("exact_gemm_g128", x, abits, lin, out)
+
+
+def linear_t(x, abits, lin, out=None):
+    """Dispatch: GEMV for decode-sized R, GEMM otherwise (TLinG, speed_fair_kaggle.py:735-742)."""
+    R = x.shape[0]
+    return gemv_g128(x, abits, lin, out) if R <= (15 if abits == 15 else 16) else gemm_g128(x, abits, lin, out)
+
+
+def _linear(fn, x, abits, lin, out):
+    R, K = x.shape
+    if K != lin.K:
+        raise ExactError(f"{fn}: x has K = {K}, linear has K = {lin.K}")
+    _need(x, I16 if abits == 15 else I8, "x")
+    if out is None:
+        out = torch.empty((R, lin.N), dtype=I64, device=x.device)
+    _need(out, I64, "out", R * lin.N)
+    _lib.call(fn, _ptr(x), abits, _ptr(lin.wp), _ptr(lin.mp), _ptr(out), R, lin.N, K, _stream())
+    return out
+
+
+def requant_group(t, s, b=None, out=None):
+    R, N = t.shape
+    out = torch.empty_like(t) if out is None else out
+    _lib.call("exact_requant_group", _ptr(t), _ptr(_need(s, I32, "s", R)), _ptr(b), _ptr(out), R, N, _stream())
+    return out
+
+
+def requant_channel(acc, s, M, Mbits, b=None, out=None):
+    R, N = acc.shape
+    out = torch.empty_like(acc) if out is None else out
+    _lib.call("exact_requant_channel", _ptr(acc), _ptr(_need(s, I32, "s", R)), _ptr(_need(M, I64, "M", N)), int(Mbits),
+              _ptr(b), _ptr(out), R, N, _stream())
+    return out
+
+
+# ----------------------------------------------------------------------------- nonlinearities
+def qrow(x, bits=15, xq=None, s=None):
+    R, K = x.shape
+    _need(x, I64, "x")
+    xq = torch.empty((R, K), dtype=I16 if bits > 7 else I8, device=x.device) if xq is None else xq
+    s = torch.empty(R, dtype=I32, device=x.device) if s is None else s
+    _lib.call("exact_qrow", _ptr(x), bits, _ptr(xq), _ptr(s), R, K, _stream())
+    return xq, s
+
+
+def irms(x, g):
+    R, D = x.shape
+    y = torch.empty_like(_need(x, I64, "x"))
+    _lib.call("exact_irms", _ptr(x), _ptr(_need(g, I64, "g", D)), _ptr(y), R, D, _stream())
+    return y
+
+
+def rmsnorm_qrow(x, g, bits=15, res_t=None, res_s=None, xq=None, s=None):
+    """x += rs(res_t, 28 - res_s) (in place) when res_t is given; then qrow(irms(x, g), bits)."""
+    R, D = x.shape
+    _need(x, I64, "x")
+    xq = torch.empty((R, D), dtype=I16 if bits > 7 else I8, device=x.device) if xq is None else xq
+    s = torch.empty(R, dtype=I32, device=x.device) if s is None else s
+    _lib.call("exact_rmsnorm_qrow", _ptr(x), _ptr(res_t), _ptr(res_s), _ptr(_need(g, I64, "g", D)), bits, _ptr(xq), _ptr(s),
+              R, D, _stream())
+    return xq, s
+
+
+def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None):
+    R, N2 = t.shape
+    I = N2 // 2
+    xq = torch.empty((R, I), dtype=I16 if bits > 7 else I8, device=t.device) if xq is None else xq
+    sq = torch.empty(R, dtype=I32, device=t.device) if sq is None else sq
+    _lib.call("exact_swiglu_qrow", _ptr(_need(t, I64, "t")), _ptr(s), _ptr(silu), bits, _ptr(xq), _ptr(sq), R, I, _stream())
+    return xq, sq
+
+
+def isilu(x, silu):
+    y = torch.empty_like(_need(x, I64, "x"))
+    _lib.call("exact_isilu", _ptr(x), _ptr(silu), _ptr(y), x.numel(), _stream())
+    return y
+
+
+def isig(x, sig):
+    y = torch.empty_like(_need(x, I64, "x"))
+    _lib.call("exact_isig", _ptr(x), _ptr(sig), _ptr(y), x.numel(), _stream())
+    return y
+
+
+def isoftmax(sc, expt, n_valid=None):
+    R, N = sc.shape
+    p = torch.empty_like(_need(sc, I64, "sc"))
+    _lib.call("exact_isoftmax", _ptr(sc), _ptr(n_valid), _ptr(expt), _ptr(p), R, N, _stream())
+    return p
+
+
+# ----------------------------------------------------------------------------- attention / plumbing
+def qkv_rope_cache(t, s, b, cos, sin, slot, pos, cache, qq, sq, H, KV, hd):
+    R = t.shape[0]
+    kq, sk, v = cache
+    Smax = kq.shape[2]
+    _lib.call("exact_qkv_rope_cache", _ptr(t), _ptr(s), _ptr(b), _ptr(cos), _ptr(sin), _ptr(slot), _ptr(pos), _ptr(qq),
+              _ptr(sq), _ptr(kq), _ptr(sk), _ptr(v), R, H, KV, hd, Smax, _stream())
+
+
+def attention(qq, sq, cache, slot, pos, expt, out, H, KV, hd, inv):
+    R = qq.shape[0]
+    kq, sk, v = cache
+    Smax = kq.shape[2]
+    _lib.call("exact_attention", _ptr(qq), _ptr(sq), _ptr(kq), _ptr(sk), _ptr(v), _ptr(slot), _ptr(pos), _ptr(expt),
+              _ptr(out), R, H, KV, hd, Smax, inv, _stream())
+    return out
+
+
+def embed(ids, table, out):
+    R = ids.shape[0]
+    V, D = table.shape
+    _lib.call("exact_embed", _ptr(_need(ids, I32, "ids")), _ptr(_need(table, I32, "emb")), _ptr(out), R, D, V, _stream())
+    return out
+
+
+def embed_table(lin, V, D):
+    emb = torch.empty((V, D), dtype=I32, device=lin.wp.device)
+    _lib.call("exact_embed_table", _ptr(lin.wp), _ptr(lin.mp), _ptr(emb), V, D, _stream())
+    return emb
+
+
+def logits_argmax(t, s, lg=None, ids=None):
+    R, N = t.shape
+    _lib.call("exact_logits_argmax", _ptr(t), _ptr(s), _ptr(lg), _ptr(ids), R, N, _stream())
+    return lg, ids
+
+
+def advance(pos):
+    _lib.call("exact_advance", _ptr(pos), pos.numel(), _stream())
+
+
+def zero_(t):
+    _lib.call("exact_zero", _ptr(t), t.numel() * t.element_size(), _stream())
+    return t
+
+
+# ----------------------------------------------------------------------------- the reference's op
+@torch.library.custom_op("exact::gemv", mutates_args=())
+def gemv(x16: torch.Tensor, wT: torch.Tensor, Mg: torch.Tensor) -> torch.Tensor:
+    """exact::gemv(x16, wT, Mg) -> int64 (N,) (speed_fair_kaggle.py:698-700); wT / Mg are packed buffers
+    whose output count is carried by Mg: N = Mg.numel() // G rounded to the packed rows."""
+    K = x16.shape[-1]
+    G = K // 128
+    N = Mg.numel() // G
+    lin = PackedLinear(wT, Mg, N, K)
+    return gemv_g128(x16.view(1, K), 15, lin).view(N)
+
+
+@gemv.register_fake
+def _gemv_fake(x16, wT, Mg):
+    G = x16.shape[-1] // 128
+    return torch.empty((Mg.numel() // G,), dtype=torch.int64, device=x16.device)
+
+
+def np_to_dev(a, dtype, device):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dtype)

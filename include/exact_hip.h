@@ -1,0 +1,152 @@
+/* exact_hip.h - C ABI of the MI355X (gfx950) exact integer forward path.
+ *
+ * Plain C: device pointers, sizes and a hipStream_t (passed as void*), no torch types.
+ * Every entry point validates shapes on the host, launches on the given stream, never
+ * allocates device memory and never synchronises, so a caller may capture it in a HIP graph.
+ * Return value: EXACT_OK (0) or one of the EXACT_E_* codes below (nothing was launched unless
+ * the code is EXACT_E_LAUNCH).
+ *
+ * Data formats
+ *   activations  int64 Q16, row-major (R, D)
+ *   xq           quantised rows from qrow: int16 (bits 8..15) or int8 (bits <= 7), shifts s int32 (R)
+ *   packed linear (N outputs, K inputs, K % 128 == 0, Np = N rounded up to 64, G = K / 128):
+ *       wp int8  [Np/64][G][8][64][16]  wp[((nb*G+g)*8+j)*1024 + l*16 + b] = W[n = nb*64+l][k = g*128+j*16+b]
+ *       mp int16 [Np/64][G][64]         mp[(nb*G+g)*64 + l] = M[g][n]   (positive group-128 scales)
+ *     One 8 KiB tile holds 64 output rows x one 128-wide group; rows n >= N are zero.
+ *   t            int64 (R, N): t = sum_g acc_g * M_g, acc_g = sum_{k in g} xq[k] * W[n][k] (exact)
+ *   tables       EXP_T (10242 x Q24) and SILU_T / SIG_T (8194 x Q16) as int32 device arrays
+ */
+#ifndef EXACT_HIP_H
+#define EXACT_HIP_H
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EXACT_OK 0
+#define EXACT_E_ARG 1        /* null pointer, bad size or shape */
+#define EXACT_E_UNSUPPORTED 2 /* size outside what the kernels handle (e.g. K % 128, R too large) */
+#define EXACT_E_LAUNCH 3     /* the HIP launch reported an error */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int exact_version(void);
+
+/* Last HIP error string seen by the library (for diagnostics; not thread-safe). */
+const char* exact_last_error(void);
+
+/* ---- weights ------------------------------------------------------------------------------------
+ * Seeded synthetic linear written straight into the packed layout. W[n][k] for logical index
+ * i = n*K + k is -127 + #{j : thr[j] <= (splitmix64(key_w, i) >> 32)} with the 254 thresholds of a
+ * rounded, clipped N(0, 40^2); M[g][n] = m_lo + (((splitmix64(key_m, n*G + g) >> 32) * (m_hi - m_lo)) >> 32).
+ * No counterpart in the reference (it quantises downloaded float checkpoints, exact_llm.py:82-88);
+ * this is the seeded integer artifact of SPEC.md:7-12 generated on the device. */
+int exact_synth_linear(uint64_t key_w, uint64_t key_m, int32_t m_lo, int32_t m_hi, const uint32_t* thr,
+                       int8_t* wp, int16_t* mp, int32_t N, int32_t K, void* stream);
+
+/* out[i] = lo + (((splitmix64(key, i) >> 32) * (hi - lo)) >> 32), i < n (gains, biases). */
+int exact_synth_vector(uint64_t key, int64_t lo, int64_t hi, int64_t* out, int64_t n, void* stream);
+
+/* Repack a (K, N) row-major int8 weight (QLin.w layout, exact_llm.py:85) and (G, N) int16 scales
+ * (GQLin.M, speed_fair_kaggle.py:717) into the packed layout. Replaces TLinG's wT = w.T.contiguous()
+ * and Mg = M.T (speed_fair_kaggle.py:730-731). */
+int exact_pack_linear(const int8_t* w_kn, const int16_t* m_gn, int8_t* wp, int16_t* mp,
+                      int32_t N, int32_t K, void* stream);
+
+/* ---- linears ------------------------------------------------------------------------------------
+ * Exact group-128 GEMV for decode, R <= 8 rows (one to eight tokens): t[r][n] = sum_g acc_g * M[g][n].
+ * abits = 15: x is int16 (xq from qrow(x, 15), the spec); abits = 7: x is int8 (exact_torch A8 mode).
+ * Replaces the reference's exact::gemv op and its CUDA kernel gemv_g128_v2
+ * (experiments/speed_fair_kaggle.py:656-702) and TLinG's R == 1 branch (:735-738), extended to R <= 8. */
+int exact_gemv_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
+                    int32_t R, int32_t N, int32_t K, void* stream);
+
+/* Exact group-128 GEMM for prefill (any R): same output as exact_gemv_g128.
+ * Replaces TLinG's R > 1 fp64 bmm branch (speed_fair_kaggle.py:739-742) and TLin._acc's
+ * torch._int_mm A16/A8 passes (exact_torch.py:94-119). */
+int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
+                    int32_t R, int32_t N, int32_t K, void* stream);
+
+/* Group epilogue y = round_shift(t, 28 - s[r]) + b[n] (b may be NULL)
+ * (speed_fair_kaggle.py:725,743; SPEC.md:18). */
+int exact_requant_group(const int64_t* t, const int32_t* s, const int64_t* b, int64_t* y,
+                        int32_t R, int32_t N, void* stream);
+
+/* Per-channel epilogue with the per-row overflow drop rule: y may alias acc
+ * (exact_llm.py:93-96; speed_fair_kaggle.py:745-746; SPEC.md:28). */
+int exact_requant_channel(const int64_t* acc, const int32_t* s, const int64_t* M, int32_t Mbits,
+                          const int64_t* b, int64_t* y, int32_t R, int32_t N, void* stream);
+
+/* ---- integer nonlinearities ---------------------------------------------------------------------- */
+/* Per-row quantiser qrow(x, bits) (exact_llm.py:41-46): xq int16 for bits >= 8, int8 for bits <= 7. */
+int exact_qrow(const int64_t* x, int32_t bits, void* xq, int32_t* s, int32_t R, int32_t K, void* stream);
+
+/* Integer RMSNorm alone, y = irms(x, g) (exact_llm.py:100-106). */
+int exact_irms(const int64_t* x, const int64_t* g, int64_t* y, int32_t R, int32_t D, void* stream);
+
+/* Fused residual + irms + qrow: if res_t != NULL, x += round_shift(res_t, 28 - res_s[r]) (written back
+ * to x); then xq, s = qrow(irms(x, g), bits). Covers exact_llm.py:177-178 (o-proj residual, post-norm),
+ * :179-180/166 (down-proj residual, next input norm) and the final norm before the head. */
+int exact_rmsnorm_qrow(int64_t* x, const int64_t* res_t, const int32_t* res_s, const int64_t* g,
+                       int32_t bits, void* xq, int32_t* s, int32_t R, int32_t D, void* stream);
+
+/* SwiGLU on a fused gate|up total: g = rs(t[r][n], 28 - s[r]), u = rs(t[r][I + n], 28 - s[r]),
+ * h = round_shift(isilu(g) * u, 16); xq, sq = qrow(h, bits). t's gate half is overwritten with h.
+ * (exact_llm.py:179; isilu exact_llm.py:118-122). */
+int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq,
+                      int32_t* sq, int32_t R, int32_t I, void* stream);
+
+/* Elementwise LUT nonlinearities on int64 arrays (isilu exact_llm.py:118-122; isig moe_exact_kaggle.py:420-424). */
+int exact_isilu(const int64_t* x, const int32_t* silu_t, int64_t* y, int64_t n, void* stream);
+int exact_isig(const int64_t* x, const int32_t* sig_t, int64_t* y, int64_t n, void* stream);
+
+/* Integer softmax rows over the first n_valid[r] entries (all if n_valid == NULL) -> Q20
+ * (exact_llm.py:109-115). */
+int exact_isoftmax(const int64_t* sc, const int32_t* n_valid, const int32_t* exp_t, int64_t* p,
+                   int32_t R, int32_t N, void* stream);
+
+/* ---- attention ------------------------------------------------------------------------------------
+ * KV cache (per layer): kq int16 [B][KV][Smax][hd], sk int32 [B][KV][Smax], v int64 [B][KV][Smax][hd].
+ * Row r of a call belongs to cache slot slot[r] at position pos[r].
+ *
+ * q/k/v epilogue: y = rs(t, 28 - s[r]) + b for the fused q|k|v total (N = (H + 2 KV) * hd); RoPE on q and
+ * k with the Q16 tables at pos[r]; k rows quantised per head (qrow 15) into the cache, v stored as is;
+ * q rows quantised per head into qq (R, H, hd) int16 and sq (R, H).
+ * (exact_torch.py:144-151; GraphDecoder._step speed_fair_kaggle.py:614-619). */
+int exact_qkv_rope_cache(const int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
+                         const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* qq,
+                         int32_t* sq, int16_t* kq, int32_t* sk, int64_t* v, int32_t R, int32_t H,
+                         int32_t KV, int32_t hd, int32_t Smax, void* stream);
+
+/* Integer attention of R query rows against the cache, keys 0..pos[r] of slot[r]:
+ * sc = rs((qq . kq) * INV, 32 - sq - sk); p = isoftmax(sc) (Q20); out = rs(p . v, 20), out (R, H*hd) int64.
+ * (exact_llm.py:170-176; exact_torch.py:162-166; speed_fair_kaggle.py:620-624). Used for decode and,
+ * with pos[r] = p0 + r, for causal prefill. */
+int exact_attention(const int16_t* qq, const int32_t* sq, const int16_t* kq, const int32_t* sk,
+                    const int64_t* v, const int32_t* slot, const int32_t* pos, const int32_t* exp_t,
+                    int64_t* out, int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t Smax, int32_t INV,
+                    void* stream);
+
+/* ---- model plumbing ------------------------------------------------------------------------------ */
+/* x[r] = emb[ids[r]] from an int32 Q16 table (V, D) (exact_llm.py:163; GraphDecoder.step :641). */
+int exact_embed(const int32_t* ids, const int32_t* emb, int64_t* x, int32_t R, int32_t D, int32_t V,
+                void* stream);
+
+/* Q16 embedding table from a packed int8 table: emb[v][k] = rint(W[v][k] * M[k/128][v] / 2^12)
+ * (round half to even, numpy rint), i.e. rint(e * 2^16) of the float row e = W*M/2^28. */
+int exact_embed_table(const int8_t* wp, const int16_t* mp, int32_t* emb, int32_t V, int32_t D, void* stream);
+
+/* Logits and greedy tokens: lg = rs(t, 28 - s[r]) (lg may alias t); ids[r] = first argmax of lg[r]
+ * (exact_llm.py:180,267). lg or ids may be NULL to skip. */
+int exact_logits_argmax(const int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int32_t R,
+                        int32_t N, void* stream);
+
+/* pos[r] += 1 for r < R (advances a decode step inside a captured graph; GraphDecoder.step :645). */
+int exact_advance(int32_t* pos, int32_t R, void* stream);
+
+/* dst[i] = 0 for i < n (graph-safe clear; no hipMemsetAsync). */
+int exact_zero(void* dst, int64_t nbytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

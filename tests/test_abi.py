@@ -1,0 +1,41 @@
+"""CPU checks of the C ABI: the library loads and exports every entry point the header declares."""
+import os
+import re
+
+import pytest
+
+from exact_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    src = open(os.path.join(ROOT, "include", "exact_hip.h")).read()
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(exact_\w+)\(", src, re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "exact_gemv_g128" in names and "exact_attention" in names and len(names) >= 20
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES or name in _lib.OTHER, name
+    assert lib.exact_version() >= 100
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_host_side_validation_rejects_bad_shapes_without_launching():
+    """Argument checks happen on the host: null pointers and unsupported K return codes, no GPU needed."""
+    lib = _lib.load()
+    assert lib.exact_gemv_g128(None, 15, None, None, None, 1, 64, 128, None) == 1
+    fake = 1 << 20   # never dereferenced: validation fails before any launch
+    assert lib.exact_gemv_g128(fake, 15, fake, fake, fake, 1, 64, 100, None) == 2      # K % 128
+    assert lib.exact_gemv_g128(fake, 9, fake, fake, fake, 1, 64, 128, None) == 2       # abits
+    assert lib.exact_gemv_g128(fake, 15, fake, fake, fake, 16, 64, 128, None) == 2     # R > 15 in A16
+    assert lib.exact_synth_linear(1, 2, 0, 40000, fake, fake, fake, 64, 128, None) == 1  # scale range
+    assert lib.exact_attention(fake, fake, fake, fake, fake, fake, fake, fake, fake, 1, 4, 2, 96, 64, 8192, None) == 2

@@ -1,0 +1,152 @@
+"""GPU parity of the HIP kernels against the oracle (bit-exact)."""
+import numpy as np
+import pytest
+import torch
+
+import exact_oracle as O
+from exact_amd import ops, synth
+from exact_amd.ops import I8, I16, I32, I64, PackedLinear
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+rng = np.random.default_rng(2024)
+
+
+def dev(a, dt):
+    return ops.np_to_dev(a, dt, DEV)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def thr():
+    return torch.tensor(synth.thresholds().astype(np.int64)).to(torch.int32).to(DEV)
+
+
+def synth_lin(thr, seed, name, N, K):
+    kw, km = synth.key(seed, name + ".w"), synth.key(seed, name + ".m")
+    wp, mp = PackedLinear.alloc(N, K, DEV)
+    ops.synth_linear(wp, mp, N, K, kw, km, synth.M_LO, synth.M_HI, thr)
+    return PackedLinear(wp, mp, N, K), kw, km
+
+
+def oracle_t(xq, w, M):
+    acc = O.group_acc(xq.astype(np.int64), w)
+    return (acc * M[:, None, :]).sum(0)
+
+
+def test_synth_matches_numpy_generator_and_pack(thr):
+    N, K = 200, 384
+    lin, kw, km = synth_lin(thr, 7, "t", N, K)
+    w = synth.weights_np(kw, N, K)
+    M = synth.scales_np(km, N, K)
+    wp2, mp2 = ops.pack_linear(dev(w, I8), dev(M, I16))
+    assert torch.equal(lin.wp, wp2) and torch.equal(lin.mp, mp2)
+
+
+@pytest.mark.parametrize("abits", [15, 7])
+@pytest.mark.parametrize("R", [1, 2, 5, 8])
+@pytest.mark.parametrize("N,K", [(64, 128), (200, 384), (896, 896), (4864, 896), (896, 4864), (1000, 1408)])
+def test_gemv_small_shapes(thr, abits, R, N, K):
+    lin, kw, km = synth_lin(thr, 11, f"g{N}x{K}", N, K)
+    lim = (1 << abits) - 1
+    xq = rng.integers(-lim, lim + 1, (R, K))
+    xq[0, :3] = [lim, -lim, 0]
+    t = ops.gemv_g128(dev(xq, I16 if abits == 15 else I8), abits, lin)
+    exp = oracle_t(xq, synth.weights_np(kw, N, K), synth.scales_np(km, N, K))
+    assert np.array_equal(host(t), exp)
+
+
+@pytest.mark.parametrize("abits", [15, 7])
+def test_gemm_chunked_rows(thr, abits):
+    N, K, R = 640, 512, 37
+    lin, kw, km = synth_lin(thr, 12, "gemm", N, K)
+    lim = (1 << abits) - 1
+    xq = rng.integers(-lim, lim + 1, (R, K))
+    t = ops.gemm_g128(dev(xq, I16 if abits == 15 else I8), abits, lin)
+    assert np.array_equal(host(t), oracle_t(xq, synth.weights_np(kw, N, K), synth.scales_np(km, N, K)))
+
+
+@pytest.mark.parametrize("name,N,K", [("q", 3584, 3584), ("kv", 512, 3584), ("gate", 18944, 3584), ("down", 3584, 18944)])
+@pytest.mark.parametrize("R", [1, 8])
+def test_gemv_7b_shapes(thr, name, N, K, R):
+    """Full Qwen2.5-7B GEMV shapes, x int8 U[-127, 127] (A8) and int16 (A16), bit-exact vs numpy."""
+    lin, kw, km = synth_lin(thr, 70, name, N, K)
+    w = synth.weights_np(kw, N, K)
+    M = synth.scales_np(km, N, K)
+    for abits in (7, 15):
+        lim = (1 << abits) - 1
+        xq = rng.integers(-lim, lim + 1, (R, K))
+        t = ops.gemv_g128(dev(xq, I16 if abits == 15 else I8), abits, lin)
+        assert np.array_equal(host(t), oracle_t(xq, w, M)), (name, R, abits)
+
+
+def test_gemv_7b_head_rows(thr):
+    """lm_head 152064 x 3584: all rows computed on the GPU, checked on the first and last 4096 rows."""
+    N, K = 152064, 3584
+    lin, kw, km = synth_lin(thr, 71, "head", N, K)
+    M = synth.scales_np(km, N, K)
+    for abits, R in ((7, 1), (15, 8)):
+        lim = (1 << abits) - 1
+        xq = rng.integers(-lim, lim + 1, (R, K))
+        t = host(ops.gemv_g128(dev(xq, I16 if abits == 15 else I8), abits, lin))
+        for n0, n1 in ((0, 4096), (N - 4096, N)):
+            exp = oracle_t(xq, synth.weights_np(kw, N, K, n0, n1), M[:, n0:n1])
+            assert np.array_equal(t[:, n0:n1], exp)
+
+
+def test_requant_and_qrow_and_irms():
+    R, N = 5, 3000
+    t = rng.integers(-(1 << 50), 1 << 50, (R, N))
+    s = rng.integers(0, 30, R).astype(np.int32)
+    b = rng.integers(-1000, 1000, N)
+    y = host(ops.requant_group(dev(t, I64), dev(s, I32), dev(b, I64)))
+    assert np.array_equal(y, O.round_shift(t, 28 - s[:, None].astype(np.int64)) + b)
+    x = rng.integers(-(1 << 40), 1 << 40, (R, 2048)) >> rng.integers(0, 40, (R, 1))
+    for bits in (15, 7):
+        xq, sq = ops.qrow(dev(x, I64), bits)
+        exq, es = O.qrow(x, bits)
+        assert np.array_equal(host(xq).astype(np.int64), exq) and np.array_equal(host(sq), es[:, 0])
+    g = synth.vector_np(synth.key(1, "g"), 2048, *synth.GAIN)
+    assert np.array_equal(host(ops.irms(dev(x, I64), dev(g, I64))), O.irms(x, g))
+
+
+def test_requant_channel_drop_rule():
+    R, N = 4, 700
+    acc = rng.integers(-(1 << 45), 1 << 45, (R, N))
+    acc[1] >>= 30
+    M = rng.integers(1 << 20, 1 << 26, N)
+    s = rng.integers(0, 20, R).astype(np.int32)
+    b = rng.integers(-100, 100, N)
+    Mbits = int(M.max()).bit_length()
+    y = host(ops.requant_channel(dev(acc, I64), dev(s, I32), dev(M, I64), Mbits, dev(b, I64)))
+    assert np.array_equal(y, O.requant_channel(acc, s[:, None].astype(np.int64), M, Mbits, b))
+
+
+def test_lut_nonlinearities_and_softmax():
+    from exact_amd.tables import exp_t, silu_t, sig_t
+    x = np.concatenate([rng.integers(-(20 << 16), 20 << 16, 50000), [-(16 << 16) - 1, -(16 << 16), (16 << 16) - 1, 16 << 16]])
+    silu, sig, ex = dev(silu_t(), I32), dev(sig_t(), I32), dev(exp_t(), I32)
+    assert np.array_equal(host(ops.isilu(dev(x, I64), silu)), O.isilu(x))
+    assert np.array_equal(host(ops.isig(dev(x, I64), sig)), O.isig(x))
+    sc = rng.integers(-(1 << 24), 1 << 24, (6, 300))
+    nv = np.array([300, 1, 17, 299, 150, 64], np.int32)
+    p = host(ops.isoftmax(dev(sc, I64), ex, dev(nv, I32)))
+    valid = np.arange(300)[None, :] < nv[:, None]
+    assert np.array_equal(p, O.isoftmax(sc, valid))
+
+
+def test_swiglu_qrow():
+    from exact_amd.tables import silu_t
+    R, I = 3, 4864
+    t = rng.integers(-(1 << 44), 1 << 44, (R, 2 * I))
+    s = rng.integers(10, 20, R).astype(np.int32)
+    td = dev(t, I64)
+    hq, sh = ops.swiglu_qrow(td, dev(s, I32), dev(silu_t(), I32))
+    g = O.round_shift(t[:, :I], 28 - s[:, None].astype(np.int64))
+    u = O.round_shift(t[:, I:], 28 - s[:, None].astype(np.int64))
+    eq, es = O.qrow(O.round_shift(O.isilu(g) * u, 16), 15)
+    assert np.array_equal(host(hq).astype(np.int64), eq) and np.array_equal(host(sh), es[:, 0])

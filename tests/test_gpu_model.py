@@ -1,0 +1,97 @@
+"""GPU model parity: logits and greedy tokens bit-identical to the oracle (and to the reference's golden)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import exact_oracle as O
+import helpers
+from exact_amd import synth
+from exact_amd.model import DeviceWeights, GraphDecoder, TModel
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "intmodel_tiny.npz")
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def test_golden_reference_intmodel_per_channel():
+    """The reference's own IntModel logits and receipts (tests/golden/make_golden.py), per-channel mode."""
+    z = np.load(GOLD)
+    cfg_d = eval(bytes(z["cfg_json"]).decode(), {})
+    cfg = synth.ModelConfig("golden", D=cfg_d["D"], H=cfg_d["H"], KV=cfg_d["KV"], hd=cfg_d["hd"], I=cfg_d["I"],
+                            V=cfg_d["V"], NL=cfg_d["NL"], theta=cfg_d["theta"])
+    arrays = {k: z[k] for k in z.files}
+    arrays["emb"] = z["emb"].astype(np.int64)
+    w = DeviceWeights.from_arrays(cfg, arrays, DEV, mode="channel")
+    tm = TModel(w, Smax=cfg_d["T"])
+    lg = host(tm.forward(z["prompt"].tolist()))
+    assert np.array_equal(lg, z["logits"])
+    # greedy continuation with the KV cache equals the oracle's (which equals the reference's generate)
+    om = O.Model({"emb": arrays["emb"], "gf": z["gf"], "head": O.Lin(z["head.w"], z["head.M"], mode="channel"),
+                  "layers": [dict(g1=z[f"{i}.g1"], g2=z[f"{i}.g2"],
+                                  **{k: O.Lin(z[f"{i}.{k}.w"], z[f"{i}.{k}.M"], z[f"{i}.{k}.b"] if f"{i}.{k}.b" in z else None,
+                                              mode="channel") for k in ("q", "k", "v", "o", "gate", "up", "down")})
+                             for i in range(cfg.NL)]}, cfg_d)
+    toks, rows = O.greedy_decode(om, z["prompt"].tolist(), 5)
+    cache = tm.new_cache(B=1)
+    lg = tm.forward(z["prompt"].tolist(), cache)
+    tok = int(host(lg)[-1].argmax())
+    got = [tok]
+    for _ in range(4):
+        lg, ids = tm.decode_rows([tok], cache)
+        tok = int(host(ids)[0])
+        got.append(tok)
+    assert got == toks
+
+
+@pytest.mark.parametrize("name", ["tiny", "tiny-tied"])
+def test_synthetic_prefill_and_decode_match_oracle(name):
+    cfg = synth.CONFIGS[name]
+    seed = 3
+    om = helpers.oracle_model(cfg, seed, T=128)
+    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=128)
+    ids = helpers.prompt(9, 20, cfg.V)
+    assert np.array_equal(host(tm.forward(ids)), om(ids))
+    # prefill 12 tokens then 6 greedy decode steps through the cache
+    otoks, orows = O.greedy_decode(om, ids[:12], 6)
+    cache = tm.new_cache(B=1)
+    lg = host(tm.forward(ids[:12], cache))
+    assert np.array_equal(lg[-1], orows[0])
+    tok = int(lg[-1].argmax())
+    for i in range(1, 6):
+        lgi, nid = tm.decode_rows([tok], cache)
+        assert np.array_equal(host(lgi)[0], orows[i]), i
+        tok = int(host(nid)[0])
+        assert tok == otoks[i]
+
+
+def test_batch_decode_and_graph_replay_match_eager():
+    cfg = synth.CONFIGS["tiny"]
+    seed = 4
+    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=64, batch=4)
+    om = helpers.oracle_model(cfg, seed, T=64)
+    prompts = [helpers.prompt(100 + b, 6 + b, cfg.V) for b in range(4)]
+    cache = tm.new_cache()
+    first = []
+    for b, p in enumerate(prompts):
+        lg = host(tm.forward(p, cache, slot=b))
+        first.append(int(lg[-1].argmax()))
+    gd = GraphDecoder(tm, cache, 4)
+    gd.load(first)
+    gd.capture()
+    steps = []
+    for _ in range(5):
+        lg, ids = gd.step()
+        steps.append((host(lg).copy(), host(ids).copy()))
+    for b, p in enumerate(prompts):
+        otoks, orows = O.greedy_decode(om, p, 6)
+        assert otoks[0] == first[b]
+        for i in range(5):
+            assert np.array_equal(steps[i][0][b], orows[i + 1]), (b, i)
+            assert int(steps[i][1][b]) == otoks[i + 1]
