@@ -50,8 +50,17 @@ def gemv_pass(args):
     x_i = torch.randint(-127, 128, (1, I), generator=g, dtype=torch.int8).to(dev)
     x_a = torch.randint(-127, 128, (1, cfg.H * cfg.hd), generator=g, dtype=torch.int8).to(dev)
     xin = {"qkv": x_d, "o": x_a, "gateup": x_d, "down": x_i}
-    outs = {k: torch.zeros((1, v[0]), dtype=I64, device=dev) for k, v in shapes.items()}
-    out_head = torch.zeros((1, cfg.V), dtype=I64, device=dev)
+    # every GEMV of the pass writes its own exact output: one buffer, zeroed once per step, sliced per launch
+    nout = NL * sum(v[0] for v in shapes.values()) + cfg.V
+    obuf = torch.zeros(nout, dtype=I64, device=dev)
+    outs, off = [], 0
+    for li in range(NL):
+        o = {}
+        for k, v in shapes.items():
+            o[k] = obuf[off:off + v[0]].view(1, v[0])
+            off += v[0]
+        outs.append(o)
+    out_head = obuf[off:off + cfg.V].view(1, cfg.V)
 
     def nbytes(N, K, R=1):
         return N * K + N * (K // 128) * 2 + R * K + R * N * 8
@@ -59,10 +68,11 @@ def gemv_pass(args):
     pass_bytes = sum(nbytes(*shapes[k]) for k in shapes) * NL + nbytes(cfg.V, D)
 
     def step():
-        for L in layers:
+        ops.zero_(obuf)
+        for L, o in zip(layers, outs):
             for k in shapes:
-                ops.gemv_g128(xin[k], 7, L[k], outs[k])
-        ops.gemv_g128(x_d, 7, head, out_head)
+                ops.gemv_g128_acc(xin[k], 7, L[k], o[k])
+        ops.gemv_g128_acc(x_d, 7, head, out_head)
 
     torch.cuda.synchronize()
     step()
@@ -98,10 +108,10 @@ def gemv_pass(args):
         a.record(st)
         for _ in range(reps):
             if k == "head":
-                ops.gemv_g128(x_d, 7, head, out_head)
+                ops.gemv_g128_acc(x_d, 7, head, out_head)
             else:
-                for L in layers:
-                    ops.gemv_g128(xin[k], 7, L[k], outs[k])
+                for L, o in zip(layers, outs):
+                    ops.gemv_g128_acc(xin[k], 7, L[k], o[k])
         b.record(st)
         torch.cuda.synchronize()
         n = reps * (1 if k == "head" else NL)
@@ -110,6 +120,41 @@ def gemv_pass(args):
     del layers, head
     torch.cuda.empty_cache()
     return dict(ms=ms, wall=wall, pass_bytes=pass_bytes, per=per)
+
+
+def model_decode(args, name="qwen2.5-7b", prompt_len=16):
+    """Full integer decode step of the 7B-architecture model (embedding, 28 layers of irms, fused q|k|v GEMV,
+    RoPE, integer attention over the KV cache, o, SwiGLU, down, head + greedy argmax), A16 activations as in
+    the spec, bs1, one HIP graph per step."""
+    import numpy as np
+    import torch
+    from exact_amd import synth
+    from exact_amd.model import DeviceWeights, GraphDecoder, TModel
+    cfg = synth.CONFIGS[name]
+    tm = TModel(DeviceWeights.synthetic(cfg, 11, "cuda"), Smax=prompt_len + args.warmup + args.steps + 8)
+    ids = np.random.default_rng(0).integers(0, cfg.V, prompt_len).tolist()
+    cache = tm.new_cache(B=1)
+    lg = tm.forward(ids, cache)
+    first = int(lg[-1].argmax())
+    gd = GraphDecoder(tm, cache, 1)
+    gd.load([first])
+    gd.capture()
+    for _ in range(args.warmup):
+        gd.step()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(args.steps):
+        gd.step()
+    b.record(st)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    wbytes = synth.param_bytes(cfg)
+    del tm, gd, cache
+    torch.cuda.empty_cache()
+    return {"model": name, "tok_s": round(1000.0 / ms, 2), "ms_per_token": round(ms, 4), "abits": 15,
+            "weights_GB": round(wbytes / 1e9, 3), "GBps": round(wbytes / ms / 1e6, 1), "prompt": prompt_len}
 
 
 def prefill_gemm(args):
@@ -180,6 +225,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-model", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs the exact path on a single MI355X; "
@@ -193,6 +239,7 @@ def main():
     exact_amd.load()
     r = gemv_pass(args)
     pre = {} if args.no_prefill else prefill_gemm(args)
+    mdl = None if args.no_model else model_decode(args)
     cpu = None if args.no_cpu else cpu_baseline()
     tok_s = 1000.0 / r["ms"]
     pass_gbps = r["pass_bytes"] / (r["ms"] * 1e-3) / 1e9
@@ -207,6 +254,7 @@ def main():
                    "weights_GB": round(r["pass_bytes"] / 1e9, 3), "parallelism": "single GPU"},
         "gemv_GBps": round(pass_gbps, 1),
         "gemv_per_shape": r["per"],
+        "model_decode": mdl,
         "prefill_gemm": pre,
         "prefill_TOPS": (round(min(v["TOPS"] for v in pre.values()), 2) if pre else None),
         "roofline": {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",

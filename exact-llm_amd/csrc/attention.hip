@@ -10,12 +10,12 @@
 namespace exact {
 
 // grid (R, H + 2*KV), block 64 (one wave per head slot), hd <= 256
-__global__ void k_qkv_rope_cache(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
+__global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restrict__ s,
                                  const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
                                  const int64_t* __restrict__ sin_t, const int32_t* __restrict__ slot,
                                  const int32_t* __restrict__ pos, int16_t* __restrict__ qq, int32_t* __restrict__ sq,
                                  int16_t* __restrict__ kq, int32_t* __restrict__ sk, int64_t* __restrict__ v, int H,
-                                 int KV, int hd, int Smax) {
+                                 int KV, int hd, int Smax, int clear_t) {
   __shared__ int64_t y[256];
   const int r = blockIdx.x, hs = blockIdx.y, lane = threadIdx.x;
   const int N = (H + 2 * KV) * hd;
@@ -25,6 +25,7 @@ __global__ void k_qkv_rope_cache(const int64_t* __restrict__ t, const int32_t* _
   const int base = hs * hd;   // q heads, then k heads, then v heads, each hd wide
   for (int j = lane; j < hd; j += 64) {
     const int64_t val = shr64(t[(int64_t)r * N + base + j], sh);
+    if (clear_t) t[(int64_t)r * N + base + j] = 0;
     y[j] = b ? val + b[base + j] : val;
   }
   __syncthreads();
@@ -128,15 +129,15 @@ __global__ __launch_bounds__(256) void k_attention(const int16_t* __restrict__ q
 
 using namespace exact;
 
-extern "C" int exact_qkv_rope_cache(const int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
+extern "C" int exact_qkv_rope_cache(int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
                                     const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* qq, int32_t* sq,
                                     int16_t* kq, int32_t* sk, int64_t* v, int32_t R, int32_t H, int32_t KV, int32_t hd,
-                                    int32_t Smax, void* stream) {
+                                    int32_t Smax, int32_t clear_t, void* stream) {
   if (!t || !s || !cos_t || !sin_t || !slot || !pos || !qq || !sq || !kq || !sk || !v) return EXACT_E_ARG;
   if (R <= 0 || H <= 0 || KV <= 0 || H % KV || hd <= 0 || Smax <= 0) return EXACT_E_ARG;
   if (hd > 256 || hd % 2) return EXACT_E_UNSUPPORTED;
   hipLaunchKernelGGL(k_qkv_rope_cache, dim3(R, H + 2 * KV), dim3(64), 0, as_stream(stream), t, s, b, cos_t, sin_t, slot,
-                     pos, qq, sq, kq, sk, v, H, KV, hd, Smax);
+                     pos, qq, sq, kq, sk, v, H, KV, hd, Smax, clear_t);
   return launch_status("qkv_rope_cache");
 }
 

@@ -86,9 +86,9 @@ __global__ void k_irms(const int64_t* __restrict__ x, const int64_t* __restrict_
   for (int i = threadIdx.x; i < D; i += blockDim.x) y[(int64_t)r * D + i] = buf[i];
 }
 
-__global__ void k_rmsnorm_qrow(int64_t* __restrict__ x, const int64_t* __restrict__ res_t,
+__global__ void k_rmsnorm_qrow(int64_t* __restrict__ x, int64_t* __restrict__ res_t,
                                const int32_t* __restrict__ res_s, const int64_t* __restrict__ g, int bits, void* xq,
-                               int32_t* s, int D) {
+                               int32_t* s, int D, int clear_t) {
   extern __shared__ int64_t buf[];
   __shared__ int64_t red[16];
   const int r = blockIdx.x;
@@ -97,6 +97,7 @@ __global__ void k_rmsnorm_qrow(int64_t* __restrict__ x, const int64_t* __restric
     const int sh = 28 - res_s[r];
     for (int i = threadIdx.x; i < D; i += blockDim.x) {
       const int64_t v = (int64_t)((uint64_t)xr[i] + (uint64_t)shr64(res_t[(int64_t)r * D + i], sh));
+      if (clear_t) res_t[(int64_t)r * D + i] = 0;
       buf[i] = v;
       xr[i] = v;
     }
@@ -110,7 +111,7 @@ __global__ void k_rmsnorm_qrow(int64_t* __restrict__ x, const int64_t* __restric
 
 // gate|up total -> h = shr(isilu(g) * u, 16) (stored over the gate half) -> qrow
 __global__ void k_swiglu_qrow(int64_t* __restrict__ t, const int32_t* __restrict__ s, const int32_t* __restrict__ silu,
-                              int bits, void* xq, int32_t* sq, int I) {
+                              int bits, void* xq, int32_t* sq, int I, int clear_t) {
   __shared__ int64_t red[16];
   const int r = blockIdx.x;
   int64_t* tr = t + (int64_t)r * 2 * I;
@@ -120,6 +121,7 @@ __global__ void k_swiglu_qrow(int64_t* __restrict__ t, const int32_t* __restrict
     const int64_t gv = shr64(tr[i], sh), uv = shr64(tr[I + i], sh);
     const int64_t hv = shr64(lut16(silu, gv, false) * uv, EXACT_F);
     tr[i] = hv;
+    if (clear_t) tr[I + i] = 0;
     const int64_t a = abs64(hv);
     m = a > m ? a : m;
   }
@@ -129,6 +131,7 @@ __global__ void k_swiglu_qrow(int64_t* __restrict__ t, const int32_t* __restrict
   const int64_t lim = (1LL << bits) - 1;
   for (int i = threadIdx.x; i < I; i += blockDim.x) {
     int64_t v = shr64(tr[i], q);
+    if (clear_t) tr[i] = 0;
     v = v > lim ? lim : (v < -lim ? -lim : v);
     if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * I + i, v);
     else store_q<int16_t>(xq, (int64_t)r * I + i, v);
@@ -197,7 +200,7 @@ __global__ void k_embed(const int32_t* __restrict__ ids, const int32_t* __restri
   for (int i = threadIdx.x; i < D; i += blockDim.x) x[(int64_t)r * D + i] = emb[(int64_t)id * D + i];
 }
 
-__global__ void k_logits_argmax(const int64_t* t, const int32_t* __restrict__ s, int64_t* lg, int32_t* ids, int N) {
+__global__ void k_logits_argmax(int64_t* t, const int32_t* __restrict__ s, int64_t* lg, int32_t* ids, int N, int clear_t) {
   __shared__ int64_t bv[16];
   __shared__ int bi[16];
   const int r = blockIdx.x;
@@ -206,6 +209,7 @@ __global__ void k_logits_argmax(const int64_t* t, const int32_t* __restrict__ s,
   int bidx = 0x7fffffff;
   for (int i = threadIdx.x; i < N; i += blockDim.x) {
     const int64_t v = shr64(t[(int64_t)r * N + i], sh);
+    if (clear_t) t[(int64_t)r * N + i] = 0;
     if (lg) lg[(int64_t)r * N + i] = v;
     if (v > best) { best = v; bidx = i; }   // i increases per thread: keeps the first max
   }
@@ -255,19 +259,19 @@ extern "C" int exact_irms(const int64_t* x, const int64_t* g, int64_t* y, int32_
   return launch_status("irms");
 }
 
-extern "C" int exact_rmsnorm_qrow(int64_t* x, const int64_t* res_t, const int32_t* res_s, const int64_t* g, int32_t bits,
-                                  void* xq, int32_t* s, int32_t R, int32_t D, void* stream) {
+extern "C" int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res_s, const int64_t* g, int32_t bits,
+                                  void* xq, int32_t* s, int32_t R, int32_t D, int32_t clear_t, void* stream) {
   if (!x || !g || !xq || !s || R <= 0 || D <= 0 || bits < 1 || bits > 15 || (res_t && !res_s)) return EXACT_E_ARG;
   if (D > SMEM_ROW_MAX) return EXACT_E_UNSUPPORTED;
   hipLaunchKernelGGL(k_rmsnorm_qrow, dim3(R), dim3(blk_for(D)), D * 8, as_stream(stream), x, res_t, res_s, g, bits, xq, s,
-                     D);
+                     D, clear_t);
   return launch_status("rmsnorm_qrow");
 }
 
 extern "C" int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq, int32_t* sq,
-                                 int32_t R, int32_t I, void* stream) {
+                                 int32_t R, int32_t I, int32_t clear_t, void* stream) {
   if (!t || !s || !silu_t || !xq || !sq || R <= 0 || I <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
-  hipLaunchKernelGGL(k_swiglu_qrow, dim3(R), dim3(blk_for(I)), 0, as_stream(stream), t, s, silu_t, bits, xq, sq, I);
+  hipLaunchKernelGGL(k_swiglu_qrow, dim3(R), dim3(blk_for(I)), 0, as_stream(stream), t, s, silu_t, bits, xq, sq, I, clear_t);
   return launch_status("swiglu_qrow");
 }
 
@@ -317,10 +321,10 @@ extern "C" int exact_embed(const int32_t* ids, const int32_t* emb, int64_t* x, i
   return launch_status("embed");
 }
 
-extern "C" int exact_logits_argmax(const int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int32_t R, int32_t N,
-                                   void* stream) {
-  if (!t || !s || R <= 0 || N <= 0) return EXACT_E_ARG;
-  hipLaunchKernelGGL(k_logits_argmax, dim3(R), dim3(1024), 0, as_stream(stream), t, s, lg, ids, N);
+extern "C" int exact_logits_argmax(int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int32_t R, int32_t N,
+                                   int32_t clear_t, void* stream) {
+  if (!t || !s || R <= 0 || N <= 0 || (clear_t && lg == t)) return EXACT_E_ARG;
+  hipLaunchKernelGGL(k_logits_argmax, dim3(R), dim3(1024), 0, as_stream(stream), t, s, lg, ids, N, clear_t);
   return launch_status("logits_argmax");
 }
 

@@ -15,7 +15,18 @@
 #define EXACT_EXP_N 10242     // 40*256 + 2 entries
 #define EXACT_LUT16_N 8194    // 32*256 + 2 entries
 
+// Packed-weight tile order. Tile (nb, g) holds output rows [64 nb, 64 nb + 64) x input group g (8 KiB).
+// Group-major order ([g][nb]) puts the tiles that concurrently running waves read next to each other,
+// so the whole GPU sweeps the weight matrix front to back like a linear stream.
+#ifndef EXACT_TILE_GN
+#define EXACT_TILE_GN 1
+#endif
+
 namespace exact {
+
+__host__ __device__ __forceinline__ int64_t tile_index(int64_t nb, int64_t g, int64_t nbs, int64_t G) {
+  return EXACT_TILE_GN ? g * nbs + nb : nb * G + g;
+}
 
 __device__ __forceinline__ int64_t shl64(int64_t a, int m) {
   return m >= 64 ? 0 : (int64_t)((uint64_t)a << m);

@@ -37,76 +37,124 @@ __device__ __forceinline__ void split_a16(v4i p0, v4i p1, v4i& hi, v4i& lo) {
   lo[3] = __builtin_amdgcn_perm(p1[3], p1[2], 0x06040200u) ^ 0x80808080;
 }
 
-template <int ABITS>
+// Per-group operands of one wave: the 8 KiB weight tile (8 x 16 B per lane), the A-operand bytes of
+// the x rows (A8: 2 x 16 B, A16: 4 x 16 B raw int16) and the four int16 scales of the lane's columns.
+struct GroupRegs {
+  v4i b[8];
+  v4i xa[4];
+  int m[4];
+};
+
+template <int ABITS, bool NT>
+__device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                           const void* __restrict__ xv, size_t tile, int g, int R, int K, int row, int c) {
+  // issue order = use order (scales are read last but are tiny; tiles last so waiting on them drains the group)
+  const int16_t* ms = mp + tile * 64 + row;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) G_.m[q] = ms[16 * q];
+  const int kb = g * 128 + 16 * c;
+  const v4i zero = {0, 0, 0, 0};
+  if (ABITS == 15) {
+    const int16_t* xp = reinterpret_cast<const int16_t*>(xv) + (size_t)(row < R ? row : 0) * K + kb;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      G_.xa[2 * h] = *reinterpret_cast<const v4i*>(xp + 64 * h);
+      G_.xa[2 * h + 1] = *reinterpret_cast<const v4i*>(xp + 64 * h + 8);
+    }
+    if (row >= R)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) G_.xa[i] = zero;
+  } else {
+    const int8_t* xp = reinterpret_cast<const int8_t*>(xv) + (size_t)(row < R ? row : 0) * K + kb;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) G_.xa[h] = *reinterpret_cast<const v4i*>(xp + 64 * h);
+    if (row >= R) G_.xa[0] = G_.xa[1] = zero;
+  }
+  const v4i* tp = reinterpret_cast<const v4i*>(wp + tile * 8192 + c * 1024 + row * 16);
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const v4i* a = tp + (4 * h * 1024 + 16 * q * 16) / 16;
+      G_.b[4 * h + q] = NT ? __builtin_nontemporal_load(a) : *a;
+    }
+}
+
+template <int ABITS, int VR>
+__device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc)[4][VR], int R, int row, int lane) {
+  const v4i zero = {0, 0, 0, 0};
+  const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+  v4i ahi[2], alo[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (ABITS == 15) {
+      split_a16(G_.xa[2 * h], G_.xa[2 * h + 1], ahi[h], alo[h]);
+      if (row == R) alo[h] = ones;          // all-ones row: colsum(W) in the lo pass
+    } else {
+      ahi[h] = G_.xa[h];
+      alo[h] = zero;
+    }
+  }
+  const int rsel = R & 3, rlane = (lane & 15) + 16 * (R >> 2);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v4i chi = zero, clo = zero;
+    chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[0], G_.b[q], chi, 0, 0, 0);
+    chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[1], G_.b[4 + q], chi, 0, 0, 0);
+    if (ABITS == 15) {
+      clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[0], G_.b[q], clo, 0, 0, 0);
+      clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[1], G_.b[4 + q], clo, 0, 0, 0);
+    }
+    const int64_t m = (int64_t)G_.m[q];
+    int cs = 0;
+    if (ABITS == 15) cs = __shfl(sel4(clo, rsel), rlane, 64);
+#pragma unroll
+    for (int v = 0; v < VR; ++v) {
+      const int a = (ABITS == 15) ? (chi[v] << 8) + clo[v] + 128 * cs : chi[v];
+      acc[q][v] += (int64_t)a * m;
+    }
+  }
+}
+
+// One wave per (64-row block nb, group range [g0, g1)). The next group's loads are issued before the
+// current group's matrix-core work and every load is unconditional inside the loop, so each wave keeps
+// two tiles (16 KiB) in flight. Lane l holds output rows 4*(l/16) + v, v < VR (VR = 1, 2 or 4 covers
+// R <= 1, 2 or 16). out_mode 0: plain store (the wave owns all groups of its rows), 1: 64-bit atomic add.
+template <int ABITS, bool NT, int VR>
 __global__ __launch_bounds__(256) void k_gemv_g128(const void* __restrict__ xv, const int8_t* __restrict__ wp,
                                                    const int16_t* __restrict__ mp, int64_t* __restrict__ t, int R,
-                                                   int N, int K, int G, int gpw, int nsplit, int use_atomic) {
+                                                   int N, int K, int G, int nsplit, int out_mode) {
   const int lane = threadIdx.x & 63;
   const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int nbs = (N + 63) >> 6;
   if (task >= nbs * nsplit) return;
   const int nb = task / nsplit, sp = task - nb * nsplit;
-  const int g0 = sp * gpw;
-  const int g1 = min(G, g0 + gpw);
+  const int g0 = (int)(((int64_t)sp * G) / nsplit);
+  const int g1 = (int)(((int64_t)(sp + 1) * G) / nsplit);
   const int row = lane & 15, c = lane >> 4;
 
-  int64_t acc[4][4];
+  int64_t acc[4][VR];
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) acc[q][v] = 0;
+    for (int v = 0; v < VR; ++v) acc[q][v] = 0;
 
-  const v4i zero = {0, 0, 0, 0};
-  const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-  const int rsel = R & 3, rlane = (lane & 15) + 16 * (R >> 2);
-
-  for (int g = g0; g < g1; ++g) {
-    const int8_t* tile = wp + ((size_t)nb * G + g) * 8192;
-    v4i b[2][4];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        b[h][q] = *reinterpret_cast<const v4i*>(tile + (4 * h + c) * 1024 + (16 * q + row) * 16);
-
-    v4i ahi[2], alo[2];
-    const int kb = g * 128 + 16 * c;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (ABITS == 15) {
-        if (row < R) {
-          const int16_t* xp = reinterpret_cast<const int16_t*>(xv) + (size_t)row * K + kb + 64 * h;
-          v4i p0 = *reinterpret_cast<const v4i*>(xp);
-          v4i p1 = *reinterpret_cast<const v4i*>(xp + 8);
-          split_a16(p0, p1, ahi[h], alo[h]);
-        } else {
-          ahi[h] = zero;
-          alo[h] = (row == R) ? ones : zero;
-        }
-      } else {
-        ahi[h] = (row < R) ? *reinterpret_cast<const v4i*>(reinterpret_cast<const int8_t*>(xv) + (size_t)row * K + kb + 64 * h)
-                           : zero;
-      }
+  if (g0 < g1) {
+    GroupRegs ra, rb;
+    load_group<ABITS, NT>(ra, wp, mp, xv, tile_index(nb, g0, nbs, G), g0, R, K, row, c);
+    int g = g0;
+    for (; g + 2 < g1; g += 2) {
+      load_group<ABITS, NT>(rb, wp, mp, xv, tile_index(nb, g + 1, nbs, G), g + 1, R, K, row, c);
+      compute_group<ABITS, VR>(ra, acc, R, row, lane);
+      load_group<ABITS, NT>(ra, wp, mp, xv, tile_index(nb, g + 2, nbs, G), g + 2, R, K, row, c);
+      compute_group<ABITS, VR>(rb, acc, R, row, lane);
     }
-
-    const int16_t* ms = mp + ((size_t)nb * G + g) * 64;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      v4i chi = zero, clo = zero;
-      chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[0], b[0][q], chi, 0, 0, 0);
-      chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[1], b[1][q], chi, 0, 0, 0);
-      if (ABITS == 15) {
-        clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[0], b[0][q], clo, 0, 0, 0);
-        clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[1], b[1][q], clo, 0, 0, 0);
-      }
-      const int64_t m = (int64_t)ms[16 * q + row];
-      int cs = 0;
-      if (ABITS == 15) cs = __shfl(sel4(clo, rsel), rlane, 64);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        int a = (ABITS == 15) ? (chi[v] << 8) + clo[v] + 128 * cs : chi[v];
-        acc[q][v] += (int64_t)a * m;
-      }
+    if (g + 1 < g1) {
+      load_group<ABITS, NT>(rb, wp, mp, xv, tile_index(nb, g + 1, nbs, G), g + 1, R, K, row, c);
+      compute_group<ABITS, VR>(ra, acc, R, row, lane);
+      compute_group<ABITS, VR>(rb, acc, R, row, lane);
+    } else {
+      compute_group<ABITS, VR>(ra, acc, R, row, lane);
     }
   }
 
@@ -114,11 +162,11 @@ __global__ __launch_bounds__(256) void k_gemv_g128(const void* __restrict__ xv, 
   for (int q = 0; q < 4; ++q) {
     const int n = nb * 64 + 16 * q + row;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < VR; ++v) {
       const int r = 4 * c + v;
       if (r < R && n < N) {
         int64_t* dst = t + (size_t)r * N + n;
-        if (use_atomic)
+        if (out_mode)
           atomicAdd(reinterpret_cast<unsigned long long*>(dst), (unsigned long long)acc[q][v]);
         else
           *dst = acc[q][v];
@@ -149,32 +197,43 @@ int zero_bytes(void* dst, int64_t nbytes, hipStream_t st) {
   return launch_status("zero");
 }
 
-// Work split: enough waves to cover the chip (~2048), whole groups per wave.
-static void gemv_split(int N, int G, int* gpw, int* nsplit) {
-  const int64_t tiles = (int64_t)((N + 63) / 64) * G;
-  int g = (int)(tiles / 2048);
-  if (g < 1) g = 1;
-  if (g > G) g = G;
-  *gpw = g;
-  *nsplit = (G + g - 1) / g;
+// Work split: about GEMV_WAVES waves over the chip, groups spread evenly over the splits of a row block.
+#ifndef GEMV_WAVES
+#define GEMV_WAVES 3072
+#endif
+#ifndef GEMV_NT
+#define GEMV_NT 1
+#endif
+static int gemv_nsplit(int N, int G) {
+  const int64_t nbs = (N + 63) / 64;
+  int64_t ns = (GEMV_WAVES + nbs - 1) / nbs;
+  if (ns < 1) ns = 1;
+  if (ns > G) ns = G;
+  return (int)ns;
 }
 
+// accumulate: t += x.W (t holds the caller's running total, e.g. zeros left by a consumer kernel);
+// otherwise t is overwritten (zero-filled first when the row blocks are split).
 int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, int64_t* t, int R, int N, int K,
-                hipStream_t st, bool zero_first) {
+                hipStream_t st, bool accumulate) {
   const int G = K / 128;
-  int gpw, nsplit;
-  gemv_split(N, G, &gpw, &nsplit);
-  const int use_atomic = nsplit > 1;
-  if (use_atomic && zero_first) {
+  const int nsplit = gemv_nsplit(N, G);
+  const int out_mode = (accumulate || nsplit > 1) ? 1 : 0;
+  if (!accumulate && nsplit > 1) {
     int e = zero_bytes(t, (int64_t)R * N * 8, st);
     if (e) return e;
   }
   const int tasks = ((N + 63) / 64) * nsplit;
   dim3 grid((tasks + 3) / 4), block(256);
-  if (abits == 15)
-    hipLaunchKernelGGL(k_gemv_g128<15>, grid, block, 0, st, x, wp, mp, t, R, N, K, G, gpw, nsplit, use_atomic);
-  else
-    hipLaunchKernelGGL(k_gemv_g128<7>, grid, block, 0, st, x, wp, mp, t, R, N, K, G, gpw, nsplit, use_atomic);
+#define GEMV_GO(AB, VR) \
+  hipLaunchKernelGGL((k_gemv_g128<AB, GEMV_NT != 0, VR>), grid, block, 0, st, x, wp, mp, t, R, N, K, G, nsplit, out_mode)
+  const int vr = R <= 1 ? 1 : (R <= 2 ? 2 : 4);
+  if (abits == 15) {
+    if (vr == 1) GEMV_GO(15, 1); else if (vr == 2) GEMV_GO(15, 2); else GEMV_GO(15, 4);
+  } else {
+    if (vr == 1) GEMV_GO(7, 1); else if (vr == 2) GEMV_GO(7, 2); else GEMV_GO(7, 4);
+  }
+#undef GEMV_GO
   return launch_status("gemv_g128");
 }
 
@@ -201,6 +260,14 @@ extern "C" int exact_gemv_g128(const void* x, int32_t abits, const int8_t* wp, c
   if (e) return e;
   const int rmax = abits == 15 ? 15 : 16;   // one A row is the all-ones colsum row in the A16 mode
   if (R > rmax) return EXACT_E_UNSUPPORTED;
+  return gemv_launch(x, abits, wp, mp, t, R, N, K, as_stream(stream), false);
+}
+
+extern "C" int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
+                                   int32_t R, int32_t N, int32_t K, void* stream) {
+  int e = check_linear(x, abits, wp, mp, t, R, N, K);
+  if (e) return e;
+  if (R > (abits == 15 ? 15 : 16)) return EXACT_E_UNSUPPORTED;
   return gemv_launch(x, abits, wp, mp, t, R, N, K, as_stream(stream), true);
 }
 
@@ -215,7 +282,7 @@ extern "C" int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, c
   if (e) return e;
   for (int r0 = 0; r0 < R; r0 += chunk) {
     const int rr = std::min(chunk, R - r0);
-    e = gemv_launch(reinterpret_cast<const int8_t*>(x) + r0 * xrow, abits, wp, mp, t + (size_t)r0 * N, rr, N, K, st, false);
+    e = gemv_launch(reinterpret_cast<const int8_t*>(x) + r0 * xrow, abits, wp, mp, t + (size_t)r0 * N, rr, N, K, st, true);
     if (e) return e;
   }
   return EXACT_OK;

@@ -16,25 +16,26 @@ U64 = ctypes.c_uint64
 
 # name -> argument types (all return int status except where noted)
 SIGNATURES = {
-    "exact_synth_linear": [U64, U64, I32, I32, P, P, P, I32, I32, P],
+    "exact_synth_linear": [U64, U64, I32, I32, P, P, P, I32, I32, I32, I32, P],
     "exact_synth_vector": [U64, I64, I64, P, I64, P],
-    "exact_pack_linear": [P, P, P, P, I32, I32, P],
+    "exact_pack_linear": [P, P, P, P, I32, I32, I32, I32, P],
     "exact_gemv_g128": [P, I32, P, P, P, I32, I32, I32, P],
+    "exact_gemv_g128_acc": [P, I32, P, P, P, I32, I32, I32, P],
     "exact_gemm_g128": [P, I32, P, P, P, I32, I32, I32, P],
     "exact_requant_group": [P, P, P, P, I32, I32, P],
     "exact_requant_channel": [P, P, P, I32, P, P, I32, I32, P],
     "exact_qrow": [P, I32, P, P, I32, I32, P],
     "exact_irms": [P, P, P, I32, I32, P],
-    "exact_rmsnorm_qrow": [P, P, P, P, I32, P, P, I32, I32, P],
-    "exact_swiglu_qrow": [P, P, P, I32, P, P, I32, I32, P],
+    "exact_rmsnorm_qrow": [P, P, P, P, I32, P, P, I32, I32, I32, P],
+    "exact_swiglu_qrow": [P, P, P, I32, P, P, I32, I32, I32, P],
     "exact_isilu": [P, P, P, I64, P],
     "exact_isig": [P, P, P, I64, P],
     "exact_isoftmax": [P, P, P, P, I32, I32, P],
-    "exact_qkv_rope_cache": [P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, P],
+    "exact_qkv_rope_cache": [P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
     "exact_attention": [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
     "exact_embed": [P, P, P, I32, I32, I32, P],
     "exact_embed_table": [P, P, P, I32, I32, P],
-    "exact_logits_argmax": [P, P, P, P, I32, I32, P],
+    "exact_logits_argmax": [P, P, P, P, I32, I32, I32, P],
     "exact_advance": [P, I32, P],
     "exact_zero": [P, I64, P],
 }

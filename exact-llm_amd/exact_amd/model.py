@@ -44,7 +44,7 @@ class DeviceWeights:
             off, bs = 0, []
             for name, n in parts:
                 kw, km, kb = _lin_keys(seed, name)
-                ops.synth_linear(wp, mp, n, K, kw, km, synth.M_LO, synth.M_HI, thr, n_off=off)
+                ops.synth_linear(wp, mp, n, K, kw, km, synth.M_LO, synth.M_HI, thr, n_off=off, Ntot=N)
                 if bias:
                     bs.append(ops.synth_vector(kb, synth.BIAS[0], synth.BIAS[1], n, device))
                 off += n
@@ -167,8 +167,9 @@ class TModel:
 
     # ---------------------------------------------------------------- linears
     def _lin(self, x, lin, out):
-        """t for a group-mode linear (the caller applies shr(t, 28 - s) + b in the consumer kernel)."""
-        return ops.linear_t(x, self.abits, lin, out)
+        """t for a group-mode linear (the consumer kernel applies shr(t, 28 - s) + b and leaves out zeroed,
+        so decode-sized calls accumulate into it without a separate clear)."""
+        return ops.linear_t(x, self.abits, lin, out, zeroed=True)
 
     def _lin_channel(self, x, s, lin, out):
         """channel mode: y = requant_channel(acc) written over out; the consumer then uses s = 28."""
@@ -187,7 +188,7 @@ class TModel:
         res_t, res_s = None, None
         for li, L in enumerate(self.w.layers):
             cache = self._cache.layers[li]
-            ops.rmsnorm_qrow(ws.x, L["g1"], self.abits, res_t, res_s, ws.xq, ws.s)
+            ops.rmsnorm_qrow(ws.x, L["g1"], self.abits, res_t, res_s, ws.xq, ws.s, clear=group)
             if group:
                 self._lin(ws.xq, L["qkv"], ws.t_qkv)
                 s_qkv, b_qkv = ws.s, L["qkv"].bias
@@ -199,12 +200,13 @@ class TModel:
                     ws.t_qkv[:, off:off + lin.N].copy_(y)
                     off += lin.N
                 s_qkv, b_qkv = ws.s28, None
-            ops.qkv_rope_cache(ws.t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache, ws.qq, ws.sq, H, KV, hd)
+            ops.qkv_rope_cache(ws.t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache, ws.qq, ws.sq, H, KV, hd,
+                               clear=group)
             ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv)
             ops.qrow(ws.att, self.abits, ws.aq, ws.sa)
             if group:
                 self._lin(ws.aq, L["o"], ws.t_o)
-                ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.sa, ws.xq, ws.s)
+                ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.sa, ws.xq, ws.s, clear=True)
             else:
                 self._lin_channel(ws.aq, ws.sa, L["o"], ws.t_o)
                 ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.s28, ws.xq, ws.s)
@@ -212,7 +214,7 @@ class TModel:
                 raise ExactError("MoE blocks run through MoEModel")
             if group:
                 self._lin(ws.xq, L["gateup"], ws.t_gu)
-                ops.swiglu_qrow(ws.t_gu, ws.s, tab.silu, self.abits, ws.hq, ws.sh)
+                ops.swiglu_qrow(ws.t_gu, ws.s, tab.silu, self.abits, ws.hq, ws.sh, clear=True)
                 self._lin(ws.hq, L["down"], ws.t_d)
                 res_t, res_s = ws.t_d, ws.sh
             else:
@@ -224,10 +226,10 @@ class TModel:
                 ops.swiglu_qrow(ws.t_gu, ws.s28, tab.silu, self.abits, ws.hq, ws.sh)
                 self._lin_channel(ws.hq, ws.sh, L["down"], ws.t_d)
                 res_t, res_s = ws.t_d, ws.s28
-        ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s)
+        ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=group)
         if group:
             self._lin(ws.xq, self.w.head, ws.t_head)
-            ops.logits_argmax(ws.t_head, ws.s, ws.logits if want_logits else None, ws.next_ids)
+            ops.logits_argmax(ws.t_head, ws.s, ws.logits if want_logits else None, ws.next_ids, clear=True)
         else:
             self._lin_channel(ws.xq, ws.s, self.w.head, ws.t_head)
             ops.logits_argmax(ws.t_head, ws.s28, ws.logits if want_logits else None, ws.next_ids)

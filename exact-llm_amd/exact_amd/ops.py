@@ -59,26 +59,12 @@ class PackedLinear:
         mp = torch.empty(nb * G * 64, dtype=I16, device=device)
         return wp, mp
 
-    def part(self, n0, n1):
-        """View of output rows [n0, n1) (n0 % 64 == 0): shares the packed storage."""
-        if n0 % 64:
-            raise ExactError("sub-linear must start on a 64-row boundary")
-        nb0, nb1 = n0 // 64, (n1 + 63) // 64
-        b = None if self.bias is None else self.bias[n0:n1]
-        return PackedLinear(self.wp[nb0 * self.G * 8192: nb1 * self.G * 8192], self.mp[nb0 * self.G * 64: nb1 * self.G * 64],
-                            n1 - n0, self.K, b, self.mode)
 
-
-def synth_linear(wp, mp, N, K, kw, km, m_lo, m_hi, thr_dev, n_off=0):
-    """Generate an (N, K) synthetic linear into rows [n_off, n_off + N) of packed buffers."""
-    G = K // 128
-    nb0 = n_off // 64
-    if n_off % 64:
-        raise ExactError("parts of a fused linear must start on 64-row boundaries")
-    w = wp[nb0 * G * 8192:]
-    m = mp[nb0 * G * 64:]
-    _lib.call("exact_synth_linear", ctypes.c_uint64(kw), ctypes.c_uint64(km), m_lo, m_hi, _ptr(thr_dev), _ptr(w), _ptr(m),
-              N, K, _stream())
+def synth_linear(wp, mp, N, K, kw, km, m_lo, m_hi, thr_dev, n_off=0, Ntot=None):
+    """Generate an (N, K) synthetic linear into rows [n_off, n_off + N) of a packed buffer of Ntot rows."""
+    Ntot = N if Ntot is None else Ntot
+    _lib.call("exact_synth_linear", ctypes.c_uint64(kw), ctypes.c_uint64(km), m_lo, m_hi, _ptr(thr_dev), _ptr(wp), _ptr(mp),
+              N, K, n_off, Ntot, _stream())
 
 
 def synth_vector(k, lo, hi, n, device):
@@ -87,17 +73,15 @@ def synth_vector(k, lo, hi, n, device):
     return out
 
 
-def pack_linear(w_kn, m_gn, wp=None, mp=None, n_off=0):
-    """Pack a (K, N) int8 weight and (G, N) int16 scales (device tensors)."""
+def pack_linear(w_kn, m_gn, wp=None, mp=None, n_off=0, Ntot=None):
+    """Pack a (K, N) int8 weight and (G, N) int16 scales (device tensors) into rows [n_off, n_off + N)."""
     K, N = w_kn.shape
     _need(w_kn, I8, "w_kn")
     _need(m_gn, I16, "m_gn")
+    Ntot = N if Ntot is None else Ntot
     if wp is None:
-        wp, mp = PackedLinear.alloc(N, K, w_kn.device)
-    G = K // 128
-    nb0 = n_off // 64
-    _lib.call("exact_pack_linear", _ptr(w_kn), _ptr(m_gn), _ptr(wp[nb0 * G * 8192:]), _ptr(mp[nb0 * G * 64:]), N, K,
-              _stream())
+        wp, mp = PackedLinear.alloc(Ntot, K, w_kn.device)
+    _lib.call("exact_pack_linear", _ptr(w_kn), _ptr(m_gn), _ptr(wp), _ptr(mp), N, K, n_off, Ntot, _stream())
     return wp, mp
 
 
@@ -107,14 +91,24 @@ def gemv_g128(x, abits, lin, out=None):
     return _linear("exact_gemv_g128", x, abits, lin, out)
 
 
+def gemv_g128_acc(x, abits, lin, out):
+    """out (R, N) += sum_g acc_g * M_g (out holds zeros or a running total)."""
+    return _linear("exact_gemv_g128_acc", x, abits, lin, out)
+
+
 def gemm_g128(x, abits, lin, out=None):
     return _linear("exact_gemm_g128", x, abits, lin, out)
 
 
-def linear_t(x, abits, lin, out=None):
-    """Dispatch: GEMV for decode-sized R, GEMM otherwise (TLinG, speed_fair_kaggle.py:735-742)."""
+def linear_t(x, abits, lin, out=None, zeroed=False):
+    """Dispatch: GEMV for decode-sized R, GEMM otherwise (TLinG, speed_fair_kaggle.py:735-742).
+    zeroed: out already holds zeros (left by a clearing consumer), so the GEMV accumulates into it."""
     R = x.shape[0]
-    return gemv_g128(x, abits, lin, out) if R <= (15 if abits == 15 else 16) else gemm_g128(x, abits, lin, out)
+    if R <= (15 if abits == 15 else 16):
+        if zeroed and out is not None:
+            return gemv_g128_acc(x, abits, lin, out)
+        return gemv_g128(x, abits, lin, out)
+    return gemm_g128(x, abits, lin, out)
 
 
 def _linear(fn, x, abits, lin, out):
@@ -161,23 +155,24 @@ def irms(x, g):
     return y
 
 
-def rmsnorm_qrow(x, g, bits=15, res_t=None, res_s=None, xq=None, s=None):
-    """x += rs(res_t, 28 - res_s) (in place) when res_t is given; then qrow(irms(x, g), bits)."""
+def rmsnorm_qrow(x, g, bits=15, res_t=None, res_s=None, xq=None, s=None, clear=False):
+    """x += rs(res_t, 28 - res_s) (in place) when res_t is given; then qrow(irms(x, g), bits).
+    clear: leave res_t zeroed for the next accumulating GEMV."""
     R, D = x.shape
     _need(x, I64, "x")
     xq = torch.empty((R, D), dtype=I16 if bits > 7 else I8, device=x.device) if xq is None else xq
     s = torch.empty(R, dtype=I32, device=x.device) if s is None else s
     _lib.call("exact_rmsnorm_qrow", _ptr(x), _ptr(res_t), _ptr(res_s), _ptr(_need(g, I64, "g", D)), bits, _ptr(xq), _ptr(s),
-              R, D, _stream())
+              R, D, int(clear), _stream())
     return xq, s
 
 
-def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None):
+def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None, clear=False):
     R, N2 = t.shape
     I = N2 // 2
     xq = torch.empty((R, I), dtype=I16 if bits > 7 else I8, device=t.device) if xq is None else xq
     sq = torch.empty(R, dtype=I32, device=t.device) if sq is None else sq
-    _lib.call("exact_swiglu_qrow", _ptr(_need(t, I64, "t")), _ptr(s), _ptr(silu), bits, _ptr(xq), _ptr(sq), R, I, _stream())
+    _lib.call("exact_swiglu_qrow", _ptr(_need(t, I64, "t")), _ptr(s), _ptr(silu), bits, _ptr(xq), _ptr(sq), R, I, int(clear), _stream())
     return xq, sq
 
 
@@ -201,12 +196,12 @@ def isoftmax(sc, expt, n_valid=None):
 
 
 # ----------------------------------------------------------------------------- attention / plumbing
-def qkv_rope_cache(t, s, b, cos, sin, slot, pos, cache, qq, sq, H, KV, hd):
+def qkv_rope_cache(t, s, b, cos, sin, slot, pos, cache, qq, sq, H, KV, hd, clear=False):
     R = t.shape[0]
     kq, sk, v = cache
     Smax = kq.shape[2]
     _lib.call("exact_qkv_rope_cache", _ptr(t), _ptr(s), _ptr(b), _ptr(cos), _ptr(sin), _ptr(slot), _ptr(pos), _ptr(qq),
-              _ptr(sq), _ptr(kq), _ptr(sk), _ptr(v), R, H, KV, hd, Smax, _stream())
+              _ptr(sq), _ptr(kq), _ptr(sk), _ptr(v), R, H, KV, hd, Smax, int(clear), _stream())
 
 
 def attention(qq, sq, cache, slot, pos, expt, out, H, KV, hd, inv):
@@ -231,9 +226,9 @@ def embed_table(lin, V, D):
     return emb
 
 
-def logits_argmax(t, s, lg=None, ids=None):
+def logits_argmax(t, s, lg=None, ids=None, clear=False):
     R, N = t.shape
-    _lib.call("exact_logits_argmax", _ptr(t), _ptr(s), _ptr(lg), _ptr(ids), R, N, _stream())
+    _lib.call("exact_logits_argmax", _ptr(t), _ptr(s), _ptr(lg), _ptr(ids), R, N, int(clear), _stream())
     return lg, ids
 
 

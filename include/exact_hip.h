@@ -9,10 +9,13 @@
  * Data formats
  *   activations  int64 Q16, row-major (R, D)
  *   xq           quantised rows from qrow: int16 (bits 8..15) or int8 (bits <= 7), shifts s int32 (R)
- *   packed linear (N outputs, K inputs, K % 128 == 0, Np = N rounded up to 64, G = K / 128):
- *       wp int8  [Np/64][G][8][64][16]  wp[((nb*G+g)*8+j)*1024 + l*16 + b] = W[n = nb*64+l][k = g*128+j*16+b]
- *       mp int16 [Np/64][G][64]         mp[(nb*G+g)*64 + l] = M[g][n]   (positive group-128 scales)
- *     One 8 KiB tile holds 64 output rows x one 128-wide group; rows n >= N are zero.
+ *   packed linear (N outputs, K inputs, K % 128 == 0, nbs = ceil(N / 64), G = K / 128), tiles in
+ *   group-major order T = g * nbs + nb:
+ *       wp int8  [G][nbs][8][64][16]  wp[(T*8 + j)*1024 + l*16 + b] = W[n = nb*64+l][k = g*128+j*16+b]
+ *       mp int16 [G][nbs][64]         mp[T*64 + l] = M[g][n]   (positive group-128 scales)
+ *     One 8 KiB tile holds 64 output rows x one 128-wide group; rows n >= N are zero. A buffer of Ntot
+ *     rows may stack several linears of the same K (fused q|k|v, gate|up), each at a row offset n_off
+ *     that is a multiple of 64.
  *   t            int64 (R, N): t = sum_g acc_g * M_g, acc_g = sum_{k in g} xq[k] * W[n][k] (exact)
  *   tables       EXP_T (10242 x Q24) and SILU_T / SIG_T (8194 x Q16) as int32 device arrays
  */
@@ -41,7 +44,7 @@ const char* exact_last_error(void);
  * No counterpart in the reference (it quantises downloaded float checkpoints, exact_llm.py:82-88);
  * this is the seeded integer artifact of SPEC.md:7-12 generated on the device. */
 int exact_synth_linear(uint64_t key_w, uint64_t key_m, int32_t m_lo, int32_t m_hi, const uint32_t* thr,
-                       int8_t* wp, int16_t* mp, int32_t N, int32_t K, void* stream);
+                       int8_t* wp, int16_t* mp, int32_t N, int32_t K, int32_t n_off, int32_t Ntot, void* stream);
 
 /* out[i] = lo + (((splitmix64(key, i) >> 32) * (hi - lo)) >> 32), i < n (gains, biases). */
 int exact_synth_vector(uint64_t key, int64_t lo, int64_t hi, int64_t* out, int64_t n, void* stream);
@@ -50,7 +53,7 @@ int exact_synth_vector(uint64_t key, int64_t lo, int64_t hi, int64_t* out, int64
  * (GQLin.M, speed_fair_kaggle.py:717) into the packed layout. Replaces TLinG's wT = w.T.contiguous()
  * and Mg = M.T (speed_fair_kaggle.py:730-731). */
 int exact_pack_linear(const int8_t* w_kn, const int16_t* m_gn, int8_t* wp, int16_t* mp,
-                      int32_t N, int32_t K, void* stream);
+                      int32_t N, int32_t K, int32_t n_off, int32_t Ntot, void* stream);
 
 /* ---- linears ------------------------------------------------------------------------------------
  * Exact group-128 GEMV for decode, R <= 8 rows (one to eight tokens): t[r][n] = sum_g acc_g * M[g][n].
@@ -59,6 +62,11 @@ int exact_pack_linear(const int8_t* w_kn, const int16_t* m_gn, int8_t* wp, int16
  * (experiments/speed_fair_kaggle.py:656-702) and TLinG's R == 1 branch (:735-738), extended to R <= 8. */
 int exact_gemv_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
                     int32_t R, int32_t N, int32_t K, void* stream);
+
+/* Accumulating form: t[r][n] += sum_g acc_g * M[g][n]. No counterpart in the reference; used by fused
+ * decode steps whose consumer kernels leave t zeroed after reading it, so no zero-fill launch is needed. */
+int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
+                        int32_t R, int32_t N, int32_t K, void* stream);
 
 /* Exact group-128 GEMM for prefill (any R): same output as exact_gemv_g128.
  * Replaces TLinG's R > 1 fp64 bmm branch (speed_fair_kaggle.py:739-742) and TLin._acc's
@@ -85,15 +93,17 @@ int exact_irms(const int64_t* x, const int64_t* g, int64_t* y, int32_t R, int32_
 
 /* Fused residual + irms + qrow: if res_t != NULL, x += round_shift(res_t, 28 - res_s[r]) (written back
  * to x); then xq, s = qrow(irms(x, g), bits). Covers exact_llm.py:177-178 (o-proj residual, post-norm),
- * :179-180/166 (down-proj residual, next input norm) and the final norm before the head. */
-int exact_rmsnorm_qrow(int64_t* x, const int64_t* res_t, const int32_t* res_s, const int64_t* g,
-                       int32_t bits, void* xq, int32_t* s, int32_t R, int32_t D, void* stream);
+ * :179-180/166 (down-proj residual, next input norm) and the final norm before the head.
+ * clear_t != 0 leaves res_t zeroed after reading it (ready for the next accumulating GEMV). */
+int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res_s, const int64_t* g,
+                       int32_t bits, void* xq, int32_t* s, int32_t R, int32_t D, int32_t clear_t, void* stream);
 
 /* SwiGLU on a fused gate|up total: g = rs(t[r][n], 28 - s[r]), u = rs(t[r][I + n], 28 - s[r]),
- * h = round_shift(isilu(g) * u, 16); xq, sq = qrow(h, bits). t's gate half is overwritten with h.
+ * h = round_shift(isilu(g) * u, 16); xq, sq = qrow(h, bits). t's gate half is overwritten with h, or all
+ * of t is left zeroed when clear_t != 0.
  * (exact_llm.py:179; isilu exact_llm.py:118-122). */
 int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq,
-                      int32_t* sq, int32_t R, int32_t I, void* stream);
+                      int32_t* sq, int32_t R, int32_t I, int32_t clear_t, void* stream);
 
 /* Elementwise LUT nonlinearities on int64 arrays (isilu exact_llm.py:118-122; isig moe_exact_kaggle.py:420-424). */
 int exact_isilu(const int64_t* x, const int32_t* silu_t, int64_t* y, int64_t n, void* stream);
@@ -110,12 +120,12 @@ int exact_isoftmax(const int64_t* sc, const int32_t* n_valid, const int32_t* exp
  *
  * q/k/v epilogue: y = rs(t, 28 - s[r]) + b for the fused q|k|v total (N = (H + 2 KV) * hd); RoPE on q and
  * k with the Q16 tables at pos[r]; k rows quantised per head (qrow 15) into the cache, v stored as is;
- * q rows quantised per head into qq (R, H, hd) int16 and sq (R, H).
+ * q rows quantised per head into qq (R, H, hd) int16 and sq (R, H); clear_t != 0 leaves t zeroed.
  * (exact_torch.py:144-151; GraphDecoder._step speed_fair_kaggle.py:614-619). */
-int exact_qkv_rope_cache(const int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
+int exact_qkv_rope_cache(int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
                          const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* qq,
                          int32_t* sq, int16_t* kq, int32_t* sk, int64_t* v, int32_t R, int32_t H,
-                         int32_t KV, int32_t hd, int32_t Smax, void* stream);
+                         int32_t KV, int32_t hd, int32_t Smax, int32_t clear_t, void* stream);
 
 /* Integer attention of R query rows against the cache, keys 0..pos[r] of slot[r]:
  * sc = rs((qq . kq) * INV, 32 - sq - sk); p = isoftmax(sc) (Q20); out = rs(p . v, 20), out (R, H*hd) int64.
@@ -135,10 +145,10 @@ int exact_embed(const int32_t* ids, const int32_t* emb, int64_t* x, int32_t R, i
  * (round half to even, numpy rint), i.e. rint(e * 2^16) of the float row e = W*M/2^28. */
 int exact_embed_table(const int8_t* wp, const int16_t* mp, int32_t* emb, int32_t V, int32_t D, void* stream);
 
-/* Logits and greedy tokens: lg = rs(t, 28 - s[r]) (lg may alias t); ids[r] = first argmax of lg[r]
- * (exact_llm.py:180,267). lg or ids may be NULL to skip. */
-int exact_logits_argmax(const int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int32_t R,
-                        int32_t N, void* stream);
+/* Logits and greedy tokens: lg = rs(t, 28 - s[r]) (lg may alias t unless clear_t); ids[r] = first argmax
+ * of lg[r] (exact_llm.py:180,267). lg or ids may be NULL to skip; clear_t != 0 leaves t zeroed. */
+int exact_logits_argmax(int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int32_t R,
+                        int32_t N, int32_t clear_t, void* stream);
 
 /* pos[r] += 1 for r < R (advances a decode step inside a captured graph; GraphDecoder.step :645). */
 int exact_advance(int32_t* pos, int32_t R, void* stream);
