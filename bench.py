@@ -99,24 +99,32 @@ def gemv_pass(args):
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
 
-    # per-shape launch durations: events around NL launches over distinct weights (no cache reuse)
+    # per-shape launch durations: one HIP graph of NL launches over distinct weights (no cache reuse),
+    # timed with HIP events on the launch stream
     per = {}
     for k, (N, K) in list(shapes.items()) + [("head", (cfg.V, D))]:
-        reps = 3
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        a.record(st)
-        for _ in range(reps):
+        def shape_step():
             if k == "head":
                 ops.gemv_g128_acc(x_d, 7, head, out_head)
             else:
                 for L, o in zip(layers, outs):
                     ops.gemv_g128_acc(xin[k], 7, L[k], o[k])
+        sg = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(sg):
+            shape_step()
+        sg.replay()
+        reps = 5
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(st)
+        for _ in range(reps):
+            sg.replay()
         b.record(st)
         torch.cuda.synchronize()
         n = reps * (1 if k == "head" else NL)
         us = a.elapsed_time(b) * 1000.0 / n
         per[k] = dict(N=N, K=K, us=round(us, 2), GBps=round(nbytes(N, K) / us / 1e3, 1))
+        del sg
     del layers, head
     torch.cuda.empty_cache()
     return dict(ms=ms, wall=wall, pass_bytes=pass_bytes, per=per)
