@@ -1,0 +1,317 @@
+// Exact group-128 int8 GEMM for prefill on CDNA4 matrix cores (gfx950).
+//
+//   t[m][n] = sum_g M[g][n] * sum_{k in g} xq[m][k] * W[n][k]          (SPEC.md:18; GQLin)
+//
+// Block tile (WM x 64) x (WN x 64): WM x WN waves of 64 x 64 outputs, one 128-wide group per k-step.
+//   * Operand tiles move global -> LDS with gfx950's direct loads (global_load_lds_dwordx4: each
+//     lane's 16 bytes land at lds_base + 16 * lane), S stages deep, so S - 1 groups are in flight
+//     while one is computed. B is the packed weight layout itself (WN 8 KiB tiles per group).
+//   * v_mfma_i32_32x32x32_i8 produces the exact int32 group accumulator of each 32 x 32 sub-tile
+//     (|acc| < 2^29). The rescale t += acc * M[g][n] is an exact 64-bit integer multiply-add.
+//   * Within a group the four sub-tiles of a wave run their MFMA chains one after another; each
+//     finished sub-tile's rescale is interleaved with the next sub-tile's chain, so the VALU work
+//     and the matrix cores overlap.
+// int8 activations (A8): A rows sit row-major in LDS with the 16-byte chunk index XOR-swizzled by
+// (row >> 1) & 7 (conflict-free 16-row fragment reads).
+// int16 activations (A16, the spec): raw int16 rows in LDS, chunk index XOR-swizzled by row & 15; each
+// fragment is split into int8 digits hi = x >> 8 and lo = (x & 255) - 128 (exact_torch.py:101-102)
+// and acc = 256 hi.W + lo.W + 128 colsum(W): the hi pass accumulates, is shifted by 8, and the lo pass
+// accumulates on top; 128 colsum(W) M is a per-column term added once per group.
+//
+// Replaces TLinG's fp64 bmm branch (experiments/speed_fair_kaggle.py:739-742) and the cuBLASLt
+// torch._int_mm passes of TLin._acc (exact_torch.py:94-119).
+#include "exact_common.h"
+#include "abi_util.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+namespace exact {
+
+int zero_bytes(void* dst, int64_t nbytes, hipStream_t st);
+
+// Block = (WM x 64) x (WN x 64): WM x WN waves of 64 x 64 outputs; S LDS stages.
+template <int ABITS, int WM, int WN, int S>
+struct GemmCfg {
+  static constexpr int BM = WM * 64, BN = WN * 64, NT = WN;   // NT packed weight tiles per group
+  static constexpr int WAVES = WM * WN, THREADS = WAVES * 64;
+  static constexpr int ROWB = ABITS == 15 ? 256 : 128;     // LDS bytes per A row per group
+  static constexpr int A_BYTES = BM * ROWB;
+  static constexpr int B_BYTES = NT * 8192;
+  static constexpr int STAGE = A_BYTES + B_BYTES + 1024;   // + 1 KiB for the BN int16 scales (DMA granule)
+  static constexpr int A_KB_PER_WAVE = A_BYTES / 1024 / WAVES;
+  static constexpr int B_KB_PER_WAVE = B_BYTES / 1024 / WAVES;
+  static constexpr int DMA_PER_GROUP = A_KB_PER_WAVE + B_KB_PER_WAVE;   // per wave (wave 0 issues one more)
+  static_assert(S >= 2 && S <= 4, "2 to 4 stages");
+  static_assert(A_BYTES % (1024 * WAVES) == 0 && B_BYTES % (1024 * WAVES) == 0, "tiles split evenly over waves");
+  static_assert(BN * 2 <= 1024 && NT * 8 <= 64, "scales of one group fit one 1 KiB copy");
+};
+
+// LDS byte offset of 16-byte chunk c of A row r
+template <int ABITS>
+__device__ __forceinline__ int a_off(int r, int c) {
+  return ABITS == 15 ? r * 256 + ((c ^ (r & 15)) << 4) : r * 128 + ((c ^ ((r >> 1) & 7)) << 4);
+}
+
+// s_waitcnt immediate: vmcnt <= n, expcnt and lgkmcnt not waited on (gfx9 encoding)
+#define VMCNT_LE(n) ((((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14)))
+
+// int16 -> (hi, lo - 128) int8 digits of 16 values held in two 16-byte chunks
+__device__ __forceinline__ void split16(v4i p0, v4i p1, v4i& hi, v4i& lo) {
+  hi[0] = __builtin_amdgcn_perm(p0[1], p0[0], 0x07050301u);
+  hi[1] = __builtin_amdgcn_perm(p0[3], p0[2], 0x07050301u);
+  hi[2] = __builtin_amdgcn_perm(p1[1], p1[0], 0x07050301u);
+  hi[3] = __builtin_amdgcn_perm(p1[3], p1[2], 0x07050301u);
+  lo[0] = __builtin_amdgcn_perm(p0[1], p0[0], 0x06040200u) ^ 0x80808080;
+  lo[1] = __builtin_amdgcn_perm(p0[3], p0[2], 0x06040200u) ^ 0x80808080;
+  lo[2] = __builtin_amdgcn_perm(p1[1], p1[0], 0x06040200u) ^ 0x80808080;
+  lo[3] = __builtin_amdgcn_perm(p1[3], p1[2], 0x06040200u) ^ 0x80808080;
+}
+
+template <int ABITS, int WM, int WN, int S>
+__global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_g128(const void* __restrict__ xv, const int8_t* __restrict__ wp,
+                                                      const int16_t* __restrict__ mp, int64_t* __restrict__ t, int M,
+                                                      int N, int K, int G, int nbs, int tiles_m, int tiles_n,
+                                                      int ksplit, int use_atomic) {
+  using C = GemmCfg<ABITS, WM, WN, S>;
+  extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int l32 = lane & 31, lh = lane >> 5;
+
+  // XCD-aware order: the blocks of one XCD take consecutive logical tiles (same column block,
+  // increasing row block), so each XCD's L2 streams its own slice of the weights once.
+  const int nblk = tiles_m * tiles_n * ksplit;
+  const int per_xcd = (nblk + 7) / 8;
+  const int lb = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (lb >= nblk) return;
+  const int kz = lb / (tiles_m * tiles_n);
+  const int rem = lb - kz * tiles_m * tiles_n;
+  const int bn = rem / tiles_m, bm = rem - bn * tiles_m;
+  const int g0 = (int)(((int64_t)kz * G) / ksplit), g1 = (int)(((int64_t)(kz + 1) * G) / ksplit);
+  const int row0 = bm * C::BM, nb0 = bn * C::NT;
+  const size_t xrow = (size_t)K * (ABITS == 15 ? 2 : 1);
+  const int8_t* xb = reinterpret_cast<const int8_t*>(xv);
+
+  // direct global -> LDS copies of group g into stage stg (rows past M / tiles past nbs read a valid
+  // neighbour; those outputs are never stored)
+  auto issue = [&](int g, int stg) {
+    int8_t* sA = smem + stg * C::STAGE;
+    int8_t* sB = sA + C::A_BYTES;
+#pragma unroll
+    for (int i = 0; i < C::A_KB_PER_WAVE; ++i) {
+      const int seg = wave * C::A_KB_PER_WAVE + i;          // 1 KiB LDS segment
+      int r, c;
+      if (ABITS == 15) { r = seg * 4 + (lane >> 4); c = (lane & 15) ^ (r & 15); }
+      else { r = seg * 8 + (lane >> 3); c = (lane & 7) ^ ((r >> 1) & 7); }
+      const int gr = row0 + r < M ? row0 + r : M - 1;
+      const int8_t* src = xb + (size_t)gr * xrow + (size_t)g * C::ROWB + c * 16;
+      int8_t* dst = sA + seg * 1024;
+      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_KB_PER_WAVE; ++i) {
+      const int seg = wave * C::B_KB_PER_WAVE + i;          // tile seg / 8, chunk seg % 8
+      const int nb = nb0 + (seg >> 3) < nbs ? nb0 + (seg >> 3) : nbs - 1;
+      const int8_t* src = wp + tile_index(nb, g, nbs, G) * 8192 + (seg & 7) * 1024 + lane * 16;
+      int8_t* dst = sB + seg * 1024;
+      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+    }
+    if (wave == 0) {   // scales: lanes < 8 NT fetch the tiles' 128-byte rows, the rest refetch into padding
+      const int ll = lane % (C::NT * 8);
+      const int nb = nb0 + (ll >> 3) < nbs ? nb0 + (ll >> 3) : nbs - 1;
+      const int8_t* src = reinterpret_cast<const int8_t*>(mp + tile_index(nb, g, nbs, G) * 64) + (ll & 7) * 16;
+      int8_t* dst = sB + C::B_BYTES;
+      __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+    }
+  };
+
+  int64_t acc[2][2][16];       // [row sub-tile][col sub-tile][register] running totals
+  int64_t colc[2] = {0, 0};    // A16: sum_g 128 colsum_g M_g for the lane's two columns
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0;
+
+  // One group from LDS stage stg: all A / B fragments of the group are read first, then the four
+  // 32 x 32 sub-tiles run their MFMA chains one after the other; each finished sub-tile is rescaled
+  // (t += acc * M, 64-bit) while the next sub-tile's chain occupies the matrix cores.
+  auto group = [&](int stg) {
+    const int8_t* sA = smem + stg * C::STAGE;
+    const int8_t* sB = sA + C::A_BYTES;
+    const int16_t* sM = reinterpret_cast<const int16_t*>(sB + C::B_BYTES);
+    v4i bf[2][4], ah[2][4], al[2][4];
+    int mcol[2], cs[2] = {0, 0};
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int n = wn * 64 + b * 32 + l32;
+      mcol[b] = sM[n];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        bf[b][ks] = *reinterpret_cast<const v4i*>(sB + (n >> 6) * 8192 + (ks * 2 + lh) * 1024 + (n & 63) * 16);
+        if (ABITS == 15) {
+#pragma unroll
+          for (int d = 0; d < 4; ++d) cs[b] = __builtin_amdgcn_sdot4(bf[b][ks][d], 0x01010101, cs[b], false);
+        }
+      }
+    }
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int r = wm * 64 + a * 32 + l32;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int ch = ks * 2 + lh;                      // 16-byte int8 chunk of the 128-k group
+        if (ABITS == 15) {
+          const v4i p0 = *reinterpret_cast<const v4i*>(sA + a_off<15>(r, 2 * ch));
+          const v4i p1 = *reinterpret_cast<const v4i*>(sA + a_off<15>(r, 2 * ch + 1));
+          split16(p0, p1, ah[a][ks], al[a][ks]);
+        } else {
+          ah[a][ks] = *reinterpret_cast<const v4i*>(sA + a_off<7>(r, ch));
+        }
+      }
+    }
+    // sub-tile t's MFMA chain runs while sub-tile t - 1 is rescaled (the scheduling groups below pin
+    // that interleave: one MFMA, then eight VALU instructions of the previous sub-tile's rescale)
+    v16i cprev = {};
+#pragma unroll
+    for (int tile = 0; tile < 5; ++tile) {
+      v16i c = {};
+      if (tile < 4) {
+        const int a = tile >> 1, b = tile & 1;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) c = __builtin_amdgcn_mfma_i32_32x32x32_i8(ah[a][ks], bf[b][ks], c, 0, 0, 0);
+        if (ABITS == 15) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) c[i] <<= 8;
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) c = __builtin_amdgcn_mfma_i32_32x32x32_i8(al[a][ks], bf[b][ks], c, 0, 0, 0);
+        }
+      }
+      if (tile > 0) {
+        const int a = (tile - 1) >> 1, b = (tile - 1) & 1;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[a][b][i] += (int64_t)cprev[i] * (int64_t)mcol[b];
+      }
+      cprev = c;
+    }
+    // keep every rescale inside this group's block: without a use here the compiler sinks them past
+    // the block barrier, where they no longer overlap the matrix-core work
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int i = 0; i < 16; i += 4)
+          asm volatile("" ::"v"(acc[a][b][i]), "v"(acc[a][b][i + 1]), "v"(acc[a][b][i + 2]), "v"(acc[a][b][i + 3]));
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);          // fragment reads
+#pragma unroll
+    for (int k = 0; k < (ABITS == 15 ? 8 : 4); ++k) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+    for (int t = 1; t < 4; ++t)
+#pragma unroll
+      for (int k = 0; k < (ABITS == 15 ? 8 : 4); ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // one MFMA of sub-tile t
+        __builtin_amdgcn_sched_group_barrier(0x002, ABITS == 15 ? 6 : 8, 0);   // rescale of sub-tile t - 1
+      }
+    if (ABITS == 15) {
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int full = cs[b] + __shfl_xor(cs[b], 32, 64);   // the column's other 64 k
+        colc[b] += (int64_t)(128 * full) * (int64_t)mcol[b];
+      }
+    }
+  };
+  auto wait_next = [&](int g) {   // group g + 1 landed in LDS (later groups may stay in flight); block sync
+    const int last = g + S - 1 < g1 - 1 ? g + S - 1 : g1 - 1;
+    const int after = last - (g + 1);
+    if (after >= 2) __builtin_amdgcn_s_waitcnt(VMCNT_LE(2 * C::DMA_PER_GROUP));
+    else if (after == 1) __builtin_amdgcn_s_waitcnt(VMCNT_LE(C::DMA_PER_GROUP));
+    else __builtin_amdgcn_s_waitcnt(VMCNT_LE(0));
+    // a plain barrier: __syncthreads() would also drain the later groups' copies (a full fence)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  if (g0 < g1) {
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i)
+      if (g0 + i < g1) issue(g0 + i, i);
+    wait_next(g0 - 1);
+    for (int g = g0; g < g1; ++g) {
+      if (g + S - 1 < g1) issue(g + S - 1, (g + S - 1 - g0) % S);
+      group((g - g0) % S);
+      wait_next(g);
+    }
+  }
+
+  // C layout of v_mfma_i32_32x32x32_i8: lane l holds column l % 32 and rows 8 (i / 4) + 4 (l / 32) + i % 4
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int col = nb0 * 64 + wn * 64 + b * 32 + l32;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = row0 + wm * 64 + a * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
+        if (row < M && col < N) {
+          const int64_t val = acc[a][b][i] + colc[b];
+          int64_t* dst = t + (size_t)row * N + col;
+          if (use_atomic) atomicAdd(reinterpret_cast<unsigned long long*>(dst), (unsigned long long)val);
+          else *dst = val;
+        }
+      }
+  }
+}
+
+template <int ABITS, int WM, int WN, int S>
+static int gemm_launch(const void* x, const int8_t* wp, const int16_t* mp, int64_t* t, int M, int N, int K,
+                       hipStream_t st, int ksplit_req) {
+  using C = GemmCfg<ABITS, WM, WN, S>;
+  static bool attr_set = false;
+  const size_t lds = S * (size_t)C::STAGE;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_g128<ABITS, WM, WN, S>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    attr_set = true;
+  }
+  const int G = K / 128, nbs = (N + 63) / 64;
+  const int tiles_m = (M + C::BM - 1) / C::BM, tiles_n = (nbs + C::NT - 1) / C::NT;
+  int ksplit = ksplit_req;
+  if (ksplit <= 0) {   // split K when the output tiles alone cannot fill the 256 CUs
+    ksplit = 1;
+    while (tiles_m * tiles_n * ksplit < 400 && G / (ksplit * 2) >= 8) ksplit *= 2;
+  }
+  if (ksplit > G) ksplit = G;
+  const int use_atomic = ksplit > 1;
+  if (use_atomic) {
+    int e = zero_bytes(t, (int64_t)M * N * 8, st);
+    if (e) return e;
+  }
+  const int nblk = tiles_m * tiles_n * ksplit;
+  const int grid = ((nblk + 7) / 8) * 8;
+  hipLaunchKernelGGL((k_gemm_g128<ABITS, WM, WN, S>), dim3(grid), dim3(C::THREADS), lds, st, x, wp, mp, t, M, N, K, G, nbs,
+                     tiles_m, tiles_n, ksplit, use_atomic);
+  return launch_status("gemm_g128");
+}
+
+#ifndef GEMM_KSPLIT
+#define GEMM_KSPLIT 0
+#endif
+// (waves along M, waves along N, LDS stages)
+#ifndef GEMM_A8_CFG
+#define GEMM_A8_CFG 4, 2, 2
+#endif
+#ifndef GEMM_A16_CFG
+#define GEMM_A16_CFG 2, 2, 3
+#endif
+
+int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, int64_t* t, int M, int N, int K,
+              hipStream_t st) {
+  return abits == 15 ? gemm_launch<15, GEMM_A16_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT)
+                     : gemm_launch<7, GEMM_A8_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
+}
+
+}  // namespace exact

@@ -214,6 +214,9 @@ static int gemv_nsplit(int N, int G) {
 
 // accumulate: t += x.W (t holds the caller's running total, e.g. zeros left by a consumer kernel);
 // otherwise t is overwritten (zero-filled first when the row blocks are split).
+int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, int64_t* t, int M, int N, int K,
+              hipStream_t st);
+
 int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, int64_t* t, int R, int N, int K,
                 hipStream_t st, bool accumulate) {
   const int G = K / 128;
@@ -275,15 +278,6 @@ extern "C" int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, c
                                int32_t N, int32_t K, void* stream) {
   int e = check_linear(x, abits, wp, mp, t, R, N, K);
   if (e) return e;
-  const int chunk = abits == 15 ? 15 : 16;
-  const size_t xrow = (size_t)K * (abits == 15 ? 2 : 1);
-  hipStream_t st = as_stream(stream);
-  e = zero_bytes(t, (int64_t)R * N * 8, st);
-  if (e) return e;
-  for (int r0 = 0; r0 < R; r0 += chunk) {
-    const int rr = std::min(chunk, R - r0);
-    e = gemv_launch(reinterpret_cast<const int8_t*>(x) + r0 * xrow, abits, wp, mp, t + (size_t)r0 * N, rr, N, K, st, true);
-    if (e) return e;
-  }
-  return EXACT_OK;
+  if (R <= (abits == 15 ? 15 : 16)) return gemv_launch(x, abits, wp, mp, t, R, N, K, as_stream(stream), false);
+  return gemm_mfma(x, abits, wp, mp, t, R, N, K, as_stream(stream));
 }
