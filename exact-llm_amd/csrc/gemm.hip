@@ -266,6 +266,211 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_g128(const void* __res
   }
 }
 
+// a copy of x the compiler cannot see through (keeps cheap per-lane arithmetic inside a loop)
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// dword 3 of a raw buffer resource (32-bit untyped data, no swizzle)
+#define BUF_DW3 0x00020000
+#define LDS __attribute__((address_space(3)))
+
+// s_waitcnt immediate: vmcnt <= vm and lgkmcnt <= lg (gfx9 encoding; expcnt not waited on)
+#define WAITCNT(vm, lg) ((((vm) & 15) | (7 << 4) | (((lg) & 15) << 8) | ((((vm) >> 4) & 3) << 14)))
+
+// A8 kernel with the operand fragments software-pipelined across groups. Per wave and group the four
+// 32 x 32 sub-tiles run in the order (0,0) (0,1) (1,0) (1,1); each chain of four MFMAs is interleaved
+// with the LDS reads the next chains need and with the rescale of the chain before it:
+//   chain (0,0): read B1 (this group)       rescale (1,1) of the previous group
+//   chain (0,1): read A1 (this group)       rescale (0,0)
+//   -- wait until group g + 1 has landed, block barrier, start the copy of group g + S --
+//   chain (1,0): read A0 (group g + 1)      rescale (0,1)
+//   chain (1,1): read B0 + scales (g + 1)   rescale (1,0)
+// so one barrier per group, and every LDS read overlaps matrix-core work.
+template <int WM, int WN, int S>
+__global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __restrict__ xb, const int8_t* __restrict__ wp,
+                                                     const int16_t* __restrict__ mp, int64_t* __restrict__ t, int M,
+                                                     int N, int K, int G, int nbs, int tiles_m, int tiles_n,
+                                                     int ksplit, int use_atomic) {
+  using C = GemmCfg<7, WM, WN, S>;
+  static_assert(EXACT_TILE_GN, "the block's tiles of one group are contiguous in the group-major layout");
+  static_assert(C::BN == 128, "one dword copy per lane covers the block's 128 scales");
+  constexpr int SM_BYTES = C::WAVES * 256;                  // each wave keeps its own copy of the scales
+  constexpr int STAGE = C::A_BYTES + C::B_BYTES + SM_BYTES;
+  constexpr int DPG = C::A_KB_PER_WAVE + C::B_KB_PER_WAVE + 1;   // copies per wave per group
+  extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int l32 = lane & 31, lh = lane >> 5;
+
+  const int nblk = tiles_m * tiles_n * ksplit;
+  const int per_xcd = (nblk + 7) / 8;
+  const int lb = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (lb >= nblk) return;
+  const int kz = lb / (tiles_m * tiles_n);
+  const int rem = lb - kz * tiles_m * tiles_n;
+  const int bn = rem / tiles_m, bm = rem - bn * tiles_m;
+  const int g0 = (int)(((int64_t)kz * G) / ksplit), g1 = (int)(((int64_t)(kz + 1) * G) / ksplit);
+  const int row0 = bm * C::BM, nb0 = bn * C::NT;
+
+  // The per-lane addresses below are recomputed from an opaque copy of the lane id in every group:
+  // hoisted out of the loop they would need registers the running totals leave no room for.
+  const int ncol = (nbs - nb0) * 64;                        // valid packed columns from nb0 on
+  // buffer resources: 32-bit per-lane offsets, the group and the block enter as scalar offsets
+  const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, (int)((uint32_t)M * (uint32_t)K), BUF_DW3);
+  const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc((void*)wp, (short)0, -1, BUF_DW3);
+  const __amdgpu_buffer_rsrc_t rM = __builtin_amdgcn_make_buffer_rsrc((void*)mp, (short)0, -1, BUF_DW3);
+  auto issue = [&](int g, int stg, int ln) {
+    int8_t* sA = smem + stg * STAGE;
+    int8_t* sB = sA + C::A_BYTES;
+    const int tile0 = g * nbs + nb0;
+#pragma unroll
+    for (int i = 0; i < C::A_KB_PER_WAVE; ++i) {
+      const int seg = wave * C::A_KB_PER_WAVE + i;          // 1 KiB LDS segment = 8 rows x 128 bytes
+      const int r = seg * 8 + (ln >> 3), c = (ln & 7) ^ ((r >> 1) & 7);
+      const int gr = row0 + r < M ? row0 + r : M - 1;       // rows past M read a valid row, never stored
+      const uint32_t aoff = (uint32_t)gr * (uint32_t)K + (uint32_t)(c * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (LDS void*)(sA + seg * 1024), 16, (int)aoff, g * 128, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_KB_PER_WAVE; ++i) {
+      const int seg = wave * C::B_KB_PER_WAVE + i;          // tile seg / 8, 1 KiB chunk seg % 8
+      const int tl = nb0 + (seg >> 3) < nbs ? (seg >> 3) : nbs - 1 - nb0;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (LDS void*)(sB + seg * 1024), 16, ln * 16,
+                                               (tile0 + tl) * 8192 + (seg & 7) * 1024, 0, 0);
+    }
+    const int moff = (2 * ln < ncol ? 2 * ln : ncol - 2) * 2;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rM, (LDS void*)(sB + C::B_BYTES + wave * 256), 4, moff, tile0 * 128, 0, 0);
+  };
+  // fragment reads; A chunk ks * 2 + lh of row r sits at a_off(r, lh) ^ (ks << 5) (XOR swizzle)
+  auto readA = [&](v4i (&f)[4], int stg, int a, int ln) {
+    const int off = a_off<7>(wm * 64 + a * 32 + (ln & 31), ln >> 5);
+    const int8_t* base = smem + stg * STAGE + (off & ~127);
+    const int cb = off & 127;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) f[ks] = *reinterpret_cast<const v4i*>(base + (cb ^ (ks << 5)));
+  };
+  auto readB = [&](v4i (&f)[4], int stg, int b, int ln) {
+    const int8_t* base = smem + stg * STAGE + C::A_BYTES + wn * 8192 + (ln >> 5) * 1024 + (b * 32 + (ln & 31)) * 16;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) f[ks] = *reinterpret_cast<const v4i*>(base + ks * 2048);
+  };
+  auto readM = [&](int stg, int b, int ln) {
+    return (int)*reinterpret_cast<const int16_t*>(smem + stg * STAGE + C::A_BYTES + C::B_BYTES + wave * 256 +
+                                                  (wn * 64 + b * 32 + (ln & 31)) * 2);
+  };
+  auto chain = [&](const v4i (&a)[4], const v4i (&b)[4]) {
+    v16i c = {};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[ks], b[ks], c, 0, 0, 0);
+    return c;
+  };
+  int64_t acc[2][2][16];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0;
+  // t += c * m, pinned in place: without a use here the compiler sinks the multiply-adds past the next
+  // barrier, where they no longer overlap the matrix-core work
+  auto rescale = [&](int64_t (&ac)[16], const v16i& c, int m_) {
+    const int m = opaque(m_);   // a plain 32-bit value here, so each product is one v_mad_i64_i32
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ac[i] += (int64_t)c[i] * (int64_t)m;
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) asm volatile("" ::"v"(ac[i]), "v"(ac[i + 1]), "v"(ac[i + 2]), "v"(ac[i + 3]));
+  };
+  // one chain of 4 MFMAs interleaved with `reads` LDS reads and the 16 rescale multiply-adds
+#define PIPE_PATTERN(reads)                                                                    \
+  do {                                                                                         \
+    _Pragma("unroll") for (int k_ = 0; k_ < 4; ++k_) {                                         \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                       \
+      if (k_ < (reads)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                      \
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                                       \
+    }                                                                                          \
+  } while (0)
+
+  if (g0 < g1) {
+    const int nst = g1 - g0 < S ? g1 - g0 : S;
+    for (int i = 0; i < nst; ++i) issue(g0 + i, i, opaque(lane));
+    // group g0 landed: the later groups' copies may stay in flight
+    if (nst >= 4) __builtin_amdgcn_s_waitcnt(WAITCNT(3 * DPG, 15));
+    else if (nst == 3) __builtin_amdgcn_s_waitcnt(WAITCNT(2 * DPG, 15));
+    else if (nst == 2) __builtin_amdgcn_s_waitcnt(WAITCNT(DPG, 15));
+    else __builtin_amdgcn_s_waitcnt(WAITCNT(0, 15));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    v4i A0[4], B0[4], A1[4], B1[4];
+    readA(A0, 0, 0, lane);
+    readB(B0, 0, 0, lane);
+    int m0 = readM(0, 0, lane), m1 = readM(0, 1, lane);
+    v16i cp = {};
+    int mprev = 0;
+    int stg = 0;
+    for (int g = g0; g < g1; ++g) {
+      const int ln = opaque(lane);
+      const int nstg = stg + 1 == S ? 0 : stg + 1;
+      readB(B1, stg, 1, ln);
+      const v16i c00 = chain(A0, B0);
+      rescale(acc[1][1], cp, mprev);
+      PIPE_PATTERN(4);
+      __builtin_amdgcn_sched_barrier(0);
+      readA(A1, stg, 1, ln);
+      const v16i c01 = chain(A0, B1);
+      rescale(acc[0][0], c00, m0);
+      PIPE_PATTERN(4);
+      // all of this wave's reads of stage stg are done; group g + 1 has landed; then stage stg is
+      // free for group g + S
+      const int ahead = (g1 - 1 < g + S - 1 ? g1 - 1 : g + S - 1) - (g + 1);   // groups in flight after g + 1
+      if (ahead >= 2) __builtin_amdgcn_s_waitcnt(WAITCNT(2 * DPG, 0));
+      else if (ahead == 1) __builtin_amdgcn_s_waitcnt(WAITCNT(DPG, 0));
+      else __builtin_amdgcn_s_waitcnt(WAITCNT(0, 0));
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (g + S < g1) issue(g + S, stg, ln);
+      readA(A0, nstg, 0, ln);
+      const v16i c10 = chain(A1, B0);
+      rescale(acc[0][1], c01, m1);
+      PIPE_PATTERN(4);
+      __builtin_amdgcn_sched_barrier(0);
+      readB(B0, nstg, 0, ln);
+      const int mn0 = readM(nstg, 0, ln), mn1 = readM(nstg, 1, ln);
+      const v16i c11 = chain(A1, B1);
+      rescale(acc[1][0], c10, m0);
+      PIPE_PATTERN(4);
+      cp = c11;
+      mprev = m1;
+      m0 = mn0;
+      m1 = mn1;
+      stg = nstg;
+    }
+    rescale(acc[1][1], cp, mprev);
+  }
+#undef PIPE_PATTERN
+
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int col = nb0 * 64 + wn * 64 + b * 32 + l32;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = row0 + wm * 64 + a * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
+        if (row < M && col < N) {
+          const int64_t val = acc[a][b][i];
+          int64_t* dst = t + (size_t)row * N + col;
+          if (use_atomic) atomicAdd(reinterpret_cast<unsigned long long*>(dst), (unsigned long long)val);
+          else *dst = val;
+        }
+      }
+  }
+}
+
 template <int ABITS, int WM, int WN, int S>
 static int gemm_launch(const void* x, const int8_t* wp, const int16_t* mp, int64_t* t, int M, int N, int K,
                        hipStream_t st, int ksplit_req) {
@@ -308,10 +513,50 @@ static int gemm_launch(const void* x, const int8_t* wp, const int16_t* mp, int64
 #define GEMM_A16_CFG 2, 2, 3
 #endif
 
+#ifndef GEMM_A8P_CFG
+#define GEMM_A8P_CFG 4, 2, 3
+#endif
+
+template <int WM, int WN, int S>
+static int gemm_launch_a8p(const void* x, const int8_t* wp, const int16_t* mp, int64_t* t, int M, int N, int K,
+                           hipStream_t st, int ksplit_req) {
+  using C = GemmCfg<7, WM, WN, S>;
+  static bool attr_set = false;
+  const size_t lds = S * (size_t)(C::A_BYTES + C::B_BYTES + C::WAVES * 256);
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_a8p<WM, WN, S>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    attr_set = true;
+  }
+  const int G = K / 128, nbs = (N + 63) / 64;
+  const int tiles_m = (M + C::BM - 1) / C::BM, tiles_n = (nbs + C::NT - 1) / C::NT;
+  int ksplit = ksplit_req;
+  if (ksplit <= 0) {
+    ksplit = 1;
+    while (tiles_m * tiles_n * ksplit < 400 && G / (ksplit * 2) >= 8) ksplit *= 2;
+  }
+  if (ksplit > G) ksplit = G;
+  const int use_atomic = ksplit > 1;
+  if (use_atomic) {
+    int e = zero_bytes(t, (int64_t)M * N * 8, st);
+    if (e) return e;
+  }
+  const int nblk = tiles_m * tiles_n * ksplit;
+  const int grid = ((nblk + 7) / 8) * 8;
+  hipLaunchKernelGGL((k_gemm_a8p<WM, WN, S>), dim3(grid), dim3(C::THREADS), lds, st,
+                     reinterpret_cast<const int8_t*>(x), wp, mp, t, M, N, K, G, nbs, tiles_m, tiles_n, ksplit, use_atomic);
+  return launch_status("gemm_g128");
+}
+
+#ifndef GEMM_A8P
+#define GEMM_A8P 1
+#endif
+
 int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, int64_t* t, int M, int N, int K,
               hipStream_t st) {
-  return abits == 15 ? gemm_launch<15, GEMM_A16_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT)
-                     : gemm_launch<7, GEMM_A8_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
+  if (abits == 15) return gemm_launch<15, GEMM_A16_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
+  if (GEMM_A8P && (int64_t)M * K < (1LL << 32)) return gemm_launch_a8p<GEMM_A8P_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
+  return gemm_launch<7, GEMM_A8_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
 }
 
 }  // namespace exact
