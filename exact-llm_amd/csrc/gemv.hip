@@ -45,9 +45,10 @@ struct GroupRegs {
   int m[4];
 };
 
+// xrow: this lane's activation row (any valid row when the lane's row is unused); valid: row < R
 template <int ABITS, bool NT>
 __device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
-                                           const void* __restrict__ xv, size_t tile, int g, int R, int K, int row, int c) {
+                                           const int8_t* __restrict__ xrow, bool valid, size_t tile, int g, int row, int c) {
   // issue order = use order (scales are read last but are tiny; tiles last so waiting on them drains the group)
   const int16_t* ms = mp + tile * 64 + row;
 #pragma unroll
@@ -55,20 +56,20 @@ __device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restri
   const int kb = g * 128 + 16 * c;
   const v4i zero = {0, 0, 0, 0};
   if (ABITS == 15) {
-    const int16_t* xp = reinterpret_cast<const int16_t*>(xv) + (size_t)(row < R ? row : 0) * K + kb;
+    const int16_t* xp = reinterpret_cast<const int16_t*>(xrow) + kb;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       G_.xa[2 * h] = *reinterpret_cast<const v4i*>(xp + 64 * h);
       G_.xa[2 * h + 1] = *reinterpret_cast<const v4i*>(xp + 64 * h + 8);
     }
-    if (row >= R)
+    if (!valid)
 #pragma unroll
       for (int i = 0; i < 4; ++i) G_.xa[i] = zero;
   } else {
-    const int8_t* xp = reinterpret_cast<const int8_t*>(xv) + (size_t)(row < R ? row : 0) * K + kb;
+    const int8_t* xp = xrow + kb;
 #pragma unroll
     for (int h = 0; h < 2; ++h) G_.xa[h] = *reinterpret_cast<const v4i*>(xp + 64 * h);
-    if (row >= R) G_.xa[0] = G_.xa[1] = zero;
+    if (!valid) G_.xa[0] = G_.xa[1] = zero;
   }
   const v4i* tp = reinterpret_cast<const v4i*>(wp + tile * 8192 + c * 1024 + row * 16);
 #pragma unroll
@@ -116,10 +117,39 @@ __device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc
   }
 }
 
-// One wave per (64-row block nb, group range [g0, g1)). The next group's loads are issued before the
-// current group's matrix-core work and every load is unconditional inside the loop, so each wave keeps
-// two tiles (16 KiB) in flight. Lane l holds output rows 4*(l/16) + v, v < VR (VR = 1, 2 or 4 covers
-// R <= 1, 2 or 16). out_mode 0: plain store (the wave owns all groups of its rows), 1: 64-bit atomic add.
+// The group loop of one wave over groups [g0, g1) of row block nb. The next group's loads are issued
+// before the current group's matrix-core work and every load is unconditional inside the loop, so
+// each wave keeps two tiles (16 KiB) in flight.
+template <int ABITS, bool NT, int VR>
+__device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t* __restrict__ wp,
+                                            const int16_t* __restrict__ mp, const int8_t* __restrict__ xrow, bool valid,
+                                            int R, int nb, int nbs, int G, int g0, int g1, int row, int c, int lane) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int v = 0; v < VR; ++v) acc[q][v] = 0;
+  if (g0 >= g1) return;
+  GroupRegs ra, rb;
+  load_group<ABITS, NT>(ra, wp, mp, xrow, valid, tile_index(nb, g0, nbs, G), g0, row, c);
+  int g = g0;
+  for (; g + 2 < g1; g += 2) {
+    load_group<ABITS, NT>(rb, wp, mp, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
+    compute_group<ABITS, VR>(ra, acc, R, row, lane);
+    load_group<ABITS, NT>(ra, wp, mp, xrow, valid, tile_index(nb, g + 2, nbs, G), g + 2, row, c);
+    compute_group<ABITS, VR>(rb, acc, R, row, lane);
+  }
+  if (g + 1 < g1) {
+    load_group<ABITS, NT>(rb, wp, mp, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
+    compute_group<ABITS, VR>(ra, acc, R, row, lane);
+    compute_group<ABITS, VR>(rb, acc, R, row, lane);
+  } else {
+    compute_group<ABITS, VR>(ra, acc, R, row, lane);
+  }
+}
+
+// One wave per (64-row block nb, group range [g0, g1)). Lane l holds output rows 4*(l/16) + v, v < VR
+// (VR = 1, 2 or 4 covers R <= 1, 2 or 16). out_mode 0: plain store (the wave owns all groups of its
+// rows), 1: 64-bit atomic add.
 template <int ABITS, bool NT, int VR>
 __global__ __launch_bounds__(256) void k_gemv_g128(const void* __restrict__ xv, const int8_t* __restrict__ wp,
                                                    const int16_t* __restrict__ mp, int64_t* __restrict__ t, int R,
@@ -132,31 +162,11 @@ __global__ __launch_bounds__(256) void k_gemv_g128(const void* __restrict__ xv, 
   const int g0 = (int)(((int64_t)sp * G) / nsplit);
   const int g1 = (int)(((int64_t)(sp + 1) * G) / nsplit);
   const int row = lane & 15, c = lane >> 4;
+  const size_t xbytes = (size_t)K * (ABITS == 15 ? 2 : 1);
+  const int8_t* xrow = reinterpret_cast<const int8_t*>(xv) + (size_t)(row < R ? row : 0) * xbytes;
 
   int64_t acc[4][VR];
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-#pragma unroll
-    for (int v = 0; v < VR; ++v) acc[q][v] = 0;
-
-  if (g0 < g1) {
-    GroupRegs ra, rb;
-    load_group<ABITS, NT>(ra, wp, mp, xv, tile_index(nb, g0, nbs, G), g0, R, K, row, c);
-    int g = g0;
-    for (; g + 2 < g1; g += 2) {
-      load_group<ABITS, NT>(rb, wp, mp, xv, tile_index(nb, g + 1, nbs, G), g + 1, R, K, row, c);
-      compute_group<ABITS, VR>(ra, acc, R, row, lane);
-      load_group<ABITS, NT>(ra, wp, mp, xv, tile_index(nb, g + 2, nbs, G), g + 2, R, K, row, c);
-      compute_group<ABITS, VR>(rb, acc, R, row, lane);
-    }
-    if (g + 1 < g1) {
-      load_group<ABITS, NT>(rb, wp, mp, xv, tile_index(nb, g + 1, nbs, G), g + 1, R, K, row, c);
-      compute_group<ABITS, VR>(ra, acc, R, row, lane);
-      compute_group<ABITS, VR>(rb, acc, R, row, lane);
-    } else {
-      compute_group<ABITS, VR>(ra, acc, R, row, lane);
-    }
-  }
+  gemv_groups<ABITS, NT, VR>(acc, wp, mp, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane);
 
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -171,6 +181,51 @@ __global__ __launch_bounds__(256) void k_gemv_g128(const void* __restrict__ xv, 
         else
           *dst = acc[q][v];
       }
+    }
+  }
+}
+
+// Expert GEMV (MoE): task = (chunk, 64-row block, group split). Chunk ch holds pairs
+// [chunk_p0, chunk_p0 + chunk_n) of expert chunk_e; pair p reads activation row row_map[p] (or p
+// when row_map is null) and adds its result into output row p (t must hold zeros or a running total).
+// Expert e's packed linear starts at wp + e * w_stride, mp + e * m_stride.
+template <int ABITS, bool NT>
+__global__ __launch_bounds__(256) void k_gemv_experts(const void* __restrict__ xv, const int32_t* __restrict__ row_map,
+                                                      const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                                      int64_t w_stride, int64_t m_stride, const int32_t* __restrict__ chunk_e,
+                                                      const int32_t* __restrict__ chunk_p0, const int32_t* __restrict__ chunk_n,
+                                                      const int32_t* __restrict__ nchunks, int64_t* __restrict__ t, int N,
+                                                      int K, int G, int nsplit) {
+  constexpr int RMAX = ABITS == 15 ? 15 : 16;
+  const int lane = threadIdx.x & 63;
+  const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nbs = (N + 63) >> 6;
+  const int per_chunk = nbs * nsplit;
+  const int ch = task / per_chunk;
+  if (ch >= nchunks[0]) return;
+  const int rest = task - ch * per_chunk;
+  const int nb = rest / nsplit, sp = rest - nb * nsplit;
+  const int g0 = (int)(((int64_t)sp * G) / nsplit);
+  const int g1 = (int)(((int64_t)(sp + 1) * G) / nsplit);
+  const int e = chunk_e[ch], p0 = chunk_p0[ch];
+  int R = chunk_n[ch];
+  R = R < RMAX ? R : RMAX;
+  const int row = lane & 15, c = lane >> 4;
+  const int pr = p0 + (row < R ? row : 0);
+  const size_t xbytes = (size_t)K * (ABITS == 15 ? 2 : 1);
+  const int8_t* xrow = reinterpret_cast<const int8_t*>(xv) + (size_t)(row_map ? row_map[pr] : pr) * xbytes;
+
+  int64_t acc[4][4];
+  gemv_groups<ABITS, NT, 4>(acc, wp + (size_t)e * w_stride, mp + (size_t)e * m_stride, xrow, row < R, R, nb, nbs, G, g0,
+                            g1, row, c, lane);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = nb * 64 + 16 * q + row;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = 4 * c + v;
+      if (r < R && n < N)
+        atomicAdd(reinterpret_cast<unsigned long long*>(t + (size_t)(p0 + r) * N + n), (unsigned long long)acc[q][v]);
     }
   }
 }
@@ -280,4 +335,28 @@ extern "C" int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, c
   if (e) return e;
   if (R <= (abits == 15 ? 15 : 16)) return gemv_launch(x, abits, wp, mp, t, R, N, K, as_stream(stream), false);
   return gemm_mfma(x, abits, wp, mp, t, R, N, K, as_stream(stream));
+}
+
+extern "C" int exact_gemv_g128_experts(const void* x, int32_t abits, const int32_t* row_map, const int8_t* wp,
+                                       const int16_t* mp, int64_t w_stride, int64_t m_stride, const int32_t* chunk_e,
+                                       const int32_t* chunk_p0, const int32_t* chunk_n, const int32_t* nchunks,
+                                       int32_t max_chunks, int64_t* t, int32_t N, int32_t K, void* stream) {
+  int e = check_linear(x, abits, wp, mp, t, 1, N, K);
+  if (e) return e;
+  if (!chunk_e || !chunk_p0 || !chunk_n || !nchunks || max_chunks <= 0 || w_stride < 0 || m_stride < 0) return EXACT_E_ARG;
+  if ((w_stride & 15) || (m_stride & 7)) return EXACT_E_UNSUPPORTED;
+  const int G = K / 128;
+  const int64_t nbs = (N + 63) / 64;
+  int64_t ns = (GEMV_WAVES + (int64_t)max_chunks * nbs - 1) / ((int64_t)max_chunks * nbs);
+  ns = ns < 1 ? 1 : (ns > G ? G : ns);
+  const int64_t tasks = (int64_t)max_chunks * nbs * ns;
+  if (tasks > (1LL << 30)) return EXACT_E_UNSUPPORTED;
+  dim3 grid((unsigned)((tasks + 3) / 4)), block(256);
+  if (abits == 15)
+    hipLaunchKernelGGL((k_gemv_experts<15, GEMV_NT != 0>), grid, block, 0, as_stream(stream), x, row_map, wp, mp, w_stride,
+                       m_stride, chunk_e, chunk_p0, chunk_n, nchunks, t, N, K, G, (int)ns);
+  else
+    hipLaunchKernelGGL((k_gemv_experts<7, GEMV_NT != 0>), grid, block, 0, as_stream(stream), x, row_map, wp, mp, w_stride,
+                       m_stride, chunk_e, chunk_p0, chunk_n, nchunks, t, N, K, G, (int)ns);
+  return launch_status("gemv_g128_experts");
 }

@@ -1,0 +1,165 @@
+// Mixture-of-experts routing, dispatch and combination (MoEInt.moe, moe_exact_kaggle.py:454-467).
+//
+//   logits = shr(t_router, 28 - s)                        router linear, no bias
+//   p      = isoftmax(logits) over all experts (Q20)      exact_llm.py:109-115
+//   sel    = the top-k experts by a stable sort of -p    ties go to the lower expert index
+//   out    = sum_j shr(p_j * down_e(h_e), 20) + shr(isig(sgate(m)) * shared(m), 16)
+//
+// Dispatch groups the R x k (row, expert) pairs by expert (stable: row-major order inside an expert)
+// and cuts each expert's pairs into chunks of at most chunk_rows, so the expert GEMV streams each
+// expert's weights once per chunk instead of once per pair. The combination is exact in any order.
+#include "exact_common.h"
+#include "abi_util.h"
+
+namespace exact {
+
+// One block per row. The probabilities stay in LDS for the rank computation: expert i has rank
+// #{j : p_j > p_i or (p_j == p_i and j < i)}, which is its position in a stable sort of -p.
+__global__ void k_router_topk(int64_t* __restrict__ t, const int32_t* __restrict__ s, const int32_t* __restrict__ T,
+                              int64_t* __restrict__ p_sel, int32_t* __restrict__ e_sel, int NE, int k, int clear_t) {
+  extern __shared__ int64_t sp[];
+  __shared__ int64_t red[16];
+  const int r = blockIdx.x;
+  const int sh = 28 - s[r];
+  int64_t* tr = t + (int64_t)r * NE;
+  int64_t mx = INT64_MIN;
+  for (int i = threadIdx.x; i < NE; i += blockDim.x) {
+    const int64_t y = shr64(tr[i], sh);
+    if (clear_t) tr[i] = 0;
+    sp[i] = y;
+    mx = y > mx ? y : mx;
+  }
+  mx = block_max64(mx, red);
+  int64_t es = 0;
+  for (int i = threadIdx.x; i < NE; i += blockDim.x) es += lut_exp(T, mx - sp[i]);
+  es = block_sum64(es, red);
+  for (int i = threadIdx.x; i < NE; i += blockDim.x) sp[i] = floordiv64(shl64(lut_exp(T, mx - sp[i]), 20), es);
+  __syncthreads();
+  for (int i = threadIdx.x; i < NE; i += blockDim.x) {
+    const int64_t pi = sp[i];
+    int rank = 0;
+    for (int j = 0; j < NE; ++j) {
+      const int64_t pj = sp[j];
+      rank += (pj > pi) || (pj == pi && j < i);
+    }
+    if (rank < k) {
+      p_sel[(int64_t)r * k + rank] = pi;
+      e_sel[(int64_t)r * k + rank] = i;
+    }
+  }
+}
+
+// One block. Pair q = r * k + j. Every thread owns experts e = tid, tid + blockDim, ...: it counts its
+// pairs, and after a block-wide prefix it places them (in q order) and writes its chunks.
+__global__ void k_moe_dispatch(const int32_t* __restrict__ e_sel, const int32_t* __restrict__ s, int32_t* __restrict__ pidx,
+                               int32_t* __restrict__ pair_row, int32_t* __restrict__ s_pair, int32_t* __restrict__ chunk_e,
+                               int32_t* __restrict__ chunk_p0, int32_t* __restrict__ chunk_n, int32_t* __restrict__ nchunks,
+                               int P, int NE, int k, int CH) {
+  extern __shared__ int32_t lds[];
+  int32_t* es = lds;              // P expert ids
+  int32_t* cnt = es + P;          // NE counts
+  int32_t* off = cnt + NE;        // NE pair offsets
+  int32_t* coff = off + NE;       // NE chunk offsets
+  for (int q = threadIdx.x; q < P; q += blockDim.x) es[q] = e_sel[q];
+  __syncthreads();
+  for (int e = threadIdx.x; e < NE; e += blockDim.x) {
+    int c = 0;
+    for (int q = 0; q < P; ++q) c += es[q] == e;
+    cnt[e] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int po = 0, co = 0;
+    for (int e = 0; e < NE; ++e) {
+      off[e] = po;
+      coff[e] = co;
+      po += cnt[e];
+      co += (cnt[e] + CH - 1) / CH;
+    }
+    nchunks[0] = co;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < NE; e += blockDim.x) {
+    int pos = off[e];
+    for (int q = 0; q < P; ++q)
+      if (es[q] == e) {
+        pidx[q] = pos;
+        pair_row[pos] = q / k;
+        s_pair[pos] = s[q / k];
+        ++pos;
+      }
+    const int n = cnt[e];
+    for (int c = 0; c * CH < n; ++c) {
+      const int idx = coff[e] + c;
+      chunk_e[idx] = e;
+      chunk_p0[idx] = off[e] + c * CH;
+      chunk_n[idx] = n - c * CH < CH ? n - c * CH : CH;
+    }
+  }
+}
+
+// One block per row: x += sum_j shr(p_j * shr(t_ed[pair], 28 - sh_pair), 20)
+//                        + shr(isig(shr(t_sg, 28 - s)) * shr(t_sd, 28 - sh_s), 16)
+__global__ void k_moe_combine(int64_t* __restrict__ x, int64_t* __restrict__ t_ed, const int32_t* __restrict__ sh_pair,
+                              const int64_t* __restrict__ p_sel, const int32_t* __restrict__ pidx, int64_t* __restrict__ t_sd,
+                              const int32_t* __restrict__ sh_s, int64_t* __restrict__ t_sg, const int32_t* __restrict__ s,
+                              const int32_t* __restrict__ sig_t, int D, int k, int clear_t) {
+  const int r = blockIdx.x;
+  int64_t gate = 0;
+  if (t_sd) gate = lut16(sig_t, shr64(t_sg[r], 28 - s[r]), true);
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    int64_t acc = 0;
+    for (int j = 0; j < k; ++j) {
+      const int q = pidx[r * k + j];
+      int64_t* te = t_ed + (int64_t)q * D + d;
+      const int64_t y = shr64(*te, 28 - sh_pair[q]);
+      if (clear_t) *te = 0;
+      acc += shr64(p_sel[r * k + j] * y, 20);
+    }
+    if (t_sd) {
+      int64_t* ts = t_sd + (int64_t)r * D + d;
+      acc += shr64(gate * shr64(*ts, 28 - sh_s[r]), 16);
+      if (clear_t) *ts = 0;
+    }
+    x[(int64_t)r * D + d] += acc;
+  }
+  if (t_sd && clear_t) {
+    __syncthreads();   // every thread has read the gate logit
+    if (threadIdx.x == 0) t_sg[r] = 0;
+  }
+}
+
+}  // namespace exact
+
+using namespace exact;
+
+extern "C" int exact_router_topk(int64_t* t, const int32_t* s, const int32_t* exp_t, int64_t* p_sel, int32_t* e_sel,
+                                 int32_t R, int32_t NE, int32_t k, int32_t clear_t, void* stream) {
+  if (!t || !s || !exp_t || !p_sel || !e_sel || R <= 0 || NE <= 0 || k <= 0 || k > NE) return EXACT_E_ARG;
+  if (NE > 4096) return EXACT_E_UNSUPPORTED;
+  hipLaunchKernelGGL(k_router_topk, dim3(R), dim3(256), NE * sizeof(int64_t), as_stream(stream), t, s, exp_t, p_sel, e_sel,
+                     NE, k, clear_t);
+  return launch_status("router_topk");
+}
+
+extern "C" int exact_moe_dispatch(const int32_t* e_sel, const int32_t* s, int32_t* pidx, int32_t* pair_row, int32_t* s_pair,
+                                  int32_t* chunk_e, int32_t* chunk_p0, int32_t* chunk_n, int32_t* nchunks, int32_t R,
+                                  int32_t NE, int32_t k, int32_t chunk_rows, void* stream) {
+  if (!e_sel || !s || !pidx || !pair_row || !s_pair || !chunk_e || !chunk_p0 || !chunk_n || !nchunks) return EXACT_E_ARG;
+  if (R <= 0 || NE <= 0 || k <= 0 || k > NE || chunk_rows <= 0) return EXACT_E_ARG;
+  const int64_t P = (int64_t)R * k;
+  if (P + 3LL * NE > 16384) return EXACT_E_UNSUPPORTED;   // 64 KiB of LDS
+  hipLaunchKernelGGL(k_moe_dispatch, dim3(1), dim3(256), (size_t)(P + 3 * NE) * sizeof(int32_t), as_stream(stream), e_sel,
+                     s, pidx, pair_row, s_pair, chunk_e, chunk_p0, chunk_n, nchunks, (int)P, NE, k, chunk_rows);
+  return launch_status("moe_dispatch");
+}
+
+extern "C" int exact_moe_combine(int64_t* x, int64_t* t_ed, const int32_t* sh_pair, const int64_t* p_sel, const int32_t* pidx,
+                                 int64_t* t_sd, const int32_t* sh_s, int64_t* t_sg, const int32_t* s, const int32_t* sig_t,
+                                 int32_t R, int32_t D, int32_t k, int32_t clear_t, void* stream) {
+  if (!x || !t_ed || !sh_pair || !p_sel || !pidx || R <= 0 || D <= 0 || k <= 0) return EXACT_E_ARG;
+  if (t_sd && (!sh_s || !t_sg || !s || !sig_t)) return EXACT_E_ARG;
+  hipLaunchKernelGGL(k_moe_combine, dim3(R), dim3(256), 0, as_stream(stream), x, t_ed, sh_pair, p_sel, pidx, t_sd, sh_s,
+                     t_sg, s, sig_t, D, k, clear_t);
+  return launch_status("moe_combine");
+}

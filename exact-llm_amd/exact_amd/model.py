@@ -59,10 +59,21 @@ class DeviceWeights:
                 o=fused([(f"L{li}.o", D)], H * hd, False))
             if cfg.moe:
                 L["router"] = fused([(f"L{li}.router", cfg.NE)], D, False)
-                L["experts"] = [(fused([(f"L{li}.e{e}.gate", cfg.MI), (f"L{li}.e{e}.up", cfg.MI)], D, False),
-                                 fused([(f"L{li}.e{e}.down", D)], cfg.MI, False)) for e in range(cfg.NE)]
-                L["shared"] = (fused([(f"L{li}.sg", cfg.SI), (f"L{li}.su", cfg.SI)], D, False),
-                               fused([(f"L{li}.sd", D)], cfg.SI, False))
+                # experts: gate|up (2 MI x D) and down (D x MI) of all NE experts, each in one allocation
+                egu = ops.ExpertLinears(cfg.NE, 2 * cfg.MI, D, device)
+                edn = ops.ExpertLinears(cfg.NE, D, cfg.MI, device)
+                for e in range(cfg.NE):
+                    wp, mp = egu.part(e)
+                    for name, off in ((f"L{li}.e{e}.gate", 0), (f"L{li}.e{e}.up", cfg.MI)):
+                        kw, km, _ = _lin_keys(seed, name)
+                        ops.synth_linear(wp, mp, cfg.MI, D, kw, km, synth.M_LO, synth.M_HI, thr, n_off=off,
+                                         Ntot=2 * cfg.MI)
+                    wp, mp = edn.part(e)
+                    kw, km, _ = _lin_keys(seed, f"L{li}.e{e}.down")
+                    ops.synth_linear(wp, mp, D, cfg.MI, kw, km, synth.M_LO, synth.M_HI, thr)
+                L["egu"], L["edown"] = egu, edn
+                L["sgu"] = fused([(f"L{li}.sg", cfg.SI), (f"L{li}.su", cfg.SI)], D, False)
+                L["sd"] = fused([(f"L{li}.sd", D)], cfg.SI, False)
                 L["sgate"] = fused([(f"L{li}.sgate", 1)], D, False)
             else:
                 L["gateup"] = fused([(f"L{li}.gate", cfg.I), (f"L{li}.up", cfg.I)], D, False)
@@ -125,20 +136,32 @@ class Cache:
 
 
 class Workspace:
-    """Activation buffers for R rows (allocated once; reused by every step and by captured graphs)."""
+    """Activation buffers for R rows (allocated once; reused by every step and by captured graphs).
+    t buffers start zeroed and are left zeroed by the kernels that consume them."""
 
-    def __init__(self, cfg, R, device, nq, I):
+    def __init__(self, cfg, R, device, nq, I, abits=15):
         D, H, hd, V = cfg.D, cfg.H, cfg.hd, cfg.V
         z = lambda *sh, dt=I64: torch.zeros(sh, dtype=dt, device=device)
+        adt = I16 if abits == 15 else I8
         self.R = R
-        self.x, self.xq, self.s = z(R, D), z(R, D, dt=I16), z(R, dt=I32)
+        self.x, self.xq, self.s = z(R, D), z(R, D, dt=adt), z(R, dt=I32)
         self.t_qkv, self.qq, self.sq = z(R, nq), z(R, H, hd, dt=I16), z(R, H, dt=I32)
-        self.att, self.aq, self.sa = z(R, H * hd), z(R, H * hd, dt=I16), z(R, dt=I32)
-        self.t_o, self.t_gu, self.hq, self.sh = z(R, D), z(R, 2 * I), z(R, I, dt=I16), z(R, dt=I32)
+        self.att, self.aq, self.sa = z(R, H * hd), z(R, H * hd, dt=adt), z(R, dt=I32)
+        self.t_o, self.t_gu, self.hq, self.sh = z(R, D), z(R, 2 * I), z(R, I, dt=adt), z(R, dt=I32)
         self.t_d, self.t_head = z(R, D), z(R, V)
         self.logits, self.next_ids = z(R, V), z(R, dt=I32)
         self.s28 = torch.full((R,), 28, dtype=I32, device=device)
         self.ids, self.slot, self.pos = z(R, dt=I32), z(R, dt=I32), z(R, dt=I32)
+        if cfg.moe:
+            k, P = cfg.topk, R * cfg.topk
+            nch = ops.max_chunks(P, cfg.NE, abits)
+            self.t_rt, self.p_sel, self.e_sel = z(R, cfg.NE), z(R, k), z(R, k, dt=I32)
+            self.disp = dict(pidx=z(P, dt=I32), pair_row=z(P, dt=I32), s_pair=z(P, dt=I32), chunk_e=z(nch, dt=I32),
+                             chunk_p0=z(nch, dt=I32), chunk_n=z(nch, dt=I32), nchunks=z(1, dt=I32))
+            self.t_egu, self.ehq, self.esh = z(P, 2 * cfg.MI), z(P, cfg.MI, dt=adt), z(P, dt=I32)
+            self.t_ed = z(P, D)
+            self.t_sgu, self.shq, self.ssh = z(R, 2 * cfg.SI), z(R, cfg.SI, dt=adt), z(R, dt=I32)
+            self.t_sd, self.t_sg = z(R, D), z(R, 1)
 
 
 class TModel:
@@ -153,7 +176,7 @@ class TModel:
         self.tab = DeviceTables(self.dev, Smax, c.hd, c.theta)
         self.nl = len(weights.layers)
         self.nq = (c.H + 2 * c.KV) * c.hd
-        self.I = c.I if not c.moe else max(c.MI, c.SI)
+        self.I = c.I if not c.moe else 1
         self._ws = {}
 
     # ---------------------------------------------------------------- buffers
@@ -162,7 +185,7 @@ class TModel:
 
     def workspace(self, R):
         if R not in self._ws:
-            self._ws[R] = Workspace(self.cfg, R, self.dev, self.nq, self.I)
+            self._ws[R] = Workspace(self.cfg, R, self.dev, self.nq, self.I, self.abits)
         return self._ws[R]
 
     # ---------------------------------------------------------------- linears
@@ -211,7 +234,11 @@ class TModel:
                 self._lin_channel(ws.aq, ws.sa, L["o"], ws.t_o)
                 ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.s28, ws.xq, ws.s)
             if c.moe:
-                raise ExactError("MoE blocks run through MoEModel")
+                if not group:
+                    raise ExactError("MoE layers need group-128 linears")
+                self._moe(ws, L)
+                res_t, res_s = None, None
+                continue
             if group:
                 self._lin(ws.xq, L["gateup"], ws.t_gu)
                 ops.swiglu_qrow(ws.t_gu, ws.s, tab.silu, self.abits, ws.hq, ws.sh, clear=True)
@@ -234,6 +261,24 @@ class TModel:
             self._lin_channel(ws.xq, ws.s, self.w.head, ws.t_head)
             ops.logits_argmax(ws.t_head, ws.s28, ws.logits if want_logits else None, ws.next_ids)
         return ws
+
+    def _moe(self, ws, L):
+        """MoE block on m = ws.xq (scale ws.s), added into ws.x (MoEInt.moe, moe_exact_kaggle.py:454-467):
+        router -> isoftmax -> stable top-k -> experts grouped into chunks -> SwiGLU per (row, expert) pair ->
+        combination weighted by the Q20 probabilities, plus the isig-gated shared expert."""
+        c, tab, k = self.cfg, self.tab, self.cfg.topk
+        self._lin(ws.xq, L["router"], ws.t_rt)
+        ops.router_topk(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, clear=True)
+        ops.moe_dispatch(ws.e_sel, ws.s, c.NE, k, ops.chunk_rows(self.abits), ws.disp)
+        ops.gemv_experts(ws.xq, self.abits, ws.disp["pair_row"], L["egu"], ws.disp, ws.t_egu)
+        ops.swiglu_qrow(ws.t_egu, ws.disp["s_pair"], tab.silu, self.abits, ws.ehq, ws.esh, clear=True)
+        ops.gemv_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed)
+        self._lin(ws.xq, L["sgu"], ws.t_sgu)
+        ops.swiglu_qrow(ws.t_sgu, ws.s, tab.silu, self.abits, ws.shq, ws.ssh, clear=True)
+        self._lin(ws.shq, L["sd"], ws.t_sd)
+        self._lin(ws.xq, L["sgate"], ws.t_sg)
+        ops.moe_combine(ws.x, ws.t_ed, ws.esh, ws.p_sel, ws.disp["pidx"], k, ws.t_sd, ws.ssh, ws.t_sg, ws.s, tab.sig,
+                        clear=True)
 
     # ---------------------------------------------------------------- reference-shaped API
     def forward(self, ids, cache=None, last_only=False, slot=0):

@@ -241,6 +241,65 @@ def zero_(t):
     return t
 
 
+# ----------------------------------------------------------------------------- mixture of experts
+class ExpertLinears:
+    """NE packed linears of one shape (N, K) in one allocation: expert e at wp[e * w_stride:], mp[e * m_stride:]."""
+
+    def __init__(self, NE, N, K, device):
+        nb, G = (N + 63) // 64, K // 128
+        self.NE, self.N, self.K = NE, N, K
+        self.w_stride, self.m_stride = nb * G * 8192, nb * G * 64
+        self.wp = torch.empty(NE * self.w_stride, dtype=I8, device=device)
+        self.mp = torch.empty(NE * self.m_stride, dtype=I16, device=device)
+
+    def part(self, e):
+        return (self.wp[e * self.w_stride:(e + 1) * self.w_stride], self.mp[e * self.m_stride:(e + 1) * self.m_stride])
+
+
+def chunk_rows(abits):
+    return 15 if abits == 15 else 16
+
+
+def max_chunks(P, NE, abits):
+    return min(P, -(-P // chunk_rows(abits)) + NE)
+
+
+def router_topk(t, s, expt, k, p_sel, e_sel, clear=False):
+    R, NE = t.shape
+    _lib.call("exact_router_topk", _ptr(_need(t, I64, "t")), _ptr(_need(s, I32, "s", R)), _ptr(expt),
+              _ptr(_need(p_sel, I64, "p_sel", R * k)), _ptr(_need(e_sel, I32, "e_sel", R * k)), R, NE, k, int(clear),
+              _stream())
+    return p_sel, e_sel
+
+
+def moe_dispatch(e_sel, s, NE, k, chunk, out):
+    """out: dict of int32 tensors pidx (P,), pair_row (P,), s_pair (P,), chunk_e/chunk_p0/chunk_n (max chunks,), nchunks (1,)."""
+    R = s.shape[0]
+    _lib.call("exact_moe_dispatch", _ptr(_need(e_sel, I32, "e_sel", R * k)), _ptr(_need(s, I32, "s", R)),
+              *(_ptr(_need(out[n], I32, n)) for n in ("pidx", "pair_row", "s_pair", "chunk_e", "chunk_p0", "chunk_n",
+                                                       "nchunks")), R, NE, k, chunk, _stream())
+    return out
+
+
+def gemv_experts(x, abits, row_map, lin, disp, out):
+    """out[p] += x[row_map[p]] . W_{expert of p} for the dispatched chunks (row_map None: x row p)."""
+    _need(x, I16 if abits == 15 else I8, "x")
+    _need(out, I64, "out")
+    if x.shape[1] != lin.K or out.shape[1] != lin.N:
+        raise ExactError(f"gemv_experts: x {tuple(x.shape)}, out {tuple(out.shape)} against ({lin.N}, {lin.K})")
+    _lib.call("exact_gemv_g128_experts", _ptr(x), abits, _ptr(row_map), _ptr(lin.wp), _ptr(lin.mp), lin.w_stride,
+              lin.m_stride, _ptr(disp["chunk_e"]), _ptr(disp["chunk_p0"]), _ptr(disp["chunk_n"]), _ptr(disp["nchunks"]),
+              disp["chunk_e"].numel(), _ptr(out), lin.N, lin.K, _stream())
+    return out
+
+
+def moe_combine(x, t_ed, sh_pair, p_sel, pidx, k, t_sd=None, sh_s=None, t_sg=None, s=None, sig=None, clear=False):
+    R, D = x.shape
+    _lib.call("exact_moe_combine", _ptr(_need(x, I64, "x")), _ptr(_need(t_ed, I64, "t_ed")), _ptr(sh_pair), _ptr(p_sel),
+              _ptr(pidx), _ptr(t_sd), _ptr(sh_s), _ptr(t_sg), _ptr(s), _ptr(sig), R, D, k, int(clear), _stream())
+    return x
+
+
 # ----------------------------------------------------------------------------- the reference's op
 @torch.library.custom_op("exact::gemv", mutates_args=())
 def gemv(x16: torch.Tensor, wT: torch.Tensor, Mg: torch.Tensor) -> torch.Tensor:

@@ -136,6 +136,36 @@ int exact_attention(const int16_t* qq, const int32_t* sq, const int16_t* kq, con
                     int64_t* out, int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t Smax, int32_t INV,
                     void* stream);
 
+/* ---- mixture of experts (MoEInt.moe, moe_exact_kaggle.py:454-467) ------------------------------------
+ * Router: logits = rs(t, 28 - s[r]) (t (R, NE) from the router linear); p = isoftmax over all NE experts
+ * (Q20); the k experts with the largest p, ties to the lower index (np.argsort(-p, kind="stable")[:k],
+ * moe_exact_kaggle.py:457). Writes p_sel, e_sel (R, k) in rank order; clear_t != 0 leaves t zeroed. */
+int exact_router_topk(int64_t* t, const int32_t* s, const int32_t* exp_t, int64_t* p_sel, int32_t* e_sel,
+                      int32_t R, int32_t NE, int32_t k, int32_t clear_t, void* stream);
+
+/* Dispatch: the P = R*k pairs q = r*k + j grouped by expert (row order inside an expert), replacing the
+ * per-expert Python loop `rows = nonzero(sel == e)` (moe_exact_kaggle.py:459-463). Outputs: pidx[q] = position
+ * of pair q; pair_row[p] = its token row; s_pair[p] = s[row]; chunks of <= chunk_rows pairs of one expert
+ * (chunk_e, chunk_p0, chunk_n; count in nchunks[0]; at most min(P, ceil(P/chunk_rows) + NE) chunks). */
+int exact_moe_dispatch(const int32_t* e_sel, const int32_t* s, int32_t* pidx, int32_t* pair_row, int32_t* s_pair,
+                       int32_t* chunk_e, int32_t* chunk_p0, int32_t* chunk_n, int32_t* nchunks, int32_t R,
+                       int32_t NE, int32_t k, int32_t chunk_rows, void* stream);
+
+/* Expert GEMV: for every chunk, t[p] += x[row_map ? row_map[p] : p] . W_e for its pairs p, with expert e's
+ * packed linear at wp + e*w_stride, mp + e*m_stride (bytes / int16 elements). chunk_n <= 15 (abits 15) or
+ * 16 (abits 7). The per-expert gate/up and down linears of MoEInt.moe (moe_exact_kaggle.py:461-462). */
+int exact_gemv_g128_experts(const void* x, int32_t abits, const int32_t* row_map, const int8_t* wp,
+                            const int16_t* mp, int64_t w_stride, int64_t m_stride, const int32_t* chunk_e,
+                            const int32_t* chunk_p0, const int32_t* chunk_n, const int32_t* nchunks,
+                            int32_t max_chunks, int64_t* t, int32_t N, int32_t K, void* stream);
+
+/* Combination (moe_exact_kaggle.py:463-467): x[r] += sum_j rs(p_sel[r][j] * rs(t_ed[pidx[r*k+j]], 28 - sh_pair), 20)
+ *   + rs(isig(rs(t_sg[r], 28 - s[r])) * rs(t_sd[r], 28 - sh_s[r]), 16)   (shared expert; skipped if t_sd is NULL).
+ * clear_t != 0 leaves t_ed, t_sd and t_sg zeroed. */
+int exact_moe_combine(int64_t* x, int64_t* t_ed, const int32_t* sh_pair, const int64_t* p_sel, const int32_t* pidx,
+                      int64_t* t_sd, const int32_t* sh_s, int64_t* t_sg, const int32_t* s, const int32_t* sig_t,
+                      int32_t R, int32_t D, int32_t k, int32_t clear_t, void* stream);
+
 /* ---- model plumbing ------------------------------------------------------------------------------ */
 /* x[r] = emb[ids[r]] from an int32 Q16 table (V, D) (exact_llm.py:163; GraphDecoder.step :641). */
 int exact_embed(const int32_t* ids, const int32_t* emb, int64_t* x, int32_t R, int32_t D, int32_t V,

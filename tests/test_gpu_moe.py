@@ -1,0 +1,189 @@
+"""GPU parity of the mixture-of-experts path (MoEInt.moe, moe_exact_kaggle.py:454-467) against the oracle:
+router top-k with ties, dispatch bookkeeping, the expert GEMV, the combination, and whole models."""
+import numpy as np
+import pytest
+import torch
+
+import exact_oracle as O
+import helpers
+from exact_amd import ops, synth
+from exact_amd.model import DeviceWeights, GraphDecoder, TModel
+from exact_amd.tables import DeviceTables
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+I32, I64 = torch.int32, torch.int64
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def dev(a, dt):
+    return torch.tensor(np.asarray(a), dtype=dt, device=DEV)
+
+
+@pytest.fixture(scope="module")
+def tab():
+    return DeviceTables(DEV, 16, 64, 1e4)
+
+
+@pytest.mark.parametrize("R,NE,k", [(1, 60, 4), (8, 60, 4), (37, 6, 2), (5, 64, 8)])
+def test_router_topk_matches_oracle(tab, R, NE, k):
+    rng = np.random.default_rng(R * 100 + NE)
+    t = rng.integers(-(1 << 40), 1 << 40, (R, NE))
+    # ties: copies of one logit inside a row, so equal probabilities must resolve to the lower index
+    t[:, NE // 2] = t[:, 1]
+    t[:, NE - 1] = t[:, 0]
+    if R > 2:
+        t[2] = t[2, 0]                                   # an all-equal row
+    s = rng.integers(0, 20, R)
+    td = dev(t, I64)
+    p_sel, e_sel = torch.zeros((R, k), dtype=I64, device=DEV), torch.zeros((R, k), dtype=I32, device=DEV)
+    ops.router_topk(td, dev(s, I32), tab.exp, k, p_sel, e_sel, clear=True)
+    lg = O.round_shift(t, (28 - s)[:, None])
+    p = O.isoftmax(lg, np.ones_like(lg, bool))
+    sel = np.argsort(-p, axis=-1, kind="stable")[:, :k]
+    assert np.array_equal(host(e_sel), sel)
+    assert np.array_equal(host(p_sel), np.take_along_axis(p, sel, -1))
+    assert not host(td).any()                            # cleared for the next accumulating GEMV
+
+
+@pytest.mark.parametrize("R,NE,k,ch", [(1, 60, 4, 15), (8, 60, 4, 15), (256, 60, 4, 15), (40, 6, 2, 16)])
+def test_dispatch_groups_pairs_by_expert(R, NE, k, ch):
+    rng = np.random.default_rng(R + NE)
+    e_sel = np.stack([rng.choice(NE, k, replace=False) for _ in range(R)])
+    s = rng.integers(0, 30, R)
+    P = R * k
+    nmax = ops.max_chunks(P, NE, 15 if ch == 15 else 7)
+    out = {n: torch.full((P,), -1, dtype=I32, device=DEV) for n in ("pidx", "pair_row", "s_pair")}
+    out.update({n: torch.full((nmax,), -1, dtype=I32, device=DEV) for n in ("chunk_e", "chunk_p0", "chunk_n")})
+    out["nchunks"] = torch.zeros(1, dtype=I32, device=DEV)
+    ops.moe_dispatch(dev(e_sel, I32), dev(s, I32), NE, k, ch, out)
+    o = {n: host(v) for n, v in out.items()}
+    q = np.arange(P)
+    # stable grouping: positions sorted by (expert, pair index)
+    order = np.lexsort((q, e_sel.reshape(-1)))
+    assert np.array_equal(o["pidx"][order], q)
+    assert np.array_equal(o["pair_row"][o["pidx"]], q // k)
+    assert np.array_equal(o["s_pair"][o["pidx"]], s[q // k])
+    n = int(o["nchunks"][0])
+    assert n <= nmax
+    covered = np.zeros(P, int)
+    for c in range(n):
+        e, p0, cnt = o["chunk_e"][c], o["chunk_p0"][c], o["chunk_n"][c]
+        assert 1 <= cnt <= ch
+        pairs = order[p0:p0 + cnt]
+        assert (e_sel.reshape(-1)[pairs] == e).all()
+        covered[p0:p0 + cnt] += 1
+    assert (covered == 1).all()
+
+
+@pytest.mark.parametrize("abits", [15, 7])
+@pytest.mark.parametrize("R,NE,k,N,K", [(1, 60, 4, 2816, 2048), (8, 60, 4, 2048, 1408), (50, 6, 2, 384, 256)])
+def test_expert_gemv_matches_oracle(abits, R, NE, k, N, K):
+    rng = np.random.default_rng(abits + R)
+    lin = ops.ExpertLinears(NE, N, K, DEV)
+    thr = dev(synth.thresholds().astype(np.int64), I64).to(I32)
+    used = sorted(set(rng.choice(NE, min(NE, 2 * k + 2), replace=False).tolist()))
+    e_sel = np.stack([rng.choice(used, k, replace=False) for _ in range(R)])
+    ws, Ms = {}, {}
+    for e in used:
+        wp, mp = lin.part(e)
+        kw, km = synth.key(7, f"e{e}.w"), synth.key(7, f"e{e}.m")
+        ops.synth_linear(wp, mp, N, K, kw, km, synth.M_LO, synth.M_HI, thr)
+        ws[e], Ms[e] = synth.weights_np(kw, N, K), synth.scales_np(km, N, K)
+    lim = (1 << abits) - 1
+    x = rng.integers(-lim, lim + 1, (R, K))
+    P = R * k
+    disp = {n: torch.zeros((P,), dtype=I32, device=DEV) for n in ("pidx", "pair_row", "s_pair")}
+    nmax = ops.max_chunks(P, NE, abits)
+    disp.update({n: torch.zeros((nmax,), dtype=I32, device=DEV) for n in ("chunk_e", "chunk_p0", "chunk_n")})
+    disp["nchunks"] = torch.zeros(1, dtype=I32, device=DEV)
+    ops.moe_dispatch(dev(e_sel, I32), torch.zeros(R, dtype=I32, device=DEV), NE, k, ops.chunk_rows(abits), disp)
+    xd = dev(x, torch.int16 if abits == 15 else torch.int8)
+    t = torch.zeros((P, N), dtype=I64, device=DEV)
+    ops.gemv_experts(xd, abits, disp["pair_row"], lin, disp, t)
+    got = host(t)
+    pidx = host(disp["pidx"])
+    for q in range(P):
+        r, e = q // k, e_sel.reshape(-1)[q]
+        want = (O.group_acc(x[r:r + 1], ws[e]) * Ms[e][:, None, :]).sum(0)[0]
+        assert np.array_equal(got[pidx[q]], want), (q, e)
+
+
+def test_combine_matches_oracle(tab):
+    rng = np.random.default_rng(5)
+    R, k, D, NE = 6, 4, 512, 60
+    x = rng.integers(-(1 << 30), 1 << 30, (R, D))
+    P = R * k
+    pidx = rng.permutation(P)
+    t_ed = rng.integers(-(1 << 44), 1 << 44, (P, D))
+    sh_pair = rng.integers(0, 26, P)
+    p_sel = rng.integers(0, 1 << 20, (R, k))
+    t_sd = rng.integers(-(1 << 44), 1 << 44, (R, D))
+    sh_s = rng.integers(0, 26, R)
+    t_sg = rng.integers(-(1 << 46), 1 << 46, (R, 1))
+    s = rng.integers(0, 24, R)
+    xd = dev(x, I64)
+    args = [dev(a, dt) for a, dt in ((t_ed, I64), (sh_pair, I32), (p_sel, I64), (pidx, I32), (t_sd, I64), (sh_s, I32),
+                                     (t_sg, I64), (s, I32))]
+    ops.moe_combine(xd, args[0], args[1], args[2], args[3], k, args[4], args[5], args[6], args[7], tab.sig, clear=True)
+    want = x.copy()
+    for r in range(R):
+        for j in range(k):
+            q = pidx[r * k + j]
+            want[r] += O.round_shift(p_sel[r, j] * O.round_shift(t_ed[q], 28 - sh_pair[q]), 20)
+        gate = O.isig(O.round_shift(t_sg[r, 0], 28 - s[r]))
+        want[r] += O.round_shift(gate * O.round_shift(t_sd[r], 28 - sh_s[r]), 16)
+    assert np.array_equal(host(xd), want)
+    assert not host(args[0]).any() and not host(args[4]).any() and not host(args[6]).any()
+
+
+@pytest.mark.parametrize("abits", [15, 7])
+def test_tiny_moe_prefill_and_decode_match_oracle(abits):
+    cfg = synth.CONFIGS["tiny-moe"]
+    seed = 11
+    om = helpers.oracle_model(cfg, seed, T=64, abits=abits)
+    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=64, abits=abits)
+    ids = helpers.prompt(21, 24, cfg.V)
+    stats = {}
+    assert np.array_equal(host(tm.forward(ids)), om.forward(ids, stats=stats))
+    assert len({int(e) for st in stats.values() for sel in st for e in sel.reshape(-1)}) > cfg.topk
+    otoks, orows = O.greedy_decode(om, ids[:10], 5)
+    cache = tm.new_cache(B=1)
+    lg = host(tm.forward(ids[:10], cache))
+    assert np.array_equal(lg[-1], orows[0])
+    tok = int(lg[-1].argmax())
+    for i in range(1, 5):
+        lgi, nid = tm.decode_rows([tok], cache)
+        assert np.array_equal(host(lgi)[0], orows[i]), i
+        tok = int(host(nid)[0])
+        assert tok == otoks[i]
+
+
+def test_tiny_moe_batch_graph_decode_matches_oracle():
+    cfg = synth.CONFIGS["tiny-moe"]
+    seed = 12
+    B = 3
+    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=48, batch=B)
+    om = helpers.oracle_model(cfg, seed, T=48)
+    prompts = [helpers.prompt(300 + b, 5 + 2 * b, cfg.V) for b in range(B)]
+    cache = tm.new_cache()
+    first = []
+    for b, p in enumerate(prompts):
+        first.append(int(host(tm.forward(p, cache, slot=b))[-1].argmax()))
+    gd = GraphDecoder(tm, cache, B)
+    gd.load(first)
+    gd.capture()
+    want = [O.greedy_decode(om, p, 4) for p in prompts]
+    toks = [list(first)]
+    for i in range(1, 4):
+        lg, nid = gd.step()
+        lgh = host(lg)
+        for b in range(B):
+            assert np.array_equal(lgh[b], want[b][1][i]), (i, b)
+        toks.append(host(nid).tolist())
+    for b in range(B):
+        assert [t[b] for t in toks] == want[b][0][:4]
