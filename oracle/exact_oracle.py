@@ -217,15 +217,28 @@ def linear_group(x, w, Mg, b=None, abits=15, n_chunk=16384):
     return y
 
 
+_GROUP_T = None
+
+
+def set_group_kernel(fn):
+    """Route t = sum_g acc_g * M_g through fn(xq, w, Mg) (the C restatement in exact_c.c, used for
+    large-model fixtures); None restores the numpy path."""
+    global _GROUP_T
+    _GROUP_T = fn
+
+
 def linear_group_t(x, w, Mg, b=None, abits=15, n_chunk=16384):
     """linear_group returning (y, t) where t = sum_g acc_g * M_g is the raw int64 total."""
     x = np.asarray(x, dtype=I64)
     xq, s = qrow(x, abits)
     N = w.shape[1]
-    t = np.empty((x.shape[0], N), I64)
-    for j in range(0, N, n_chunk):
-        acc = group_acc(xq, w[:, j:j + n_chunk])                            # (G, R, n)
-        t[:, j:j + n_chunk] = (acc * np.asarray(Mg[:, j:j + n_chunk], I64)[:, None, :]).sum(0)
+    if _GROUP_T is not None:
+        t = _GROUP_T(xq, w, Mg)
+    else:
+        t = np.empty((x.shape[0], N), I64)
+        for j in range(0, N, n_chunk):
+            acc = group_acc(xq, w[:, j:j + n_chunk])                        # (G, R, n)
+            t[:, j:j + n_chunk] = (acc * np.asarray(Mg[:, j:j + n_chunk], I64)[:, None, :]).sum(0)
     y = round_shift(t, 28 - s)
     return (y if b is None else y + b), t
 
