@@ -7,6 +7,8 @@
 #include "exact_common.h"
 #include "abi_util.h"
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+
 namespace exact {
 
 // grid (R, H + 2*KV), block 64 (one wave per head slot), hd <= 256
@@ -74,9 +76,11 @@ __global__ __launch_bounds__(256) void k_attention(const int16_t* __restrict__ q
                                                    const int16_t* __restrict__ kq, const int32_t* __restrict__ sk,
                                                    const int64_t* __restrict__ v, const int32_t* __restrict__ slot,
                                                    const int32_t* __restrict__ pos, const int32_t* __restrict__ expt,
-                                                   int64_t* __restrict__ out, int H, int KV, int hd, int Smax, int INV) {
+                                                   int64_t* __restrict__ out, int32_t* __restrict__ obits, int H, int KV,
+                                                   int hd, int Smax, int INV) {
   extern __shared__ int64_t sc[];   // Smax entries
   __shared__ int32_t qs[256];
+  __shared__ int ored[4];
   __shared__ int64_t red[16];
   __shared__ int64_t part[256];
   const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
@@ -88,11 +92,17 @@ __global__ __launch_bounds__(256) void k_attention(const int16_t* __restrict__ q
   const int64_t cbase = ((int64_t)sl * KV + kh) * Smax;
   int64_t mx = INT64_MIN;
   for (int si = tid; si < S; si += blockDim.x) {
-    const int16_t* kr = kq + (cbase + si) * hd;
+    // 16-byte key loads, four in flight; each pair of int16 products is exact in int32 (< 2^31)
+    const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + si) * hd);
     int64_t dot = 0;
-    for (int j = 0; j < hd; j += 2) {
-      const int32_t kk = *reinterpret_cast<const int32_t*>(kr + j);
-      dot += (int64_t)qs[j] * (int16_t)(kk & 0xffff) + (int64_t)qs[j + 1] * (int16_t)(kk >> 16);
+#pragma unroll 4
+    for (int j8 = 0; j8 < hd / 8; ++j8) {
+      const v4i kk = kr[j8];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int j = j8 * 8 + 2 * c;
+        dot += (int64_t)(qs[j] * (int32_t)(int16_t)(kk[c] & 0xffff) + qs[j + 1] * (int32_t)(int16_t)(kk[c] >> 16));
+      }
     }
     const int64_t val = shr64(dot * INV, 32 - sqv - sk[cbase + si]);
     sc[si] = val;
@@ -106,7 +116,7 @@ __global__ __launch_bounds__(256) void k_attention(const int16_t* __restrict__ q
     es += e;
   }
   es = block_sum64(es, red);
-  for (int si = tid; si < S; si += blockDim.x) sc[si] = floordiv64(shl64(sc[si], 20), es);
+  for (int si = tid; si < S; si += blockDim.x) sc[si] = floordiv_pos(shl64(sc[si], 20), es);
   __syncthreads();
   // p.V: thread (j, part) sums keys si = part, part + nparts, ...
   const int nparts = blockDim.x / hd;   // hd divides 256
@@ -114,14 +124,22 @@ __global__ __launch_bounds__(256) void k_attention(const int16_t* __restrict__ q
   int64_t a = 0;
   if (pp < nparts) {
     const int64_t* vb = v + cbase * hd + j;
+#pragma unroll 4
     for (int si = pp; si < S; si += nparts) a = (int64_t)((uint64_t)a + (uint64_t)(sc[si] * vb[(int64_t)si * hd]));
   }
   part[tid] = a;
   __syncthreads();
+  int m = 0;
   if (tid < hd) {
     uint64_t tot = 0;
     for (int k = 0; k < nparts; ++k) tot += (uint64_t)part[k * hd + tid];
-    out[((int64_t)r * H + h) * hd + tid] = shr64((int64_t)tot, 20);
+    const int64_t o = shr64((int64_t)tot, 20);
+    out[((int64_t)r * H + h) * hd + tid] = o;
+    m = bitlen64(abs64(o));
+  }
+  if (obits) {   // bit length of this head's max |out|, for the row quantisation of the o-projection input
+    m = block_max_i32(m, ored);
+    if (tid == 0) obits[(int64_t)r * H + h] = m;
   }
 }
 
@@ -143,12 +161,12 @@ extern "C" int exact_qkv_rope_cache(int64_t* t, const int32_t* s, const int64_t*
 
 extern "C" int exact_attention(const int16_t* qq, const int32_t* sq, const int16_t* kq, const int32_t* sk,
                                const int64_t* v, const int32_t* slot, const int32_t* pos, const int32_t* exp_t,
-                               int64_t* out, int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t Smax, int32_t INV,
-                               void* stream) {
+                               int64_t* out, int32_t* obits, int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t Smax,
+                               int32_t INV, void* stream) {
   if (!qq || !sq || !kq || !sk || !v || !slot || !pos || !exp_t || !out) return EXACT_E_ARG;
   if (R <= 0 || H <= 0 || KV <= 0 || H % KV || hd <= 0 || Smax <= 0) return EXACT_E_ARG;
-  if (hd > 256 || 256 % hd || Smax > 8192) return EXACT_E_UNSUPPORTED;
+  if (hd > 256 || 256 % hd || hd % 8 || Smax > 8192) return EXACT_E_UNSUPPORTED;
   hipLaunchKernelGGL(k_attention, dim3(R, H), dim3(256), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot, pos,
-                     exp_t, out, H, KV, hd, Smax, INV);
+                     exp_t, out, obits, H, KV, hd, Smax, INV);
   return launch_status("attention");
 }

@@ -70,7 +70,7 @@ __device__ void irms_inplace(int64_t* buf, const int64_t* __restrict__ g, int D,
   if (rt < 1) rt = 1;
   const int64_t den = shl64(rt, k);
   for (int i = threadIdx.x; i < D; i += blockDim.x) {
-    const int64_t y = floordiv64(shl64(buf[i], EXACT_F), den);
+    const int64_t y = floordiv_pos(shl64(buf[i], EXACT_F), den);
     buf[i] = shr64(y * g[i], EXACT_F);
   }
   __syncthreads();
@@ -86,57 +86,161 @@ __global__ void k_irms(const int64_t* __restrict__ x, const int64_t* __restrict_
   for (int i = threadIdx.x; i < D; i += blockDim.x) y[(int64_t)r * D + i] = buf[i];
 }
 
-__global__ void k_rmsnorm_qrow(int64_t* __restrict__ x, int64_t* __restrict__ res_t,
-                               const int32_t* __restrict__ res_s, const int64_t* __restrict__ g, int bits, void* xq,
-                               int32_t* s, int D, int clear_t) {
-  extern __shared__ int64_t buf[];
-  __shared__ int64_t red[16];
-  const int r = blockIdx.x;
+// One workgroup per row, EPT elements per thread held in registers: every global load of the row
+// (x, the residual total and the gains) is issued before the first use, so the row costs one memory
+// round trip instead of one per loop iteration. x += rs(res_t, 28 - res_s) in place; then
+// qrow(irms(x, g), bits) (exact_llm.py:41-46, 100-106).
+template <int EPT>
+__global__ __launch_bounds__(1024) void k_rmsnorm_qrow(int64_t* __restrict__ x, int64_t* __restrict__ res_t,
+                                                       const int32_t* __restrict__ res_s, const int64_t* __restrict__ g,
+                                                       int bits, void* xq, int32_t* s, int D, int clear_t) {
+  __shared__ int red_a[16], red_c[16];
+  __shared__ int64_t red_b[16];
+  const int r = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
   int64_t* xr = x + (int64_t)r * D;
-  if (res_t) {
-    const int sh = 28 - res_s[r];
-    for (int i = threadIdx.x; i < D; i += blockDim.x) {
-      const int64_t v = (int64_t)((uint64_t)xr[i] + (uint64_t)shr64(res_t[(int64_t)r * D + i], sh));
-      if (clear_t) res_t[(int64_t)r * D + i] = 0;
-      buf[i] = v;
-      xr[i] = v;
+  int64_t* tr = res_t ? res_t + (int64_t)r * D : nullptr;
+  int64_t v[EPT], gv[EPT], rv[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tid + j * nt;
+    v[j] = 0; gv[j] = 0; rv[j] = 0;
+    if (i < D) {
+      v[j] = xr[i];
+      gv[j] = g[i];
+      if (tr) rv[j] = tr[i];
     }
-  } else {
-    for (int i = threadIdx.x; i < D; i += blockDim.x) buf[i] = xr[i];
   }
-  __syncthreads();
-  irms_inplace(buf, g, D, red);
-  qrow_store(buf, D, bits, xq, s, r, red);
-}
-
-// gate|up total -> h = shr(isilu(g) * u, 16) (stored over the gate half) -> qrow
-__global__ void k_swiglu_qrow(int64_t* __restrict__ t, const int32_t* __restrict__ s, const int32_t* __restrict__ silu,
-                              int bits, void* xq, int32_t* sq, int I, int clear_t) {
-  __shared__ int64_t red[16];
-  const int r = blockIdx.x;
-  int64_t* tr = t + (int64_t)r * 2 * I;
-  const int sh = 28 - s[r];
-  int64_t m = 0;
-  for (int i = threadIdx.x; i < I; i += blockDim.x) {
-    const int64_t gv = shr64(tr[i], sh), uv = shr64(tr[I + i], sh);
-    const int64_t hv = shr64(lut16(silu, gv, false) * uv, EXACT_F);
-    tr[i] = hv;
-    if (clear_t) tr[I + i] = 0;
-    const int64_t a = abs64(hv);
-    m = a > m ? a : m;
+  int m = 0;   // max bit length of |x|
+  const int sh = tr ? 28 - res_s[r] : 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tid + j * nt;
+    if (i < D) {
+      if (tr) {
+        v[j] = (int64_t)((uint64_t)v[j] + (uint64_t)shr64(rv[j], sh));
+        xr[i] = v[j];
+        if (clear_t) tr[i] = 0;
+      }
+      const int bl = bitlen64(abs64(v[j]));
+      m = bl > m ? bl : m;
+    }
   }
-  m = block_max64(m, red);
-  int q = bitlen64(m) - bits;
+  m = block_max_i32(m, red_a);
+  int k = m - 24;
+  if (k < 0) k = 0;
+  int64_t ss = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int64_t xs = shr64(v[j], k);   // elements past D hold 0
+    ss = (int64_t)((uint64_t)ss + (uint64_t)(xs * xs));
+  }
+  ss = block_sum64_1(ss, red_b);
+  const int64_t ms = floordiv64(ss, D) + 1;
+  int64_t rt = isqrt64(ms);
+  if (rt < 1) rt = 1;
+  const int64_t den = shl64(rt, k);
+  int m2 = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    v[j] = shr64(floordiv_pos(shl64(v[j], EXACT_F), den) * gv[j], EXACT_F);
+    const int bl = bitlen64(abs64(v[j]));
+    m2 = (tid + j * nt < D && bl > m2) ? bl : m2;
+  }
+  m2 = block_max_i32(m2, red_c);
+  int q = m2 - bits;
   if (q < 0) q = 0;
   const int64_t lim = (1LL << bits) - 1;
-  for (int i = threadIdx.x; i < I; i += blockDim.x) {
-    int64_t v = shr64(tr[i], q);
-    if (clear_t) tr[i] = 0;
-    v = v > lim ? lim : (v < -lim ? -lim : v);
-    if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * I + i, v);
-    else store_q<int16_t>(xq, (int64_t)r * I + i, v);
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tid + j * nt;
+    if (i < D) {
+      int64_t w = shr64(v[j], q);
+      w = w > lim ? lim : (w < -lim ? -lim : w);
+      if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * D + i, w);
+      else store_q<int16_t>(xq, (int64_t)r * D + i, w);
+    }
   }
-  if (threadIdx.x == 0) sq[r] = q;
+  if (tid == 0) s[r] = q;
+}
+
+// Rows too long for one workgroup are split into slices of QSLICE elements; the producer kernel writes
+// each slice's bit length of max |v| to part[r * nparts + slice], and k_quant_rows quantises every slice
+// with the row's shift s = max(bitlen(max_row |v|) - bits, 0) (qrow, exact_llm.py:41-46), using
+// bitlen(max |v|) = max bitlen(|v|).
+#define QSLICE 1024
+
+// gate|up total -> h = shr(isilu(g) * u, 16) (stored over the gate half), slice maxima of |h|
+__global__ __launch_bounds__(256) void k_swiglu_part(int64_t* __restrict__ t, const int32_t* __restrict__ s,
+                                                     const int32_t* __restrict__ silu, int32_t* __restrict__ part, int I,
+                                                     int nparts, int clear_t) {
+  constexpr int EPT = QSLICE / 256;
+  __shared__ int red[4];
+  const int r = blockIdx.y, b = blockIdx.x;
+  int64_t* tr = t + (int64_t)r * 2 * I;
+  const int sh = 28 - s[r];
+  int64_t gv[EPT], uv[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = b * QSLICE + j * 256 + threadIdx.x;
+    gv[j] = i < I ? tr[i] : 0;
+    uv[j] = i < I ? tr[I + i] : 0;
+  }
+  int m = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = b * QSLICE + j * 256 + threadIdx.x;
+    if (i < I) {
+      const int64_t hv = shr64(lut16(silu, shr64(gv[j], sh), false) * shr64(uv[j], sh), EXACT_F);
+      tr[i] = hv;
+      if (clear_t) tr[I + i] = 0;
+      const int bl = bitlen64(abs64(hv));
+      m = bl > m ? bl : m;
+    }
+  }
+  m = block_max_i32(m, red);
+  if (threadIdx.x == 0) part[(int64_t)r * nparts + b] = m;
+}
+
+// grid (slices, R): xq[r][i] = clip(shr(src[r * ld + i], s_r), +-(2^bits - 1)), s_r from the slice maxima
+__global__ __launch_bounds__(256) void k_quant_rows(int64_t* __restrict__ src, int64_t ld, const int32_t* __restrict__ part,
+                                                    int nparts, int bits, void* xq, int32_t* __restrict__ s, int K,
+                                                    int clear) {
+  __shared__ int qs;
+  const int r = blockIdx.y, b = blockIdx.x;
+  if (threadIdx.x < 64) {
+    int m = 0;
+    for (int i = threadIdx.x; i < nparts; i += 64) {
+      const int v = part[(int64_t)r * nparts + i];
+      m = v > m ? v : m;
+    }
+    m = wave_max_i32(m);
+    if (threadIdx.x == 0) {
+      const int q = m - bits;
+      qs = q < 0 ? 0 : q;
+    }
+  }
+  __syncthreads();
+  const int q = qs;
+  if (b == 0 && threadIdx.x == 0) s[r] = q;
+  const int64_t lim = (1LL << bits) - 1;
+  constexpr int EPT = QSLICE / 256;
+  int64_t vv[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = b * QSLICE + j * 256 + threadIdx.x;
+    vv[j] = i < K ? src[(int64_t)r * ld + i] : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = b * QSLICE + j * 256 + threadIdx.x;
+    if (i < K) {
+      if (clear) src[(int64_t)r * ld + i] = 0;
+      int64_t v = shr64(vv[j], q);
+      v = v > lim ? lim : (v < -lim ? -lim : v);
+      if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * K + i, v);
+      else store_q<int16_t>(xq, (int64_t)r * K + i, v);
+    }
+  }
 }
 
 __global__ void k_requant_group(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
@@ -189,7 +293,7 @@ __global__ void k_isoftmax(const int64_t* __restrict__ sc, const int32_t* __rest
   for (int i = threadIdx.x; i < nv; i += blockDim.x) es += lut_exp(T, mx - row[i]);
   es = block_sum64(es, red);
   for (int i = threadIdx.x; i < N; i += blockDim.x)
-    p[(int64_t)r * N + i] = i < nv ? floordiv64(shl64(lut_exp(T, mx - row[i]), 20), es) : 0;
+    p[(int64_t)r * N + i] = i < nv ? floordiv_pos(shl64(lut_exp(T, mx - row[i]), 20), es) : 0;
 }
 
 __global__ void k_embed(const int32_t* __restrict__ ids, const int32_t* __restrict__ emb, int64_t* __restrict__ x,
@@ -200,33 +304,57 @@ __global__ void k_embed(const int32_t* __restrict__ ids, const int32_t* __restri
   for (int i = threadIdx.x; i < D; i += blockDim.x) x[(int64_t)r * D + i] = emb[(int64_t)id * D + i];
 }
 
-__global__ void k_logits_argmax(int64_t* t, const int32_t* __restrict__ s, int64_t* lg, int32_t* ids, int N, int clear_t) {
-  __shared__ int64_t bv[16];
-  __shared__ int bi[16];
-  const int r = blockIdx.x;
+// logits = shr(t, 28 - s) over slices of LSLICE columns; each slice's first maximum (value, index)
+// goes to part; k_argmax_parts picks the row's first maximum (exact_llm.py:267: np.argmax)
+#define LSLICE 4096
+__device__ __forceinline__ void argmax_merge(int64_t& best, int& bidx, int64_t ov, int oi) {
+  if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
+}
+
+__global__ __launch_bounds__(256) void k_logits_part(int64_t* t, const int32_t* __restrict__ s, int64_t* lg,
+                                                     int64_t* __restrict__ part, int N, int nparts, int clear_t) {
+  __shared__ int64_t bv[4];
+  __shared__ int bi[4];
+  const int r = blockIdx.y, b = blockIdx.x;
   const int sh = 28 - s[r];
+  constexpr int EPT = LSLICE / 256;
+  int64_t tv[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = b * LSLICE + j * 256 + threadIdx.x;
+    tv[j] = i < N ? t[(int64_t)r * N + i] : 0;
+  }
   int64_t best = INT64_MIN;
   int bidx = 0x7fffffff;
-  for (int i = threadIdx.x; i < N; i += blockDim.x) {
-    const int64_t v = shr64(t[(int64_t)r * N + i], sh);
-    if (clear_t) t[(int64_t)r * N + i] = 0;
-    if (lg) lg[(int64_t)r * N + i] = v;
-    if (v > best) { best = v; bidx = i; }   // i increases per thread: keeps the first max
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = b * LSLICE + j * 256 + threadIdx.x;
+    if (i < N) {
+      const int64_t v = shr64(tv[j], sh);
+      if (clear_t) t[(int64_t)r * N + i] = 0;
+      if (lg) lg[(int64_t)r * N + i] = v;
+      if (v > best) { best = v; bidx = i; }   // i increases per thread: keeps the first max
+    }
   }
-  // wave reduction with lowest-index tie-break
-  for (int o = 32; o > 0; o >>= 1) {
-    const int64_t ov = __shfl_xor(best, o, 64);
-    const int oi = __shfl_xor(bidx, o, 64);
-    if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
-  }
-  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  for (int o = 32; o > 0; o >>= 1) argmax_merge(best, bidx, __shfl_xor(best, o, 64), __shfl_xor(bidx, o, 64));
+  const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { bv[w] = best; bi[w] = bidx; }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int i = 1; i < nw; ++i)
-      if (bv[i] > best || (bv[i] == best && bi[i] < bidx)) { best = bv[i]; bidx = bi[i]; }
-    if (ids) ids[r] = bidx;
+    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) argmax_merge(best, bidx, bv[i], bi[i]);
+    part[((int64_t)r * nparts + b) * 2] = best;
+    part[((int64_t)r * nparts + b) * 2 + 1] = bidx;
   }
+}
+
+__global__ void k_argmax_parts(const int64_t* __restrict__ part, int nparts, int32_t* __restrict__ ids) {
+  const int r = blockIdx.x;
+  int64_t best = INT64_MIN;
+  int bidx = 0x7fffffff;
+  for (int i = threadIdx.x; i < nparts; i += 64)
+    argmax_merge(best, bidx, part[((int64_t)r * nparts + i) * 2], (int)part[((int64_t)r * nparts + i) * 2 + 1]);
+  for (int o = 32; o > 0; o >>= 1) argmax_merge(best, bidx, __shfl_xor(best, o, 64), __shfl_xor(bidx, o, 64));
+  if (threadIdx.x == 0) ids[r] = bidx;
 }
 
 __global__ void k_advance(int32_t* pos, int R) {
@@ -234,7 +362,7 @@ __global__ void k_advance(int32_t* pos, int R) {
   if (i < R) pos[i] += 1;
 }
 
-static inline int blk_for(int n) { return n >= 2048 ? 512 : 256; }
+static inline int blk_for(int n) { return n >= 2048 ? 1024 : 256; }
 
 }  // namespace exact
 
@@ -263,16 +391,34 @@ extern "C" int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res
                                   void* xq, int32_t* s, int32_t R, int32_t D, int32_t clear_t, void* stream) {
   if (!x || !g || !xq || !s || R <= 0 || D <= 0 || bits < 1 || bits > 15 || (res_t && !res_s)) return EXACT_E_ARG;
   if (D > SMEM_ROW_MAX) return EXACT_E_UNSUPPORTED;
-  hipLaunchKernelGGL(k_rmsnorm_qrow, dim3(R), dim3(blk_for(D)), D * 8, as_stream(stream), x, res_t, res_s, g, bits, xq, s,
-                     D, clear_t);
+  const int nt = D >= 1024 ? 1024 : ((D + 63) / 64) * 64;
+  const int ept = (D + nt - 1) / nt;
+  hipStream_t st = as_stream(stream);
+#define RMS_GO(E) hipLaunchKernelGGL(k_rmsnorm_qrow<E>, dim3(R), dim3(nt), 0, st, x, res_t, res_s, g, bits, xq, s, D, clear_t)
+  if (ept <= 1) RMS_GO(1);
+  else if (ept <= 2) RMS_GO(2);
+  else if (ept <= 4) RMS_GO(4);
+  else RMS_GO(8);
+#undef RMS_GO
   return launch_status("rmsnorm_qrow");
 }
 
 extern "C" int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq, int32_t* sq,
-                                 int32_t R, int32_t I, int32_t clear_t, void* stream) {
-  if (!t || !s || !silu_t || !xq || !sq || R <= 0 || I <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
-  hipLaunchKernelGGL(k_swiglu_qrow, dim3(R), dim3(blk_for(I)), 0, as_stream(stream), t, s, silu_t, bits, xq, sq, I, clear_t);
+                                 int32_t* part, int32_t R, int32_t I, int32_t clear_t, void* stream) {
+  if (!t || !s || !silu_t || !xq || !sq || !part || R <= 0 || I <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
+  const int np = (I + QSLICE - 1) / QSLICE;
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(k_swiglu_part, dim3(np, R), dim3(256), 0, st, t, s, silu_t, part, I, np, clear_t);
+  hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, t, (int64_t)2 * I, part, np, bits, xq, sq, I, clear_t);
   return launch_status("swiglu_qrow");
+}
+
+extern "C" int exact_quant_rows(int64_t* src, int64_t ld, const int32_t* part, int32_t nparts, int32_t bits, void* xq,
+                                int32_t* s, int32_t R, int32_t K, int32_t clear, void* stream) {
+  if (!src || !part || !xq || !s || R <= 0 || K <= 0 || ld < K || nparts <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
+  hipLaunchKernelGGL(k_quant_rows, dim3((K + QSLICE - 1) / QSLICE, R), dim3(256), 0, as_stream(stream), src, ld, part, nparts,
+                     bits, xq, s, K, clear);
+  return launch_status("quant_rows");
 }
 
 extern "C" int exact_requant_group(const int64_t* t, const int32_t* s, const int64_t* b, int64_t* y, int32_t R, int32_t N,
@@ -321,10 +467,13 @@ extern "C" int exact_embed(const int32_t* ids, const int32_t* emb, int64_t* x, i
   return launch_status("embed");
 }
 
-extern "C" int exact_logits_argmax(int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int32_t R, int32_t N,
-                                   int32_t clear_t, void* stream) {
-  if (!t || !s || R <= 0 || N <= 0 || (clear_t && lg == t)) return EXACT_E_ARG;
-  hipLaunchKernelGGL(k_logits_argmax, dim3(R), dim3(1024), 0, as_stream(stream), t, s, lg, ids, N, clear_t);
+extern "C" int exact_logits_argmax(int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int64_t* part, int32_t R,
+                                   int32_t N, int32_t clear_t, void* stream) {
+  if (!t || !s || !part || R <= 0 || N <= 0 || (clear_t && lg == t)) return EXACT_E_ARG;
+  const int np = (N + LSLICE - 1) / LSLICE;
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(k_logits_part, dim3(np, R), dim3(256), 0, st, t, s, lg, part, N, np, clear_t);
+  if (ids) hipLaunchKernelGGL(k_argmax_parts, dim3(R), dim3(64), 0, st, part, np, ids);
   return launch_status("logits_argmax");
 }
 

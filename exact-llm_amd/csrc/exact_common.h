@@ -52,6 +52,19 @@ __device__ __forceinline__ int64_t floordiv64(int64_t a, int64_t b) {
   return (r != 0 && ((r < 0) != (b < 0))) ? q - 1 : q;
 }
 
+// floor(a / b) for b > 0: a float64 estimate of the quotient, then an exact integer correction of the
+// remainder into [0, b). Exact for every int64 a (the estimate only bounds the number of correction
+// steps: one or two whenever |a / b| < 2^50, which covers every use here).
+__device__ __forceinline__ int64_t floordiv_pos(int64_t a, int64_t b) {
+  double qd = __builtin_floor((double)a / (double)b);
+  qd = qd > 9.2e18 ? 9.2e18 : (qd < -9.2e18 ? -9.2e18 : qd);
+  int64_t q = (int64_t)qd;
+  int64_t r = (int64_t)((uint64_t)a - (uint64_t)q * (uint64_t)b);
+  while (r < 0) { --q; r += b; }
+  while (r >= b) { ++q; r -= b; }
+  return q;
+}
+
 __device__ __forceinline__ int64_t isqrt64(int64_t n) {
   if (n <= 0) return 0;
   int64_t r = (int64_t)__builtin_sqrt((double)n);
@@ -112,6 +125,35 @@ __device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t* scratch) {
   __syncthreads();
   if ((threadIdx.x & 63) == 0) scratch[w] = v;
   __syncthreads();
+  uint64_t r = 0;
+  for (int i = 0; i < nw; ++i) r += (uint64_t)scratch[i];
+  return (int64_t)r;
+}
+
+// Single-barrier block reductions: each call needs its own scratch array (no barrier protects a reused
+// one). bitlen(max |v|) = max bitlen(|v|), so the max reductions of qrow / irms run on 32-bit bit lengths.
+__device__ __forceinline__ int wave_max_i32(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const int w = __shfl_xor(v, o, 64);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+__device__ __forceinline__ int block_max_i32(int v, int* scratch) {
+  v = wave_max_i32(v);
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const int nw = blockDim.x >> 6;
+  int r = scratch[0];
+  for (int i = 1; i < nw; ++i) r = scratch[i] > r ? scratch[i] : r;
+  return r;
+}
+__device__ __forceinline__ int64_t block_sum64_1(int64_t v, int64_t* scratch) {
+  v = wave_sum64(v);
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const int nw = blockDim.x >> 6;
   uint64_t r = 0;
   for (int i = 0; i < nw; ++i) r += (uint64_t)scratch[i];
   return (int64_t)r;

@@ -33,7 +33,7 @@ __global__ void k_router_topk(int64_t* __restrict__ t, const int32_t* __restrict
   int64_t es = 0;
   for (int i = threadIdx.x; i < NE; i += blockDim.x) es += lut_exp(T, mx - sp[i]);
   es = block_sum64(es, red);
-  for (int i = threadIdx.x; i < NE; i += blockDim.x) sp[i] = floordiv64(shl64(lut_exp(T, mx - sp[i]), 20), es);
+  for (int i = threadIdx.x; i < NE; i += blockDim.x) sp[i] = floordiv_pos(shl64(lut_exp(T, mx - sp[i]), 20), es);
   __syncthreads();
   for (int i = threadIdx.x; i < NE; i += blockDim.x) {
     const int64_t pi = sp[i];

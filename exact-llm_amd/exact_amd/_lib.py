@@ -27,15 +27,16 @@ SIGNATURES = {
     "exact_qrow": [P, I32, P, P, I32, I32, P],
     "exact_irms": [P, P, P, I32, I32, P],
     "exact_rmsnorm_qrow": [P, P, P, P, I32, P, P, I32, I32, I32, P],
-    "exact_swiglu_qrow": [P, P, P, I32, P, P, I32, I32, I32, P],
+    "exact_swiglu_qrow": [P, P, P, I32, P, P, P, I32, I32, I32, P],
+    "exact_quant_rows": [P, I64, P, I32, I32, P, P, I32, I32, I32, P],
     "exact_isilu": [P, P, P, I64, P],
     "exact_isig": [P, P, P, I64, P],
     "exact_isoftmax": [P, P, P, P, I32, I32, P],
     "exact_qkv_rope_cache": [P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
-    "exact_attention": [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
+    "exact_attention": [P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
     "exact_embed": [P, P, P, I32, I32, I32, P],
     "exact_embed_table": [P, P, P, I32, I32, P],
-    "exact_logits_argmax": [P, P, P, P, I32, I32, I32, P],
+    "exact_logits_argmax": [P, P, P, P, P, I32, I32, I32, P],
     "exact_advance": [P, I32, P],
     "exact_zero": [P, I64, P],
     "exact_router_topk": [P, P, P, P, P, I32, I32, I32, I32, P],

@@ -151,6 +151,9 @@ class Workspace:
         self.t_d, self.t_head = z(R, D), z(R, V)
         self.logits, self.next_ids = z(R, V), z(R, dt=I32)
         self.s28 = torch.full((R,), 28, dtype=I32, device=device)
+        self.part_sw = ops.swiglu_parts(R, max(I, cfg.SI if cfg.moe else 0), device)
+        self.part_lg = ops.logits_parts(R, V, device)
+        self.obits = z(R, H, dt=I32)
         self.ids, self.slot, self.pos = z(R, dt=I32), z(R, dt=I32), z(R, dt=I32)
         if cfg.moe:
             k, P = cfg.topk, R * cfg.topk
@@ -162,6 +165,7 @@ class Workspace:
             self.t_ed = z(P, D)
             self.t_sgu, self.shq, self.ssh = z(R, 2 * cfg.SI), z(R, cfg.SI, dt=adt), z(R, dt=I32)
             self.t_sd, self.t_sg = z(R, D), z(R, 1)
+            self.part_esw = ops.swiglu_parts(P, cfg.MI, device)
 
 
 class TModel:
@@ -225,8 +229,8 @@ class TModel:
                 s_qkv, b_qkv = ws.s28, None
             ops.qkv_rope_cache(ws.t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache, ws.qq, ws.sq, H, KV, hd,
                                clear=group)
-            ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv)
-            ops.qrow(ws.att, self.abits, ws.aq, ws.sa)
+            ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv, ws.obits)
+            ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa)
             if group:
                 self._lin(ws.aq, L["o"], ws.t_o)
                 ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.sa, ws.xq, ws.s, clear=True)
@@ -241,7 +245,7 @@ class TModel:
                 continue
             if group:
                 self._lin(ws.xq, L["gateup"], ws.t_gu)
-                ops.swiglu_qrow(ws.t_gu, ws.s, tab.silu, self.abits, ws.hq, ws.sh, clear=True)
+                ops.swiglu_qrow(ws.t_gu, ws.s, tab.silu, self.abits, ws.hq, ws.sh, clear=True, part=ws.part_sw)
                 self._lin(ws.hq, L["down"], ws.t_d)
                 res_t, res_s = ws.t_d, ws.sh
             else:
@@ -250,16 +254,17 @@ class TModel:
                 yu = self._lin_channel(ws.xq, ws.s, L["up"], torch.empty((R, I), dtype=I64, device=self.dev))
                 ws.t_gu[:, :I].copy_(yg)
                 ws.t_gu[:, I:].copy_(yu)
-                ops.swiglu_qrow(ws.t_gu, ws.s28, tab.silu, self.abits, ws.hq, ws.sh)
+                ops.swiglu_qrow(ws.t_gu, ws.s28, tab.silu, self.abits, ws.hq, ws.sh, part=ws.part_sw)
                 self._lin_channel(ws.hq, ws.sh, L["down"], ws.t_d)
                 res_t, res_s = ws.t_d, ws.s28
         ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=group)
         if group:
             self._lin(ws.xq, self.w.head, ws.t_head)
-            ops.logits_argmax(ws.t_head, ws.s, ws.logits if want_logits else None, ws.next_ids, clear=True)
+            ops.logits_argmax(ws.t_head, ws.s, ws.logits if want_logits else None, ws.next_ids, clear=True,
+                              part=ws.part_lg)
         else:
             self._lin_channel(ws.xq, ws.s, self.w.head, ws.t_head)
-            ops.logits_argmax(ws.t_head, ws.s28, ws.logits if want_logits else None, ws.next_ids)
+            ops.logits_argmax(ws.t_head, ws.s28, ws.logits if want_logits else None, ws.next_ids, part=ws.part_lg)
         return ws
 
     def _moe(self, ws, L):
@@ -271,10 +276,10 @@ class TModel:
         ops.router_topk(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, clear=True)
         ops.moe_dispatch(ws.e_sel, ws.s, c.NE, k, ops.chunk_rows(self.abits), ws.disp)
         ops.gemv_experts(ws.xq, self.abits, ws.disp["pair_row"], L["egu"], ws.disp, ws.t_egu)
-        ops.swiglu_qrow(ws.t_egu, ws.disp["s_pair"], tab.silu, self.abits, ws.ehq, ws.esh, clear=True)
+        ops.swiglu_qrow(ws.t_egu, ws.disp["s_pair"], tab.silu, self.abits, ws.ehq, ws.esh, clear=True, part=ws.part_esw)
         ops.gemv_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed)
         self._lin(ws.xq, L["sgu"], ws.t_sgu)
-        ops.swiglu_qrow(ws.t_sgu, ws.s, tab.silu, self.abits, ws.shq, ws.ssh, clear=True)
+        ops.swiglu_qrow(ws.t_sgu, ws.s, tab.silu, self.abits, ws.shq, ws.ssh, clear=True, part=ws.part_sw)
         self._lin(ws.shq, L["sd"], ws.t_sd)
         self._lin(ws.xq, L["sgate"], ws.t_sg)
         ops.moe_combine(ws.x, ws.t_ed, ws.esh, ws.p_sel, ws.disp["pidx"], k, ws.t_sd, ws.ssh, ws.t_sg, ws.s, tab.sig,

@@ -167,13 +167,31 @@ def rmsnorm_qrow(x, g, bits=15, res_t=None, res_s=None, xq=None, s=None, clear=F
     return xq, s
 
 
-def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None, clear=False):
+QSLICE, LSLICE = 1024, 4096   # row slice lengths of the multi-block row kernels
+
+
+def swiglu_parts(R, I, device):
+    return torch.empty(R * -(-I // QSLICE), dtype=I32, device=device)
+
+
+def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None, clear=False, part=None):
     R, N2 = t.shape
     I = N2 // 2
     xq = torch.empty((R, I), dtype=I16 if bits > 7 else I8, device=t.device) if xq is None else xq
     sq = torch.empty(R, dtype=I32, device=t.device) if sq is None else sq
-    _lib.call("exact_swiglu_qrow", _ptr(_need(t, I64, "t")), _ptr(s), _ptr(silu), bits, _ptr(xq), _ptr(sq), R, I, int(clear), _stream())
+    part = swiglu_parts(R, I, t.device) if part is None else _need(part, I32, "part", R * -(-I // QSLICE))
+    _lib.call("exact_swiglu_qrow", _ptr(_need(t, I64, "t")), _ptr(s), _ptr(silu), bits, _ptr(xq), _ptr(sq), _ptr(part), R, I,
+              int(clear), _stream())
     return xq, sq
+
+
+def quant_rows(src, part, nparts, bits, xq, s, K=None, clear=False):
+    """qrow of src rows (first K columns) given per-slice bit lengths of max |src| part (R, nparts) int32."""
+    R, ld = src.shape
+    K = ld if K is None else K
+    _lib.call("exact_quant_rows", _ptr(_need(src, I64, "src")), ld, _ptr(_need(part, I32, "part", R * nparts)), nparts, bits,
+              _ptr(xq), _ptr(_need(s, I32, "s", R)), R, K, int(clear), _stream())
+    return xq, s
 
 
 def isilu(x, silu):
@@ -204,12 +222,14 @@ def qkv_rope_cache(t, s, b, cos, sin, slot, pos, cache, qq, sq, H, KV, hd, clear
               _ptr(sq), _ptr(kq), _ptr(sk), _ptr(v), R, H, KV, hd, Smax, int(clear), _stream())
 
 
-def attention(qq, sq, cache, slot, pos, expt, out, H, KV, hd, inv):
+def attention(qq, sq, cache, slot, pos, expt, out, H, KV, hd, inv, obits=None):
     R = qq.shape[0]
     kq, sk, v = cache
     Smax = kq.shape[2]
+    if obits is not None:
+        _need(obits, I32, "obits", R * H)
     _lib.call("exact_attention", _ptr(qq), _ptr(sq), _ptr(kq), _ptr(sk), _ptr(v), _ptr(slot), _ptr(pos), _ptr(expt),
-              _ptr(out), R, H, KV, hd, Smax, inv, _stream())
+              _ptr(out), _ptr(obits), R, H, KV, hd, Smax, inv, _stream())
     return out
 
 
@@ -226,9 +246,14 @@ def embed_table(lin, V, D):
     return emb
 
 
-def logits_argmax(t, s, lg=None, ids=None, clear=False):
+def logits_parts(R, N, device):
+    return torch.empty(R * -(-N // LSLICE) * 2, dtype=I64, device=device)
+
+
+def logits_argmax(t, s, lg=None, ids=None, clear=False, part=None):
     R, N = t.shape
-    _lib.call("exact_logits_argmax", _ptr(t), _ptr(s), _ptr(lg), _ptr(ids), R, N, int(clear), _stream())
+    part = logits_parts(R, N, t.device) if part is None else _need(part, I64, "part", R * -(-N // LSLICE) * 2)
+    _lib.call("exact_logits_argmax", _ptr(t), _ptr(s), _ptr(lg), _ptr(ids), _ptr(part), R, N, int(clear), _stream())
     return lg, ids
 
 

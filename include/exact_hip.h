@@ -100,10 +100,17 @@ int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res_s, const i
 
 /* SwiGLU on a fused gate|up total: g = rs(t[r][n], 28 - s[r]), u = rs(t[r][I + n], 28 - s[r]),
  * h = round_shift(isilu(g) * u, 16); xq, sq = qrow(h, bits). t's gate half is overwritten with h, or all
- * of t is left zeroed when clear_t != 0.
+ * of t is left zeroed when clear_t != 0. part: int32 workspace of R * ceil(I / 1024) slice bit lengths.
  * (exact_llm.py:179; isilu exact_llm.py:118-122). */
 int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq,
-                      int32_t* sq, int32_t R, int32_t I, int32_t clear_t, void* stream);
+                      int32_t* sq, int32_t* part, int32_t R, int32_t I, int32_t clear_t, void* stream);
+
+/* qrow with the row maximum supplied in parts (a producer kernel wrote part[r * nparts + i] =
+ * bitlen(max |src| over its slice i of row r)): s = max(max_i part - bits, 0), xq = clip(rs(src, s))
+ * (exact_llm.py:41-46; bitlen of the row max = max of the slice bit lengths). src rows are ld apart;
+ * clear != 0 leaves src zeroed. */
+int exact_quant_rows(int64_t* src, int64_t ld, const int32_t* part, int32_t nparts, int32_t bits, void* xq,
+                     int32_t* s, int32_t R, int32_t K, int32_t clear, void* stream);
 
 /* Elementwise LUT nonlinearities on int64 arrays (isilu exact_llm.py:118-122; isig moe_exact_kaggle.py:420-424). */
 int exact_isilu(const int64_t* x, const int32_t* silu_t, int64_t* y, int64_t n, void* stream);
@@ -130,11 +137,12 @@ int exact_qkv_rope_cache(int64_t* t, const int32_t* s, const int64_t* b, const i
 /* Integer attention of R query rows against the cache, keys 0..pos[r] of slot[r]:
  * sc = rs((qq . kq) * INV, 32 - sq - sk); p = isoftmax(sc) (Q20); out = rs(p . v, 20), out (R, H*hd) int64.
  * (exact_llm.py:170-176; exact_torch.py:162-166; speed_fair_kaggle.py:620-624). Used for decode and,
- * with pos[r] = p0 + r, for causal prefill. */
+ * with pos[r] = p0 + r, for causal prefill. obits (optional, R * H): bit length of max |out| per head,
+ * the parts that exact_quant_rows takes for the o-projection input. */
 int exact_attention(const int16_t* qq, const int32_t* sq, const int16_t* kq, const int32_t* sk,
                     const int64_t* v, const int32_t* slot, const int32_t* pos, const int32_t* exp_t,
-                    int64_t* out, int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t Smax, int32_t INV,
-                    void* stream);
+                    int64_t* out, int32_t* obits, int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t Smax,
+                    int32_t INV, void* stream);
 
 /* ---- mixture of experts (MoEInt.moe, moe_exact_kaggle.py:454-467) ------------------------------------
  * Router: logits = rs(t, 28 - s[r]) (t (R, NE) from the router linear); p = isoftmax over all NE experts
@@ -176,8 +184,9 @@ int exact_embed(const int32_t* ids, const int32_t* emb, int64_t* x, int32_t R, i
 int exact_embed_table(const int8_t* wp, const int16_t* mp, int32_t* emb, int32_t V, int32_t D, void* stream);
 
 /* Logits and greedy tokens: lg = rs(t, 28 - s[r]) (lg may alias t unless clear_t); ids[r] = first argmax
- * of lg[r] (exact_llm.py:180,267). lg or ids may be NULL to skip; clear_t != 0 leaves t zeroed. */
-int exact_logits_argmax(int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int32_t R,
+ * of lg[r] (exact_llm.py:180,267). lg or ids may be NULL to skip; clear_t != 0 leaves t zeroed.
+ * part: int64 workspace of R * ceil(N / 4096) * 2 (per-slice first maxima). */
+int exact_logits_argmax(int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int64_t* part, int32_t R,
                         int32_t N, int32_t clear_t, void* stream);
 
 /* pos[r] += 1 for r < R (advances a decode step inside a captured graph; GraphDecoder.step :645). */

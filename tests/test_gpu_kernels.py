@@ -139,6 +139,43 @@ def test_lut_nonlinearities_and_softmax():
     assert np.array_equal(p, O.isoftmax(sc, valid))
 
 
+def test_logits_argmax_first_max_across_slices():
+    """Multi-slice argmax keeps numpy's first maximum: ties inside a slice, across slices, at slice edges."""
+    R, N = 5, 152064
+    t = rng.integers(-(1 << 40), 1 << 40, (R, N))
+    s = rng.integers(8, 16, R).astype(np.int32)
+    lg = O.round_shift(t, 28 - s[:, None].astype(np.int64))
+    top = lg.max() + (1 << 30)
+    for r, cols in enumerate([(4095, 4096), (100000, 7), (152063,), (0, 152063), (4096, 8191, 8192)]):
+        for c in cols:
+            t[r, c] = top << (28 - int(s[r]))
+    lg = O.round_shift(t, 28 - s[:, None].astype(np.int64))
+    td, ids = dev(t, I64), torch.zeros(R, dtype=I32, device=DEV)
+    out = torch.zeros((R, N), dtype=I64, device=DEV)
+    ops.logits_argmax(td, dev(s, I32), out, ids, clear=True)
+    assert np.array_equal(host(out), lg)
+    assert host(ids).tolist() == lg.argmax(-1).tolist()
+    assert not host(td).any()
+
+
+def test_quant_rows_from_partial_maxima():
+    R, K, ld = 3, 5000, 5120
+    x = rng.integers(-(1 << 40), 1 << 40, (R, ld))
+    x[1] >>= 30                                    # a row with a small shift
+    x[2] = 0                                       # an all-zero row: s = 0
+    nparts = 7
+    part = np.zeros((R, nparts), np.int64)
+    for r in range(R):                             # any split of the row into parts gives the same maximum
+        for i, chunk in enumerate(np.array_split(np.abs(x[r, :K]), nparts)):
+            part[r, i] = O.bitlen(chunk.max())
+    xd = dev(x, I64)
+    xq, sq = torch.zeros((R, K), dtype=torch.int16, device=DEV), torch.zeros(R, dtype=I32, device=DEV)
+    ops.quant_rows(xd, dev(part, I32), nparts, 15, xq, sq, K=K, clear=True)
+    eq, es = O.qrow(x[:, :K], 15)
+    assert np.array_equal(host(xq).astype(np.int64), eq) and np.array_equal(host(sq), es[:, 0])
+    assert not host(xd)[:, :K].any() and np.array_equal(host(xd)[:, K:], x[:, K:])
+
+
 def test_swiglu_qrow():
     from exact_amd.tables import silu_t
     R, I = 3, 4864
