@@ -8,7 +8,10 @@ Also reported: the pass's HBM rate, per-shape GEMV rates (HIP events on the laun
 prefill GEMM rate (M = 2048, K = 3584 -> N = 18944 and K = 18944 -> N = 3584) and the numpy oracle
 timed on the host cores as the CPU baseline.
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
+Also: full-model decode (embedding to greedy token) of the 7B shape, the 0.5B (bs1), 14B (bs1, bs8) and
+MoE (bs1) configurations, and the exact integer attention of a 2048-token prefill layer.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill] [--no-model]
 """
 import argparse
 import json
@@ -21,6 +24,11 @@ sys.path.insert(0, os.path.join(ROOT, "exact-llm_amd"))
 
 METRIC = "decode tok/s (7B-shape, bs1); GEMV HBM GB/s; prefill int8 MFMA TOPS"
 HBM_PEAK_GBPS = 8000.0
+# gate|up launch: 37888*3584 int8 weights + 37888*28*2 scale bytes + 3584 x bytes + 37888*8 output bytes
+GATEUP_BYTES = 37888 * 3584 + 37888 * 28 * 2 + 3584 + 37888 * 8
+# HBM bytes per gate|up launch from FETCH_SIZE / WRITE_SIZE counter runs, each scaled by the same counter on a
+# 512 MiB device copy (profiles/gemv_gateup_7b_traffic.md)
+GATEUP_TRAFFIC_BYTES = 139_850_000
 INT8_PEAK_TOPS = 5000.0
 
 
@@ -130,39 +138,96 @@ def gemv_pass(args):
     return dict(ms=ms, wall=wall, pass_bytes=pass_bytes, per=per)
 
 
-def model_decode(args, name="qwen2.5-7b", prompt_len=16):
-    """Full integer decode step of the 7B-architecture model (embedding, 28 layers of irms, fused q|k|v GEMV,
-    RoPE, integer attention over the KV cache, o, SwiGLU, down, head + greedy argmax), A16 activations as in
-    the spec, bs1, one HIP graph per step."""
+def active_bytes(cfg):
+    """int8 weight + int16 scale bytes read per decode token (MoE: the top-k experts, the shared expert and the router)."""
+    from exact_amd import synth
+    if not cfg.moe:
+        return synth.param_bytes(cfg)
+    D = cfg.D
+    lb = lambda N, K: N * K + N * (K // 128) * 2
+    layer = (lb((cfg.H + 2 * cfg.KV) * cfg.hd, D) + lb(D, cfg.H * cfg.hd) + lb(cfg.NE, D) + lb(1, D)
+             + cfg.topk * (lb(2 * cfg.MI, D) + lb(D, cfg.MI)) + lb(2 * cfg.SI, D) + lb(D, cfg.SI))
+    return cfg.NL * layer + lb(cfg.V, D)
+
+
+def model_decode(args, name="qwen2.5-7b", prompt_len=16, B=1):
+    """Full integer decode steps of a model (embedding, per layer irms, fused q|k|v GEMV, RoPE, integer
+    attention over the KV cache, o, SwiGLU or MoE, down, head + greedy argmax), A16 activations as in the
+    spec, B sequences per step, one HIP graph per step. Prefill (each sequence's prompt) is timed too."""
     import numpy as np
     import torch
     from exact_amd import synth
     from exact_amd.model import DeviceWeights, GraphDecoder, TModel
     cfg = synth.CONFIGS[name]
-    tm = TModel(DeviceWeights.synthetic(cfg, 11, "cuda"), Smax=prompt_len + args.warmup + args.steps + 8)
-    ids = np.random.default_rng(0).integers(0, cfg.V, prompt_len).tolist()
-    cache = tm.new_cache(B=1)
-    lg = tm.forward(ids, cache)
-    first = int(lg[-1].argmax())
-    gd = GraphDecoder(tm, cache, 1)
-    gd.load([first])
+    tm = TModel(DeviceWeights.synthetic(cfg, 11, "cuda"), Smax=prompt_len + args.warmup + args.steps + 8, batch=B)
+    rng = np.random.default_rng(0)
+    cache = tm.new_cache()
+    st = torch.cuda.current_stream()
+    first = []
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(st)
+    for s_ in range(B):
+        lg = tm.forward(rng.integers(0, cfg.V, prompt_len).tolist(), cache, last_only=True, slot=s_)
+        first.append(int(lg[-1].argmax()))
+    b.record(st)
+    torch.cuda.synchronize()
+    prefill_ms = a.elapsed_time(b) / B
+    tm._ws.pop(prompt_len, None)
+    gd = GraphDecoder(tm, cache, B)
+    gd.load(first)
     gd.capture()
     for _ in range(args.warmup):
         gd.step()
     torch.cuda.synchronize()
-    st = torch.cuda.current_stream()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record(st)
     for _ in range(args.steps):
         gd.step()
     b.record(st)
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / args.steps
-    wbytes = synth.param_bytes(cfg)
+    wbytes = active_bytes(cfg)
     del tm, gd, cache
     torch.cuda.empty_cache()
-    return {"model": name, "tok_s": round(1000.0 / ms, 2), "ms_per_token": round(ms, 4), "abits": 15,
-            "weights_GB": round(wbytes / 1e9, 3), "GBps": round(wbytes / ms / 1e6, 1), "prompt": prompt_len}
+    return {"model": name, "batch": B, "tok_s": round(1000.0 * B / ms, 2), "ms_per_step": round(ms, 4), "abits": 15,
+            "weights_GB_per_step": round(wbytes / 1e9, 3), "GBps": round(wbytes / ms / 1e6, 1),
+            "frac_hbm": round(wbytes / ms / 1e6 / HBM_PEAK_GBPS, 4), "prompt": prompt_len,
+            "prefill_ms_per_sequence": round(prefill_ms, 3)}
+
+
+def attention_prefill(args, S=2048, H=28, KV=4, hd=128):
+    """Exact integer causal attention of one 2048-token prefill layer (28 q / 4 kv heads, hd 128) from the
+    KV cache: algorithmic ops 2*(S(S+1)/2)*hd*H for q.k and the same for p.v."""
+    import torch
+    from exact_amd import ops
+    from exact_amd.tables import DeviceTables
+    dev = "cuda"
+    tab = DeviceTables(dev, S, hd, 1e6)
+    g = torch.Generator(device="cpu").manual_seed(3)
+    kq = torch.randint(-32767, 32768, (1, KV, S, hd), generator=g, dtype=torch.int16).to(dev)
+    sk = torch.randint(0, 16, (1, KV, S), generator=g, dtype=torch.int32).to(dev)
+    v = torch.randint(-(1 << 30), 1 << 30, (1, KV, S, hd), generator=g, dtype=torch.int64).to(dev)
+    qq = torch.randint(-32767, 32768, (S, H, hd), generator=g, dtype=torch.int16).to(dev)
+    sq = torch.randint(0, 16, (S, H), generator=g, dtype=torch.int32).to(dev)
+    slot = torch.zeros(S, dtype=torch.int32, device=dev)
+    pos = torch.arange(S, dtype=torch.int32, device=dev)
+    out = torch.empty((S, H * hd), dtype=torch.int64, device=dev)
+    ops.attention(qq, sq, (kq, sk, v), slot, pos, tab.exp, out, H, KV, hd, tab.inv)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 3
+    a.record(st)
+    for _ in range(reps):
+        ops.attention(qq, sq, (kq, sk, v), slot, pos, tab.exp, out, H, KV, hd, tab.inv)
+    b.record(st)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1000.0 / reps
+    ops_ = 2 * 2 * (S * (S + 1) // 2) * hd * H
+    del kq, sk, v, qq, out
+    torch.cuda.empty_cache()
+    return {"S": S, "H": H, "KV": KV, "hd": hd, "us": round(us, 1), "G_ops": round(ops_ / 1e9, 2),
+            "TOPS": round(ops_ / us / 1e6, 3)}
 
 
 def prefill_gemm(args):
@@ -234,6 +299,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-model", action="store_true")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the GEMV pass (profiling runs of the other parts)")
+    ap.add_argument("--models", default="7b,c1,c4,c4b8,c5", help="model decode runs: 7b, c1, c4, c4b8, c5")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also copy 512 MiB on the device three times (calibrates the HBM traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs the exact path on a single MI355X; "
@@ -245,10 +314,29 @@ def main():
         sys.exit(1)
     import exact_amd
     exact_amd.load()
-    r = gemv_pass(args)
+    if args.copy_probe:
+        src = torch.randint(0, 100, (512 << 20,), dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    r = None if args.no_gemv else gemv_pass(args)
     pre = {} if args.no_prefill else prefill_gemm(args)
-    mdl = None if args.no_model else model_decode(args)
+    mdl, models = None, None
+    if not args.no_model:
+        want = set(args.models.split(","))
+        mdl = model_decode(args) if "7b" in want else None
+        runs = {"C1_qwen2.5-0.5b_bs1": ("c1", "qwen2.5-0.5b", 16, 1), "C4_qwen2.5-14b_bs1": ("c4", "qwen2.5-14b", 128, 1),
+                "C4_qwen2.5-14b_bs8": ("c4b8", "qwen2.5-14b", 128, 8),
+                "C5_qwen1.5-moe-a2.7b_bs1": ("c5", "qwen1.5-moe-a2.7b", 256, 1)}
+        models = {k: model_decode(args, n, p, B=b) for k, (tag, n, p, b) in runs.items() if tag in want}
+    att = None if args.no_prefill else attention_prefill(args)
     cpu = None if args.no_cpu else cpu_baseline()
+    if r is None:
+        print(json.dumps({"metric": METRIC, "value": None, "model_decode": mdl, "model_configs": models,
+                          "prefill_gemm": pre, "attention_prefill": att}), flush=True)
+        return
     tok_s = 1000.0 / r["ms"]
     pass_gbps = r["pass_bytes"] / (r["ms"] * 1e-3) / 1e9
     dom = r["per"]["gateup"]
@@ -263,11 +351,14 @@ def main():
         "gemv_GBps": round(pass_gbps, 1),
         "gemv_per_shape": r["per"],
         "model_decode": mdl,
+        "model_configs": models,
         "prefill_gemm": pre,
+        "attention_prefill": att,
         "prefill_TOPS": (round(min(v["TOPS"] for v in pre.values()), 2) if pre else None),
         "roofline": {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(dom["GBps"] / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "k_gemv_g128<7> on gate|up 37888x3584 (136 MB per launch)"},
+                     "frac": round(dom["GBps"] / HBM_PEAK_GBPS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
+                     "algorithmic_bytes": GATEUP_BYTES,
+                     "kernel": "k_gemv_g128<7,true,1> on gate|up 37888x3584, bs1 A8"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -71,18 +71,21 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
   }
 }
 
-// grid (R, H), block 256. Scores in LDS (Smax entries), then max, exp LUT, sum, Q20 p, and p.V.
-__global__ __launch_bounds__(256) void k_attention(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
-                                                   const int16_t* __restrict__ kq, const int32_t* __restrict__ sk,
-                                                   const int64_t* __restrict__ v, const int32_t* __restrict__ slot,
-                                                   const int32_t* __restrict__ pos, const int32_t* __restrict__ expt,
-                                                   int64_t* __restrict__ out, int32_t* __restrict__ obits, int H, int KV,
-                                                   int hd, int Smax, int INV) {
+// grid (R, H), block ATT_THREADS. Scores in LDS (Smax entries), then max, exp LUT, sum, Q20 p, and p.V:
+// thread t owns the dimension pair 2 (t % (hd/2)) and every (ATT_THREADS / (hd/2))-th key, with 16-byte
+// V loads, eight in flight.
+#define ATT_THREADS 512
+__global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
+                                                           const int16_t* __restrict__ kq, const int32_t* __restrict__ sk,
+                                                           const int64_t* __restrict__ v, const int32_t* __restrict__ slot,
+                                                           const int32_t* __restrict__ pos, const int32_t* __restrict__ expt,
+                                                           int64_t* __restrict__ out, int32_t* __restrict__ obits, int H,
+                                                           int KV, int hd, int Smax, int INV) {
   extern __shared__ int64_t sc[];   // Smax entries
   __shared__ int32_t qs[256];
-  __shared__ int ored[4];
+  __shared__ int ored[ATT_THREADS / 64];
   __shared__ int64_t red[16];
-  __shared__ int64_t part[256];
+  __shared__ int64_t part[ATT_THREADS * 2];
   const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const int kh = h / (H / KV);
   const int S = min(pos[r] + 1, Smax), sl = slot[r];
@@ -118,23 +121,29 @@ __global__ __launch_bounds__(256) void k_attention(const int16_t* __restrict__ q
   es = block_sum64(es, red);
   for (int si = tid; si < S; si += blockDim.x) sc[si] = floordiv_pos(shl64(sc[si], 20), es);
   __syncthreads();
-  // p.V: thread (j, part) sums keys si = part, part + nparts, ...
-  const int nparts = blockDim.x / hd;   // hd divides 256
-  const int j = tid % hd, pp = tid / hd;
-  int64_t a = 0;
+  const int npair = hd >> 1, nparts = blockDim.x / npair;   // hd divides 2 * ATT_THREADS
+  const int dp = tid % npair, pp = tid / npair;
+  int64_t a0 = 0, a1 = 0;
   if (pp < nparts) {
-    const int64_t* vb = v + cbase * hd + j;
-#pragma unroll 4
-    for (int si = pp; si < S; si += nparts) a = (int64_t)((uint64_t)a + (uint64_t)(sc[si] * vb[(int64_t)si * hd]));
+    const int64_t* vb = v + cbase * hd + 2 * dp;
+#pragma unroll 8
+    for (int si = pp; si < S; si += nparts) {
+      const v4i vv = *reinterpret_cast<const v4i*>(vb + (int64_t)si * hd);
+      const int64_t p = sc[si];
+      a0 = (int64_t)((uint64_t)a0 + (uint64_t)(p * (((int64_t)vv[1] << 32) | (uint32_t)vv[0])));
+      a1 = (int64_t)((uint64_t)a1 + (uint64_t)(p * (((int64_t)vv[3] << 32) | (uint32_t)vv[2])));
+    }
   }
-  part[tid] = a;
+  part[2 * tid] = a0;
+  part[2 * tid + 1] = a1;
   __syncthreads();
   int m = 0;
   if (tid < hd) {
+    const int d = tid;   // dimension d sits in pair d / 2, half d % 2
     uint64_t tot = 0;
-    for (int k = 0; k < nparts; ++k) tot += (uint64_t)part[k * hd + tid];
+    for (int k = 0; k < nparts; ++k) tot += (uint64_t)part[2 * (k * npair + (d >> 1)) + (d & 1)];
     const int64_t o = shr64((int64_t)tot, 20);
-    out[((int64_t)r * H + h) * hd + tid] = o;
+    out[((int64_t)r * H + h) * hd + d] = o;
     m = bitlen64(abs64(o));
   }
   if (obits) {   // bit length of this head's max |out|, for the row quantisation of the o-projection input
@@ -165,8 +174,9 @@ extern "C" int exact_attention(const int16_t* qq, const int32_t* sq, const int16
                                int32_t INV, void* stream) {
   if (!qq || !sq || !kq || !sk || !v || !slot || !pos || !exp_t || !out) return EXACT_E_ARG;
   if (R <= 0 || H <= 0 || KV <= 0 || H % KV || hd <= 0 || Smax <= 0) return EXACT_E_ARG;
-  if (hd > 256 || 256 % hd || hd % 8 || Smax > 8192) return EXACT_E_UNSUPPORTED;
-  hipLaunchKernelGGL(k_attention, dim3(R, H), dim3(256), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot, pos,
+  if (hd > 256 || (2 * ATT_THREADS) % hd || hd % 8 || Smax > 8192) return EXACT_E_UNSUPPORTED;
+  hipLaunchKernelGGL(k_attention, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot,
+                     pos,
                      exp_t, out, obits, H, KV, hd, Smax, INV);
   return launch_status("attention");
 }

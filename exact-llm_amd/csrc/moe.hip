@@ -13,15 +13,22 @@
 
 namespace exact {
 
-// One block per row. The probabilities stay in LDS for the rank computation: expert i has rank
-// #{j : p_j > p_i or (p_j == p_i and j < i)}, which is its position in a stable sort of -p.
-__global__ void k_router_topk(int64_t* __restrict__ t, const int32_t* __restrict__ s, const int32_t* __restrict__ T,
-                              int64_t* __restrict__ p_sel, int32_t* __restrict__ e_sel, int NE, int k, int clear_t) {
+// One block per row of t (row stride ld). The probabilities stay in LDS for the rank computation:
+// expert i has rank #{j : p_j > p_i or (p_j == p_i and j < i)}, its position in a stable sort of -p.
+// With gate_col >= 0 the same row also holds the shared expert's gate logit (the router and the gate
+// linear share one GEMV): gate[r] = isig(shr(t[r][gate_col], 28 - s)).
+__global__ void k_router_topk(int64_t* __restrict__ t, int ld, const int32_t* __restrict__ s, const int32_t* __restrict__ T,
+                              int64_t* __restrict__ p_sel, int32_t* __restrict__ e_sel, int gate_col,
+                              const int32_t* __restrict__ sig_t, int64_t* __restrict__ gate, int NE, int k, int clear_t) {
   extern __shared__ int64_t sp[];
   __shared__ int64_t red[16];
   const int r = blockIdx.x;
   const int sh = 28 - s[r];
-  int64_t* tr = t + (int64_t)r * NE;
+  int64_t* tr = t + (int64_t)r * ld;
+  if (gate_col >= 0 && threadIdx.x == 0) {
+    gate[r] = lut16(sig_t, shr64(tr[gate_col], sh), true);
+    if (clear_t) tr[gate_col] = 0;
+  }
   int64_t mx = INT64_MIN;
   for (int i = threadIdx.x; i < NE; i += blockDim.x) {
     const int64_t y = shr64(tr[i], sh);
@@ -98,47 +105,43 @@ __global__ void k_moe_dispatch(const int32_t* __restrict__ e_sel, const int32_t*
   }
 }
 
-// One block per row: x += sum_j shr(p_j * shr(t_ed[pair], 28 - sh_pair), 20)
-//                        + shr(isig(shr(t_sg, 28 - s)) * shr(t_sd, 28 - sh_s), 16)
-__global__ void k_moe_combine(int64_t* __restrict__ x, int64_t* __restrict__ t_ed, const int32_t* __restrict__ sh_pair,
-                              const int64_t* __restrict__ p_sel, const int32_t* __restrict__ pidx, int64_t* __restrict__ t_sd,
-                              const int32_t* __restrict__ sh_s, int64_t* __restrict__ t_sg, const int32_t* __restrict__ s,
-                              const int32_t* __restrict__ sig_t, int D, int k, int clear_t) {
-  const int r = blockIdx.x;
-  int64_t gate = 0;
-  if (t_sd) gate = lut16(sig_t, shr64(t_sg[r], 28 - s[r]), true);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    int64_t acc = 0;
-    for (int j = 0; j < k; ++j) {
-      const int q = pidx[r * k + j];
-      int64_t* te = t_ed + (int64_t)q * D + d;
-      const int64_t y = shr64(*te, 28 - sh_pair[q]);
-      if (clear_t) *te = 0;
-      acc += shr64(p_sel[r * k + j] * y, 20);
-    }
-    if (t_sd) {
-      int64_t* ts = t_sd + (int64_t)r * D + d;
-      acc += shr64(gate * shr64(*ts, 28 - sh_s[r]), 16);
-      if (clear_t) *ts = 0;
-    }
-    x[(int64_t)r * D + d] += acc;
+// grid (ceil(D / 256), R), one element per thread: x += sum_j shr(p_j * shr(t_ed[pair], 28 - sh_pair), 20)
+//                                                     + shr(gate * shr(t_sd, 28 - sh_s), 16)
+__global__ __launch_bounds__(256) void k_moe_combine(int64_t* __restrict__ x, int64_t* __restrict__ t_ed,
+                                                     const int32_t* __restrict__ sh_pair, const int64_t* __restrict__ p_sel,
+                                                     const int32_t* __restrict__ pidx, int64_t* __restrict__ t_sd,
+                                                     const int32_t* __restrict__ sh_s, const int64_t* __restrict__ gate, int D,
+                                                     int k, int clear_t) {
+  const int r = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x;
+  if (d >= D) return;
+  int64_t acc = 0;
+  for (int j = 0; j < k; ++j) {
+    const int q = pidx[r * k + j];
+    int64_t* te = t_ed + (int64_t)q * D + d;
+    const int64_t y = shr64(*te, 28 - sh_pair[q]);
+    if (clear_t) *te = 0;
+    acc += shr64(p_sel[r * k + j] * y, 20);
   }
-  if (t_sd && clear_t) {
-    __syncthreads();   // every thread has read the gate logit
-    if (threadIdx.x == 0) t_sg[r] = 0;
+  if (t_sd) {
+    int64_t* ts = t_sd + (int64_t)r * D + d;
+    acc += shr64(gate[r] * shr64(*ts, 28 - sh_s[r]), 16);
+    if (clear_t) *ts = 0;
   }
+  x[(int64_t)r * D + d] += acc;
 }
 
 }  // namespace exact
 
 using namespace exact;
 
-extern "C" int exact_router_topk(int64_t* t, const int32_t* s, const int32_t* exp_t, int64_t* p_sel, int32_t* e_sel,
-                                 int32_t R, int32_t NE, int32_t k, int32_t clear_t, void* stream) {
-  if (!t || !s || !exp_t || !p_sel || !e_sel || R <= 0 || NE <= 0 || k <= 0 || k > NE) return EXACT_E_ARG;
+extern "C" int exact_router_topk(int64_t* t, int32_t ld, const int32_t* s, const int32_t* exp_t, int64_t* p_sel,
+                                 int32_t* e_sel, int32_t gate_col, const int32_t* sig_t, int64_t* gate, int32_t R, int32_t NE,
+                                 int32_t k, int32_t clear_t, void* stream) {
+  if (!t || !s || !exp_t || !p_sel || !e_sel || R <= 0 || NE <= 0 || k <= 0 || k > NE || ld < NE) return EXACT_E_ARG;
+  if (gate_col >= 0 && (gate_col >= ld || (gate_col < NE) || !sig_t || !gate)) return EXACT_E_ARG;
   if (NE > 4096) return EXACT_E_UNSUPPORTED;
-  hipLaunchKernelGGL(k_router_topk, dim3(R), dim3(256), NE * sizeof(int64_t), as_stream(stream), t, s, exp_t, p_sel, e_sel,
-                     NE, k, clear_t);
+  hipLaunchKernelGGL(k_router_topk, dim3(R), dim3(256), NE * sizeof(int64_t), as_stream(stream), t, ld, s, exp_t, p_sel, e_sel,
+                     gate_col, sig_t, gate, NE, k, clear_t);
   return launch_status("router_topk");
 }
 
@@ -155,11 +158,11 @@ extern "C" int exact_moe_dispatch(const int32_t* e_sel, const int32_t* s, int32_
 }
 
 extern "C" int exact_moe_combine(int64_t* x, int64_t* t_ed, const int32_t* sh_pair, const int64_t* p_sel, const int32_t* pidx,
-                                 int64_t* t_sd, const int32_t* sh_s, int64_t* t_sg, const int32_t* s, const int32_t* sig_t,
-                                 int32_t R, int32_t D, int32_t k, int32_t clear_t, void* stream) {
+                                 int64_t* t_sd, const int32_t* sh_s, const int64_t* gate, int32_t R, int32_t D, int32_t k,
+                                 int32_t clear_t, void* stream) {
   if (!x || !t_ed || !sh_pair || !p_sel || !pidx || R <= 0 || D <= 0 || k <= 0) return EXACT_E_ARG;
-  if (t_sd && (!sh_s || !t_sg || !s || !sig_t)) return EXACT_E_ARG;
-  hipLaunchKernelGGL(k_moe_combine, dim3(R), dim3(256), 0, as_stream(stream), x, t_ed, sh_pair, p_sel, pidx, t_sd, sh_s,
-                     t_sg, s, sig_t, D, k, clear_t);
+  if (t_sd && (!sh_s || !gate)) return EXACT_E_ARG;
+  hipLaunchKernelGGL(k_moe_combine, dim3((D + 255) / 256, R), dim3(256), 0, as_stream(stream), x, t_ed, sh_pair, p_sel, pidx,
+                     t_sd, sh_s, gate, D, k, clear_t);
   return launch_status("moe_combine");
 }

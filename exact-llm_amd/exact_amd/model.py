@@ -35,20 +35,27 @@ class DeviceWeights:
     def synthetic(cls, cfg, seed, device, layers=None):
         self = cls(cfg, device)
         thr = torch.tensor(synth.thresholds().astype(np.int64), dtype=I64).to(torch.int32).to(device)
+        if any(n % 64 for n in ((cfg.MI, cfg.SI) if cfg.moe else (cfg.I,))):
+            raise ExactError("fused gate|up linears need intermediate sizes that are multiples of 64")
         D, H, KV, hd = cfg.D, cfg.H, cfg.KV, cfg.hd
         nl = cfg.NL if layers is None else layers
 
         def fused(parts, K, bias):
-            N = sum(n for _, n in parts)
+            # each part starts on a 64-row boundary of the packed buffer (and of the output row)
+            offs, N = [], 0
+            for _, n in parts:
+                offs.append(N)
+                N = offs[-1] + n if len(offs) == len(parts) else -(-(offs[-1] + n) // 64) * 64
             wp, mp = PackedLinear.alloc(N, K, device)
-            off, bs = 0, []
-            for name, n in parts:
+            bs = []
+            for (name, n), off in zip(parts, offs):
                 kw, km, kb = _lin_keys(seed, name)
                 ops.synth_linear(wp, mp, n, K, kw, km, synth.M_LO, synth.M_HI, thr, n_off=off, Ntot=N)
                 if bias:
                     bs.append(ops.synth_vector(kb, synth.BIAS[0], synth.BIAS[1], n, device))
-                off += n
             b = torch.cat(bs) if bias else None
+            if bias and N != sum(n for _, n in parts):
+                raise ExactError("biased fused linears need 64-row aligned parts")
             return PackedLinear(wp, mp, N, K, b)
 
         for li in range(nl):
@@ -58,7 +65,8 @@ class DeviceWeights:
                 qkv=fused([(f"L{li}.q", H * hd), (f"L{li}.k", KV * hd), (f"L{li}.v", KV * hd)], D, True),
                 o=fused([(f"L{li}.o", D)], H * hd, False))
             if cfg.moe:
-                L["router"] = fused([(f"L{li}.router", cfg.NE)], D, False)
+                # router logits and the shared expert's gate logit in one GEMV (gate at column gate_col)
+                L["router"] = fused([(f"L{li}.router", cfg.NE), (f"L{li}.sgate", 1)], D, False)
                 # experts: gate|up (2 MI x D) and down (D x MI) of all NE experts, each in one allocation
                 egu = ops.ExpertLinears(cfg.NE, 2 * cfg.MI, D, device)
                 edn = ops.ExpertLinears(cfg.NE, D, cfg.MI, device)
@@ -74,7 +82,6 @@ class DeviceWeights:
                 L["egu"], L["edown"] = egu, edn
                 L["sgu"] = fused([(f"L{li}.sg", cfg.SI), (f"L{li}.su", cfg.SI)], D, False)
                 L["sd"] = fused([(f"L{li}.sd", D)], cfg.SI, False)
-                L["sgate"] = fused([(f"L{li}.sgate", 1)], D, False)
             else:
                 L["gateup"] = fused([(f"L{li}.gate", cfg.I), (f"L{li}.up", cfg.I)], D, False)
                 L["down"] = fused([(f"L{li}.down", D)], cfg.I, False)
@@ -158,13 +165,15 @@ class Workspace:
         if cfg.moe:
             k, P = cfg.topk, R * cfg.topk
             nch = ops.max_chunks(P, cfg.NE, abits)
-            self.t_rt, self.p_sel, self.e_sel = z(R, cfg.NE), z(R, k), z(R, k, dt=I32)
+            self.gate_col = -(-cfg.NE // 64) * 64
+            self.t_rt, self.p_sel, self.e_sel = z(R, self.gate_col + 1), z(R, k), z(R, k, dt=I32)
+            self.gate = z(R)
             self.disp = dict(pidx=z(P, dt=I32), pair_row=z(P, dt=I32), s_pair=z(P, dt=I32), chunk_e=z(nch, dt=I32),
                              chunk_p0=z(nch, dt=I32), chunk_n=z(nch, dt=I32), nchunks=z(1, dt=I32))
             self.t_egu, self.ehq, self.esh = z(P, 2 * cfg.MI), z(P, cfg.MI, dt=adt), z(P, dt=I32)
             self.t_ed = z(P, D)
             self.t_sgu, self.shq, self.ssh = z(R, 2 * cfg.SI), z(R, cfg.SI, dt=adt), z(R, dt=I32)
-            self.t_sd, self.t_sg = z(R, D), z(R, 1)
+            self.t_sd = z(R, D)
             self.part_esw = ops.swiglu_parts(P, cfg.MI, device)
 
 
@@ -269,11 +278,13 @@ class TModel:
 
     def _moe(self, ws, L):
         """MoE block on m = ws.xq (scale ws.s), added into ws.x (MoEInt.moe, moe_exact_kaggle.py:454-467):
-        router -> isoftmax -> stable top-k -> experts grouped into chunks -> SwiGLU per (row, expert) pair ->
-        combination weighted by the Q20 probabilities, plus the isig-gated shared expert."""
+        router (with the shared-expert gate logit in the same GEMV) -> isoftmax -> stable top-k -> experts grouped
+        into chunks -> SwiGLU per (row, expert) pair -> combination weighted by the Q20 probabilities, plus the
+        isig-gated shared expert."""
         c, tab, k = self.cfg, self.tab, self.cfg.topk
         self._lin(ws.xq, L["router"], ws.t_rt)
-        ops.router_topk(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, clear=True)
+        ops.router_topk(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, clear=True, NE=c.NE, gate_col=ws.gate_col,
+                        sig=tab.sig, gate=ws.gate)
         ops.moe_dispatch(ws.e_sel, ws.s, c.NE, k, ops.chunk_rows(self.abits), ws.disp)
         ops.gemv_experts(ws.xq, self.abits, ws.disp["pair_row"], L["egu"], ws.disp, ws.t_egu)
         ops.swiglu_qrow(ws.t_egu, ws.disp["s_pair"], tab.silu, self.abits, ws.ehq, ws.esh, clear=True, part=ws.part_esw)
@@ -281,9 +292,7 @@ class TModel:
         self._lin(ws.xq, L["sgu"], ws.t_sgu)
         ops.swiglu_qrow(ws.t_sgu, ws.s, tab.silu, self.abits, ws.shq, ws.ssh, clear=True, part=ws.part_sw)
         self._lin(ws.shq, L["sd"], ws.t_sd)
-        self._lin(ws.xq, L["sgate"], ws.t_sg)
-        ops.moe_combine(ws.x, ws.t_ed, ws.esh, ws.p_sel, ws.disp["pidx"], k, ws.t_sd, ws.ssh, ws.t_sg, ws.s, tab.sig,
-                        clear=True)
+        ops.moe_combine(ws.x, ws.t_ed, ws.esh, ws.p_sel, ws.disp["pidx"], k, ws.t_sd, ws.ssh, ws.gate, clear=True)
 
     # ---------------------------------------------------------------- reference-shaped API
     def forward(self, ids, cache=None, last_only=False, slot=0):

@@ -289,11 +289,13 @@ def max_chunks(P, NE, abits):
     return min(P, -(-P // chunk_rows(abits)) + NE)
 
 
-def router_topk(t, s, expt, k, p_sel, e_sel, clear=False):
-    R, NE = t.shape
-    _lib.call("exact_router_topk", _ptr(_need(t, I64, "t")), _ptr(_need(s, I32, "s", R)), _ptr(expt),
-              _ptr(_need(p_sel, I64, "p_sel", R * k)), _ptr(_need(e_sel, I32, "e_sel", R * k)), R, NE, k, int(clear),
-              _stream())
+def router_topk(t, s, expt, k, p_sel, e_sel, clear=False, NE=None, gate_col=-1, sig=None, gate=None):
+    """Top-k of isoftmax(rs(t[:, :NE], 28 - s)); with gate_col >= 0 also gate = isig(rs(t[:, gate_col], 28 - s))."""
+    R, ld = t.shape
+    NE = ld if NE is None else NE
+    _lib.call("exact_router_topk", _ptr(_need(t, I64, "t")), ld, _ptr(_need(s, I32, "s", R)), _ptr(expt),
+              _ptr(_need(p_sel, I64, "p_sel", R * k)), _ptr(_need(e_sel, I32, "e_sel", R * k)), gate_col, _ptr(sig),
+              _ptr(gate), R, NE, k, int(clear), _stream())
     return p_sel, e_sel
 
 
@@ -318,10 +320,10 @@ def gemv_experts(x, abits, row_map, lin, disp, out):
     return out
 
 
-def moe_combine(x, t_ed, sh_pair, p_sel, pidx, k, t_sd=None, sh_s=None, t_sg=None, s=None, sig=None, clear=False):
+def moe_combine(x, t_ed, sh_pair, p_sel, pidx, k, t_sd=None, sh_s=None, gate=None, clear=False):
     R, D = x.shape
     _lib.call("exact_moe_combine", _ptr(_need(x, I64, "x")), _ptr(_need(t_ed, I64, "t_ed")), _ptr(sh_pair), _ptr(p_sel),
-              _ptr(pidx), _ptr(t_sd), _ptr(sh_s), _ptr(t_sg), _ptr(s), _ptr(sig), R, D, k, int(clear), _stream())
+              _ptr(pidx), _ptr(t_sd), _ptr(sh_s), _ptr(gate), R, D, k, int(clear), _stream())
     return x
 
 

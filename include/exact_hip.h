@@ -145,11 +145,14 @@ int exact_attention(const int16_t* qq, const int32_t* sq, const int16_t* kq, con
                     int32_t INV, void* stream);
 
 /* ---- mixture of experts (MoEInt.moe, moe_exact_kaggle.py:454-467) ------------------------------------
- * Router: logits = rs(t, 28 - s[r]) (t (R, NE) from the router linear); p = isoftmax over all NE experts
- * (Q20); the k experts with the largest p, ties to the lower index (np.argsort(-p, kind="stable")[:k],
- * moe_exact_kaggle.py:457). Writes p_sel, e_sel (R, k) in rank order; clear_t != 0 leaves t zeroed. */
-int exact_router_topk(int64_t* t, const int32_t* s, const int32_t* exp_t, int64_t* p_sel, int32_t* e_sel,
-                      int32_t R, int32_t NE, int32_t k, int32_t clear_t, void* stream);
+ * Router: logits = rs(t[r][0..NE), 28 - s[r]) (t rows ld apart, from the router linear); p = isoftmax over all
+ * NE experts (Q20); the k experts with the largest p, ties to the lower index (np.argsort(-p,
+ * kind="stable")[:k], moe_exact_kaggle.py:457). Writes p_sel, e_sel (R, k) in rank order. With gate_col >= 0
+ * the row also carries the shared expert's gate logit (router and gate linear fused in one GEMV):
+ * gate[r] = isig(rs(t[r][gate_col], 28 - s[r])) (moe_exact_kaggle.py:465-467). clear_t != 0 leaves t zeroed. */
+int exact_router_topk(int64_t* t, int32_t ld, const int32_t* s, const int32_t* exp_t, int64_t* p_sel, int32_t* e_sel,
+                      int32_t gate_col, const int32_t* sig_t, int64_t* gate, int32_t R, int32_t NE, int32_t k,
+                      int32_t clear_t, void* stream);
 
 /* Dispatch: the P = R*k pairs q = r*k + j grouped by expert (row order inside an expert), replacing the
  * per-expert Python loop `rows = nonzero(sel == e)` (moe_exact_kaggle.py:459-463). Outputs: pidx[q] = position
@@ -168,11 +171,11 @@ int exact_gemv_g128_experts(const void* x, int32_t abits, const int32_t* row_map
                             int32_t max_chunks, int64_t* t, int32_t N, int32_t K, void* stream);
 
 /* Combination (moe_exact_kaggle.py:463-467): x[r] += sum_j rs(p_sel[r][j] * rs(t_ed[pidx[r*k+j]], 28 - sh_pair), 20)
- *   + rs(isig(rs(t_sg[r], 28 - s[r])) * rs(t_sd[r], 28 - sh_s[r]), 16)   (shared expert; skipped if t_sd is NULL).
- * clear_t != 0 leaves t_ed, t_sd and t_sg zeroed. */
+ *   + rs(gate[r] * rs(t_sd[r], 28 - sh_s[r]), 16)   (shared expert; skipped if t_sd is NULL).
+ * clear_t != 0 leaves t_ed and t_sd zeroed. */
 int exact_moe_combine(int64_t* x, int64_t* t_ed, const int32_t* sh_pair, const int64_t* p_sel, const int32_t* pidx,
-                      int64_t* t_sd, const int32_t* sh_s, int64_t* t_sg, const int32_t* s, const int32_t* sig_t,
-                      int32_t R, int32_t D, int32_t k, int32_t clear_t, void* stream);
+                      int64_t* t_sd, const int32_t* sh_s, const int64_t* gate, int32_t R, int32_t D, int32_t k,
+                      int32_t clear_t, void* stream);
 
 /* ---- model plumbing ------------------------------------------------------------------------------ */
 /* x[r] = emb[ids[r]] from an int32 Q16 table (V, D) (exact_llm.py:163; GraphDecoder.step :641). */

@@ -39,14 +39,21 @@ def test_router_topk_matches_oracle(tab, R, NE, k):
     if R > 2:
         t[2] = t[2, 0]                                   # an all-equal row
     s = rng.integers(0, 20, R)
-    td = dev(t, I64)
+    # the router row as the fused router|gate GEMV leaves it: NE logits, padding, the gate logit at a 64 boundary
+    gcol = -(-NE // 64) * 64
+    tg = rng.integers(-(1 << 44), 1 << 44, R)
+    tfull = np.zeros((R, gcol + 1), np.int64)
+    tfull[:, :NE], tfull[:, gcol] = t, tg
+    td = dev(tfull, I64)
     p_sel, e_sel = torch.zeros((R, k), dtype=I64, device=DEV), torch.zeros((R, k), dtype=I32, device=DEV)
-    ops.router_topk(td, dev(s, I32), tab.exp, k, p_sel, e_sel, clear=True)
+    gate = torch.zeros(R, dtype=I64, device=DEV)
+    ops.router_topk(td, dev(s, I32), tab.exp, k, p_sel, e_sel, clear=True, NE=NE, gate_col=gcol, sig=tab.sig, gate=gate)
     lg = O.round_shift(t, (28 - s)[:, None])
     p = O.isoftmax(lg, np.ones_like(lg, bool))
     sel = np.argsort(-p, axis=-1, kind="stable")[:, :k]
     assert np.array_equal(host(e_sel), sel)
     assert np.array_equal(host(p_sel), np.take_along_axis(p, sel, -1))
+    assert np.array_equal(host(gate), O.isig(O.round_shift(tg, 28 - s)))
     assert not host(td).any()                            # cleared for the next accumulating GEMV
 
 
@@ -124,21 +131,19 @@ def test_combine_matches_oracle(tab):
     p_sel = rng.integers(0, 1 << 20, (R, k))
     t_sd = rng.integers(-(1 << 44), 1 << 44, (R, D))
     sh_s = rng.integers(0, 26, R)
-    t_sg = rng.integers(-(1 << 46), 1 << 46, (R, 1))
-    s = rng.integers(0, 24, R)
+    gate = O.isig(rng.integers(-(20 << 16), 20 << 16, R))          # isig outputs in [0, 2^16]
     xd = dev(x, I64)
     args = [dev(a, dt) for a, dt in ((t_ed, I64), (sh_pair, I32), (p_sel, I64), (pidx, I32), (t_sd, I64), (sh_s, I32),
-                                     (t_sg, I64), (s, I32))]
-    ops.moe_combine(xd, args[0], args[1], args[2], args[3], k, args[4], args[5], args[6], args[7], tab.sig, clear=True)
+                                     (gate, I64))]
+    ops.moe_combine(xd, args[0], args[1], args[2], args[3], k, args[4], args[5], args[6], clear=True)
     want = x.copy()
     for r in range(R):
         for j in range(k):
             q = pidx[r * k + j]
             want[r] += O.round_shift(p_sel[r, j] * O.round_shift(t_ed[q], 28 - sh_pair[q]), 20)
-        gate = O.isig(O.round_shift(t_sg[r, 0], 28 - s[r]))
-        want[r] += O.round_shift(gate * O.round_shift(t_sd[r], 28 - sh_s[r]), 16)
+        want[r] += O.round_shift(gate[r] * O.round_shift(t_sd[r], 28 - sh_s[r]), 16)
     assert np.array_equal(host(xd), want)
-    assert not host(args[0]).any() and not host(args[4]).any() and not host(args[6]).any()
+    assert not host(args[0]).any() and not host(args[4]).any()
 
 
 @pytest.mark.parametrize("abits", [15, 7])
