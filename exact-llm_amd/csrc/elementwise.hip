@@ -201,6 +201,52 @@ __global__ __launch_bounds__(256) void k_swiglu_part(int64_t* __restrict__ t, co
   if (threadIdx.x == 0) part[(int64_t)r * nparts + b] = m;
 }
 
+// One workgroup (1024 threads) per row with EPT gate/up pairs per thread in registers: all loads of the
+// row are issued before the first use, one block reduction gives the row's shift, and the quantised
+// row is stored directly (rows longer than 8192 use the multi-block pair below, which is faster there).
+template <int EPT>
+__global__ __launch_bounds__(1024) void k_swiglu_qrow_row(int64_t* __restrict__ t, const int32_t* __restrict__ s,
+                                                          const int32_t* __restrict__ silu, int bits, void* xq,
+                                                          int32_t* __restrict__ sq, int I, int clear_t) {
+  __shared__ int red[16];
+  const int r = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
+  int64_t* tr = t + (int64_t)r * 2 * I;
+  const int sh = 28 - s[r];
+  int64_t hv[EPT], uv[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tid + j * nt;
+    hv[j] = i < I ? tr[i] : 0;
+    uv[j] = i < I ? tr[I + i] : 0;
+  }
+  int m = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tid + j * nt;
+    if (i < I) {
+      hv[j] = shr64(lut16(silu, shr64(hv[j], sh), false) * shr64(uv[j], sh), EXACT_F);
+      if (clear_t) { tr[i] = 0; tr[I + i] = 0; }
+      const int bl = bitlen64(abs64(hv[j]));
+      m = bl > m ? bl : m;
+    }
+  }
+  m = block_max_i32(m, red);
+  int q = m - bits;
+  if (q < 0) q = 0;
+  const int64_t lim = (1LL << bits) - 1;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tid + j * nt;
+    if (i < I) {
+      int64_t v = shr64(hv[j], q);
+      v = v > lim ? lim : (v < -lim ? -lim : v);
+      if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * I + i, v);
+      else store_q<int16_t>(xq, (int64_t)r * I + i, v);
+    }
+  }
+  if (tid == 0) sq[r] = q;
+}
+
 // grid (slices, R): xq[r][i] = clip(shr(src[r * ld + i], s_r), +-(2^bits - 1)), s_r from the slice maxima
 __global__ __launch_bounds__(256) void k_quant_rows(int64_t* __restrict__ src, int64_t ld, const int32_t* __restrict__ part,
                                                     int nparts, int bits, void* xq, int32_t* __restrict__ s, int K,
@@ -406,8 +452,18 @@ extern "C" int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res
 extern "C" int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq, int32_t* sq,
                                  int32_t* part, int32_t R, int32_t I, int32_t clear_t, void* stream) {
   if (!t || !s || !silu_t || !xq || !sq || !part || R <= 0 || I <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
-  const int np = (I + QSLICE - 1) / QSLICE;
   hipStream_t st = as_stream(stream);
+  const int nt = I >= 1024 ? 1024 : ((I + 63) / 64) * 64;
+  const int ept = (I + nt - 1) / nt;
+#define SWG_GO(E) hipLaunchKernelGGL(k_swiglu_qrow_row<E>, dim3(R), dim3(nt), 0, st, t, s, silu_t, bits, xq, sq, I, clear_t)
+  if (ept <= 8) {   // rows up to 8192: one workgroup; longer rows go faster over many workgroups
+    if (ept <= 2) SWG_GO(2);
+    else if (ept <= 4) SWG_GO(4);
+    else SWG_GO(8);
+    return launch_status("swiglu_qrow");
+  }
+#undef SWG_GO
+  const int np = (I + QSLICE - 1) / QSLICE;
   hipLaunchKernelGGL(k_swiglu_part, dim3(np, R), dim3(256), 0, st, t, s, silu_t, part, I, np, clear_t);
   hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, t, (int64_t)2 * I, part, np, bits, xq, sq, I, clear_t);
   return launch_status("swiglu_qrow");

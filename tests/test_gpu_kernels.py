@@ -176,14 +176,17 @@ def test_quant_rows_from_partial_maxima():
     assert not host(xd)[:, :K].any() and np.array_equal(host(xd)[:, K:], x[:, K:])
 
 
-def test_swiglu_qrow():
+@pytest.mark.parametrize("R,I,bits", [(3, 4864, 15), (2, 18944, 15), (5, 1408, 7), (2, 24576, 15), (4, 100, 15)])
+def test_swiglu_qrow(R, I, bits):
+    """One-workgroup rows (I <= 20480) and the two-kernel slice path (longer rows); both leave t zeroed."""
     from exact_amd.tables import silu_t
-    R, I = 3, 4864
     t = rng.integers(-(1 << 44), 1 << 44, (R, 2 * I))
     s = rng.integers(10, 20, R).astype(np.int32)
     td = dev(t, I64)
-    hq, sh = ops.swiglu_qrow(td, dev(s, I32), dev(silu_t(), I32))
+    hq, sh = ops.swiglu_qrow(td, dev(s, I32), dev(silu_t(), I32), bits=bits, clear=True)
     g = O.round_shift(t[:, :I], 28 - s[:, None].astype(np.int64))
     u = O.round_shift(t[:, I:], 28 - s[:, None].astype(np.int64))
-    eq, es = O.qrow(O.round_shift(O.isilu(g) * u, 16), 15)
+    eq, es = O.qrow(O.round_shift(O.isilu(g) * u, 16), bits)
     assert np.array_equal(host(hq).astype(np.int64), eq) and np.array_equal(host(sh), es[:, 0])
+    assert not host(td).any()
+
