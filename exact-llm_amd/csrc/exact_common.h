@@ -65,6 +65,14 @@ __device__ __forceinline__ int64_t floordiv_pos(int64_t a, int64_t b) {
   return q;
 }
 
+// SplitMix64 output for counter idx + 1 (Steele, Lea and Flood 2014; exact_llm.py:243-247)
+__host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t key, uint64_t idx) {
+  uint64_t z = key + (idx + 1ULL) * 0x9E3779B97F4A7C15ULL;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  return z ^ (z >> 31);
+}
+
 __device__ __forceinline__ int64_t isqrt64(int64_t n) {
   if (n <= 0) return 0;
   int64_t r = (int64_t)__builtin_sqrt((double)n);

@@ -14,13 +14,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 namespace exact {
 
-__device__ __forceinline__ uint64_t splitmix64(uint64_t key, uint64_t idx) {
-  uint64_t z = key + (idx + 1ULL) * 0x9E3779B97F4A7C15ULL;
-  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
-  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
-  return z ^ (z >> 31);
-}
-
 // one thread per 16-byte (row, 16-k) chunk of the packed tile array
 __global__ void k_synth_w(uint64_t key, const uint32_t* __restrict__ thr, int8_t* __restrict__ wp, int N, int K, int G,
                           int64_t nchunks, int nb_off, int64_t nbs_tot) {

@@ -9,6 +9,8 @@ with the layer order of IntModel.__call__ (exact_llm.py:161-180):
 Every step runs in hand-written HIP kernels (libexact_hip.so); Python only allocates buffers and
 sequences launches on the current stream, so a whole decode step can be captured in a HIP graph.
 """
+import hashlib
+
 import numpy as np
 import torch
 
@@ -328,6 +330,56 @@ class TModel:
         for r in range(B):
             cache.n[r] += 1
         return ws.logits.clone(), ws.next_ids.clone()
+
+
+def step_hash(prev, lg_row):
+    """Chained per-step receipt hash: sha256 of the previous hash and the int64 logits row, first 16 hex
+    digits (exact_llm.py:260-261)."""
+    return hashlib.sha256(prev.encode() + np.ascontiguousarray(lg_row, np.int64).tobytes()).hexdigest()[:16]
+
+
+def generate(tm, prompt_ids, n, seed, temp):
+    """Sampled generation with a receipt (exact_llm.generate, exact_llm.py:262-268): the integer sampler runs on
+    the device; each step's logits row comes to the host only for the receipt hash. Uses the KV cache (the
+    reference re-runs the whole sequence per step; the logits are identical by causality).
+    Returns (receipt dict, greedy tokens)."""
+    tnum = ops.temp_num(temp)
+    cache = tm.new_cache(B=1)
+    dev = tm.dev
+    step = torch.zeros(1, dtype=I32, device=dev)
+    ids = torch.zeros(1, dtype=I32, device=dev)
+    chain, toks, greedy = "start", [], []
+    lg = tm.forward(list(prompt_ids), cache, last_only=True)
+    for t in range(n):
+        step.fill_(t)
+        ops.sample(lg, seed, step, tnum, tm.tab.exp, ids)
+        row = lg[0].cpu().numpy()
+        tok = int(ids.cpu()[0])
+        chain = step_hash(chain, row)
+        toks.append(tok)
+        greedy.append(int(row.argmax()))
+        if t + 1 < n:
+            lg, _ = tm.decode_rows([tok], cache)
+    return dict(prompt=list(prompt_ids), seed=seed, temp=temp, tokens=toks, chain=chain), greedy
+
+
+def verify(tm, receipt):
+    """Recompute a receipt (exact_llm.verify, exact_llm.py:269-276): (ok, first bad position, "chain" or None)."""
+    tnum = ops.temp_num(receipt["temp"])
+    cache = tm.new_cache(B=1)
+    step = torch.zeros(1, dtype=I32, device=tm.dev)
+    ids = torch.zeros(1, dtype=I32, device=tm.dev)
+    chain = "start"
+    lg = tm.forward(list(receipt["prompt"]), cache, last_only=True)
+    for t, rec in enumerate(receipt["tokens"]):
+        step.fill_(t)
+        ops.sample(lg, receipt["seed"], step, tnum, tm.tab.exp, ids)
+        chain = step_hash(chain, lg[0].cpu().numpy())
+        if int(ids.cpu()[0]) != rec:
+            return False, t
+        if t + 1 < len(receipt["tokens"]):
+            lg, _ = tm.decode_rows([rec], cache)
+    return chain == receipt["chain"], (None if chain == receipt["chain"] else "chain")
 
 
 class GraphDecoder:

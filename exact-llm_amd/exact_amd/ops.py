@@ -257,6 +257,19 @@ def logits_argmax(t, s, lg=None, ids=None, clear=False, part=None):
     return lg, ids
 
 
+def temp_num(temp):
+    """Temperature as the integer multiplier round(2^16 / temp) (exact_llm.py:249)."""
+    return int(round((1 << 16) / temp))
+
+
+def sample(lg, seed, step, tnum, expt, ids, p_out=None):
+    """ids[r] = sample_int(lg[r], seed, step[r], tnum) (exact_llm.py:256-259), on the device."""
+    R, V = lg.shape
+    _lib.call("exact_sample", _ptr(_need(lg, I64, "lg")), R, V, ctypes.c_uint64(seed), _ptr(_need(step, I32, "step", R)), tnum,
+              _ptr(expt), _ptr(_need(ids, I32, "ids", R)), _ptr(p_out), _stream())
+    return ids
+
+
 def advance(pos):
     _lib.call("exact_advance", _ptr(pos), pos.numel(), _stream())
 

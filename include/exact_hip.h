@@ -192,6 +192,13 @@ int exact_embed_table(const int8_t* wp, const int16_t* mp, int32_t* emb, int32_t
 int exact_logits_argmax(int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int64_t* part, int32_t R,
                         int32_t N, int32_t clear_t, void* stream);
 
+/* Integer sampler (sample_int, exact_llm.py:256-259) for R logits rows lg (R, V):
+ * p = isoftmax_row(rs(lg * tnum, 16)) (Q20), target = (u20 * sum(p)) >> 20 with u20 = splitmix64(seed, step[r]) >> 44,
+ * ids[r] = searchsorted(cumsum(p), target, 'right'). tnum = round(2^16 / temperature) (exact_llm.py:249).
+ * p_out (optional, R * V) receives p. */
+int exact_sample(const int64_t* lg, int32_t R, int32_t V, uint64_t seed, const int32_t* step, int64_t tnum,
+                 const int32_t* exp_t, int32_t* ids, int64_t* p_out, void* stream);
+
 /* pos[r] += 1 for r < R (advances a decode step inside a captured graph; GraphDecoder.step :645). */
 int exact_advance(int32_t* pos, int32_t R, void* stream);
 
