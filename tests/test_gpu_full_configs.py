@@ -22,14 +22,15 @@ def host(t):
     return t.cpu().numpy()
 
 
-@pytest.mark.parametrize("name", ["c1", "c5", "c4"])
-def test_full_config_matches_oracle_fixture(name):
+@pytest.mark.parametrize("name,batch", [("c1", None), ("c5", None), ("c4", 1), ("c4", None)])
+def test_full_config_matches_oracle_fixture(name, batch):
+    """batch None: every fixture sequence decoded together (bs8 for c4); 1: the first sequence alone."""
     path = os.path.join(GOLD, f"full_{name}.json")
     if not os.path.exists(path):
         pytest.skip(f"{path} not written yet (tests/golden/make_full_configs.py {name})")
     spec = json.load(open(path))
     cfg = synth.CONFIGS[spec["config"]]
-    seqs = spec["sequences"]
+    seqs = spec["sequences"] if batch is None else spec["sequences"][:batch]
     B, n = len(seqs), spec["new_tokens"]
     print(f"{name}: {cfg.name} B={B} prompt={spec['prompt_len']} new={n}", flush=True)
     tm = TModel(DeviceWeights.synthetic(cfg, spec["seed"], DEV), Smax=spec["prompt_len"] + n, batch=B,
