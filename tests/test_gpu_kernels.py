@@ -70,6 +70,24 @@ def test_gemm_chunked_rows(thr, abits):
     assert np.array_equal(host(t), oracle_t(xq, synth.weights_np(kw, N, K), synth.scales_np(km, N, K)))
 
 
+@pytest.mark.parametrize("name,N,K", [("gateup", 18944, 3584), ("down", 3584, 18944)])
+def test_prefill_gemm_full_shapes(thr, name, N, K):
+    """The 2048-token prefill GEMMs at full size, A8 (the benchmark) and A16 (the spec): 40 whole output rows and
+    64 whole output columns against numpy (every row block, column block and K split is covered)."""
+    M_ = 2048
+    lin, kw, km = synth_lin(thr, 72, name, N, K)
+    w = synth.weights_np(kw, N, K)
+    Mg = synth.scales_np(km, N, K)
+    rows = np.sort(np.concatenate([[0, M_ - 1], rng.choice(M_, 38, replace=False)]))
+    cols = np.sort(np.concatenate([[0, N - 1], rng.choice(N, 62, replace=False)]))
+    for abits in (7, 15):
+        lim = (1 << abits) - 1
+        xq = rng.integers(-lim, lim + 1, (M_, K))
+        t = host(ops.gemm_g128(dev(xq, I16 if abits == 15 else I8), abits, lin))
+        assert np.array_equal(t[rows], oracle_t(xq[rows], w, Mg)), (name, abits, "rows")
+        assert np.array_equal(t[:, cols], oracle_t(xq, w[:, cols], Mg[:, cols])), (name, abits, "cols")
+
+
 @pytest.mark.parametrize("name,N,K", [("q", 3584, 3584), ("kv", 512, 3584), ("gate", 18944, 3584), ("down", 3584, 18944)])
 @pytest.mark.parametrize("R", [1, 8])
 def test_gemv_7b_shapes(thr, name, N, K, R):
