@@ -212,22 +212,31 @@ def attention_prefill(args, S=2048, H=28, KV=4, hd=128):
     slot = torch.zeros(S, dtype=torch.int32, device=dev)
     pos = torch.arange(S, dtype=torch.int32, device=dev)
     out = torch.empty((S, H * hd), dtype=torch.int64, device=dev)
-    ops.attention(qq, sq, (kq, sk, v), slot, pos, tab.exp, out, H, KV, hd, tab.inv)
-    torch.cuda.synchronize()
+    ref = torch.empty((S, H * hd), dtype=torch.int64, device=dev)
+    ws = ops.prefill_workspace(S, H, KV, hd, S, dev)
+    run_rows = lambda: ops.attention(qq, sq, (kq, sk, v), slot, pos, tab.exp, ref, H, KV, hd, tab.inv)
+    run_mfma = lambda: ops.attention_prefill(qq, sq, (kq, sk, v), 0, pos, S, tab.exp, out, H, KV, hd, tab.inv, ws)
     st = torch.cuda.current_stream()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps = 3
-    a.record(st)
-    for _ in range(reps):
-        ops.attention(qq, sq, (kq, sk, v), slot, pos, tab.exp, out, H, KV, hd, tab.inv)
-    b.record(st)
-    torch.cuda.synchronize()
-    us = a.elapsed_time(b) * 1000.0 / reps
+
+    def timed(fn, reps=3):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(reps):
+            fn()
+        b.record(st)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1000.0 / reps
+
+    us_rows = timed(run_rows)
+    us = timed(run_mfma, 5)
+    same = bool(torch.equal(out, ref))
     ops_ = 2 * 2 * (S * (S + 1) // 2) * hd * H
-    del kq, sk, v, qq, out
+    del kq, sk, v, qq, out, ref, ws
     torch.cuda.empty_cache()
     return {"S": S, "H": H, "KV": KV, "hd": hd, "us": round(us, 1), "G_ops": round(ops_ / 1e9, 2),
-            "TOPS": round(ops_ / us / 1e6, 3)}
+            "TOPS": round(ops_ / us / 1e6, 3), "row_kernel_us": round(us_rows, 1), "equal_to_row_kernel": same}
 
 
 def prefill_gemm(args):

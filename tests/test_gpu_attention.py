@@ -1,0 +1,114 @@
+"""GPU parity of integer attention (exact_llm.py:170-176; exact_torch.py:162-166) against the oracle:
+the row kernel (decode and small prefill) and the matrix-core prefill kernel, bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import exact_oracle as O
+from exact_amd import ops
+from exact_amd.tables import exp_t
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+I16, I32, I64 = torch.int16, torch.int32, torch.int64
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def make_case(seed, B, slot, H, KV, hd, Smax, nkeys, R, vmag):
+    """A cache with nkeys written positions in `slot` (other slots hold unrelated data) and R query rows
+    at positions nkeys - R .. nkeys - 1. vmag: ("small" | "large" | "wrap") magnitude of v."""
+    rng = np.random.default_rng(seed)
+    kq = rng.integers(-32767, 32768, (B, KV, Smax, hd))
+    sk = rng.integers(0, 4, (B, KV, Smax))
+    if vmag == "small":
+        v = rng.integers(-(1 << 29), 1 << 29, (B, KV, Smax, hd))
+    elif vmag == "large":
+        v = rng.integers(-(1 << 29), 1 << 29, (B, KV, Smax, hd)) << rng.integers(0, 20, (B, KV, Smax, 1))
+    else:   # products beyond int64: the sum is taken modulo 2^64, as numpy's int64 matmul does
+        v = rng.integers(-(1 << 62), 1 << 62, (B, KV, Smax, hd))
+    qq = rng.integers(-32767, 32768, (R, H, hd))
+    qq[0, 0, :4] = [32767, -32767, 0, -1]
+    sq = rng.integers(0, 4, (R, H))
+    pos = np.arange(nkeys - R, nkeys)
+    return kq, sk, v, qq, sq, pos
+
+
+def oracle_rows(kq, sk, v, qq, sq, pos, slot, H, KV, rows):
+    hd = qq.shape[-1]
+    out = np.zeros((len(rows), H * hd), np.int64)
+    inv = O.inv_sqrt_hd(hd)
+    S = int(pos[rows].max()) + 1
+    valid = np.arange(S)[None, :] <= pos[rows][:, None]
+    for h in range(H):
+        kh = h // (H // KV)
+        out[:, h * hd:(h + 1) * hd] = O.attention_head_q(qq[rows, h], sq[rows, h][:, None], kq[slot, kh, :S],
+                                                         sk[slot, kh, :S][:, None], v[slot, kh, :S], valid, inv)
+    return out
+
+
+def to_dev(kq, sk, v, qq, sq, pos):
+    d = lambda a, dt: torch.tensor(np.ascontiguousarray(a), dtype=dt, device=DEV)
+    return (d(kq, I16), d(sk, I32), d(v, I64)), d(qq, I16), d(sq, I32), d(pos, I32)
+
+
+def run_prefill(cache, qq, sq, pos, slot, nkeys, H, KV, hd):
+    R = qq.shape[0]
+    out = torch.full((R, H * hd), -7, dtype=I64, device=DEV)
+    obits = torch.full((R, H), -1, dtype=I32, device=DEV)
+    ws = ops.prefill_workspace(R, H, KV, hd, nkeys, DEV)
+    ops.attention_prefill(qq, sq, cache, slot, pos, nkeys, torch.tensor(exp_t(), dtype=I32, device=DEV), out, H, KV, hd,
+                          O.inv_sqrt_hd(hd), ws, obits)
+    return host(out), host(obits)
+
+
+def obits_of(out, H):
+    a = np.abs(out.reshape(out.shape[0], H, -1)).max(-1)
+    return np.vectorize(O.bitlen)(a)
+
+
+@pytest.mark.parametrize("H,KV,nkeys,R,vmag", [(4, 2, 1, 1, "small"), (4, 2, 33, 33, "small"), (4, 1, 100, 37, "large"),
+                                               (2, 2, 64, 64, "wrap"), (28, 4, 161, 129, "small")])
+def test_prefill_matches_oracle(H, KV, nkeys, R, vmag):
+    hd, Smax, slot = 128, 192, 1
+    case = make_case(nkeys * 7 + R, 2, slot, H, KV, hd, Smax, nkeys, R, vmag)
+    cache, qq, sq, pos = to_dev(*case)
+    out, obits = run_prefill(cache, qq, sq, pos, slot, nkeys, H, KV, hd)
+    want = oracle_rows(*case, slot, H, KV, np.arange(R))
+    assert np.array_equal(out, want)
+    assert np.array_equal(obits, obits_of(want, H))
+
+
+@pytest.mark.parametrize("R,nkeys", [(3, 50), (17, 17)])
+def test_row_attention_matches_oracle(R, nkeys):
+    H, KV, hd, Smax, slot = 4, 2, 128, 64, 1
+    case = make_case(R + nkeys, 2, slot, H, KV, hd, Smax, nkeys, R, "large")
+    cache, qq, sq, pos = to_dev(*case)
+    out = torch.zeros((R, H * hd), dtype=I64, device=DEV)
+    obits = torch.zeros((R, H), dtype=I32, device=DEV)
+    slots = torch.full((R,), slot, dtype=I32, device=DEV)
+    ops.attention(qq, sq, cache, slots, pos, torch.tensor(exp_t(), dtype=I32, device=DEV), out, H, KV, hd,
+                  O.inv_sqrt_hd(hd), obits)
+    want = oracle_rows(*case, slot, H, KV, np.arange(R))
+    assert np.array_equal(host(out), want)
+    assert np.array_equal(host(obits), obits_of(want, H))
+
+
+def test_prefill_full_size_2048():
+    """Attention prefill at the 7B shape (28 q heads, 4 KV heads, hd 128, 2048 tokens): every row equal to the
+    row kernel's result, and 24 rows (first, last and random) equal to the oracle."""
+    H, KV, hd, S, slot = 28, 4, 128, 2048, 0
+    case = make_case(2048, 1, slot, H, KV, hd, S, S, S, "small")
+    cache, qq, sq, pos = to_dev(*case)
+    out, obits = run_prefill(cache, qq, sq, pos, slot, S, H, KV, hd)
+    ref = torch.zeros((S, H * hd), dtype=I64, device=DEV)
+    refbits = torch.zeros((S, H), dtype=I32, device=DEV)
+    ops.attention(qq, sq, cache, torch.zeros(S, dtype=I32, device=DEV), pos,
+                  torch.tensor(exp_t(), dtype=I32, device=DEV), ref, H, KV, hd, O.inv_sqrt_hd(hd), refbits)
+    assert np.array_equal(out, host(ref))
+    assert np.array_equal(obits, host(refbits))
+    rows = np.sort(np.concatenate([[0, 1, 31, 32, S - 1], np.random.default_rng(3).choice(S, 19, replace=False)]))
+    assert np.array_equal(out[rows], oracle_rows(*case, slot, H, KV, rows))
