@@ -34,7 +34,7 @@ SIGNATURES = {
     "exact_isoftmax": [P, P, P, P, I32, I32, P],
     "exact_qkv_rope_cache": [P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
     "exact_attention": [P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
-    "exact_attention_prefill": [P, P, P, P, P, I32, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, I32, P],
+    "exact_attention_prefill": [P, P, P, P, P, I32, P, P, P, P, P, I64, I32, I32, I32, I32, I32, I32, I32, P],
     "exact_embed": [P, P, P, I32, I32, I32, P],
     "exact_embed_table": [P, P, P, I32, I32, P],
     "exact_logits_argmax": [P, P, P, P, P, I32, I32, I32, P],
@@ -46,7 +46,8 @@ SIGNATURES = {
     "exact_gemv_g128_experts": [P, I32, P, P, P, I64, I64, P, P, P, P, I32, P, I32, I32, P],
     "exact_moe_combine": [P, P, P, P, P, P, P, P, I32, I32, I32, I32, P],
 }
-OTHER = {"exact_version": ([], ctypes.c_int), "exact_last_error": ([], ctypes.c_char_p)}
+OTHER = {"exact_version": ([], ctypes.c_int), "exact_last_error": ([], ctypes.c_char_p),
+         "exact_attention_prefill_workspace": ([I32, I32, I32], ctypes.c_int64)}
 ERRORS = {1: "bad argument", 2: "unsupported size", 3: "HIP launch error"}
 
 

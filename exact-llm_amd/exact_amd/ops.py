@@ -233,13 +233,12 @@ def attention(qq, sq, cache, slot, pos, expt, out, H, KV, hd, inv, obits=None):
     return out
 
 
-def prefill_workspace(R, H, KV, hd, nkeys, device):
-    """Workspace of attention_prefill for R query rows over nkeys keys."""
-    kpad = -(-nkeys // 32) * 32
-    return {"scores": torch.empty(H * R * kpad, dtype=I64, device=device),
-            "pdig": torch.empty(3 * H * R * kpad, dtype=I8, device=device),
-            "vdig": torch.empty(KV * 8 * hd * kpad, dtype=I8, device=device),
-            "vbits": torch.empty(KV, dtype=I32, device=device), "R": R, "kpad": kpad}
+def prefill_workspace(KV, hd, nkeys, device):
+    """Workspace of attention_prefill for up to nkeys keys (digit copies of one slot's k and v)."""
+    n = _lib.load().exact_attention_prefill_workspace(KV, hd, nkeys)
+    if n < 0:
+        raise ExactError(f"attention_prefill: unsupported KV={KV}, hd={hd}, nkeys={nkeys}")
+    return torch.empty(int(n), dtype=I8, device=device)
 
 
 def attention_prefill(qq, sq, cache, slot, pos, nkeys, expt, out, H, KV, hd, inv, ws, obits=None):
@@ -247,15 +246,12 @@ def attention_prefill(qq, sq, cache, slot, pos, nkeys, expt, out, H, KV, hd, inv
     R = qq.shape[0]
     kq, sk, v = cache
     Smax = kq.shape[2]
-    kpad = -(-nkeys // 32) * 32
-    if ws["R"] < R or ws["kpad"] < kpad:
-        raise ExactError(f"attention_prefill workspace holds {ws['R']} rows x {ws['kpad']} keys, needs {R} x {kpad}")
     if obits is not None:
         _need(obits, I32, "obits", R * H)
     _need(pos, I32, "pos", R)
+    _need(ws, I8, "workspace")
     _lib.call("exact_attention_prefill", _ptr(qq), _ptr(sq), _ptr(kq), _ptr(sk), _ptr(v), int(slot), _ptr(pos), _ptr(expt),
-              _ptr(out), _ptr(obits), _ptr(ws["scores"]), _ptr(ws["pdig"]), _ptr(ws["vdig"]), _ptr(ws["vbits"]), R, H, KV,
-              hd, Smax, nkeys, inv, _stream())
+              _ptr(out), _ptr(obits), _ptr(ws), ws.numel(), R, H, KV, hd, Smax, nkeys, inv, _stream())
     return out
 
 

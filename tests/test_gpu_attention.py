@@ -18,12 +18,15 @@ def host(t):
     return t.cpu().numpy()
 
 
-def make_case(seed, B, slot, H, KV, hd, Smax, nkeys, R, vmag):
+def make_case(seed, B, slot, H, KV, hd, Smax, nkeys, R, vmag, shifts=4):
     """A cache with nkeys written positions in `slot` (other slots hold unrelated data) and R query rows
-    at positions nkeys - R .. nkeys - 1. vmag: ("small" | "large" | "wrap") magnitude of v."""
+    at positions nkeys - R .. nkeys - 1. vmag: ("small" | "large" | "wrap") magnitude of v; q and k row
+    shifts drawn from [0, shifts) (or [0, shifts[0]) for q and [0, shifts[1]) for k). Shift sums above 32
+    take the left-shift branch of shr; the kernel's float64 scores cover sums up to 33, int64 the rest."""
     rng = np.random.default_rng(seed)
     kq = rng.integers(-32767, 32768, (B, KV, Smax, hd))
-    sk = rng.integers(0, 4, (B, KV, Smax))
+    qs, ks = (shifts, shifts) if np.isscalar(shifts) else shifts
+    sk = rng.integers(0, ks, (B, KV, Smax))
     if vmag == "small":
         v = rng.integers(-(1 << 29), 1 << 29, (B, KV, Smax, hd))
     elif vmag == "large":
@@ -32,7 +35,7 @@ def make_case(seed, B, slot, H, KV, hd, Smax, nkeys, R, vmag):
         v = rng.integers(-(1 << 62), 1 << 62, (B, KV, Smax, hd))
     qq = rng.integers(-32767, 32768, (R, H, hd))
     qq[0, 0, :4] = [32767, -32767, 0, -1]
-    sq = rng.integers(0, 4, (R, H))
+    sq = rng.integers(0, qs, (R, H))
     pos = np.arange(nkeys - R, nkeys)
     return kq, sk, v, qq, sq, pos
 
@@ -59,7 +62,7 @@ def run_prefill(cache, qq, sq, pos, slot, nkeys, H, KV, hd):
     R = qq.shape[0]
     out = torch.full((R, H * hd), -7, dtype=I64, device=DEV)
     obits = torch.full((R, H), -1, dtype=I32, device=DEV)
-    ws = ops.prefill_workspace(R, H, KV, hd, nkeys, DEV)
+    ws = ops.prefill_workspace(KV, hd, nkeys, DEV)
     ops.attention_prefill(qq, sq, cache, slot, pos, nkeys, torch.tensor(exp_t(), dtype=I32, device=DEV), out, H, KV, hd,
                           O.inv_sqrt_hd(hd), ws, obits)
     return host(out), host(obits)
@@ -70,11 +73,14 @@ def obits_of(out, H):
     return np.vectorize(O.bitlen)(a)
 
 
-@pytest.mark.parametrize("H,KV,nkeys,R,vmag", [(4, 2, 1, 1, "small"), (4, 2, 33, 33, "small"), (4, 1, 100, 37, "large"),
-                                               (2, 2, 64, 64, "wrap"), (28, 4, 161, 129, "small")])
-def test_prefill_matches_oracle(H, KV, nkeys, R, vmag):
+@pytest.mark.parametrize("H,KV,nkeys,R,vmag,shifts", [(4, 2, 1, 1, "small", 4), (4, 2, 33, 33, "small", 4),
+                                                      (4, 1, 100, 37, "large", 4), (2, 2, 64, 64, "wrap", 4),
+                                                      (28, 4, 161, 129, "small", 4), (4, 2, 150, 150, "small", 22),
+                                                      (7, 7, 190, 70, "large", 1), (4, 2, 120, 120, "small", (18, 17)),
+                                                      (4, 2, 120, 120, "small", (18, 18))])
+def test_prefill_matches_oracle(H, KV, nkeys, R, vmag, shifts):
     hd, Smax, slot = 128, 192, 1
-    case = make_case(nkeys * 7 + R, 2, slot, H, KV, hd, Smax, nkeys, R, vmag)
+    case = make_case(nkeys * 7 + R, 2, slot, H, KV, hd, Smax, nkeys, R, vmag, shifts)
     cache, qq, sq, pos = to_dev(*case)
     out, obits = run_prefill(cache, qq, sq, pos, slot, nkeys, H, KV, hd)
     want = oracle_rows(*case, slot, H, KV, np.arange(R))
