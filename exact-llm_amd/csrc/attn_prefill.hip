@@ -27,6 +27,7 @@ namespace exact {
 int zero_bytes(void* dst, int64_t nbytes, hipStream_t st);
 
 #define AP_HD 128
+#define AP_TN 4608   // exp entries in LDS; the fast path needs the table to be zero from entry AP_TN - 2 on
 
 // int16 -> (hi, lo - 128) int8 digits of 16 values held in two 16-byte chunks
 __device__ __forceinline__ void split_digits(v4i p0, v4i p1, v4i& hi, v4i& lo) {
@@ -94,11 +95,12 @@ __global__ __launch_bounds__(256) void k_vdigits(const int64_t* __restrict__ v, 
 
 // Digits of every cached k of the sequence for the q.k product: kdig[(((kh * 2 + p) * 4 + kb) * kpad + j) * 32 + c]
 // = digit p (0: hi, 1: lo - 128) of k[j][32 kb + c]; ck[kh * kpad + j] = 128 sum_d k[j][d] - 16384 hd and
-// skk[kh * kpad + j] = sk[j] (zeros from nkeys on); skmax[kh] = max sk (zeroed before). grid (kpad / 32, KV),
-// block 256: 8 threads per key.
+// skk[kh * kpad + j] = sk[j] (zeros from nkeys on); skmax[kh] = max sk; tnz[0] = 1 if the exp table T has a
+// nonzero entry from AP_TN - 2 on (both zeroed before). grid (kpad / 32, KV), block 256: 8 threads per key.
 __global__ __launch_bounds__(256) void k_kdigits(const int16_t* __restrict__ kq, const int32_t* __restrict__ sk, int sl, int KV,
                                                  int Smax, int nkeys, int kpad, int8_t* __restrict__ kdig, int32_t* __restrict__ ck,
-                                                 int32_t* __restrict__ skk, int32_t* __restrict__ skmax) {
+                                                 int32_t* __restrict__ skk, int32_t* __restrict__ skmax,
+                                                 const int32_t* __restrict__ T, int32_t* __restrict__ tnz) {
   const int kh = blockIdx.y, tid = threadIdx.x;
   const int j = blockIdx.x * 32 + (tid >> 3), c = tid & 7;   // c: 16 dimensions 16 c .. 16 c + 15
   const int64_t row = ((int64_t)sl * KV + kh) * Smax + j;
@@ -126,6 +128,11 @@ __global__ __launch_bounds__(256) void k_kdigits(const int16_t* __restrict__ kq,
   }
   skv = wave_max_i32(skv);
   if ((tid & 63) == 0) atomicMax(skmax + kh, skv);
+  if (blockIdx.x == 0 && blockIdx.y == 0) {   // the fast path keeps exp entries [0, AP_TN) in LDS
+    int nz = 0;
+    for (int i = AP_TN - 2 + tid; i < EXACT_EXP_N; i += 256) nz |= T[i] != 0;
+    if (nz) atomicOr(tnz, 1);
+  }
 }
 
 // floor(a / b) for b > 0 given rb ~ 1 / b: the estimate is corrected exactly, as in floordiv_pos
@@ -144,73 +151,167 @@ struct QK {
   const int8_t* kd;      // this KV head's k digits
   const int32_t* ckh;    // 128 sum k - 16384 hd per key
   const int32_t* skh;    // sk per key
-  int kpad, l32, half;
-  v4i qh[4], ql[4];      // q digits: B operand, column = query l32, dimensions 32 kb + 16 half + [0, 16)
+  const v4i* qd;         // LDS q digits [kb][hi, lo][lane]: B operand, column = query l32, dimensions 32 kb + 16 half + [0, 16)
+  int kpad, l32, half, lane;
 };
 
-__device__ __forceinline__ void qk_tile(const QK& c, int j0, v16i& hh, v16i& xx, v16i& ll) {
+// k digits of one 32-key tile: A operand, row = key l32
+struct KTile {
+  v4i hi[4], lo[4];
+};
+
+// per-key terms of the 16 keys a lane holds in a tile (keys j0 + 8 g + 4 half + [0, 4))
+struct KCol {
+  v4i ck[4], sk[4];
+};
+
+__device__ __forceinline__ void load_kcol(const QK& c, int j0, KCol& k) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    k.ck[g] = *reinterpret_cast<const v4i*>(c.ckh + j0 + 8 * g + 4 * c.half);
+    k.sk[g] = *reinterpret_cast<const v4i*>(c.skh + j0 + 8 * g + 4 * c.half);
+  }
+}
+
+__device__ __forceinline__ void load_ktile(const QK& c, int j0, KTile& k) {
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    k.hi[kb] = *reinterpret_cast<const v4i*>(c.kd + ((int64_t)kb * c.kpad + j0 + c.l32) * 32 + 16 * c.half);
+    k.lo[kb] = *reinterpret_cast<const v4i*>(c.kd + ((int64_t)(4 + kb) * c.kpad + j0 + c.l32) * 32 + 16 * c.half);
+  }
+}
+
+__device__ __forceinline__ void mfma_ktile(const QK& c, const KTile& k, v16i& hh, v16i& xx, v16i& ll) {
   hh = v16i{};
   xx = v16i{};
   ll = v16i{};
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
-    const v4i khi = *reinterpret_cast<const v4i*>(c.kd + ((int64_t)kb * c.kpad + j0 + c.l32) * 32 + 16 * c.half);
-    const v4i klo = *reinterpret_cast<const v4i*>(c.kd + ((int64_t)(4 + kb) * c.kpad + j0 + c.l32) * 32 + 16 * c.half);
-    hh = __builtin_amdgcn_mfma_i32_32x32x32_i8(khi, c.qh[kb], hh, 0, 0, 0);
-    xx = __builtin_amdgcn_mfma_i32_32x32x32_i8(khi, c.ql[kb], xx, 0, 0, 0);
-    xx = __builtin_amdgcn_mfma_i32_32x32x32_i8(klo, c.qh[kb], xx, 0, 0, 0);
-    ll = __builtin_amdgcn_mfma_i32_32x32x32_i8(klo, c.ql[kb], ll, 0, 0, 0);
+    const v4i qh = c.qd[(2 * kb) * 64 + c.lane], ql = c.qd[(2 * kb + 1) * 64 + c.lane];
+    hh = __builtin_amdgcn_mfma_i32_32x32x32_i8(k.hi[kb], qh, hh, 0, 0, 0);
+    xx = __builtin_amdgcn_mfma_i32_32x32x32_i8(k.hi[kb], ql, xx, 0, 0, 0);
+    xx = __builtin_amdgcn_mfma_i32_32x32x32_i8(k.lo[kb], qh, xx, 0, 0, 0);
+    ll = __builtin_amdgcn_mfma_i32_32x32x32_i8(k.lo[kb], ql, ll, 0, 0, 0);
   }
 }
 
-// Float64 scores, exact when every |dot * INV| * 2^(sq + sk - 32) < 2^52 (the kernel checks sq + sk <= 33 and
-// INV < 2^14 over the block): dot < 2^38 and dot * INV < 2^52 are exact, the power-of-two scalings are exact,
-// and floor(w + 1/2) is shr's round-half-up. Masked keys (past the row's position) get -1e300.
+// ---- float64 path. Exact when every |dot * INV| * 2^(sq + sk - 32) < 2^52, which the kernel checks over the
+// block (sq + sk <= 33, INV < 2^14): dot < 2^38 and dot * INV < 2^52 are exact in float64, the power-of-two
+// scalings are exact, and floor(w + 1/2) is shr's round-half-up. (256 HH + (HL + LH)) < 2^30 and
+// LL + 128 (sum q + sum k) - 16384 hd < 2^31 are exact in int32.
 #define AP_NEG (-1e300)
-template <bool MASK>
-__device__ __forceinline__ void scores_f64(const QK& c, int j0, int rterm, double fscale, int mypos, double (&sc)[16]) {
-  v16i hh, xx, ll;
-  qk_tile(c, j0, hh, xx, ll);
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const v4i ckv = *reinterpret_cast<const v4i*>(c.ckh + j0 + 8 * g + 4 * c.half);
-    const v4i skv = *reinterpret_cast<const v4i*>(c.skh + j0 + 8 * g + 4 * c.half);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = 4 * g + u;
-      const double d = __builtin_fma((double)hh[i], 65536.0, __builtin_fma((double)xx[i], 256.0, (double)(ll[i] + ckv[u] + rterm)));
-      double w = __builtin_floor(__builtin_ldexp(d * fscale, skv[u]) + 0.5);
-      if (MASK) w = j0 + 8 * g + 4 * c.half + u <= mypos ? w : AP_NEG;
-      sc[i] = w;
-    }
-  }
+
+// max of two float64 values that are never NaN: one v_max_f64 (fmax adds NaN quieting)
+__device__ __forceinline__ double max_f64(double a, double b) {
+  double r;
+  asm("v_max_f64 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
 }
 
-// exp LUT of mx - sc (>= 0, exact in float64): lut_exp without 64-bit integer work; 0 for masked keys
-__device__ __forceinline__ int exp_f64(const int32_t* T, double mx, double sc) {
-  const double dd = mx - sc;
-  const int di = (int)__builtin_fmin(dd, (double)((40 << EXACT_F) - 1));
+// unrounded score w (float64, exact) of an element; the score is floor(w + 1/2)
+__device__ __forceinline__ double raw_score(int hh, int xx, int llc, double fscale, int skv) {
+  const int m = (hh << 8) + xx;
+  return __builtin_ldexp(__builtin_fma((double)m, 256.0, (double)llc) * fscale, skv);
+}
+
+// lut_exp(mx - sc) for mx - sc = dd >= 0: indices past AP_TN - 2 read entry AP_TN - 2 (zero, like every later
+// one), which also covers the reference's cut at 40.0
+__device__ __forceinline__ int exp_lds(const int32_t* T, double dd) {
+  const int di = (int)__builtin_fmin(dd, (double)((AP_TN - 1) * 256 - 1));
   const int i = di >> 8, fr = di & 255;
   const int a = T[i], b = T[i + 1];
-  const int e = a - (((a - b) * fr + 128) >> 8);
-  return dd < (double)(40 << EXACT_F) ? e : 0;
+  return a - (((a - b) * fr + 128) >> 8);
 }
 
-// floor(e 2^20 / es) for 0 <= e <= 2^24 < es... : the estimate e 2^20 * (1 / es) is within 2^-31 of the quotient,
-// and the remainder (exact in float64, below 2^53) corrects it by one either way.
-__device__ __forceinline__ int pdiv_f64(int e, double es, double res) {
-  const double a = (double)e * 1048576.0;
-  double q = __builtin_floor(a * res);
-  const double r = __builtin_fma(-q, es, a);
+// floor(e 2^20 / es) for 0 <= e <= 2^24, es < 2^53: the estimate e * (2^20 / es) is within 2^-31 of the
+// quotient and the remainder (exact in float64) corrects it by one either way
+__device__ __forceinline__ int pdiv_f64(int e, double es, double res20) {
+  const double ed = (double)e;
+  double q = __builtin_floor(ed * res20);
+  const double r = __builtin_fma(-q, es, ed * 1048576.0);
   q = r < 0.0 ? q - 1.0 : q;
   q = r >= es ? q + 1.0 : q;
   return (int)q;
 }
 
-// int64 scores (any sq, sk): shr64 as the reference
-__device__ __forceinline__ void scores_i64(const QK& c, int j0, int64_t rterm, int sqv, int INV, int64_t (&sc)[16]) {
-  v16i hh, xx, ll;
-  qk_tile(c, j0, hh, xx, ll);
+// Balanced base-256 digits of p (0 <= p <= 2^20) for 4 keys at once: u = p + 128 + 128 * 256 holds d0 + 128,
+// d1 + 128 and d2 in bytes 0, 1, 2; the planes take byte a of each u (planes 0 and 1 then flip bit 7).
+__device__ __forceinline__ void pack_digits(int p0, int p1, int p2, int p3, int& w0, int& w1, int& w2) {
+  const int u0 = p0 + 32896, u1 = p1 + 32896, u2 = p2 + 32896, u3 = p3 + 32896;
+  const int y = __builtin_amdgcn_perm(u1, u0, 0x05010400u);   // u0.b0 u1.b0 u0.b1 u1.b1
+  const int z = __builtin_amdgcn_perm(u3, u2, 0x05010400u);   // u2.b0 u3.b0 u2.b1 u3.b1
+  const int y2 = __builtin_amdgcn_perm(u1, u0, 0x0c0c0602u);  // u0.b2 u1.b2 0 0
+  const int z2 = __builtin_amdgcn_perm(u3, u2, 0x0c0c0602u);
+  w0 = __builtin_amdgcn_perm(z, y, 0x05040100u) ^ 0x80808080;
+  w1 = __builtin_amdgcn_perm(z, y, 0x07060302u) ^ 0x80808080;
+  w2 = __builtin_amdgcn_perm(z2, y2, 0x05040100u);
+}
+
+struct FastCtx {
+  const int32_t* T;   // LDS exp table
+  double fscale;      // INV 2^(sq - 32)
+  int rterm, mypos;
+};
+
+// the 16 unrounded scores of a tile (masked keys AP_NEG)
+template <bool MASK>
+__device__ __forceinline__ void tile_raw(const QK& c, const FastCtx& f, int j0, const KCol& kc, const v16i& hh, const v16i& xx,
+                                         const v16i& ll, double (&wv)[16]) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const v4i ckv = kc.ck[g], skv = kc.sk[g];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = 4 * g + u;
+      double x = raw_score(hh[i], xx[i], ll[i] + ckv[u] + f.rterm, f.fscale, skv[u]);
+      if (MASK) x = j0 + 8 * g + 4 * c.half + u <= f.mypos ? x : AP_NEG;
+      wv[i] = x;
+    }
+  }
+}
+
+template <bool MASK>
+__device__ __forceinline__ double tile_max(const QK& c, const FastCtx& f, int j0, const KCol& kc, const v16i& hh, const v16i& xx,
+                                           const v16i& ll, double mw) {
+  double wv[16];
+  tile_raw<MASK>(c, f, j0, kc, hh, xx, ll, wv);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) mw = max_f64(mw, wv[i]);
+  return mw;
+}
+
+template <bool MASK>
+__device__ __forceinline__ int tile_esum(const QK& c, const FastCtx& f, int j0, const KCol& kc, const v16i& hh, const v16i& xx,
+                                         const v16i& ll, double mx) {
+  double wv[16];
+  tile_raw<MASK>(c, f, j0, kc, hh, xx, ll, wv);
+  int part = 0;   // 16 terms <= 2^24
+#pragma unroll
+  for (int i = 0; i < 16; ++i) part += exp_lds(f.T, mx - __builtin_floor(wv[i] + 0.5));
+  return part;
+}
+
+template <bool MASK>
+__device__ __forceinline__ void tile_pdig(const QK& c, const FastCtx& f, int j0, const KCol& kc, const v16i& hh, const v16i& xx,
+                                          const v16i& ll, double mx, double esd, double res20, v4i (&pa)[3]) {
+  double wv[16];
+  tile_raw<MASK>(c, f, j0, kc, hh, xx, ll, wv);
+  int p[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) p[i] = pdiv_f64(exp_lds(f.T, mx - __builtin_floor(wv[i] + 0.5)), esd, res20);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+        int w0, w1, w2;
+        pack_digits(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3], w0, w1, w2);
+        pa[0][g] = w0;
+        pa[1][g] = w1;
+        pa[2][g] = w2;
+      }
+}
+
+// ---- int64 path (any shifts, any exp table): shr64 and lut_exp as the reference, exp table in global memory
+__device__ __forceinline__ void scores_i64(const QK& c, int j0, const v16i& hh, const v16i& xx, const v16i& ll, int64_t rterm,
+                                           int sqv, int INV, int64_t (&sc)[16]) {
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const v4i ckv = *reinterpret_cast<const v4i*>(c.ckh + j0 + 8 * g + 4 * c.half);
@@ -224,163 +325,292 @@ __device__ __forceinline__ void scores_i64(const QK& c, int j0, int64_t rterm, i
   }
 }
 
-// byte i % 4 of word i / 4 of the three balanced digit planes of p (0 <= p <= 2^20); planes 0 and 1 still
-// carry +128 (flipped by the caller with ^ 0x80808080)
-__device__ __forceinline__ void put_digits(int p, int i, v4i (&pa)[3]) {
-  const int t0 = p + 128;
-  const int t1 = (t0 >> 8) + 128;
-  const int sh = 8 * (i & 3);
-  pa[0][i >> 2] |= (t0 & 255) << sh;
-  pa[1][i >> 2] |= (t1 & 255) << sh;
-  pa[2][i >> 2] |= (t1 >> 8) << sh;
-}
+#define AP_WAVES 8     // waves per block
+#define AP_PROD 4      // waves 0..3 produce p digits in the third pass, waves 4..7 multiply them into V
 
 struct AttnLDS {
   int32_t* T;
-  v4i (*Pl)[4][3][64];
-  int64_t (*red_mx)[32];
-  int64_t (*red_es)[32];
-  int* rowbits;
+  v4i (*Pl)[AP_PROD][3][64];
+  double (*red_w)[32];
+  int64_t (*red_a)[32];
+  int64_t (*red_b)[32];
 };
 
-template <int NB, bool FAST>
-__device__ __forceinline__ void attn_body(const QK& c, const AttnLDS& L, int64_t rterm, int sqv, int INV, int mypos,
-                                          int ntile, int firstpos, const int8_t* __restrict__ vd, int64_t vplane,
-                                          int w, int lane, v16i (&acc)[NB + 2]) {
-  const int l32 = c.l32, half = c.half;
-  const int rt32 = (int)rterm;
-  const double fscale = __builtin_ldexp((double)INV, sqv - 32);
-  // pass 1: row maximum
-  int64_t mx;
-  double mxd = AP_NEG;
-  if (FAST) {
-    for (int t = w; t < ntile; t += 4) {
-      double sc[16];
-      if (32 * t + 31 <= firstpos) scores_f64<false>(c, 32 * t, rt32, fscale, mypos, sc);
-      else scores_f64<true>(c, 32 * t, rt32, fscale, mypos, sc);
+// Consumer side of the third pass: p . v of one step (AP_PROD tiles of p digits in LDS) into the shift classes.
+// vb holds the step's V digits (loaded by the caller one step ahead when NB = 4).
+template <int NB>
+__device__ __forceinline__ void pv_mfma(const AttnLDS& L, int buf, int tiles, int lane, const v4i (&vb)[AP_PROD][NB],
+                                        v16i (&acc)[NB + 2]) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mxd = __builtin_fmax(mxd, sc[i]);
-    }
-    mxd = __builtin_fmax(mxd, __shfl_xor(mxd, 32, 64));
-    mx = (int64_t)mxd;
-  } else {
-    mx = INT64_MIN;
-    for (int t = w; t < ntile; t += 4) {
-      int64_t sc[16];
-      scores_i64(c, 32 * t, rterm, sqv, INV, sc);
+  for (int tt = 0; tt < AP_PROD; ++tt) {
+    if (tt < tiles) {
+      v4i pv[3];
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (32 * t + 8 * (i >> 2) + 4 * half + (i & 3) <= mypos) mx = sc[i] > mx ? sc[i] : mx;
-    }
-    const int64_t o = __shfl_xor(mx, 32, 64);
-    mx = o > mx ? o : mx;
-  }
-  if (half == 0) L.red_mx[w][l32] = mx;
-  __syncthreads();
+      for (int a = 0; a < 3; ++a) pv[a] = L.Pl[buf][tt][a][lane];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) mx = L.red_mx[k][l32] > mx ? L.red_mx[k][l32] : mx;
-  mxd = (double)mx;
-  // pass 2: sum of exp
-  int64_t es = 0;
-  for (int t = w; t < ntile; t += 4) {
-    if (FAST) {
-      double sc[16];
-      if (32 * t + 31 <= firstpos) scores_f64<false>(c, 32 * t, rt32, fscale, mypos, sc);
-      else scores_f64<true>(c, 32 * t, rt32, fscale, mypos, sc);
-      int part = 0;   // 16 terms <= 2^24
+      for (int a = 0; a < 3; ++a)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) part += exp_f64(L.T, mxd, sc[i]);
-      es += part;
-    } else {
-      int64_t sc[16];
-      scores_i64(c, 32 * t, rterm, sqv, INV, sc);
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (32 * t + 8 * (i >> 2) + 4 * half + (i & 3) <= mypos) es += lut_exp(L.T, mx - sc[i]);
-    }
-  }
-  es += __shfl_xor(es, 32, 64);
-  if (half == 0) L.red_es[w][l32] = es;
-  __syncthreads();
-  es = L.red_es[0][l32] + L.red_es[1][l32] + L.red_es[2][l32] + L.red_es[3][l32];
-  const double esd = (double)es, res = 1.0 / esd;
-  // pass 3: p digits, then p . v per shift class
-#pragma unroll
-  for (int k = 0; k < NB + 2; ++k) acc[k] = v16i{};
-  const int nsteps = (ntile + 3) / 4;
-  for (int s = 0; s < nsteps; ++s) {
-    const int t = 4 * s + w, buf = s & 1;
-    v4i pa[3] = {v4i{}, v4i{}, v4i{}};
-    if (t < ntile) {
-      if (FAST) {
-        double sc[16];
-        if (32 * t + 31 <= firstpos) scores_f64<false>(c, 32 * t, rt32, fscale, mypos, sc);
-        else scores_f64<true>(c, 32 * t, rt32, fscale, mypos, sc);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) put_digits(pdiv_f64(exp_f64(L.T, mxd, sc[i]), esd, res), i, pa);
-      } else {
-        int64_t sc[16];
-        scores_i64(c, 32 * t, rterm, sqv, INV, sc);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const bool ok = 32 * t + 8 * (i >> 2) + 4 * half + (i & 3) <= mypos;
-          put_digits(ok ? (int)floordiv_rcp(shl64(lut_exp(L.T, mx - sc[i]), 20), es, res) : 0, i, pa);
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        pa[0][q] ^= 0x80808080;
-        pa[1][q] ^= 0x80808080;
-      }
-    }
-#pragma unroll
-    for (int a = 0; a < 3; ++a) L.Pl[buf][w][a][lane] = pa[a];
-    __syncthreads();
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      if (4 * s + tt < ntile) {
-        const int jb = 32 * (4 * s + tt);
-        v4i pv[3], vb[NB];
-#pragma unroll
-        for (int a = 0; a < 3; ++a) pv[a] = L.Pl[buf][tt][a][lane];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) vb[b] = *reinterpret_cast<const v4i*>(vd + b * vplane + jb);
-#pragma unroll
-        for (int a = 0; a < 3; ++a)
-#pragma unroll
-          for (int b = 0; b < NB; ++b) acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pv[a], vb[b], acc[a + b], 0, 0, 0);
-      }
+        for (int b = 0; b < NB; ++b) acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pv[a], vb[tt][b], acc[a + b], 0, 0, 0);
     }
   }
 }
 
-// grid (ceil(R / 32), H), block 256 (4 waves): query rows [32 x, 32 x + 32) of head y, heaviest tiles first.
-// Key tiles of 32; in the first two passes wave w takes tiles w, w + 4, ...; in the third, each step of 4 tiles
-// has wave w turn tile 4 step + w into p digits (LDS, double-buffered) and then every wave multiplies the 4
-// tiles' p into V for its 32 dimensions. NB = V digits; the instantiation whose NB the KV head does not need
-// returns at once (both are launched, so the host need not read vbits). Scores run in float64 when the block's
-// shifts allow it exactly, else in int64.
 template <int NB>
-__global__ __launch_bounds__(256) void k_attn_fused(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
+__device__ __forceinline__ void load_v(const int8_t* __restrict__ vd, int64_t vplane, int s, int ntile, v4i (&vb)[AP_PROD][NB]) {
+#pragma unroll
+  for (int tt = 0; tt < AP_PROD; ++tt) {
+    const int t = AP_PROD * s + tt < ntile ? AP_PROD * s + tt : ntile - 1;   // stays inside the written keys
+#pragma unroll
+    for (int b = 0; b < NB; ++b) vb[tt][b] = *reinterpret_cast<const v4i*>(vd + b * vplane + 32 * t);
+  }
+}
+
+// Consumer loop of the third pass: iteration s multiplies step s - 1 (the producers fill step s meanwhile).
+// NB = 4 loads the V digits one step ahead; NB = 8 (no registers to spare) loads them tile by tile.
+template <int NB>
+__device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile, const int8_t* __restrict__ vd, int64_t vplane,
+                                        int lane, v16i (&acc)[NB + 2]) {
+#pragma unroll
+  for (int k = 0; k < NB + 2; ++k) acc[k] = v16i{};
+  if constexpr (NB == 4) {
+    v4i vb[AP_PROD][NB];
+    load_v<NB>(vd, vplane, 0, ntile, vb);
+    for (int s = 0; s <= nsteps; ++s) {
+      if (s >= 1) pv_mfma<NB>(L, (s - 1) & 1, min(AP_PROD, ntile - AP_PROD * (s - 1)), lane, vb, acc);
+      if (s < nsteps) load_v<NB>(vd, vplane, s, ntile, vb);
+      __syncthreads();
+    }
+  } else {
+    for (int s = 0; s <= nsteps; ++s) {
+      if (s >= 1) {
+        const int buf = (s - 1) & 1;
+        for (int tt = 0; tt < AP_PROD && AP_PROD * (s - 1) + tt < ntile; ++tt) {
+          const int t = AP_PROD * (s - 1) + tt;
+          v4i pv[3], vb[NB];
+#pragma unroll
+          for (int b = 0; b < NB; ++b) vb[b] = *reinterpret_cast<const v4i*>(vd + b * vplane + 32 * t);
+#pragma unroll
+          for (int a = 0; a < 3; ++a) pv[a] = L.Pl[buf][tt][a][lane];
+#pragma unroll
+          for (int a = 0; a < 3; ++a)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pv[a], vb[b], acc[a + b], 0, 0, 0);
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Passes 1 and 2 for the float64 path: wave w takes tiles w, w + 8, ... (k digits of the next tile loaded while
+// this one is finished); returns the row maximum score and the row sum of exp.
+__device__ __forceinline__ void passes12_f64(const QK& c, const AttnLDS& L, const FastCtx& f, int ntile, int firstpos, int w,
+                                             double& mx, int64_t& es) {
+  KTile kt;
+  KCol kc;
+  double mw = AP_NEG;
+  if (w < ntile) {
+    load_ktile(c, 32 * w, kt);
+    load_kcol(c, 32 * w, kc);
+  }
+  for (int t = w; t < ntile; t += AP_WAVES) {
+    v16i hh, xx, ll;
+    mfma_ktile(c, kt, hh, xx, ll);
+    const KCol cur = kc;
+    if (t + AP_WAVES < ntile) {
+      load_ktile(c, 32 * (t + AP_WAVES), kt);
+      load_kcol(c, 32 * (t + AP_WAVES), kc);
+    }
+    mw = 32 * t + 31 <= firstpos ? tile_max<false>(c, f, 32 * t, cur, hh, xx, ll, mw) : tile_max<true>(c, f, 32 * t, cur, hh, xx, ll, mw);
+  }
+  mw = __builtin_fmax(mw, __shfl_xor(mw, 32, 64));
+  if (c.half == 0) L.red_w[w][c.l32] = mw;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < AP_WAVES; ++k) mw = __builtin_fmax(mw, L.red_w[k][c.l32]);
+  mx = __builtin_floor(mw + 0.5);
+  int64_t e = 0;
+  if (w < ntile) {
+    load_ktile(c, 32 * w, kt);
+    load_kcol(c, 32 * w, kc);
+  }
+  for (int t = w; t < ntile; t += AP_WAVES) {
+    v16i hh, xx, ll;
+    mfma_ktile(c, kt, hh, xx, ll);
+    const KCol cur = kc;
+    if (t + AP_WAVES < ntile) {
+      load_ktile(c, 32 * (t + AP_WAVES), kt);
+      load_kcol(c, 32 * (t + AP_WAVES), kc);
+    }
+    e += 32 * t + 31 <= firstpos ? tile_esum<false>(c, f, 32 * t, cur, hh, xx, ll, mx) : tile_esum<true>(c, f, 32 * t, cur, hh, xx, ll, mx);
+  }
+  e += __shfl_xor(e, 32, 64);
+  if (c.half == 0) L.red_a[w][c.l32] = e;
+  __syncthreads();
+  es = 0;
+#pragma unroll
+  for (int k = 0; k < AP_WAVES; ++k) es += L.red_a[k][c.l32];
+}
+
+// Producer loop of the third pass (float64 path): iteration s turns tile AP_PROD s + w into p digits.
+__device__ __forceinline__ void produce_f64(const QK& c, const AttnLDS& L, const FastCtx& f, int nsteps, int ntile, int firstpos,
+                                            int w, int lane, double mx, int64_t es) {
+  const double esd = (double)es, res20 = 1048576.0 / esd;   // 2^20 / es: the reciprocal scaled exactly
+  KTile kt;
+  KCol kc;
+  if (w < ntile) {
+    load_ktile(c, 32 * w, kt);
+    load_kcol(c, 32 * w, kc);
+  }
+  for (int s = 0; s <= nsteps; ++s) {
+    const int t = AP_PROD * s + w;
+    if (s < nsteps) {
+      v4i pa[3] = {v4i{}, v4i{}, v4i{}};
+      if (t < ntile) {
+        v16i hh, xx, ll;
+        mfma_ktile(c, kt, hh, xx, ll);
+        const KCol cur = kc;
+        if (t + AP_PROD < ntile) {
+          load_ktile(c, 32 * (t + AP_PROD), kt);
+          load_kcol(c, 32 * (t + AP_PROD), kc);
+        }
+        if (32 * t + 31 <= firstpos) tile_pdig<false>(c, f, 32 * t, cur, hh, xx, ll, mx, esd, res20, pa);
+        else tile_pdig<true>(c, f, 32 * t, cur, hh, xx, ll, mx, esd, res20, pa);
+      }
+#pragma unroll
+      for (int a = 0; a < 3; ++a) L.Pl[s & 1][w][a][lane] = pa[a];
+    }
+    __syncthreads();
+  }
+}
+
+// The int64 path (any shifts, any exp table): shr64 and lut_exp as the reference, exp table in global memory.
+__device__ __forceinline__ void passes12_i64(const QK& c, const AttnLDS& L, const int32_t* __restrict__ Tg, int64_t rterm, int sqv,
+                                             int INV, int mypos, int ntile, int w, int64_t& mx, int64_t& es) {
+  auto valid = [&](int t, int i) { return 32 * t + 8 * (i >> 2) + 4 * c.half + (i & 3) <= mypos; };
+  int64_t m = INT64_MIN;
+  for (int t = w; t < ntile; t += AP_WAVES) {
+    KTile kt;
+    v16i hh, xx, ll;
+    int64_t sc[16];
+    load_ktile(c, 32 * t, kt);
+    mfma_ktile(c, kt, hh, xx, ll);
+    scores_i64(c, 32 * t, hh, xx, ll, rterm, sqv, INV, sc);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (valid(t, i)) m = sc[i] > m ? sc[i] : m;
+  }
+  {
+    const int64_t o = __shfl_xor(m, 32, 64);
+    m = o > m ? o : m;
+  }
+  if (c.half == 0) L.red_a[w][c.l32] = m;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < AP_WAVES; ++k) m = L.red_a[k][c.l32] > m ? L.red_a[k][c.l32] : m;
+  mx = m;
+  int64_t e = 0;
+  for (int t = w; t < ntile; t += AP_WAVES) {
+    KTile kt;
+    v16i hh, xx, ll;
+    int64_t sc[16];
+    load_ktile(c, 32 * t, kt);
+    mfma_ktile(c, kt, hh, xx, ll);
+    scores_i64(c, 32 * t, hh, xx, ll, rterm, sqv, INV, sc);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (valid(t, i)) e += lut_exp(Tg, mx - sc[i]);
+  }
+  e += __shfl_xor(e, 32, 64);
+  if (c.half == 0) L.red_b[w][c.l32] = e;
+  __syncthreads();
+  es = 0;
+#pragma unroll
+  for (int k = 0; k < AP_WAVES; ++k) es += L.red_b[k][c.l32];
+}
+
+__device__ __forceinline__ void produce_i64(const QK& c, const AttnLDS& L, const int32_t* __restrict__ Tg, int64_t rterm, int sqv,
+                                            int INV, int mypos, int nsteps, int ntile, int w, int lane, int64_t mx, int64_t es) {
+  const double res = 1.0 / (double)es;
+  for (int s = 0; s <= nsteps; ++s) {
+    const int t = AP_PROD * s + w;
+    if (s < nsteps) {
+      v4i pa[3] = {v4i{}, v4i{}, v4i{}};
+      if (t < ntile) {
+        KTile kt;
+        v16i hh, xx, ll;
+        int64_t sc[16];
+        load_ktile(c, 32 * t, kt);
+        mfma_ktile(c, kt, hh, xx, ll);
+        scores_i64(c, 32 * t, hh, xx, ll, rterm, sqv, INV, sc);
+        int p[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const bool ok = 32 * t + 8 * (i >> 2) + 4 * c.half + (i & 3) <= mypos;
+          p[i] = ok ? (int)floordiv_rcp(shl64(lut_exp(Tg, mx - sc[i]), 20), es, res) : 0;
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          int w0, w1, w2;
+          pack_digits(p[4 * g], p[4 * g + 1], p[4 * g + 2], p[4 * g + 3], w0, w1, w2);
+          pa[0][g] = w0;
+          pa[1][g] = w1;
+          pa[2][g] = w2;
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < 3; ++a) L.Pl[s & 1][w][a][lane] = pa[a];
+    }
+    __syncthreads();
+  }
+}
+
+// grid ceil(R / 32) H, block 512 (8 waves): 32 query rows of one head per block, heaviest tiles first.
+// Key tiles of 32. Passes 1 and 2 (row maximum, row sum of exp): wave w takes tiles w, w + 8, ... Pass 3, in
+// steps of 4 tiles: waves 0..3 turn tile 4 s + w into p digits (LDS, double-buffered) while waves 4..7 multiply
+// the previous step's p into V, each for 32 dimensions (a producer and a consumer share each SIMD). NB = V
+// digits; the instantiation whose NB the KV head does not need returns at once (both are launched, so the host
+// need not read the V bit lengths). Scores run in float64 when the block's shifts allow it exactly (and the exp
+// table fits the LDS copy), else in int64.
+template <int NB>
+__global__ __launch_bounds__(512) void k_attn_fused(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
                                                     const int8_t* __restrict__ kdig, const int32_t* __restrict__ ck,
-                                                    const int32_t* __restrict__ skk, const int32_t* __restrict__ skmax,
-                                                    const int8_t* __restrict__ vdig, const int32_t* __restrict__ vbits,
-                                                    const int32_t* __restrict__ pos, const int32_t* __restrict__ Tg,
-                                                    int64_t* __restrict__ out, int32_t* __restrict__ obits, int R, int H, int KV,
-                                                    int nkeys, int kpad, int INV) {
-  __shared__ int32_t T[EXACT_EXP_N];
-  __shared__ v4i Pl[2][4][3][64];
-  __shared__ int64_t red_mx[4][32], red_es[4][32];
+                                                    const int32_t* __restrict__ skk, const int32_t* __restrict__ flags,
+                                                    const int8_t* __restrict__ vdig, const int32_t* __restrict__ pos,
+                                                    const int32_t* __restrict__ Tg, int64_t* __restrict__ out,
+                                                    int32_t* __restrict__ obits, int R, int H, int KV, int nkeys, int kpad,
+                                                    int INV) {
+  __shared__ int32_t T[AP_TN];
+  __shared__ v4i Pl[2][AP_PROD][3][64];
+  __shared__ v4i Qd[8][64];
+  __shared__ double red_w[AP_WAVES][32];
+  __shared__ int64_t red_a[AP_WAVES][32], red_b[AP_WAVES][32];
   __shared__ int rowbits[32];
-  const int h = blockIdx.y, kh = h / (H / KV);
-  if ((vbits[kh] + 2 <= 32 ? 4 : 8) != NB) return;
-  const int q0 = (gridDim.x - 1 - blockIdx.x) * 32;
+  // Work item (query tile, head), heaviest tiles first. Workgroups go round-robin to the 8 XCDs (each with its
+  // own L2), so when KV divides 8, block b works on KV head (b % 8) % KV: each L2 then holds the k and v digits
+  // of one KV head. Item j of a KV head is query tile nqt - 1 - j / hq of head kh hq + j % hq.
+  const int nqt = (R + 31) / 32, hq = H / KV;
+  int kh, j;
+  if (8 % KV == 0) {
+    kh = (blockIdx.x & 7) % KV;
+    j = (blockIdx.x >> 3) * (8 / KV) + (blockIdx.x & 7) / KV;
+  } else {
+    kh = (blockIdx.x % H) / hq;
+    j = (blockIdx.x / H) * hq + (blockIdx.x % H) % hq;
+  }
+  if (j >= nqt * hq) return;   // the grid is rounded up to a multiple of 8
+  const int h = kh * hq + j % hq;
+  // flags: vbits[KV], skmax[KV], exp-table tail nonzero
+  if ((flags[kh] + 2 <= 32 ? 4 : 8) != NB) return;
+  const int q0 = (nqt - 1 - j / hq) * 32;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  for (int i = tid; i < EXACT_EXP_N; i += 256) T[i] = Tg[i];
+  for (int i = tid; i < AP_TN; i += blockDim.x) T[i] = Tg[i];
   if (tid < 32) rowbits[tid] = 0;
   QK c;
   c.l32 = lane & 31;
   c.half = lane >> 5;
+  c.lane = lane;
+  c.qd = &Qd[0][0];
   c.kpad = kpad;
   c.kd = kdig + (int64_t)kh * 2 * 4 * kpad * 32;
   c.ckh = ck + (int64_t)kh * kpad;
@@ -390,47 +620,68 @@ __global__ __launch_bounds__(256) void k_attn_fused(const int16_t* __restrict__ 
   const int jmax = max(0, min(pos[qlast], nkeys - 1));       // positions increase with the row
   const int firstpos = max(0, min(pos[q0], nkeys - 1));
   const int mypos = max(0, min(pos[qr], nkeys - 1));
-  const int ntile = jmax / 32 + 1;
+  const int ntile = jmax / 32 + 1, nsteps = (ntile + AP_PROD - 1) / AP_PROD;
   int sqs = 0;
   {
     const v4i* qp = reinterpret_cast<const v4i*>(qq + ((int64_t)qr * H + h) * AP_HD);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const v4i a0 = qp[(32 * kb + 16 * c.half) / 8], a1 = qp[(32 * kb + 16 * c.half) / 8 + 1];
-      split_digits(a0, a1, c.qh[kb], c.ql[kb]);
+      v4i qh, ql;
+      split_digits(a0, a1, qh, ql);
+      if (w == 0) {   // every wave holds the same rows
+        Qd[2 * kb][lane] = qh;
+        Qd[2 * kb + 1][lane] = ql;
+      }
       sqs += sum16(a0, a1);
     }
   }
   sqs += __shfl_xor(sqs, 32, 64);
+  __syncthreads();
   const int sqv = sq[(int64_t)qr * H + h];
-  const bool fast = wave_max_i32(sqv) + skmax[kh] <= 33 && INV >= 0 && INV < (1 << 14);   // uniform over the block
-  AttnLDS L{T, Pl, red_mx, red_es, rowbits};
-  const int8_t* vd = vdig + (int64_t)kh * 8 * AP_HD * kpad + (int64_t)(32 * w + c.l32) * kpad + 16 * c.half;
+  // uniform over the block: every wave sees the same 32 rows
+  const bool fast = wave_max_i32(sqv) + flags[KV + kh] <= 33 && INV >= 0 && INV < (1 << 14) && flags[2 * KV] == 0;
+  AttnLDS L{T, Pl, red_w, red_a, red_b};
+  const int dc = w - AP_PROD;   // consumer: dimensions 32 dc + [0, 32)
+  const int8_t* vd = vdig + (int64_t)kh * 8 * AP_HD * kpad + (int64_t)(32 * dc + c.l32) * kpad + 16 * c.half;
   const int64_t vplane = (int64_t)AP_HD * kpad;
   v16i acc[NB + 2];
-  if (fast) attn_body<NB, true>(c, L, 128 * (int64_t)sqs, sqv, INV, mypos, ntile, firstpos, vd, vplane, w, lane, acc);
-  else attn_body<NB, false>(c, L, 128 * (int64_t)sqs, sqv, INV, mypos, ntile, firstpos, vd, vplane, w, lane, acc);
-  // C layout: lane holds dimension 32 w + l32 of query rows 8 (i / 4) + 4 half + i % 4
+  if (fast) {
+    FastCtx f{T, __builtin_ldexp((double)INV, sqv - 32), 128 * sqs, mypos};
+    double mx;
+    int64_t es;
+    passes12_f64(c, L, f, ntile, firstpos, w, mx, es);
+    if (w < AP_PROD) produce_f64(c, L, f, nsteps, ntile, firstpos, w, lane, mx, es);
+    else consume<NB>(L, nsteps, ntile, vd, vplane, lane, acc);
+  } else {
+    int64_t mx, es;
+    passes12_i64(c, L, Tg, 128 * (int64_t)sqs, sqv, INV, mypos, ntile, w, mx, es);
+    if (w < AP_PROD) produce_i64(c, L, Tg, 128 * (int64_t)sqs, sqv, INV, mypos, nsteps, ntile, w, lane, mx, es);
+    else consume<NB>(L, nsteps, ntile, vd, vplane, lane, acc);
+  }
+  if (w >= AP_PROD) {
+    // C layout: lane holds dimension 32 dc + l32 of query rows 8 (i / 4) + 4 half + i % 4
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    uint64_t tot = 0;
+    for (int i = 0; i < 16; ++i) {
+      uint64_t tot = 0;
 #pragma unroll
-    for (int k = 0; k < NB + 2; ++k) tot += (uint64_t)shl64((int64_t)acc[k][i], 8 * k);
-    const int row = 8 * (i >> 2) + 4 * c.half + (i & 3);
-    const int64_t o = shr64((int64_t)tot, 20);
-    if (q0 + row < R) out[((int64_t)(q0 + row) * H + h) * AP_HD + 32 * w + c.l32] = o;
-    atomicMax(rowbits + row, bitlen64(abs64(o)));
+      for (int k = 0; k < NB + 2; ++k) tot += (uint64_t)shl64((int64_t)acc[k][i], 8 * k);
+      const int row = 8 * (i >> 2) + 4 * c.half + (i & 3);
+      const int64_t o = shr64((int64_t)tot, 20);
+      if (q0 + row < R) out[((int64_t)(q0 + row) * H + h) * AP_HD + 32 * dc + c.l32] = o;
+      atomicMax(rowbits + row, bitlen64(abs64(o)));
+    }
   }
   __syncthreads();
   if (obits && tid < 32 && q0 + tid < R) obits[(int64_t)(q0 + tid) * H + h] = rowbits[tid];
 }
 
 // workspace layout (bytes, each part 256-aligned): vdig KV*8*hd*kpad, kdig KV*2*hd*kpad, ck and skk KV*kpad*4
-// each, vbits and skmax KV*4 each
+// each, flags (2 KV + 1) int32: vbits, skmax, exp-table tail
 static int64_t al256(int64_t n) { return (n + 255) & ~(int64_t)255; }
 static int64_t ws_bytes(int KV, int kpad) {
   return al256((int64_t)KV * 8 * AP_HD * kpad) + al256((int64_t)KV * 2 * AP_HD * kpad) + 2 * al256((int64_t)KV * kpad * 4) +
-         al256((int64_t)KV * 8);
+         al256((int64_t)(2 * KV + 1) * 4);
 }
 
 }  // namespace exact
@@ -460,15 +711,15 @@ extern "C" int exact_attention_prefill(const int16_t* qq, const int32_t* sq, con
   int32_t* vbits = reinterpret_cast<int32_t*>(reinterpret_cast<int8_t*>(skk) + al256((int64_t)KV * kpad * 4));
   int32_t* skmax = vbits + KV;
   hipStream_t st = as_stream(stream);
-  int e = zero_bytes(vbits, (int64_t)KV * 8, st);
+  int e = zero_bytes(vbits, (int64_t)(2 * KV + 1) * 4, st);
   if (e) return e;
   hipLaunchKernelGGL(k_vdigits, dim3(kpad / 32, KV), dim3(256), 0, st, v, slot, KV, Smax, nkeys, kpad, vdig, vbits);
   hipLaunchKernelGGL(k_kdigits, dim3(kpad / 32, KV), dim3(256), 0, st, kq, sk, slot, KV, Smax, nkeys, kpad, kdig, ck, skk,
-                     skmax);
-  const dim3 grid((R + 31) / 32, H);
-  hipLaunchKernelGGL(k_attn_fused<4>, grid, dim3(256), 0, st, qq, sq, kdig, ck, skk, skmax, vdig, vbits, pos, exp_t, out, obits,
-                     R, H, KV, nkeys, kpad, INV);
-  hipLaunchKernelGGL(k_attn_fused<8>, grid, dim3(256), 0, st, qq, sq, kdig, ck, skk, skmax, vdig, vbits, pos, exp_t, out, obits,
-                     R, H, KV, nkeys, kpad, INV);
+                     skmax, exp_t, vbits + 2 * KV);
+  const dim3 grid(((R + 31) / 32 * H + 7) / 8 * 8);
+  hipLaunchKernelGGL(k_attn_fused<4>, grid, dim3(64 * AP_WAVES), 0, st, qq, sq, kdig, ck, skk, vbits, vdig, pos, exp_t, out, obits, R, H,
+                     KV, nkeys, kpad, INV);
+  hipLaunchKernelGGL(k_attn_fused<8>, grid, dim3(64 * AP_WAVES), 0, st, qq, sq, kdig, ck, skk, vbits, vdig, pos, exp_t, out, obits, R, H,
+                     KV, nkeys, kpad, INV);
   return launch_status("attention_prefill");
 }

@@ -164,6 +164,7 @@ class Workspace:
         self.part_lg = ops.logits_parts(R, V, device)
         self.obits = z(R, H, dt=I32)
         self.ids, self.slot, self.pos = z(R, dt=I32), z(R, dt=I32), z(R, dt=I32)
+        self.seq = None   # (slot, keys) when the rows are one sequence's consecutive positions (prefill)
         if cfg.moe:
             k, P = cfg.topk, R * cfg.topk
             nch = ops.max_chunks(P, cfg.NE, abits)
@@ -193,10 +194,18 @@ class TModel:
         self.nq = (c.H + 2 * c.KV) * c.hd
         self.I = c.I if not c.moe else 1
         self._ws = {}
+        self._pws = None
 
     # ---------------------------------------------------------------- buffers
     def new_cache(self, B=None):
         return Cache(self.cfg, self.batch if B is None else B, self.Smax, self.dev, self.nl)
+
+    PREFILL_MIN_ROWS = 32
+
+    def _prefill_ws(self):
+        if self._pws is None:
+            self._pws = ops.prefill_workspace(self.cfg.KV, self.cfg.hd, self.Smax, self.dev)
+        return self._pws
 
     def workspace(self, R):
         if R not in self._ws:
@@ -240,7 +249,11 @@ class TModel:
                 s_qkv, b_qkv = ws.s28, None
             ops.qkv_rope_cache(ws.t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache, ws.qq, ws.sq, H, KV, hd,
                                clear=group)
-            ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv, ws.obits)
+            if ws.seq is not None:
+                ops.attention_prefill(ws.qq, ws.sq, cache, ws.seq[0], ws.pos, ws.seq[1], tab.exp, ws.att, H, KV, hd, tab.inv,
+                                      self._prefill_ws(), ws.obits)
+            else:
+                ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv, ws.obits)
             ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa)
             if group:
                 self._lin(ws.aq, L["o"], ws.t_o)
@@ -311,7 +324,10 @@ class TModel:
         ws.ids.copy_(torch.tensor(ids, dtype=I32))
         ws.slot.fill_(slot)
         ws.pos.copy_(torch.arange(p0, p0 + T, dtype=I32))
+        # the matrix-core attention for prefill chunks of 32 rows or more (hd 128); the row kernel otherwise
+        ws.seq = (slot, p0 + T) if T >= self.PREFILL_MIN_ROWS and self.cfg.hd == 128 else None
         self.forward_rows(ws)
+        ws.seq = None
         cache.n[slot] = p0 + T
         out = ws.logits.clone()
         return out[-1:] if last_only else out

@@ -62,6 +62,7 @@ CONFIGS = {
     # small models for tests
     "tiny": ModelConfig("tiny", D=256, H=4, KV=2, hd=64, I=384, V=1000, NL=2, theta=1e4),
     "tiny-tied": ModelConfig("tiny-tied", D=128, H=2, KV=1, hd=64, I=256, V=700, NL=2, tie=True),
+    "tiny-hd128": ModelConfig("tiny-hd128", D=256, H=2, KV=1, hd=128, I=384, V=900, NL=2, theta=1e4),
     "tiny-moe": ModelConfig("tiny-moe", D=256, H=4, KV=4, hd=64, I=0, V=800, NL=2, NE=6, topk=2, MI=128, SI=256),
 }
 

@@ -71,6 +71,29 @@ def test_synthetic_prefill_and_decode_match_oracle(name):
         assert tok == otoks[i]
 
 
+def test_chunked_prefill_on_matrix_core_attention_matches_oracle():
+    """hd 128: prompt chunks of 32 rows or more take the matrix-core attention (exact_attention_prefill), here a
+    75-token prompt as one chunk and as chunks of 40 + 35 continuing the cache, then greedy decode steps."""
+    cfg = synth.CONFIGS["tiny-hd128"]
+    seed = 4
+    om = helpers.oracle_model(cfg, seed, T=96)
+    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=96)
+    ids = helpers.prompt(17, 75, cfg.V)
+    want = om(ids)
+    assert np.array_equal(host(tm.forward(ids)), want)
+    cache = tm.new_cache(B=1)
+    lg1 = host(tm.forward(ids[:40], cache))
+    lg2 = host(tm.forward(ids[40:], cache))
+    assert np.array_equal(np.concatenate([lg1, lg2]), want)
+    otoks, orows = O.greedy_decode(om, ids, 4)
+    tok = int(lg2[-1].argmax())
+    assert tok == otoks[0]
+    for i in range(1, 4):
+        lgi, nid = tm.decode_rows([tok], cache)
+        assert np.array_equal(host(lgi)[0], orows[i]), i
+        tok = int(host(nid)[0])
+
+
 def test_batch_decode_and_graph_replay_match_eager():
     cfg = synth.CONFIGS["tiny"]
     seed = 4
