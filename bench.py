@@ -213,7 +213,7 @@ def attention_prefill(args, S=2048, H=28, KV=4, hd=128):
     pos = torch.arange(S, dtype=torch.int32, device=dev)
     out = torch.empty((S, H * hd), dtype=torch.int64, device=dev)
     ref = torch.empty((S, H * hd), dtype=torch.int64, device=dev)
-    ws = ops.prefill_workspace(KV, hd, S, dev)
+    ws = ops.prefill_workspace(S, H, KV, hd, S, dev)
     run_rows = lambda: ops.attention(qq, sq, (kq, sk, v), slot, pos, tab.exp, ref, H, KV, hd, tab.inv)
     run_mfma = lambda: ops.attention_prefill(qq, sq, (kq, sk, v), 0, pos, S, tab.exp, out, H, KV, hd, tab.inv, ws)
     st = torch.cuda.current_stream()

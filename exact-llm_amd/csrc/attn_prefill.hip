@@ -96,7 +96,8 @@ __global__ __launch_bounds__(256) void k_vdigits(const int64_t* __restrict__ v, 
 // Digits of every cached k of the sequence for the q.k product: kdig[(((kh * 2 + p) * 4 + kb) * kpad + j) * 32 + c]
 // = digit p (0: hi, 1: lo - 128) of k[j][32 kb + c]; ck[kh * kpad + j] = 128 sum_d k[j][d] - 16384 hd and
 // skk[kh * kpad + j] = sk[j] (zeros from nkeys on); skmax[kh] = max sk; tnz[0] = 1 if the exp table T has a
-// nonzero entry from AP_TN - 2 on (both zeroed before). grid (kpad / 32, KV), block 256: 8 threads per key.
+// nonzero entry from AP_TN - 2 on, else tnz[1] = 1 + the last nonzero index (all zeroed before). grid
+// (kpad / 32, KV), block 256: 8 threads per key.
 __global__ __launch_bounds__(256) void k_kdigits(const int16_t* __restrict__ kq, const int32_t* __restrict__ sk, int sl, int KV,
                                                  int Smax, int nkeys, int kpad, int8_t* __restrict__ kdig, int32_t* __restrict__ ck,
                                                  int32_t* __restrict__ skk, int32_t* __restrict__ skmax,
@@ -129,9 +130,11 @@ __global__ __launch_bounds__(256) void k_kdigits(const int16_t* __restrict__ kq,
   skv = wave_max_i32(skv);
   if ((tid & 63) == 0) atomicMax(skmax + kh, skv);
   if (blockIdx.x == 0 && blockIdx.y == 0) {   // the fast path keeps exp entries [0, AP_TN) in LDS
-    int nz = 0;
+    int nz = 0, last = 0;
     for (int i = AP_TN - 2 + tid; i < EXACT_EXP_N; i += 256) nz |= T[i] != 0;
+    for (int i = tid; i < AP_TN - 2; i += 256) last = T[i] != 0 ? i + 1 : last;
     if (nz) atomicOr(tnz, 1);
+    atomicMax(tnz + 1, last);
   }
 }
 
@@ -214,14 +217,9 @@ __device__ __forceinline__ double raw_score(int hh, int xx, int llc, double fsca
   return __builtin_ldexp(__builtin_fma((double)m, 256.0, (double)llc) * fscale, skv);
 }
 
-// lut_exp(mx - sc) for mx - sc = dd >= 0: indices past AP_TN - 2 read entry AP_TN - 2 (zero, like every later
-// one), which also covers the reference's cut at 40.0
-__device__ __forceinline__ int exp_lds(const int32_t* T, double dd) {
-  const int di = (int)__builtin_fmin(dd, (double)((AP_TN - 1) * 256 - 1));
-  const int i = di >> 8, fr = di & 255;
-  const int a = T[i], b = T[i + 1];
-  return a - (((a - b) * fr + 128) >> 8);
-}
+// lut_exp(mx - sc) for mx - sc = dd >= 0 (exp16 below), given that T is zero from entry tz on (tz <= AP_TN - 2):
+// indices past tz read entry tz (one address for every such lane, so the LDS read broadcasts), which also covers
+// the reference's cut at 40.0. lim = 256 tz.
 
 // floor(e 2^20 / es) for 0 <= e <= 2^24, es < 2^53: the estimate e * (2^20 / es) is within 2^-31 of the
 // quotient and the remainder (exact in float64) corrects it by one either way
@@ -250,6 +248,7 @@ __device__ __forceinline__ void pack_digits(int p0, int p1, int p2, int p3, int&
 struct FastCtx {
   const int32_t* T;   // LDS exp table
   double fscale;      // INV 2^(sq - 32)
+  double tlim;        // 256 x the index from which the exp table is zero
   int rterm, mypos;
 };
 
@@ -280,14 +279,31 @@ __device__ __forceinline__ double tile_max(const QK& c, const FastCtx& f, int j0
   return mw;
 }
 
+// exp_lds for the 16 elements of a tile with every LDS read issued before the first use
+__device__ __forceinline__ void exp16(const int32_t* T, double mx, const double (&wv)[16], double lim, int (&e)[16]) {
+  int di[16], a[16], b[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) di[i] = (int)__builtin_fmin(mx - __builtin_floor(wv[i] + 0.5), lim);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    a[i] = T[di[i] >> 8];
+    b[i] = T[(di[i] >> 8) + 1];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) e[i] = a[i] - (((a[i] - b[i]) * (di[i] & 255) + 128) >> 8);
+}
+
 template <bool MASK>
 __device__ __forceinline__ int tile_esum(const QK& c, const FastCtx& f, int j0, const KCol& kc, const v16i& hh, const v16i& xx,
                                          const v16i& ll, double mx) {
   double wv[16];
   tile_raw<MASK>(c, f, j0, kc, hh, xx, ll, wv);
+  int e[16];
+  exp16(f.T, mx, wv, f.tlim, e);
   int part = 0;   // 16 terms <= 2^24
 #pragma unroll
-  for (int i = 0; i < 16; ++i) part += exp_lds(f.T, mx - __builtin_floor(wv[i] + 0.5));
+  for (int i = 0; i < 16; ++i) part += e[i];
   return part;
 }
 
@@ -297,8 +313,9 @@ __device__ __forceinline__ void tile_pdig(const QK& c, const FastCtx& f, int j0,
   double wv[16];
   tile_raw<MASK>(c, f, j0, kc, hh, xx, ll, wv);
   int p[16];
+  exp16(f.T, mx, wv, f.tlim, p);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) p[i] = pdiv_f64(exp_lds(f.T, mx - __builtin_floor(wv[i] + 0.5)), esd, res20);
+  for (int i = 0; i < 16; ++i) p[i] = pdiv_f64(p[i], esd, res20);
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
         int w0, w1, w2;
@@ -325,38 +342,23 @@ __device__ __forceinline__ void scores_i64(const QK& c, int j0, const v16i& hh, 
   }
 }
 
-#define AP_WAVES 8     // waves per block
-#define AP_PROD 4      // waves 0..3 produce p digits in the third pass, waves 4..7 multiply them into V
+#define AP_PROD 4      // the p.v kernel: waves 0..3 produce p digits, waves 4..7 multiply them into V
+#define AP_CONS 4
+#define AP_SW 4        // waves of the statistics kernel
 
 struct AttnLDS {
   int32_t* T;
   v4i (*Pl)[AP_PROD][3][64];
-  double (*red_w)[32];
-  int64_t (*red_a)[32];
-  int64_t (*red_b)[32];
+  double* red_w;      // [waves][32]
+  int64_t* red_a;     // [waves][32]
+  int64_t* red_b;     // [waves][32]
 };
 
-// Consumer side of the third pass: p . v of one step (AP_PROD tiles of p digits in LDS) into the shift classes.
-// vb holds the step's V digits (loaded by the caller one step ahead when NB = 4).
+// Consumer loop of the third pass: iteration s multiplies step s - 1 (the producers fill step s meanwhile).
+// NB = 4 holds the V digits of a whole step and loads the next step's while this one's products run; NB = 8
+// (no registers for that) loads one tile ahead.
 template <int NB>
-__device__ __forceinline__ void pv_mfma(const AttnLDS& L, int buf, int tiles, int lane, const v4i (&vb)[AP_PROD][NB],
-                                        v16i (&acc)[NB + 2]) {
-#pragma unroll
-  for (int tt = 0; tt < AP_PROD; ++tt) {
-    if (tt < tiles) {
-      v4i pv[3];
-#pragma unroll
-      for (int a = 0; a < 3; ++a) pv[a] = L.Pl[buf][tt][a][lane];
-#pragma unroll
-      for (int a = 0; a < 3; ++a)
-#pragma unroll
-        for (int b = 0; b < NB; ++b) acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pv[a], vb[tt][b], acc[a + b], 0, 0, 0);
-    }
-  }
-}
-
-template <int NB>
-__device__ __forceinline__ void load_v(const int8_t* __restrict__ vd, int64_t vplane, int s, int ntile, v4i (&vb)[AP_PROD][NB]) {
+__device__ __forceinline__ void load_v_step(const int8_t* __restrict__ vd, int64_t vplane, int s, int ntile, v4i (&vb)[AP_PROD][NB]) {
 #pragma unroll
   for (int tt = 0; tt < AP_PROD; ++tt) {
     const int t = AP_PROD * s + tt < ntile ? AP_PROD * s + tt : ntile - 1;   // stays inside the written keys
@@ -365,8 +367,6 @@ __device__ __forceinline__ void load_v(const int8_t* __restrict__ vd, int64_t vp
   }
 }
 
-// Consumer loop of the third pass: iteration s multiplies step s - 1 (the producers fill step s meanwhile).
-// NB = 4 loads the V digits one step ahead; NB = 8 (no registers to spare) loads them tile by tile.
 template <int NB>
 __device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile, const int8_t* __restrict__ vd, int64_t vplane,
                                         int lane, v16i (&acc)[NB + 2]) {
@@ -374,27 +374,54 @@ __device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile,
   for (int k = 0; k < NB + 2; ++k) acc[k] = v16i{};
   if constexpr (NB == 4) {
     v4i vb[AP_PROD][NB];
-    load_v<NB>(vd, vplane, 0, ntile, vb);
+    load_v_step<NB>(vd, vplane, 0, ntile, vb);
     for (int s = 0; s <= nsteps; ++s) {
-      if (s >= 1) pv_mfma<NB>(L, (s - 1) & 1, min(AP_PROD, ntile - AP_PROD * (s - 1)), lane, vb, acc);
-      if (s < nsteps) load_v<NB>(vd, vplane, s, ntile, vb);
+      if (s >= 1) {
+        const int buf = (s - 1) & 1, tiles = min(AP_PROD, ntile - AP_PROD * (s - 1));
+        v4i cur[AP_PROD][NB];
+#pragma unroll
+        for (int tt = 0; tt < AP_PROD; ++tt)
+#pragma unroll
+          for (int b = 0; b < NB; ++b) cur[tt][b] = vb[tt][b];
+        if (s < nsteps) load_v_step<NB>(vd, vplane, s, ntile, vb);
+#pragma unroll
+        for (int tt = 0; tt < AP_PROD; ++tt) {
+          if (tt < tiles) {
+            v4i pv[3];
+#pragma unroll
+            for (int a = 0; a < 3; ++a) pv[a] = L.Pl[buf][tt][a][lane];
+#pragma unroll
+            for (int a = 0; a < 3; ++a)
+#pragma unroll
+              for (int b = 0; b < NB; ++b) acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pv[a], cur[tt][b], acc[a + b], 0, 0, 0);
+          }
+        }
+      }
       __syncthreads();
     }
   } else {
+    v4i vb[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) vb[b] = *reinterpret_cast<const v4i*>(vd + b * vplane);
     for (int s = 0; s <= nsteps; ++s) {
       if (s >= 1) {
         const int buf = (s - 1) & 1;
+#pragma unroll 1
         for (int tt = 0; tt < AP_PROD && AP_PROD * (s - 1) + tt < ntile; ++tt) {
           const int t = AP_PROD * (s - 1) + tt;
-          v4i pv[3], vb[NB];
+          v4i pv[3], cur[NB];
 #pragma unroll
-          for (int b = 0; b < NB; ++b) vb[b] = *reinterpret_cast<const v4i*>(vd + b * vplane + 32 * t);
+          for (int b = 0; b < NB; ++b) cur[b] = vb[b];
+          const int tn = t + 1 < ntile ? t + 1 : t;
+#pragma unroll
+          for (int b = 0; b < NB; ++b) vb[b] = *reinterpret_cast<const v4i*>(vd + b * vplane + 32 * tn);
 #pragma unroll
           for (int a = 0; a < 3; ++a) pv[a] = L.Pl[buf][tt][a][lane];
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int a = 0; a < 3; ++a)
 #pragma unroll
-            for (int b = 0; b < NB; ++b) acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pv[a], vb[b], acc[a + b], 0, 0, 0);
+            for (int b = 0; b < NB; ++b) acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pv[a], cur[b], acc[a + b], 0, 0, 0);
         }
       }
       __syncthreads();
@@ -402,57 +429,50 @@ __device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile,
   }
 }
 
-// Passes 1 and 2 for the float64 path: wave w takes tiles w, w + 8, ... (k digits of the next tile loaded while
-// this one is finished); returns the row maximum score and the row sum of exp.
+// Passes 1 and 2 for the float64 path: wave w of NW takes tiles w, w + NW, ...; the row maximum score and the
+// row sum of exp. The per-key terms come in with each group of 4 keys (the statistics kernel runs 4 waves per
+// SIMD, which hide the loads).
+template <int NW>
 __device__ __forceinline__ void passes12_f64(const QK& c, const AttnLDS& L, const FastCtx& f, int ntile, int firstpos, int w,
                                              double& mx, int64_t& es) {
-  KTile kt;
-  KCol kc;
   double mw = AP_NEG;
-  if (w < ntile) {
-    load_ktile(c, 32 * w, kt);
-    load_kcol(c, 32 * w, kc);
-  }
-  for (int t = w; t < ntile; t += AP_WAVES) {
+  for (int t = w; t < ntile; t += NW) {
+    KTile kt;
+    KCol kc;
     v16i hh, xx, ll;
+    load_ktile(c, 32 * t, kt);
+    load_kcol(c, 32 * t, kc);
+    __builtin_amdgcn_sched_barrier(0);   // every load of the tile in flight before the first use
     mfma_ktile(c, kt, hh, xx, ll);
-    const KCol cur = kc;
-    if (t + AP_WAVES < ntile) {
-      load_ktile(c, 32 * (t + AP_WAVES), kt);
-      load_kcol(c, 32 * (t + AP_WAVES), kc);
-    }
-    mw = 32 * t + 31 <= firstpos ? tile_max<false>(c, f, 32 * t, cur, hh, xx, ll, mw) : tile_max<true>(c, f, 32 * t, cur, hh, xx, ll, mw);
+    mw = 32 * t + 31 <= firstpos ? tile_max<false>(c, f, 32 * t, kc, hh, xx, ll, mw) : tile_max<true>(c, f, 32 * t, kc, hh, xx, ll, mw);
   }
-  mw = __builtin_fmax(mw, __shfl_xor(mw, 32, 64));
-  if (c.half == 0) L.red_w[w][c.l32] = mw;
+  mw = max_f64(mw, __shfl_xor(mw, 32, 64));
+  if (c.half == 0) L.red_w[w * 32 + c.l32] = mw;
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < AP_WAVES; ++k) mw = __builtin_fmax(mw, L.red_w[k][c.l32]);
+  for (int k = 0; k < NW; ++k) mw = max_f64(mw, L.red_w[k * 32 + c.l32]);
   mx = __builtin_floor(mw + 0.5);
   int64_t e = 0;
-  if (w < ntile) {
-    load_ktile(c, 32 * w, kt);
-    load_kcol(c, 32 * w, kc);
-  }
-  for (int t = w; t < ntile; t += AP_WAVES) {
+  for (int t = w; t < ntile; t += NW) {
+    KTile kt;
+    KCol kc;
     v16i hh, xx, ll;
+    load_ktile(c, 32 * t, kt);
+    load_kcol(c, 32 * t, kc);
+    __builtin_amdgcn_sched_barrier(0);
     mfma_ktile(c, kt, hh, xx, ll);
-    const KCol cur = kc;
-    if (t + AP_WAVES < ntile) {
-      load_ktile(c, 32 * (t + AP_WAVES), kt);
-      load_kcol(c, 32 * (t + AP_WAVES), kc);
-    }
-    e += 32 * t + 31 <= firstpos ? tile_esum<false>(c, f, 32 * t, cur, hh, xx, ll, mx) : tile_esum<true>(c, f, 32 * t, cur, hh, xx, ll, mx);
+    e += 32 * t + 31 <= firstpos ? tile_esum<false>(c, f, 32 * t, kc, hh, xx, ll, mx) : tile_esum<true>(c, f, 32 * t, kc, hh, xx, ll, mx);
   }
   e += __shfl_xor(e, 32, 64);
-  if (c.half == 0) L.red_a[w][c.l32] = e;
+  if (c.half == 0) L.red_a[w * 32 + c.l32] = e;
   __syncthreads();
   es = 0;
 #pragma unroll
-  for (int k = 0; k < AP_WAVES; ++k) es += L.red_a[k][c.l32];
+  for (int k = 0; k < NW; ++k) es += L.red_a[k * 32 + c.l32];
 }
 
-// Producer loop of the third pass (float64 path): iteration s turns tile AP_PROD s + w into p digits.
+// Producer loop of the third pass (float64 path): iteration s turns tile AP_PROD s + w into p digits; the next
+// tile's k digits and key terms load while this one is finished.
 __device__ __forceinline__ void produce_f64(const QK& c, const AttnLDS& L, const FastCtx& f, int nsteps, int ntile, int firstpos,
                                             int w, int lane, double mx, int64_t es) {
   const double esd = (double)es, res20 = 1048576.0 / esd;   // 2^20 / es: the reciprocal scaled exactly
@@ -474,6 +494,7 @@ __device__ __forceinline__ void produce_f64(const QK& c, const AttnLDS& L, const
           load_ktile(c, 32 * (t + AP_PROD), kt);
           load_kcol(c, 32 * (t + AP_PROD), kc);
         }
+        __builtin_amdgcn_sched_barrier(0);   // the next tile's loads in flight before this tile's epilogue
         if (32 * t + 31 <= firstpos) tile_pdig<false>(c, f, 32 * t, cur, hh, xx, ll, mx, esd, res20, pa);
         else tile_pdig<true>(c, f, 32 * t, cur, hh, xx, ll, mx, esd, res20, pa);
       }
@@ -485,11 +506,12 @@ __device__ __forceinline__ void produce_f64(const QK& c, const AttnLDS& L, const
 }
 
 // The int64 path (any shifts, any exp table): shr64 and lut_exp as the reference, exp table in global memory.
+template <int NW>
 __device__ __forceinline__ void passes12_i64(const QK& c, const AttnLDS& L, const int32_t* __restrict__ Tg, int64_t rterm, int sqv,
                                              int INV, int mypos, int ntile, int w, int64_t& mx, int64_t& es) {
   auto valid = [&](int t, int i) { return 32 * t + 8 * (i >> 2) + 4 * c.half + (i & 3) <= mypos; };
   int64_t m = INT64_MIN;
-  for (int t = w; t < ntile; t += AP_WAVES) {
+  for (int t = w; t < ntile; t += NW) {
     KTile kt;
     v16i hh, xx, ll;
     int64_t sc[16];
@@ -504,13 +526,13 @@ __device__ __forceinline__ void passes12_i64(const QK& c, const AttnLDS& L, cons
     const int64_t o = __shfl_xor(m, 32, 64);
     m = o > m ? o : m;
   }
-  if (c.half == 0) L.red_a[w][c.l32] = m;
+  if (c.half == 0) L.red_a[w * 32 + c.l32] = m;
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < AP_WAVES; ++k) m = L.red_a[k][c.l32] > m ? L.red_a[k][c.l32] : m;
+  for (int k = 0; k < NW; ++k) m = L.red_a[k * 32 + c.l32] > m ? L.red_a[k * 32 + c.l32] : m;
   mx = m;
   int64_t e = 0;
-  for (int t = w; t < ntile; t += AP_WAVES) {
+  for (int t = w; t < ntile; t += NW) {
     KTile kt;
     v16i hh, xx, ll;
     int64_t sc[16];
@@ -522,11 +544,11 @@ __device__ __forceinline__ void passes12_i64(const QK& c, const AttnLDS& L, cons
       if (valid(t, i)) e += lut_exp(Tg, mx - sc[i]);
   }
   e += __shfl_xor(e, 32, 64);
-  if (c.half == 0) L.red_b[w][c.l32] = e;
+  if (c.half == 0) L.red_b[w * 32 + c.l32] = e;
   __syncthreads();
   es = 0;
 #pragma unroll
-  for (int k = 0; k < AP_WAVES; ++k) es += L.red_b[k][c.l32];
+  for (int k = 0; k < NW; ++k) es += L.red_b[k * 32 + c.l32];
 }
 
 __device__ __forceinline__ void produce_i64(const QK& c, const AttnLDS& L, const int32_t* __restrict__ Tg, int64_t rterm, int sqv,
@@ -565,32 +587,20 @@ __device__ __forceinline__ void produce_i64(const QK& c, const AttnLDS& L, const
   }
 }
 
-// grid ceil(R / 32) H, block 512 (8 waves): 32 query rows of one head per block, heaviest tiles first.
-// Key tiles of 32. Passes 1 and 2 (row maximum, row sum of exp): wave w takes tiles w, w + 8, ... Pass 3, in
-// steps of 4 tiles: waves 0..3 turn tile 4 s + w into p digits (LDS, double-buffered) while waves 4..7 multiply
-// the previous step's p into V, each for 32 dimensions (a producer and a consumer share each SIMD). NB = V
-// digits; the instantiation whose NB the KV head does not need returns at once (both are launched, so the host
-// need not read the V bit lengths). Scores run in float64 when the block's shifts allow it exactly (and the exp
-// table fits the LDS copy), else in int64.
-template <int NB>
-__global__ __launch_bounds__(512) void k_attn_fused(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
-                                                    const int8_t* __restrict__ kdig, const int32_t* __restrict__ ck,
-                                                    const int32_t* __restrict__ skk, const int32_t* __restrict__ flags,
-                                                    const int8_t* __restrict__ vdig, const int32_t* __restrict__ pos,
-                                                    const int32_t* __restrict__ Tg, int64_t* __restrict__ out,
-                                                    int32_t* __restrict__ obits, int R, int H, int KV, int nkeys, int kpad,
-                                                    int INV) {
-  __shared__ int32_t T[AP_TN];
-  __shared__ v4i Pl[2][AP_PROD][3][64];
-  __shared__ v4i Qd[8][64];
-  __shared__ double red_w[AP_WAVES][32];
-  __shared__ int64_t red_a[AP_WAVES][32], red_b[AP_WAVES][32];
-  __shared__ int rowbits[32];
-  // Work item (query tile, head), heaviest tiles first. Workgroups go round-robin to the 8 XCDs (each with its
-  // own L2), so when KV divides 8, block b works on KV head (b % 8) % KV: each L2 then holds the k and v digits
-  // of one KV head. Item j of a KV head is query tile nqt - 1 - j / hq of head kh hq + j % hq.
+// What a block (32 query rows of one head) knows after set-up, in both kernels.
+struct Block {
+  QK c;
+  int h, kh, q0, mypos, firstpos, ntile, sqs, sqv;
+  bool fast;
+};
+
+// Work item (query tile, head), heaviest tiles first. Workgroups go round-robin to the 8 XCDs (each with its own
+// L2), so when KV divides 8, block b works on KV head (b % 8) % KV: each L2 then holds the k and v digits of one
+// KV head. Item j of a KV head is query tile nqt - 1 - j / hq of head kh hq + j % hq. Returns false for the
+// blocks past the work (the grid is rounded up to a multiple of 8).
+__device__ __forceinline__ bool block_item(int R, int H, int KV, int& h, int& kh, int& q0) {
   const int nqt = (R + 31) / 32, hq = H / KV;
-  int kh, j;
+  int j;
   if (8 % KV == 0) {
     kh = (blockIdx.x & 7) % KV;
     j = (blockIdx.x >> 3) * (8 / KV) + (blockIdx.x & 7) / KV;
@@ -598,15 +608,26 @@ __global__ __launch_bounds__(512) void k_attn_fused(const int16_t* __restrict__ 
     kh = (blockIdx.x % H) / hq;
     j = (blockIdx.x / H) * hq + (blockIdx.x % H) % hq;
   }
-  if (j >= nqt * hq) return;   // the grid is rounded up to a multiple of 8
-  const int h = kh * hq + j % hq;
-  // flags: vbits[KV], skmax[KV], exp-table tail nonzero
-  if ((flags[kh] + 2 <= 32 ? 4 : 8) != NB) return;
-  const int q0 = (nqt - 1 - j / hq) * 32;
+  if (j >= nqt * hq) return false;
+  h = kh * hq + j % hq;
+  q0 = (nqt - 1 - j / hq) * 32;
+  return true;
+}
+
+// Loads the exp table and the q digits into LDS (ends with a barrier) and fills b. flags: vbits[KV], skmax[KV],
+// exp-table tail nonzero. The float64 decision depends only on the block's rows, so both kernels agree.
+__device__ __forceinline__ void block_setup(Block& b, int h, int kh, int q0, const int16_t* __restrict__ qq,
+                                            const int32_t* __restrict__ sq, const int8_t* __restrict__ kdig,
+                                            const int32_t* __restrict__ ck, const int32_t* __restrict__ skk,
+                                            const int32_t* __restrict__ flags, const int32_t* __restrict__ pos,
+                                            const int32_t* __restrict__ Tg, int32_t* T, v4i (*Qd)[64], int R, int H, int KV,
+                                            int nkeys, int kpad, int INV) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   for (int i = tid; i < AP_TN; i += blockDim.x) T[i] = Tg[i];
-  if (tid < 32) rowbits[tid] = 0;
-  QK c;
+  b.h = h;
+  b.kh = kh;
+  b.q0 = q0;
+  QK& c = b.c;
   c.l32 = lane & 31;
   c.half = lane >> 5;
   c.lane = lane;
@@ -618,79 +639,135 @@ __global__ __launch_bounds__(512) void k_attn_fused(const int16_t* __restrict__ 
   const int qr = q0 + c.l32 < R ? q0 + c.l32 : R - 1;
   const int qlast = q0 + 31 < R ? q0 + 31 : R - 1;
   const int jmax = max(0, min(pos[qlast], nkeys - 1));       // positions increase with the row
-  const int firstpos = max(0, min(pos[q0], nkeys - 1));
-  const int mypos = max(0, min(pos[qr], nkeys - 1));
-  const int ntile = jmax / 32 + 1, nsteps = (ntile + AP_PROD - 1) / AP_PROD;
+  b.firstpos = max(0, min(pos[q0], nkeys - 1));
+  b.mypos = max(0, min(pos[qr], nkeys - 1));
+  b.ntile = jmax / 32 + 1;
   int sqs = 0;
-  {
-    const v4i* qp = reinterpret_cast<const v4i*>(qq + ((int64_t)qr * H + h) * AP_HD);
+  const v4i* qp = reinterpret_cast<const v4i*>(qq + ((int64_t)qr * H + h) * AP_HD);
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const v4i a0 = qp[(32 * kb + 16 * c.half) / 8], a1 = qp[(32 * kb + 16 * c.half) / 8 + 1];
-      v4i qh, ql;
-      split_digits(a0, a1, qh, ql);
-      if (w == 0) {   // every wave holds the same rows
-        Qd[2 * kb][lane] = qh;
-        Qd[2 * kb + 1][lane] = ql;
-      }
-      sqs += sum16(a0, a1);
+  for (int kb = 0; kb < 4; ++kb) {
+    const v4i a0 = qp[(32 * kb + 16 * c.half) / 8], a1 = qp[(32 * kb + 16 * c.half) / 8 + 1];
+    v4i qh, ql;
+    split_digits(a0, a1, qh, ql);
+    if (w == 0) {   // every wave holds the same rows
+      Qd[2 * kb][lane] = qh;
+      Qd[2 * kb + 1][lane] = ql;
     }
+    sqs += sum16(a0, a1);
   }
-  sqs += __shfl_xor(sqs, 32, 64);
-  __syncthreads();
-  const int sqv = sq[(int64_t)qr * H + h];
+  b.sqs = sqs + __shfl_xor(sqs, 32, 64);
+  b.sqv = sq[(int64_t)qr * H + h];
   // uniform over the block: every wave sees the same 32 rows
-  const bool fast = wave_max_i32(sqv) + flags[KV + kh] <= 33 && INV >= 0 && INV < (1 << 14) && flags[2 * KV] == 0;
-  AttnLDS L{T, Pl, red_w, red_a, red_b};
+  b.fast = wave_max_i32(b.sqv) + flags[KV + kh] <= 33 && INV >= 0 && INV < (1 << 14) && flags[2 * KV] == 0;
+  __syncthreads();
+}
+
+// Passes 1 and 2 (row maximum score, row sum of exp). grid as k_attn_pv, block 64 AP_SW. st_mx / st_es: [H][R]
+// int64 (the float64 path stores its exact integer maximum as an int64 too).
+__global__ __launch_bounds__(64 * AP_SW, 3) void k_attn_stats(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
+                                                              const int8_t* __restrict__ kdig, const int32_t* __restrict__ ck,
+                                                              const int32_t* __restrict__ skk, const int32_t* __restrict__ flags,
+                                                              const int32_t* __restrict__ pos, const int32_t* __restrict__ Tg,
+                                                              int64_t* __restrict__ st_mx, int64_t* __restrict__ st_es, int R,
+                                                              int H, int KV, int nkeys, int kpad, int INV) {
+  __shared__ int32_t T[AP_TN];
+  __shared__ v4i Qd[8][64];
+  __shared__ double red_w[AP_SW * 32];
+  __shared__ int64_t red_a[AP_SW * 32], red_b[AP_SW * 32];
+  int h, kh, q0;
+  if (!block_item(R, H, KV, h, kh, q0)) return;
+  Block b;
+  block_setup(b, h, kh, q0, qq, sq, kdig, ck, skk, flags, pos, Tg, T, Qd, R, H, KV, nkeys, kpad, INV);
+  const int w = threadIdx.x >> 6;
+  AttnLDS L{T, nullptr, red_w, red_a, red_b};
+  int64_t mx, es;
+  if (b.fast) {
+    const FastCtx f{T, __builtin_ldexp((double)INV, b.sqv - 32), 256.0 * flags[2 * KV + 1], 128 * b.sqs, b.mypos};
+    double m;
+    passes12_f64<AP_SW>(b.c, L, f, b.ntile, b.firstpos, w, m, es);
+    mx = (int64_t)m;
+  } else {
+    passes12_i64<AP_SW>(b.c, L, Tg, 128 * (int64_t)b.sqs, b.sqv, INV, b.mypos, b.ntile, w, mx, es);
+  }
+  const int row = q0 + b.c.l32;
+  if (w == 0 && b.c.half == 0 && row < R) {
+    st_mx[(int64_t)h * R + row] = mx;
+    st_es[(int64_t)h * R + row] = es;
+  }
+}
+
+// Pass 3. grid ceil(R / 32) H rounded up to a multiple of 8, block 512 (8 waves): 32 query rows of one head per
+// block, heaviest tiles first. In steps of 4 key tiles of 32, waves 0..3 turn tile 4 s + w into p digits (LDS,
+// double-buffered) while waves 4..7 multiply the previous step's p into V, each for 32 dimensions (a producer
+// and a consumer share each SIMD). NB = V digits; the instantiation whose NB the KV head does not need returns at
+// once (both are launched, so the host need not read the V bit lengths).
+template <int NB>
+__global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
+                                                 const int8_t* __restrict__ kdig, const int32_t* __restrict__ ck,
+                                                 const int32_t* __restrict__ skk, const int32_t* __restrict__ flags,
+                                                 const int8_t* __restrict__ vdig, const int32_t* __restrict__ pos,
+                                                 const int32_t* __restrict__ Tg, const int64_t* __restrict__ st_mx,
+                                                 const int64_t* __restrict__ st_es, int64_t* __restrict__ out,
+                                                 int32_t* __restrict__ obits, int R, int H, int KV, int nkeys, int kpad,
+                                                 int INV) {
+  __shared__ int32_t T[AP_TN];
+  __shared__ v4i Pl[2][AP_PROD][3][64];
+  __shared__ v4i Qd[8][64];
+  __shared__ int rowbits[32];
+  int h, kh, q0;
+  if (!block_item(R, H, KV, h, kh, q0)) return;
+  if ((flags[kh] + 2 <= 32 ? 4 : 8) != NB) return;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  if (tid < 32) rowbits[tid] = 0;
+  Block b;
+  block_setup(b, h, kh, q0, qq, sq, kdig, ck, skk, flags, pos, Tg, T, Qd, R, H, KV, nkeys, kpad, INV);
+  const QK& c = b.c;
+  const int row = q0 + c.l32 < R ? q0 + c.l32 : R - 1;
+  const int64_t mx = st_mx[(int64_t)h * R + row], es = st_es[(int64_t)h * R + row];
+  AttnLDS L{T, Pl, nullptr, nullptr, nullptr};
+  const int nsteps = (b.ntile + AP_PROD - 1) / AP_PROD;
   const int dc = w - AP_PROD;   // consumer: dimensions 32 dc + [0, 32)
   const int8_t* vd = vdig + (int64_t)kh * 8 * AP_HD * kpad + (int64_t)(32 * dc + c.l32) * kpad + 16 * c.half;
   const int64_t vplane = (int64_t)AP_HD * kpad;
-  v16i acc[NB + 2];
-  if (fast) {
-    FastCtx f{T, __builtin_ldexp((double)INV, sqv - 32), 128 * sqs, mypos};
-    double mx;
-    int64_t es;
-    passes12_f64(c, L, f, ntile, firstpos, w, mx, es);
-    if (w < AP_PROD) produce_f64(c, L, f, nsteps, ntile, firstpos, w, lane, mx, es);
-    else consume<NB>(L, nsteps, ntile, vd, vplane, lane, acc);
-  } else {
-    int64_t mx, es;
-    passes12_i64(c, L, Tg, 128 * (int64_t)sqs, sqv, INV, mypos, ntile, w, mx, es);
-    if (w < AP_PROD) produce_i64(c, L, Tg, 128 * (int64_t)sqs, sqv, INV, mypos, nsteps, ntile, w, lane, mx, es);
-    else consume<NB>(L, nsteps, ntile, vd, vplane, lane, acc);
-  }
   if (w >= AP_PROD) {
+    v16i acc[NB + 2];
+    consume<NB>(L, nsteps, b.ntile, vd, vplane, lane, acc);
     // C layout: lane holds dimension 32 dc + l32 of query rows 8 (i / 4) + 4 half + i % 4
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       uint64_t tot = 0;
 #pragma unroll
       for (int k = 0; k < NB + 2; ++k) tot += (uint64_t)shl64((int64_t)acc[k][i], 8 * k);
-      const int row = 8 * (i >> 2) + 4 * c.half + (i & 3);
+      const int r = 8 * (i >> 2) + 4 * c.half + (i & 3);
       const int64_t o = shr64((int64_t)tot, 20);
-      if (q0 + row < R) out[((int64_t)(q0 + row) * H + h) * AP_HD + 32 * dc + c.l32] = o;
-      atomicMax(rowbits + row, bitlen64(abs64(o)));
+      if (q0 + r < R) out[((int64_t)(q0 + r) * H + h) * AP_HD + 32 * dc + c.l32] = o;
+      atomicMax(rowbits + r, bitlen64(abs64(o)));
     }
+  } else if (b.fast) {
+    const FastCtx f{T, __builtin_ldexp((double)INV, b.sqv - 32), 256.0 * flags[2 * KV + 1], 128 * b.sqs, b.mypos};
+    produce_f64(c, L, f, nsteps, b.ntile, b.firstpos, w, lane, (double)mx, es);
+  } else {
+    produce_i64(c, L, Tg, 128 * (int64_t)b.sqs, b.sqv, INV, b.mypos, nsteps, b.ntile, w, lane, mx, es);
   }
   __syncthreads();
   if (obits && tid < 32 && q0 + tid < R) obits[(int64_t)(q0 + tid) * H + h] = rowbits[tid];
 }
 
 // workspace layout (bytes, each part 256-aligned): vdig KV*8*hd*kpad, kdig KV*2*hd*kpad, ck and skk KV*kpad*4
-// each, flags (2 KV + 1) int32: vbits, skmax, exp-table tail
+// each, flags (2 KV + 2) int32: vbits, skmax, exp-table tail, exp-table zero index; row maxima and sums H*R*8 each
 static int64_t al256(int64_t n) { return (n + 255) & ~(int64_t)255; }
-static int64_t ws_bytes(int KV, int kpad) {
+static int64_t ws_bytes(int R, int H, int KV, int kpad) {
   return al256((int64_t)KV * 8 * AP_HD * kpad) + al256((int64_t)KV * 2 * AP_HD * kpad) + 2 * al256((int64_t)KV * kpad * 4) +
-         al256((int64_t)(2 * KV + 1) * 4);
+         al256((int64_t)(2 * KV + 2) * 4) + 2 * al256((int64_t)H * R * 8);
 }
 
 }  // namespace exact
 
 using namespace exact;
 
-extern "C" int64_t exact_attention_prefill_workspace(int32_t KV, int32_t hd, int32_t nkeys) {
-  if (KV <= 0 || hd != AP_HD || nkeys <= 0) return -1;
-  return ws_bytes(KV, (nkeys + 31) / 32 * 32);
+extern "C" int64_t exact_attention_prefill_workspace(int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t nkeys) {
+  if (R <= 0 || H <= 0 || KV <= 0 || hd != AP_HD || nkeys <= 0) return -1;
+  return ws_bytes(R, H, KV, (nkeys + 31) / 32 * 32);
 }
 
 extern "C" int exact_attention_prefill(const int16_t* qq, const int32_t* sq, const int16_t* kq, const int32_t* sk,
@@ -702,24 +779,26 @@ extern "C" int exact_attention_prefill(const int16_t* qq, const int32_t* sq, con
   // per shift class, 3 digit pairs x nkeys products of |.| <= 2^14 stay below 2^31
   if (hd != AP_HD || nkeys > 32768) return EXACT_E_UNSUPPORTED;
   const int kpad = (nkeys + 31) / 32 * 32;
-  if (work_bytes < ws_bytes(KV, kpad) || (reinterpret_cast<uintptr_t>(work) & 255)) return EXACT_E_ARG;
-  int8_t* base = static_cast<int8_t*>(work);
-  int8_t* vdig = base;
+  if (work_bytes < ws_bytes(R, H, KV, kpad) || (reinterpret_cast<uintptr_t>(work) & 255)) return EXACT_E_ARG;
+  int8_t* vdig = static_cast<int8_t*>(work);
   int8_t* kdig = vdig + al256((int64_t)KV * 8 * AP_HD * kpad);
   int32_t* ck = reinterpret_cast<int32_t*>(kdig + al256((int64_t)KV * 2 * AP_HD * kpad));
   int32_t* skk = reinterpret_cast<int32_t*>(reinterpret_cast<int8_t*>(ck) + al256((int64_t)KV * kpad * 4));
-  int32_t* vbits = reinterpret_cast<int32_t*>(reinterpret_cast<int8_t*>(skk) + al256((int64_t)KV * kpad * 4));
-  int32_t* skmax = vbits + KV;
+  int32_t* flags = reinterpret_cast<int32_t*>(reinterpret_cast<int8_t*>(skk) + al256((int64_t)KV * kpad * 4));
+  int64_t* st_mx = reinterpret_cast<int64_t*>(reinterpret_cast<int8_t*>(flags) + al256((int64_t)(2 * KV + 2) * 4));
+  int64_t* st_es = reinterpret_cast<int64_t*>(reinterpret_cast<int8_t*>(st_mx) + al256((int64_t)H * R * 8));
   hipStream_t st = as_stream(stream);
-  int e = zero_bytes(vbits, (int64_t)(2 * KV + 1) * 4, st);
+  int e = zero_bytes(flags, (int64_t)(2 * KV + 2) * 4, st);
   if (e) return e;
-  hipLaunchKernelGGL(k_vdigits, dim3(kpad / 32, KV), dim3(256), 0, st, v, slot, KV, Smax, nkeys, kpad, vdig, vbits);
+  hipLaunchKernelGGL(k_vdigits, dim3(kpad / 32, KV), dim3(256), 0, st, v, slot, KV, Smax, nkeys, kpad, vdig, flags);
   hipLaunchKernelGGL(k_kdigits, dim3(kpad / 32, KV), dim3(256), 0, st, kq, sk, slot, KV, Smax, nkeys, kpad, kdig, ck, skk,
-                     skmax, exp_t, vbits + 2 * KV);
+                     flags + KV, exp_t, flags + 2 * KV);
   const dim3 grid(((R + 31) / 32 * H + 7) / 8 * 8);
-  hipLaunchKernelGGL(k_attn_fused<4>, grid, dim3(64 * AP_WAVES), 0, st, qq, sq, kdig, ck, skk, vbits, vdig, pos, exp_t, out, obits, R, H,
+  hipLaunchKernelGGL(k_attn_stats, grid, dim3(64 * AP_SW), 0, st, qq, sq, kdig, ck, skk, flags, pos, exp_t, st_mx, st_es, R, H,
                      KV, nkeys, kpad, INV);
-  hipLaunchKernelGGL(k_attn_fused<8>, grid, dim3(64 * AP_WAVES), 0, st, qq, sq, kdig, ck, skk, vbits, vdig, pos, exp_t, out, obits, R, H,
-                     KV, nkeys, kpad, INV);
+  hipLaunchKernelGGL(k_attn_pv<4>, grid, dim3(64 * (AP_PROD + AP_CONS)), 0, st, qq, sq, kdig, ck, skk, flags, vdig, pos, exp_t, st_mx, st_es, out,
+                     obits, R, H, KV, nkeys, kpad, INV);
+  hipLaunchKernelGGL(k_attn_pv<8>, grid, dim3(64 * (AP_PROD + AP_CONS)), 0, st, qq, sq, kdig, ck, skk, flags, vdig, pos, exp_t, st_mx, st_es, out,
+                     obits, R, H, KV, nkeys, kpad, INV);
   return launch_status("attention_prefill");
 }

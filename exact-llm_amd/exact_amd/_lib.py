@@ -47,7 +47,7 @@ SIGNATURES = {
     "exact_moe_combine": [P, P, P, P, P, P, P, P, I32, I32, I32, I32, P],
 }
 OTHER = {"exact_version": ([], ctypes.c_int), "exact_last_error": ([], ctypes.c_char_p),
-         "exact_attention_prefill_workspace": ([I32, I32, I32], ctypes.c_int64)}
+         "exact_attention_prefill_workspace": ([I32, I32, I32, I32, I32], ctypes.c_int64)}
 ERRORS = {1: "bad argument", 2: "unsupported size", 3: "HIP launch error"}
 
 

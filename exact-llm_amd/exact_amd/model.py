@@ -202,10 +202,10 @@ class TModel:
 
     PREFILL_MIN_ROWS = 32
 
-    def _prefill_ws(self):
-        if self._pws is None:
-            self._pws = ops.prefill_workspace(self.cfg.KV, self.cfg.hd, self.Smax, self.dev)
-        return self._pws
+    def _prefill_ws(self, R):
+        if self._pws is None or self._pws[0] < R:
+            self._pws = (R, ops.prefill_workspace(R, self.cfg.H, self.cfg.KV, self.cfg.hd, self.Smax, self.dev))
+        return self._pws[1]
 
     def workspace(self, R):
         if R not in self._ws:
@@ -251,7 +251,7 @@ class TModel:
                                clear=group)
             if ws.seq is not None:
                 ops.attention_prefill(ws.qq, ws.sq, cache, ws.seq[0], ws.pos, ws.seq[1], tab.exp, ws.att, H, KV, hd, tab.inv,
-                                      self._prefill_ws(), ws.obits)
+                                      self._prefill_ws(R), ws.obits)
             else:
                 ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv, ws.obits)
             ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa)

@@ -233,11 +233,12 @@ def attention(qq, sq, cache, slot, pos, expt, out, H, KV, hd, inv, obits=None):
     return out
 
 
-def prefill_workspace(KV, hd, nkeys, device):
-    """Workspace of attention_prefill for up to nkeys keys (digit copies of one slot's k and v)."""
-    n = _lib.load().exact_attention_prefill_workspace(KV, hd, nkeys)
+def prefill_workspace(R, H, KV, hd, nkeys, device):
+    """Workspace of attention_prefill for up to R query rows over up to nkeys keys (digit copies of one slot's k
+    and v, per-row softmax statistics)."""
+    n = _lib.load().exact_attention_prefill_workspace(R, H, KV, hd, nkeys)
     if n < 0:
-        raise ExactError(f"attention_prefill: unsupported KV={KV}, hd={hd}, nkeys={nkeys}")
+        raise ExactError(f"attention_prefill: unsupported R={R}, H={H}, KV={KV}, hd={hd}, nkeys={nkeys}")
     return torch.empty(int(n), dtype=I8, device=device)
 
 

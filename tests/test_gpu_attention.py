@@ -62,7 +62,7 @@ def run_prefill(cache, qq, sq, pos, slot, nkeys, H, KV, hd):
     R = qq.shape[0]
     out = torch.full((R, H * hd), -7, dtype=I64, device=DEV)
     obits = torch.full((R, H), -1, dtype=I32, device=DEV)
-    ws = ops.prefill_workspace(KV, hd, nkeys, DEV)
+    ws = ops.prefill_workspace(R, H, KV, hd, nkeys, DEV)
     ops.attention_prefill(qq, sq, cache, slot, pos, nkeys, torch.tensor(exp_t(), dtype=I32, device=DEV), out, H, KV, hd,
                           O.inv_sqrt_hd(hd), ws, obits)
     return host(out), host(obits)
