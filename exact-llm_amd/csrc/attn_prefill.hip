@@ -52,58 +52,48 @@ __device__ __forceinline__ int sum16(v4i p0, v4i p1) {
   return s;
 }
 
-// Position of key jj (0..31) inside its 32-key group in kdig/vdig order: the group is stored as the keys
-// 8c + 4h + u (u < 4) at 16 h + 4 c + u, so half h of a wave reads its 16 keys as one 16-byte chunk, in the order
-// 8 (m / 4) + 4 h + m % 4 (m = byte) in which a transposed 32x32 MFMA result holds them.
-__device__ __forceinline__ int key_slot(int jj) { return 16 * ((jj >> 2) & 1) + 4 * (jj >> 3) + (jj & 3); }
-
-// Balanced base-256 digits of every v of the sequence, transposed: vdig[((kh * 8 + b) * hd + d) * kpad + slot]
-// (slot: key_slot inside each 32-key group; zeros from nkeys on); vbits[kh] = max bit length of |v| over the
-// KV head (zeroed before). grid (kpad / 32, KV), block 256: 32 keys read row-major, staged in LDS, written 32
-// keys per (digit, dimension).
-#define VD_STRIDE 36   // bytes per LDS row of 32 keys, padded against bank conflicts
-__global__ __launch_bounds__(256) void k_vdigits(const int64_t* __restrict__ v, int sl, int KV, int Smax, int nkeys, int kpad,
-                                                 int8_t* __restrict__ vdig, int32_t* __restrict__ vbits) {
-  __shared__ __align__(16) int8_t st[8 * AP_HD * VD_STRIDE];
-  const int kh = blockIdx.y, j0 = blockIdx.x * 32, tid = threadIdx.x;
+// V digits for the p.v product: vdig[(((kh * 8 + b) * ntile + t) * 2 + half) * hd + d][m] (16 bytes) is balanced
+// base-256 digit b of v[32 t + 8 (m / 4) + 4 half + m % 4][d] (zero from nkeys on): the 16 keys in the order in
+// which a transposed 32x32 MFMA result holds them for lane half `half`, and consecutive dimensions 16 bytes apart
+// (so a wave's loads are contiguous). vbits[kh] = max bit length of |v| over the KV head.
+__device__ __forceinline__ void vdigits_tile(const int64_t* __restrict__ v, int sl, int KV, int Smax, int nkeys, int kh, int t,
+                                             int ntile, int8_t* __restrict__ vdig, int32_t* __restrict__ vbits) {
+  const int d = threadIdx.x & (AP_HD - 1), half = threadIdx.x >> 7;
   const int64_t cbase = ((int64_t)sl * KV + kh) * Smax;
+  v4i pk[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) pk[b] = v4i{};
   int bl = 0;
-#pragma unroll 4
-  for (int i = 0; i < 32 * AP_HD / 256; ++i) {
-    const int e = tid + 256 * i, key = e / AP_HD, d = e % AP_HD;
-    int64_t x = j0 + key < nkeys ? v[(cbase + j0 + key) * AP_HD + d] : 0;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int key = 32 * t + 8 * (m >> 2) + 4 * half + (m & 3);
+    int64_t x = key < nkeys ? v[(cbase + key) * AP_HD + d] : 0;
     const int b0 = bitlen64(abs64(x));
     bl = b0 > bl ? b0 : bl;
-    const int slot = key_slot(key);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       const int64_t dg = ((x + 128) & 255) - 128;
-      st[(b * AP_HD + d) * VD_STRIDE + slot] = (int8_t)dg;
+      pk[b][m >> 2] |= (int)(dg & 255) << (8 * (m & 3));
       x = (x - dg) >> 8;
     }
   }
+#pragma unroll
+  for (int b = 0; b < 8; ++b)
+    *reinterpret_cast<v4i*>(vdig + (((((int64_t)kh * 8 + b) * ntile + t) * 2 + half) * AP_HD + d) * 16) = pk[b];
   bl = wave_max_i32(bl);
-  if ((tid & 63) == 0) atomicMax(vbits + kh, bl);
-  __syncthreads();
-  int8_t* dst = vdig + (int64_t)kh * 8 * AP_HD * kpad + j0;
-#pragma unroll 4
-  for (int i = 0; i < 8 * AP_HD * 8 / 256; ++i) {
-    const int idx = tid + 256 * i, row = idx >> 3, w = idx & 7;   // row = b * hd + d, w = dword of 32 keys
-    *reinterpret_cast<int32_t*>(dst + (int64_t)row * kpad + 4 * w) = *reinterpret_cast<const int32_t*>(st + row * VD_STRIDE + 4 * w);
-  }
+  if ((threadIdx.x & 63) == 0) atomicMax(vbits + kh, bl);
 }
 
 // Digits of every cached k of the sequence for the q.k product: kdig[(((kh * 2 + p) * 4 + kb) * kpad + j) * 32 + c]
 // = digit p (0: hi, 1: lo - 128) of k[j][32 kb + c]; ck[kh * kpad + j] = 128 sum_d k[j][d] - 16384 hd and
 // skk[kh * kpad + j] = sk[j] (zeros from nkeys on); skmax[kh] = max sk; tnz[0] = 1 if the exp table T has a
-// nonzero entry from AP_TN - 2 on, else tnz[1] = 1 + the last nonzero index (all zeroed before). grid
-// (kpad / 32, KV), block 256: 8 threads per key.
-__global__ __launch_bounds__(256) void k_kdigits(const int16_t* __restrict__ kq, const int32_t* __restrict__ sk, int sl, int KV,
-                                                 int Smax, int nkeys, int kpad, int8_t* __restrict__ kdig, int32_t* __restrict__ ck,
-                                                 int32_t* __restrict__ skk, int32_t* __restrict__ skmax,
-                                                 const int32_t* __restrict__ T, int32_t* __restrict__ tnz) {
-  const int kh = blockIdx.y, tid = threadIdx.x;
-  const int j = blockIdx.x * 32 + (tid >> 3), c = tid & 7;   // c: 16 dimensions 16 c .. 16 c + 15
+// nonzero entry from AP_TN - 2 on, else tnz[1] = 1 + the last nonzero index. 8 threads per key.
+__device__ __forceinline__ void kdigits_tile(const int16_t* __restrict__ kq, const int32_t* __restrict__ sk, int sl, int KV,
+                                             int Smax, int nkeys, int kpad, int kh, int t, int8_t* __restrict__ kdig,
+                                             int32_t* __restrict__ ck, int32_t* __restrict__ skk, int32_t* __restrict__ skmax,
+                                             const int32_t* __restrict__ T, int32_t* __restrict__ tnz) {
+  const int tid = threadIdx.x;
+  const int j = 32 * t + (tid >> 3), c = tid & 7;   // c: 16 dimensions 16 c .. 16 c + 15
   const int64_t row = ((int64_t)sl * KV + kh) * Smax + j;
   v4i p0 = {}, p1 = {};
   if (j < nkeys) {
@@ -129,13 +119,29 @@ __global__ __launch_bounds__(256) void k_kdigits(const int16_t* __restrict__ kq,
   }
   skv = wave_max_i32(skv);
   if ((tid & 63) == 0) atomicMax(skmax + kh, skv);
-  if (blockIdx.x == 0 && blockIdx.y == 0) {   // the fast path keeps exp entries [0, AP_TN) in LDS
+  if (kh == 0) {   // the fast path keeps exp entries [0, AP_TN) in LDS; the KV head 0 blocks scan the table
     int nz = 0, last = 0;
-    for (int i = AP_TN - 2 + tid; i < EXACT_EXP_N; i += 256) nz |= T[i] != 0;
-    for (int i = tid; i < AP_TN - 2; i += 256) last = T[i] != 0 ? i + 1 : last;
+    for (int i = 256 * t + tid; i < EXACT_EXP_N; i += 8 * kpad) {
+      const int x = T[i];
+      if (i >= AP_TN - 2) nz |= x != 0;
+      else last = x != 0 ? i + 1 : last;
+    }
     if (nz) atomicOr(tnz, 1);
-    atomicMax(tnz + 1, last);
+    if (last) atomicMax(tnz + 1, last);
   }
+}
+
+// grid (kpad / 32, 2 KV), block 256: blocks with y < KV write V digits, the others k digits (flags zeroed before:
+// vbits[KV], skmax[KV], exp-table tail, exp-table zero index)
+__global__ __launch_bounds__(256) void k_attn_digits(const int64_t* __restrict__ v, const int16_t* __restrict__ kq,
+                                                     const int32_t* __restrict__ sk, const int32_t* __restrict__ T, int sl, int KV,
+                                                     int Smax, int nkeys, int kpad, int8_t* __restrict__ vdig,
+                                                     int8_t* __restrict__ kdig, int32_t* __restrict__ ck, int32_t* __restrict__ skk,
+                                                     int32_t* __restrict__ flags) {
+  if ((int)blockIdx.y < KV)
+    vdigits_tile(v, sl, KV, Smax, nkeys, blockIdx.y, blockIdx.x, kpad / 32, vdig, flags);
+  else
+    kdigits_tile(kq, sk, sl, KV, Smax, nkeys, kpad, blockIdx.y - KV, blockIdx.x, kdig, ck, skk, flags + KV, T, flags + 2 * KV);
 }
 
 // floor(a / b) for b > 0 given rb ~ 1 / b: the estimate is corrected exactly, as in floordiv_pos
@@ -363,7 +369,7 @@ __device__ __forceinline__ void load_v_step(const int8_t* __restrict__ vd, int64
   for (int tt = 0; tt < AP_PROD; ++tt) {
     const int t = AP_PROD * s + tt < ntile ? AP_PROD * s + tt : ntile - 1;   // stays inside the written keys
 #pragma unroll
-    for (int b = 0; b < NB; ++b) vb[tt][b] = *reinterpret_cast<const v4i*>(vd + b * vplane + 32 * t);
+    for (int b = 0; b < NB; ++b) vb[tt][b] = *reinterpret_cast<const v4i*>(vd + b * vplane + (int64_t)t * (2 * AP_HD * 16));
   }
 }
 
@@ -414,7 +420,7 @@ __device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile,
           for (int b = 0; b < NB; ++b) cur[b] = vb[b];
           const int tn = t + 1 < ntile ? t + 1 : t;
 #pragma unroll
-          for (int b = 0; b < NB; ++b) vb[b] = *reinterpret_cast<const v4i*>(vd + b * vplane + 32 * tn);
+          for (int b = 0; b < NB; ++b) vb[b] = *reinterpret_cast<const v4i*>(vd + b * vplane + (int64_t)tn * (2 * AP_HD * 16));
 #pragma unroll
           for (int a = 0; a < 3; ++a) pv[a] = L.Pl[buf][tt][a][lane];
           __builtin_amdgcn_sched_barrier(0);
@@ -426,6 +432,26 @@ __device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile,
       }
       __syncthreads();
     }
+  }
+}
+
+// consume, then out = shr(sum_s C_s 256^s, 20) (modulo 2^64, as the reference's int64 p . v) for dimension d
+// of the block's rows, and the rows' bit lengths in rowbits. C layout: lane holds rows 8 (i / 4) + 4 half + i % 4.
+template <int NB>
+__device__ __forceinline__ void consume_store(const AttnLDS& L, int nsteps, int ntile, const int8_t* __restrict__ vd,
+                                              int64_t vplane, int lane, int64_t* __restrict__ out, int* rowbits, int q0, int R,
+                                              int H, int h, int d, int half) {
+  v16i acc[NB + 2];
+  consume<NB>(L, nsteps, ntile, vd, vplane, lane, acc);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    uint64_t tot = 0;
+#pragma unroll
+    for (int k = 0; k < NB + 2; ++k) tot += (uint64_t)shl64((int64_t)acc[k][i], 8 * k);
+    const int r = 8 * (i >> 2) + 4 * half + (i & 3);
+    const int64_t o = shr64((int64_t)tot, 20);
+    if (q0 + r < R) out[((int64_t)(q0 + r) * H + h) * AP_HD + d] = o;
+    atomicMax(rowbits + r, bitlen64(abs64(o)));
   }
 }
 
@@ -699,9 +725,7 @@ __global__ __launch_bounds__(64 * AP_SW, 3) void k_attn_stats(const int16_t* __r
 // Pass 3. grid ceil(R / 32) H rounded up to a multiple of 8, block 512 (8 waves): 32 query rows of one head per
 // block, heaviest tiles first. In steps of 4 key tiles of 32, waves 0..3 turn tile 4 s + w into p digits (LDS,
 // double-buffered) while waves 4..7 multiply the previous step's p into V, each for 32 dimensions (a producer
-// and a consumer share each SIMD). NB = V digits; the instantiation whose NB the KV head does not need returns at
-// once (both are launched, so the host need not read the V bit lengths).
-template <int NB>
+// and a consumer share each SIMD). The consumers use 4 V digits when every |v| of the KV head is below 2^30, else 8.
 __global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
                                                  const int8_t* __restrict__ kdig, const int32_t* __restrict__ ck,
                                                  const int32_t* __restrict__ skk, const int32_t* __restrict__ flags,
@@ -716,7 +740,6 @@ __global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int1
   __shared__ int rowbits[32];
   int h, kh, q0;
   if (!block_item(R, H, KV, h, kh, q0)) return;
-  if ((flags[kh] + 2 <= 32 ? 4 : 8) != NB) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   if (tid < 32) rowbits[tid] = 0;
   Block b;
@@ -727,22 +750,11 @@ __global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int1
   AttnLDS L{T, Pl, nullptr, nullptr, nullptr};
   const int nsteps = (b.ntile + AP_PROD - 1) / AP_PROD;
   const int dc = w - AP_PROD;   // consumer: dimensions 32 dc + [0, 32)
-  const int8_t* vd = vdig + (int64_t)kh * 8 * AP_HD * kpad + (int64_t)(32 * dc + c.l32) * kpad + 16 * c.half;
-  const int64_t vplane = (int64_t)AP_HD * kpad;
+  const int8_t* vd = vdig + (int64_t)kh * 8 * AP_HD * kpad + ((int64_t)c.half * AP_HD + 32 * dc + c.l32) * 16;
+  const int64_t vplane = (int64_t)AP_HD * kpad;   // one digit plane: kpad / 32 tiles x 2 halves x hd x 16 bytes
   if (w >= AP_PROD) {
-    v16i acc[NB + 2];
-    consume<NB>(L, nsteps, b.ntile, vd, vplane, lane, acc);
-    // C layout: lane holds dimension 32 dc + l32 of query rows 8 (i / 4) + 4 half + i % 4
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      uint64_t tot = 0;
-#pragma unroll
-      for (int k = 0; k < NB + 2; ++k) tot += (uint64_t)shl64((int64_t)acc[k][i], 8 * k);
-      const int r = 8 * (i >> 2) + 4 * c.half + (i & 3);
-      const int64_t o = shr64((int64_t)tot, 20);
-      if (q0 + r < R) out[((int64_t)(q0 + r) * H + h) * AP_HD + 32 * dc + c.l32] = o;
-      atomicMax(rowbits + r, bitlen64(abs64(o)));
-    }
+    if (flags[kh] + 2 <= 32) consume_store<4>(L, nsteps, b.ntile, vd, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
+    else consume_store<8>(L, nsteps, b.ntile, vd, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
   } else if (b.fast) {
     const FastCtx f{T, __builtin_ldexp((double)INV, b.sqv - 32), 256.0 * flags[2 * KV + 1], 128 * b.sqs, b.mypos};
     produce_f64(c, L, f, nsteps, b.ntile, b.firstpos, w, lane, (double)mx, es);
@@ -756,6 +768,7 @@ __global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int1
 // workspace layout (bytes, each part 256-aligned): vdig KV*8*hd*kpad, kdig KV*2*hd*kpad, ck and skk KV*kpad*4
 // each, flags (2 KV + 2) int32: vbits, skmax, exp-table tail, exp-table zero index; row maxima and sums H*R*8 each
 static int64_t al256(int64_t n) { return (n + 255) & ~(int64_t)255; }
+static int64_t al16(int64_t n) { return (n + 15) & ~(int64_t)15; }
 static int64_t ws_bytes(int R, int H, int KV, int kpad) {
   return al256((int64_t)KV * 8 * AP_HD * kpad) + al256((int64_t)KV * 2 * AP_HD * kpad) + 2 * al256((int64_t)KV * kpad * 4) +
          al256((int64_t)(2 * KV + 2) * 4) + 2 * al256((int64_t)H * R * 8);
@@ -788,17 +801,14 @@ extern "C" int exact_attention_prefill(const int16_t* qq, const int32_t* sq, con
   int64_t* st_mx = reinterpret_cast<int64_t*>(reinterpret_cast<int8_t*>(flags) + al256((int64_t)(2 * KV + 2) * 4));
   int64_t* st_es = reinterpret_cast<int64_t*>(reinterpret_cast<int8_t*>(st_mx) + al256((int64_t)H * R * 8));
   hipStream_t st = as_stream(stream);
-  int e = zero_bytes(flags, (int64_t)(2 * KV + 2) * 4, st);
+  int e = zero_bytes(flags, al16((int64_t)(2 * KV + 2) * 4), st);
   if (e) return e;
-  hipLaunchKernelGGL(k_vdigits, dim3(kpad / 32, KV), dim3(256), 0, st, v, slot, KV, Smax, nkeys, kpad, vdig, flags);
-  hipLaunchKernelGGL(k_kdigits, dim3(kpad / 32, KV), dim3(256), 0, st, kq, sk, slot, KV, Smax, nkeys, kpad, kdig, ck, skk,
-                     flags + KV, exp_t, flags + 2 * KV);
+  hipLaunchKernelGGL(k_attn_digits, dim3(kpad / 32, 2 * KV), dim3(256), 0, st, v, kq, sk, exp_t, slot, KV, Smax, nkeys, kpad,
+                     vdig, kdig, ck, skk, flags);
   const dim3 grid(((R + 31) / 32 * H + 7) / 8 * 8);
   hipLaunchKernelGGL(k_attn_stats, grid, dim3(64 * AP_SW), 0, st, qq, sq, kdig, ck, skk, flags, pos, exp_t, st_mx, st_es, R, H,
                      KV, nkeys, kpad, INV);
-  hipLaunchKernelGGL(k_attn_pv<4>, grid, dim3(64 * (AP_PROD + AP_CONS)), 0, st, qq, sq, kdig, ck, skk, flags, vdig, pos, exp_t, st_mx, st_es, out,
-                     obits, R, H, KV, nkeys, kpad, INV);
-  hipLaunchKernelGGL(k_attn_pv<8>, grid, dim3(64 * (AP_PROD + AP_CONS)), 0, st, qq, sq, kdig, ck, skk, flags, vdig, pos, exp_t, st_mx, st_es, out,
-                     obits, R, H, KV, nkeys, kpad, INV);
+  hipLaunchKernelGGL(k_attn_pv, grid, dim3(64 * (AP_PROD + AP_CONS)), 0, st, qq, sq, kdig, ck, skk, flags, vdig, pos, exp_t, st_mx,
+                     st_es, out, obits, R, H, KV, nkeys, kpad, INV);
   return launch_status("attention_prefill");
 }
