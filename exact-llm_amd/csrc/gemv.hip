@@ -259,6 +259,10 @@ int zero_bytes(void* dst, int64_t nbytes, hipStream_t st) {
 #ifndef GEMV_NT
 #define GEMV_NT 1
 #endif
+// prefill rows up to this many GEMV row chunks run as chunked GEMVs rather than as the GEMM
+#ifndef GEMV_CHUNKS_MAX
+#define GEMV_CHUNKS_MAX 3
+#endif
 static int gemv_nsplit(int N, int G) {
   const int64_t nbs = (N + 63) / 64;
   int64_t ns = (GEMV_WAVES + nbs - 1) / nbs;
@@ -333,8 +337,18 @@ extern "C" int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, c
                                int32_t N, int32_t K, void* stream) {
   int e = check_linear(x, abits, wp, mp, t, R, N, K);
   if (e) return e;
-  if (R <= (abits == 15 ? 15 : 16)) return gemv_launch(x, abits, wp, mp, t, R, N, K, as_stream(stream), false);
-  return gemm_mfma(x, abits, wp, mp, t, R, N, K, as_stream(stream));
+  const int rmax = abits == 15 ? 15 : 16;
+  if (R > GEMV_CHUNKS_MAX * rmax) return gemm_mfma(x, abits, wp, mp, t, R, N, K, as_stream(stream));
+  // Up to GEMV_CHUNKS_MAX row chunks: one GEMV per chunk streams the weights once per chunk, which beats the
+  // 128-row GEMM tiles (mostly padding at these R) while the weight passes stay few.
+  const size_t xrow = (size_t)K * (abits == 15 ? 2 : 1);
+  for (int r0 = 0; r0 < R; r0 += rmax) {
+    const int rows = R - r0 < rmax ? R - r0 : rmax;
+    e = gemv_launch(static_cast<const int8_t*>(x) + r0 * xrow, abits, wp, mp, t + (size_t)r0 * N, rows, N, K, as_stream(stream),
+                    false);
+    if (e) return e;
+  }
+  return EXACT_OK;
 }
 
 extern "C" int exact_gemv_g128_experts(const void* x, int32_t abits, const int32_t* row_map, const int8_t* wp,

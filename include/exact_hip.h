@@ -68,7 +68,8 @@ int exact_gemv_g128(const void* x, int32_t abits, const int8_t* wp, const int16_
 int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
                         int32_t R, int32_t N, int32_t K, void* stream);
 
-/* Exact group-128 GEMM for prefill (any R): same output as exact_gemv_g128.
+/* Exact group-128 GEMM for prefill (any R): same output as exact_gemv_g128. Up to 3 x 15 rows (A16) or
+ * 3 x 16 rows (A8) run as row chunks of the GEMV kernel, more rows on the MFMA GEMM kernels.
  * Replaces TLinG's R > 1 fp64 bmm branch (speed_fair_kaggle.py:739-742) and TLin._acc's
  * torch._int_mm A16/A8 passes (exact_torch.py:94-119). */
 int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
