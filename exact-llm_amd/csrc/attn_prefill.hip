@@ -144,17 +144,6 @@ __global__ __launch_bounds__(256) void k_attn_digits(const int64_t* __restrict__
     kdigits_tile(kq, sk, sl, KV, Smax, nkeys, kpad, blockIdx.y - KV, blockIdx.x, kdig, ck, skk, flags + KV, T, flags + 2 * KV);
 }
 
-// floor(a / b) for b > 0 given rb ~ 1 / b: the estimate is corrected exactly, as in floordiv_pos
-__device__ __forceinline__ int64_t floordiv_rcp(int64_t a, int64_t b, double rb) {
-  double qd = __builtin_floor((double)a * rb);
-  qd = qd > 9.2e18 ? 9.2e18 : (qd < -9.2e18 ? -9.2e18 : qd);
-  int64_t q = (int64_t)qd;
-  int64_t r = (int64_t)((uint64_t)a - (uint64_t)q * (uint64_t)b);
-  while (r < 0) { --q; r += b; }
-  while (r >= b) { ++q; r -= b; }
-  return q;
-}
-
 // Scores of a tile (keys x queries) from the digit products: HH, HL + LH, LL.
 struct QK {
   const int8_t* kd;      // this KV head's k digits

@@ -135,14 +135,15 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_qrow(int64_t* __restrict__ x, 
     ss = (int64_t)((uint64_t)ss + (uint64_t)(xs * xs));
   }
   ss = block_sum64_1(ss, red_b);
-  const int64_t ms = floordiv64(ss, D) + 1;
+  const int64_t ms = floordiv_pos(ss, D) + 1;   // ss >= 0 (a sum of squares; wraps only past 2^63, as numpy)
   int64_t rt = isqrt64(ms);
   if (rt < 1) rt = 1;
   const int64_t den = shl64(rt, k);
+  const double rden = 1.0 / (double)den;
   int m2 = 0;
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
-    v[j] = shr64(floordiv_pos(shl64(v[j], EXACT_F), den) * gv[j], EXACT_F);
+    v[j] = shr64(floordiv_rcp(shl64(v[j], EXACT_F), den, rden) * gv[j], EXACT_F);
     const int bl = bitlen64(abs64(v[j]));
     m2 = (tid + j * nt < D && bl > m2) ? bl : m2;
   }

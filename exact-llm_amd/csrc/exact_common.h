@@ -65,6 +65,18 @@ __device__ __forceinline__ int64_t floordiv_pos(int64_t a, int64_t b) {
   return q;
 }
 
+// floor(a / b) for b > 0 given rb ~ 1 / b (one reciprocal for many divisions by the same b): the estimate is
+// corrected exactly, as in floordiv_pos
+__device__ __forceinline__ int64_t floordiv_rcp(int64_t a, int64_t b, double rb) {
+  double qd = __builtin_floor((double)a * rb);
+  qd = qd > 9.2e18 ? 9.2e18 : (qd < -9.2e18 ? -9.2e18 : qd);
+  int64_t q = (int64_t)qd;
+  int64_t r = (int64_t)((uint64_t)a - (uint64_t)q * (uint64_t)b);
+  while (r < 0) { --q; r += b; }
+  while (r >= b) { ++q; r -= b; }
+  return q;
+}
+
 // SplitMix64 output for counter idx + 1 (Steele, Lea and Flood 2014; exact_llm.py:243-247)
 __host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t key, uint64_t idx) {
   uint64_t z = key + (idx + 1ULL) * 0x9E3779B97F4A7C15ULL;
