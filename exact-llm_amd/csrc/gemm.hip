@@ -288,11 +288,11 @@ __device__ __forceinline__ int opaque(int x) {
 //   chain (1,0): read A0 (group g + 1)      rescale (0,1)
 //   chain (1,1): read B0 + scales (g + 1)   rescale (1,0)
 // so one barrier per group, and every LDS read overlaps matrix-core work.
-template <int WM, int WN, int S>
+template <int WM, int WN, int S, bool PAIRS>
 __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __restrict__ xb, const int8_t* __restrict__ wp,
                                                      const int16_t* __restrict__ mp, int64_t* __restrict__ t, int M,
                                                      int N, int K, int G, int nbs, int tiles_m, int tiles_n,
-                                                     int ksplit, int use_atomic) {
+                                                     int ksplit, int use_atomic, const int64_t* __restrict__ colterm) {
   using C = GemmCfg<7, WM, WN, S>;
   static_assert(EXACT_TILE_GN, "the block's tiles of one group are contiguous in the group-major layout");
   static_assert(C::BN == 128, "one dword copy per lane covers the block's 128 scales");
@@ -453,21 +453,67 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
   }
 #undef PIPE_PATTERN
 
+  if constexpr (PAIRS) {
+    // A16 as digit rows: rows 2r (hi = x >> 8) and 2r + 1 (lo = (x & 255) - 128) of the A operand come from
+    // activation row r and sit in one lane at i and i + 1 (i % 4 in {0, 2}), so
+    // t[r] = 256 T[2r] + T[2r + 1] + 128 sum_g colsum_g M_g (exact_torch.py:101-102), colterm = the last sum.
 #pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    const int col = nb0 * 64 + wn * 64 + b * 32 + l32;
+    for (int b = 0; b < 2; ++b) {
+      const int col = nb0 * 64 + wn * 64 + b * 32 + l32;
+      const int64_t ct = (kz == 0 && col < N) ? 128 * colterm[col] : 0;
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = row0 + wm * 64 + a * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
-        if (row < M && col < N) {
-          const int64_t val = acc[a][b][i];
-          int64_t* dst = t + (size_t)row * N + col;
-          if (use_atomic) atomicAdd(reinterpret_cast<unsigned long long*>(dst), (unsigned long long)val);
-          else *dst = val;
+        for (int i = 0; i < 16; i += 2) {
+          const int row = row0 + wm * 64 + a * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);   // even
+          if (row < M && col < N) {
+            const int64_t val = (int64_t)((uint64_t)acc[a][b][i] << 8) + acc[a][b][i + 1] + ct;
+            int64_t* dst = t + (size_t)(row >> 1) * N + col;
+            if (use_atomic) atomicAdd(reinterpret_cast<unsigned long long*>(dst), (unsigned long long)val);
+            else *dst = val;
+          }
         }
-      }
+    }
+  } else {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int col = nb0 * 64 + wn * 64 + b * 32 + l32;
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int row = row0 + wm * 64 + a * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
+          if (row < M && col < N) {
+            const int64_t val = acc[a][b][i];
+            int64_t* dst = t + (size_t)row * N + col;
+            if (use_atomic) atomicAdd(reinterpret_cast<unsigned long long*>(dst), (unsigned long long)val);
+            else *dst = val;
+          }
+        }
+    }
+  }
+}
+
+// int16 rows -> interleaved int8 digit rows: x8[2r] = x[r] >> 8, x8[2r + 1] = (x[r] & 255) - 128.
+// 16 values per thread; K % 16 == 0.
+__global__ __launch_bounds__(256) void k_split_rows_a16(const int16_t* __restrict__ x, int8_t* __restrict__ x8, int64_t M,
+                                                        int K) {
+  const int64_t n16 = M * (K / 16);
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / (K / 16), c = (i - r * (K / 16)) * 16;
+    const v4i* src = reinterpret_cast<const v4i*>(x + r * K + c);
+    const v4i p0 = src[0], p1 = src[1];
+    v4i hi, lo;
+    hi[0] = __builtin_amdgcn_perm(p0[1], p0[0], 0x07050301u);
+    hi[1] = __builtin_amdgcn_perm(p0[3], p0[2], 0x07050301u);
+    hi[2] = __builtin_amdgcn_perm(p1[1], p1[0], 0x07050301u);
+    hi[3] = __builtin_amdgcn_perm(p1[3], p1[2], 0x07050301u);
+    lo[0] = __builtin_amdgcn_perm(p0[1], p0[0], 0x06040200u) ^ 0x80808080;
+    lo[1] = __builtin_amdgcn_perm(p0[3], p0[2], 0x06040200u) ^ 0x80808080;
+    lo[2] = __builtin_amdgcn_perm(p1[1], p1[0], 0x06040200u) ^ 0x80808080;
+    lo[3] = __builtin_amdgcn_perm(p1[3], p1[2], 0x06040200u) ^ 0x80808080;
+    *reinterpret_cast<v4i*>(x8 + (2 * r) * K + c) = hi;
+    *reinterpret_cast<v4i*>(x8 + (2 * r + 1) * K + c) = lo;
   }
 }
 
@@ -517,14 +563,15 @@ static int gemm_launch(const void* x, const int8_t* wp, const int16_t* mp, int64
 #define GEMM_A8P_CFG 4, 2, 3
 #endif
 
-template <int WM, int WN, int S>
+// M: rows of the A operand (digit rows when PAIRS: the output has M / 2 rows, written through colterm)
+template <int WM, int WN, int S, bool PAIRS = false>
 static int gemm_launch_a8p(const void* x, const int8_t* wp, const int16_t* mp, int64_t* t, int M, int N, int K,
-                           hipStream_t st, int ksplit_req) {
+                           hipStream_t st, int ksplit_req, const int64_t* colterm = nullptr) {
   using C = GemmCfg<7, WM, WN, S>;
   static bool attr_set = false;
   const size_t lds = S * (size_t)(C::A_BYTES + C::B_BYTES + C::WAVES * 256);
   if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_a8p<WM, WN, S>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_a8p<WM, WN, S, PAIRS>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr_set = true;
   }
@@ -538,13 +585,14 @@ static int gemm_launch_a8p(const void* x, const int8_t* wp, const int16_t* mp, i
   if (ksplit > G) ksplit = G;
   const int use_atomic = ksplit > 1;
   if (use_atomic) {
-    int e = zero_bytes(t, (int64_t)M * N * 8, st);
+    int e = zero_bytes(t, (int64_t)(PAIRS ? M / 2 : M) * N * 8, st);
     if (e) return e;
   }
   const int nblk = tiles_m * tiles_n * ksplit;
   const int grid = ((nblk + 7) / 8) * 8;
-  hipLaunchKernelGGL((k_gemm_a8p<WM, WN, S>), dim3(grid), dim3(C::THREADS), lds, st,
-                     reinterpret_cast<const int8_t*>(x), wp, mp, t, M, N, K, G, nbs, tiles_m, tiles_n, ksplit, use_atomic);
+  hipLaunchKernelGGL((k_gemm_a8p<WM, WN, S, PAIRS>), dim3(grid), dim3(C::THREADS), lds, st,
+                     reinterpret_cast<const int8_t*>(x), wp, mp, t, M, N, K, G, nbs, tiles_m, tiles_n, ksplit, use_atomic,
+                     colterm);
   return launch_status("gemm_g128");
 }
 
@@ -559,4 +607,24 @@ int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, int
   return gemm_launch<7, GEMM_A8_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
 }
 
+int gemm_a16_digit_rows(const int16_t* x, const int8_t* wp, const int16_t* mp, const int64_t* colterm, int8_t* x8, int64_t* t,
+                        int M, int N, int K, hipStream_t st) {
+  const int64_t n16 = (int64_t)M * (K / 16);
+  const int blocks = (int)std::min<int64_t>((n16 + 255) / 256, 8192);
+  hipLaunchKernelGGL(k_split_rows_a16, dim3(blocks), dim3(256), 0, st, x, x8, (int64_t)M, K);
+  return gemm_launch_a8p<GEMM_A8P_CFG, true>(x8, wp, mp, t, 2 * M, N, K, st, GEMM_KSPLIT, colterm);
+}
+
 }  // namespace exact
+
+using namespace exact;
+
+extern "C" int exact_gemm_g128_a16(const int16_t* x, const int8_t* wp, const int16_t* mp, const int64_t* colterm, int8_t* x8,
+                                   int64_t* t, int32_t R, int32_t N, int32_t K, void* stream) {
+  if (!x || !wp || !mp || !colterm || !x8 || !t || R <= 0 || N <= 0 || K <= 0) return EXACT_E_ARG;
+  if (K % 128 || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(x8) & 15) ||
+      (reinterpret_cast<uintptr_t>(wp) & 15))
+    return EXACT_E_UNSUPPORTED;
+  if (2 * (int64_t)R * K >= (1LL << 32)) return EXACT_E_UNSUPPORTED;   // 32-bit buffer offsets of the digit rows
+  return gemm_a16_digit_rows(x, wp, mp, colterm, x8, t, R, N, K, as_stream(stream));
+}

@@ -96,8 +96,40 @@ def gemv_g128_acc(x, abits, lin, out):
     return _linear("exact_gemv_g128_acc", x, abits, lin, out)
 
 
+GEMV_CHUNK_ROWS = {15: 45, 7: 48}   # up to 3 GEMV row chunks (exact_gemm_g128 runs those as GEMVs)
+_DIGIT_ROWS = {}                     # device -> int8 workspace of the A16 digit rows
+
+
+def colterm(lin):
+    """sum_g colsum_g * M_g per output column (int64, N): the A16 digit GEMM's 128 * colsum term. One A8 GEMV of
+    an all-ones row, cached on the linear."""
+    ct = getattr(lin, "_colterm", None)
+    if ct is None:
+        ones = torch.ones((1, lin.K), dtype=I8, device=lin.wp.device)
+        ct = gemv_g128(ones, 7, lin).reshape(-1)
+        lin._colterm = ct
+    return ct
+
+
 def gemm_g128(x, abits, lin, out=None):
-    return _linear("exact_gemm_g128", x, abits, lin, out)
+    R, K = x.shape
+    if abits != 15 or R <= GEMV_CHUNK_ROWS[15]:
+        return _linear("exact_gemm_g128", x, abits, lin, out)
+    # A16 on the int8 GEMM as interleaved digit rows (exact_gemm_g128_a16)
+    if K != lin.K:
+        raise ExactError(f"exact_gemm_g128_a16: x has K = {K}, linear has K = {lin.K}")
+    _need(x, I16, "x")
+    if out is None:
+        out = torch.empty((R, lin.N), dtype=I64, device=x.device)
+    _need(out, I64, "out", R * lin.N)
+    ct = colterm(lin)
+    ws = _DIGIT_ROWS.get(x.device)
+    if ws is None or ws.numel() < 2 * R * K:
+        ws = torch.empty(2 * R * K, dtype=I8, device=x.device)
+        _DIGIT_ROWS[x.device] = ws
+    _lib.call("exact_gemm_g128_a16", _ptr(x), _ptr(lin.wp), _ptr(lin.mp), _ptr(ct), _ptr(ws), _ptr(out), R, lin.N, K,
+              _stream())
+    return out
 
 
 def linear_t(x, abits, lin, out=None, zeroed=False):

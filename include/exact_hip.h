@@ -75,6 +75,15 @@ int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const in
 int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
                     int32_t R, int32_t N, int32_t K, void* stream);
 
+/* The int16 (A16) GEMM on the int8 matrix cores as interleaved digit rows: x is split into rows
+ * x8[2r] = x[r] >> 8 and x8[2r + 1] = (x[r] & 255) - 128 (exact_torch.py:101-102), the A8 GEMM runs on the
+ * 2R digit rows, and each output row combines its pair: t[r] = 256 T[2r] + T[2r + 1] + 128 colterm.
+ * colterm[n] = sum_g (sum_{k in g} W[k][n]) * M[g][n]: exact_gemv_g128 of an all-ones int8 row (A8) gives it,
+ * once per linear. x8: caller workspace of 2 R K bytes (16-byte aligned). Same output as exact_gemm_g128
+ * with abits 15; 2 R K < 2^32. */
+int exact_gemm_g128_a16(const int16_t* x, const int8_t* wp, const int16_t* mp, const int64_t* colterm, int8_t* x8,
+                        int64_t* t, int32_t R, int32_t N, int32_t K, void* stream);
+
 /* Group epilogue y = round_shift(t, 28 - s[r]) + b[n] (b may be NULL)
  * (speed_fair_kaggle.py:725,743; SPEC.md:18). */
 int exact_requant_group(const int64_t* t, const int32_t* s, const int64_t* b, int64_t* y,
