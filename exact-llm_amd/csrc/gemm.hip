@@ -322,17 +322,24 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, (int)((uint32_t)M * (uint32_t)K), BUF_DW3);
   const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc((void*)wp, (short)0, -1, BUF_DW3);
   const __amdgpu_buffer_rsrc_t rM = __builtin_amdgcn_make_buffer_rsrc((void*)mp, (short)0, -1, BUF_DW3);
+  // per-lane copy offsets, fixed over the groups (the group enters as a scalar offset)
+  uint32_t aoffs[C::A_KB_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < C::A_KB_PER_WAVE; ++i) {
+    const int seg = wave * C::A_KB_PER_WAVE + i;            // 1 KiB LDS segment = 8 rows x 128 bytes
+    const int r = seg * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+    const int gr = row0 + r < M ? row0 + r : M - 1;         // rows past M read a valid row, never stored
+    aoffs[i] = (uint32_t)gr * (uint32_t)K + (uint32_t)(c * 16);
+  }
+  const int moff = (2 * lane < ncol ? 2 * lane : ncol - 2) * 2;
   auto issue = [&](int g, int stg, int ln) {
     int8_t* sA = smem + stg * STAGE;
     int8_t* sB = sA + C::A_BYTES;
     const int tile0 = g * nbs + nb0;
 #pragma unroll
     for (int i = 0; i < C::A_KB_PER_WAVE; ++i) {
-      const int seg = wave * C::A_KB_PER_WAVE + i;          // 1 KiB LDS segment = 8 rows x 128 bytes
-      const int r = seg * 8 + (ln >> 3), c = (ln & 7) ^ ((r >> 1) & 7);
-      const int gr = row0 + r < M ? row0 + r : M - 1;       // rows past M read a valid row, never stored
-      const uint32_t aoff = (uint32_t)gr * (uint32_t)K + (uint32_t)(c * 16);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (LDS void*)(sA + seg * 1024), 16, (int)aoff, g * 128, 0, 0);
+      const int seg = wave * C::A_KB_PER_WAVE + i;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (LDS void*)(sA + seg * 1024), 16, (int)aoffs[i], g * 128, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < C::B_KB_PER_WAVE; ++i) {
@@ -341,7 +348,6 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (LDS void*)(sB + seg * 1024), 16, ln * 16,
                                                (tile0 + tl) * 8192 + (seg & 7) * 1024, 0, 0);
     }
-    const int moff = (2 * ln < ncol ? 2 * ln : ncol - 2) * 2;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rM, (LDS void*)(sB + C::B_BYTES + wave * 256), 4, moff, tile0 * 128, 0, 0);
   };
   // fragment reads; A chunk ks * 2 + lh of row r sits at a_off(r, lh) ^ (ks << 5) (XOR swizzle)
@@ -367,21 +373,31 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
     for (int ks = 0; ks < 4; ++ks) c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[ks], b[ks], c, 0, 0, 0);
     return c;
   };
-  int64_t acc[2][2][16];
+  // PAIRS: one running total per output row pair (256 hi + lo fits int32 per group: 2^29 + 2^21)
+  constexpr int NT_ = PAIRS ? 8 : 16;
+  int64_t acc[2][2][NT_];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0;
+      for (int i = 0; i < NT_; ++i) acc[a][b][i] = 0;
   // t += c * m, pinned in place: without a use here the compiler sinks the multiply-adds past the next
   // barrier, where they no longer overlap the matrix-core work
-  auto rescale = [&](int64_t (&ac)[16], const v16i& c, int m_) {
+  auto rescale = [&](int64_t (&ac)[NT_], const v16i& c, int m_) {
     const int m = opaque(m_);   // a plain 32-bit value here, so each product is one v_mad_i64_i32
+    if constexpr (PAIRS) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) ac[i] += (int64_t)c[i] * (int64_t)m;
+      for (int j = 0; j < 8; ++j) {
+        const int i = 2 * j;   // i % 4 in {0, 2}: rows 2r (hi) and 2r + 1 (lo) at i and i + 1
+        ac[j] += (int64_t)((c[i] << 8) + c[i + 1]) * (int64_t)m;
+      }
+    } else {
 #pragma unroll
-    for (int i = 0; i < 16; i += 4) asm volatile("" ::"v"(ac[i]), "v"(ac[i + 1]), "v"(ac[i + 2]), "v"(ac[i + 3]));
+      for (int i = 0; i < 16; ++i) ac[i] += (int64_t)c[i] * (int64_t)m;
+    }
+#pragma unroll
+    for (int i = 0; i < NT_; i += 4) asm volatile("" ::"v"(ac[i]), "v"(ac[i + 1]), "v"(ac[i + 2]), "v"(ac[i + 3]));
   };
   // one chain of 4 MFMAs interleaved with `reads` LDS reads and the 16 rescale multiply-adds
 #define PIPE_PATTERN(reads)                                                                    \
@@ -412,7 +428,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
     int mprev = 0;
     int stg = 0;
     for (int g = g0; g < g1; ++g) {
-      const int ln = opaque(lane);
+      const int ln = lane;
       const int nstg = stg + 1 == S ? 0 : stg + 1;
       readB(B1, stg, 1, ln);
       const v16i c00 = chain(A0, B0);
@@ -455,8 +471,9 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
 
   if constexpr (PAIRS) {
     // A16 as digit rows: rows 2r (hi = x >> 8) and 2r + 1 (lo = (x & 255) - 128) of the A operand come from
-    // activation row r and sit in one lane at i and i + 1 (i % 4 in {0, 2}), so
-    // t[r] = 256 T[2r] + T[2r + 1] + 128 sum_g colsum_g M_g (exact_torch.py:101-102), colterm = the last sum.
+    // activation row r and sit in one lane at i and i + 1 (i % 4 in {0, 2}); the rescale combined them per
+    // group, so t[r] = sum_g (256 hi_g + lo_g) M_g + 128 sum_g colsum_g M_g (exact_torch.py:101-102), colterm
+    // = the last sum.
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int col = nb0 * 64 + wn * 64 + b * 32 + l32;
@@ -467,7 +484,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
         for (int i = 0; i < 16; i += 2) {
           const int row = row0 + wm * 64 + a * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);   // even
           if (row < M && col < N) {
-            const int64_t val = (int64_t)((uint64_t)acc[a][b][i] << 8) + acc[a][b][i + 1] + ct;
+            const int64_t val = acc[a][b][i >> 1] + ct;
             int64_t* dst = t + (size_t)(row >> 1) * N + col;
             if (use_atomic) atomicAdd(reinterpret_cast<unsigned long long*>(dst), (unsigned long long)val);
             else *dst = val;
