@@ -548,9 +548,10 @@ static int gemm_launch(const void* x, const int8_t* wp, const int16_t* mp, int64
   const int G = K / 128, nbs = (N + 63) / 64;
   const int tiles_m = (M + C::BM - 1) / C::BM, tiles_n = (nbs + C::NT - 1) / C::NT;
   int ksplit = ksplit_req;
-  if (ksplit <= 0) {   // split K when the output tiles alone cannot fill the 256 CUs
+  if (ksplit <= 0) {   // split K only when the output tiles fill fewer than half the 256 CUs (the split costs a
+                       // zero fill and 64-bit atomics on t, more than a partly idle chip)
     ksplit = 1;
-    while (tiles_m * tiles_n * ksplit < 400 && G / (ksplit * 2) >= 8) ksplit *= 2;
+    while (tiles_m * tiles_n * ksplit < 128 && G / (ksplit * 2) >= 8) ksplit *= 2;
   }
   if (ksplit > G) ksplit = G;
   const int use_atomic = ksplit > 1;
@@ -597,7 +598,7 @@ static int gemm_launch_a8p(const void* x, const int8_t* wp, const int16_t* mp, i
   int ksplit = ksplit_req;
   if (ksplit <= 0) {
     ksplit = 1;
-    while (tiles_m * tiles_n * ksplit < 400 && G / (ksplit * 2) >= 8) ksplit *= 2;
+    while (tiles_m * tiles_n * ksplit < 128 && G / (ksplit * 2) >= 8) ksplit *= 2;
   }
   if (ksplit > G) ksplit = G;
   const int use_atomic = ksplit > 1;
