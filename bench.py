@@ -375,7 +375,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(dom["GBps"] / HBM_PEAK_GBPS, 4), "traffic": GATEUP_TRAFFIC_BYTES,
                      "algorithmic_bytes": GATEUP_BYTES,
-                     "kernel": "k_gemv_g128<7,true,1> on gate|up 37888x3584, bs1 A8"},
+                     "kernel": "k_gemv_g128<7,true,1,16> on gate|up 37888x3584, bs1 A8"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

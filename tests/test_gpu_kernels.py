@@ -91,7 +91,7 @@ def test_prefill_gemm_full_shapes(thr, name, N, K):
 
 
 @pytest.mark.parametrize("name,N,K", [("q", 3584, 3584), ("kv", 512, 3584), ("gate", 18944, 3584), ("down", 3584, 18944)])
-@pytest.mark.parametrize("R", [1, 8])
+@pytest.mark.parametrize("R", [1, 2, 8])
 def test_gemv_7b_shapes(thr, name, N, K, R):
     """Full Qwen2.5-7B GEMV shapes, x int8 U[-127, 127] (A8) and int16 (A16), bit-exact vs numpy."""
     lin, kw, km = synth_lin(thr, 70, name, N, K)
