@@ -203,6 +203,64 @@ def model_decode(args, name="qwen2.5-7b", prompt_len=16, B=1):
             "prefill_ms_per_sequence": round(prefill_ms, 3)}
 
 
+def trace_capture(args, name="qwen2.5-7b", prompt_len=16, steps=32, reps=3):
+    """Cost of the trace commitment in graph decode (the reference's T0-T3, prover_commit_cost_gpu_kaggle.py:791-845),
+    7B shape, bs1, A16: T0 plain graph decode; T1 + the totals of every linear left in a static device trace buffer
+    by the graph; T2 + copy of each step's trace to pinned host memory on a side stream; T3 + SHA-256 commitment
+    of each step's trace (4 leaves in 4 threads). Median of `reps` runs of `steps` steps after a prompt, each run
+    re-prefilled; logits of the first 8 steps must equal T0's."""
+    import numpy as np
+    import torch
+    from exact_amd import synth
+    from exact_amd.model import DeviceWeights, GraphDecoder, TModel
+    cfg = synth.CONFIGS[name]
+    tm = TModel(DeviceWeights.synthetic(cfg, 11, "cuda"), Smax=prompt_len + steps + 8, batch=1)
+    ids = np.random.default_rng(1).integers(0, cfg.V, prompt_len).tolist()
+    res, base = {}, None
+    for mode, rmode in (("T0", None), ("T1", "device"), ("T2", "host"), ("T3", "commit")):
+        cache = tm.new_cache(B=1)
+        first = int(tm.forward(ids, cache, last_only=True)[0].argmax())
+        gd = GraphDecoder(tm, cache, 1, trace=rmode is not None)
+        gd.load([first])
+        gd.capture()
+        times, rows, ndig = [], [], 0
+        for rep in range(reps):
+            cache.n[0] = 0
+            tm.forward(ids, cache, last_only=True)
+            gd.load([first])
+            gd.nstep = 0
+            rec = gd.record(rmode) if rmode else None
+            got = []
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for j in range(steps):
+                lg, _ = gd.step()
+                if j < 8:
+                    got.append(lg.clone())
+            digests = rec.finish() if rec else None
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+            if rep == 0:
+                rows = got
+                ndig = len(digests) if digests is not None else 0
+        res[mode + "_tok_s"] = round(steps / float(np.median(times)), 2)
+        if base is None:
+            base = rows
+        else:
+            res[mode + "_logits_equal_T0"] = all(torch.equal(a, b) for a, b in zip(rows, base))
+        if mode == "T3":
+            res["T3_digests_per_run"] = ndig
+        if rmode:
+            res["trace_ints_per_token"] = gd.layout.total
+        del gd
+    for mode in ("T1", "T2", "T3"):
+        res[mode + "_overhead"] = round(res["T0_tok_s"] / res[mode + "_tok_s"] - 1, 4)
+    res.update(model=name, batch=1, steps=steps, prompt=prompt_len, reps=reps)
+    del tm
+    torch.cuda.empty_cache()
+    return res
+
+
 def attention_prefill(args, S=2048, H=28, KV=4, hd=128):
     """Exact integer causal attention of one 2048-token prefill layer (28 q / 4 kv heads, hd 128) from the
     KV cache: algorithmic ops 2*(S(S+1)/2)*hd*H for q.k and the same for p.v."""
@@ -318,6 +376,7 @@ def main():
     ap.add_argument("--no-model", action="store_true")
     ap.add_argument("--no-gemv", action="store_true", help="skip the GEMV pass (profiling runs of the other parts)")
     ap.add_argument("--models", default="7b,c1,c4,c4b8,c5", help="model decode runs: 7b, c1, c4, c4b8, c5")
+    ap.add_argument("--no-trace", action="store_true", help="skip the trace-capture cost runs (7B decode T0-T3)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also copy 512 MiB on the device three times (calibrates the HBM traffic counters)")
     args = ap.parse_args()
@@ -340,7 +399,7 @@ def main():
         del src, dst
     r = None if args.no_gemv else gemv_pass(args)
     pre = {} if args.no_prefill else prefill_gemm(args)
-    mdl, models = None, None
+    mdl, models, trc = None, None, None
     if not args.no_model:
         want = set(args.models.split(","))
         mdl = model_decode(args) if "7b" in want else None
@@ -348,11 +407,12 @@ def main():
                 "C4_qwen2.5-14b_bs8": ("c4b8", "qwen2.5-14b", 128, 8),
                 "C5_qwen1.5-moe-a2.7b_bs1": ("c5", "qwen1.5-moe-a2.7b", 256, 1)}
         models = {k: model_decode(args, n, p, B=b) for k, (tag, n, p, b) in runs.items() if tag in want}
+        trc = trace_capture(args) if "7b" in want and not args.no_trace else None
     att = None if args.no_prefill else attention_prefill(args)
     cpu = None if args.no_cpu else cpu_baseline()
     if r is None:
         print(json.dumps({"metric": METRIC, "value": None, "model_decode": mdl, "model_configs": models,
-                          "prefill_gemm": pre, "attention_prefill": att}), flush=True)
+                          "trace_capture": trc, "prefill_gemm": pre, "attention_prefill": att}), flush=True)
         return
     tok_s = 1000.0 / r["ms"]
     pass_gbps = r["pass_bytes"] / (r["ms"] * 1e-3) / 1e9
@@ -369,6 +429,7 @@ def main():
         "gemv_per_shape": r["per"],
         "model_decode": mdl,
         "model_configs": models,
+        "trace_capture": trc,
         "prefill_gemm": pre,
         "attention_prefill": att,
         "prefill_TOPS": (round(min(v["TOPS"] for v in pre.values()), 2) if pre else None),

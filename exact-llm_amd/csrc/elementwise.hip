@@ -170,10 +170,11 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_qrow(int64_t* __restrict__ x, 
 // bitlen(max |v|) = max bitlen(|v|).
 #define QSLICE 1024
 
-// gate|up total -> h = shr(isilu(g) * u, 16) (stored over the gate half), slice maxima of |h|
+// gate|up total -> h = shr(isilu(g) * u, 16) (stored in hout (R, I) when given, else over the gate half),
+// slice maxima of |h|
 __global__ __launch_bounds__(256) void k_swiglu_part(int64_t* __restrict__ t, const int32_t* __restrict__ s,
                                                      const int32_t* __restrict__ silu, int32_t* __restrict__ part, int I,
-                                                     int nparts, int clear_t) {
+                                                     int nparts, int clear_t, int64_t* __restrict__ hout) {
   constexpr int EPT = QSLICE / 256;
   __shared__ int red[4];
   const int r = blockIdx.y, b = blockIdx.x;
@@ -192,8 +193,13 @@ __global__ __launch_bounds__(256) void k_swiglu_part(int64_t* __restrict__ t, co
     const int i = b * QSLICE + j * 256 + threadIdx.x;
     if (i < I) {
       const int64_t hv = shr64(lut16(silu, shr64(gv[j], sh), false) * shr64(uv[j], sh), EXACT_F);
-      tr[i] = hv;
-      if (clear_t) tr[I + i] = 0;
+      if (hout) {
+        hout[(int64_t)r * I + i] = hv;
+        if (clear_t) { tr[i] = 0; tr[I + i] = 0; }
+      } else {
+        tr[i] = hv;
+        if (clear_t) tr[I + i] = 0;
+      }
       const int bl = bitlen64(abs64(hv));
       m = bl > m ? bl : m;
     }
@@ -451,8 +457,9 @@ extern "C" int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res
 }
 
 extern "C" int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq, int32_t* sq,
-                                 int32_t* part, int32_t R, int32_t I, int32_t clear_t, void* stream) {
+                                 int32_t* part, int32_t R, int32_t I, int32_t clear_t, int64_t* h, void* stream) {
   if (!t || !s || !silu_t || !xq || !sq || !part || R <= 0 || I <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
+  if (h == t) return EXACT_E_ARG;
   hipStream_t st = as_stream(stream);
   const int nt = I >= 1024 ? 1024 : ((I + 63) / 64) * 64;
   const int ept = (I + nt - 1) / nt;
@@ -465,8 +472,11 @@ extern "C" int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* si
   }
 #undef SWG_GO
   const int np = (I + QSLICE - 1) / QSLICE;
-  hipLaunchKernelGGL(k_swiglu_part, dim3(np, R), dim3(256), 0, st, t, s, silu_t, part, I, np, clear_t);
-  hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, t, (int64_t)2 * I, part, np, bits, xq, sq, I, clear_t);
+  hipLaunchKernelGGL(k_swiglu_part, dim3(np, R), dim3(256), 0, st, t, s, silu_t, part, I, np, clear_t, h);
+  if (h)
+    hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, h, (int64_t)I, part, np, bits, xq, sq, I, 0);
+  else
+    hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, t, (int64_t)2 * I, part, np, bits, xq, sq, I, clear_t);
   return launch_status("swiglu_qrow");
 }
 

@@ -17,6 +17,7 @@ import torch
 from . import ops, synth
 from .ops import I8, I16, I32, I64, PackedLinear, ExactError
 from .tables import DeviceTables
+from .trace import TraceLayout, TraceRecorder
 
 
 def _lin_keys(seed, name):
@@ -58,7 +59,7 @@ class DeviceWeights:
             b = torch.cat(bs) if bias else None
             if bias and N != sum(n for _, n in parts):
                 raise ExactError("biased fused linears need 64-row aligned parts")
-            return PackedLinear(wp, mp, N, K, b)
+            return PackedLinear(wp, mp, N, K, b, parts=[(name.split(".")[-1], off, n) for (name, n), off in zip(parts, offs)])
 
         for li in range(nl):
             L = dict(
@@ -165,6 +166,8 @@ class Workspace:
         self.obits = z(R, H, dt=I32)
         self.ids, self.slot, self.pos = z(R, dt=I32), z(R, dt=I32), z(R, dt=I32)
         self.seq = None   # (slot, keys) when the rows are one sequence's consecutive positions (prefill)
+        self.h = None     # (R, I) SwiGLU values when the gate|up totals must stay intact (trace capture)
+        self.I = I
         if cfg.moe:
             k, P = cfg.topk, R * cfg.topk
             nch = ops.max_chunks(P, cfg.NE, abits)
@@ -225,19 +228,35 @@ class TModel:
         return out
 
     # ---------------------------------------------------------------- one pass over R rows
-    def forward_rows(self, ws, want_logits=True):
+    def forward_rows(self, ws, want_logits=True, trace=None):
         """Runs the model on ws.ids with (slot, pos) per row; KV of each row is written into the cache
-        at (slot, pos). Leaves logits in ws.logits and greedy ids in ws.next_ids."""
+        at (slot, pos). Leaves logits in ws.logits and greedy ids in ws.next_ids.
+        trace: (TraceLayout, int64 device buffer): every linear's totals t are produced in the buffer's slots
+        and left there (the buffer is zeroed first); the consumer kernels read them without clearing."""
         c, R, tab = self.cfg, ws.R, self.tab
         H, KV, hd, D = c.H, c.KV, c.hd, c.D
         group = self.w.mode == "group"
+        keep = trace is not None
+        if keep:
+            layout, tbuf = trace
+            if layout.R != R or tbuf.numel() < layout.total:
+                raise ExactError("trace buffer does not match the rows of this pass")
+            if ws.h is None:
+                ws.h = torch.zeros((R, ws.I), dtype=I64, device=self.dev)
+            tbuf.zero_()
+            slot = lambda key: layout.slot(tbuf, key)
+        clear = group and not keep
         ops.embed(ws.ids, self.w.emb, ws.x)
         res_t, res_s = None, None
         for li, L in enumerate(self.w.layers):
             cache = self._cache.layers[li]
-            ops.rmsnorm_qrow(ws.x, L["g1"], self.abits, res_t, res_s, ws.xq, ws.s, clear=group)
+            ops.rmsnorm_qrow(ws.x, L["g1"], self.abits, res_t, res_s, ws.xq, ws.s, clear=clear)
+            if keep:
+                t_qkv, t_o, t_gu, t_d = (slot(f"L{li}.{k}") for k in ("qkv", "o", "gateup", "down"))
+            else:
+                t_qkv, t_o, t_gu, t_d = ws.t_qkv, ws.t_o, ws.t_gu, ws.t_d
             if group:
-                self._lin(ws.xq, L["qkv"], ws.t_qkv)
+                self._lin(ws.xq, L["qkv"], t_qkv)
                 s_qkv, b_qkv = ws.s, L["qkv"].bias
             else:
                 off = 0
@@ -247,8 +266,8 @@ class TModel:
                     ws.t_qkv[:, off:off + lin.N].copy_(y)
                     off += lin.N
                 s_qkv, b_qkv = ws.s28, None
-            ops.qkv_rope_cache(ws.t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache, ws.qq, ws.sq, H, KV, hd,
-                               clear=group)
+            ops.qkv_rope_cache(t_qkv if group else ws.t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache, ws.qq,
+                               ws.sq, H, KV, hd, clear=clear)
             if ws.seq is not None:
                 ops.attention_prefill(ws.qq, ws.sq, cache, ws.seq[0], ws.pos, ws.seq[1], tab.exp, ws.att, H, KV, hd, tab.inv,
                                       self._prefill_ws(R), ws.obits)
@@ -256,8 +275,8 @@ class TModel:
                 ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv, ws.obits)
             ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa)
             if group:
-                self._lin(ws.aq, L["o"], ws.t_o)
-                ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.sa, ws.xq, ws.s, clear=True)
+                self._lin(ws.aq, L["o"], t_o)
+                ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, t_o, ws.sa, ws.xq, ws.s, clear=clear)
             else:
                 self._lin_channel(ws.aq, ws.sa, L["o"], ws.t_o)
                 ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.s28, ws.xq, ws.s)
@@ -268,10 +287,11 @@ class TModel:
                 res_t, res_s = None, None
                 continue
             if group:
-                self._lin(ws.xq, L["gateup"], ws.t_gu)
-                ops.swiglu_qrow(ws.t_gu, ws.s, tab.silu, self.abits, ws.hq, ws.sh, clear=True, part=ws.part_sw)
-                self._lin(ws.hq, L["down"], ws.t_d)
-                res_t, res_s = ws.t_d, ws.sh
+                self._lin(ws.xq, L["gateup"], t_gu)
+                ops.swiglu_qrow(t_gu, ws.s, tab.silu, self.abits, ws.hq, ws.sh, clear=clear, part=ws.part_sw,
+                                h=ws.h if keep else None)
+                self._lin(ws.hq, L["down"], t_d)
+                res_t, res_s = t_d, ws.sh
             else:
                 I = L["gate"].N
                 yg = self._lin_channel(ws.xq, ws.s, L["gate"], torch.empty((R, I), dtype=I64, device=self.dev))
@@ -281,10 +301,11 @@ class TModel:
                 ops.swiglu_qrow(ws.t_gu, ws.s28, tab.silu, self.abits, ws.hq, ws.sh, part=ws.part_sw)
                 self._lin_channel(ws.hq, ws.sh, L["down"], ws.t_d)
                 res_t, res_s = ws.t_d, ws.s28
-        ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=group)
+        ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=clear)
         if group:
-            self._lin(ws.xq, self.w.head, ws.t_head)
-            ops.logits_argmax(ws.t_head, ws.s, ws.logits if want_logits else None, ws.next_ids, clear=True,
+            t_head = slot("head") if keep else ws.t_head
+            self._lin(ws.xq, self.w.head, t_head)
+            ops.logits_argmax(t_head, ws.s, ws.logits if want_logits else None, ws.next_ids, clear=clear,
                               part=ws.part_lg)
         else:
             self._lin_channel(ws.xq, ws.s, self.w.head, ws.t_head)
@@ -331,6 +352,31 @@ class TModel:
         cache.n[slot] = p0 + T
         out = ws.logits.clone()
         return out[-1:] if last_only else out
+
+    def forward_traced(self, ids, cache=None, slot=0):
+        """forward() that also returns the trace of the pass: {name: (T, n) int64} with the reference's names
+        L{i}.q, .k, .v, .o, .gate, .up, .down and head (gpu_engine_trace_verify_kaggle.py:790-792)."""
+        if cache is None:
+            cache = self.new_cache(B=1)
+            slot = 0
+        T = len(ids)
+        layout = TraceLayout(self.w, T)
+        buf = torch.empty(layout.total, dtype=I64, device=self.dev)
+        p0 = cache.n[slot]
+        if p0 + T > self.Smax:
+            raise ExactError(f"sequence of {p0 + T} positions exceeds the cache ({self.Smax})")
+        self._cache = cache
+        ws = self.workspace(T)
+        ws.ids.copy_(torch.tensor(ids, dtype=I32))
+        ws.slot.fill_(slot)
+        ws.pos.copy_(torch.arange(p0, p0 + T, dtype=I32))
+        ws.seq = (slot, p0 + T) if T >= self.PREFILL_MIN_ROWS and self.cfg.hd == 128 else None
+        try:
+            self.forward_rows(ws, trace=(layout, buf))
+        finally:
+            ws.seq = None
+        cache.n[slot] = p0 + T
+        return ws.logits.clone(), layout.split(buf.cpu().numpy())
 
     def decode_rows(self, tokens, cache):
         """One decode step for B sequences (row r = cache slot r, at position cache.n[r])."""
@@ -403,10 +449,27 @@ class GraphDecoder:
     live on the device; one replay runs every kernel of a step, writes the logits and the greedy next
     ids, and advances the positions. step() = copy tokens (optional) + replay."""
 
-    def __init__(self, tm, cache, B):
+    def __init__(self, tm, cache, B, trace=False):
+        """trace=True: every step also leaves the totals of every linear in one of two static device buffers
+        (step j in trace_bufs[j % 2], laid out by self.layout), one captured graph per buffer; attach a
+        TraceRecorder with record() to copy and commit them."""
         self.tm, self.cache, self.B = tm, cache, B
         self.ws = tm.workspace(B)
         self.graph = None
+        self.trace = trace
+        self.nstep = 0
+        self.recorder = None
+        if trace:
+            self.layout = TraceLayout(tm.w, B)
+            self.trace_bufs = [torch.zeros(self.layout.total, dtype=I64, device=tm.dev) for _ in range(2)]
+            self.graphs = [None, None]
+
+    def record(self, mode="commit", keep=False):
+        """Attach a TraceRecorder (modes "device", "host", "commit"); returns it."""
+        if not self.trace:
+            raise ExactError("this decoder was built without trace capture")
+        self.recorder = TraceRecorder(self, mode, keep)
+        return self.recorder
 
     def load(self, tokens):
         ws = self.ws
@@ -414,13 +477,13 @@ class GraphDecoder:
         ws.slot.copy_(torch.arange(self.B, dtype=I32))
         ws.pos.copy_(torch.tensor(self.cache.n[:self.B], dtype=I32))
 
-    def _step(self):
+    def _step(self, b=0):
         self.tm._cache = self.cache
-        self.tm.forward_rows(self.ws)
+        self.tm.forward_rows(self.ws, trace=(self.layout, self.trace_bufs[b]) if self.trace else None)
         ops.advance(self.ws.pos)
 
     def capture(self):
-        """Warm up once outside the graph (restoring positions), then capture one step."""
+        """Warm up once outside the graph (restoring positions), then capture one step (one per trace buffer)."""
         ws = self.ws
         pos0 = ws.pos.clone()
         ids0 = ws.ids.clone()
@@ -432,9 +495,13 @@ class GraphDecoder:
         ws.pos.copy_(pos0)
         ws.ids.copy_(ids0)
         torch.cuda.synchronize()
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self._step()
+        for b in range(2 if self.trace else 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._step(b)
+            if self.trace:
+                self.graphs[b] = g
+            self.graph = g
         torch.cuda.synchronize()
 
     def step(self, feed_argmax=True):
@@ -442,10 +509,18 @@ class GraphDecoder:
         consumes the greedy ids directly on the device."""
         if max(self.cache.n[:self.B]) >= self.tm.Smax:
             raise ExactError("cache full")
+        b = self.nstep % 2
+        if self.recorder is not None:
+            self.recorder.before_step(b)
         if self.graph is None:
-            self._step()
+            self._step(b)
+        elif self.trace:
+            self.graphs[b].replay()
         else:
             self.graph.replay()
+        if self.recorder is not None:
+            self.recorder.after_step(b)
+        self.nstep += 1
         for r in range(self.B):
             self.cache.n[r] += 1
         if feed_argmax:

@@ -44,10 +44,12 @@ class PackedLinear:
     """A linear in the packed device layout: wp int8 [Np/64][G][8][64][16], mp int16 [Np/64][G][64].
     mode 'group': y = shr(t, 28 - s) + b; mode 'channel': M (N,) int64 with the per-row drop rule."""
 
-    def __init__(self, wp, mp, N, K, bias=None, mode="group", M=None, Mbits=None):
+    def __init__(self, wp, mp, N, K, bias=None, mode="group", M=None, Mbits=None, parts=None):
         self.wp, self.mp, self.N, self.K = wp, mp, N, K
         self.G = K // 128
         self.bias, self.mode, self.M, self.Mbits = bias, mode, M, Mbits
+        # (name, first output column, width) of each linear fused into this one
+        self.parts = [("", 0, N)] if parts is None else parts
 
     @staticmethod
     def alloc(N, K, device):
@@ -206,14 +208,16 @@ def swiglu_parts(R, I, device):
     return torch.empty(R * -(-I // QSLICE), dtype=I32, device=device)
 
 
-def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None, clear=False, part=None):
+def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None, clear=False, part=None, h=None):
+    """h: optional (R, I) int64 scratch; with it and clear=False, t is left intact (trace capture)."""
     R, N2 = t.shape
     I = N2 // 2
     xq = torch.empty((R, I), dtype=I16 if bits > 7 else I8, device=t.device) if xq is None else xq
     sq = torch.empty(R, dtype=I32, device=t.device) if sq is None else sq
     part = swiglu_parts(R, I, t.device) if part is None else _need(part, I32, "part", R * -(-I // QSLICE))
+    hp = None if h is None else _ptr(_need(h, I64, "h", R * I))
     _lib.call("exact_swiglu_qrow", _ptr(_need(t, I64, "t")), _ptr(s), _ptr(silu), bits, _ptr(xq), _ptr(sq), _ptr(part), R, I,
-              int(clear), _stream())
+              int(clear), hp, _stream())
     return xq, sq
 
 

@@ -109,11 +109,12 @@ int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res_s, const i
                        int32_t bits, void* xq, int32_t* s, int32_t R, int32_t D, int32_t clear_t, void* stream);
 
 /* SwiGLU on a fused gate|up total: g = rs(t[r][n], 28 - s[r]), u = rs(t[r][I + n], 28 - s[r]),
- * h = round_shift(isilu(g) * u, 16); xq, sq = qrow(h, bits). t's gate half is overwritten with h, or all
- * of t is left zeroed when clear_t != 0. part: int32 workspace of R * ceil(I / 1024) slice bit lengths.
- * (exact_llm.py:179; isilu exact_llm.py:118-122). */
+ * h = round_shift(isilu(g) * u, 16); xq, sq = qrow(h, bits). h: optional int64 (R, I) scratch for the
+ * SwiGLU values; when NULL they may be written over t's gate half. t is left zeroed when clear_t != 0,
+ * and is left as it was when clear_t == 0 and h is given (the totals stay readable, e.g. for a trace).
+ * part: int32 workspace of R * ceil(I / 1024) slice bit lengths. (exact_llm.py:179; isilu exact_llm.py:118-122). */
 int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq,
-                      int32_t* sq, int32_t* part, int32_t R, int32_t I, int32_t clear_t, void* stream);
+                      int32_t* sq, int32_t* part, int32_t R, int32_t I, int32_t clear_t, int64_t* h, void* stream);
 
 /* qrow with the row maximum supplied in parts (a producer kernel wrote part[r * nparts + i] =
  * bitlen(max |src| over its slice i of row r)): s = max(max_i part - bits, 0), xq = clip(rs(src, s))

@@ -209,4 +209,10 @@ def test_swiglu_qrow(R, I, bits):
     eq, es = O.qrow(O.round_shift(O.isilu(g) * u, 16), bits)
     assert np.array_equal(host(hq).astype(np.int64), eq) and np.array_equal(host(sh), es[:, 0])
     assert not host(td).any()
+    # with an h scratch and no clear, t stays as it was (trace capture) and the result is the same
+    td = dev(t, I64)
+    h = torch.full((R, I), -3, dtype=I64, device=DEV)
+    hq, sh = ops.swiglu_qrow(td, dev(s, I32), dev(silu_t(), I32), bits=bits, clear=False, h=h)
+    assert np.array_equal(host(hq).astype(np.int64), eq) and np.array_equal(host(sh), es[:, 0])
+    assert np.array_equal(host(td), t)
 
