@@ -32,6 +32,7 @@ class DeviceWeights:
         self.cfg, self.device = cfg, device
         self.layers = []
         self.mode = "group"
+        self.tables = None   # host integer tables shipped with the weights (an artifact's), else built
 
     # -- seeded synthetic model generated on the device
     @classmethod
@@ -97,40 +98,76 @@ class DeviceWeights:
 
     # -- from integer arrays in the oracle's layout (w (K, N) int8; group M (G, N) or channel M (N,))
     @classmethod
-    def from_arrays(cls, cfg, arrays, device, mode="group"):
-        """arrays: emb (V, D) Q16, gf, and per layer i: f'{i}.g1', f'{i}.g2', f'{i}.{name}.w' / '.M' / '.b'."""
+    def from_arrays(cls, cfg, arrays, device, mode="group", tables=None):
+        """arrays: emb (V, D) Q16, gf, head.w / head.M (/ head.b), and per layer i: f'{i}.g1', f'{i}.g2',
+        f'{i}.{name}.w' / '.M' / '.b' for name in q, k, v, o, gate, up, down. Group mode fuses q|k|v and
+        gate|up into one packed linear each (parts adjacent, in that order), as the decode step expects;
+        channel mode keeps them separate. tables: optional host integer tables (exp, silu, sig, cos, sin) that
+        the model then uses instead of building its own (an artifact's shipped tables)."""
+        if cfg.moe:
+            raise ExactError("integer arrays of MoE models are not supported; use DeviceWeights.synthetic")
         self = cls(cfg, device)
         self.mode = mode
+        self.tables = tables
 
-        def lin(pfx):
-            w = arrays[pfx + ".w"]
+        def group_lin(pfxs):
+            ws = [np.asarray(arrays[p + ".w"]) for p in pfxs]
+            Ms = [np.asarray(arrays[p + ".M"], np.int64) for p in pfxs]
+            K = ws[0].shape[0]
+            if any(w.shape[0] != K for w in ws) or any(M.shape != (K // 128, w.shape[1]) for w, M in zip(ws, Ms)):
+                raise ExactError(f"{pfxs}: weights (K, N) with group scales (K/128, N) expected")
+            M = np.concatenate(Ms, 1)
+            if M.max() >= 1 << 15 or M.min() < 0:
+                raise ExactError("group scales must fit int16")
+            w = np.concatenate(ws, 1)
+            bs = [arrays.get(p + ".b") for p in pfxs]
+            if any(b is not None for b in bs):
+                b = np.concatenate([np.zeros(w_.shape[1], np.int64) if b_ is None else np.asarray(b_, np.int64)
+                                    for w_, b_ in zip(ws, bs)])
+                bt = ops.np_to_dev(b, I64, device)
+            else:
+                bt = None
+            wp, mp = ops.pack_linear(ops.np_to_dev(w, I8, device), ops.np_to_dev(M, I16, device))
+            parts, off = [], 0
+            for p, w_ in zip(pfxs, ws):
+                parts.append((p.rsplit(".", 1)[-1], off, w_.shape[1]))
+                off += w_.shape[1]
+            return PackedLinear(wp, mp, w.shape[1], K, bt, parts=parts)
+
+        def channel_lin(pfx):
+            w = np.asarray(arrays[pfx + ".w"])
             K, N = w.shape
             M = np.asarray(arrays[pfx + ".M"], np.int64)
             b = arrays.get(pfx + ".b")
             bt = None if b is None else ops.np_to_dev(b, I64, device)
-            wd = ops.np_to_dev(w, I8, device)
-            if mode == "group":
-                if M.max() >= 1 << 15 or M.min() < 0:
-                    raise ExactError("group scales must fit int16")
-                wp, mp = ops.pack_linear(wd, ops.np_to_dev(M, I16, device))
-                return PackedLinear(wp, mp, N, K, bt)
             ones = torch.ones((K // 128, N), dtype=I16, device=device)
-            wp, mp = ops.pack_linear(wd, ones)
+            wp, mp = ops.pack_linear(ops.np_to_dev(w, I8, device), ones)
             Mbits = int(M.max()).bit_length()
             return PackedLinear(wp, mp, N, K, bt, "channel", ops.np_to_dev(M, I64, device), Mbits)
 
         for i in range(cfg.NL):
-            L = dict(g1=ops.np_to_dev(arrays[f"{i}.g1"], I64, device), g2=ops.np_to_dev(arrays[f"{i}.g2"], I64, device),
-                     q=lin(f"{i}.q"), k=lin(f"{i}.k"), v=lin(f"{i}.v"), o=lin(f"{i}.o"), gate=lin(f"{i}.gate"),
-                     up=lin(f"{i}.up"), down=lin(f"{i}.down"))
+            L = dict(g1=ops.np_to_dev(arrays[f"{i}.g1"], I64, device), g2=ops.np_to_dev(arrays[f"{i}.g2"], I64, device))
+            if mode == "group":
+                L.update(qkv=group_lin([f"{i}.q", f"{i}.k", f"{i}.v"]), o=group_lin([f"{i}.o"]),
+                         gateup=group_lin([f"{i}.gate", f"{i}.up"]), down=group_lin([f"{i}.down"]))
+            else:
+                L.update({k: channel_lin(f"{i}.{k}") for k in ("q", "k", "v", "o", "gate", "up", "down")})
             self.layers.append(L)
         self.gf = ops.np_to_dev(arrays["gf"], I64, device)
         emb = np.asarray(arrays["emb"], np.int64)
         if np.abs(emb).max() >= 1 << 31:
             raise ExactError("embedding rows must fit int32")
         self.emb = ops.np_to_dev(emb, I32, device)
-        self.head = lin("head")
+        self.head = group_lin(["head"]) if mode == "group" else channel_lin("head")
         return self
+
+    @classmethod
+    def from_artifact(cls, path, device, verify=True):
+        """A model from an on-disk exact artifact (exact_amd.artifact; SPEC.md:7-12): integer weights, scales and
+        the shipped tables, each file checked against the manifest's SHA-256 first."""
+        from . import artifact
+        cfg, mode, arrays, tables = artifact.load(path, verify=verify)
+        return cls.from_arrays(cfg, arrays, device, mode=mode, tables=tables)
 
 
 class Cache:
@@ -192,7 +229,8 @@ class TModel:
         self.dev = weights.device
         self.abits = abits
         self.Smax, self.batch = Smax, batch
-        self.tab = DeviceTables(self.dev, Smax, c.hd, c.theta)
+        self.tab = DeviceTables(self.dev, Smax, c.hd, c.theta) if weights.tables is None else \
+            DeviceTables.from_host(self.dev, weights.tables, Smax, c.hd)
         self.nl = len(weights.layers)
         self.nq = (c.H + 2 * c.KV) * c.hd
         self.I = c.I if not c.moe else 1

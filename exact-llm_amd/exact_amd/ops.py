@@ -418,4 +418,7 @@ def _gemv_fake(x16, wT, Mg):
 
 
 def np_to_dev(a, dtype, device):
-    return torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dtype)
+    a = np.ascontiguousarray(a)
+    if not a.flags.writeable:     # a read-only memory map (an artifact file): one transient host copy
+        a = a.copy()
+    return torch.from_numpy(a).to(device=device, dtype=dtype)

@@ -163,6 +163,32 @@ def linear_specs(cfg, li):
     return s
 
 
+def arrays(cfg, seed):
+    """Host integer arrays (DeviceWeights.from_arrays layout) of the dense synthetic model (cfg, seed): the same
+    integers DeviceWeights.synthetic generates on the device."""
+    if cfg.moe:
+        raise ValueError("dense models only")
+    out = {}
+    for li in range(cfg.NL):
+        out[f"{li}.g1"] = vector_np(key(seed, f"L{li}.g1"), cfg.D, *GAIN)
+        out[f"{li}.g2"] = vector_np(key(seed, f"L{li}.g2"), cfg.D, *GAIN)
+        for name, N, K, bias in linear_specs(cfg, li):
+            short = name.split(".", 1)[1]
+            out[f"{li}.{short}.w"] = weights_np(key(seed, name + ".w"), N, K)
+            out[f"{li}.{short}.M"] = scales_np(key(seed, name + ".m"), N, K)
+            if bias:
+                out[f"{li}.{short}.b"] = vector_np(key(seed, name + ".b"), N, *BIAS)
+    ew, eM = weights_np(key(seed, "emb.w"), cfg.V, cfg.D), scales_np(key(seed, "emb.m"), cfg.V, cfg.D)
+    out["emb"] = embed_np(ew, eM)
+    out["gf"] = vector_np(key(seed, "gf"), cfg.D, *GAIN)
+    if cfg.tie:
+        out["head.w"], out["head.M"] = ew, eM
+    else:
+        out["head.w"] = weights_np(key(seed, "head.w"), cfg.V, cfg.D)
+        out["head.M"] = scales_np(key(seed, "head.m"), cfg.V, cfg.D)
+    return out
+
+
 def head_name(cfg):
     return "emb" if cfg.tie else "head"
 

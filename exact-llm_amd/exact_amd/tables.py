@@ -47,16 +47,38 @@ def inv_sqrt_hd(hd):
     return int(round((1 << 16) / math.sqrt(hd)))
 
 
+def host_tables(T, hd, theta):
+    """The tables of a model as host int64 arrays: exp, silu, sig, cos (T, hd), sin (T, hd)."""
+    c, s = rope(T, hd, theta)
+    return dict(exp=exp_t(), silu=silu_t(), sig=sig_t(), cos=c, sin=s)
+
+
 class DeviceTables:
     """The tables as int32 / int64 device tensors."""
 
     def __init__(self, device, T, hd, theta):
+        self._load(device, host_tables(T, hd, theta), T, hd)
+
+    @classmethod
+    def from_host(cls, device, tables, T, hd):
+        """From given integer tables (an artifact's): RoPE rows for at least T positions."""
+        self = cls.__new__(cls)
+        self._load(device, tables, T, hd)
+        return self
+
+    def _load(self, device, tab, T, hd):
         import torch
-        self.exp = torch.tensor(exp_t(), dtype=torch.int32, device=device)
-        self.silu = torch.tensor(silu_t(), dtype=torch.int32, device=device)
-        self.sig = torch.tensor(sig_t(), dtype=torch.int32, device=device)
-        c, s = rope(T, hd, theta)
-        self.cos = torch.tensor(c, dtype=torch.int64, device=device)
-        self.sin = torch.tensor(s, dtype=torch.int64, device=device)
+        from ._lib import ExactError
+        if len(tab["exp"]) != 256 * 40 + 2 or len(tab["silu"]) != 32 * 256 + 2 or len(tab["sig"]) != 32 * 256 + 2:
+            raise ExactError("table sizes differ from the spec's (exp 10242, silu and sig 8194 entries)")
+        if np.shape(tab["cos"])[0] < T or np.shape(tab["cos"])[1:] != (hd,) or np.shape(tab["sin"]) != np.shape(tab["cos"]):
+            raise ExactError(f"RoPE tables need ({T}, {hd}) rows")
+        if max(np.abs(np.asarray(tab[k], np.int64)).max() for k in ("exp", "silu", "sig")) >= 1 << 31:
+            raise ExactError("exp/silu/sig tables must fit int32")
+        self.exp = torch.tensor(np.asarray(tab["exp"], np.int64), dtype=torch.int32, device=device)
+        self.silu = torch.tensor(np.asarray(tab["silu"], np.int64), dtype=torch.int32, device=device)
+        self.sig = torch.tensor(np.asarray(tab["sig"], np.int64), dtype=torch.int32, device=device)
+        self.cos = torch.tensor(np.asarray(tab["cos"], np.int64)[:T], dtype=torch.int64, device=device)
+        self.sin = torch.tensor(np.asarray(tab["sin"], np.int64)[:T], dtype=torch.int64, device=device)
         self.T = T
         self.inv = inv_sqrt_hd(hd)
