@@ -3,6 +3,7 @@
 // primitives and exact_hip.h for the reference line each entry point replaces.
 #include "exact_common.h"
 #include "abi_util.h"
+#include "row_ops.h"
 
 namespace exact {
 
@@ -11,11 +12,6 @@ static char g_errbuf[256];
 void set_error(const char* where, hipError_t e) {
   snprintf(g_errbuf, sizeof(g_errbuf), "%s: %s", where, hipGetErrorString(e));
   g_err = g_errbuf;
-}
-
-template <typename T>
-__device__ __forceinline__ void store_q(void* xq, int64_t i, int64_t v) {
-  reinterpret_cast<T*>(xq)[i] = (T)v;
 }
 
 // qrow of a row held in `buf` (length K), writes xq / s for row r
@@ -94,74 +90,8 @@ template <int EPT>
 __global__ __launch_bounds__(1024) void k_rmsnorm_qrow(int64_t* __restrict__ x, int64_t* __restrict__ res_t,
                                                        const int32_t* __restrict__ res_s, const int64_t* __restrict__ g,
                                                        int bits, void* xq, int32_t* s, int D, int clear_t) {
-  __shared__ int red_a[16], red_c[16];
-  __shared__ int64_t red_b[16];
-  const int r = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
-  int64_t* xr = x + (int64_t)r * D;
-  int64_t* tr = res_t ? res_t + (int64_t)r * D : nullptr;
-  int64_t v[EPT], gv[EPT], rv[EPT];
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int i = tid + j * nt;
-    v[j] = 0; gv[j] = 0; rv[j] = 0;
-    if (i < D) {
-      v[j] = xr[i];
-      gv[j] = g[i];
-      if (tr) rv[j] = tr[i];
-    }
-  }
-  int m = 0;   // max bit length of |x|
-  const int sh = tr ? 28 - res_s[r] : 0;
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int i = tid + j * nt;
-    if (i < D) {
-      if (tr) {
-        v[j] = (int64_t)((uint64_t)v[j] + (uint64_t)shr64(rv[j], sh));
-        xr[i] = v[j];
-        if (clear_t) tr[i] = 0;
-      }
-      const int bl = bitlen64(abs64(v[j]));
-      m = bl > m ? bl : m;
-    }
-  }
-  m = block_max_i32(m, red_a);
-  int k = m - 24;
-  if (k < 0) k = 0;
-  int64_t ss = 0;
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int64_t xs = shr64(v[j], k);   // elements past D hold 0
-    ss = (int64_t)((uint64_t)ss + (uint64_t)(xs * xs));
-  }
-  ss = block_sum64_1(ss, red_b);
-  const int64_t ms = floordiv_pos(ss, D) + 1;   // ss >= 0 (a sum of squares; wraps only past 2^63, as numpy)
-  int64_t rt = isqrt64(ms);
-  if (rt < 1) rt = 1;
-  const int64_t den = shl64(rt, k);
-  const double rden = 1.0 / (double)den;
-  int m2 = 0;
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    v[j] = shr64(floordiv_rcp(shl64(v[j], EXACT_F), den, rden) * gv[j], EXACT_F);
-    const int bl = bitlen64(abs64(v[j]));
-    m2 = (tid + j * nt < D && bl > m2) ? bl : m2;
-  }
-  m2 = block_max_i32(m2, red_c);
-  int q = m2 - bits;
-  if (q < 0) q = 0;
-  const int64_t lim = (1LL << bits) - 1;
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int i = tid + j * nt;
-    if (i < D) {
-      int64_t w = shr64(v[j], q);
-      w = w > lim ? lim : (w < -lim ? -lim : w);
-      if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * D + i, w);
-      else store_q<int16_t>(xq, (int64_t)r * D + i, w);
-    }
-  }
-  if (tid == 0) s[r] = q;
+  __shared__ RowScratch sc;
+  rmsnorm_qrow_row<EPT>(blockIdx.x, x, res_t, res_s, g, bits, xq, s, D, clear_t, sc);
 }
 
 // Rows too long for one workgroup are split into slices of QSLICE elements; the producer kernel writes
