@@ -288,17 +288,20 @@ __device__ __forceinline__ int opaque(int x) {
 //   chain (1,0): read A0 (group g + 1)      rescale (0,1)
 //   chain (1,1): read B0 + scales (g + 1)   rescale (1,0)
 // so one barrier per group, and every LDS read overlaps matrix-core work.
-template <int WM, int WN, int S, bool PAIRS>
+// WIDE: scales M = mh * 2^15 + mp (mp in [0, 2^15)), both planes copied per group.
+template <int WM, int WN, int S, bool PAIRS, bool WIDE>
 __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __restrict__ xb, const int8_t* __restrict__ wp,
-                                                     const int16_t* __restrict__ mp, int64_t* __restrict__ t, int M,
-                                                     int N, int K, int G, int nbs, int tiles_m, int tiles_n,
-                                                     int ksplit, int use_atomic, const int64_t* __restrict__ colterm) {
+                                                     const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
+                                                     int64_t* __restrict__ t, int M, int N, int K, int G, int nbs,
+                                                     int tiles_m, int tiles_n, int ksplit, int use_atomic,
+                                                     const int64_t* __restrict__ colterm) {
   using C = GemmCfg<7, WM, WN, S>;
   static_assert(EXACT_TILE_GN, "the block's tiles of one group are contiguous in the group-major layout");
   static_assert(C::BN == 128, "one dword copy per lane covers the block's 128 scales");
-  constexpr int SM_BYTES = C::WAVES * 256;                  // each wave keeps its own copy of the scales
+  constexpr int SMW = WIDE ? 512 : 256;                     // each wave keeps its own copy of the scales
+  constexpr int SM_BYTES = C::WAVES * SMW;
   constexpr int STAGE = C::A_BYTES + C::B_BYTES + SM_BYTES;
-  constexpr int DPG = C::A_KB_PER_WAVE + C::B_KB_PER_WAVE + 1;   // copies per wave per group
+  constexpr int DPG = C::A_KB_PER_WAVE + C::B_KB_PER_WAVE + (WIDE ? 2 : 1);   // copies per wave per group
   extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -322,6 +325,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
   const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, (int)((uint32_t)M * (uint32_t)K), BUF_DW3);
   const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc((void*)wp, (short)0, -1, BUF_DW3);
   const __amdgpu_buffer_rsrc_t rM = __builtin_amdgcn_make_buffer_rsrc((void*)mp, (short)0, -1, BUF_DW3);
+  const __amdgpu_buffer_rsrc_t rMh = __builtin_amdgcn_make_buffer_rsrc((void*)(WIDE ? mh : mp), (short)0, -1, BUF_DW3);
   // per-lane copy offsets, fixed over the groups (the group enters as a scalar offset)
   uint32_t aoffs[C::A_KB_PER_WAVE];
 #pragma unroll
@@ -348,7 +352,10 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rB, (LDS void*)(sB + seg * 1024), 16, ln * 16,
                                                (tile0 + tl) * 8192 + (seg & 7) * 1024, 0, 0);
     }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rM, (LDS void*)(sB + C::B_BYTES + wave * 256), 4, moff, tile0 * 128, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rM, (LDS void*)(sB + C::B_BYTES + wave * SMW), 4, moff, tile0 * 128, 0, 0);
+    if constexpr (WIDE)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rMh, (LDS void*)(sB + C::B_BYTES + wave * SMW + 256), 4, moff, tile0 * 128, 0,
+                                               0);
   };
   // fragment reads; A chunk ks * 2 + lh of row r sits at a_off(r, lh) ^ (ks << 5) (XOR swizzle)
   auto readA = [&](v4i (&f)[4], int stg, int a, int ln) {
@@ -364,8 +371,10 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
     for (int ks = 0; ks < 4; ++ks) f[ks] = *reinterpret_cast<const v4i*>(base + ks * 2048);
   };
   auto readM = [&](int stg, int b, int ln) {
-    return (int)*reinterpret_cast<const int16_t*>(smem + stg * STAGE + C::A_BYTES + C::B_BYTES + wave * 256 +
-                                                  (wn * 64 + b * 32 + (ln & 31)) * 2);
+    const int8_t* p = smem + stg * STAGE + C::A_BYTES + C::B_BYTES + wave * SMW + (wn * 64 + b * 32 + (ln & 31)) * 2;
+    int m = (int)*reinterpret_cast<const int16_t*>(p);
+    if constexpr (WIDE) m |= (int)*reinterpret_cast<const int16_t*>(p + 256) << 15;
+    return m;
   };
   auto chain = [&](const v4i (&a)[4], const v4i (&b)[4]) {
     v16i c = {};
@@ -582,14 +591,15 @@ static int gemm_launch(const void* x, const int8_t* wp, const int16_t* mp, int64
 #endif
 
 // M: rows of the A operand (digit rows when PAIRS: the output has M / 2 rows, written through colterm)
-template <int WM, int WN, int S, bool PAIRS = false>
-static int gemm_launch_a8p(const void* x, const int8_t* wp, const int16_t* mp, int64_t* t, int M, int N, int K,
-                           hipStream_t st, int ksplit_req, const int64_t* colterm = nullptr) {
+template <int WM, int WN, int S, bool PAIRS, bool WIDE>
+static int gemm_launch_a8p_t(const void* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int M, int N,
+                             int K, hipStream_t st, int ksplit_req, const int64_t* colterm) {
   using C = GemmCfg<7, WM, WN, S>;
   static bool attr_set = false;
-  const size_t lds = S * (size_t)(C::A_BYTES + C::B_BYTES + C::WAVES * 256);
+  const size_t lds = S * (size_t)(C::A_BYTES + C::B_BYTES + C::WAVES * (WIDE ? 512 : 256));
+  static_assert(S * (C::A_BYTES + C::B_BYTES + C::WAVES * (WIDE ? 512 : 256)) <= 160 * 1024, "fits the 160 KiB LDS");
   if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_a8p<WM, WN, S, PAIRS>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_a8p<WM, WN, S, PAIRS, WIDE>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr_set = true;
   }
@@ -608,41 +618,52 @@ static int gemm_launch_a8p(const void* x, const int8_t* wp, const int16_t* mp, i
   }
   const int nblk = tiles_m * tiles_n * ksplit;
   const int grid = ((nblk + 7) / 8) * 8;
-  hipLaunchKernelGGL((k_gemm_a8p<WM, WN, S, PAIRS>), dim3(grid), dim3(C::THREADS), lds, st,
-                     reinterpret_cast<const int8_t*>(x), wp, mp, t, M, N, K, G, nbs, tiles_m, tiles_n, ksplit, use_atomic,
+  hipLaunchKernelGGL((k_gemm_a8p<WM, WN, S, PAIRS, WIDE>), dim3(grid), dim3(C::THREADS), lds, st,
+                     reinterpret_cast<const int8_t*>(x), wp, mp, mh, t, M, N, K, G, nbs, tiles_m, tiles_n, ksplit, use_atomic,
                      colterm);
   return launch_status("gemm_g128");
+}
+
+template <int WM, int WN, int S, bool PAIRS = false>
+static int gemm_launch_a8p(const void* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int M, int N,
+                           int K, hipStream_t st, int ksplit_req, const int64_t* colterm = nullptr) {
+  if (mh) return gemm_launch_a8p_t<WM, WN, S, PAIRS, true>(x, wp, mp, mh, t, M, N, K, st, ksplit_req, colterm);
+  return gemm_launch_a8p_t<WM, WN, S, PAIRS, false>(x, wp, mp, nullptr, t, M, N, K, st, ksplit_req, colterm);
 }
 
 #ifndef GEMM_A8P
 #define GEMM_A8P 1
 #endif
 
-int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, int64_t* t, int M, int N, int K,
-              hipStream_t st) {
+// Wide scales (mh) run on the A8 kernel only: int8 rows with M K < 2^32 (int16 rows take exact_gemm_g128_a16).
+int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int M, int N,
+              int K, hipStream_t st) {
+  const bool a8p = GEMM_A8P && abits == 7 && (int64_t)M * K < (1LL << 32);
+  if (mh && !a8p) return EXACT_E_UNSUPPORTED;
   if (abits == 15) return gemm_launch<15, GEMM_A16_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
-  if (GEMM_A8P && (int64_t)M * K < (1LL << 32)) return gemm_launch_a8p<GEMM_A8P_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
+  if (a8p) return gemm_launch_a8p<GEMM_A8P_CFG>(x, wp, mp, mh, t, M, N, K, st, GEMM_KSPLIT);
   return gemm_launch<7, GEMM_A8_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
 }
 
-int gemm_a16_digit_rows(const int16_t* x, const int8_t* wp, const int16_t* mp, const int64_t* colterm, int8_t* x8, int64_t* t,
-                        int M, int N, int K, hipStream_t st) {
+int gemm_a16_digit_rows(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, const int64_t* colterm,
+                        int8_t* x8, int64_t* t, int M, int N, int K, hipStream_t st) {
   const int64_t n16 = (int64_t)M * (K / 16);
   const int blocks = (int)std::min<int64_t>((n16 + 255) / 256, 8192);
   hipLaunchKernelGGL(k_split_rows_a16, dim3(blocks), dim3(256), 0, st, x, x8, (int64_t)M, K);
-  return gemm_launch_a8p<GEMM_A8P_CFG, true>(x8, wp, mp, t, 2 * M, N, K, st, GEMM_KSPLIT, colterm);
+  return gemm_launch_a8p<GEMM_A8P_CFG, true>(x8, wp, mp, mh, t, 2 * M, N, K, st, GEMM_KSPLIT, colterm);
 }
 
 }  // namespace exact
 
 using namespace exact;
 
-extern "C" int exact_gemm_g128_a16(const int16_t* x, const int8_t* wp, const int16_t* mp, const int64_t* colterm, int8_t* x8,
-                                   int64_t* t, int32_t R, int32_t N, int32_t K, void* stream) {
+extern "C" int exact_gemm_g128_a16(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                                   const int64_t* colterm, int8_t* x8, int64_t* t, int32_t R, int32_t N, int32_t K,
+                                   void* stream) {
   if (!x || !wp || !mp || !colterm || !x8 || !t || R <= 0 || N <= 0 || K <= 0) return EXACT_E_ARG;
   if (K % 128 || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(x8) & 15) ||
       (reinterpret_cast<uintptr_t>(wp) & 15))
     return EXACT_E_UNSUPPORTED;
   if (2 * (int64_t)R * K >= (1LL << 32)) return EXACT_E_UNSUPPORTED;   // 32-bit buffer offsets of the digit rows
-  return gemm_a16_digit_rows(x, wp, mp, colterm, x8, t, R, N, K, as_stream(stream));
+  return gemm_a16_digit_rows(x, wp, mp, mh, colterm, x8, t, R, N, K, as_stream(stream));
 }

@@ -45,14 +45,21 @@ struct GroupRegs {
   int m[4];
 };
 
-// xrow: this lane's activation row (any valid row when the lane's row is unused); valid: row < R
+// xrow: this lane's activation row (any valid row when the lane's row is unused); valid: row < R.
+// mh: NULL (int16 scales in mp) or the high plane of wide scales: M = mh * 2^15 + mp, mp in [0, 2^15).
 template <int ABITS, bool NT>
 __device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
-                                           const int8_t* __restrict__ xrow, bool valid, size_t tile, int g, int row, int c) {
+                                           const int16_t* __restrict__ mh, const int8_t* __restrict__ xrow, bool valid,
+                                           size_t tile, int g, int row, int c) {
   // issue order = use order (scales are read last but are tiny; tiles last so waiting on them drains the group)
   const int16_t* ms = mp + tile * 64 + row;
 #pragma unroll
   for (int q = 0; q < 4; ++q) G_.m[q] = ms[16 * q];
+  if (mh) {   // uniform over the launch
+    const int16_t* hs = mh + tile * 64 + row;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) G_.m[q] |= (int)hs[16 * q] << 15;
+  }
   const int kb = g * 128 + 16 * c;
   const v4i zero = {0, 0, 0, 0};
   if (ABITS == 15) {
@@ -122,24 +129,25 @@ __device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc
 // each wave keeps two tiles (16 KiB) in flight.
 template <int ABITS, bool NT, int VR>
 __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t* __restrict__ wp,
-                                            const int16_t* __restrict__ mp, const int8_t* __restrict__ xrow, bool valid,
-                                            int R, int nb, int nbs, int G, int g0, int g1, int row, int c, int lane) {
+                                            const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
+                                            const int8_t* __restrict__ xrow, bool valid, int R, int nb, int nbs, int G,
+                                            int g0, int g1, int row, int c, int lane) {
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
     for (int v = 0; v < VR; ++v) acc[q][v] = 0;
   if (g0 >= g1) return;
   GroupRegs ra, rb;
-  load_group<ABITS, NT>(ra, wp, mp, xrow, valid, tile_index(nb, g0, nbs, G), g0, row, c);
+  load_group<ABITS, NT>(ra, wp, mp, mh, xrow, valid, tile_index(nb, g0, nbs, G), g0, row, c);
   int g = g0;
   for (; g + 2 < g1; g += 2) {
-    load_group<ABITS, NT>(rb, wp, mp, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
+    load_group<ABITS, NT>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
     compute_group<ABITS, VR>(ra, acc, R, row, lane);
-    load_group<ABITS, NT>(ra, wp, mp, xrow, valid, tile_index(nb, g + 2, nbs, G), g + 2, row, c);
+    load_group<ABITS, NT>(ra, wp, mp, mh, xrow, valid, tile_index(nb, g + 2, nbs, G), g + 2, row, c);
     compute_group<ABITS, VR>(rb, acc, R, row, lane);
   }
   if (g + 1 < g1) {
-    load_group<ABITS, NT>(rb, wp, mp, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
+    load_group<ABITS, NT>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
     compute_group<ABITS, VR>(ra, acc, R, row, lane);
     compute_group<ABITS, VR>(rb, acc, R, row, lane);
   } else {
@@ -152,8 +160,9 @@ __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t*
 // out_mode 0: plain store (the wave owns all groups of its rows), 1: 64-bit atomic add.
 template <int ABITS, bool NT, int VR, int BW>
 __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ xv, const int8_t* __restrict__ wp,
-                                                       const int16_t* __restrict__ mp, int64_t* __restrict__ t, int R,
-                                                       int N, int K, int G, int nsplit, int out_mode) {
+                                                       const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
+                                                       int64_t* __restrict__ t, int R, int N, int K, int G, int nsplit,
+                                                       int out_mode) {
   const int lane = threadIdx.x & 63;
   const int task = blockIdx.x * BW + (threadIdx.x >> 6);
   const int nbs = (N + 63) >> 6;
@@ -166,7 +175,7 @@ __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ 
   const int8_t* xrow = reinterpret_cast<const int8_t*>(xv) + (size_t)(row < R ? row : 0) * xbytes;
 
   int64_t acc[4][VR];
-  gemv_groups<ABITS, NT, VR>(acc, wp, mp, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane);
+  gemv_groups<ABITS, NT, VR>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane);
 
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -216,7 +225,8 @@ __global__ __launch_bounds__(256) void k_gemv_experts(const void* __restrict__ x
   const int8_t* xrow = reinterpret_cast<const int8_t*>(xv) + (size_t)(row_map ? row_map[pr] : pr) * xbytes;
 
   int64_t acc[4][4];
-  gemv_groups<ABITS, NT, 4>(acc, wp + (size_t)e * w_stride, mp + (size_t)e * m_stride, xrow, row < R, R, nb, nbs, G, g0,
+  gemv_groups<ABITS, NT, 4>(acc, wp + (size_t)e * w_stride, mp + (size_t)e * m_stride, nullptr, xrow, row < R, R, nb, nbs,
+                            G, g0,
                             g1, row, c, lane);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -277,11 +287,11 @@ static int gemv_nsplit(int N, int G) {
 
 // accumulate: t += x.W (t holds the caller's running total, e.g. zeros left by a consumer kernel);
 // otherwise t is overwritten (zero-filled first when the row blocks are split).
-int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, int64_t* t, int M, int N, int K,
-              hipStream_t st);
+int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int M, int N,
+              int K, hipStream_t st);
 
-int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, int64_t* t, int R, int N, int K,
-                hipStream_t st, bool accumulate) {
+int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int R, int N,
+                int K, hipStream_t st, bool accumulate) {
   const int G = K / 128;
   const int nsplit = gemv_nsplit(N, G);
   const int out_mode = (accumulate || nsplit > 1) ? 1 : 0;
@@ -299,7 +309,7 @@ int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, i
   const int bw = wide ? 16 : 4;
   dim3 grid((tasks + bw - 1) / bw), block(64 * bw);
 #define GEMV_GO(AB, VR, BW) \
-  hipLaunchKernelGGL((k_gemv_g128<AB, GEMV_NT != 0, VR, BW>), grid, block, 0, st, x, wp, mp, t, R, N, K, G, nsplit, \
+  hipLaunchKernelGGL((k_gemv_g128<AB, GEMV_NT != 0, VR, BW>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, G, nsplit, \
                      out_mode)
   const int vr = R <= 1 ? 1 : (R <= 2 ? 2 : 4);
   if (abits == 15) {
@@ -330,36 +340,36 @@ extern "C" int exact_zero(void* dst, int64_t nbytes, void* stream) {
   return zero_bytes(dst, nbytes, as_stream(stream));
 }
 
-extern "C" int exact_gemv_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t, int32_t R,
-                               int32_t N, int32_t K, void* stream) {
+extern "C" int exact_gemv_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                               int64_t* t, int32_t R, int32_t N, int32_t K, void* stream) {
   int e = check_linear(x, abits, wp, mp, t, R, N, K);
   if (e) return e;
   const int rmax = abits == 15 ? 15 : 16;   // one A row is the all-ones colsum row in the A16 mode
   if (R > rmax) return EXACT_E_UNSUPPORTED;
-  return gemv_launch(x, abits, wp, mp, t, R, N, K, as_stream(stream), false);
+  return gemv_launch(x, abits, wp, mp, mh, t, R, N, K, as_stream(stream), false);
 }
 
-extern "C" int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
-                                   int32_t R, int32_t N, int32_t K, void* stream) {
+extern "C" int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                                   int64_t* t, int32_t R, int32_t N, int32_t K, void* stream) {
   int e = check_linear(x, abits, wp, mp, t, R, N, K);
   if (e) return e;
   if (R > (abits == 15 ? 15 : 16)) return EXACT_E_UNSUPPORTED;
-  return gemv_launch(x, abits, wp, mp, t, R, N, K, as_stream(stream), true);
+  return gemv_launch(x, abits, wp, mp, mh, t, R, N, K, as_stream(stream), true);
 }
 
-extern "C" int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t, int32_t R,
-                               int32_t N, int32_t K, void* stream) {
+extern "C" int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                               int64_t* t, int32_t R, int32_t N, int32_t K, void* stream) {
   int e = check_linear(x, abits, wp, mp, t, R, N, K);
   if (e) return e;
   const int rmax = abits == 15 ? 15 : 16;
-  if (R > GEMV_CHUNKS_MAX * rmax) return gemm_mfma(x, abits, wp, mp, t, R, N, K, as_stream(stream));
+  if (R > GEMV_CHUNKS_MAX * rmax) return gemm_mfma(x, abits, wp, mp, mh, t, R, N, K, as_stream(stream));
   // Up to GEMV_CHUNKS_MAX row chunks: one GEMV per chunk streams the weights once per chunk, which beats the
   // 128-row GEMM tiles (mostly padding at these R) while the weight passes stay few.
   const size_t xrow = (size_t)K * (abits == 15 ? 2 : 1);
   for (int r0 = 0; r0 < R; r0 += rmax) {
     const int rows = R - r0 < rmax ? R - r0 : rmax;
-    e = gemv_launch(static_cast<const int8_t*>(x) + r0 * xrow, abits, wp, mp, t + (size_t)r0 * N, rows, N, K, as_stream(stream),
-                    false);
+    e = gemv_launch(static_cast<const int8_t*>(x) + r0 * xrow, abits, wp, mp, mh, t + (size_t)r0 * N, rows, N, K,
+                    as_stream(stream), false);
     if (e) return e;
   }
   return EXACT_OK;

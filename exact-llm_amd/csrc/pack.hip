@@ -94,6 +94,19 @@ __global__ void k_pack(const int8_t* __restrict__ w, const int16_t* __restrict__
   }
 }
 
+// scales only: mp[tile * 64 + l] = m[g][n] (0 past N), the scale layout of k_pack
+__global__ void k_pack_scales(const int16_t* __restrict__ m, int16_t* __restrict__ mp, int N, int G, int64_t n,
+                              int nb_off, int64_t nbs_tot) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int l = (int)(i & 63);
+    const int64_t lt = i >> 6;
+    const int g = (int)(lt % G);
+    const int64_t nb = lt / G;
+    const int64_t col = nb * 64 + l;
+    mp[tile_index(nb + nb_off, g, nbs_tot, G) * 64 + l] = col < N ? m[(int64_t)g * N + col] : (int16_t)0;
+  }
+}
+
 // emb[v][k] = rint(W[v][k] * M[k/128][v] / 4096), round half to even
 __global__ void k_embed_table(const int8_t* __restrict__ wp, const int16_t* __restrict__ mp, int32_t* __restrict__ emb,
                               int V, int D, int G) {
@@ -162,6 +175,18 @@ extern "C" int exact_pack_linear(const int8_t* w_kn, const int16_t* m_gn, int8_t
   hipLaunchKernelGGL(k_pack, dim3(grid_for(nch)), dim3(256), 0, as_stream(stream), w_kn, m_gn, wp, mp, N, K, G, nch,
                      n_off / 64, cdiv(Ntot, 64));
   return launch_status("pack_linear");
+}
+
+extern "C" int exact_pack_scales(const int16_t* m_gn, int16_t* mp, int32_t N, int32_t K, int32_t n_off, int32_t Ntot,
+                                 void* stream) {
+  if (!m_gn || !mp) return EXACT_E_ARG;
+  int e = check_part(N, K, n_off, Ntot);
+  if (e) return e;
+  const int G = K / 128;
+  const int64_t n = cdiv(N, 64) * G * 64;
+  hipLaunchKernelGGL(k_pack_scales, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), m_gn, mp, N, G, n, n_off / 64,
+                     cdiv(Ntot, 64));
+  return launch_status("pack_scales");
 }
 
 extern "C" int exact_embed_table(const int8_t* wp, const int16_t* mp, int32_t* emb, int32_t V, int32_t D, void* stream) {

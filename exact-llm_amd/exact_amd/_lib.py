@@ -19,10 +19,11 @@ SIGNATURES = {
     "exact_synth_linear": [U64, U64, I32, I32, P, P, P, I32, I32, I32, I32, P],
     "exact_synth_vector": [U64, I64, I64, P, I64, P],
     "exact_pack_linear": [P, P, P, P, I32, I32, I32, I32, P],
-    "exact_gemv_g128": [P, I32, P, P, P, I32, I32, I32, P],
-    "exact_gemv_g128_acc": [P, I32, P, P, P, I32, I32, I32, P],
-    "exact_gemm_g128": [P, I32, P, P, P, I32, I32, I32, P],
-    "exact_gemm_g128_a16": [P, P, P, P, P, P, I32, I32, I32, P],
+    "exact_pack_scales": [P, P, I32, I32, I32, I32, P],
+    "exact_gemv_g128": [P, I32, P, P, P, P, I32, I32, I32, P],
+    "exact_gemv_g128_acc": [P, I32, P, P, P, P, I32, I32, I32, P],
+    "exact_gemm_g128": [P, I32, P, P, P, P, I32, I32, I32, P],
+    "exact_gemm_g128_a16": [P, P, P, P, P, P, P, I32, I32, I32, P],
     "exact_requant_group": [P, P, P, P, I32, I32, P],
     "exact_requant_channel": [P, P, P, I32, P, P, I32, I32, P],
     "exact_qrow": [P, I32, P, P, I32, I32, P],

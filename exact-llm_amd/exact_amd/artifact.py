@@ -89,6 +89,7 @@ def write(path, cfg, arrays, tables, mode="group"):
         architecture=dict(name=cfg.name, layers=cfg.NL, hidden=cfg.D, heads=cfg.H, kv_heads=cfg.KV, head_dim=cfg.hd,
                           intermediate=cfg.I, vocab=cfg.V, rope_theta=cfg.theta, tied_head=cfg.tie),
         linear_mode=mode,
+        head_mode="group" if np.ndim(arrays["head.M"]) == 2 else "channel",
         tables=dict(exp="Q24 exp(-i/256), i < 10242", silu="Q16 SiLU on [-16, 16) at 1/256 steps",
                     sig="Q16 sigmoid on [-16, 16) at 1/256 steps", cos="Q16 RoPE cos (T, hd)", sin="Q16 RoPE sin (T, hd)"),
         arrays=index,

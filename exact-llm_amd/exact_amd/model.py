@@ -117,8 +117,6 @@ class DeviceWeights:
             if any(w.shape[0] != K for w in ws) or any(M.shape != (K // 128, w.shape[1]) for w, M in zip(ws, Ms)):
                 raise ExactError(f"{pfxs}: weights (K, N) with group scales (K/128, N) expected")
             M = np.concatenate(Ms, 1)
-            if M.max() >= 1 << 15 or M.min() < 0:
-                raise ExactError("group scales must fit int16")
             w = np.concatenate(ws, 1)
             bs = [arrays.get(p + ".b") for p in pfxs]
             if any(b is not None for b in bs):
@@ -127,12 +125,11 @@ class DeviceWeights:
                 bt = ops.np_to_dev(b, I64, device)
             else:
                 bt = None
-            wp, mp = ops.pack_linear(ops.np_to_dev(w, I8, device), ops.np_to_dev(M, I16, device))
             parts, off = [], 0
             for p, w_ in zip(pfxs, ws):
                 parts.append((p.rsplit(".", 1)[-1], off, w_.shape[1]))
                 off += w_.shape[1]
-            return PackedLinear(wp, mp, w.shape[1], K, bt, parts=parts)
+            return ops.pack_group_linear(w, M, device, bt, parts)   # wide scales (>= 2^15) as two planes
 
         def channel_lin(pfx):
             w = np.asarray(arrays[pfx + ".w"])
@@ -158,7 +155,9 @@ class DeviceWeights:
         if np.abs(emb).max() >= 1 << 31:
             raise ExactError("embedding rows must fit int32")
         self.emb = ops.np_to_dev(emb, I32, device)
-        self.head = group_lin(["head"]) if mode == "group" else channel_lin("head")
+        # the head follows its scales: (G, N) group-128, (N,) per-channel (the reference's group engines keep a
+        # per-channel head, speed_fair_kaggle.py:780)
+        self.head = group_lin(["head"]) if np.ndim(arrays["head.M"]) == 2 else channel_lin("head")
         return self
 
     @classmethod
@@ -340,13 +339,16 @@ class TModel:
                 self._lin_channel(ws.hq, ws.sh, L["down"], ws.t_d)
                 res_t, res_s = ws.t_d, ws.s28
         ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=clear)
-        if group:
+        head = self.w.head
+        if head.mode == "group":
             t_head = slot("head") if keep else ws.t_head
-            self._lin(ws.xq, self.w.head, t_head)
+            self._lin(ws.xq, head, t_head)
             ops.logits_argmax(t_head, ws.s, ws.logits if want_logits else None, ws.next_ids, clear=clear,
                               part=ws.part_lg)
         else:
-            self._lin_channel(ws.xq, ws.s, self.w.head, ws.t_head)
+            # per-channel head: acc (the traced total), then the drop rule and M (exact_llm.py:89-96)
+            acc = ops.linear_t(ws.xq, self.abits, head, slot("head") if keep else None)
+            ops.requant_channel(acc, ws.s, head.M, head.Mbits, head.bias, out=ws.t_head)
             ops.logits_argmax(ws.t_head, ws.s28, ws.logits if want_logits else None, ws.next_ids, part=ws.part_lg)
         return ws
 

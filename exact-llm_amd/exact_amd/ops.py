@@ -42,10 +42,12 @@ def _need(t, dtype, name, numel=None):
 # ----------------------------------------------------------------------------- packed linears
 class PackedLinear:
     """A linear in the packed device layout: wp int8 [Np/64][G][8][64][16], mp int16 [Np/64][G][64].
+    Wide group scales (>= 2^15) add a high plane mh of the same layout: M = mh * 2^15 + mp.
     mode 'group': y = shr(t, 28 - s) + b; mode 'channel': M (N,) int64 with the per-row drop rule."""
 
-    def __init__(self, wp, mp, N, K, bias=None, mode="group", M=None, Mbits=None, parts=None):
+    def __init__(self, wp, mp, N, K, bias=None, mode="group", M=None, Mbits=None, parts=None, mh=None):
         self.wp, self.mp, self.N, self.K = wp, mp, N, K
+        self.mh = mh
         self.G = K // 128
         self.bias, self.mode, self.M, self.Mbits = bias, mode, M, Mbits
         # (name, first output column, width) of each linear fused into this one
@@ -85,6 +87,31 @@ def pack_linear(w_kn, m_gn, wp=None, mp=None, n_off=0, Ntot=None):
         wp, mp = PackedLinear.alloc(Ntot, K, w_kn.device)
     _lib.call("exact_pack_linear", _ptr(w_kn), _ptr(m_gn), _ptr(wp), _ptr(mp), N, K, n_off, Ntot, _stream())
     return wp, mp
+
+
+def pack_scales(m_gn, mp, N, K, n_off=0, Ntot=None):
+    """Pack (G, N) int16 values into the scale layout (the high plane of wide scales)."""
+    _need(m_gn, I16, "m_gn", (K // 128) * N)
+    _lib.call("exact_pack_scales", _ptr(m_gn), _ptr(mp), N, K, n_off, N if Ntot is None else Ntot, _stream())
+    return mp
+
+
+def pack_group_linear(w_kn, M_gn, device, bias=None, parts=None):
+    """PackedLinear of a (K, N) int8 weight (host array) with (G, N) non-negative integer group scales of any size
+    below 2^30: int16 scales when every M < 2^15, else the two planes M = mh * 2^15 + (M mod 2^15)."""
+    M = np.asarray(M_gn, np.int64)
+    K, N = np.shape(w_kn)
+    if M.shape != (K // 128, N) or K % 128:
+        raise ExactError(f"group scales of shape ({K // 128}, {N}) expected, got {M.shape}")
+    if M.min() < 0 or M.max() >= 1 << 30:
+        raise ExactError("group scales must lie in [0, 2^30)")
+    wide = M.max() >= 1 << 15
+    wp, mp = pack_linear(np_to_dev(w_kn, I8, device), np_to_dev(M & 0x7FFF if wide else M, I16, device))
+    mh = None
+    if wide:
+        mh = torch.empty_like(mp)
+        pack_scales(np_to_dev(M >> 15, I16, device), mh, N, K)
+    return PackedLinear(wp, mp, N, K, bias, parts=parts, mh=mh)
 
 
 # ----------------------------------------------------------------------------- linears
@@ -129,8 +156,8 @@ def gemm_g128(x, abits, lin, out=None):
     if ws is None or ws.numel() < 2 * R * K:
         ws = torch.empty(2 * R * K, dtype=I8, device=x.device)
         _DIGIT_ROWS[x.device] = ws
-    _lib.call("exact_gemm_g128_a16", _ptr(x), _ptr(lin.wp), _ptr(lin.mp), _ptr(ct), _ptr(ws), _ptr(out), R, lin.N, K,
-              _stream())
+    _lib.call("exact_gemm_g128_a16", _ptr(x), _ptr(lin.wp), _ptr(lin.mp), _ptr(lin.mh), _ptr(ct), _ptr(ws), _ptr(out), R,
+              lin.N, K, _stream())
     return out
 
 
@@ -153,7 +180,7 @@ def _linear(fn, x, abits, lin, out):
     if out is None:
         out = torch.empty((R, lin.N), dtype=I64, device=x.device)
     _need(out, I64, "out", R * lin.N)
-    _lib.call(fn, _ptr(x), abits, _ptr(lin.wp), _ptr(lin.mp), _ptr(out), R, lin.N, K, _stream())
+    _lib.call(fn, _ptr(x), abits, _ptr(lin.wp), _ptr(lin.mp), _ptr(lin.mh), _ptr(out), R, lin.N, K, _stream())
     return out
 
 

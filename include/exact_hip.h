@@ -55,24 +55,34 @@ int exact_synth_vector(uint64_t key, int64_t lo, int64_t hi, int64_t* out, int64
 int exact_pack_linear(const int8_t* w_kn, const int16_t* m_gn, int8_t* wp, int16_t* mp,
                       int32_t N, int32_t K, int32_t n_off, int32_t Ntot, void* stream);
 
+/* Repack (G, N) int16 values into the scale layout of exact_pack_linear alone: the high plane mh of wide
+ * scales (below). */
+int exact_pack_scales(const int16_t* m_gn, int16_t* mp, int32_t N, int32_t K, int32_t n_off, int32_t Ntot,
+                      void* stream);
+
 /* ---- linears ------------------------------------------------------------------------------------
- * Exact group-128 GEMV for decode, R <= 8 rows (one to eight tokens): t[r][n] = sum_g acc_g * M[g][n].
+ * Group scales: mh == NULL: M = mp, int16 in [0, 2^15). Wide scales (M < 2^30; quantised checkpoints give
+ * up to about 2^21, the reference asserts M < 2^27, group128_quality_kaggle.py:419): M = mh * 2^15 + mp
+ * with the low plane mp in [0, 2^15) and the high plane mh packed by exact_pack_scales.
+ *
+ * Exact group-128 GEMV for decode, R <= 15 (int16 x) or 16 (int8 x) rows: t[r][n] = sum_g acc_g * M[g][n].
  * abits = 15: x is int16 (xq from qrow(x, 15), the spec); abits = 7: x is int8 (exact_torch A8 mode).
  * Replaces the reference's exact::gemv op and its CUDA kernel gemv_g128_v2
- * (experiments/speed_fair_kaggle.py:656-702) and TLinG's R == 1 branch (:735-738), extended to R <= 8. */
-int exact_gemv_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
+ * (experiments/speed_fair_kaggle.py:656-702) and TLinG's R == 1 branch (:735-738), extended to R rows. */
+int exact_gemv_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,
                     int32_t R, int32_t N, int32_t K, void* stream);
 
 /* Accumulating form: t[r][n] += sum_g acc_g * M[g][n]. No counterpart in the reference; used by fused
  * decode steps whose consumer kernels leave t zeroed after reading it, so no zero-fill launch is needed. */
-int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
+int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,
                         int32_t R, int32_t N, int32_t K, void* stream);
 
 /* Exact group-128 GEMM for prefill (any R): same output as exact_gemv_g128. Up to 3 x 15 rows (A16) or
- * 3 x 16 rows (A8) run as row chunks of the GEMV kernel, more rows on the MFMA GEMM kernels.
+ * 3 x 16 rows (A8) run as row chunks of the GEMV kernel, more rows on the MFMA GEMM kernels (wide scales:
+ * int8 x only there; int16 x with wide scales takes exact_gemm_g128_a16, else 2 is returned).
  * Replaces TLinG's R > 1 fp64 bmm branch (speed_fair_kaggle.py:739-742) and TLin._acc's
  * torch._int_mm A16/A8 passes (exact_torch.py:94-119). */
-int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, int64_t* t,
+int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,
                     int32_t R, int32_t N, int32_t K, void* stream);
 
 /* The int16 (A16) GEMM on the int8 matrix cores as interleaved digit rows: x is split into rows
@@ -81,8 +91,8 @@ int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_
  * colterm[n] = sum_g (sum_{k in g} W[k][n]) * M[g][n]: exact_gemv_g128 of an all-ones int8 row (A8) gives it,
  * once per linear. x8: caller workspace of 2 R K bytes (16-byte aligned). Same output as exact_gemm_g128
  * with abits 15; 2 R K < 2^32. */
-int exact_gemm_g128_a16(const int16_t* x, const int8_t* wp, const int16_t* mp, const int64_t* colterm, int8_t* x8,
-                        int64_t* t, int32_t R, int32_t N, int32_t K, void* stream);
+int exact_gemm_g128_a16(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, const int64_t* colterm,
+                        int8_t* x8, int64_t* t, int32_t R, int32_t N, int32_t K, void* stream);
 
 /* Group epilogue y = round_shift(t, 28 - s[r]) + b[n] (b may be NULL)
  * (speed_fair_kaggle.py:725,743; SPEC.md:18). */

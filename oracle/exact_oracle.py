@@ -22,6 +22,9 @@ Pinning (what checks each function against something other than this file):
                                         SIG_T has no reference-held vector: parity unpinned beyond its closed form
   * sampler (splitmix64, sample_int) -> known-answer values of splitmix64 from its published
                                         definition + brute-force inverse CDF
+  * quantize_channel / quantize_group -> closed-form properties (the column / group maximum maps to
+                                        +-127 exactly, |w - w8 sc| <= sc / 2, M = rint(sc 2^28), zero
+                                        columns give w8 = 0, M = 0) checked on random and constructed inputs
 """
 import hashlib
 import math
@@ -275,6 +278,35 @@ class Lin:
         if self.mode == "group":
             return linear_group(x, self.w, self.M, self.b, abits)
         return linear_channel(x, self.w, self.M, self.b, abits)
+
+
+# ----------------------------------------------------------------------------- float checkpoint -> integers
+def quantize_channel(w_in_out):
+    """Per-channel quantisation of a float (in, out) weight (QLin.__init__, exact_llm.py:83-86), float64:
+    sc = max_k |w[k, n]| (1e-12 for an all-zero column) / 127; w8 = clip(rint(w / sc), -127, 127) int8;
+    M = rint(sc * 2^28) int64."""
+    w = np.asarray(w_in_out, np.float64)
+    sc = np.abs(w).max(0)
+    sc = np.where(sc == 0, 1e-12, sc) / 127.0
+    return np.clip(np.rint(w / sc), -127, 127).astype(np.int8), np.rint(sc * (1 << 28)).astype(I64)
+
+
+def quantize_group(w_in_out, G=128):
+    """Group-128 quantisation (GQLin.__init__, speed_fair_kaggle.py:715-721; the reference takes the (out, in)
+    checkpoint array and transposes it first): the per-channel rule of quantize_channel applied to every
+    128-row group of the (in, out) weight; M (K/G, N)."""
+    w = np.asarray(w_in_out, np.float64)
+    K, N = w.shape
+    w8 = np.empty((K, N), np.int8)
+    M = np.empty((-(-K // G), N), I64)
+    for gi, a in enumerate(range(0, K, G)):
+        w8[a:a + G], M[gi] = quantize_channel(w[a:a + G])
+    return w8, M
+
+
+def q16(v):
+    """Q16 integers of float64 values (norm gains, biases, embedding rows: exact_llm.py:85-87, 143, 163)."""
+    return np.rint(np.asarray(v, np.float64) * ONE).astype(I64)
 
 
 # ----------------------------------------------------------------------------- attention

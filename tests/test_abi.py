@@ -32,11 +32,11 @@ def test_library_exports_every_declared_symbol():
 def test_host_side_validation_rejects_bad_shapes_without_launching():
     """Argument checks happen on the host: null pointers and unsupported K return codes, no GPU needed."""
     lib = _lib.load()
-    assert lib.exact_gemv_g128(None, 15, None, None, None, 1, 64, 128, None) == 1
+    assert lib.exact_gemv_g128(None, 15, None, None, None, None, 1, 64, 128, None) == 1
     fake = 1 << 20   # never dereferenced: validation fails before any launch
-    assert lib.exact_gemv_g128(fake, 15, fake, fake, fake, 1, 64, 100, None) == 2      # K % 128
-    assert lib.exact_gemv_g128(fake, 9, fake, fake, fake, 1, 64, 128, None) == 2       # abits
-    assert lib.exact_gemv_g128(fake, 15, fake, fake, fake, 16, 64, 128, None) == 2     # R > 15 in A16
+    assert lib.exact_gemv_g128(fake, 15, fake, fake, None, fake, 1, 64, 100, None) == 2      # K % 128
+    assert lib.exact_gemv_g128(fake, 9, fake, fake, None, fake, 1, 64, 128, None) == 2       # abits
+    assert lib.exact_gemv_g128(fake, 15, fake, fake, None, fake, 16, 64, 128, None) == 2     # R > 15 in A16
     assert lib.exact_synth_linear(1, 2, 0, 40000, fake, fake, fake, 64, 128, 0, 64, None) == 1  # scale range
     assert lib.exact_synth_linear(1, 2, 1, 400, fake, fake, fake, 64, 128, 32, 128, None) == 2  # part offset % 64
     assert lib.exact_attention(fake, fake, fake, fake, fake, fake, fake, fake, fake, None, 1, 4, 2, 96, 64, 8192, None) == 2

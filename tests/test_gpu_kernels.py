@@ -216,3 +216,32 @@ def test_swiglu_qrow(R, I, bits):
     assert np.array_equal(host(hq).astype(np.int64), eq) and np.array_equal(host(sh), es[:, 0])
     assert np.array_equal(host(td), t)
 
+
+
+@pytest.mark.parametrize("abits", [15, 7])
+@pytest.mark.parametrize("R,N,K,mbits", [(1, 3584, 3584, 21), (5, 896, 4864, 27), (16, 500, 1408, 30), (46, 640, 896, 22),
+                                         (130, 1000, 2048, 21)])
+def test_wide_group_scales(abits, R, N, K, mbits):
+    """Group scales beyond int16 (quantised checkpoints give M up to about 2^21; the reference allows < 2^27) as two
+    planes M = mh * 2^15 + low: GEMV, chunked GEMV and GEMM (A8, and A16 as digit rows) equal the int64 numpy sum
+    (which wraps as the kernels do)."""
+    w = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    M = rng.integers(0, 1 << mbits, (K // 128, N))
+    M[0, :3] = [0, (1 << 15) - 1, 1 << 15]
+    lin = ops.pack_group_linear(w, M, DEV)
+    assert lin.mh is not None
+    lim = (1 << abits) - 1
+    xq = rng.integers(-lim, lim + 1, (R, K))
+    xq[0, :2] = [lim, -lim]
+    t = ops.linear_t(dev(xq, I16 if abits == 15 else I8), abits, lin)
+    assert np.array_equal(host(t), oracle_t(xq, w, M)), (R, abits)
+
+
+def test_wide_scales_a16_generic_gemm_entry_is_refused():
+    """The generic GEMM entry with int16 rows above the GEMV sizes runs the legacy A16 kernel, which takes int16 scales
+    only: with a high plane it returns 'unsupported' (the digit-row entry, which ops uses, covers it)."""
+    K, N, R = 256, 64, 60
+    lin = ops.pack_group_linear(rng.integers(-127, 128, (K, N)).astype(np.int8), rng.integers(1 << 15, 1 << 20, (2, N)), DEV)
+    x = dev(rng.integers(-100, 100, (R, K)), I16)
+    with pytest.raises(ops.ExactError, match="unsupported"):
+        ops._linear("exact_gemm_g128", x, 15, lin, None)
