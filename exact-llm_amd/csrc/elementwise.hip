@@ -388,9 +388,14 @@ extern "C" int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res
 
 extern "C" int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq, int32_t* sq,
                                  int32_t* part, int32_t R, int32_t I, int32_t clear_t, int64_t* h, void* stream) {
-  if (!t || !s || !silu_t || !xq || !sq || !part || R <= 0 || I <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
-  if (h == t) return EXACT_E_ARG;
+  if (!t || !s || !silu_t || !part || R <= 0 || I <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
+  if (h == t || (!xq && !h) || (xq && !sq)) return EXACT_E_ARG;
   hipStream_t st = as_stream(stream);
+  if (!xq) {   // h and the slice bit lengths only: the consumer quantises (exact_gemv_g128_qrow_acc)
+    const int np = (I + QSLICE - 1) / QSLICE;
+    hipLaunchKernelGGL(k_swiglu_part, dim3(np, R), dim3(256), 0, st, t, s, silu_t, part, I, np, clear_t, h);
+    return launch_status("swiglu_qrow");
+  }
   const int nt = I >= 1024 ? 1024 : ((I + 63) / 64) * 64;
   const int ept = (I + nt - 1) / nt;
 #define SWG_GO(E) hipLaunchKernelGGL(k_swiglu_qrow_row<E>, dim3(R), dim3(nt), 0, st, t, s, silu_t, bits, xq, sq, I, clear_t)

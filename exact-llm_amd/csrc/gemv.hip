@@ -45,13 +45,11 @@ struct GroupRegs {
   int m[4];
 };
 
-// xrow: this lane's activation row (any valid row when the lane's row is unused); valid: row < R.
-// mh: NULL (int16 scales in mp) or the high plane of wide scales: M = mh * 2^15 + mp, mp in [0, 2^15).
-template <int ABITS, bool NT>
-__device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
-                                           const int16_t* __restrict__ mh, const int8_t* __restrict__ xrow, bool valid,
-                                           size_t tile, int g, int row, int c) {
-  // issue order = use order (scales are read last but are tiny; tiles last so waiting on them drains the group)
+// Scales and weight tile of one group. mh: NULL (int16 scales in mp) or the high plane of wide scales:
+// M = mh * 2^15 + mp, mp in [0, 2^15).
+template <bool NT>
+__device__ __forceinline__ void load_w(GroupRegs& G_, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                       const int16_t* __restrict__ mh, size_t tile, int row, int c) {
   const int16_t* ms = mp + tile * 64 + row;
 #pragma unroll
   for (int q = 0; q < 4; ++q) G_.m[q] = ms[16 * q];
@@ -60,6 +58,20 @@ __device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restri
 #pragma unroll
     for (int q = 0; q < 4; ++q) G_.m[q] |= (int)hs[16 * q] << 15;
   }
+  const v4i* tp = reinterpret_cast<const v4i*>(wp + tile * 8192 + c * 1024 + row * 16);
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const v4i* a = tp + (4 * h * 1024 + 16 * q * 16) / 16;
+      G_.b[4 * h + q] = NT ? __builtin_nontemporal_load(a) : *a;
+    }
+}
+
+// A-operand bytes of group g. xrow: this lane's activation row (any valid row when the lane's row is unused);
+// valid: row < R. xrow may point into LDS (a wave's quantised slice, offset so that group g sits at g * 128).
+template <int ABITS>
+__device__ __forceinline__ void load_x(GroupRegs& G_, const int8_t* xrow, bool valid, int g, int c) {
   const int kb = g * 128 + 16 * c;
   const v4i zero = {0, 0, 0, 0};
   if (ABITS == 15) {
@@ -78,14 +90,15 @@ __device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restri
     for (int h = 0; h < 2; ++h) G_.xa[h] = *reinterpret_cast<const v4i*>(xp + 64 * h);
     if (!valid) G_.xa[0] = G_.xa[1] = zero;
   }
-  const v4i* tp = reinterpret_cast<const v4i*>(wp + tile * 8192 + c * 1024 + row * 16);
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const v4i* a = tp + (4 * h * 1024 + 16 * q * 16) / 16;
-      G_.b[4 * h + q] = NT ? __builtin_nontemporal_load(a) : *a;
-    }
+}
+
+// issue order: scales, activations, then the tile (waiting on the tile drains the group)
+template <int ABITS, bool NT>
+__device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                           const int16_t* __restrict__ mh, const int8_t* xrow, bool valid,
+                                           size_t tile, int g, int row, int c) {
+  load_x<ABITS>(G_, xrow, valid, g, c);
+  load_w<NT>(G_, wp, mp, mh, tile, row, c);
 }
 
 template <int ABITS, int VR>
@@ -127,18 +140,29 @@ __device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc
 // The group loop of one wave over groups [g0, g1) of row block nb. The next group's loads are issued
 // before the current group's matrix-core work and every load is unconditional inside the loop, so
 // each wave keeps two tiles (16 KiB) in flight.
-template <int ABITS, bool NT, int VR>
+// pro: run after the first group's weight tile is in flight and before its activations are read (the
+// quantising GEMV fills its LDS slice there).
+struct NoPrologue {
+  __device__ void operator()() const {}
+};
+
+template <int ABITS, bool NT, int VR, typename Pro = NoPrologue>
 __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t* __restrict__ wp,
                                             const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
-                                            const int8_t* __restrict__ xrow, bool valid, int R, int nb, int nbs, int G,
-                                            int g0, int g1, int row, int c, int lane) {
+                                            const int8_t* xrow, bool valid, int R, int nb, int nbs, int G,
+                                            int g0, int g1, int row, int c, int lane, Pro pro = Pro()) {
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
     for (int v = 0; v < VR; ++v) acc[q][v] = 0;
-  if (g0 >= g1) return;
+  if (g0 >= g1) {
+    pro();
+    return;
+  }
   GroupRegs ra, rb;
-  load_group<ABITS, NT>(ra, wp, mp, mh, xrow, valid, tile_index(nb, g0, nbs, G), g0, row, c);
+  load_w<NT>(ra, wp, mp, mh, tile_index(nb, g0, nbs, G), row, c);
+  pro();
+  load_x<ABITS>(ra, xrow, valid, g0, c);
   int g = g0;
   for (; g + 2 < g1; g += 2) {
     load_group<ABITS, NT>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
@@ -190,6 +214,75 @@ __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ 
         else
           *dst = acc[q][v];
       }
+    }
+  }
+}
+
+// int64 activations each lane loads per row in the quantising GEMV: a wave's slice holds up to 64 * XQ_LOADS columns
+#define XQ_LOADS 8
+
+// GEMV whose int16 / int8 activations are quantised from int64 rows on the fly (qrow, exact_llm.py:41-46): row r's
+// shift is s = max(bitlen(max |x_r|) - abits, 0), with bitlen(max |x_r|) = max_i part[r * nparts + i] as the producer
+// kernel wrote it (attention's per-head bit lengths, or SwiGLU's per-slice ones). Each wave quantises the columns of
+// its own groups into LDS (xs[r][g0 * 128 ...g1 * 128), clipped to +-(2^abits - 1)) and runs the group loop on them;
+// block 0 writes s_out. Replaces a k_quant_rows launch + GEMV pair. t += x.W (accumulate).
+template <int ABITS, bool NT, int VR>
+__global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict__ xs, int64_t ldx,
+                                                      const int32_t* __restrict__ part, int nparts,
+                                                      const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                                      const int16_t* __restrict__ mh, int64_t* __restrict__ t,
+                                                      int32_t* __restrict__ s_out, int R, int N, int K, int G, int nsplit,
+                                                      int gmax) {
+  extern __shared__ __attribute__((aligned(16))) int8_t xlds[];
+  constexpr int EB = ABITS == 15 ? 2 : 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int task = blockIdx.x * 4 + wave;
+  const int nbs = (N + 63) >> 6;
+  if (task >= nbs * nsplit) return;   // no block-wide barrier below
+  const int nb = task / nsplit, sp = task - nb * nsplit;
+  const int g0 = (int)(((int64_t)sp * G) / nsplit);
+  const int g1 = (int)(((int64_t)(sp + 1) * G) / nsplit);
+  const int ncol = (g1 - g0) * 128;
+  const int rowb = gmax * 128 * EB;                       // LDS bytes per row of a wave's slice
+  int8_t* mine = xlds + (size_t)wave * R * rowb;
+  // quantise this wave's columns of every row: the row's slice bit lengths and its values are loaded together
+  auto quantise = [&]() {
+    const int64_t lim = (1LL << ABITS) - 1;
+    for (int r = 0; r < R; ++r) {
+      const int pv = lane < nparts ? part[(int64_t)r * nparts + lane] : 0;
+      const int64_t* src = xs + (int64_t)r * ldx + (int64_t)g0 * 128;
+      int64_t xv[XQ_LOADS];
+#pragma unroll
+      for (int j = 0; j < XQ_LOADS; ++j) xv[j] = lane + 64 * j < ncol ? src[lane + 64 * j] : 0;
+      const int m = wave_max_i32(pv);
+      const int sh = m - ABITS > 0 ? m - ABITS : 0;
+      if (blockIdx.x == 0 && wave == 0 && lane == 0) s_out[r] = sh;
+#pragma unroll
+      for (int j = 0; j < XQ_LOADS; ++j) {
+        const int i = lane + 64 * j;
+        if (i < ncol) {
+          int64_t q = shr64(xv[j], sh);
+          q = q > lim ? lim : (q < -lim ? -lim : q);
+          if (ABITS == 15) reinterpret_cast<int16_t*>(mine + (size_t)r * rowb)[i] = (int16_t)q;
+          else mine[(size_t)r * rowb + i] = (int8_t)q;
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done (wave-private region)
+    __builtin_amdgcn_wave_barrier();
+  };
+  const int row = lane & 15, c = lane >> 4;
+  // group g's columns sit at (g - g0) * 128 of the slice: offset the row base back by g0 * 128 elements
+  const int8_t* xrow = mine + (size_t)(row < R ? row : 0) * rowb - (ptrdiff_t)g0 * 128 * EB;
+  int64_t acc[4][VR];
+  gemv_groups<ABITS, NT, VR>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane, quantise);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = nb * 64 + 16 * q + row;
+#pragma unroll
+    for (int v = 0; v < VR; ++v) {
+      const int r = 4 * c + v;
+      if (r < R && n < N) atomicAdd(reinterpret_cast<unsigned long long*>(t + (size_t)r * N + n), (unsigned long long)acc[q][v]);
     }
   }
 }
@@ -355,6 +448,37 @@ extern "C" int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* w
   if (e) return e;
   if (R > (abits == 15 ? 15 : 16)) return EXACT_E_UNSUPPORTED;
   return gemv_launch(x, abits, wp, mp, mh, t, R, N, K, as_stream(stream), true);
+}
+
+// LDS of the quantised slices: 4 waves x R rows x gmax groups x 128 values
+#define GEMV_XQ_LDS_MAX (64 * 1024)
+
+extern "C" int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const int32_t* part, int32_t nparts, int32_t abits,
+                                        const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int32_t* s_out,
+                                        int32_t R, int32_t N, int32_t K, void* stream) {
+  if (!xs || !part || !wp || !mp || !t || !s_out || R <= 0 || N <= 0 || K <= 0 || nparts <= 0 || ldx < K)
+    return EXACT_E_ARG;
+  if ((abits != 15 && abits != 7) || K % 128 || (reinterpret_cast<uintptr_t>(wp) & 15)) return EXACT_E_UNSUPPORTED;
+  if (R > (abits == 15 ? 15 : 16)) return EXACT_E_UNSUPPORTED;
+  const int G = K / 128;
+  const int nsplit = gemv_nsplit(N, G);
+  const int gmax = (G + nsplit - 1) / nsplit;
+  const size_t lds = (size_t)4 * R * gmax * 128 * (abits == 15 ? 2 : 1);
+  if (lds > GEMV_XQ_LDS_MAX || gmax * 128 > 64 * XQ_LOADS || nparts > 64) return EXACT_E_UNSUPPORTED;
+  const int tasks = ((N + 63) / 64) * nsplit;
+  dim3 grid((tasks + 3) / 4), block(256);
+  hipStream_t st = as_stream(stream);
+#define XQ_GO(AB, VR)                                                                                                 \
+  hipLaunchKernelGGL((k_gemv_g128_xq<AB, GEMV_NT != 0, VR>), grid, block, lds, st, xs, ldx, part, nparts, wp, mp, mh, t, \
+                     s_out, R, N, K, G, nsplit, gmax)
+  const int vr = R <= 1 ? 1 : (R <= 2 ? 2 : 4);
+  if (abits == 15) {
+    if (vr == 1) XQ_GO(15, 1); else if (vr == 2) XQ_GO(15, 2); else XQ_GO(15, 4);
+  } else {
+    if (vr == 1) XQ_GO(7, 1); else if (vr == 2) XQ_GO(7, 2); else XQ_GO(7, 4);
+  }
+#undef XQ_GO
+  return launch_status("gemv_g128_qrow_acc");
 }
 
 extern "C" int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh,

@@ -241,6 +241,7 @@ class TModel:
         return Cache(self.cfg, self.batch if B is None else B, self.Smax, self.dev, self.nl)
 
     PREFILL_MIN_ROWS = 32
+    QROW_FUSE_ROWS = 2
 
     def _prefill_ws(self, R):
         if self._pws is None or self._pws[0] < R:
@@ -283,6 +284,12 @@ class TModel:
             tbuf.zero_()
             slot = lambda key: layout.slot(tbuf, key)
         clear = group and not keep
+        # decode passes of up to QROW_FUSE_ROWS rows: the o and down GEMVs quantise their int64 inputs themselves (no
+        # qrow launch); every 64-row block of the GEMV re-reads its slice of the row, which costs more than the saved
+        # launch at 8 rows
+        xfuse = group and R <= self.QROW_FUSE_ROWS
+        if xfuse and ws.h is None and c.I > 8192 and not c.moe:
+            ws.h = torch.zeros((R, ws.I), dtype=I64, device=self.dev)
         ops.embed(ws.ids, self.w.emb, ws.x)
         res_t, res_s = None, None
         for li, L in enumerate(self.w.layers):
@@ -310,9 +317,13 @@ class TModel:
                                       self._prefill_ws(R), ws.obits)
             else:
                 ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv, ws.obits)
-            ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa)
+            if xfuse:
+                ops.gemv_qrow_acc(ws.att, ws.obits, H, self.abits, L["o"], t_o, ws.sa)
+            else:
+                ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa)
             if group:
-                self._lin(ws.aq, L["o"], t_o)
+                if not xfuse:
+                    self._lin(ws.aq, L["o"], t_o)
                 ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, t_o, ws.sa, ws.xq, ws.s, clear=clear)
             else:
                 self._lin_channel(ws.aq, ws.sa, L["o"], ws.t_o)
@@ -325,9 +336,13 @@ class TModel:
                 continue
             if group:
                 self._lin(ws.xq, L["gateup"], t_gu)
-                ops.swiglu_qrow(t_gu, ws.s, tab.silu, self.abits, ws.hq, ws.sh, clear=clear, part=ws.part_sw,
-                                h=ws.h if keep else None)
-                self._lin(ws.hq, L["down"], t_d)
+                if xfuse and c.I > 8192:   # rows beyond one workgroup: SwiGLU slices, then the down GEMV quantises
+                    ops.swiglu_part(t_gu, ws.s, tab.silu, ws.h, ws.part_sw, clear=clear)
+                    ops.gemv_qrow_acc(ws.h, ws.part_sw, -(-c.I // ops.QSLICE), self.abits, L["down"], t_d, ws.sh)
+                else:
+                    ops.swiglu_qrow(t_gu, ws.s, tab.silu, self.abits, ws.hq, ws.sh, clear=clear, part=ws.part_sw,
+                                    h=ws.h if keep else None)
+                    self._lin(ws.hq, L["down"], t_d)
                 res_t, res_s = t_d, ws.sh
             else:
                 I = L["gate"].N

@@ -125,6 +125,22 @@ def gemv_g128_acc(x, abits, lin, out):
     return _linear("exact_gemv_g128_acc", x, abits, lin, out)
 
 
+def gemv_qrow_acc(xs, part, nparts, abits, lin, out, s_out, K=None):
+    """out (R, N) += qrow(xs[:, :K], abits) . W in one launch, the row shifts from the producer's slice bit lengths
+    part (R, nparts); s_out (R,) int32 receives the shifts. xs: int64 (R, ldx)."""
+    R, ldx = xs.shape
+    K = lin.K if K is None else K
+    if K != lin.K:
+        raise ExactError(f"gemv_qrow_acc: K = {K}, linear has K = {lin.K}")
+    _need(xs, I64, "xs")
+    _need(part, I32, "part", R * nparts)
+    _need(out, I64, "out", R * lin.N)
+    _need(s_out, I32, "s_out", R)
+    _lib.call("exact_gemv_g128_qrow_acc", _ptr(xs), ldx, _ptr(part), nparts, abits, _ptr(lin.wp), _ptr(lin.mp), _ptr(lin.mh),
+              _ptr(out), _ptr(s_out), R, lin.N, K, _stream())
+    return out
+
+
 GEMV_CHUNK_ROWS = {15: 45, 7: 48}   # up to 3 GEMV row chunks (exact_gemm_g128 runs those as GEMVs)
 _DIGIT_ROWS = {}                     # device -> int8 workspace of the A16 digit rows
 
@@ -233,6 +249,16 @@ QSLICE, LSLICE = 1024, 4096   # row slice lengths of the multi-block row kernels
 
 def swiglu_parts(R, I, device):
     return torch.empty(R * -(-I // QSLICE), dtype=I32, device=device)
+
+
+def swiglu_part(t, s, silu, h, part, clear=False):
+    """h (R, I) = SwiGLU of the gate|up totals and part = bit lengths of max |h| per 1024-column slice, without the
+    qrow (the consumer GEMV quantises: gemv_qrow_acc)."""
+    R, N2 = t.shape
+    I = N2 // 2
+    _lib.call("exact_swiglu_qrow", _ptr(_need(t, I64, "t")), _ptr(s), _ptr(silu), 15, None, None,
+              _ptr(_need(part, I32, "part", R * -(-I // QSLICE))), R, I, int(clear), _ptr(_need(h, I64, "h", R * I)), _stream())
+    return h, part
 
 
 def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None, clear=False, part=None, h=None):

@@ -85,6 +85,17 @@ int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const in
 int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,
                     int32_t R, int32_t N, int32_t K, void* stream);
 
+/* qrow fused into the GEMV that consumes it: t += qrow(xs, abits) . W (t holds zeros or a running total), where
+ * row r of xs (int64, ldx apart) is quantised with s = max(max_i part[r * nparts + i] - abits, 0) and
+ * part holds the producer's bit lengths of max |xs| over slices of the row (exact_attention's per-head
+ * obits, exact_swiglu_qrow's slice bit lengths); s_out[r] = s. Replaces exact_quant_rows + exact_gemv_g128_acc
+ * (qrow, exact_llm.py:41-46; TLinG, speed_fair_kaggle.py:735-738) with one launch. R <= 15 (abits 15) or
+ * 16 (abits 7), nparts <= 64; returns 2 when a wave's share of a row exceeds 512 columns (the GEMV's group
+ * split leaves 4 groups or fewer per wave at the decode shapes) or the slices of a block 64 KiB of LDS. */
+int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const int32_t* part, int32_t nparts, int32_t abits,
+                             const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int32_t* s_out,
+                             int32_t R, int32_t N, int32_t K, void* stream);
+
 /* The int16 (A16) GEMM on the int8 matrix cores as interleaved digit rows: x is split into rows
  * x8[2r] = x[r] >> 8 and x8[2r + 1] = (x[r] & 255) - 128 (exact_torch.py:101-102), the A8 GEMM runs on the
  * 2R digit rows, and each output row combines its pair: t[r] = 256 T[2r] + T[2r + 1] + 128 colterm.
@@ -122,7 +133,9 @@ int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res_s, const i
  * h = round_shift(isilu(g) * u, 16); xq, sq = qrow(h, bits). h: optional int64 (R, I) scratch for the
  * SwiGLU values; when NULL they may be written over t's gate half. t is left zeroed when clear_t != 0,
  * and is left as it was when clear_t == 0 and h is given (the totals stay readable, e.g. for a trace).
- * part: int32 workspace of R * ceil(I / 1024) slice bit lengths. (exact_llm.py:179; isilu exact_llm.py:118-122). */
+ * part: int32 workspace of R * ceil(I / 1024) slice bit lengths. xq may be NULL when h is given: then only h and
+ * part are produced (bit length of max |h| per 1024-column slice), for exact_gemv_g128_qrow_acc to quantise.
+ * (exact_llm.py:179; isilu exact_llm.py:118-122). */
 int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq,
                       int32_t* sq, int32_t* part, int32_t R, int32_t I, int32_t clear_t, int64_t* h, void* stream);
 

@@ -245,3 +245,52 @@ def test_wide_scales_a16_generic_gemm_entry_is_refused():
     x = dev(rng.integers(-100, 100, (R, K)), I16)
     with pytest.raises(ops.ExactError, match="unsupported"):
         ops._linear("exact_gemm_g128", x, 15, lin, None)
+
+
+@pytest.mark.parametrize("abits", [15, 7])
+@pytest.mark.parametrize("R,N,K,slice_", [(1, 3584, 3584, 128), (3, 896, 896, 64), (15, 512, 18944, 1024), (2, 5120, 13824, 1024),
+                                         (1, 2048, 2048, 128)])
+def test_gemv_qrow_acc(thr, abits, R, N, K, slice_):
+    """qrow folded into the consuming GEMV: t += qrow(xs).W with the row shifts from slice bit lengths equals the
+    oracle's qrow then linear totals; the shifts come back in s_out; t accumulates onto what it held."""
+    if abits == 7 and R > 16 or abits == 15 and R > 15:
+        pytest.skip("beyond the GEMV rows")
+    lin, kw, km = synth_lin(thr, 91, "xq", N, K)
+    w, M = synth.weights_np(kw, N, K), synth.scales_np(km, N, K)
+    ldx = K + 256
+    xs = rng.integers(-(1 << 40), 1 << 40, (R, ldx)) >> rng.integers(0, 38, (R, 1))
+    xs[0, 5] = 0
+    nparts = -(-K // slice_)
+    part = np.array([[O.bitlen(np.array([np.abs(xs[r, i * slice_:min(K, (i + 1) * slice_)]).max()]))[0]
+                      for i in range(nparts)] for r in range(R)], np.int32)
+    xq, s = O.qrow(xs[:, :K], abits)
+    base = rng.integers(-(1 << 50), 1 << 50, (R, N))
+    t = dev(base, I64)
+    s_out = torch.full((R,), -1, dtype=I32, device=DEV)
+    ops.gemv_qrow_acc(dev(xs, I64), dev(part, I32), nparts, abits, lin, t, s_out)
+    assert np.array_equal(host(s_out), s[:, 0])
+    assert np.array_equal(host(t), base + oracle_t(xq, w, M))
+
+
+def test_swiglu_part_then_qrow_gemv_matches_swiglu_qrow(thr):
+    """SwiGLU slices without the qrow (h and slice bit lengths) feeding gemv_qrow_acc give the same totals and shift
+    as swiglu_qrow + GEMV, and leave the gate|up totals zeroed with clear."""
+    from exact_amd.tables import silu_t
+    R, I, D = 2, 18944, 3584
+    lin, kw, km = synth_lin(thr, 92, "down", D, I)
+    w, M = synth.weights_np(kw, D, I), synth.scales_np(km, D, I)
+    tg = rng.integers(-(1 << 44), 1 << 44, (R, 2 * I))
+    s = rng.integers(10, 20, R).astype(np.int32)
+    td = dev(tg, I64)
+    h = torch.empty((R, I), dtype=I64, device=DEV)
+    part = torch.empty(R * -(-I // 1024), dtype=I32, device=DEV)
+    ops.swiglu_part(td, dev(s, I32), dev(silu_t(), I32), h, part, clear=True)
+    t = torch.zeros((R, D), dtype=I64, device=DEV)
+    sh = torch.empty(R, dtype=I32, device=DEV)
+    ops.gemv_qrow_acc(h, part, -(-I // 1024), 15, lin, t, sh)
+    g = O.round_shift(tg[:, :I], 28 - s[:, None].astype(np.int64))
+    u = O.round_shift(tg[:, I:], 28 - s[:, None].astype(np.int64))
+    eq, es = O.qrow(O.round_shift(O.isilu(g) * u, 16), 15)
+    assert np.array_equal(host(sh), es[:, 0])
+    assert np.array_equal(host(t), oracle_t(eq, w, M))
+    assert not host(td).any()
