@@ -645,8 +645,25 @@ int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, con
   return gemm_launch<7, GEMM_A8_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
 }
 
+int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int R, int N,
+                int K, hipStream_t st, bool accumulate, const int64_t* colterm);
+
+#ifndef A16_GEMV_CHUNKS_MAX
+#define A16_GEMV_CHUNKS_MAX 3
+#endif
+
+// int16 rows with colterm: up to 3 x 16 rows as GEMV row chunks (one weight stream per chunk, no all-ones row
+// needed), more rows as interleaved digit rows on the A8 GEMM
 int gemm_a16_digit_rows(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, const int64_t* colterm,
                         int8_t* x8, int64_t* t, int M, int N, int K, hipStream_t st) {
+  if (M <= A16_GEMV_CHUNKS_MAX * 16) {
+    for (int r0 = 0; r0 < M; r0 += 16) {
+      const int rows = M - r0 < 16 ? M - r0 : 16;
+      int e = gemv_launch(x + (size_t)r0 * K, 15, wp, mp, mh, t + (size_t)r0 * N, rows, N, K, st, false, colterm);
+      if (e) return e;
+    }
+    return EXACT_OK;
+  }
   const int64_t n16 = (int64_t)M * (K / 16);
   const int blocks = (int)std::min<int64_t>((n16 + 255) / 256, 8192);
   hipLaunchKernelGGL(k_split_rows_a16, dim3(blocks), dim3(256), 0, st, x, x8, (int64_t)M, K);

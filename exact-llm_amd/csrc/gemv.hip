@@ -101,7 +101,9 @@ __device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restri
   load_w<NT>(G_, wp, mp, mh, tile, row, c);
 }
 
-template <int ABITS, int VR>
+// CT: int16 rows without the all-ones row; the caller adds 128 colterm (sum_g colsum_g M_g) once instead, so
+// all 16 A rows carry activations.
+template <int ABITS, int VR, bool CT = false>
 __device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc)[4][VR], int R, int row, int lane) {
   const v4i zero = {0, 0, 0, 0};
   const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
@@ -110,7 +112,7 @@ __device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc
   for (int h = 0; h < 2; ++h) {
     if (ABITS == 15) {
       split_a16(G_.xa[2 * h], G_.xa[2 * h + 1], ahi[h], alo[h]);
-      if (row == R) alo[h] = ones;          // all-ones row: colsum(W) in the lo pass
+      if (!CT && row == R) alo[h] = ones;   // all-ones row: colsum(W) in the lo pass
     } else {
       ahi[h] = G_.xa[h];
       alo[h] = zero;
@@ -128,7 +130,7 @@ __device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc
     }
     const int64_t m = (int64_t)G_.m[q];
     int cs = 0;
-    if (ABITS == 15) cs = __shfl(sel4(clo, rsel), rlane, 64);
+    if (ABITS == 15 && !CT) cs = __shfl(sel4(clo, rsel), rlane, 64);
 #pragma unroll
     for (int v = 0; v < VR; ++v) {
       const int a = (ABITS == 15) ? (chi[v] << 8) + clo[v] + 128 * cs : chi[v];
@@ -146,7 +148,7 @@ struct NoPrologue {
   __device__ void operator()() const {}
 };
 
-template <int ABITS, bool NT, int VR, typename Pro = NoPrologue>
+template <int ABITS, bool NT, int VR, typename Pro = NoPrologue, bool CT = false>
 __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t* __restrict__ wp,
                                             const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
                                             const int8_t* xrow, bool valid, int R, int nb, int nbs, int G,
@@ -166,27 +168,29 @@ __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t*
   int g = g0;
   for (; g + 2 < g1; g += 2) {
     load_group<ABITS, NT>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
-    compute_group<ABITS, VR>(ra, acc, R, row, lane);
+    compute_group<ABITS, VR, CT>(ra, acc, R, row, lane);
     load_group<ABITS, NT>(ra, wp, mp, mh, xrow, valid, tile_index(nb, g + 2, nbs, G), g + 2, row, c);
-    compute_group<ABITS, VR>(rb, acc, R, row, lane);
+    compute_group<ABITS, VR, CT>(rb, acc, R, row, lane);
   }
   if (g + 1 < g1) {
     load_group<ABITS, NT>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
-    compute_group<ABITS, VR>(ra, acc, R, row, lane);
-    compute_group<ABITS, VR>(rb, acc, R, row, lane);
+    compute_group<ABITS, VR, CT>(ra, acc, R, row, lane);
+    compute_group<ABITS, VR, CT>(rb, acc, R, row, lane);
   } else {
-    compute_group<ABITS, VR>(ra, acc, R, row, lane);
+    compute_group<ABITS, VR, CT>(ra, acc, R, row, lane);
   }
 }
 
 // One wave per (64-row block nb, group range [g0, g1)); BW waves per block take consecutive tasks.
 // Lane l holds output rows 4*(l/16) + v, v < VR (VR = 1, 2 or 4 covers R <= 1, 2 or 16).
 // out_mode 0: plain store (the wave owns all groups of its rows), 1: 64-bit atomic add.
-template <int ABITS, bool NT, int VR, int BW>
+// CT (int16 rows): colterm[n] = sum_g colsum_g M_g given, 128 colterm added by the first split of each row block,
+// so R may be 16.
+template <int ABITS, bool NT, int VR, int BW, bool CT = false>
 __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ xv, const int8_t* __restrict__ wp,
                                                        const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
                                                        int64_t* __restrict__ t, int R, int N, int K, int G, int nsplit,
-                                                       int out_mode) {
+                                                       int out_mode, const int64_t* __restrict__ colterm) {
   const int lane = threadIdx.x & 63;
   const int task = blockIdx.x * BW + (threadIdx.x >> 6);
   const int nbs = (N + 63) >> 6;
@@ -199,16 +203,18 @@ __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ 
   const int8_t* xrow = reinterpret_cast<const int8_t*>(xv) + (size_t)(row < R ? row : 0) * xbytes;
 
   int64_t acc[4][VR];
-  gemv_groups<ABITS, NT, VR>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane);
+  gemv_groups<ABITS, NT, VR, NoPrologue, CT>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane);
 
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int n = nb * 64 + 16 * q + row;
+    const int64_t ct = (CT && sp == 0 && n < N) ? 128 * colterm[n] : 0;
 #pragma unroll
     for (int v = 0; v < VR; ++v) {
       const int r = 4 * c + v;
       if (r < R && n < N) {
         int64_t* dst = t + (size_t)r * N + n;
+        if (CT) acc[q][v] += ct;
         if (out_mode)
           atomicAdd(reinterpret_cast<unsigned long long*>(dst), (unsigned long long)acc[q][v]);
         else
@@ -383,8 +389,9 @@ static int gemv_nsplit(int N, int G) {
 int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int M, int N,
               int K, hipStream_t st);
 
+// colterm (int16 rows only): the colsum term comes from colterm instead of an all-ones row, so R <= 16
 int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int R, int N,
-                int K, hipStream_t st, bool accumulate) {
+                int K, hipStream_t st, bool accumulate, const int64_t* colterm = nullptr) {
   const int G = K / 128;
   const int nsplit = gemv_nsplit(N, G);
   const int out_mode = (accumulate || nsplit > 1) ? 1 : 0;
@@ -403,9 +410,12 @@ int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, c
   dim3 grid((tasks + bw - 1) / bw), block(64 * bw);
 #define GEMV_GO(AB, VR, BW) \
   hipLaunchKernelGGL((k_gemv_g128<AB, GEMV_NT != 0, VR, BW>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, G, nsplit, \
-                     out_mode)
+                     out_mode, nullptr)
   const int vr = R <= 1 ? 1 : (R <= 2 ? 2 : 4);
-  if (abits == 15) {
+  if (abits == 15 && colterm) {
+    hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, 4, 4, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, G, nsplit,
+                       out_mode, colterm);
+  } else if (abits == 15) {
     if (vr == 1) GEMV_GO(15, 1, 4); else if (vr == 2) GEMV_GO(15, 2, 4); else GEMV_GO(15, 4, 4);
   } else if (wide) {
     if (vr == 1) GEMV_GO(7, 1, 16); else if (vr == 2) GEMV_GO(7, 2, 16); else GEMV_GO(7, 4, 16);

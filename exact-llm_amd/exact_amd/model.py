@@ -9,6 +9,7 @@ with the layer order of IntModel.__call__ (exact_llm.py:161-180):
 Every step runs in hand-written HIP kernels (libexact_hip.so); Python only allocates buffers and
 sequences launches on the current stream, so a whole decode step can be captured in a HIP graph.
 """
+import collections
 import hashlib
 
 import numpy as np
@@ -235,6 +236,7 @@ class TModel:
         self.I = c.I if not c.moe else 1
         self._ws = {}
         self._pws = None
+        self._graphs = collections.OrderedDict()   # captured prefill passes
 
     # ---------------------------------------------------------------- buffers
     def new_cache(self, B=None):
@@ -386,8 +388,13 @@ class TModel:
         ops.moe_combine(ws.x, ws.t_ed, ws.esh, ws.p_sel, ws.disp["pidx"], k, ws.t_sd, ws.ssh, ws.gate, clear=True)
 
     # ---------------------------------------------------------------- reference-shaped API
-    def forward(self, ids, cache=None, last_only=False, slot=0):
-        """int64 Q16 logits (T, V) of the new tokens ids (a list) for cache slot `slot` (exact_torch.py:171-193)."""
+    PREFILL_GRAPHS = 8   # captured prefill passes kept (least recently used dropped)
+
+    def forward(self, ids, cache=None, last_only=False, slot=0, graph=False):
+        """int64 Q16 logits (T, V) of the new tokens ids (a list) for cache slot `slot` (exact_torch.py:171-193).
+        graph=True: the pass for this (length, cache, slot, start position) runs eagerly the first time and is
+        captured as a HIP graph, which later calls with the same shape replay (one launch from the host instead
+        of about 12 per layer); the prompt ids and positions are copied in before each replay."""
         if cache is None:
             cache = self.new_cache(B=1)
             slot = 0
@@ -402,8 +409,23 @@ class TModel:
         ws.pos.copy_(torch.arange(p0, p0 + T, dtype=I32))
         # the matrix-core attention for prefill chunks of 32 rows or more (hd 128); the row kernel otherwise
         ws.seq = (slot, p0 + T) if T >= self.PREFILL_MIN_ROWS and self.cfg.hd == 128 else None
-        self.forward_rows(ws)
-        ws.seq = None
+        key = (T, id(cache), slot, p0)
+        g = self._graphs.get(key) if graph else None
+        try:
+            if g is not None:
+                self._graphs.move_to_end(key)
+                g[0].replay()
+            else:
+                self.forward_rows(ws)
+                if graph:   # capture the same pass (capture records, it does not run the kernels again)
+                    cg = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(cg):
+                        self.forward_rows(ws)
+                    self._graphs[key] = (cg, cache)   # the graph holds the cache's buffers
+                    while len(self._graphs) > self.PREFILL_GRAPHS:
+                        self._graphs.popitem(last=False)
+        finally:
+            ws.seq = None
         cache.n[slot] = p0 + T
         out = ws.logits.clone()
         return out[-1:] if last_only else out

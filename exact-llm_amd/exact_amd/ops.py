@@ -141,7 +141,8 @@ def gemv_qrow_acc(xs, part, nparts, abits, lin, out, s_out, K=None):
     return out
 
 
-GEMV_CHUNK_ROWS = {15: 45, 7: 48}   # up to 3 GEMV row chunks (exact_gemm_g128 runs those as GEMVs)
+GEMV_CHUNK_ROWS = {15: 15, 7: 48}   # int8 rows: up to 3 GEMV row chunks in exact_gemm_g128; int16 rows above 15 take
+                                    # exact_gemm_g128_a16 (GEMV chunks of 16 with colterm up to 48 rows, digit rows beyond)
 _DIGIT_ROWS = {}                     # device -> int8 workspace of the A16 digit rows
 
 

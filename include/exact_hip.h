@@ -101,7 +101,8 @@ int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const int32_t* part
  * 2R digit rows, and each output row combines its pair: t[r] = 256 T[2r] + T[2r + 1] + 128 colterm.
  * colterm[n] = sum_g (sum_{k in g} W[k][n]) * M[g][n]: exact_gemv_g128 of an all-ones int8 row (A8) gives it,
  * once per linear. x8: caller workspace of 2 R K bytes (16-byte aligned). Same output as exact_gemm_g128
- * with abits 15; 2 R K < 2^32. */
+ * with abits 15; 2 R K < 2^32. Up to 48 rows run as GEMV row chunks of 16 (colterm replaces the GEMV's
+ * all-ones row; x8 is not used then). */
 int exact_gemm_g128_a16(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, const int64_t* colterm,
                         int8_t* x8, int64_t* t, int32_t R, int32_t N, int32_t K, void* stream);
 

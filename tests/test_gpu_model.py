@@ -118,3 +118,28 @@ def test_batch_decode_and_graph_replay_match_eager():
         for i in range(5):
             assert np.array_equal(steps[i][0][b], orows[i + 1]), (b, i)
             assert int(steps[i][1][b]) == otoks[i + 1]
+
+
+@pytest.mark.parametrize("name,T", [("tiny", 12), ("tiny-hd128", 40)])
+def test_graph_prefill_replays_match_oracle(name, T):
+    """Prefill captured as a HIP graph (forward(graph=True)): the first call runs eagerly and captures, later calls of
+    the same length, slot and start position replay it with new prompts; every replay equals the oracle, with eager
+    passes and host synchronisations in between, and a second chunk continues the cache."""
+    cfg = synth.CONFIGS[name]
+    seed = 8
+    om = helpers.oracle_model(cfg, seed, T=128)
+    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=128, batch=2)
+    cache = tm.new_cache()
+    for rep in range(4):
+        ids = helpers.prompt(100 + rep, T, cfg.V)
+        cache.n[1] = 0
+        got = host(tm.forward(ids, cache, slot=1, graph=True))
+        assert np.array_equal(got, om(ids)), rep
+        more = helpers.prompt(200 + rep, T, cfg.V)
+        got2 = host(tm.forward(more, cache, slot=1, graph=True))   # second chunk, start position T
+        assert np.array_equal(got2, om(ids + more)[T:]), rep
+        # an eager pass on another slot in between
+        other = helpers.prompt(300 + rep, 5, cfg.V)
+        cache.n[0] = 0
+        assert np.array_equal(host(tm.forward(other, cache, slot=0)), om(other))
+    assert len(tm._graphs) == 2
