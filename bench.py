@@ -53,89 +53,98 @@ def gemv_pass(args):
     shapes = {"qkv": (nqkv, D), "o": (D, cfg.H * cfg.hd), "gateup": (2 * I, D), "down": (D, I)}
     layers = [{k: lin(f"L{li}.{k}", *v) for k, v in shapes.items()} for li in range(NL)]
     head = lin("head", cfg.V, D)
-    g = torch.Generator(device="cpu").manual_seed(1)
-    x_d = torch.randint(-127, 128, (1, D), generator=g, dtype=torch.int8).to(dev)
-    x_i = torch.randint(-127, 128, (1, I), generator=g, dtype=torch.int8).to(dev)
-    x_a = torch.randint(-127, 128, (1, cfg.H * cfg.hd), generator=g, dtype=torch.int8).to(dev)
-    xin = {"qkv": x_d, "o": x_a, "gateup": x_d, "down": x_i}
-    # every GEMV of the pass writes its own exact output: one buffer, zeroed once per step, sliced per launch
-    nout = NL * sum(v[0] for v in shapes.values()) + cfg.V
-    obuf = torch.zeros(nout, dtype=I64, device=dev)
-    outs, off = [], 0
-    for li in range(NL):
-        o = {}
-        for k, v in shapes.items():
-            o[k] = obuf[off:off + v[0]].view(1, v[0])
-            off += v[0]
-        outs.append(o)
-    out_head = obuf[off:off + cfg.V].view(1, cfg.V)
 
     def nbytes(N, K, R=1):
         return N * K + N * (K // 128) * 2 + R * K + R * N * 8
 
-    pass_bytes = sum(nbytes(*shapes[k]) for k in shapes) * NL + nbytes(cfg.V, D)
-
-    def step():
-        ops.zero_(obuf)
-        for L, o in zip(layers, outs):
-            for k in shapes:
-                ops.gemv_g128_acc(xin[k], 7, L[k], o[k])
-        ops.gemv_g128_acc(x_d, 7, head, out_head)
-
-    torch.cuda.synchronize()
-    step()
-    torch.cuda.synchronize()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        step()
-    torch.cuda.current_stream().wait_stream(s)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(st)
-    for _ in range(args.steps):
-        graph.replay()
-    e1.record(st)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
 
-    # per-shape launch durations: one HIP graph of NL launches over distinct weights (no cache reuse),
-    # timed with HIP events on the launch stream
-    per = {}
-    for k, (N, K) in list(shapes.items()) + [("head", (cfg.V, D))]:
-        def shape_step():
-            if k == "head":
-                ops.gemv_g128_acc(x_d, 7, head, out_head)
-            else:
-                for L, o in zip(layers, outs):
+    def measure(R):
+        """The pass and its per-shape launches for R activation rows (R tokens per pass)."""
+        g = torch.Generator(device="cpu").manual_seed(1)
+        x_d = torch.randint(-127, 128, (R, D), generator=g, dtype=torch.int8).to(dev)
+        x_i = torch.randint(-127, 128, (R, I), generator=g, dtype=torch.int8).to(dev)
+        x_a = torch.randint(-127, 128, (R, cfg.H * cfg.hd), generator=g, dtype=torch.int8).to(dev)
+        xin = {"qkv": x_d, "o": x_a, "gateup": x_d, "down": x_i}
+        # every GEMV of the pass writes its own exact output: one buffer, zeroed once per step, sliced per launch
+        nout = NL * sum(v[0] for v in shapes.values()) + cfg.V
+        obuf = torch.zeros(R * nout, dtype=I64, device=dev)
+        outs, off = [], 0
+        for li in range(NL):
+            o = {}
+            for k, v in shapes.items():
+                o[k] = obuf[off:off + R * v[0]].view(R, v[0])
+                off += R * v[0]
+            outs.append(o)
+        out_head = obuf[off:off + R * cfg.V].view(R, cfg.V)
+        pass_bytes = sum(nbytes(*shapes[k], R) for k in shapes) * NL + nbytes(cfg.V, D, R)
+
+        def step():
+            ops.zero_(obuf)
+            for L, o in zip(layers, outs):
+                for k in shapes:
                     ops.gemv_g128_acc(xin[k], 7, L[k], o[k])
-        sg = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(sg):
-            shape_step()
-        sg.replay()
-        reps = 5
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ops.gemv_g128_acc(x_d, 7, head, out_head)
+
         torch.cuda.synchronize()
-        a.record(st)
-        for _ in range(reps):
+        step()
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(st)
+        for _ in range(args.steps):
+            graph.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = e0.elapsed_time(e1) / args.steps
+
+        # per-shape launch durations: one HIP graph of NL launches over distinct weights (no cache reuse),
+        # timed with HIP events on the launch stream
+        per = {}
+        for k, (N, K) in list(shapes.items()) + [("head", (cfg.V, D))]:
+            def shape_step():
+                if k == "head":
+                    ops.gemv_g128_acc(x_d, 7, head, out_head)
+                else:
+                    for L, o in zip(layers, outs):
+                        ops.gemv_g128_acc(xin[k], 7, L[k], o[k])
+            sg = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(sg):
+                shape_step()
             sg.replay()
-        b.record(st)
-        torch.cuda.synchronize()
-        n = reps * (1 if k == "head" else NL)
-        us = a.elapsed_time(b) * 1000.0 / n
-        per[k] = dict(N=N, K=K, us=round(us, 2), GBps=round(nbytes(N, K) / us / 1e3, 1))
-        del sg
+            reps = 5
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record(st)
+            for _ in range(reps):
+                sg.replay()
+            b.record(st)
+            torch.cuda.synchronize()
+            n = reps * (1 if k == "head" else NL)
+            us = a.elapsed_time(b) * 1000.0 / n
+            per[k] = dict(N=N, K=K, us=round(us, 2), GBps=round(nbytes(N, K, R) / us / 1e3, 1))
+            del sg
+        del graph, obuf
+        return dict(ms=ms, wall=wall, pass_bytes=pass_bytes, per=per)
+
+    r1 = measure(1)
+    r8 = measure(8)
+    r1["bs8"] = r8
     del layers, head
     torch.cuda.empty_cache()
-    return dict(ms=ms, wall=wall, pass_bytes=pass_bytes, per=per)
+    return r1
 
 
 def active_bytes(cfg):
@@ -434,6 +443,8 @@ def main():
                    "weights_GB": round(r["pass_bytes"] / 1e9, 3), "parallelism": "single GPU"},
         "gemv_GBps": round(pass_gbps, 1),
         "gemv_per_shape": r["per"],
+        "gemv_bs8": {"tok_s": round(8000.0 / r["bs8"]["ms"], 2), "ms_per_step": round(r["bs8"]["ms"], 4),
+                     "GBps": round(r["bs8"]["pass_bytes"] / (r["bs8"]["ms"] * 1e-3) / 1e9, 1), "per_shape": r["bs8"]["per"]},
         "model_decode": mdl,
         "model_configs": models,
         "trace_capture": trc,

@@ -45,19 +45,23 @@ struct GroupRegs {
   int m[4];
 };
 
-// Scales and weight tile of one group. mh: NULL (int16 scales in mp) or the high plane of wide scales:
-// M = mh * 2^15 + mp, mp in [0, 2^15).
-template <bool NT>
-__device__ __forceinline__ void load_w(GroupRegs& G_, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
-                                       const int16_t* __restrict__ mh, size_t tile, int row, int c) {
+// Scales of one group. mh: the high plane of wide scales when WIDE: M = mh * 2^15 + mp, mp in [0, 2^15).
+template <bool WIDE>
+__device__ __forceinline__ void load_scales(GroupRegs& G_, const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
+                                            size_t tile, int row) {
   const int16_t* ms = mp + tile * 64 + row;
 #pragma unroll
   for (int q = 0; q < 4; ++q) G_.m[q] = ms[16 * q];
-  if (mh) {   // uniform over the launch
+  if constexpr (WIDE) {   // a template parameter: a run-time branch here cost the int8 kernels 40 VGPRs
     const int16_t* hs = mh + tile * 64 + row;
 #pragma unroll
     for (int q = 0; q < 4; ++q) G_.m[q] |= (int)hs[16 * q] << 15;
   }
+}
+
+// The group's 8 KiB weight tile.
+template <bool NT>
+__device__ __forceinline__ void load_tile(GroupRegs& G_, const int8_t* __restrict__ wp, size_t tile, int row, int c) {
   const v4i* tp = reinterpret_cast<const v4i*>(wp + tile * 8192 + c * 1024 + row * 16);
 #pragma unroll
   for (int h = 0; h < 2; ++h)
@@ -93,12 +97,13 @@ __device__ __forceinline__ void load_x(GroupRegs& G_, const int8_t* xrow, bool v
 }
 
 // issue order: scales, activations, then the tile (waiting on the tile drains the group)
-template <int ABITS, bool NT>
+template <int ABITS, bool NT, bool WIDE>
 __device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
                                            const int16_t* __restrict__ mh, const int8_t* xrow, bool valid,
                                            size_t tile, int g, int row, int c) {
+  load_scales<WIDE>(G_, mp, mh, tile, row);
   load_x<ABITS>(G_, xrow, valid, g, c);
-  load_w<NT>(G_, wp, mp, mh, tile, row, c);
+  load_tile<NT>(G_, wp, tile, row, c);
 }
 
 // CT: int16 rows without the all-ones row; the caller adds 128 colterm (sum_g colsum_g M_g) once instead, so
@@ -148,7 +153,7 @@ struct NoPrologue {
   __device__ void operator()() const {}
 };
 
-template <int ABITS, bool NT, int VR, typename Pro = NoPrologue, bool CT = false>
+template <int ABITS, bool NT, int VR, typename Pro = NoPrologue, bool CT = false, bool WIDE = false>
 __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t* __restrict__ wp,
                                             const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
                                             const int8_t* xrow, bool valid, int R, int nb, int nbs, int G,
@@ -162,18 +167,23 @@ __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t*
     return;
   }
   GroupRegs ra, rb;
-  load_w<NT>(ra, wp, mp, mh, tile_index(nb, g0, nbs, G), row, c);
-  pro();
-  load_x<ABITS>(ra, xrow, valid, g0, c);
+  if constexpr (__is_same(Pro, NoPrologue)) {
+    load_group<ABITS, NT, WIDE>(ra, wp, mp, mh, xrow, valid, tile_index(nb, g0, nbs, G), g0, row, c);
+  } else {   // the first tile in flight while the prologue runs
+    load_scales<WIDE>(ra, mp, mh, tile_index(nb, g0, nbs, G), row);
+    load_tile<NT>(ra, wp, tile_index(nb, g0, nbs, G), row, c);
+    pro();
+    load_x<ABITS>(ra, xrow, valid, g0, c);
+  }
   int g = g0;
   for (; g + 2 < g1; g += 2) {
-    load_group<ABITS, NT>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
+    load_group<ABITS, NT, WIDE>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
     compute_group<ABITS, VR, CT>(ra, acc, R, row, lane);
-    load_group<ABITS, NT>(ra, wp, mp, mh, xrow, valid, tile_index(nb, g + 2, nbs, G), g + 2, row, c);
+    load_group<ABITS, NT, WIDE>(ra, wp, mp, mh, xrow, valid, tile_index(nb, g + 2, nbs, G), g + 2, row, c);
     compute_group<ABITS, VR, CT>(rb, acc, R, row, lane);
   }
   if (g + 1 < g1) {
-    load_group<ABITS, NT>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
+    load_group<ABITS, NT, WIDE>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
     compute_group<ABITS, VR, CT>(ra, acc, R, row, lane);
     compute_group<ABITS, VR, CT>(rb, acc, R, row, lane);
   } else {
@@ -186,7 +196,7 @@ __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t*
 // out_mode 0: plain store (the wave owns all groups of its rows), 1: 64-bit atomic add.
 // CT (int16 rows): colterm[n] = sum_g colsum_g M_g given, 128 colterm added by the first split of each row block,
 // so R may be 16.
-template <int ABITS, bool NT, int VR, int BW, bool CT = false>
+template <int ABITS, bool NT, int VR, int BW, bool CT = false, bool WIDE = false>
 __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ xv, const int8_t* __restrict__ wp,
                                                        const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
                                                        int64_t* __restrict__ t, int R, int N, int K, int G, int nsplit,
@@ -203,7 +213,7 @@ __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ 
   const int8_t* xrow = reinterpret_cast<const int8_t*>(xv) + (size_t)(row < R ? row : 0) * xbytes;
 
   int64_t acc[4][VR];
-  gemv_groups<ABITS, NT, VR, NoPrologue, CT>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane);
+  gemv_groups<ABITS, NT, VR, NoPrologue, CT, WIDE>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane);
 
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -232,7 +242,7 @@ __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ 
 // kernel wrote it (attention's per-head bit lengths, or SwiGLU's per-slice ones). Each wave quantises the columns of
 // its own groups into LDS (xs[r][g0 * 128 ...g1 * 128), clipped to +-(2^abits - 1)) and runs the group loop on them;
 // block 0 writes s_out. Replaces a k_quant_rows launch + GEMV pair. t += x.W (accumulate).
-template <int ABITS, bool NT, int VR>
+template <int ABITS, bool NT, int VR, bool WIDE>
 __global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict__ xs, int64_t ldx,
                                                       const int32_t* __restrict__ part, int nparts,
                                                       const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
@@ -281,7 +291,8 @@ __global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict_
   // group g's columns sit at (g - g0) * 128 of the slice: offset the row base back by g0 * 128 elements
   const int8_t* xrow = mine + (size_t)(row < R ? row : 0) * rowb - (ptrdiff_t)g0 * 128 * EB;
   int64_t acc[4][VR];
-  gemv_groups<ABITS, NT, VR>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane, quantise);
+  gemv_groups<ABITS, NT, VR, decltype(quantise), false, WIDE>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c,
+                                                              lane, quantise);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int n = nb * 64 + 16 * q + row;
@@ -408,13 +419,23 @@ int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, c
   const bool wide = abits == 7 && (int64_t)N * K >= (32LL << 20) && (tasks + 15) / 16 <= GEMV_CUS;
   const int bw = wide ? 16 : 4;
   dim3 grid((tasks + bw - 1) / bw), block(64 * bw);
-#define GEMV_GO(AB, VR, BW) \
-  hipLaunchKernelGGL((k_gemv_g128<AB, GEMV_NT != 0, VR, BW>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, G, nsplit, \
-                     out_mode, nullptr)
+#define GEMV_GO(AB, VR, BW)                                                                                          \
+  do {                                                                                                               \
+    if (mh)                                                                                                          \
+      hipLaunchKernelGGL((k_gemv_g128<AB, GEMV_NT != 0, VR, BW, false, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N, \
+                         K, G, nsplit, out_mode, nullptr);                                                          \
+    else                                                                                                             \
+      hipLaunchKernelGGL((k_gemv_g128<AB, GEMV_NT != 0, VR, BW>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, G,       \
+                         nsplit, out_mode, nullptr);                                                                 \
+  } while (0)
   const int vr = R <= 1 ? 1 : (R <= 2 ? 2 : 4);
   if (abits == 15 && colterm) {
-    hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, 4, 4, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, G, nsplit,
-                       out_mode, colterm);
+    if (mh)
+      hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, 4, 4, true, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, G,
+                         nsplit, out_mode, colterm);
+    else
+      hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, 4, 4, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, G, nsplit,
+                         out_mode, colterm);
   } else if (abits == 15) {
     if (vr == 1) GEMV_GO(15, 1, 4); else if (vr == 2) GEMV_GO(15, 2, 4); else GEMV_GO(15, 4, 4);
   } else if (wide) {
@@ -478,9 +499,15 @@ extern "C" int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const in
   const int tasks = ((N + 63) / 64) * nsplit;
   dim3 grid((tasks + 3) / 4), block(256);
   hipStream_t st = as_stream(stream);
-#define XQ_GO(AB, VR)                                                                                                 \
-  hipLaunchKernelGGL((k_gemv_g128_xq<AB, GEMV_NT != 0, VR>), grid, block, lds, st, xs, ldx, part, nparts, wp, mp, mh, t, \
-                     s_out, R, N, K, G, nsplit, gmax)
+#define XQ_GO(AB, VR)                                                                                                  \
+  do {                                                                                                                 \
+    if (mh)                                                                                                            \
+      hipLaunchKernelGGL((k_gemv_g128_xq<AB, GEMV_NT != 0, VR, true>), grid, block, lds, st, xs, ldx, part, nparts, wp, mp, \
+                         mh, t, s_out, R, N, K, G, nsplit, gmax);                                                      \
+    else                                                                                                               \
+      hipLaunchKernelGGL((k_gemv_g128_xq<AB, GEMV_NT != 0, VR, false>), grid, block, lds, st, xs, ldx, part, nparts, wp,   \
+                         mp, mh, t, s_out, R, N, K, G, nsplit, gmax);                                                  \
+  } while (0)
   const int vr = R <= 1 ? 1 : (R <= 2 ? 2 : 4);
   if (abits == 15) {
     if (vr == 1) XQ_GO(15, 1); else if (vr == 2) XQ_GO(15, 2); else XQ_GO(15, 4);
