@@ -382,6 +382,59 @@ def cpu_baseline():
                       "(float64 BLAS per group), extrapolated as 28 layers + head"}
 
 
+def cpu_model_c1():
+    """The oracle's whole-model decode on the host (the reference's numpy CPU path, exact_llm.py:161-180, 262-268) for
+    the Qwen2.5-0.5B-shape model of the C1 config, both variants of the reference's generate: KV-cached (one new row
+    per step) and as-reference (the whole sequence recomputed every step). A bounded sample: a 16-token prompt, then
+    2 cached decode steps and 1 uncached step at length 17."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import exact_c
+    import exact_oracle as O
+    from exact_amd import synth
+    cfg = synth.CONFIGS["qwen2.5-0.5b"]
+    seed = 11
+    thr = synth.thresholds()
+    t0 = time.perf_counter()
+
+    def lin(name, N, K, bias):   # the synthetic model's integers, from the oracle's C generator
+        key = lambda s_: synth.key(seed, name + s_)
+        b = synth.vector_np(key(".b"), N, *synth.BIAS) if bias else None
+        return O.Lin(exact_c.weights(key(".w"), thr, N, K), exact_c.scales(key(".m"), N, K, synth.M_LO, synth.M_HI), b)
+
+    layers = []
+    for i in range(cfg.NL):
+        L = dict(g1=synth.vector_np(synth.key(seed, f"L{i}.g1"), cfg.D, *synth.GAIN),
+                 g2=synth.vector_np(synth.key(seed, f"L{i}.g2"), cfg.D, *synth.GAIN))
+        for name, N, K, bias in synth.linear_specs(cfg, i):
+            L[name.split(".", 1)[1]] = lin(name, N, K, bias)
+        layers.append(L)
+    ew = exact_c.weights(synth.key(seed, "emb.w"), thr, cfg.V, cfg.D)
+    eM = exact_c.scales(synth.key(seed, "emb.m"), cfg.V, cfg.D, synth.M_LO, synth.M_HI)
+    m = O.Model(dict(emb=exact_c.embed(ew, eM), gf=synth.vector_np(synth.key(seed, "gf"), cfg.D, *synth.GAIN),
+                     layers=layers, head=O.Lin(ew, eM)),
+                dict(D=cfg.D, H=cfg.H, KV=cfg.KV, hd=cfg.hd, NL=cfg.NL, theta=cfg.theta, T=64, topk=0))
+    build_s = time.perf_counter() - t0
+    ids = np.random.default_rng(0).integers(0, cfg.V, 16).tolist()
+    cache = m.new_cache()
+    t0 = time.perf_counter()
+    lg = m(ids, cache)
+    prefill_s = time.perf_counter() - t0
+    tok = int(lg[-1].argmax())
+    t0 = time.perf_counter()
+    for _ in range(2):
+        tok = int(m([tok], cache)[-1].argmax())
+    cached_s = (time.perf_counter() - t0) / 2
+    t0 = time.perf_counter()
+    m(ids + [tok])
+    uncached_s = time.perf_counter() - t0
+    return {"unit": "tok/s", "cores": os.cpu_count(), "kind": "port",
+            "kv_cached_tok_s": round(1.0 / cached_s, 3), "as_reference_tok_s_at_17": round(1.0 / uncached_s, 3),
+            "prefill_16_s": round(prefill_s, 2), "model_build_s": round(build_s, 1),
+            "sample": "Qwen2.5-0.5B-shape integer model (24 layers, group-128 A16), numpy oracle: 16-token prompt, "
+                      "2 KV-cached decode steps, 1 step recomputing all 17 positions"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -426,6 +479,7 @@ def main():
         trc = trace_capture(args) if "7b" in want and not args.no_trace else None
     att = None if args.no_prefill else attention_prefill(args)
     cpu = None if args.no_cpu else cpu_baseline()
+    cpu_c1 = None if args.no_cpu else cpu_model_c1()
     if r is None:
         print(json.dumps({"metric": METRIC, "value": None, "model_decode": mdl, "model_configs": models,
                           "trace_capture": trc, "prefill_gemm": pre, "attention_prefill": att}), flush=True)
@@ -456,6 +510,7 @@ def main():
                      "algorithmic_bytes": GATEUP_BYTES,
                      "kernel": "k_gemv_g128<7,true,1,16> on gate|up 37888x3584, bs1 A8"},
         "cpu_baseline": cpu,
+        "cpu_model_c1": cpu_c1,
     }
     print(json.dumps(line), flush=True)
 
