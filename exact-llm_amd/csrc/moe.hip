@@ -56,23 +56,26 @@ __global__ void k_router_topk(int64_t* __restrict__ t, int ld, const int32_t* __
   }
 }
 
-// One block. Pair q = r * k + j. Every thread owns experts e = tid, tid + blockDim, ...: it counts its
-// pairs, and after a block-wide prefix it places them (in q order) and writes its chunks.
-__global__ void k_moe_dispatch(const int32_t* __restrict__ e_sel, const int32_t* __restrict__ s, int32_t* __restrict__ pidx,
-                               int32_t* __restrict__ pair_row, int32_t* __restrict__ s_pair, int32_t* __restrict__ chunk_e,
-                               int32_t* __restrict__ chunk_p0, int32_t* __restrict__ chunk_n, int32_t* __restrict__ nchunks,
-                               int P, int NE, int k, int CH) {
+// One block of 16 waves. Pair q = r * k + j. Wave w owns experts e = w, w + 16, ...: it walks the pairs 64 at a
+// time, and a ballot of "pair q belongs to e" gives both the expert's count and, with the count of set bits
+// below each lane, each pair's stable position (q order) inside its expert. Then the chunks of each expert.
+__global__ __launch_bounds__(1024) void k_moe_dispatch(const int32_t* __restrict__ e_sel, const int32_t* __restrict__ s,
+                                                       int32_t* __restrict__ pidx, int32_t* __restrict__ pair_row,
+                                                       int32_t* __restrict__ s_pair, int32_t* __restrict__ chunk_e,
+                                                       int32_t* __restrict__ chunk_p0, int32_t* __restrict__ chunk_n,
+                                                       int32_t* __restrict__ nchunks, int P, int NE, int k, int CH) {
   extern __shared__ int32_t lds[];
   int32_t* es = lds;              // P expert ids
   int32_t* cnt = es + P;          // NE counts
   int32_t* off = cnt + NE;        // NE pair offsets
   int32_t* coff = off + NE;       // NE chunk offsets
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   for (int q = threadIdx.x; q < P; q += blockDim.x) es[q] = e_sel[q];
   __syncthreads();
-  for (int e = threadIdx.x; e < NE; e += blockDim.x) {
+  for (int e = wave; e < NE; e += nw) {
     int c = 0;
-    for (int q = 0; q < P; ++q) c += es[q] == e;
-    cnt[e] = c;
+    for (int b = 0; b < P; b += 64) c += __popcll(__ballot(b + lane < P && es[b + lane] == e));
+    if (lane == 0) cnt[e] = c;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -86,17 +89,23 @@ __global__ void k_moe_dispatch(const int32_t* __restrict__ e_sel, const int32_t*
     nchunks[0] = co;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < NE; e += blockDim.x) {
-    int pos = off[e];
-    for (int q = 0; q < P; ++q)
-      if (es[q] == e) {
+  const uint64_t below = lane ? (~0ULL >> (64 - lane)) : 0ULL;   // lanes below this one
+  for (int e = wave; e < NE; e += nw) {
+    int run = off[e];
+    for (int b = 0; b < P; b += 64) {
+      const int q = b + lane;
+      const bool mine = q < P && es[q] == e;
+      const uint64_t m = __ballot(mine);
+      if (mine) {
+        const int pos = run + __popcll(m & below);
         pidx[q] = pos;
         pair_row[pos] = q / k;
         s_pair[pos] = s[q / k];
-        ++pos;
       }
+      run += __popcll(m);
+    }
     const int n = cnt[e];
-    for (int c = 0; c * CH < n; ++c) {
+    for (int c = lane; c * CH < n; c += 64) {
       const int idx = coff[e] + c;
       chunk_e[idx] = e;
       chunk_p0[idx] = off[e] + c * CH;
@@ -152,7 +161,7 @@ extern "C" int exact_moe_dispatch(const int32_t* e_sel, const int32_t* s, int32_
   if (R <= 0 || NE <= 0 || k <= 0 || k > NE || chunk_rows <= 0) return EXACT_E_ARG;
   const int64_t P = (int64_t)R * k;
   if (P + 3LL * NE > 16384) return EXACT_E_UNSUPPORTED;   // 64 KiB of LDS
-  hipLaunchKernelGGL(k_moe_dispatch, dim3(1), dim3(256), (size_t)(P + 3 * NE) * sizeof(int32_t), as_stream(stream), e_sel,
+  hipLaunchKernelGGL(k_moe_dispatch, dim3(1), dim3(1024), (size_t)(P + 3 * NE) * sizeof(int32_t), as_stream(stream), e_sel,
                      s, pidx, pair_row, s_pair, chunk_e, chunk_p0, chunk_n, nchunks, (int)P, NE, k, chunk_rows);
   return launch_status("moe_dispatch");
 }
