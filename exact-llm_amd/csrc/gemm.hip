@@ -289,12 +289,17 @@ __device__ __forceinline__ int opaque(int x) {
 //   chain (1,1): read B0 + scales (g + 1)   rescale (1,0)
 // so one barrier per group, and every LDS read overlaps matrix-core work.
 // WIDE: scales M = mh * 2^15 + mp (mp in [0, 2^15)), both planes copied per group.
-template <int WM, int WN, int S, bool PAIRS, bool WIDE>
+// GROUPED (MoE experts): row tile bm is dispatched chunk bm (chunk_e / chunk_p0 / chunk_n, nchunks of them): the
+// A rows of pairs chunk_p0 .. + chunk_n (twice as many digit rows with PAIRS) against expert chunk_e's weights at
+// wp + e w_stride, mp + e m_stride, colterm + e N; blocks past nchunks exit.
+template <int WM, int WN, int S, bool PAIRS, bool WIDE, bool GROUPED = false>
 __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __restrict__ xb, const int8_t* __restrict__ wp,
                                                      const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
                                                      int64_t* __restrict__ t, int M, int N, int K, int G, int nbs,
                                                      int tiles_m, int tiles_n, int ksplit, int use_atomic,
-                                                     const int64_t* __restrict__ colterm) {
+                                                     const int64_t* __restrict__ colterm, const int32_t* __restrict__ chunk_e,
+                                                     const int32_t* __restrict__ chunk_p0, const int32_t* __restrict__ chunk_n,
+                                                     const int32_t* __restrict__ nchunks, int64_t w_stride, int64_t m_stride) {
   using C = GemmCfg<7, WM, WN, S>;
   static_assert(EXACT_TILE_GN, "the block's tiles of one group are contiguous in the group-major layout");
   static_assert(C::BN == 128, "one dword copy per lane covers the block's 128 scales");
@@ -316,7 +321,19 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
   const int rem = lb - kz * tiles_m * tiles_n;
   const int bn = rem / tiles_m, bm = rem - bn * tiles_m;
   const int g0 = (int)(((int64_t)kz * G) / ksplit), g1 = (int)(((int64_t)(kz + 1) * G) / ksplit);
-  const int row0 = bm * C::BM, nb0 = bn * C::NT;
+  const int nb0 = bn * C::NT;
+  int row0 = bm * C::BM, Mlim = M;
+  if constexpr (GROUPED) {   // uniform over the block: an early exit before any barrier
+    if (bm >= nchunks[0]) return;
+    const int e = chunk_e[bm];
+    const int cn = chunk_n[bm] < (PAIRS ? C::BM / 2 : C::BM) ? chunk_n[bm] : (PAIRS ? C::BM / 2 : C::BM);
+    row0 = (PAIRS ? 2 : 1) * chunk_p0[bm];
+    Mlim = row0 + (PAIRS ? 2 : 1) * cn;
+    if (Mlim > M) Mlim = M;
+    wp += (int64_t)e * w_stride;
+    mp += (int64_t)e * m_stride;
+    if (colterm) colterm += (int64_t)e * N;
+  }
 
   // The per-lane addresses below are recomputed from an opaque copy of the lane id in every group:
   // hoisted out of the loop they would need registers the running totals leave no room for.
@@ -332,7 +349,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
   for (int i = 0; i < C::A_KB_PER_WAVE; ++i) {
     const int seg = wave * C::A_KB_PER_WAVE + i;            // 1 KiB LDS segment = 8 rows x 128 bytes
     const int r = seg * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
-    const int gr = row0 + r < M ? row0 + r : M - 1;         // rows past M read a valid row, never stored
+    const int gr = row0 + r < Mlim ? row0 + r : Mlim - 1;   // rows past the tile's rows read a valid row, never stored
     aoffs[i] = (uint32_t)gr * (uint32_t)K + (uint32_t)(c * 16);
   }
   const int moff = (2 * lane < ncol ? 2 * lane : ncol - 2) * 2;
@@ -492,7 +509,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
           const int row = row0 + wm * 64 + a * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);   // even
-          if (row < M && col < N) {
+          if (row < Mlim && col < N) {
             const int64_t val = acc[a][b][i >> 1] + ct;
             int64_t* dst = t + (size_t)(row >> 1) * N + col;
             if (use_atomic) atomicAdd(reinterpret_cast<unsigned long long*>(dst), (unsigned long long)val);
@@ -509,7 +526,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int row = row0 + wm * 64 + a * 32 + 8 * (i >> 2) + 4 * lh + (i & 3);
-          if (row < M && col < N) {
+          if (row < Mlim && col < N) {
             const int64_t val = acc[a][b][i];
             int64_t* dst = t + (size_t)row * N + col;
             if (use_atomic) atomicAdd(reinterpret_cast<unsigned long long*>(dst), (unsigned long long)val);
@@ -523,11 +540,11 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
 // int16 rows -> interleaved int8 digit rows: x8[2r] = x[r] >> 8, x8[2r + 1] = (x[r] & 255) - 128.
 // 16 values per thread; K % 16 == 0.
 __global__ __launch_bounds__(256) void k_split_rows_a16(const int16_t* __restrict__ x, int8_t* __restrict__ x8, int64_t M,
-                                                        int K) {
+                                                        int K, const int32_t* __restrict__ row_map = nullptr) {
   const int64_t n16 = M * (K / 16);
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t r = i / (K / 16), c = (i - r * (K / 16)) * 16;
-    const v4i* src = reinterpret_cast<const v4i*>(x + r * K + c);
+    const v4i* src = reinterpret_cast<const v4i*>(x + (row_map ? (int64_t)row_map[r] : r) * K + c);
     const v4i p0 = src[0], p1 = src[1];
     v4i hi, lo;
     hi[0] = __builtin_amdgcn_perm(p0[1], p0[0], 0x07050301u);
@@ -540,6 +557,16 @@ __global__ __launch_bounds__(256) void k_split_rows_a16(const int16_t* __restric
     lo[3] = __builtin_amdgcn_perm(p1[3], p1[2], 0x06040200u) ^ 0x80808080;
     *reinterpret_cast<v4i*>(x8 + (2 * r) * K + c) = hi;
     *reinterpret_cast<v4i*>(x8 + (2 * r + 1) * K + c) = lo;
+  }
+}
+
+// gathered int8 rows: x8[p] = x[row_map[p]] (16 bytes per thread; K % 16 == 0)
+__global__ __launch_bounds__(256) void k_gather_rows_a8(const int8_t* __restrict__ x, int8_t* __restrict__ x8, int64_t P, int K,
+                                                        const int32_t* __restrict__ row_map) {
+  const int64_t n16 = P * (K / 16);
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t p = i / (K / 16), c = (i - p * (K / 16)) * 16;
+    *reinterpret_cast<v4i*>(x8 + p * K + c) = *reinterpret_cast<const v4i*>(x + (int64_t)row_map[p] * K + c);
   }
 }
 
@@ -620,8 +647,32 @@ static int gemm_launch_a8p_t(const void* x, const int8_t* wp, const int16_t* mp,
   const int grid = ((nblk + 7) / 8) * 8;
   hipLaunchKernelGGL((k_gemm_a8p<WM, WN, S, PAIRS, WIDE>), dim3(grid), dim3(C::THREADS), lds, st,
                      reinterpret_cast<const int8_t*>(x), wp, mp, mh, t, M, N, K, G, nbs, tiles_m, tiles_n, ksplit, use_atomic,
-                     colterm);
+                     colterm, nullptr, nullptr, nullptr, nullptr, (int64_t)0, (int64_t)0);
   return launch_status("gemm_g128");
+}
+
+// MoE experts: one grouped launch over the dispatched chunks (row tile = chunk), max_chunks row tiles
+template <int WM, int WN, int S, bool PAIRS>
+static int gemm_launch_experts(const int8_t* x8, const int8_t* wp, const int16_t* mp, int64_t w_stride, int64_t m_stride,
+                               const int64_t* colterm, const int32_t* chunk_e, const int32_t* chunk_p0,
+                               const int32_t* chunk_n, const int32_t* nchunks, int max_chunks, int64_t* t, int M, int N,
+                               int K, hipStream_t st) {
+  using C = GemmCfg<7, WM, WN, S>;
+  static bool attr_set = false;
+  const size_t lds = S * (size_t)(C::A_BYTES + C::B_BYTES + C::WAVES * 256);
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_a8p<WM, WN, S, PAIRS, false, true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    attr_set = true;
+  }
+  const int G = K / 128, nbs = (N + 63) / 64;
+  const int tiles_n = (nbs + C::NT - 1) / C::NT;
+  const int nblk = max_chunks * tiles_n;
+  const int grid = ((nblk + 7) / 8) * 8;
+  hipLaunchKernelGGL((k_gemm_a8p<WM, WN, S, PAIRS, false, true>), dim3(grid), dim3(C::THREADS), lds, st, x8, wp, mp, nullptr, t,
+                     M, N, K, G, nbs, max_chunks, tiles_n, 1, 0, colterm, chunk_e, chunk_p0, chunk_n, nchunks, w_stride,
+                     m_stride);
+  return launch_status("gemm_g128_experts");
 }
 
 template <int WM, int WN, int S, bool PAIRS = false>
@@ -666,13 +717,48 @@ int gemm_a16_digit_rows(const int16_t* x, const int8_t* wp, const int16_t* mp, c
   }
   const int64_t n16 = (int64_t)M * (K / 16);
   const int blocks = (int)std::min<int64_t>((n16 + 255) / 256, 8192);
-  hipLaunchKernelGGL(k_split_rows_a16, dim3(blocks), dim3(256), 0, st, x, x8, (int64_t)M, K);
+  hipLaunchKernelGGL(k_split_rows_a16, dim3(blocks), dim3(256), 0, st, x, x8, (int64_t)M, K, nullptr);
   return gemm_launch_a8p<GEMM_A8P_CFG, true>(x8, wp, mp, mh, t, 2 * M, N, K, st, GEMM_KSPLIT, colterm);
 }
 
 }  // namespace exact
 
 using namespace exact;
+
+// pairs per dispatched chunk the experts GEMM takes: one 256-row tile (128 pairs as digit-row pairs)
+#define EXPERT_CHUNK_A16 128
+#define EXPERT_CHUNK_A8 256
+
+extern "C" int exact_gemm_g128_experts(const void* x, int32_t abits, const int32_t* row_map, const int8_t* wp, const int16_t* mp,
+                                       int64_t w_stride, int64_t m_stride, const int64_t* colterm, int8_t* x8,
+                                       const int32_t* chunk_e, const int32_t* chunk_p0, const int32_t* chunk_n,
+                                       const int32_t* nchunks, int32_t max_chunks, int64_t* t, int32_t P, int32_t N, int32_t K,
+                                       void* stream) {
+  if (!x || !wp || !mp || !x8 || !chunk_e || !chunk_p0 || !chunk_n || !nchunks || !t) return EXACT_E_ARG;
+  if (P <= 0 || N <= 0 || K <= 0 || max_chunks <= 0 || w_stride <= 0 || m_stride <= 0) return EXACT_E_ARG;
+  if (abits == 15 && !colterm) return EXACT_E_ARG;
+  if ((abits != 15 && abits != 7) || K % 128 || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(x8) & 15) ||
+      (reinterpret_cast<uintptr_t>(wp) & 15) || (w_stride & 15))
+    return EXACT_E_UNSUPPORTED;
+  const int64_t rows = (abits == 15 ? 2 : 1) * (int64_t)P;
+  if (rows * K >= (1LL << 32)) return EXACT_E_UNSUPPORTED;   // 32-bit buffer offsets
+  hipStream_t st = as_stream(stream);
+  const int64_t n16 = (int64_t)P * (K / 16);
+  const int blocks = (int)std::min<int64_t>((n16 + 255) / 256, 8192);
+  if (abits == 15) {
+    hipLaunchKernelGGL(k_split_rows_a16, dim3(blocks), dim3(256), 0, st, static_cast<const int16_t*>(x), x8, (int64_t)P, K,
+                       row_map);
+    return gemm_launch_experts<GEMM_A8P_CFG, true>(x8, wp, mp, w_stride, m_stride, colterm, chunk_e, chunk_p0, chunk_n,
+                                                   nchunks, max_chunks, t, (int)rows, N, K, st);
+  }
+  const int8_t* xa = static_cast<const int8_t*>(x);
+  if (row_map) {
+    hipLaunchKernelGGL(k_gather_rows_a8, dim3(blocks), dim3(256), 0, st, xa, x8, (int64_t)P, K, row_map);
+    xa = x8;
+  }
+  return gemm_launch_experts<GEMM_A8P_CFG, false>(xa, wp, mp, w_stride, m_stride, nullptr, chunk_e, chunk_p0, chunk_n, nchunks,
+                                                  max_chunks, t, (int)rows, N, K, st);
+}
 
 extern "C" int exact_gemm_g128_a16(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh,
                                    const int64_t* colterm, int8_t* x8, int64_t* t, int32_t R, int32_t N, int32_t K,

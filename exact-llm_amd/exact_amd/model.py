@@ -244,6 +244,7 @@ class TModel:
 
     PREFILL_MIN_ROWS = 32
     QROW_FUSE_ROWS = 2
+    EXPERT_GEMM_MIN_PAIRS = 64   # (row, expert) pairs from which the MoE experts run as one grouped GEMM
 
     def _prefill_ws(self, R):
         if self._pws is None or self._pws[0] < R:
@@ -375,13 +376,23 @@ class TModel:
         into chunks -> SwiGLU per (row, expert) pair -> combination weighted by the Q20 probabilities, plus the
         isig-gated shared expert."""
         c, tab, k = self.cfg, self.tab, self.cfg.topk
+        P = ws.R * k
         self._lin(ws.xq, L["router"], ws.t_rt)
         ops.router_topk(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, clear=True, NE=c.NE, gate_col=ws.gate_col,
                         sig=tab.sig, gate=ws.gate)
-        ops.moe_dispatch(ws.e_sel, ws.s, c.NE, k, ops.chunk_rows(self.abits), ws.disp)
-        ops.gemv_experts(ws.xq, self.abits, ws.disp["pair_row"], L["egu"], ws.disp, ws.t_egu)
-        ops.swiglu_qrow(ws.t_egu, ws.disp["s_pair"], tab.silu, self.abits, ws.ehq, ws.esh, clear=True, part=ws.part_esw)
-        ops.gemv_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed)
+        grouped = P >= self.EXPERT_GEMM_MIN_PAIRS   # prefill: experts on the matrix cores, one tile per 128 pairs
+        ops.moe_dispatch(ws.e_sel, ws.s, c.NE, k, ops.EXPERT_CHUNK[self.abits] if grouped else ops.chunk_rows(self.abits),
+                         ws.disp)
+        if grouped:
+            ops.gemm_experts(ws.xq, self.abits, ws.disp["pair_row"], L["egu"], ws.disp, ws.t_egu, P)
+        else:
+            ops.gemv_experts(ws.xq, self.abits, ws.disp["pair_row"], L["egu"], ws.disp, ws.t_egu)
+        ops.swiglu_qrow(ws.t_egu, ws.disp["s_pair"], tab.silu, self.abits, ws.ehq, ws.esh, clear=not grouped,
+                        part=ws.part_esw)
+        if grouped:
+            ops.gemm_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed, P)
+        else:
+            ops.gemv_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed)
         self._lin(ws.xq, L["sgu"], ws.t_sgu)
         ops.swiglu_qrow(ws.t_sgu, ws.s, tab.silu, self.abits, ws.shq, ws.ssh, clear=True, part=ws.part_sw)
         self._lin(ws.shq, L["sd"], ws.t_sd)

@@ -446,6 +446,42 @@ def gemv_experts(x, abits, row_map, lin, disp, out):
     return out
 
 
+EXPERT_CHUNK = {15: 128, 7: 256}   # pairs per dispatched chunk for gemm_experts: one 256-row matrix-core tile
+_EXPERT_ROWS = {}                   # device -> int8 workspace of the gathered (digit) rows
+
+
+def expert_colterm(lin):
+    """(NE, N) int64: each expert's sum_g colsum_g M_g (A8 GEMVs of an all-ones row), cached on the ExpertLinears."""
+    ct = getattr(lin, "_colterm", None)
+    if ct is None:
+        ones = torch.ones((1, lin.K), dtype=I8, device=lin.wp.device)
+        ct = torch.empty((lin.NE, lin.N), dtype=I64, device=lin.wp.device)
+        for e in range(lin.NE):
+            wp, mp = lin.part(e)
+            gemv_g128(ones, 7, PackedLinear(wp, mp, lin.N, lin.K), ct[e:e + 1])
+        lin._colterm = ct
+    return ct
+
+
+def gemm_experts(x, abits, row_map, lin, disp, out, P):
+    """out[p] = x[row_map[p]] . W_{expert of p} for the P dispatched pairs on the matrix cores; disp must come from
+    moe_dispatch with chunk = EXPERT_CHUNK[abits] (row_map None: x row p)."""
+    _need(x, I16 if abits == 15 else I8, "x")
+    _need(out, I64, "out", P * lin.N)
+    if x.shape[1] != lin.K or out.shape[1] != lin.N:
+        raise ExactError(f"gemm_experts: x {tuple(x.shape)}, out {tuple(out.shape)} against ({lin.N}, {lin.K})")
+    need = (2 if abits == 15 else 1) * P * lin.K
+    ws = _EXPERT_ROWS.get(x.device)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=I8, device=x.device)
+        _EXPERT_ROWS[x.device] = ws
+    ct = expert_colterm(lin) if abits == 15 else None
+    _lib.call("exact_gemm_g128_experts", _ptr(x), abits, _ptr(row_map), _ptr(lin.wp), _ptr(lin.mp), lin.w_stride, lin.m_stride,
+              _ptr(ct), _ptr(ws), _ptr(disp["chunk_e"]), _ptr(disp["chunk_p0"]), _ptr(disp["chunk_n"]), _ptr(disp["nchunks"]),
+              min(disp["chunk_e"].numel(), -(-P // EXPERT_CHUNK[abits]) + lin.NE), _ptr(out), P, lin.N, lin.K, _stream())
+    return out
+
+
 def moe_combine(x, t_ed, sh_pair, p_sel, pidx, k, t_sd=None, sh_s=None, gate=None, clear=False):
     R, D = x.shape
     _lib.call("exact_moe_combine", _ptr(_need(x, I64, "x")), _ptr(_need(t_ed, I64, "t_ed")), _ptr(sh_pair), _ptr(p_sel),

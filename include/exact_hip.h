@@ -96,6 +96,18 @@ int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const int32_t* part
                              const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int32_t* s_out,
                              int32_t R, int32_t N, int32_t K, void* stream);
 
+/* MoE expert GEMM on the matrix cores, grouped over the chunks exact_moe_dispatch wrote with chunk_rows = 128
+ * (int16 x) or 256 (int8 x): for every chunk c < nchunks[0], rows p = chunk_p0[c] .. + chunk_n[c] of the
+ * dispatched pairs, t[p] = x[row_map[p]] . W_e with e = chunk_e[c] (row_map NULL: x row p), expert e's packed
+ * linear at wp + e * w_stride, mp + e * m_stride. int16 x runs as interleaved digit rows (as
+ * exact_gemm_g128_a16) and needs colterm (NE, N) = each expert's sum_g colsum_g M_g. x8: workspace of 2 P K
+ * (int16) or P K (int8, with row_map) bytes. max_chunks: the length of the chunk arrays (launch size).
+ * Replaces the per-expert loop of MoEInt.moe (moe_exact_kaggle.py:460-464) for prefill-sized pair counts. */
+int exact_gemm_g128_experts(const void* x, int32_t abits, const int32_t* row_map, const int8_t* wp, const int16_t* mp,
+                            int64_t w_stride, int64_t m_stride, const int64_t* colterm, int8_t* x8, const int32_t* chunk_e,
+                            const int32_t* chunk_p0, const int32_t* chunk_n, const int32_t* nchunks, int32_t max_chunks,
+                            int64_t* t, int32_t P, int32_t N, int32_t K, void* stream);
+
 /* The int16 (A16) GEMM on the int8 matrix cores as interleaved digit rows: x is split into rows
  * x8[2r] = x[r] >> 8 and x8[2r + 1] = (x[r] & 255) - 128 (exact_torch.py:101-102), the A8 GEMM runs on the
  * 2R digit rows, and each output row combines its pair: t[r] = 256 T[2r] + T[2r + 1] + 128 colterm.

@@ -121,6 +121,66 @@ def test_expert_gemv_matches_oracle(abits, R, NE, k, N, K):
         assert np.array_equal(got[pidx[q]], want), (q, e)
 
 
+def _expert_case(rng, abits, R, NE, k, N, K, used):
+    lin = ops.ExpertLinears(NE, N, K, DEV)
+    thr = dev(synth.thresholds().astype(np.int64), I64).to(I32)
+    e_sel = np.stack([rng.choice(used, k, replace=False) for _ in range(R)])
+    ws, Ms = {}, {}
+    for e in range(NE):
+        wp, mp = lin.part(e)
+        kw, km = synth.key(9, f"e{e}.w"), synth.key(9, f"e{e}.m")
+        ops.synth_linear(wp, mp, N, K, kw, km, synth.M_LO, synth.M_HI, thr)
+        if e in used:
+            ws[e], Ms[e] = synth.weights_np(kw, N, K), synth.scales_np(km, N, K)
+    lim = (1 << abits) - 1
+    return lin, e_sel, ws, Ms, rng.integers(-lim, lim + 1, (R, K))
+
+
+def _dispatch(e_sel, NE, k, chunk, abits):
+    R = e_sel.shape[0]
+    P = R * k
+    disp = {n: torch.zeros((P,), dtype=I32, device=DEV) for n in ("pidx", "pair_row", "s_pair")}
+    nmax = ops.max_chunks(P, NE, abits)
+    disp.update({n: torch.zeros((nmax,), dtype=I32, device=DEV) for n in ("chunk_e", "chunk_p0", "chunk_n")})
+    disp["nchunks"] = torch.zeros(1, dtype=I32, device=DEV)
+    ops.moe_dispatch(dev(e_sel, I32), torch.zeros(R, dtype=I32, device=DEV), NE, k, chunk, disp)
+    return disp
+
+
+@pytest.mark.parametrize("abits", [15, 7])
+@pytest.mark.parametrize("R,NE,k,N,K,nused,full", [(64, 60, 4, 2816, 2048, 10, False), (17, 60, 4, 2048, 1408, 60, False),
+                                                    (300, 3, 2, 384, 256, 3, True), (40, 6, 2, 200, 384, 6, True)])
+def test_expert_gemm_matches_expert_gemv_and_oracle(abits, R, NE, k, N, K, nused, full):
+    """The grouped matrix-core expert GEMM against the expert GEMV (oracle-pinned above) on every pair, and
+    against the oracle on every pair (small shapes) or on 24 of them; (300, 3, 2) puts 200 pairs on each
+    expert, so one expert spans several 128- and 256-pair chunks, and N = 200 leaves a ragged column tile."""
+    rng = np.random.default_rng(100 * abits + R)
+    used = sorted(rng.choice(NE, nused, replace=False).tolist())
+    lin, e_sel, ws, Ms, x = _expert_case(rng, abits, R, NE, k, N, K, used)
+    P = R * k
+    xd = dev(x, torch.int16 if abits == 15 else torch.int8)
+    dv = _dispatch(e_sel, NE, k, ops.chunk_rows(abits), abits)
+    t_v = torch.zeros((P, N), dtype=I64, device=DEV)
+    ops.gemv_experts(xd, abits, dv["pair_row"], lin, dv, t_v)
+    dm = _dispatch(e_sel, NE, k, ops.EXPERT_CHUNK[abits], abits)
+    assert np.array_equal(host(dm["pidx"]), host(dv["pidx"]))
+    t_m = torch.full((P, N), -1, dtype=I64, device=DEV)   # every row is written, none accumulated
+    ops.gemm_experts(xd, abits, dm["pair_row"], lin, dm, t_m, P)
+    got = host(t_m)
+    assert np.array_equal(got, host(t_v))
+    pidx = host(dm["pidx"])
+    qs = range(P) if full else rng.choice(P, 24, replace=False)
+    for q in qs:
+        r, e = q // k, e_sel.reshape(-1)[q]
+        want = (O.group_acc(x[r:r + 1], ws[e]) * Ms[e][:, None, :]).sum(0)[0]
+        assert np.array_equal(got[pidx[q]], want), (q, e)
+    # pairs in dispatched order (row_map None): the expert down projection's input layout
+    xs = xd[dm["pair_row"].long()].contiguous()
+    t_d = torch.zeros((P, N), dtype=I64, device=DEV)
+    ops.gemm_experts(xs, abits, None, lin, dm, t_d, P)
+    assert np.array_equal(host(t_d), got)
+
+
 def test_combine_matches_oracle(tab):
     rng = np.random.default_rng(5)
     R, k, D, NE = 6, 4, 512, 60
@@ -167,6 +227,21 @@ def test_tiny_moe_prefill_and_decode_match_oracle(abits):
         assert np.array_equal(host(lgi)[0], orows[i]), i
         tok = int(host(nid)[0])
         assert tok == otoks[i]
+
+
+@pytest.mark.parametrize("abits", [15, 7])
+def test_tiny_moe_long_prefill_runs_grouped_expert_gemm(abits, monkeypatch):
+    """A 60-token prefill (120 pairs) takes the grouped expert GEMM; logits equal the oracle's."""
+    cfg = synth.CONFIGS["tiny-moe"]
+    seed = 13
+    om = helpers.oracle_model(cfg, seed, T=64, abits=abits)
+    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=64, abits=abits)
+    calls = []
+    real = ops.gemm_experts
+    monkeypatch.setattr(ops, "gemm_experts", lambda *a: calls.append(a[-1]) or real(*a))
+    ids = helpers.prompt(23, 60, cfg.V)
+    assert np.array_equal(host(tm.forward(ids)), om.forward(ids))
+    assert calls == [60 * cfg.topk] * (2 * cfg.NL)
 
 
 def test_tiny_moe_batch_graph_decode_matches_oracle():
