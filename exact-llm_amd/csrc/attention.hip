@@ -152,9 +152,228 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
   }
 }
 
+// Decode rows that each own their (slot, position) (one row, or rows of different sequences): the q/k/v epilogue,
+// RoPE and cache write of k_qkv_rope_cache and the attention of k_attention in one launch. Block (r, h) rebuilds
+// its query head and its KV head's new key and value at pos[r] from the totals t, attends over the cached
+// positions < pos[r] and over the new one from LDS, and the first query head of each KV group writes the new key
+// and value into the cache (the other blocks never read that position from the cache). The arithmetic is the
+// two kernels' own: the same shifts, rounding, RoPE, quantisation and dot products. t is left as it is.
+// Latency: everything that does not depend on the new token (the RoPE row, each thread's first cached key and
+// its first ATT_VPF value pairs) is loaded together with t, so the block waits on memory about once before the
+// exp table.
+#define ATT_KPF 16   // 16-byte key chunks prefetched per thread (hd <= 128)
+#define ATT_VPF 4    // value pairs prefetched per thread
+__global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
+                                                               const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
+                                                               const int64_t* __restrict__ sin_t, const int32_t* __restrict__ slot,
+                                                               const int32_t* __restrict__ pos, int16_t* __restrict__ kq,
+                                                               int32_t* __restrict__ sk, int64_t* __restrict__ v,
+                                                               const int32_t* __restrict__ expt, int64_t* __restrict__ out,
+                                                               int32_t* __restrict__ obits, int H, int KV, int hd, int Smax,
+                                                               int INV) {
+  extern __shared__ int64_t sc[];   // Smax entries
+  __shared__ int64_t y[3][256];     // q head, new key, new value: shr(t, 28 - s) + b
+  __shared__ int32_t qs[256], kn[256];
+  __shared__ int32_t shq[2];
+  __shared__ int ored[ATT_THREADS / 64];
+  __shared__ int64_t red[16];
+  __shared__ int64_t part[ATT_THREADS * 2];
+  const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = H / KV, kh = h / grp;
+  const int N = (H + 2 * KV) * hd;
+  const int p = pos[r], sl = slot[r];
+  if (p < 0 || p >= Smax) {   // the host keeps positions inside the cache; write nothing there
+    for (int d = tid; d < hd; d += blockDim.x) out[((int64_t)r * H + h) * hd + d] = 0;
+    if (obits && tid == 0) obits[(int64_t)r * H + h] = 0;
+    return;
+  }
+  const int64_t cbase = ((int64_t)sl * KV + kh) * Smax;
+  const int npair = hd >> 1, nparts = blockDim.x / npair;
+  const int dp = tid % npair, pp = tid / npair;
+  // ---- loads that do not depend on the new token, issued with the totals
+  v4i kpre[ATT_KPF];
+  int skpre = 0;
+  const bool kp = hd <= 8 * ATT_KPF && tid < p;
+  if (kp) {
+    const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + tid) * hd);
+#pragma unroll
+    for (int j8 = 0; j8 < ATT_KPF; ++j8)
+      if (j8 < hd / 8) kpre[j8] = kr[j8];
+    skpre = sk[cbase + tid];
+  }
+  v4i vpre[ATT_VPF];
+  const int64_t* vb = v + cbase * hd + 2 * dp;
+#pragma unroll
+  for (int i = 0; i < ATT_VPF; ++i) {
+    const int si = pp + i * nparts;
+    if (pp < nparts && si < p) vpre[i] = *reinterpret_cast<const v4i*>(vb + (int64_t)si * hd);
+  }
+  int64_t cs[4][2];
+  if (wave < 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = lane + 64 * i;
+      cs[i][0] = j < hd ? cos_t[(int64_t)p * hd + j] : 0;
+      cs[i][1] = j < hd ? sin_t[(int64_t)p * hd + j] : 0;
+    }
+  }
+  const int sh = 28 - s[r];
+  for (int j = tid; j < 3 * hd; j += blockDim.x) {
+    const int which = j / hd, jj = j - which * hd;
+    const int base = which == 0 ? h * hd : (which == 1 ? (H + kh) * hd : (H + KV + kh) * hd);
+    const int64_t val = shr64(t[(int64_t)r * N + base + jj], sh);
+    y[which][jj] = b ? val + b[base + jj] : val;
+  }
+  __syncthreads();
+  if (wave < 2) {   // wave 0: RoPE + qrow of the query head, wave 1: of the new key (k_qkv_rope_cache's steps)
+    const int half = hd >> 1;
+    const int64_t* yy = y[wave];
+    int64_t z[4];
+    int64_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = lane + 64 * i;
+      z[i] = 0;
+      if (j < hd) {
+        const int64_t rot = j < half ? -yy[j + half] : yy[j - half];
+        z[i] = shr64(yy[j] * cs[i][0] + rot * cs[i][1], EXACT_F);
+        const int64_t a = abs64(z[i]);
+        m = a > m ? a : m;
+      }
+    }
+    m = wave_max64(m);
+    int q = bitlen64(m) - 15;
+    if (q < 0) q = 0;
+    int32_t* dst = wave == 0 ? qs : kn;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = lane + 64 * i;
+      if (j < hd) {
+        const int64_t w = shr64(z[i], q);
+        dst[j] = (int32_t)(w > 32767 ? 32767 : (w < -32767 ? -32767 : w));
+      }
+    }
+    if (lane == 0) shq[wave] = q;
+  }
+  __syncthreads();
+  const int sqv = shq[0], skn = shq[1];
+  if (h % grp == 0) {   // one block per KV head writes the new position
+    for (int j = tid; j < hd; j += blockDim.x) {
+      kq[(cbase + p) * hd + j] = (int16_t)kn[j];
+      v[(cbase + p) * hd + j] = y[2][j];
+    }
+    if (tid == 0) sk[cbase + p] = skn;
+  }
+  const int S = p + 1;
+  int64_t mx = INT64_MIN;
+  for (int si = tid; si < p; si += blockDim.x) {
+    const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + si) * hd);
+    int64_t dot = 0;
+    int skv;
+    if (kp && si == tid) {   // the prefetched first key
+#pragma unroll
+      for (int j8 = 0; j8 < ATT_KPF; ++j8) {
+        if (j8 < hd / 8) {
+          const v4i kk = kpre[j8];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int j = j8 * 8 + 2 * c;
+            dot += (int64_t)(qs[j] * (int32_t)(int16_t)(kk[c] & 0xffff) + qs[j + 1] * (int32_t)(int16_t)(kk[c] >> 16));
+          }
+        }
+      }
+      skv = skpre;
+    } else {
+#pragma unroll 4
+      for (int j8 = 0; j8 < hd / 8; ++j8) {
+        const v4i kk = kr[j8];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int j = j8 * 8 + 2 * c;
+          dot += (int64_t)(qs[j] * (int32_t)(int16_t)(kk[c] & 0xffff) + qs[j + 1] * (int32_t)(int16_t)(kk[c] >> 16));
+        }
+      }
+      skv = sk[cbase + si];
+    }
+    const int64_t val = shr64(dot * INV, 32 - sqv - skv);
+    sc[si] = val;
+    mx = val > mx ? val : mx;
+  }
+  if (tid == (p % blockDim.x)) {   // the new key, from LDS
+    int64_t dot = 0;
+    for (int j = 0; j < hd; j += 2) dot += (int64_t)(qs[j] * kn[j] + qs[j + 1] * kn[j + 1]);
+    const int64_t val = shr64(dot * INV, 32 - sqv - skn);
+    sc[p] = val;
+    mx = val > mx ? val : mx;
+  }
+  mx = block_max64(mx, red);
+  int64_t es = 0;
+  for (int si = tid; si < S; si += blockDim.x) {
+    const int64_t e = lut_exp(expt, mx - sc[si]);
+    sc[si] = e;
+    es += e;
+  }
+  es = block_sum64(es, red);
+  for (int si = tid; si < S; si += blockDim.x) sc[si] = floordiv_pos(shl64(sc[si], 20), es);
+  __syncthreads();
+  int64_t a0 = 0, a1 = 0;
+  if (pp < nparts) {
+#pragma unroll
+    for (int i = 0; i < ATT_VPF; ++i) {
+      const int si = pp + i * nparts;
+      if (si < p) {
+        const v4i vv = vpre[i];
+        const int64_t pr = sc[si];
+        a0 = (int64_t)((uint64_t)a0 + (uint64_t)(pr * (((int64_t)vv[1] << 32) | (uint32_t)vv[0])));
+        a1 = (int64_t)((uint64_t)a1 + (uint64_t)(pr * (((int64_t)vv[3] << 32) | (uint32_t)vv[2])));
+      }
+    }
+#pragma unroll 8
+    for (int si = pp + ATT_VPF * nparts; si < p; si += nparts) {
+      const v4i vv = *reinterpret_cast<const v4i*>(vb + (int64_t)si * hd);
+      const int64_t pr = sc[si];
+      a0 = (int64_t)((uint64_t)a0 + (uint64_t)(pr * (((int64_t)vv[1] << 32) | (uint32_t)vv[0])));
+      a1 = (int64_t)((uint64_t)a1 + (uint64_t)(pr * (((int64_t)vv[3] << 32) | (uint32_t)vv[2])));
+    }
+    if (pp == p % nparts) {   // the new value, from LDS
+      const int64_t pr = sc[p];
+      a0 = (int64_t)((uint64_t)a0 + (uint64_t)(pr * y[2][2 * dp]));
+      a1 = (int64_t)((uint64_t)a1 + (uint64_t)(pr * y[2][2 * dp + 1]));
+    }
+  }
+  part[2 * tid] = a0;
+  part[2 * tid + 1] = a1;
+  __syncthreads();
+  int m = 0;
+  if (tid < hd) {
+    const int d = tid;
+    uint64_t tot = 0;
+    for (int k = 0; k < nparts; ++k) tot += (uint64_t)part[2 * (k * npair + (d >> 1)) + (d & 1)];
+    const int64_t o = shr64((int64_t)tot, 20);
+    out[((int64_t)r * H + h) * hd + d] = o;
+    m = bitlen64(abs64(o));
+  }
+  if (obits) {
+    m = block_max_i32(m, ored);
+    if (tid == 0) obits[(int64_t)r * H + h] = m;
+  }
+}
+
 }  // namespace exact
 
 using namespace exact;
+
+extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
+                                   const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* kq, int32_t* sk,
+                                   int64_t* v, const int32_t* exp_t, int64_t* out, int32_t* obits, int32_t R, int32_t H,
+                                   int32_t KV, int32_t hd, int32_t Smax, int32_t INV, void* stream) {
+  if (!t || !s || !cos_t || !sin_t || !slot || !pos || !kq || !sk || !v || !exp_t || !out) return EXACT_E_ARG;
+  if (R <= 0 || H <= 0 || KV <= 0 || H % KV || hd <= 0 || Smax <= 0) return EXACT_E_ARG;
+  if (hd > 256 || hd % 8 || (2 * ATT_THREADS) % hd || Smax > 8192) return EXACT_E_UNSUPPORTED;
+  hipLaunchKernelGGL(k_attention_qkv, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), t, s, b, cos_t,
+                     sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
+  return launch_status("attention_qkv");
+}
 
 extern "C" int exact_qkv_rope_cache(int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
                                     const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* qq, int32_t* sq,

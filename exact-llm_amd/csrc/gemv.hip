@@ -248,8 +248,10 @@ __global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict_
                                                       const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
                                                       const int16_t* __restrict__ mh, int64_t* __restrict__ t,
                                                       int32_t* __restrict__ s_out, int R, int N, int K, int G, int nsplit,
-                                                      int gmax) {
+                                                      int gmax, int64_t* __restrict__ zero, int64_t zero_n) {
   extern __shared__ __attribute__((aligned(16))) int8_t xlds[];
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += (int64_t)gridDim.x * blockDim.x)
+    zero[i] = 0;
   constexpr int EB = ABITS == 15 ? 2 : 1;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int task = blockIdx.x * 4 + wave;
@@ -486,9 +488,10 @@ extern "C" int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* w
 
 extern "C" int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const int32_t* part, int32_t nparts, int32_t abits,
                                         const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int32_t* s_out,
-                                        int32_t R, int32_t N, int32_t K, void* stream) {
+                                        int32_t R, int32_t N, int32_t K, int64_t* zero, int64_t zero_n, void* stream) {
   if (!xs || !part || !wp || !mp || !t || !s_out || R <= 0 || N <= 0 || K <= 0 || nparts <= 0 || ldx < K)
     return EXACT_E_ARG;
+  if (zero_n < 0 || (zero_n > 0 && !zero)) return EXACT_E_ARG;
   if ((abits != 15 && abits != 7) || K % 128 || (reinterpret_cast<uintptr_t>(wp) & 15)) return EXACT_E_UNSUPPORTED;
   if (R > (abits == 15 ? 15 : 16)) return EXACT_E_UNSUPPORTED;
   const int G = K / 128;
@@ -503,10 +506,10 @@ extern "C" int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const in
   do {                                                                                                                 \
     if (mh)                                                                                                            \
       hipLaunchKernelGGL((k_gemv_g128_xq<AB, GEMV_NT != 0, VR, true>), grid, block, lds, st, xs, ldx, part, nparts, wp, mp, \
-                         mh, t, s_out, R, N, K, G, nsplit, gmax);                                                      \
+                         mh, t, s_out, R, N, K, G, nsplit, gmax, zero, zero_n);                                        \
     else                                                                                                               \
       hipLaunchKernelGGL((k_gemv_g128_xq<AB, GEMV_NT != 0, VR, false>), grid, block, lds, st, xs, ldx, part, nparts, wp,   \
-                         mp, mh, t, s_out, R, N, K, G, nsplit, gmax);                                                  \
+                         mp, mh, t, s_out, R, N, K, G, nsplit, gmax, zero, zero_n);                                    \
   } while (0)
   const int vr = R <= 1 ? 1 : (R <= 2 ? 2 : 4);
   if (abits == 15) {

@@ -24,7 +24,7 @@ SIGNATURES = {
     "exact_gemv_g128_acc": [P, I32, P, P, P, P, I32, I32, I32, P],
     "exact_gemm_g128": [P, I32, P, P, P, P, I32, I32, I32, P],
     "exact_gemm_g128_a16": [P, P, P, P, P, P, P, I32, I32, I32, P],
-    "exact_gemv_g128_qrow_acc": [P, I64, P, I32, I32, P, P, P, P, P, I32, I32, I32, P],
+    "exact_gemv_g128_qrow_acc": [P, I64, P, I32, I32, P, P, P, P, P, I32, I32, I32, P, I64, P],
     "exact_requant_group": [P, P, P, P, I32, I32, P],
     "exact_requant_channel": [P, P, P, I32, P, P, I32, I32, P],
     "exact_qrow": [P, I32, P, P, I32, I32, P],
@@ -37,6 +37,7 @@ SIGNATURES = {
     "exact_isoftmax": [P, P, P, P, I32, I32, P],
     "exact_qkv_rope_cache": [P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
     "exact_attention": [P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
+    "exact_attention_qkv": [P, P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
     "exact_attention_prefill": [P, P, P, P, P, I32, P, P, P, P, P, I64, I32, I32, I32, I32, I32, I32, I32, P],
     "exact_embed": [P, P, P, I32, I32, I32, P],
     "exact_embed_table": [P, P, P, I32, I32, P],

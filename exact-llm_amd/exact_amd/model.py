@@ -269,9 +269,11 @@ class TModel:
         return out
 
     # ---------------------------------------------------------------- one pass over R rows
-    def forward_rows(self, ws, want_logits=True, trace=None):
+    def forward_rows(self, ws, want_logits=True, trace=None, independent=False):
         """Runs the model on ws.ids with (slot, pos) per row; KV of each row is written into the cache
         at (slot, pos). Leaves logits in ws.logits and greedy ids in ws.next_ids.
+        independent: every row is a different sequence (decode), so no row attends to another row's new key and
+        the q/k/v epilogue runs inside the attention launch.
         trace: (TraceLayout, int64 device buffer): every linear's totals t are produced in the buffer's slots
         and left there (the buffer is zeroed first); the consumer kernels read them without clearing."""
         c, R, tab = self.cfg, ws.R, self.tab
@@ -291,6 +293,7 @@ class TModel:
         # qrow launch); every 64-row block of the GEMV re-reads its slice of the row, which costs more than the saved
         # launch at 8 rows
         xfuse = group and R <= self.QROW_FUSE_ROWS
+        afuse = xfuse and ws.seq is None and (R == 1 or independent)
         if xfuse and ws.h is None and c.I > 8192 and not c.moe:
             ws.h = torch.zeros((R, ws.I), dtype=I64, device=self.dev)
         ops.embed(ws.ids, self.w.emb, ws.x)
@@ -313,15 +316,20 @@ class TModel:
                     ws.t_qkv[:, off:off + lin.N].copy_(y)
                     off += lin.N
                 s_qkv, b_qkv = ws.s28, None
-            ops.qkv_rope_cache(t_qkv if group else ws.t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache, ws.qq,
-                               ws.sq, H, KV, hd, clear=clear)
-            if ws.seq is not None:
-                ops.attention_prefill(ws.qq, ws.sq, cache, ws.seq[0], ws.pos, ws.seq[1], tab.exp, ws.att, H, KV, hd, tab.inv,
-                                      self._prefill_ws(R), ws.obits)
+            if afuse:
+                ops.attention_qkv(t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache, tab.exp, ws.att, H, KV, hd,
+                                  tab.inv, ws.obits)
             else:
-                ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv, ws.obits)
+                ops.qkv_rope_cache(t_qkv if group else ws.t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache,
+                                   ws.qq, ws.sq, H, KV, hd, clear=clear)
+                if ws.seq is not None:
+                    ops.attention_prefill(ws.qq, ws.sq, cache, ws.seq[0], ws.pos, ws.seq[1], tab.exp, ws.att, H, KV, hd,
+                                          tab.inv, self._prefill_ws(R), ws.obits)
+                else:
+                    ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv, ws.obits)
             if xfuse:
-                ops.gemv_qrow_acc(ws.att, ws.obits, H, self.abits, L["o"], t_o, ws.sa)
+                ops.gemv_qrow_acc(ws.att, ws.obits, H, self.abits, L["o"], t_o, ws.sa,
+                                  zero=t_qkv if afuse and clear else None)   # the q|k|v totals attention left
             else:
                 ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa)
             if group:
@@ -476,7 +484,7 @@ class TModel:
         ws.pos.copy_(torch.tensor(cache.n[:B], dtype=I32))
         if max(cache.n[:B]) >= self.Smax:
             raise ExactError("cache full")
-        self.forward_rows(ws)
+        self.forward_rows(ws, independent=True)
         for r in range(B):
             cache.n[r] += 1
         return ws.logits.clone(), ws.next_ids.clone()
@@ -567,7 +575,7 @@ class GraphDecoder:
 
     def _step(self, b=0):
         self.tm._cache = self.cache
-        self.tm.forward_rows(self.ws, trace=(self.layout, self.trace_bufs[b]) if self.trace else None)
+        self.tm.forward_rows(self.ws, trace=(self.layout, self.trace_bufs[b]) if self.trace else None, independent=True)
         ops.advance(self.ws.pos)
 
     def capture(self):

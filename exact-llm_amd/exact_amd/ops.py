@@ -125,9 +125,10 @@ def gemv_g128_acc(x, abits, lin, out):
     return _linear("exact_gemv_g128_acc", x, abits, lin, out)
 
 
-def gemv_qrow_acc(xs, part, nparts, abits, lin, out, s_out, K=None):
+def gemv_qrow_acc(xs, part, nparts, abits, lin, out, s_out, K=None, zero=None):
     """out (R, N) += qrow(xs[:, :K], abits) . W in one launch, the row shifts from the producer's slice bit lengths
-    part (R, nparts); s_out (R,) int32 receives the shifts. xs: int64 (R, ldx)."""
+    part (R, nparts); s_out (R,) int32 receives the shifts. xs: int64 (R, ldx). zero: an int64 tensor the launch
+    also clears."""
     R, ldx = xs.shape
     K = lin.K if K is None else K
     if K != lin.K:
@@ -137,7 +138,8 @@ def gemv_qrow_acc(xs, part, nparts, abits, lin, out, s_out, K=None):
     _need(out, I64, "out", R * lin.N)
     _need(s_out, I32, "s_out", R)
     _lib.call("exact_gemv_g128_qrow_acc", _ptr(xs), ldx, _ptr(part), nparts, abits, _ptr(lin.wp), _ptr(lin.mp), _ptr(lin.mh),
-              _ptr(out), _ptr(s_out), R, lin.N, K, _stream())
+              _ptr(out), _ptr(s_out), R, lin.N, K, _ptr(zero), 0 if zero is None else _need(zero, I64, "zero").numel(),
+              _stream())
     return out
 
 
@@ -320,6 +322,20 @@ def attention(qq, sq, cache, slot, pos, expt, out, H, KV, hd, inv, obits=None):
         _need(obits, I32, "obits", R * H)
     _lib.call("exact_attention", _ptr(qq), _ptr(sq), _ptr(kq), _ptr(sk), _ptr(v), _ptr(slot), _ptr(pos), _ptr(expt),
               _ptr(out), _ptr(obits), R, H, KV, hd, Smax, inv, _stream())
+    return out
+
+
+def attention_qkv(t, s, b, cos_t, sin_t, slot, pos, cache, expt, out, H, KV, hd, inv, obits=None):
+    """qkv_rope_cache + attention in one launch for rows that each own their (slot, position); t unchanged."""
+    R = t.shape[0]
+    kq, sk, v = cache
+    _need(t, I64, "t", R * (H + 2 * KV) * hd)
+    _need(out, I64, "out", R * H * hd)
+    if obits is not None:
+        _need(obits, I32, "obits", R * H)
+    _lib.call("exact_attention_qkv", _ptr(t), _ptr(_need(s, I32, "s", R)), _ptr(b), _ptr(cos_t), _ptr(sin_t), _ptr(slot),
+              _ptr(pos), _ptr(kq), _ptr(sk), _ptr(v), _ptr(expt), _ptr(out), _ptr(obits), R, H, KV, hd, kq.shape[2], inv,
+              _stream())
     return out
 
 

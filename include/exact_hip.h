@@ -91,10 +91,12 @@ int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_
  * obits, exact_swiglu_qrow's slice bit lengths); s_out[r] = s. Replaces exact_quant_rows + exact_gemv_g128_acc
  * (qrow, exact_llm.py:41-46; TLinG, speed_fair_kaggle.py:735-738) with one launch. R <= 15 (abits 15) or
  * 16 (abits 7), nparts <= 64; returns 2 when a wave's share of a row exceeds 512 columns (the GEMV's group
- * split leaves 4 groups or fewer per wave at the decode shapes) or the slices of a block 64 KiB of LDS. */
+ * split leaves 4 groups or fewer per wave at the decode shapes) or the slices of a block 64 KiB of LDS.
+ * zero (optional): zero_n int64 the launch also clears (a buffer whose readers have finished, e.g. the q|k|v
+ * totals exact_attention_qkv leaves in place), so no separate clear is launched. */
 int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const int32_t* part, int32_t nparts, int32_t abits,
                              const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int32_t* s_out,
-                             int32_t R, int32_t N, int32_t K, void* stream);
+                             int32_t R, int32_t N, int32_t K, int64_t* zero, int64_t zero_n, void* stream);
 
 /* MoE expert GEMM on the matrix cores, grouped over the chunks exact_moe_dispatch wrote with chunk_rows = 128
  * (int16 x) or 256 (int8 x): for every chunk c < nchunks[0], rows p = chunk_p0[c] .. + chunk_n[c] of the
@@ -190,6 +192,16 @@ int exact_attention(const int16_t* qq, const int32_t* sq, const int16_t* kq, con
                     const int64_t* v, const int32_t* slot, const int32_t* pos, const int32_t* exp_t,
                     int64_t* out, int32_t* obits, int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t Smax,
                     int32_t INV, void* stream);
+
+/* exact_qkv_rope_cache followed by exact_attention in one launch, for decode rows that each own their
+ * (slot, position): one row, or rows of different sequences (rows of one sequence in one pass read each
+ * other's new keys and take the two launches). Same results, cache contents and obits; the quantised
+ * queries stay on chip (no qq / sq) and t is left unchanged. Replaces the per-layer q/k/v epilogue + RoPE +
+ * cache write + attention of exact_llm.py:170-176 / speed_fair_kaggle.py:603-624 at decode. */
+int exact_attention_qkv(const int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
+                        const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* kq, int32_t* sk,
+                        int64_t* v, const int32_t* exp_t, int64_t* out, int32_t* obits, int32_t R, int32_t H,
+                        int32_t KV, int32_t hd, int32_t Smax, int32_t INV, void* stream);
 
 /* The same attention for the prefill of one sequence on the matrix cores: R query rows of cache slot `slot`
  * at increasing positions pos[r] (< nkeys), against keys 0..pos[r]; results identical to exact_attention

@@ -118,3 +118,48 @@ def test_prefill_full_size_2048():
     assert np.array_equal(obits, host(refbits))
     rows = np.sort(np.concatenate([[0, 1, 31, 32, S - 1], np.random.default_rng(3).choice(S, 19, replace=False)]))
     assert np.array_equal(out[rows], oracle_rows(*case, slot, H, KV, rows))
+
+
+@pytest.mark.parametrize("H,KV,hd,R,bias", [(28, 4, 128, 1, True), (28, 4, 128, 4, False), (14, 2, 64, 3, True),
+                                            (4, 4, 256, 2, True)])
+def test_fused_qkv_attention_matches_two_launches(H, KV, hd, R, bias):
+    """exact_attention_qkv against exact_qkv_rope_cache + exact_attention (both oracle-pinned above and in the
+    model tests): outputs, obits and every cache entry equal; rows in different slots at positions 0, Smax - 1 and
+    in between; the totals t are left unchanged."""
+    from exact_amd.tables import host_tables
+    rng = np.random.default_rng(H + R + hd)
+    B, Smax = R + 2, 96
+    N = (H + 2 * KV) * hd
+    kq = rng.integers(-32767, 32768, (B, KV, Smax, hd))
+    sk = rng.integers(0, 4, (B, KV, Smax))
+    v = rng.integers(-(1 << 29), 1 << 29, (B, KV, Smax, hd))
+    slot = rng.permutation(B)[:R]
+    pos = rng.integers(1, Smax - 1, R)
+    pos[0] = 0
+    if R > 1:
+        pos[1] = Smax - 1
+    t = rng.integers(-(1 << 44), 1 << 44, (R, N))
+    s = rng.integers(0, 12, R)
+    b = rng.integers(-(1 << 20), 1 << 20, N) if bias else None
+    tabs = host_tables(Smax, hd, 1e6)
+    d = lambda a, dt: torch.tensor(np.ascontiguousarray(a), dtype=dt, device=DEV)
+    cos, sin, expt = d(tabs["cos"], I64), d(tabs["sin"], I64), d(exp_t(), I32)
+    args = dict(H=H, KV=KV, hd=hd)
+    inv = O.inv_sqrt_hd(hd)
+    c_a = (d(kq, I16), d(sk, I32), d(v, I64))
+    c_b = tuple(x.clone() for x in c_a)
+    t_a, t_b = d(t, I64), d(t, I64)
+    s_d, b_d, slot_d, pos_d = d(s, I32), None if b is None else d(b, I64), d(slot, I32), d(pos, I32)
+    qq, sq = torch.empty((R, H * hd), dtype=I16, device=DEV), torch.empty((R, H), dtype=I32, device=DEV)
+    out_a = torch.full((R, H * hd), -7, dtype=I64, device=DEV)
+    out_b = torch.full((R, H * hd), -9, dtype=I64, device=DEV)
+    ob_a = torch.full((R, H), -1, dtype=I32, device=DEV)
+    ob_b = torch.full((R, H), -2, dtype=I32, device=DEV)
+    ops.qkv_rope_cache(t_a, s_d, b_d, cos, sin, slot_d, pos_d, c_a, qq, sq, clear=False, **args)
+    ops.attention(qq, sq, c_a, slot_d, pos_d, expt, out_a, inv=inv, obits=ob_a, **args)
+    ops.attention_qkv(t_b, s_d, b_d, cos, sin, slot_d, pos_d, c_b, expt, out_b, inv=inv, obits=ob_b, **args)
+    assert np.array_equal(host(out_b), host(out_a))
+    assert np.array_equal(host(ob_b), host(ob_a))
+    for x, y in zip(c_b, c_a):
+        assert np.array_equal(host(x), host(y))
+    assert np.array_equal(host(t_b), t)
