@@ -59,6 +59,9 @@ __global__ void k_router_topk(int64_t* __restrict__ t, int ld, const int32_t* __
 // One block of 16 waves. Pair q = r * k + j. Wave w owns experts e = w, w + 16, ...: it walks the pairs 64 at a
 // time, and a ballot of "pair q belongs to e" gives both the expert's count and, with the count of set bits
 // below each lane, each pair's stable position (q order) inside its expert. Then the chunks of each expert.
+// The pairs' expert ids are walked from registers, DISPATCH_RB blocks of 64 at a time, and the offsets come from
+// a wave-level scan, so no step waits on a chain of LDS reads.
+#define DISPATCH_RB 16
 __global__ __launch_bounds__(1024) void k_moe_dispatch(const int32_t* __restrict__ e_sel, const int32_t* __restrict__ s,
                                                        int32_t* __restrict__ pidx, int32_t* __restrict__ pair_row,
                                                        int32_t* __restrict__ s_pair, int32_t* __restrict__ chunk_e,
@@ -69,47 +72,84 @@ __global__ __launch_bounds__(1024) void k_moe_dispatch(const int32_t* __restrict
   int32_t* cnt = es + P;          // NE counts
   int32_t* off = cnt + NE;        // NE pair offsets
   int32_t* coff = off + NE;       // NE chunk offsets
+  int32_t* srow = coff + NE;      // P / k row shifts (no global load inside the pair walk)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   for (int q = threadIdx.x; q < P; q += blockDim.x) es[q] = e_sel[q];
+  for (int r = threadIdx.x; r < P / k; r += blockDim.x) srow[r] = s[r];
+  for (int e = threadIdx.x; e < NE; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
-  for (int e = wave; e < NE; e += nw) {
-    int c = 0;
-    for (int b = 0; b < P; b += 64) c += __popcll(__ballot(b + lane < P && es[b + lane] == e));
-    if (lane == 0) cnt[e] = c;
+  for (int b0 = 0; b0 < P; b0 += 64 * DISPATCH_RB) {
+    int ev[DISPATCH_RB];
+#pragma unroll
+    for (int i = 0; i < DISPATCH_RB; ++i) {
+      const int q = b0 + 64 * i + lane;
+      ev[i] = q < P ? es[q] : -1;
+    }
+    for (int e = wave; e < NE; e += nw) {   // cnt[e] belongs to this wave
+      int c = 0;
+#pragma unroll
+      for (int i = 0; i < DISPATCH_RB; ++i) c += __popcll(__ballot(ev[i] == e));
+      if (lane == 0) cnt[e] += c;
+    }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (wave == 0) {   // exclusive scans of the counts and of the chunk counts, 64 experts at a time
     int po = 0, co = 0;
-    for (int e = 0; e < NE; ++e) {
-      off[e] = po;
-      coff[e] = co;
-      po += cnt[e];
-      co += (cnt[e] + CH - 1) / CH;
+    for (int e0 = 0; e0 < NE; e0 += 64) {
+      const int e = e0 + lane;
+      const int c = e < NE ? cnt[e] : 0, nc = (c + CH - 1) / CH;
+      int ic = c, inc = nc;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(ic, d, 64), un = __shfl_up(inc, d, 64);
+        if (lane >= d) {
+          ic += u;
+          inc += un;
+        }
+      }
+      if (e < NE) {
+        off[e] = po + ic - c;
+        coff[e] = co + inc - nc;
+      }
+      po += __shfl(ic, 63, 64);
+      co += __shfl(inc, 63, 64);
     }
-    nchunks[0] = co;
+    if (lane == 0) nchunks[0] = co;
   }
   __syncthreads();
   const uint64_t below = lane ? (~0ULL >> (64 - lane)) : 0ULL;   // lanes below this one
   for (int e = wave; e < NE; e += nw) {
-    int run = off[e];
-    for (int b = 0; b < P; b += 64) {
-      const int q = b + lane;
-      const bool mine = q < P && es[q] == e;
-      const uint64_t m = __ballot(mine);
-      if (mine) {
-        const int pos = run + __popcll(m & below);
-        pidx[q] = pos;
-        pair_row[pos] = q / k;
-        s_pair[pos] = s[q / k];
-      }
-      run += __popcll(m);
-    }
     const int n = cnt[e];
     for (int c = lane; c * CH < n; c += 64) {
       const int idx = coff[e] + c;
       chunk_e[idx] = e;
       chunk_p0[idx] = off[e] + c * CH;
       chunk_n[idx] = n - c * CH < CH ? n - c * CH : CH;
+    }
+  }
+  for (int b0 = 0; b0 < P; b0 += 64 * DISPATCH_RB) {
+    int ev[DISPATCH_RB];
+#pragma unroll
+    for (int i = 0; i < DISPATCH_RB; ++i) {
+      const int q = b0 + 64 * i + lane;
+      ev[i] = q < P ? es[q] : -1;
+    }
+    for (int e = wave; e < NE; e += nw) {
+      int run = off[e];
+#pragma unroll
+      for (int i = 0; i < DISPATCH_RB; ++i) {
+        const bool mine = ev[i] == e;
+        const uint64_t m = __ballot(mine);
+        if (mine) {
+          const int q = b0 + 64 * i + lane;
+          const int pos = run + __popcll(m & below);
+          pidx[q] = pos;
+          pair_row[pos] = q / k;
+          s_pair[pos] = srow[q / k];
+        }
+        run += __popcll(m);
+      }
+      if (lane == 0) off[e] = run;   // the next register batch continues after these pairs
     }
   }
 }
@@ -160,8 +200,8 @@ extern "C" int exact_moe_dispatch(const int32_t* e_sel, const int32_t* s, int32_
   if (!e_sel || !s || !pidx || !pair_row || !s_pair || !chunk_e || !chunk_p0 || !chunk_n || !nchunks) return EXACT_E_ARG;
   if (R <= 0 || NE <= 0 || k <= 0 || k > NE || chunk_rows <= 0) return EXACT_E_ARG;
   const int64_t P = (int64_t)R * k;
-  if (P + 3LL * NE > 16384) return EXACT_E_UNSUPPORTED;   // 64 KiB of LDS
-  hipLaunchKernelGGL(k_moe_dispatch, dim3(1), dim3(1024), (size_t)(P + 3 * NE) * sizeof(int32_t), as_stream(stream), e_sel,
+  if (P + 3LL * NE + R > 16384) return EXACT_E_UNSUPPORTED;   // 64 KiB of LDS
+  hipLaunchKernelGGL(k_moe_dispatch, dim3(1), dim3(1024), (size_t)(P + 3 * NE + R) * sizeof(int32_t), as_stream(stream), e_sel,
                      s, pidx, pair_row, s_pair, chunk_e, chunk_p0, chunk_n, nchunks, (int)P, NE, k, chunk_rows);
   return launch_status("moe_dispatch");
 }

@@ -58,7 +58,7 @@ def test_router_topk_matches_oracle(tab, R, NE, k):
 
 
 @pytest.mark.parametrize("R,NE,k,ch", [(1, 60, 4, 15), (8, 60, 4, 15), (256, 60, 4, 15), (40, 6, 2, 16), (2048, 4, 2, 15),
-                                      (100, 130, 8, 16)])
+                                      (100, 130, 8, 16), (2048, 60, 4, 128), (333, 60, 4, 256)])
 def test_dispatch_groups_pairs_by_expert(R, NE, k, ch):
     rng = np.random.default_rng(R + NE)
     e_sel = np.stack([rng.choice(NE, k, replace=False) for _ in range(R)])
