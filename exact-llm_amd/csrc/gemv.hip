@@ -389,9 +389,19 @@ int zero_bytes(void* dst, int64_t nbytes, hipStream_t st) {
 #ifndef GEMV_CHUNKS_MAX
 #define GEMV_CHUNKS_MAX 3
 #endif
-static int gemv_nsplit(int N, int G) {
+// Above 4 rows each wave adds 64 x 16 int64 partial totals with atomics, so fewer group splits pay for most shapes.
+// Measured at 8 and 16 rows on the 7B shapes (us, int16 / int8 rows at 16): q|k|v 19.2 -> 11.3 / 17.9 -> 10.1 and
+// o 15.3 -> 11.3 / 13.7 -> 9.7 at 768 waves instead of 3072; gate|up (592 row blocks) 39.9 -> 32.6 at 1536 for int16
+// rows; int8 gate|up and down (148 groups) stay fastest at 3072.
+static int64_t gemv_waves(int64_t nbs, int G, int R, int abits) {
+  if (R <= 4) return GEMV_WAVES;
+  if (abits == 15) return nbs > 256 ? 1536 : 768;
+  return (nbs > 256 || G > 64) ? GEMV_WAVES : 768;
+}
+static int gemv_nsplit(int N, int G, int R = 1, int abits = 15) {
   const int64_t nbs = (N + 63) / 64;
-  int64_t ns = (GEMV_WAVES + nbs - 1) / nbs;
+  const int64_t waves = gemv_waves(nbs, G, R, abits);
+  int64_t ns = (waves + nbs - 1) / nbs;
   if (ns < 1) ns = 1;
   if (ns > G) ns = G;
   return (int)ns;
@@ -406,7 +416,7 @@ int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, con
 int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int R, int N,
                 int K, hipStream_t st, bool accumulate, const int64_t* colterm = nullptr) {
   const int G = K / 128;
-  const int nsplit = gemv_nsplit(N, G);
+  const int nsplit = gemv_nsplit(N, G, R, abits);
   const int out_mode = (accumulate || nsplit > 1) ? 1 : 0;
   if (!accumulate && nsplit > 1) {
     int e = zero_bytes(t, (int64_t)R * N * 8, st);
