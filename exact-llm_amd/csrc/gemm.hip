@@ -572,7 +572,7 @@ __global__ __launch_bounds__(256) void k_gather_rows_a8(const int8_t* __restrict
 
 template <int ABITS, int WM, int WN, int S>
 static int gemm_launch(const void* x, const int8_t* wp, const int16_t* mp, int64_t* t, int M, int N, int K,
-                       hipStream_t st, int ksplit_req) {
+                       hipStream_t st, int ksplit_req, bool zeroed = false) {
   using C = GemmCfg<ABITS, WM, WN, S>;
   static bool attr_set = false;
   const size_t lds = S * (size_t)C::STAGE;
@@ -591,7 +591,7 @@ static int gemm_launch(const void* x, const int8_t* wp, const int16_t* mp, int64
   }
   if (ksplit > G) ksplit = G;
   const int use_atomic = ksplit > 1;
-  if (use_atomic) {
+  if (use_atomic && !zeroed) {
     int e = zero_bytes(t, (int64_t)M * N * 8, st);
     if (e) return e;
   }
@@ -620,7 +620,7 @@ static int gemm_launch(const void* x, const int8_t* wp, const int16_t* mp, int64
 // M: rows of the A operand (digit rows when PAIRS: the output has M / 2 rows, written through colterm)
 template <int WM, int WN, int S, bool PAIRS, bool WIDE>
 static int gemm_launch_a8p_t(const void* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int M, int N,
-                             int K, hipStream_t st, int ksplit_req, const int64_t* colterm) {
+                             int K, hipStream_t st, int ksplit_req, const int64_t* colterm, bool zeroed) {
   using C = GemmCfg<7, WM, WN, S>;
   static bool attr_set = false;
   const size_t lds = S * (size_t)(C::A_BYTES + C::B_BYTES + C::WAVES * (WIDE ? 512 : 256));
@@ -639,7 +639,7 @@ static int gemm_launch_a8p_t(const void* x, const int8_t* wp, const int16_t* mp,
   }
   if (ksplit > G) ksplit = G;
   const int use_atomic = ksplit > 1;
-  if (use_atomic) {
+  if (use_atomic && !zeroed) {
     int e = zero_bytes(t, (int64_t)(PAIRS ? M / 2 : M) * N * 8, st);
     if (e) return e;
   }
@@ -677,9 +677,9 @@ static int gemm_launch_experts(const int8_t* x8, const int8_t* wp, const int16_t
 
 template <int WM, int WN, int S, bool PAIRS = false>
 static int gemm_launch_a8p(const void* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int M, int N,
-                           int K, hipStream_t st, int ksplit_req, const int64_t* colterm = nullptr) {
-  if (mh) return gemm_launch_a8p_t<WM, WN, S, PAIRS, true>(x, wp, mp, mh, t, M, N, K, st, ksplit_req, colterm);
-  return gemm_launch_a8p_t<WM, WN, S, PAIRS, false>(x, wp, mp, nullptr, t, M, N, K, st, ksplit_req, colterm);
+                           int K, hipStream_t st, int ksplit_req, const int64_t* colterm = nullptr, bool zeroed = false) {
+  if (mh) return gemm_launch_a8p_t<WM, WN, S, PAIRS, true>(x, wp, mp, mh, t, M, N, K, st, ksplit_req, colterm, zeroed);
+  return gemm_launch_a8p_t<WM, WN, S, PAIRS, false>(x, wp, mp, nullptr, t, M, N, K, st, ksplit_req, colterm, zeroed);
 }
 
 #ifndef GEMM_A8P
@@ -687,13 +687,14 @@ static int gemm_launch_a8p(const void* x, const int8_t* wp, const int16_t* mp, c
 #endif
 
 // Wide scales (mh) run on the A8 kernel only: int8 rows with M K < 2^32 (int16 rows take exact_gemm_g128_a16).
+// zeroed: t holds zeros on entry, so a K split adds into it without a clear launch.
 int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int M, int N,
-              int K, hipStream_t st) {
+              int K, hipStream_t st, bool zeroed) {
   const bool a8p = GEMM_A8P && abits == 7 && (int64_t)M * K < (1LL << 32);
   if (mh && !a8p) return EXACT_E_UNSUPPORTED;
-  if (abits == 15) return gemm_launch<15, GEMM_A16_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
-  if (a8p) return gemm_launch_a8p<GEMM_A8P_CFG>(x, wp, mp, mh, t, M, N, K, st, GEMM_KSPLIT);
-  return gemm_launch<7, GEMM_A8_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT);
+  if (abits == 15) return gemm_launch<15, GEMM_A16_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT, zeroed);
+  if (a8p) return gemm_launch_a8p<GEMM_A8P_CFG>(x, wp, mp, mh, t, M, N, K, st, GEMM_KSPLIT, nullptr, zeroed);
+  return gemm_launch<7, GEMM_A8_CFG>(x, wp, mp, t, M, N, K, st, GEMM_KSPLIT, zeroed);
 }
 
 int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int R, int N,
@@ -706,11 +707,11 @@ int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, c
 // int16 rows with colterm: up to 3 x 16 rows as GEMV row chunks (one weight stream per chunk, no all-ones row
 // needed), more rows as interleaved digit rows on the A8 GEMM
 int gemm_a16_digit_rows(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, const int64_t* colterm,
-                        int8_t* x8, int64_t* t, int M, int N, int K, hipStream_t st) {
+                        int8_t* x8, int64_t* t, int M, int N, int K, hipStream_t st, bool zeroed) {
   if (M <= A16_GEMV_CHUNKS_MAX * 16) {
     for (int r0 = 0; r0 < M; r0 += 16) {
       const int rows = M - r0 < 16 ? M - r0 : 16;
-      int e = gemv_launch(x + (size_t)r0 * K, 15, wp, mp, mh, t + (size_t)r0 * N, rows, N, K, st, false, colterm);
+      int e = gemv_launch(x + (size_t)r0 * K, 15, wp, mp, mh, t + (size_t)r0 * N, rows, N, K, st, zeroed, colterm);
       if (e) return e;
     }
     return EXACT_OK;
@@ -718,7 +719,7 @@ int gemm_a16_digit_rows(const int16_t* x, const int8_t* wp, const int16_t* mp, c
   const int64_t n16 = (int64_t)M * (K / 16);
   const int blocks = (int)std::min<int64_t>((n16 + 255) / 256, 8192);
   hipLaunchKernelGGL(k_split_rows_a16, dim3(blocks), dim3(256), 0, st, x, x8, (int64_t)M, K, nullptr);
-  return gemm_launch_a8p<GEMM_A8P_CFG, true>(x8, wp, mp, mh, t, 2 * M, N, K, st, GEMM_KSPLIT, colterm);
+  return gemm_launch_a8p<GEMM_A8P_CFG, true>(x8, wp, mp, mh, t, 2 * M, N, K, st, GEMM_KSPLIT, colterm, zeroed);
 }
 
 }  // namespace exact
@@ -760,13 +761,25 @@ extern "C" int exact_gemm_g128_experts(const void* x, int32_t abits, const int32
                                                   max_chunks, t, (int)rows, N, K, st);
 }
 
-extern "C" int exact_gemm_g128_a16(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh,
-                                   const int64_t* colterm, int8_t* x8, int64_t* t, int32_t R, int32_t N, int32_t K,
-                                   void* stream) {
+static int gemm_a16_entry(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                          const int64_t* colterm, int8_t* x8, int64_t* t, int32_t R, int32_t N, int32_t K, void* stream,
+                          bool zeroed) {
   if (!x || !wp || !mp || !colterm || !x8 || !t || R <= 0 || N <= 0 || K <= 0) return EXACT_E_ARG;
   if (K % 128 || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(x8) & 15) ||
       (reinterpret_cast<uintptr_t>(wp) & 15))
     return EXACT_E_UNSUPPORTED;
   if (2 * (int64_t)R * K >= (1LL << 32)) return EXACT_E_UNSUPPORTED;   // 32-bit buffer offsets of the digit rows
-  return gemm_a16_digit_rows(x, wp, mp, mh, colterm, x8, t, R, N, K, as_stream(stream));
+  return gemm_a16_digit_rows(x, wp, mp, mh, colterm, x8, t, R, N, K, as_stream(stream), zeroed);
+}
+
+extern "C" int exact_gemm_g128_a16(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                                   const int64_t* colterm, int8_t* x8, int64_t* t, int32_t R, int32_t N, int32_t K,
+                                   void* stream) {
+  return gemm_a16_entry(x, wp, mp, mh, colterm, x8, t, R, N, K, stream, false);
+}
+
+extern "C" int exact_gemm_g128_a16_zeroed(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                                          const int64_t* colterm, int8_t* x8, int64_t* t, int32_t R, int32_t N, int32_t K,
+                                          void* stream) {
+  return gemm_a16_entry(x, wp, mp, mh, colterm, x8, t, R, N, K, stream, true);
 }

@@ -410,7 +410,7 @@ static int gemv_nsplit(int N, int G, int R = 1, int abits = 15) {
 // accumulate: t += x.W (t holds the caller's running total, e.g. zeros left by a consumer kernel);
 // otherwise t is overwritten (zero-filled first when the row blocks are split).
 int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int M, int N,
-              int K, hipStream_t st);
+              int K, hipStream_t st, bool zeroed);
 
 // colterm (int16 rows only): the colsum term comes from colterm instead of an all-ones row, so R <= 16
 int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int R, int N,
@@ -531,22 +531,32 @@ extern "C" int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const in
   return launch_status("gemv_g128_qrow_acc");
 }
 
-extern "C" int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh,
-                               int64_t* t, int32_t R, int32_t N, int32_t K, void* stream) {
+static int gemm_entry(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,
+                      int32_t R, int32_t N, int32_t K, void* stream, bool zeroed) {
   int e = check_linear(x, abits, wp, mp, t, R, N, K);
   if (e) return e;
   const int rmax = abits == 15 ? 15 : 16;
-  if (R > GEMV_CHUNKS_MAX * rmax) return gemm_mfma(x, abits, wp, mp, mh, t, R, N, K, as_stream(stream));
+  if (R > GEMV_CHUNKS_MAX * rmax) return gemm_mfma(x, abits, wp, mp, mh, t, R, N, K, as_stream(stream), zeroed);
   // Up to GEMV_CHUNKS_MAX row chunks: one GEMV per chunk streams the weights once per chunk, which beats the
   // 128-row GEMM tiles (mostly padding at these R) while the weight passes stay few.
   const size_t xrow = (size_t)K * (abits == 15 ? 2 : 1);
   for (int r0 = 0; r0 < R; r0 += rmax) {
     const int rows = R - r0 < rmax ? R - r0 : rmax;
     e = gemv_launch(static_cast<const int8_t*>(x) + r0 * xrow, abits, wp, mp, mh, t + (size_t)r0 * N, rows, N, K,
-                    as_stream(stream), false);
+                    as_stream(stream), zeroed);
     if (e) return e;
   }
   return EXACT_OK;
+}
+
+extern "C" int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                               int64_t* t, int32_t R, int32_t N, int32_t K, void* stream) {
+  return gemm_entry(x, abits, wp, mp, mh, t, R, N, K, stream, false);
+}
+
+extern "C" int exact_gemm_g128_zeroed(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                                      int64_t* t, int32_t R, int32_t N, int32_t K, void* stream) {
+  return gemm_entry(x, abits, wp, mp, mh, t, R, N, K, stream, true);
 }
 
 extern "C" int exact_gemv_g128_experts(const void* x, int32_t abits, const int32_t* row_map, const int8_t* wp,

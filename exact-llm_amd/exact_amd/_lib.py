@@ -23,7 +23,9 @@ SIGNATURES = {
     "exact_gemv_g128": [P, I32, P, P, P, P, I32, I32, I32, P],
     "exact_gemv_g128_acc": [P, I32, P, P, P, P, I32, I32, I32, P],
     "exact_gemm_g128": [P, I32, P, P, P, P, I32, I32, I32, P],
+    "exact_gemm_g128_zeroed": [P, I32, P, P, P, P, I32, I32, I32, P],
     "exact_gemm_g128_a16": [P, P, P, P, P, P, P, I32, I32, I32, P],
+    "exact_gemm_g128_a16_zeroed": [P, P, P, P, P, P, P, I32, I32, I32, P],
     "exact_gemv_g128_qrow_acc": [P, I64, P, I32, I32, P, P, P, P, P, I32, I32, I32, P, I64, P],
     "exact_requant_group": [P, P, P, P, I32, I32, P],
     "exact_requant_channel": [P, P, P, I32, P, P, I32, I32, P],

@@ -159,10 +159,12 @@ def colterm(lin):
     return ct
 
 
-def gemm_g128(x, abits, lin, out=None):
+def gemm_g128(x, abits, lin, out=None, zeroed=False):
+    """t = x . W for any R; zeroed: out holds zeros, so split paths add into it without a clear launch."""
     R, K = x.shape
+    sfx = "_zeroed" if zeroed and out is not None else ""
     if abits != 15 or R <= GEMV_CHUNK_ROWS[15]:
-        return _linear("exact_gemm_g128", x, abits, lin, out)
+        return _linear("exact_gemm_g128" + sfx, x, abits, lin, out)
     # A16 on the int8 GEMM as interleaved digit rows (exact_gemm_g128_a16)
     if K != lin.K:
         raise ExactError(f"exact_gemm_g128_a16: x has K = {K}, linear has K = {lin.K}")
@@ -175,7 +177,7 @@ def gemm_g128(x, abits, lin, out=None):
     if ws is None or ws.numel() < 2 * R * K:
         ws = torch.empty(2 * R * K, dtype=I8, device=x.device)
         _DIGIT_ROWS[x.device] = ws
-    _lib.call("exact_gemm_g128_a16", _ptr(x), _ptr(lin.wp), _ptr(lin.mp), _ptr(lin.mh), _ptr(ct), _ptr(ws), _ptr(out), R,
+    _lib.call("exact_gemm_g128_a16" + sfx, _ptr(x), _ptr(lin.wp), _ptr(lin.mp), _ptr(lin.mh), _ptr(ct), _ptr(ws), _ptr(out), R,
               lin.N, K, _stream())
     return out
 
@@ -188,7 +190,7 @@ def linear_t(x, abits, lin, out=None, zeroed=False):
         if zeroed and out is not None:
             return gemv_g128_acc(x, abits, lin, out)
         return gemv_g128(x, abits, lin, out)
-    return gemm_g128(x, abits, lin, out)
+    return gemm_g128(x, abits, lin, out, zeroed=zeroed)
 
 
 def _linear(fn, x, abits, lin, out):

@@ -85,6 +85,12 @@ int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const in
 int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,
                     int32_t R, int32_t N, int32_t K, void* stream);
 
+/* exact_gemm_g128 for a t that holds zeros on entry (the model's consumer kernels leave their totals so): the
+ * K-split and row-chunk paths add into t instead of launching a clear first. No counterpart in the reference,
+ * whose torch GEMMs allocate their outputs. */
+int exact_gemm_g128_zeroed(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                           int64_t* t, int32_t R, int32_t N, int32_t K, void* stream);
+
 /* qrow fused into the GEMV that consumes it: t += qrow(xs, abits) . W (t holds zeros or a running total), where
  * row r of xs (int64, ldx apart) is quantised with s = max(max_i part[r * nparts + i] - abits, 0) and
  * part holds the producer's bit lengths of max |xs| over slices of the row (exact_attention's per-head
@@ -119,6 +125,11 @@ int exact_gemm_g128_experts(const void* x, int32_t abits, const int32_t* row_map
  * all-ones row; x8 is not used then). */
 int exact_gemm_g128_a16(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, const int64_t* colterm,
                         int8_t* x8, int64_t* t, int32_t R, int32_t N, int32_t K, void* stream);
+
+/* exact_gemm_g128_a16 for a t that holds zeros on entry (as exact_gemm_g128_zeroed). */
+int exact_gemm_g128_a16_zeroed(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                               const int64_t* colterm, int8_t* x8, int64_t* t, int32_t R, int32_t N, int32_t K,
+                               void* stream);
 
 /* Group epilogue y = round_shift(t, 28 - s[r]) + b[n] (b may be NULL)
  * (speed_fair_kaggle.py:725,743; SPEC.md:18). */

@@ -294,3 +294,21 @@ def test_swiglu_part_then_qrow_gemv_matches_swiglu_qrow(thr):
     assert np.array_equal(host(sh), es[:, 0])
     assert np.array_equal(host(t), oracle_t(eq, w, M))
     assert not host(td).any()
+
+
+@pytest.mark.parametrize("R", [20, 33, 47, 100, 300])
+def test_zeroed_gemm_entries_match(thr, R):
+    """exact_gemm_g128_zeroed / _a16_zeroed on a zeroed t give the oracle's totals on every path: int8 and int16
+    GEMV row chunks (R <= 48), the int16 digit-row GEMM and the int8 GEMM, with K splits (o-shaped N = 2048 leaves
+    few tiles) and without."""
+    for name, N, K in (("zo", 2048, 2048), ("zg", 4096, 512)):
+        lin, kw, km = synth_lin(thr, 72, name, N, K)
+        w = synth.weights_np(kw, N, K)
+        M = synth.scales_np(km, N, K)
+        for abits in (15, 7):
+            lim = (1 << abits) - 1
+            xq = rng.integers(-lim, lim + 1, (R, K))
+            want = oracle_t(xq, w, M)
+            t = torch.zeros((R, N), dtype=I64, device=DEV)
+            ops.linear_t(dev(xq, I16 if abits == 15 else I8), abits, lin, t, zeroed=True)
+            assert np.array_equal(host(t), want), (name, R, abits)
