@@ -89,9 +89,9 @@ __global__ void k_irms(const int64_t* __restrict__ x, const int64_t* __restrict_
 template <int EPT>
 __global__ __launch_bounds__(1024) void k_rmsnorm_qrow(int64_t* __restrict__ x, int64_t* __restrict__ res_t,
                                                        const int32_t* __restrict__ res_s, const int64_t* __restrict__ g,
-                                                       int bits, void* xq, int32_t* s, int D, int clear_t) {
+                                                       int bits, void* xq, int32_t* s, int D, int clear_t, int8_t* x8) {
   __shared__ RowScratch sc;
-  rmsnorm_qrow_row<EPT>(blockIdx.x, x, res_t, res_s, g, bits, xq, s, D, clear_t, sc);
+  rmsnorm_qrow_row<EPT>(blockIdx.x, x, res_t, res_s, g, bits, xq, s, D, clear_t, sc, x8);
 }
 
 // Rows too long for one workgroup are split into slices of QSLICE elements; the producer kernel writes
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(256) void k_swiglu_part(int64_t* __restrict__ t, co
 template <int EPT>
 __global__ __launch_bounds__(1024) void k_swiglu_qrow_row(int64_t* __restrict__ t, const int32_t* __restrict__ s,
                                                           const int32_t* __restrict__ silu, int bits, void* xq,
-                                                          int32_t* __restrict__ sq, int I, int clear_t) {
+                                                          int32_t* __restrict__ sq, int I, int clear_t, int8_t* x8) {
   __shared__ int red[16];
   const int r = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
   int64_t* tr = t + (int64_t)r * 2 * I;
@@ -179,6 +179,7 @@ __global__ __launch_bounds__(1024) void k_swiglu_qrow_row(int64_t* __restrict__ 
       v = v > lim ? lim : (v < -lim ? -lim : v);
       if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * I + i, v);
       else store_q<int16_t>(xq, (int64_t)r * I + i, v);
+      if (x8) store_digits(x8, r, I, i, v);
     }
   }
   if (tid == 0) sq[r] = q;
@@ -187,7 +188,7 @@ __global__ __launch_bounds__(1024) void k_swiglu_qrow_row(int64_t* __restrict__ 
 // grid (slices, R): xq[r][i] = clip(shr(src[r * ld + i], s_r), +-(2^bits - 1)), s_r from the slice maxima
 __global__ __launch_bounds__(256) void k_quant_rows(int64_t* __restrict__ src, int64_t ld, const int32_t* __restrict__ part,
                                                     int nparts, int bits, void* xq, int32_t* __restrict__ s, int K,
-                                                    int clear) {
+                                                    int clear, int8_t* x8) {
   __shared__ int qs;
   const int r = blockIdx.y, b = blockIdx.x;
   if (threadIdx.x < 64) {
@@ -222,6 +223,7 @@ __global__ __launch_bounds__(256) void k_quant_rows(int64_t* __restrict__ src, i
       v = v > lim ? lim : (v < -lim ? -lim : v);
       if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * K + i, v);
       else store_q<int16_t>(xq, (int64_t)r * K + i, v);
+      if (x8) store_digits(x8, r, K, i, v);
     }
   }
 }
@@ -371,13 +373,14 @@ extern "C" int exact_irms(const int64_t* x, const int64_t* g, int64_t* y, int32_
 }
 
 extern "C" int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res_s, const int64_t* g, int32_t bits,
-                                  void* xq, int32_t* s, int32_t R, int32_t D, int32_t clear_t, void* stream) {
+                                  void* xq, int32_t* s, int32_t R, int32_t D, int32_t clear_t, int8_t* x8, void* stream) {
   if (!x || !g || !xq || !s || R <= 0 || D <= 0 || bits < 1 || bits > 15 || (res_t && !res_s)) return EXACT_E_ARG;
+  if (x8 && bits < 8) return EXACT_E_ARG;   // digit rows are of int16 values
   if (D > SMEM_ROW_MAX) return EXACT_E_UNSUPPORTED;
   const int nt = D >= 1024 ? 1024 : ((D + 63) / 64) * 64;
   const int ept = (D + nt - 1) / nt;
   hipStream_t st = as_stream(stream);
-#define RMS_GO(E) hipLaunchKernelGGL(k_rmsnorm_qrow<E>, dim3(R), dim3(nt), 0, st, x, res_t, res_s, g, bits, xq, s, D, clear_t)
+#define RMS_GO(E) hipLaunchKernelGGL(k_rmsnorm_qrow<E>, dim3(R), dim3(nt), 0, st, x, res_t, res_s, g, bits, xq, s, D, clear_t, x8)
   if (ept <= 1) RMS_GO(1);
   else if (ept <= 2) RMS_GO(2);
   else if (ept <= 4) RMS_GO(4);
@@ -387,9 +390,9 @@ extern "C" int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res
 }
 
 extern "C" int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq, int32_t* sq,
-                                 int32_t* part, int32_t R, int32_t I, int32_t clear_t, int64_t* h, void* stream) {
+                                 int32_t* part, int32_t R, int32_t I, int32_t clear_t, int64_t* h, int8_t* x8, void* stream) {
   if (!t || !s || !silu_t || !part || R <= 0 || I <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
-  if (h == t || (!xq && !h) || (xq && !sq)) return EXACT_E_ARG;
+  if (h == t || (!xq && !h) || (xq && !sq) || (x8 && (!xq || bits < 8))) return EXACT_E_ARG;
   hipStream_t st = as_stream(stream);
   if (!xq) {   // h and the slice bit lengths only: the consumer quantises (exact_gemv_g128_qrow_acc)
     const int np = (I + QSLICE - 1) / QSLICE;
@@ -398,7 +401,7 @@ extern "C" int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* si
   }
   const int nt = I >= 1024 ? 1024 : ((I + 63) / 64) * 64;
   const int ept = (I + nt - 1) / nt;
-#define SWG_GO(E) hipLaunchKernelGGL(k_swiglu_qrow_row<E>, dim3(R), dim3(nt), 0, st, t, s, silu_t, bits, xq, sq, I, clear_t)
+#define SWG_GO(E) hipLaunchKernelGGL(k_swiglu_qrow_row<E>, dim3(R), dim3(nt), 0, st, t, s, silu_t, bits, xq, sq, I, clear_t, x8)
   if (ept <= 8) {   // rows up to 8192: one workgroup; longer rows go faster over many workgroups
     if (ept <= 2) SWG_GO(2);
     else if (ept <= 4) SWG_GO(4);
@@ -409,17 +412,18 @@ extern "C" int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* si
   const int np = (I + QSLICE - 1) / QSLICE;
   hipLaunchKernelGGL(k_swiglu_part, dim3(np, R), dim3(256), 0, st, t, s, silu_t, part, I, np, clear_t, h);
   if (h)
-    hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, h, (int64_t)I, part, np, bits, xq, sq, I, 0);
+    hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, h, (int64_t)I, part, np, bits, xq, sq, I, 0, x8);
   else
-    hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, t, (int64_t)2 * I, part, np, bits, xq, sq, I, clear_t);
+    hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, t, (int64_t)2 * I, part, np, bits, xq, sq, I, clear_t, x8);
   return launch_status("swiglu_qrow");
 }
 
 extern "C" int exact_quant_rows(int64_t* src, int64_t ld, const int32_t* part, int32_t nparts, int32_t bits, void* xq,
-                                int32_t* s, int32_t R, int32_t K, int32_t clear, void* stream) {
+                                int32_t* s, int32_t R, int32_t K, int32_t clear, int8_t* x8, void* stream) {
   if (!src || !part || !xq || !s || R <= 0 || K <= 0 || ld < K || nparts <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
+  if (x8 && bits < 8) return EXACT_E_ARG;
   hipLaunchKernelGGL(k_quant_rows, dim3((K + QSLICE - 1) / QSLICE, R), dim3(256), 0, as_stream(stream), src, ld, part, nparts,
-                     bits, xq, s, K, clear);
+                     bits, xq, s, K, clear, x8);
   return launch_status("quant_rows");
 }
 

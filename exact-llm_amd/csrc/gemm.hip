@@ -783,3 +783,13 @@ extern "C" int exact_gemm_g128_a16_zeroed(const int16_t* x, const int8_t* wp, co
                                           void* stream) {
   return gemm_a16_entry(x, wp, mp, mh, colterm, x8, t, R, N, K, stream, true);
 }
+
+extern "C" int exact_gemm_g128_digits(const int8_t* x8, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                                      const int64_t* colterm, int64_t* t, int32_t R, int32_t N, int32_t K, int32_t zeroed,
+                                      void* stream) {
+  if (!x8 || !wp || !mp || !colterm || !t || R <= 0 || N <= 0 || K <= 0) return EXACT_E_ARG;
+  if (K % 128 || (reinterpret_cast<uintptr_t>(x8) & 15) || (reinterpret_cast<uintptr_t>(wp) & 15)) return EXACT_E_UNSUPPORTED;
+  if (2 * (int64_t)R * K >= (1LL << 32)) return EXACT_E_UNSUPPORTED;   // 32-bit buffer offsets of the digit rows
+  return gemm_launch_a8p<GEMM_A8P_CFG, true>(x8, wp, mp, mh, t, 2 * R, N, K, as_stream(stream), GEMM_KSPLIT, colterm,
+                                             zeroed != 0);
+}

@@ -9,6 +9,13 @@ __device__ __forceinline__ void store_q(void* xq, int64_t i, int64_t v) {
   reinterpret_cast<T*>(xq)[i] = (T)v;
 }
 
+// The int16 value v of row r, column i as the interleaved int8 digit rows the int16 GEMM takes:
+// x8[2r][i] = v >> 8, x8[2r + 1][i] = (v & 255) - 128 (the digit split of exact_torch.py:101-102).
+__device__ __forceinline__ void store_digits(int8_t* x8, int64_t r, int64_t K, int64_t i, int64_t v) {
+  x8[2 * r * K + i] = (int8_t)(v >> 8);
+  x8[(2 * r + 1) * K + i] = (int8_t)((v & 255) - 128);
+}
+
 // Scratch of one block-level row pass: one array per reduction (the single-barrier reductions need
 // their own).
 struct RowScratch {
@@ -17,12 +24,13 @@ struct RowScratch {
 };
 
 // Row r of: if res_t, x += round_shift(res_t, 28 - res_s[r]) (written back; res_t zeroed when clear_t);
-// then xq, s = qrow(irms(x, g), bits) (exact_llm.py:41-46, 100-106). The block's threads hold EPT
+// then xq, s = qrow(irms(x, g), bits) (exact_llm.py:41-46, 100-106); x8 (optional): xq's digit rows too. The block's threads hold EPT
 // elements each (blockDim.x * EPT >= D); every load of the row is issued before the first use.
 template <int EPT>
 __device__ __forceinline__ void rmsnorm_qrow_row(int r, int64_t* __restrict__ x, int64_t* __restrict__ res_t,
                                                  const int32_t* __restrict__ res_s, const int64_t* __restrict__ g,
-                                                 int bits, void* xq, int32_t* s, int D, int clear_t, RowScratch& sc) {
+                                                 int bits, void* xq, int32_t* s, int D, int clear_t, RowScratch& sc,
+                                                 int8_t* x8 = nullptr) {
   const int tid = threadIdx.x, nt = blockDim.x;
   int64_t* xr = x + (int64_t)r * D;
   int64_t* tr = res_t ? res_t + (int64_t)r * D : nullptr;
@@ -86,6 +94,7 @@ __device__ __forceinline__ void rmsnorm_qrow_row(int r, int64_t* __restrict__ x,
       w = w > lim ? lim : (w < -lim ? -lim : w);
       if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * D + i, w);
       else store_q<int16_t>(xq, (int64_t)r * D + i, w);
+      if (x8) store_digits(x8, r, D, i, w);
     }
   }
   if (tid == 0) s[r] = q;

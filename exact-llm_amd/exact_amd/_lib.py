@@ -26,14 +26,15 @@ SIGNATURES = {
     "exact_gemm_g128_zeroed": [P, I32, P, P, P, P, I32, I32, I32, P],
     "exact_gemm_g128_a16": [P, P, P, P, P, P, P, I32, I32, I32, P],
     "exact_gemm_g128_a16_zeroed": [P, P, P, P, P, P, P, I32, I32, I32, P],
+    "exact_gemm_g128_digits": [P, P, P, P, P, P, I32, I32, I32, I32, P],
     "exact_gemv_g128_qrow_acc": [P, I64, P, I32, I32, P, P, P, P, P, I32, I32, I32, P, I64, P],
     "exact_requant_group": [P, P, P, P, I32, I32, P],
     "exact_requant_channel": [P, P, P, I32, P, P, I32, I32, P],
     "exact_qrow": [P, I32, P, P, I32, I32, P],
     "exact_irms": [P, P, P, I32, I32, P],
-    "exact_rmsnorm_qrow": [P, P, P, P, I32, P, P, I32, I32, I32, P],
-    "exact_swiglu_qrow": [P, P, P, I32, P, P, P, I32, I32, I32, P, P],
-    "exact_quant_rows": [P, I64, P, I32, I32, P, P, I32, I32, I32, P],
+    "exact_rmsnorm_qrow": [P, P, P, P, I32, P, P, I32, I32, I32, P, P],
+    "exact_swiglu_qrow": [P, P, P, I32, P, P, P, I32, I32, I32, P, P, P],
+    "exact_quant_rows": [P, I64, P, I32, I32, P, P, I32, I32, I32, P, P],
     "exact_isilu": [P, P, P, I64, P],
     "exact_isig": [P, P, P, I64, P],
     "exact_isoftmax": [P, P, P, P, I32, I32, P],

@@ -205,6 +205,12 @@ class Workspace:
         self.seq = None   # (slot, keys) when the rows are one sequence's consecutive positions (prefill)
         self.h = None     # (R, I) SwiGLU values when the gate|up totals must stay intact (trace capture)
         self.I = I
+        # int16 GEMM rows (prefill above 48 rows): the producers also write their rows' int8 digit rows, which the
+        # GEMM reads directly (exact_gemm_g128_digits) instead of splitting them in a launch of its own
+        self.dig = None
+        if abits == 15 and R > ops.GEMV_CHUNK_ROWS[7]:
+            hmax = max(I, cfg.SI if cfg.moe else 0)
+            self.dig = dict(x=z(2 * R, D, dt=I8), a=z(2 * R, H * hd, dt=I8), h=z(2 * R, hmax, dt=I8))
         if cfg.moe:
             k, P = cfg.topk, R * cfg.topk
             nch = ops.max_chunks(P, cfg.NE, abits)
@@ -257,10 +263,11 @@ class TModel:
         return self._ws[R]
 
     # ---------------------------------------------------------------- linears
-    def _lin(self, x, lin, out):
+    def _lin(self, x, lin, out, x8=None):
         """t for a group-mode linear (the consumer kernel applies shr(t, 28 - s) + b and leaves out zeroed,
-        so decode-sized calls accumulate into it without a separate clear)."""
-        return ops.linear_t(x, self.abits, lin, out, zeroed=True)
+        so decode-sized calls accumulate into it without a separate clear). x8: x's digit rows, when its producer
+        wrote them."""
+        return ops.linear_t(x, self.abits, lin, out, zeroed=True, x8=x8)
 
     def _lin_channel(self, x, s, lin, out):
         """channel mode: y = requant_channel(acc) written over out; the consumer then uses s = 28."""
@@ -297,16 +304,20 @@ class TModel:
         if xfuse and ws.h is None and c.I > 8192 and not c.moe:
             ws.h = torch.zeros((R, ws.I), dtype=I64, device=self.dev)
         ops.embed(ws.ids, self.w.emb, ws.x)
+        dx = da = dh = None
+        if group and ws.dig is not None:
+            dx, da = ws.dig["x"], ws.dig["a"]
+            dh = ws.dig["h"]
         res_t, res_s = None, None
         for li, L in enumerate(self.w.layers):
             cache = self._cache.layers[li]
-            ops.rmsnorm_qrow(ws.x, L["g1"], self.abits, res_t, res_s, ws.xq, ws.s, clear=clear)
+            ops.rmsnorm_qrow(ws.x, L["g1"], self.abits, res_t, res_s, ws.xq, ws.s, clear=clear, x8=dx)
             if keep:
                 t_qkv, t_o, t_gu, t_d = (slot(f"L{li}.{k}") for k in ("qkv", "o", "gateup", "down"))
             else:
                 t_qkv, t_o, t_gu, t_d = ws.t_qkv, ws.t_o, ws.t_gu, ws.t_d
             if group:
-                self._lin(ws.xq, L["qkv"], t_qkv)
+                self._lin(ws.xq, L["qkv"], t_qkv, x8=dx)
                 s_qkv, b_qkv = ws.s, L["qkv"].bias
             else:
                 off = 0
@@ -331,29 +342,29 @@ class TModel:
                 ops.gemv_qrow_acc(ws.att, ws.obits, H, self.abits, L["o"], t_o, ws.sa,
                                   zero=t_qkv if afuse and clear else None)   # the q|k|v totals attention left
             else:
-                ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa)
+                ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa, x8=da)
             if group:
                 if not xfuse:
-                    self._lin(ws.aq, L["o"], t_o)
-                ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, t_o, ws.sa, ws.xq, ws.s, clear=clear)
+                    self._lin(ws.aq, L["o"], t_o, x8=da)
+                ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, t_o, ws.sa, ws.xq, ws.s, clear=clear, x8=dx)
             else:
                 self._lin_channel(ws.aq, ws.sa, L["o"], ws.t_o)
                 ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.s28, ws.xq, ws.s)
             if c.moe:
                 if not group:
                     raise ExactError("MoE layers need group-128 linears")
-                self._moe(ws, L)
+                self._moe(ws, L, dx, dh)
                 res_t, res_s = None, None
                 continue
             if group:
-                self._lin(ws.xq, L["gateup"], t_gu)
+                self._lin(ws.xq, L["gateup"], t_gu, x8=dx)
                 if xfuse and c.I > 8192:   # rows beyond one workgroup: SwiGLU slices, then the down GEMV quantises
                     ops.swiglu_part(t_gu, ws.s, tab.silu, ws.h, ws.part_sw, clear=clear)
                     ops.gemv_qrow_acc(ws.h, ws.part_sw, -(-c.I // ops.QSLICE), self.abits, L["down"], t_d, ws.sh)
                 else:
                     ops.swiglu_qrow(t_gu, ws.s, tab.silu, self.abits, ws.hq, ws.sh, clear=clear, part=ws.part_sw,
-                                    h=ws.h if keep else None)
-                    self._lin(ws.hq, L["down"], t_d)
+                                    h=ws.h if keep else None, x8=dh)
+                    self._lin(ws.hq, L["down"], t_d, x8=dh)
                 res_t, res_s = t_d, ws.sh
             else:
                 I = L["gate"].N
@@ -364,11 +375,11 @@ class TModel:
                 ops.swiglu_qrow(ws.t_gu, ws.s28, tab.silu, self.abits, ws.hq, ws.sh, part=ws.part_sw)
                 self._lin_channel(ws.hq, ws.sh, L["down"], ws.t_d)
                 res_t, res_s = ws.t_d, ws.s28
-        ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=clear)
+        ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=clear, x8=dx)
         head = self.w.head
         if head.mode == "group":
             t_head = slot("head") if keep else ws.t_head
-            self._lin(ws.xq, head, t_head)
+            self._lin(ws.xq, head, t_head, x8=dx)
             ops.logits_argmax(t_head, ws.s, ws.logits if want_logits else None, ws.next_ids, clear=clear,
                               part=ws.part_lg)
         else:
@@ -378,14 +389,14 @@ class TModel:
             ops.logits_argmax(ws.t_head, ws.s28, ws.logits if want_logits else None, ws.next_ids, part=ws.part_lg)
         return ws
 
-    def _moe(self, ws, L):
+    def _moe(self, ws, L, dx=None, dh=None):
         """MoE block on m = ws.xq (scale ws.s), added into ws.x (MoEInt.moe, moe_exact_kaggle.py:454-467):
         router (with the shared-expert gate logit in the same GEMV) -> isoftmax -> stable top-k -> experts grouped
         into chunks -> SwiGLU per (row, expert) pair -> combination weighted by the Q20 probabilities, plus the
         isig-gated shared expert."""
         c, tab, k = self.cfg, self.tab, self.cfg.topk
         P = ws.R * k
-        self._lin(ws.xq, L["router"], ws.t_rt)
+        self._lin(ws.xq, L["router"], ws.t_rt, x8=dx)
         ops.router_topk(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, clear=True, NE=c.NE, gate_col=ws.gate_col,
                         sig=tab.sig, gate=ws.gate)
         grouped = P >= self.EXPERT_GEMM_MIN_PAIRS   # prefill: experts on the matrix cores, one tile per 128 pairs
@@ -401,9 +412,9 @@ class TModel:
             ops.gemm_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed, P)
         else:
             ops.gemv_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed)
-        self._lin(ws.xq, L["sgu"], ws.t_sgu)
-        ops.swiglu_qrow(ws.t_sgu, ws.s, tab.silu, self.abits, ws.shq, ws.ssh, clear=True, part=ws.part_sw)
-        self._lin(ws.shq, L["sd"], ws.t_sd)
+        self._lin(ws.xq, L["sgu"], ws.t_sgu, x8=dx)
+        ops.swiglu_qrow(ws.t_sgu, ws.s, tab.silu, self.abits, ws.shq, ws.ssh, clear=True, part=ws.part_sw, x8=dh)
+        self._lin(ws.shq, L["sd"], ws.t_sd, x8=dh)
         ops.moe_combine(ws.x, ws.t_ed, ws.esh, ws.p_sel, ws.disp["pidx"], k, ws.t_sd, ws.ssh, ws.gate, clear=True)
 
     # ---------------------------------------------------------------- reference-shaped API

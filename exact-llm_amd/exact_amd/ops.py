@@ -159,10 +159,20 @@ def colterm(lin):
     return ct
 
 
-def gemm_g128(x, abits, lin, out=None, zeroed=False):
-    """t = x . W for any R; zeroed: out holds zeros, so split paths add into it without a clear launch."""
+def gemm_g128(x, abits, lin, out=None, zeroed=False, x8=None):
+    """t = x . W for any R; zeroed: out holds zeros, so split paths add into it without a clear launch.
+    x8: the digit rows of the int16 x that its producer wrote (used above GEMV_CHUNK_ROWS[7] rows)."""
     R, K = x.shape
     sfx = "_zeroed" if zeroed and out is not None else ""
+    if x8 is not None and abits == 15 and R > GEMV_CHUNK_ROWS[7]:
+        if K != lin.K:
+            raise ExactError(f"exact_gemm_g128_digits: x has K = {K}, linear has K = {lin.K}")
+        if out is None:
+            out = torch.empty((R, lin.N), dtype=I64, device=x.device)
+        _need(out, I64, "out", R * lin.N)
+        _lib.call("exact_gemm_g128_digits", _digits(x8, R, K), _ptr(lin.wp), _ptr(lin.mp), _ptr(lin.mh), _ptr(colterm(lin)),
+                  _ptr(out), R, lin.N, K, int(bool(sfx)), _stream())
+        return out
     if abits != 15 or R <= GEMV_CHUNK_ROWS[15]:
         return _linear("exact_gemm_g128" + sfx, x, abits, lin, out)
     # A16 on the int8 GEMM as interleaved digit rows (exact_gemm_g128_a16)
@@ -182,15 +192,16 @@ def gemm_g128(x, abits, lin, out=None, zeroed=False):
     return out
 
 
-def linear_t(x, abits, lin, out=None, zeroed=False):
+def linear_t(x, abits, lin, out=None, zeroed=False, x8=None):
     """Dispatch: GEMV for decode-sized R, GEMM otherwise (TLinG, speed_fair_kaggle.py:735-742).
-    zeroed: out already holds zeros (left by a clearing consumer), so the GEMV accumulates into it."""
+    zeroed: out already holds zeros (left by a clearing consumer), so the GEMV accumulates into it.
+    x8: digit rows of x its producer wrote (int16 GEMM rows only)."""
     R = x.shape[0]
     if R <= (15 if abits == 15 else 16):
         if zeroed and out is not None:
             return gemv_g128_acc(x, abits, lin, out)
         return gemv_g128(x, abits, lin, out)
-    return gemm_g128(x, abits, lin, out, zeroed=zeroed)
+    return gemm_g128(x, abits, lin, out, zeroed=zeroed, x8=x8)
 
 
 def _linear(fn, x, abits, lin, out):
@@ -237,15 +248,19 @@ def irms(x, g):
     return y
 
 
-def rmsnorm_qrow(x, g, bits=15, res_t=None, res_s=None, xq=None, s=None, clear=False):
+def _digits(x8, R, K):
+    return None if x8 is None else _ptr(_need(x8, I8, "x8", 2 * R * K))
+
+
+def rmsnorm_qrow(x, g, bits=15, res_t=None, res_s=None, xq=None, s=None, clear=False, x8=None):
     """x += rs(res_t, 28 - res_s) (in place) when res_t is given; then qrow(irms(x, g), bits).
-    clear: leave res_t zeroed for the next accumulating GEMV."""
+    clear: leave res_t zeroed for the next accumulating GEMV. x8: (2R, D) int8, also receives xq's digit rows."""
     R, D = x.shape
     _need(x, I64, "x")
     xq = torch.empty((R, D), dtype=I16 if bits > 7 else I8, device=x.device) if xq is None else xq
     s = torch.empty(R, dtype=I32, device=x.device) if s is None else s
     _lib.call("exact_rmsnorm_qrow", _ptr(x), _ptr(res_t), _ptr(res_s), _ptr(_need(g, I64, "g", D)), bits, _ptr(xq), _ptr(s),
-              R, D, int(clear), _stream())
+              R, D, int(clear), _digits(x8, R, D), _stream())
     return xq, s
 
 
@@ -262,12 +277,14 @@ def swiglu_part(t, s, silu, h, part, clear=False):
     R, N2 = t.shape
     I = N2 // 2
     _lib.call("exact_swiglu_qrow", _ptr(_need(t, I64, "t")), _ptr(s), _ptr(silu), 15, None, None,
-              _ptr(_need(part, I32, "part", R * -(-I // QSLICE))), R, I, int(clear), _ptr(_need(h, I64, "h", R * I)), _stream())
+              _ptr(_need(part, I32, "part", R * -(-I // QSLICE))), R, I, int(clear), _ptr(_need(h, I64, "h", R * I)), None,
+              _stream())
     return h, part
 
 
-def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None, clear=False, part=None, h=None):
-    """h: optional (R, I) int64 scratch; with it and clear=False, t is left intact (trace capture)."""
+def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None, clear=False, part=None, h=None, x8=None):
+    """h: optional (R, I) int64 scratch; with it and clear=False, t is left intact (trace capture).
+    x8: (2R, I) int8, also receives xq's digit rows."""
     R, N2 = t.shape
     I = N2 // 2
     xq = torch.empty((R, I), dtype=I16 if bits > 7 else I8, device=t.device) if xq is None else xq
@@ -275,16 +292,17 @@ def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None, clear=False, part=None, h
     part = swiglu_parts(R, I, t.device) if part is None else _need(part, I32, "part", R * -(-I // QSLICE))
     hp = None if h is None else _ptr(_need(h, I64, "h", R * I))
     _lib.call("exact_swiglu_qrow", _ptr(_need(t, I64, "t")), _ptr(s), _ptr(silu), bits, _ptr(xq), _ptr(sq), _ptr(part), R, I,
-              int(clear), hp, _stream())
+              int(clear), hp, _digits(x8, R, I), _stream())
     return xq, sq
 
 
-def quant_rows(src, part, nparts, bits, xq, s, K=None, clear=False):
-    """qrow of src rows (first K columns) given per-slice bit lengths of max |src| part (R, nparts) int32."""
+def quant_rows(src, part, nparts, bits, xq, s, K=None, clear=False, x8=None):
+    """qrow of src rows (first K columns) given per-slice bit lengths of max |src| part (R, nparts) int32.
+    x8: (2R, K) int8, also receives xq's digit rows."""
     R, ld = src.shape
     K = ld if K is None else K
     _lib.call("exact_quant_rows", _ptr(_need(src, I64, "src")), ld, _ptr(_need(part, I32, "part", R * nparts)), nparts, bits,
-              _ptr(xq), _ptr(_need(s, I32, "s", R)), R, K, int(clear), _stream())
+              _ptr(xq), _ptr(_need(s, I32, "s", R)), R, K, int(clear), _digits(x8, R, K), _stream())
     return xq, s
 
 

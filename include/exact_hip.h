@@ -131,6 +131,14 @@ int exact_gemm_g128_a16_zeroed(const int16_t* x, const int8_t* wp, const int16_t
                                const int64_t* colterm, int8_t* x8, int64_t* t, int32_t R, int32_t N, int32_t K,
                                void* stream);
 
+/* The int16-row GEMM from digit rows a producer already wrote (exact_rmsnorm_qrow, exact_swiglu_qrow or
+ * exact_quant_rows with x8): x8 holds 2R int8 rows (x8[2r] = x[r] >> 8, x8[2r + 1] = (x[r] & 255) - 128), so
+ * no split launch runs. zeroed != 0: t holds zeros on entry (as exact_gemm_g128_zeroed). Results equal
+ * exact_gemm_g128_a16's on the int16 rows (exact_torch.py:101-102). */
+int exact_gemm_g128_digits(const int8_t* x8, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                           const int64_t* colterm, int64_t* t, int32_t R, int32_t N, int32_t K, int32_t zeroed,
+                           void* stream);
+
 /* Group epilogue y = round_shift(t, 28 - s[r]) + b[n] (b may be NULL)
  * (speed_fair_kaggle.py:725,743; SPEC.md:18). */
 int exact_requant_group(const int64_t* t, const int32_t* s, const int64_t* b, int64_t* y,
@@ -151,9 +159,12 @@ int exact_irms(const int64_t* x, const int64_t* g, int64_t* y, int32_t R, int32_
 /* Fused residual + irms + qrow: if res_t != NULL, x += round_shift(res_t, 28 - res_s[r]) (written back
  * to x); then xq, s = qrow(irms(x, g), bits). Covers exact_llm.py:177-178 (o-proj residual, post-norm),
  * :179-180/166 (down-proj residual, next input norm) and the final norm before the head.
- * clear_t != 0 leaves res_t zeroed after reading it (ready for the next accumulating GEMV). */
+ * clear_t != 0 leaves res_t zeroed after reading it (ready for the next accumulating GEMV).
+ * x8 (optional, bits >= 8): also the interleaved int8 digit rows of xq (2R rows: x8[2r] = xq[r] >> 8,
+ * x8[2r + 1] = (xq[r] & 255) - 128), which exact_gemm_g128_digits takes. */
 int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res_s, const int64_t* g,
-                       int32_t bits, void* xq, int32_t* s, int32_t R, int32_t D, int32_t clear_t, void* stream);
+                       int32_t bits, void* xq, int32_t* s, int32_t R, int32_t D, int32_t clear_t, int8_t* x8,
+                       void* stream);
 
 /* SwiGLU on a fused gate|up total: g = rs(t[r][n], 28 - s[r]), u = rs(t[r][I + n], 28 - s[r]),
  * h = round_shift(isilu(g) * u, 16); xq, sq = qrow(h, bits). h: optional int64 (R, I) scratch for the
@@ -161,16 +172,18 @@ int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res_s, const i
  * and is left as it was when clear_t == 0 and h is given (the totals stay readable, e.g. for a trace).
  * part: int32 workspace of R * ceil(I / 1024) slice bit lengths. xq may be NULL when h is given: then only h and
  * part are produced (bit length of max |h| per 1024-column slice), for exact_gemv_g128_qrow_acc to quantise.
+ * x8 (optional, with xq, bits >= 8): xq's digit rows too, as exact_rmsnorm_qrow.
  * (exact_llm.py:179; isilu exact_llm.py:118-122). */
 int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32_t bits, void* xq,
-                      int32_t* sq, int32_t* part, int32_t R, int32_t I, int32_t clear_t, int64_t* h, void* stream);
+                      int32_t* sq, int32_t* part, int32_t R, int32_t I, int32_t clear_t, int64_t* h, int8_t* x8,
+                      void* stream);
 
 /* qrow with the row maximum supplied in parts (a producer kernel wrote part[r * nparts + i] =
  * bitlen(max |src| over its slice i of row r)): s = max(max_i part - bits, 0), xq = clip(rs(src, s))
  * (exact_llm.py:41-46; bitlen of the row max = max of the slice bit lengths). src rows are ld apart;
- * clear != 0 leaves src zeroed. */
+ * clear != 0 leaves src zeroed. x8 (optional, bits >= 8): xq's digit rows too, as exact_rmsnorm_qrow. */
 int exact_quant_rows(int64_t* src, int64_t ld, const int32_t* part, int32_t nparts, int32_t bits, void* xq,
-                     int32_t* s, int32_t R, int32_t K, int32_t clear, void* stream);
+                     int32_t* s, int32_t R, int32_t K, int32_t clear, int8_t* x8, void* stream);
 
 /* Elementwise LUT nonlinearities on int64 arrays (isilu exact_llm.py:118-122; isig moe_exact_kaggle.py:420-424). */
 int exact_isilu(const int64_t* x, const int32_t* silu_t, int64_t* y, int64_t n, void* stream);

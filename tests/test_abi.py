@@ -40,6 +40,8 @@ def test_host_side_validation_rejects_bad_shapes_without_launching():
     assert lib.exact_synth_linear(1, 2, 0, 40000, fake, fake, fake, 64, 128, 0, 64, None) == 1  # scale range
     assert lib.exact_synth_linear(1, 2, 1, 400, fake, fake, fake, 64, 128, 32, 128, None) == 2  # part offset % 64
     assert lib.exact_attention(fake, fake, fake, fake, fake, fake, fake, fake, fake, None, 1, 4, 2, 96, 64, 8192, None) == 2
-    assert lib.exact_swiglu_qrow(fake, fake, fake, 15, fake, fake, None, 1, 64, 0, None, None) == 1   # no workspace
-    assert lib.exact_swiglu_qrow(fake, fake, fake, 15, fake, fake, fake, 1, 64, 0, fake, None) == 1   # h aliases t
+    assert lib.exact_swiglu_qrow(fake, fake, fake, 15, fake, fake, None, 1, 64, 0, None, None, None) == 1   # no workspace
+    assert lib.exact_swiglu_qrow(fake, fake, fake, 15, fake, fake, fake, 1, 64, 0, fake, None, None) == 1   # h aliases t
+    assert lib.exact_swiglu_qrow(fake, fake, fake, 7, fake, fake, fake, 1, 64, 0, None, fake, None) == 1   # digits of int8
+    assert lib.exact_gemm_g128_digits(fake, fake, fake, None, None, fake, 4, 64, 128, 0, None) == 1    # no colterm
     assert lib.exact_logits_argmax(fake, fake, None, fake, None, 1, 64, 0, None) == 1            # no workspace

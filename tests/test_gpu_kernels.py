@@ -312,3 +312,35 @@ def test_zeroed_gemm_entries_match(thr, R):
             t = torch.zeros((R, N), dtype=I64, device=DEV)
             ops.linear_t(dev(xq, I16 if abits == 15 else I8), abits, lin, t, zeroed=True)
             assert np.array_equal(host(t), want), (name, R, abits)
+
+
+def test_producer_digit_rows_feed_the_digit_gemm(thr):
+    """rmsnorm_qrow, quant_rows and swiglu_qrow with x8 write the int16 rows' digit rows exactly as the GEMM's own
+    split does, and exact_gemm_g128_digits on them equals exact_gemm_g128_a16 on the int16 rows."""
+    R, D, N = 64, 1024, 768
+    lin, kw, km = synth_lin(thr, 73, "dg", N, D)
+    want_split = lambda q: np.stack([q >> 8, (q & 255) - 128], 1).reshape(2 * R, -1)
+    x = dev(rng.integers(-(1 << 40), 1 << 40, (R, D)), I64)
+    g = dev(rng.integers(1 << 15, 1 << 17, D), I64)
+    x8 = torch.zeros((2 * R, D), dtype=I8, device=DEV)
+    xq, s = ops.rmsnorm_qrow(x.clone(), g, 15, x8=x8)
+    q = host(xq).astype(np.int64)
+    assert np.array_equal(host(x8), want_split(q))
+    for zeroed in (False, True):
+        t_d = torch.zeros((R, N), dtype=I64, device=DEV)
+        ops.gemm_g128(xq, 15, lin, t_d, zeroed=zeroed, x8=x8)
+        t_a = ops.gemm_g128(xq, 15, lin)
+        assert np.array_equal(host(t_d), host(t_a))
+    src = dev(rng.integers(-(1 << 40), 1 << 40, (R, 2048)), I64)
+    part = dev(np.full((R, 2), 41), I32)
+    aq = torch.zeros((R, 2048), dtype=I16, device=DEV)
+    a8 = torch.zeros((2 * R, 2048), dtype=I8, device=DEV)
+    ops.quant_rows(src, part, 2, 15, aq, torch.zeros(R, dtype=I32, device=DEV), x8=a8)
+    assert np.array_equal(host(a8), want_split(host(aq).astype(np.int64)))
+    from exact_amd.tables import silu_t
+    silu = dev(silu_t(), I32)
+    for I in (1408, 9000):   # one workgroup per row; slices over many workgroups
+        t = dev(rng.integers(-(1 << 44), 1 << 44, (R, 2 * I)), I64)
+        h8 = torch.zeros((2 * R, I), dtype=I8, device=DEV)
+        hq, _ = ops.swiglu_qrow(t, dev(rng.integers(0, 8, R), I32), silu, 15, x8=h8)
+        assert np.array_equal(host(h8), want_split(host(hq).astype(np.int64)))
