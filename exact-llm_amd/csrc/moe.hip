@@ -85,10 +85,12 @@ __global__ __launch_bounds__(1024) void k_moe_dispatch(const int32_t* __restrict
       const int q = b0 + 64 * i + lane;
       ev[i] = q < P ? es[q] : -1;
     }
+    const int nb = (P - b0 + 63) / 64 < DISPATCH_RB ? (P - b0 + 63) / 64 : DISPATCH_RB;   // blocks of 64 holding pairs
     for (int e = wave; e < NE; e += nw) {   // cnt[e] belongs to this wave
       int c = 0;
 #pragma unroll
-      for (int i = 0; i < DISPATCH_RB; ++i) c += __popcll(__ballot(ev[i] == e));
+      for (int i = 0; i < DISPATCH_RB; ++i)
+        if (i < nb) c += __popcll(__ballot(ev[i] == e));
       if (lane == 0) cnt[e] += c;
     }
   }
@@ -134,10 +136,12 @@ __global__ __launch_bounds__(1024) void k_moe_dispatch(const int32_t* __restrict
       const int q = b0 + 64 * i + lane;
       ev[i] = q < P ? es[q] : -1;
     }
+    const int nb = (P - b0 + 63) / 64 < DISPATCH_RB ? (P - b0 + 63) / 64 : DISPATCH_RB;
     for (int e = wave; e < NE; e += nw) {
       int run = off[e];
 #pragma unroll
       for (int i = 0; i < DISPATCH_RB; ++i) {
+        if (i >= nb) break;
         const bool mine = ev[i] == e;
         const uint64_t m = __ballot(mine);
         if (mine) {
