@@ -370,6 +370,12 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
   if (!t || !s || !cos_t || !sin_t || !slot || !pos || !kq || !sk || !v || !exp_t || !out) return EXACT_E_ARG;
   if (R <= 0 || H <= 0 || KV <= 0 || H % KV || hd <= 0 || Smax <= 0) return EXACT_E_ARG;
   if (hd > 256 || hd % 8 || (2 * ATT_THREADS) % hd || Smax > 8192) return EXACT_E_UNSUPPORTED;
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              8192 * 8);
+    attr_set = true;
+  }
   hipLaunchKernelGGL(k_attention_qkv, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), t, s, b, cos_t,
                      sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
   return launch_status("attention_qkv");
@@ -394,6 +400,11 @@ extern "C" int exact_attention(const int16_t* qq, const int32_t* sq, const int16
   if (!qq || !sq || !kq || !sk || !v || !slot || !pos || !exp_t || !out) return EXACT_E_ARG;
   if (R <= 0 || H <= 0 || KV <= 0 || H % KV || hd <= 0 || Smax <= 0) return EXACT_E_ARG;
   if (hd > 256 || (2 * ATT_THREADS) % hd || hd % 8 || Smax > 8192) return EXACT_E_UNSUPPORTED;
+  static bool attr_set = false;   // the scores take Smax * 8 bytes of LDS, up to 64 KiB beside the static arrays
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention), hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
+    attr_set = true;
+  }
   hipLaunchKernelGGL(k_attention, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot,
                      pos,
                      exp_t, out, obits, H, KV, hd, Smax, INV);

@@ -120,15 +120,16 @@ def test_prefill_full_size_2048():
     assert np.array_equal(out[rows], oracle_rows(*case, slot, H, KV, rows))
 
 
-@pytest.mark.parametrize("H,KV,hd,R,bias", [(28, 4, 128, 1, True), (28, 4, 128, 4, False), (14, 2, 64, 3, True),
-                                            (4, 4, 256, 2, True)])
-def test_fused_qkv_attention_matches_two_launches(H, KV, hd, R, bias):
+@pytest.mark.parametrize("H,KV,hd,R,bias,Smax", [(28, 4, 128, 1, True, 96), (28, 4, 128, 4, False, 96),
+                                                 (14, 2, 64, 3, True, 96), (4, 4, 256, 2, True, 96),
+                                                 (8, 2, 128, 2, True, 8192)])
+def test_fused_qkv_attention_matches_two_launches(H, KV, hd, R, bias, Smax):
     """exact_attention_qkv against exact_qkv_rope_cache + exact_attention (both oracle-pinned above and in the
     model tests): outputs, obits and every cache entry equal; rows in different slots at positions 0, Smax - 1 and
     in between; the totals t are left unchanged."""
     from exact_amd.tables import host_tables
     rng = np.random.default_rng(H + R + hd)
-    B, Smax = R + 2, 96
+    B = R + 2
     N = (H + 2 * KV) * hd
     kq = rng.integers(-32767, 32768, (B, KV, Smax, hd))
     sk = rng.integers(0, 4, (B, KV, Smax))
@@ -163,3 +164,14 @@ def test_fused_qkv_attention_matches_two_launches(H, KV, hd, R, bias):
     for x, y in zip(c_b, c_a):
         assert np.array_equal(host(x), host(y))
     assert np.array_equal(host(t_b), t)
+
+
+def test_row_attention_long_context_matches_oracle():
+    """Decode attention over 8000 cached keys of an 8192-position cache (64 KiB of scores in LDS) against the oracle."""
+    H, KV, hd, Smax, slot, nkeys = 4, 2, 128, 8192, 1, 8000
+    kq, sk, v, qq, sq, pos = make_case(91, 2, slot, H, KV, hd, Smax, nkeys, 1, "small")
+    cache, qd, sqd, posd = to_dev(kq, sk, v, qq, sq, pos)
+    out = torch.full((1, H * hd), -7, dtype=I64, device=DEV)
+    ops.attention(qd, sqd, cache, torch.tensor([slot], dtype=I32, device=DEV), posd,
+                  torch.tensor(exp_t(), dtype=I32, device=DEV), out, H, KV, hd, O.inv_sqrt_hd(hd))
+    assert np.array_equal(host(out), oracle_rows(kq, sk, v, qq, sq, pos, slot, H, KV, [0]))
