@@ -548,3 +548,93 @@ def np_to_dev(a, dtype, device):
     if not a.flags.writeable:     # a read-only memory map (an artifact file): one transient host copy
         a = a.copy()
     return torch.from_numpy(a).to(device=device, dtype=dtype)
+
+
+# ----------------------------------------------------------------------------- functional ops for torch callers
+# The other entry points of the boundary as torch custom ops (the pattern of exact::gemv above): functional forms
+# that allocate their outputs, leave their inputs unchanged and carry fake implementations, so torch.compile and
+# graph capture see their shapes. Packed linears travel as (wp, mp, N); the wide-scale plane is not taken here.
+@torch.library.custom_op("exact::gemm_g128", mutates_args=())
+def gemm_op(x: torch.Tensor, abits: int, wp: torch.Tensor, mp: torch.Tensor, N: int) -> torch.Tensor:
+    """t (R, N) int64 = sum_g (x_g . W_g) M_g for any R (GQLin / TLinG, speed_fair_kaggle.py:714-742)."""
+    return linear_t(x, abits, PackedLinear(wp, mp, N, x.shape[1]))
+
+
+@gemm_op.register_fake
+def _gemm_op_fake(x, abits, wp, mp, N):
+    return torch.empty((x.shape[0], N), dtype=I64, device=x.device)
+
+
+@torch.library.custom_op("exact::rmsnorm_qrow", mutates_args=())
+def rmsnorm_qrow_op(x: torch.Tensor, g: torch.Tensor, bits: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(xq, s) = qrow(irms(x, g), bits) (exact_llm.py:41-46, 100-106)."""
+    return rmsnorm_qrow(x, g, bits)
+
+
+@rmsnorm_qrow_op.register_fake
+def _rmsnorm_qrow_op_fake(x, g, bits):
+    R, D = x.shape
+    return (torch.empty((R, D), dtype=I16 if bits > 7 else I8, device=x.device),
+            torch.empty((R,), dtype=I32, device=x.device))
+
+
+@torch.library.custom_op("exact::swiglu_qrow", mutates_args=())
+def swiglu_qrow_op(t: torch.Tensor, s: torch.Tensor, silu: torch.Tensor, bits: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(hq, sh) = qrow(shr(isilu(g) u, 16), bits) of a fused gate|up total t (R, 2I) (exact_llm.py:179); t unchanged."""
+    R, N2 = t.shape
+    h = torch.empty((R, N2 // 2), dtype=I64, device=t.device)
+    return swiglu_qrow(t, s, silu, bits, h=h)
+
+
+@swiglu_qrow_op.register_fake
+def _swiglu_qrow_op_fake(t, s, silu, bits):
+    R, N2 = t.shape
+    return (torch.empty((R, N2 // 2), dtype=I16 if bits > 7 else I8, device=t.device),
+            torch.empty((R,), dtype=I32, device=t.device))
+
+
+@torch.library.custom_op("exact::attention", mutates_args=())
+def attention_op(qq: torch.Tensor, sq: torch.Tensor, kq: torch.Tensor, sk: torch.Tensor, v: torch.Tensor, slot: torch.Tensor,
+                 pos: torch.Tensor, expt: torch.Tensor, inv: int) -> torch.Tensor:
+    """out (R, H hd) = shr(isoftmax(shr((qq . kq) INV, 32 - sq - sk)) . v, 20) over keys 0..pos[r] of slot[r]
+    (exact_llm.py:170-176); qq (R, H, hd), cache kq (B, KV, Smax, hd), sk (B, KV, Smax), v (B, KV, Smax, hd)."""
+    R, H, hd = qq.shape
+    out = torch.empty((R, H * hd), dtype=I64, device=qq.device)
+    return attention(qq, sq, (kq, sk, v), slot, pos, expt, out, H, kq.shape[1], hd, inv)
+
+
+@attention_op.register_fake
+def _attention_op_fake(qq, sq, kq, sk, v, slot, pos, expt, inv):
+    R, H, hd = qq.shape
+    return torch.empty((R, H * hd), dtype=I64, device=qq.device)
+
+
+@torch.library.custom_op("exact::router_topk", mutates_args=())
+def router_topk_op(t: torch.Tensor, s: torch.Tensor, expt: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(p_sel Q20 int64, e_sel int32) = top-k of isoftmax(shr(t, 28 - s)), ties to the lower expert
+    (moe_exact_kaggle.py:454-460); t unchanged."""
+    R = t.shape[0]
+    p_sel = torch.empty((R, k), dtype=I64, device=t.device)
+    e_sel = torch.empty((R, k), dtype=I32, device=t.device)
+    return router_topk(t, s, expt, k, p_sel, e_sel)
+
+
+@router_topk_op.register_fake
+def _router_topk_op_fake(t, s, expt, k):
+    R = t.shape[0]
+    return torch.empty((R, k), dtype=I64, device=t.device), torch.empty((R, k), dtype=I32, device=t.device)
+
+
+@torch.library.custom_op("exact::logits_argmax", mutates_args=())
+def logits_argmax_op(t: torch.Tensor, s: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(logits = shr(t, 28 - s) int64, ids = first argmax int32) of the head totals (exact_llm.py:180, 267)."""
+    R, N = t.shape
+    lg = torch.empty((R, N), dtype=I64, device=t.device)
+    ids = torch.empty((R,), dtype=I32, device=t.device)
+    return logits_argmax(t, s, lg, ids)
+
+
+@logits_argmax_op.register_fake
+def _logits_argmax_op_fake(t, s):
+    R, N = t.shape
+    return torch.empty((R, N), dtype=I64, device=t.device), torch.empty((R,), dtype=I32, device=t.device)
