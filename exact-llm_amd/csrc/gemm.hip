@@ -678,6 +678,12 @@ static int gemm_launch_experts(const int8_t* x8, const int8_t* wp, const int16_t
 template <int WM, int WN, int S, bool PAIRS = false>
 static int gemm_launch_a8p(const void* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int M, int N,
                            int K, hipStream_t st, int ksplit_req, const int64_t* colterm = nullptr, bool zeroed = false) {
+  // up to 128 rows (prompts of 49-64 tokens as int16 digit rows): 128-row tiles, two 4-wave blocks per CU, instead
+  // of 256-row tiles half of padding
+  if (M <= 128 && WM != 2) {
+    if (mh) return gemm_launch_a8p_t<2, WN, 2, PAIRS, true>(x, wp, mp, mh, t, M, N, K, st, ksplit_req, colterm, zeroed);
+    return gemm_launch_a8p_t<2, WN, 2, PAIRS, false>(x, wp, mp, nullptr, t, M, N, K, st, ksplit_req, colterm, zeroed);
+  }
   if (mh) return gemm_launch_a8p_t<WM, WN, S, PAIRS, true>(x, wp, mp, mh, t, M, N, K, st, ksplit_req, colterm, zeroed);
   return gemm_launch_a8p_t<WM, WN, S, PAIRS, false>(x, wp, mp, nullptr, t, M, N, K, st, ksplit_req, colterm, zeroed);
 }

@@ -296,7 +296,7 @@ def test_swiglu_part_then_qrow_gemv_matches_swiglu_qrow(thr):
     assert not host(td).any()
 
 
-@pytest.mark.parametrize("R", [20, 33, 47, 100, 300])
+@pytest.mark.parametrize("R", [20, 33, 47, 60, 100, 300])
 def test_zeroed_gemm_entries_match(thr, R):
     """exact_gemm_g128_zeroed / _a16_zeroed on a zeroed t give the oracle's totals on every path: int8 and int16
     GEMV row chunks (R <= 48), the int16 digit-row GEMM and the int8 GEMM, with K splits (o-shaped N = 2048 leaves
