@@ -196,9 +196,7 @@ __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t*
 // out_mode 0: plain store (the wave owns all groups of its rows), 1: 64-bit atomic add.
 // CT (int16 rows): colterm[n] = sum_g colsum_g M_g given, 128 colterm added by the first split of each row block,
 // so R may be 16.
-// BRED (nsplit == BW): the block's waves are the group splits of one 64-row block; their totals are summed in LDS
-// and wave 0 stores them, so no atomics and no zero fill.
-template <int ABITS, bool NT, int VR, int BW, bool CT = false, bool WIDE = false, bool BRED = false>
+template <int ABITS, bool NT, int VR, int BW, bool CT = false, bool WIDE = false>
 __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ xv, const int8_t* __restrict__ wp,
                                                        const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
                                                        int64_t* __restrict__ t, int R, int N, int K, int G, int nsplit,
@@ -216,23 +214,6 @@ __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ 
 
   int64_t acc[4][VR];
   gemv_groups<ABITS, NT, VR, NoPrologue, CT, WIDE>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane);
-  if constexpr (BRED) {   // every wave of the block is active (grid = row blocks, nsplit = BW)
-    __shared__ int64_t red[BW - 1][4][VR][64];
-    const int w = threadIdx.x >> 6;
-    if (w > 0)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int v = 0; v < VR; ++v) red[w - 1][q][v][lane] = acc[q][v];
-    __syncthreads();
-    if (w > 0) return;
-#pragma unroll
-    for (int j = 0; j < BW - 1; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int v = 0; v < VR; ++v) acc[q][v] += red[j][q][v][lane];
-  }
 
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -405,9 +386,6 @@ int zero_bytes(void* dst, int64_t nbytes, hipStream_t st) {
 #ifndef GEMV_CUS
 #define GEMV_CUS 256
 #endif
-#ifndef GEMV_BRED_MIN_NBS
-#define GEMV_BRED_MIN_NBS 512
-#endif
 #ifndef GEMV_CHUNKS_MAX
 #define GEMV_CHUNKS_MAX 3
 #endif
@@ -438,29 +416,6 @@ int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, con
 int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int R, int N,
                 int K, hipStream_t st, bool accumulate, const int64_t* colterm = nullptr) {
   const int G = K / 128;
-  const int64_t nbs64 = (N + 63) / 64;
-  if (abits == 15 && R > 8 && nbs64 >= GEMV_BRED_MIN_NBS && G >= 8) {
-    // int16 rows above 8 on a wide weight: one 4-wave block per 64-row block, the waves split the groups and sum in
-    // LDS (7B gate|up at 16 rows 33.0 -> 30.2 us; at 8 rows the split over blocks is as fast)
-    const int out_mode = accumulate ? 1 : 0;
-    dim3 grid((unsigned)nbs64), block(256);
-    if (colterm) {
-      if (mh)
-        hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, 4, 4, true, true, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K,
-                           G, 4, out_mode, colterm);
-      else
-        hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, 4, 4, true, false, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N,
-                           K, G, 4, out_mode, colterm);
-    } else {
-      if (mh)
-        hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, 4, 4, false, true, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N,
-                           K, G, 4, out_mode, nullptr);
-      else
-        hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, 4, 4, false, false, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N,
-                           K, G, 4, out_mode, nullptr);
-    }
-    return launch_status("gemv_g128");
-  }
   const int nsplit = gemv_nsplit(N, G, R, abits);
   const int out_mode = (accumulate || nsplit > 1) ? 1 : 0;
   if (!accumulate && nsplit > 1) {

@@ -344,22 +344,3 @@ def test_producer_digit_rows_feed_the_digit_gemm(thr):
         h8 = torch.zeros((2 * R, I), dtype=I8, device=DEV)
         hq, _ = ops.swiglu_qrow(t, dev(rng.integers(0, 8, R), I32), silu, 15, x8=h8)
         assert np.array_equal(host(h8), want_split(host(hq).astype(np.int64)))
-
-
-@pytest.mark.parametrize("R", [5, 8, 9, 15, 16])
-def test_gemv_block_split_wide_weight(thr, R):
-    """int16 rows above 8 on a weight of 592 row blocks (the 7B gate|up, 37888 x 3584) take the block-split GEMV
-    (the 4 waves of a block sum their group ranges in LDS, then store); 16 rows run as the colterm chunk. Checked
-    against the oracle on the first and last 2048 outputs, plain and accumulating."""
-    N, K = 37888, 3584
-    lin, kw, km = synth_lin(thr, 74, "bs", N, K)
-    M = synth.scales_np(km, N, K)
-    xq = rng.integers(-32767, 32768, (R, K))
-    x = dev(xq, I16)
-    t = host(ops.linear_t(x, 15, lin))
-    t2 = torch.full((R, N), 0, dtype=I64, device=DEV)
-    ops.linear_t(x, 15, lin, t2, zeroed=True)
-    t2 = host(t2)
-    for n0, n1 in ((0, 2048), (N - 2048, N)):
-        exp = oracle_t(xq, synth.weights_np(kw, N, K, n0, n1), M[:, n0:n1])
-        assert np.array_equal(t[:, n0:n1], exp) and np.array_equal(t2[:, n0:n1], exp), (R, n0)
