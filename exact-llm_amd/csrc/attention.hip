@@ -74,7 +74,9 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 // grid (R, H), block ATT_THREADS. Scores in LDS (Smax entries), then max, exp LUT, sum, Q20 p, and p.V:
 // thread t owns the dimension pair 2 (t % (hd/2)) and every (ATT_THREADS / (hd/2))-th key, with 16-byte
 // V loads, eight in flight.
+#ifndef ATT_THREADS
 #define ATT_THREADS 512
+#endif
 __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
                                                            const int16_t* __restrict__ kq, const int32_t* __restrict__ sk,
                                                            const int64_t* __restrict__ v, const int32_t* __restrict__ slot,
@@ -161,8 +163,13 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
 // Latency: everything that does not depend on the new token (the RoPE row, each thread's first cached key and
 // its first ATT_VPF value pairs) is loaded together with t, so the block waits on memory about once before the
 // exp table.
+#ifndef ATT_LUT_LDS
+#define ATT_LUT_LDS 0
+#endif
 #define ATT_KPF 16   // 16-byte key chunks prefetched per thread (hd <= 128)
+#ifndef ATT_VPF
 #define ATT_VPF 4    // value pairs prefetched per thread
+#endif
 __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
                                                                const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
                                                                const int64_t* __restrict__ sin_t, const int32_t* __restrict__ slot,
@@ -217,6 +224,12 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
       cs[i][1] = j < hd ? sin_t[(int64_t)p * hd + j] : 0;
     }
   }
+#if ATT_LUT_LDS
+  int32_t* elds = reinterpret_cast<int32_t*>(sc + Smax);   // the exp table, copied with the first loads
+  for (int i = tid; i < EXACT_EXP_N; i += blockDim.x) elds[i] = expt[i];
+#else
+  const int32_t* elds = expt;
+#endif
   const int sh = 28 - s[r];
   for (int j = tid; j < 3 * hd; j += blockDim.x) {
     const int which = j / hd, jj = j - which * hd;
@@ -309,7 +322,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
   mx = block_max64(mx, red);
   int64_t es = 0;
   for (int si = tid; si < S; si += blockDim.x) {
-    const int64_t e = lut_exp(expt, mx - sc[si]);
+    const int64_t e = lut_exp(elds, mx - sc[si]);
     sc[si] = e;
     es += e;
   }
@@ -373,10 +386,11 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
   static bool attr_set = false;
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              8192 * 8);
+                              8192 * 8 + (ATT_LUT_LDS ? EXACT_EXP_N * 4 : 0));
     attr_set = true;
   }
-  hipLaunchKernelGGL(k_attention_qkv, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), t, s, b, cos_t,
+  hipLaunchKernelGGL(k_attention_qkv, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8 + (ATT_LUT_LDS ? EXACT_EXP_N * 4 : 0),
+                     as_stream(stream), t, s, b, cos_t,
                      sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
   return launch_status("attention_qkv");
 }
