@@ -450,8 +450,9 @@ def main():
                     help="also copy 512 MiB on the device three times (calibrates the HBM traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build runs the exact path on a single MI355X; "
-              "multi-GPU runs are not part of it (see DESIGN.md for how the path would shard).", file=sys.stderr)
+        print("bench.py measures one GPU: the exact path runs on a single MI355X here; runs over several GPUs "
+              "(row blocks, KV heads or experts sharded, one int64 all-reduce per split linear) are not part of it.",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
