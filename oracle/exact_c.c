@@ -1,7 +1,8 @@
 /* C restatement of the two oracle routines that dominate large-model fixture runs.
  *
  * TEST INFRASTRUCTURE: this file belongs to the oracle. Only tests/, the fixture scripts under
- * tests/golden/ and the CPU-baseline leg of bench.py load it, and only as the checker. The product
+ * tests/golden/ and the CPU-baseline leg of bench.py load it, and only as the reference results are compared
+ * with. The product
  * never links or calls it.
  *
  *   oc_weights      the seeded int8 weight generator, the same law as exact_amd.synth.weights_np:

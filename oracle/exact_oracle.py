@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY. Nothing in the product package imports this module; only
 ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` use it,
-and only as the checker (or the timed CPU baseline), never as the thing measured or shipped.
+and only as the reference the GPU results are compared with (or the timed CPU baseline), never as the thing
+measured or shipped.
 
 It restates the reference's numeric program (SPEC.md:14-32, v0.4) in numpy:
 every function names the reference file:line it follows.  Arithmetic is int64 with numpy's
