@@ -26,6 +26,13 @@
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+#ifndef GEMM_SMALL_M
+#define GEMM_SMALL_M 128       // rows up to which the 128-row tile configuration runs
+#endif
+#ifndef GEMM_SPLIT_TILES
+#define GEMM_SPLIT_TILES 128   // split K while the output tiles number fewer than this
+#endif
+
 namespace exact {
 
 int zero_bytes(void* dst, int64_t nbytes, hipStream_t st);
@@ -587,7 +594,7 @@ static int gemm_launch(const void* x, const int8_t* wp, const int16_t* mp, int64
   if (ksplit <= 0) {   // split K only when the output tiles fill fewer than half the 256 CUs (the split costs a
                        // zero fill and 64-bit atomics on t, more than a partly idle chip)
     ksplit = 1;
-    while (tiles_m * tiles_n * ksplit < 128 && G / (ksplit * 2) >= 8) ksplit *= 2;
+    while (tiles_m * tiles_n * ksplit < GEMM_SPLIT_TILES && G / (ksplit * 2) >= 8) ksplit *= 2;
   }
   if (ksplit > G) ksplit = G;
   const int use_atomic = ksplit > 1;
@@ -635,7 +642,7 @@ static int gemm_launch_a8p_t(const void* x, const int8_t* wp, const int16_t* mp,
   int ksplit = ksplit_req;
   if (ksplit <= 0) {
     ksplit = 1;
-    while (tiles_m * tiles_n * ksplit < 128 && G / (ksplit * 2) >= 8) ksplit *= 2;
+    while (tiles_m * tiles_n * ksplit < GEMM_SPLIT_TILES && G / (ksplit * 2) >= 8) ksplit *= 2;
   }
   if (ksplit > G) ksplit = G;
   const int use_atomic = ksplit > 1;
@@ -680,7 +687,7 @@ static int gemm_launch_a8p(const void* x, const int8_t* wp, const int16_t* mp, c
                            int K, hipStream_t st, int ksplit_req, const int64_t* colterm = nullptr, bool zeroed = false) {
   // up to 128 rows (prompts of 49-64 tokens as int16 digit rows): 128-row tiles, two 4-wave blocks per CU, instead
   // of 256-row tiles half of padding
-  if (M <= 128 && WM != 2) {
+  if (M <= GEMM_SMALL_M && WM != 2) {
     if (mh) return gemm_launch_a8p_t<2, WN, 2, PAIRS, true>(x, wp, mp, mh, t, M, N, K, st, ksplit_req, colterm, zeroed);
     return gemm_launch_a8p_t<2, WN, 2, PAIRS, false>(x, wp, mp, nullptr, t, M, N, K, st, ksplit_req, colterm, zeroed);
   }
