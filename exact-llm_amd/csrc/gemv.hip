@@ -442,12 +442,17 @@ int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, c
   } while (0)
   const int vr = R <= 1 ? 1 : (R <= 2 ? 2 : 4);
   if (abits == 15 && colterm) {
-    if (mh)
-      hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, 4, 4, true, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, G,
-                         nsplit, out_mode, colterm);
-    else
-      hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, 4, 4, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, G, nsplit,
-                         out_mode, colterm);
+#define GEMV_CT_GO(VR)                                                                                                 \
+  do {                                                                                                                 \
+    if (mh)                                                                                                            \
+      hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, VR, 4, true, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, \
+                         G, nsplit, out_mode, colterm);                                                                \
+    else                                                                                                               \
+      hipLaunchKernelGGL((k_gemv_g128<15, GEMV_NT != 0, VR, 4, true>), grid, block, 0, st, x, wp, mp, mh, t, R, N, K, G,    \
+                         nsplit, out_mode, colterm);                                                                   \
+  } while (0)
+    if (vr == 1) GEMV_CT_GO(1); else if (vr == 2) GEMV_CT_GO(2); else GEMV_CT_GO(4);
+#undef GEMV_CT_GO
   } else if (abits == 15) {
     if (vr == 1) GEMV_GO(15, 1, 4); else if (vr == 2) GEMV_GO(15, 2, 4); else GEMV_GO(15, 4, 4);
   } else if (wide) {
