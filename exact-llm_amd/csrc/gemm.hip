@@ -26,6 +26,12 @@
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+#ifndef GEMM_VALU_PER_MFMA
+#define GEMM_VALU_PER_MFMA 4   // VALU instructions the schedule places after each MFMA of a chain
+#endif
+#ifndef GEMM_PIPE_READS
+#define GEMM_PIPE_READS 4      // LDS reads the schedule places in each chain of 4 MFMAs
+#endif
 #ifndef GEMM_SMALL_M
 #define GEMM_SMALL_M 128       // rows up to which the 128-row tile configuration runs
 #endif
@@ -438,7 +444,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
     _Pragma("unroll") for (int k_ = 0; k_ < 4; ++k_) {                                         \
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                       \
       if (k_ < (reads)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                      \
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                                       \
+      __builtin_amdgcn_sched_group_barrier(0x002, GEMM_VALU_PER_MFMA, 0);                      \
     }                                                                                          \
   } while (0)
 
@@ -466,12 +472,12 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
       readB(B1, stg, 1, ln);
       const v16i c00 = chain(A0, B0);
       rescale(acc[1][1], cp, mprev);
-      PIPE_PATTERN(4);
+      PIPE_PATTERN(GEMM_PIPE_READS);
       __builtin_amdgcn_sched_barrier(0);
       readA(A1, stg, 1, ln);
       const v16i c01 = chain(A0, B1);
       rescale(acc[0][0], c00, m0);
-      PIPE_PATTERN(4);
+      PIPE_PATTERN(GEMM_PIPE_READS);
       // all of this wave's reads of stage stg are done; group g + 1 has landed; then stage stg is
       // free for group g + S
       const int ahead = (g1 - 1 < g + S - 1 ? g1 - 1 : g + S - 1) - (g + 1);   // groups in flight after g + 1
@@ -485,13 +491,13 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
       readA(A0, nstg, 0, ln);
       const v16i c10 = chain(A1, B0);
       rescale(acc[0][1], c01, m1);
-      PIPE_PATTERN(4);
+      PIPE_PATTERN(GEMM_PIPE_READS);
       __builtin_amdgcn_sched_barrier(0);
       readB(B0, nstg, 0, ln);
       const int mn0 = readM(nstg, 0, ln), mn1 = readM(nstg, 1, ln);
       const v16i c11 = chain(A1, B1);
       rescale(acc[1][0], c10, m0);
-      PIPE_PATTERN(4);
+      PIPE_PATTERN(GEMM_PIPE_READS);
       cp = c11;
       mprev = m1;
       m0 = mn0;
