@@ -168,8 +168,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
 #endif
 #define ATT_KPF 16   // 16-byte key chunks prefetched per thread (hd <= 128)
 #ifndef ATT_VPF
-#define ATT_VPF 4    // value pairs prefetched per thread
+#define ATT_VPF 4        // value pairs prefetched per thread (caches of up to ATT_VPF_LONG_S positions)
 #endif
+#ifndef ATT_VPF_LONG
+#define ATT_VPF_LONG 24  // ... and for longer caches (decode at a 256-token context: +3%; at 16 tokens -0.4%)
+#endif
+#ifndef ATT_VPF_LONG_S
+#define ATT_VPF_LONG_S 128
+#endif
+template <int VPF>
 __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
                                                                const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
                                                                const int64_t* __restrict__ sin_t, const int32_t* __restrict__ slot,
@@ -208,10 +215,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
       if (j8 < hd / 8) kpre[j8] = kr[j8];
     skpre = sk[cbase + tid];
   }
-  v4i vpre[ATT_VPF];
+  v4i vpre[VPF];
   const int64_t* vb = v + cbase * hd + 2 * dp;
 #pragma unroll
-  for (int i = 0; i < ATT_VPF; ++i) {
+  for (int i = 0; i < VPF; ++i) {
     const int si = pp + i * nparts;
     if (pp < nparts && si < p) vpre[i] = *reinterpret_cast<const v4i*>(vb + (int64_t)si * hd);
   }
@@ -332,7 +339,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
   int64_t a0 = 0, a1 = 0;
   if (pp < nparts) {
 #pragma unroll
-    for (int i = 0; i < ATT_VPF; ++i) {
+    for (int i = 0; i < VPF; ++i) {
       const int si = pp + i * nparts;
       if (si < p) {
         const v4i vv = vpre[i];
@@ -342,7 +349,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
       }
     }
 #pragma unroll 8
-    for (int si = pp + ATT_VPF * nparts; si < p; si += nparts) {
+    for (int si = pp + VPF * nparts; si < p; si += nparts) {
       const v4i vv = *reinterpret_cast<const v4i*>(vb + (int64_t)si * hd);
       const int64_t pr = sc[si];
       a0 = (int64_t)((uint64_t)a0 + (uint64_t)(pr * (((int64_t)vv[1] << 32) | (uint32_t)vv[0])));
@@ -385,13 +392,19 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
   if (hd > 256 || hd % 8 || (2 * ATT_THREADS) % hd || Smax > 8192) return EXACT_E_UNSUPPORTED;
   static bool attr_set = false;
   if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              8192 * 8 + (ATT_LUT_LDS ? EXACT_EXP_N * 4 : 0));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8 + (ATT_LUT_LDS ? EXACT_EXP_N * 4 : 0));
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF_LONG>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8 + (ATT_LUT_LDS ? EXACT_EXP_N * 4 : 0));
     attr_set = true;
   }
-  hipLaunchKernelGGL(k_attention_qkv, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8 + (ATT_LUT_LDS ? EXACT_EXP_N * 4 : 0),
-                     as_stream(stream), t, s, b, cos_t,
-                     sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
+  const size_t lds = (size_t)Smax * 8 + (ATT_LUT_LDS ? EXACT_EXP_N * 4 : 0);
+  if (Smax > ATT_VPF_LONG_S)
+    hipLaunchKernelGGL(k_attention_qkv<ATT_VPF_LONG>, dim3(R, H), dim3(ATT_THREADS), lds, as_stream(stream), t, s, b, cos_t,
+                       sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
+  else
+    hipLaunchKernelGGL(k_attention_qkv<ATT_VPF>, dim3(R, H), dim3(ATT_THREADS), lds, as_stream(stream), t, s, b, cos_t, sin_t,
+                       slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
   return launch_status("attention_qkv");
 }
 
