@@ -163,9 +163,6 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
 // Latency: everything that does not depend on the new token (the RoPE row, each thread's first cached key and
 // its first ATT_VPF value pairs) is loaded together with t, so the block waits on memory about once before the
 // exp table.
-#ifndef ATT_LUT_LDS
-#define ATT_LUT_LDS 0
-#endif
 #define ATT_KPF 16   // 16-byte key chunks prefetched per thread (hd <= 128)
 #ifndef ATT_VPF
 #define ATT_VPF 4        // value pairs prefetched per thread (caches of up to ATT_VPF_LONG_S positions)
@@ -231,12 +228,6 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
       cs[i][1] = j < hd ? sin_t[(int64_t)p * hd + j] : 0;
     }
   }
-#if ATT_LUT_LDS
-  int32_t* elds = reinterpret_cast<int32_t*>(sc + Smax);   // the exp table, copied with the first loads
-  for (int i = tid; i < EXACT_EXP_N; i += blockDim.x) elds[i] = expt[i];
-#else
-  const int32_t* elds = expt;
-#endif
   const int sh = 28 - s[r];
   for (int j = tid; j < 3 * hd; j += blockDim.x) {
     const int which = j / hd, jj = j - which * hd;
@@ -329,7 +320,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
   mx = block_max64(mx, red);
   int64_t es = 0;
   for (int si = tid; si < S; si += blockDim.x) {
-    const int64_t e = lut_exp(elds, mx - sc[si]);
+    const int64_t e = lut_exp(expt, mx - sc[si]);
     sc[si] = e;
     es += e;
   }
@@ -393,12 +384,12 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
   static bool attr_set = false;
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8 + (ATT_LUT_LDS ? EXACT_EXP_N * 4 : 0));
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF_LONG>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8 + (ATT_LUT_LDS ? EXACT_EXP_N * 4 : 0));
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
     attr_set = true;
   }
-  const size_t lds = (size_t)Smax * 8 + (ATT_LUT_LDS ? EXACT_EXP_N * 4 : 0);
+  const size_t lds = (size_t)Smax * 8;
   if (Smax > ATT_VPF_LONG_S)
     hipLaunchKernelGGL(k_attention_qkv<ATT_VPF_LONG>, dim3(R, H), dim3(ATT_THREADS), lds, as_stream(stream), t, s, b, cos_t,
                        sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
