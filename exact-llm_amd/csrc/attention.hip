@@ -77,6 +77,17 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #ifndef ATT_THREADS
 #define ATT_THREADS 512
 #endif
+#define ATT_KPF 16   // 16-byte key chunks prefetched per thread (hd <= 128)
+#ifndef ATT_VPF
+#define ATT_VPF 4        // value pairs prefetched per thread (caches of up to ATT_VPF_LONG_S positions)
+#endif
+#ifndef ATT_VPF_LONG
+#define ATT_VPF_LONG 24  // ... and for longer caches (decode at a 256-token context: +3%; at 16 tokens -0.4%)
+#endif
+#ifndef ATT_VPF_LONG_S
+#define ATT_VPF_LONG_S 128
+#endif
+template <int VPF>
 __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
                                                            const int16_t* __restrict__ kq, const int32_t* __restrict__ sk,
                                                            const int64_t* __restrict__ v, const int32_t* __restrict__ slot,
@@ -92,24 +103,61 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
   const int kh = h / (H / KV);
   const int S = min(pos[r] + 1, Smax), sl = slot[r];
   const int sqv = sq[r * H + h];
+  const int64_t cbase = ((int64_t)sl * KV + kh) * Smax;
+  const int npair = hd >> 1, nparts = blockDim.x / npair;   // hd divides 2 * ATT_THREADS
+  const int dp = tid % npair, pp = tid / npair;
+  // loads that do not depend on the query, issued with it: this thread's first key and its first VPF value pairs
+  v4i kpre[ATT_KPF];
+  int skpre = 0;
+  const bool kp = hd <= 8 * ATT_KPF && tid < S;
+  if (kp) {
+    const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + tid) * hd);
+#pragma unroll
+    for (int j8 = 0; j8 < ATT_KPF; ++j8)
+      if (j8 < hd / 8) kpre[j8] = kr[j8];
+    skpre = sk[cbase + tid];
+  }
+  v4i vpre[VPF];
+  const int64_t* vb = v + cbase * hd + 2 * dp;
+#pragma unroll
+  for (int i = 0; i < VPF; ++i) {
+    const int si = pp + i * nparts;
+    if (pp < nparts && si < S) vpre[i] = *reinterpret_cast<const v4i*>(vb + (int64_t)si * hd);
+  }
   for (int j = tid; j < hd; j += blockDim.x) qs[j] = qq[((int64_t)r * H + h) * hd + j];
   __syncthreads();
-  const int64_t cbase = ((int64_t)sl * KV + kh) * Smax;
   int64_t mx = INT64_MIN;
   for (int si = tid; si < S; si += blockDim.x) {
     // 16-byte key loads, four in flight; each pair of int16 products is exact in int32 (< 2^31)
     const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + si) * hd);
     int64_t dot = 0;
-#pragma unroll 4
-    for (int j8 = 0; j8 < hd / 8; ++j8) {
-      const v4i kk = kr[j8];
+    int skv;
+    if (kp && si == tid) {   // the prefetched first key
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int j = j8 * 8 + 2 * c;
-        dot += (int64_t)(qs[j] * (int32_t)(int16_t)(kk[c] & 0xffff) + qs[j + 1] * (int32_t)(int16_t)(kk[c] >> 16));
+      for (int j8 = 0; j8 < ATT_KPF; ++j8) {
+        if (j8 < hd / 8) {
+          const v4i kk = kpre[j8];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int j = j8 * 8 + 2 * c;
+            dot += (int64_t)(qs[j] * (int32_t)(int16_t)(kk[c] & 0xffff) + qs[j + 1] * (int32_t)(int16_t)(kk[c] >> 16));
+          }
+        }
       }
+      skv = skpre;
+    } else {
+#pragma unroll 4
+      for (int j8 = 0; j8 < hd / 8; ++j8) {
+        const v4i kk = kr[j8];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int j = j8 * 8 + 2 * c;
+          dot += (int64_t)(qs[j] * (int32_t)(int16_t)(kk[c] & 0xffff) + qs[j + 1] * (int32_t)(int16_t)(kk[c] >> 16));
+        }
+      }
+      skv = sk[cbase + si];
     }
-    const int64_t val = shr64(dot * INV, 32 - sqv - sk[cbase + si]);
+    const int64_t val = shr64(dot * INV, 32 - sqv - skv);
     sc[si] = val;
     mx = val > mx ? val : mx;
   }
@@ -123,13 +171,20 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
   es = block_sum64(es, red);
   for (int si = tid; si < S; si += blockDim.x) sc[si] = floordiv_pos(shl64(sc[si], 20), es);
   __syncthreads();
-  const int npair = hd >> 1, nparts = blockDim.x / npair;   // hd divides 2 * ATT_THREADS
-  const int dp = tid % npair, pp = tid / npair;
   int64_t a0 = 0, a1 = 0;
   if (pp < nparts) {
-    const int64_t* vb = v + cbase * hd + 2 * dp;
+#pragma unroll
+    for (int i = 0; i < VPF; ++i) {
+      const int si = pp + i * nparts;
+      if (si < S) {
+        const v4i vv = vpre[i];
+        const int64_t p = sc[si];
+        a0 = (int64_t)((uint64_t)a0 + (uint64_t)(p * (((int64_t)vv[1] << 32) | (uint32_t)vv[0])));
+        a1 = (int64_t)((uint64_t)a1 + (uint64_t)(p * (((int64_t)vv[3] << 32) | (uint32_t)vv[2])));
+      }
+    }
 #pragma unroll 8
-    for (int si = pp; si < S; si += nparts) {
+    for (int si = pp + VPF * nparts; si < S; si += nparts) {
       const v4i vv = *reinterpret_cast<const v4i*>(vb + (int64_t)si * hd);
       const int64_t p = sc[si];
       a0 = (int64_t)((uint64_t)a0 + (uint64_t)(p * (((int64_t)vv[1] << 32) | (uint32_t)vv[0])));
@@ -163,16 +218,6 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
 // Latency: everything that does not depend on the new token (the RoPE row, each thread's first cached key and
 // its first ATT_VPF value pairs) is loaded together with t, so the block waits on memory about once before the
 // exp table.
-#define ATT_KPF 16   // 16-byte key chunks prefetched per thread (hd <= 128)
-#ifndef ATT_VPF
-#define ATT_VPF 4        // value pairs prefetched per thread (caches of up to ATT_VPF_LONG_S positions)
-#endif
-#ifndef ATT_VPF_LONG
-#define ATT_VPF_LONG 24  // ... and for longer caches (decode at a 256-token context: +3%; at 16 tokens -0.4%)
-#endif
-#ifndef ATT_VPF_LONG_S
-#define ATT_VPF_LONG_S 128
-#endif
 template <int VPF>
 __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
                                                                const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
@@ -420,10 +465,18 @@ extern "C" int exact_attention(const int16_t* qq, const int32_t* sq, const int16
   if (hd > 256 || (2 * ATT_THREADS) % hd || hd % 8 || Smax > 8192) return EXACT_E_UNSUPPORTED;
   static bool attr_set = false;   // the scores take Smax * 8 bytes of LDS, up to 64 KiB beside the static arrays
   if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention), hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention<ATT_VPF>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              8192 * 8);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention<ATT_VPF_LONG>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
     attr_set = true;
   }
-  hipLaunchKernelGGL(k_attention, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot,
+  if (Smax > ATT_VPF_LONG_S)
+    hipLaunchKernelGGL(k_attention<ATT_VPF_LONG>, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot,
+                     pos,
+                     exp_t, out, obits, H, KV, hd, Smax, INV);
+  else
+    hipLaunchKernelGGL(k_attention<ATT_VPF>, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot,
                      pos,
                      exp_t, out, obits, H, KV, hd, Smax, INV);
   return launch_status("attention");
