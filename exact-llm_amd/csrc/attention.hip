@@ -87,7 +87,12 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #ifndef ATT_VPF_LONG_S
 #define ATT_VPF_LONG_S 128
 #endif
-template <int VPF>
+#ifndef ATT_VPF_LONG_BLOCKS
+#define ATT_VPF_LONG_BLOCKS 256
+#endif
+// PRE: prefetch the first key and VPF value pairs with the query (one round of blocks: the registers they take
+// cost more occupancy than they save latency when the blocks run in several rounds)
+template <int VPF, bool PRE>
 __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
                                                            const int16_t* __restrict__ kq, const int32_t* __restrict__ sk,
                                                            const int64_t* __restrict__ v, const int32_t* __restrict__ slot,
@@ -109,7 +114,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
   // loads that do not depend on the query, issued with it: this thread's first key and its first VPF value pairs
   v4i kpre[ATT_KPF];
   int skpre = 0;
-  const bool kp = hd <= 8 * ATT_KPF && tid < S;
+  const bool kp = PRE && hd <= 8 * ATT_KPF && tid < S;
   if (kp) {
     const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + tid) * hd);
 #pragma unroll
@@ -119,10 +124,12 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
   }
   v4i vpre[VPF];
   const int64_t* vb = v + cbase * hd + 2 * dp;
+  if constexpr (PRE) {
 #pragma unroll
-  for (int i = 0; i < VPF; ++i) {
-    const int si = pp + i * nparts;
-    if (pp < nparts && si < S) vpre[i] = *reinterpret_cast<const v4i*>(vb + (int64_t)si * hd);
+    for (int i = 0; i < VPF; ++i) {
+      const int si = pp + i * nparts;
+      if (pp < nparts && si < S) vpre[i] = *reinterpret_cast<const v4i*>(vb + (int64_t)si * hd);
+    }
   }
   for (int j = tid; j < hd; j += blockDim.x) qs[j] = qq[((int64_t)r * H + h) * hd + j];
   __syncthreads();
@@ -174,7 +181,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
   int64_t a0 = 0, a1 = 0;
   if (pp < nparts) {
 #pragma unroll
-    for (int i = 0; i < VPF; ++i) {
+    for (int i = 0; i < (PRE ? VPF : 0); ++i) {
       const int si = pp + i * nparts;
       if (si < S) {
         const v4i vv = vpre[i];
@@ -184,7 +191,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
       }
     }
 #pragma unroll 8
-    for (int si = pp + VPF * nparts; si < S; si += nparts) {
+    for (int si = pp + (PRE ? VPF : 0) * nparts; si < S; si += nparts) {
       const v4i vv = *reinterpret_cast<const v4i*>(vb + (int64_t)si * hd);
       const int64_t p = sc[si];
       a0 = (int64_t)((uint64_t)a0 + (uint64_t)(p * (((int64_t)vv[1] << 32) | (uint32_t)vv[0])));
@@ -465,18 +472,24 @@ extern "C" int exact_attention(const int16_t* qq, const int32_t* sq, const int16
   if (hd > 256 || (2 * ATT_THREADS) % hd || hd % 8 || Smax > 8192) return EXACT_E_UNSUPPORTED;
   static bool attr_set = false;   // the scores take Smax * 8 bytes of LDS, up to 64 KiB beside the static arrays
   if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention<ATT_VPF>), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              8192 * 8);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention<ATT_VPF_LONG>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention<ATT_VPF, true>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention<ATT_VPF_LONG, true>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention<1, false>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              8192 * 8);
     attr_set = true;
   }
-  if (Smax > ATT_VPF_LONG_S)
-    hipLaunchKernelGGL(k_attention<ATT_VPF_LONG>, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot,
+  if (R * H > ATT_VPF_LONG_BLOCKS)
+    hipLaunchKernelGGL((k_attention<1, false>), dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot,
+                     pos,
+                     exp_t, out, obits, H, KV, hd, Smax, INV);
+  else if (Smax > ATT_VPF_LONG_S)
+    hipLaunchKernelGGL((k_attention<ATT_VPF_LONG, true>), dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot,
                      pos,
                      exp_t, out, obits, H, KV, hd, Smax, INV);
   else
-    hipLaunchKernelGGL(k_attention<ATT_VPF>, dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot,
+    hipLaunchKernelGGL((k_attention<ATT_VPF, true>), dim3(R, H), dim3(ATT_THREADS), (size_t)Smax * 8, as_stream(stream), qq, sq, kq, sk, v, slot,
                      pos,
                      exp_t, out, obits, H, KV, hd, Smax, INV);
   return launch_status("attention");

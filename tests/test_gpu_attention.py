@@ -88,9 +88,9 @@ def test_prefill_matches_oracle(H, KV, nkeys, R, vmag, shifts):
     assert np.array_equal(obits, obits_of(want, H))
 
 
-@pytest.mark.parametrize("R,nkeys", [(3, 50), (17, 17)])
+@pytest.mark.parametrize("R,nkeys", [(3, 50), (17, 17), (70, 100)])   # 70 x 4 heads: the blocks run in several rounds
 def test_row_attention_matches_oracle(R, nkeys):
-    H, KV, hd, Smax, slot = 4, 2, 128, 64, 1
+    H, KV, hd, Smax, slot = 4, 2, 128, max(64, nkeys), 1
     case = make_case(R + nkeys, 2, slot, H, KV, hd, Smax, nkeys, R, "large")
     cache, qq, sq, pos = to_dev(*case)
     out = torch.zeros((R, H * hd), dtype=I64, device=DEV)
