@@ -248,7 +248,7 @@ class TModel:
     def new_cache(self, B=None):
         return Cache(self.cfg, self.batch if B is None else B, self.Smax, self.dev, self.nl)
 
-    PREFILL_MIN_ROWS = 32
+    PREFILL_MIN_ROWS = 96   # rows from which prefill attention runs on the matrix cores (the row kernel is faster below)
     QROW_FUSE_ROWS = 2
     EXPERT_GEMM_MIN_PAIRS = 64   # (row, expert) pairs from which the MoE experts run as one grouped GEMM
 
