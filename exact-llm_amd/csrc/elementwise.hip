@@ -375,6 +375,9 @@ extern "C" int exact_irms(const int64_t* x, const int64_t* g, int64_t* y, int32_
 #ifndef RMS_MAX_THREADS
 #define RMS_MAX_THREADS 1024
 #endif
+#ifndef RMS_LARGE_THREADS
+#define RMS_LARGE_THREADS 768    // rows above 4096: 12 waves (14B decode 196 -> 202 tok/s)
+#endif
 #ifndef RMS_SMALL_THREADS
 #define RMS_SMALL_THREADS 512    // rows of up to 2048: fewer waves per reduction (0.5B decode 893 -> 918 tok/s)
 #endif
@@ -383,7 +386,7 @@ extern "C" int exact_rmsnorm_qrow(int64_t* x, int64_t* res_t, const int32_t* res
   if (!x || !g || !xq || !s || R <= 0 || D <= 0 || bits < 1 || bits > 15 || (res_t && !res_s)) return EXACT_E_ARG;
   if (x8 && bits < 8) return EXACT_E_ARG;   // digit rows are of int16 values
   if (D > SMEM_ROW_MAX) return EXACT_E_UNSUPPORTED;
-  const int tmax = D <= 2048 ? RMS_SMALL_THREADS : RMS_MAX_THREADS;
+  const int tmax = D <= 2048 ? RMS_SMALL_THREADS : (D > 4096 ? RMS_LARGE_THREADS : RMS_MAX_THREADS);
   int nt = D >= tmax ? tmax : ((D + 63) / 64) * 64;
   if ((D + nt - 1) / nt > 8) nt = 1024;   // the row kernel holds at most 8 values per thread
   const int ept = (D + nt - 1) / nt;

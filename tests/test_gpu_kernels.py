@@ -344,3 +344,20 @@ def test_producer_digit_rows_feed_the_digit_gemm(thr):
         h8 = torch.zeros((2 * R, I), dtype=I8, device=DEV)
         hq, _ = ops.swiglu_qrow(t, dev(rng.integers(0, 8, R), I32), silu, 15, x8=h8)
         assert np.array_equal(host(h8), want_split(host(hq).astype(np.int64)))
+
+
+@pytest.mark.parametrize("D", [896, 2048, 3584, 5120])
+def test_rmsnorm_qrow_row_sizes(D):
+    """residual + irms + qrow at the model row sizes (512-, 1024- and 768-thread blocks) against the oracle."""
+    R = 3
+    x = rng.integers(-(1 << 36), 1 << 36, (R, D))
+    t = rng.integers(-(1 << 44), 1 << 44, (R, D))
+    s = rng.integers(0, 12, R)
+    g = rng.integers(1 << 15, 1 << 17, D)
+    xd, td = dev(x, I64), dev(t, I64)
+    xq, sq = ops.rmsnorm_qrow(xd, dev(g, I64), 15, td, dev(s, I32), clear=True)
+    x2 = x + O.round_shift(t, (28 - s)[:, None])
+    want_q, want_s = O.qrow(O.irms(x2, g), 15)
+    assert np.array_equal(host(xd), x2)
+    assert np.array_equal(host(xq), want_q) and np.array_equal(host(sq).reshape(-1), np.asarray(want_s).reshape(-1))
+    assert not host(td).any()
