@@ -19,8 +19,12 @@ Pinning (what checks each function against something other than this file):
   * Model.forward (IntModel)         -> golden logits written from the reference's own IntModel
                                         (tests/golden/make_golden.py) + the cells above
   * KV-cached decode                 -> equality with full recompute (attention_tc_longctx_kaggle.py:641-643)
-  * MoE routing / isig / SIG_T       -> closed forms + brute force (moe_exact_kaggle.py:419-467);
-                                        SIG_T has no reference-held vector: parity unpinned beyond its closed form
+  * Model.moe, moe_route, moe_weighted, isig / SIG_T
+                                     -> vectors of the reference's own MoEInt.moe, SIG_T / isig and GQLin
+                                        (tests/golden/make_golden_moe.py: per-channel and group-128 layers,
+                                        ties across the top-k boundary) + planted mistakes that must fail
+  * reduction order                  -> logits hashes identical with K permuted or reversed inside exact_mm
+                                        and group_acc (exact_llm.py:76-79)
   * sampler (splitmix64, sample_int) -> known-answer values of splitmix64 from its published
                                         definition + brute-force inverse CDF
   * quantize_channel / quantize_group -> closed-form properties (the column / group maximum maps to
@@ -328,6 +332,19 @@ def attention_head_q(qq, sq, kk, sk, v, valid, INV):
     return round_shift(np.matmul(p.astype(I64), np.asarray(v, I64)), 20)
 
 
+# ----------------------------------------------------------------------------- MoE routing
+def moe_route(p, k):
+    """Top-k experts per row: stable sort of -p, so equal probabilities go to the lower expert index
+    (moe_exact_kaggle.py:457)."""
+    return np.argsort(-p, axis=-1, kind="stable")[:, :k]
+
+
+def moe_weighted(p, sel, rows, e, ye):
+    """Expert e's output rows weighted by the un-renormalised Q20 router probability:
+    shr(p[rows, e] * ye, 20) (moe_exact_kaggle.py:465)."""
+    return round_shift(p[rows, e][:, None] * ye, 20)
+
+
 # ----------------------------------------------------------------------------- model
 class Model:
     """Integer Qwen2-family model (IntModel, exact_llm.py:141-180) with group-128 or per-channel
@@ -368,7 +385,7 @@ class Model:
         logits = self.lin(L["router"], m)
         NE = logits.shape[1]
         p = isoftmax(logits, np.ones((T, NE), bool))
-        sel = np.argsort(-p, axis=-1, kind="stable")[:, :self.c["topk"]]
+        sel = moe_route(p, self.c["topk"])
         if stats is not None:
             stats.append(sel.copy())
         out = np.zeros_like(m)
@@ -379,7 +396,7 @@ class Model:
             gp, up, dn = L["experts"][e]
             mm = m[rows]
             ye = self.lin(dn, round_shift(isilu(self.lin(gp, mm)) * self.lin(up, mm), F))
-            out[rows] += round_shift(p[rows, e][:, None] * ye, 20)
+            out[rows] += moe_weighted(p, sel, rows, e, ye)
         ys = self.lin(L["sd"], round_shift(isilu(self.lin(L["sg"], m)) * self.lin(L["su"], m), F))
         return out + round_shift(isig(self.lin(L["sgate"], m)) * ys, F)
 

@@ -201,7 +201,8 @@ def test_combine_matches_oracle(tab):
     for r in range(R):
         for j in range(k):
             q = pidx[r * k + j]
-            want[r] += O.round_shift(p_sel[r, j] * O.round_shift(t_ed[q], 28 - sh_pair[q]), 20)
+            ye = O.round_shift(t_ed[q], 28 - sh_pair[q])[None]
+            want[r] += O.moe_weighted(p_sel, None, [r], j, ye)[0]     # the oracle's pinned expert weighting
         want[r] += O.round_shift(gate[r] * O.round_shift(t_sd[r], 28 - sh_s[r]), 16)
     assert np.array_equal(host(xd), want)
     assert not host(args[0]).any() and not host(args[4]).any()

@@ -68,3 +68,44 @@ def test_planted_layer_order_mistake_is_caught(golden):
     W2 = dict(W)
     W2["layers"] = [dict(L, gate=L["up"], up=L["gate"]) for L in W["layers"]]
     assert not np.array_equal(O.Model(W2, cfg)(z["prompt"].tolist()), z["logits"])
+
+
+def _permuted_mm(order):
+    """exact_mm with the K axis permuted (or reversed) before the float64 product (exact_llm.py:76-79)."""
+    base = O.exact_mm
+
+    def mm(a, b):
+        K = np.shape(a)[-1]
+        p = order(K)
+        return base(np.asarray(a)[..., p], np.asarray(b)[p, :])
+    return mm
+
+
+def _permuted_group_acc(order):
+    """group_acc with each group's 128 inputs permuted (or reversed)."""
+    base = O.group_acc
+
+    def acc(xq, w, G=128):
+        p = np.concatenate([g * G + order(G) for g in range(xq.shape[1] // G)])
+        return base(np.asarray(xq)[:, p], np.asarray(w)[p, :], G)
+    return acc
+
+
+ORDERS = {"permuted": lambda K: np.random.default_rng(K).permutation(K), "reversed": lambda K: np.arange(K)[::-1]}
+
+
+@pytest.mark.parametrize("order", sorted(ORDERS))
+def test_reduction_order_invariance(golden, order, monkeypatch):
+    """The reference's M2/S1 gates: logits hashes are identical under a permuted or reversed reduction order
+    (exact_llm.py:76-79, 285-292) for the per-channel golden model, a group-128 model and a MoE model."""
+    import helpers
+    from exact_amd import synth
+    z, cfg, W = golden
+    ids = z["prompt"].tolist()
+    models = [O.Model(W, cfg)]
+    for name in ("tiny", "tiny-moe"):
+        models.append(helpers.oracle_model(synth.CONFIGS[name], 5, T=64))
+    ref = [O.h(m(ids[:9])) for m in models]
+    monkeypatch.setattr(O, "exact_mm", _permuted_mm(ORDERS[order]))
+    monkeypatch.setattr(O, "group_acc", _permuted_group_acc(ORDERS[order]))
+    assert [O.h(m(ids[:9])) for m in models] == ref
