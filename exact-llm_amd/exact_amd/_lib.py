@@ -20,6 +20,7 @@ SIGNATURES = {
     "exact_synth_vector": [U64, I64, I64, P, I64, P],
     "exact_pack_linear": [P, P, P, P, I32, I32, I32, I32, P],
     "exact_pack_scales": [P, P, I32, I32, I32, I32, P],
+    "exact_gemv": [P, P, P, P, I32, I32, P],
     "exact_gemv_g128": [P, I32, P, P, P, P, I32, I32, I32, P],
     "exact_gemv_g128_acc": [P, I32, P, P, P, P, I32, I32, I32, P],
     "exact_gemm_g128": [P, I32, P, P, P, P, I32, I32, I32, P],

@@ -3,8 +3,8 @@ current HIP stream, return or fill caller-visible tensors. Allocation (when an o
 happens here, on the host side of the ABI, never inside the library.
 
 The reference's single custom op is exact::gemv (experiments/speed_fair_kaggle.py:698-702); it is
-registered below under the same name with the same (x16, wT, Mg) -> int64 (N,) contract, where wT
-and Mg are this library's packed weight and scale buffers.
+registered below under the same name with the same contract: (x16 int16 (K,), wT int8 (N, K) row-major,
+Mg int64 (N, K/128)) -> int64 (N,), on the reference's own tensors with no repacking.
 """
 import ctypes
 
@@ -133,6 +133,7 @@ def gemv_qrow_acc(xs, part, nparts, abits, lin, out, s_out, K=None, zero=None):
     K = lin.K if K is None else K
     if K != lin.K:
         raise ExactError(f"gemv_qrow_acc: K = {K}, linear has K = {lin.K}")
+    _need_packed(lin, "gemv_qrow_acc")
     _need(xs, I64, "xs")
     _need(part, I32, "part", R * nparts)
     _need(out, I64, "out", R * lin.N)
@@ -164,6 +165,7 @@ def gemm_g128(x, abits, lin, out=None, zeroed=False, x8=None):
     x8: the digit rows of the int16 x that its producer wrote (used above GEMV_CHUNK_ROWS[7] rows)."""
     R, K = x.shape
     sfx = "_zeroed" if zeroed and out is not None else ""
+    _need_packed(lin, "gemm_g128")
     if x8 is not None and abits == 15 and R > GEMV_CHUNK_ROWS[7]:
         if K != lin.K:
             raise ExactError(f"exact_gemm_g128_digits: x has K = {K}, linear has K = {lin.K}")
@@ -204,10 +206,22 @@ def linear_t(x, abits, lin, out=None, zeroed=False, x8=None):
     return gemm_g128(x, abits, lin, out, zeroed=zeroed, x8=x8)
 
 
+def _need_packed(lin, fn):
+    """The packed buffers of lin hold ceil(N/64) * G tiles: wp int8 8192 B, mp (and mh) int16 64 per tile."""
+    if lin.K <= 0 or lin.K % 128:
+        raise ExactError(f"{fn}: K = {lin.K} is not a positive multiple of 128")
+    tiles = ((lin.N + 63) // 64) * (lin.K // 128)
+    _need(lin.wp, I8, f"{fn}: packed weights wp", tiles * 8192)
+    _need(lin.mp, I16, f"{fn}: packed scales mp", tiles * 64)
+    if lin.mh is not None:
+        _need(lin.mh, I16, f"{fn}: wide-scale plane mh", tiles * 64)
+
+
 def _linear(fn, x, abits, lin, out):
     R, K = x.shape
     if K != lin.K:
         raise ExactError(f"{fn}: x has K = {K}, linear has K = {lin.K}")
+    _need_packed(lin, fn)
     _need(x, I16 if abits == 15 else I8, "x")
     if out is None:
         out = torch.empty((R, lin.N), dtype=I64, device=x.device)
@@ -526,21 +540,38 @@ def moe_combine(x, t_ed, sh_pair, p_sel, pidx, k, t_sd=None, sh_s=None, gate=Non
 
 
 # ----------------------------------------------------------------------------- the reference's op
+def gemv_rows(x16, wT, Mg, out=None):
+    """out (N,) int64 = sum_g (sum_{k in g} x16[k] wT[n, k]) Mg[n, g] on the reference's own tensors: x16 int16 (K,),
+    wT int8 (N, K) row-major (TLinG.wT, speed_fair_kaggle.py:730), Mg int64 (N, K/128) (:731). No repacking."""
+    if x16.dim() != 1 or wT.dim() != 2 or Mg.dim() != 2:
+        raise ExactError(f"exact::gemv: expected x16 (K,), wT (N, K), Mg (N, K/128); got {tuple(x16.shape)}, "
+                         f"{tuple(wT.shape)}, {tuple(Mg.shape)}")
+    N, K = wT.shape
+    if x16.shape[0] != K or K % 128 or K == 0 or N == 0:
+        raise ExactError(f"exact::gemv: x16 has {x16.shape[0]} values, wT is ({N}, {K}); K must be a positive multiple "
+                         f"of 128 and equal to x16's length")
+    if tuple(Mg.shape) != (N, K // 128):
+        raise ExactError(f"exact::gemv: Mg must be ({N}, {K // 128}), got {tuple(Mg.shape)}")
+    _need(x16, I16, "exact::gemv: x16")
+    _need(wT, I8, "exact::gemv: wT")
+    _need(Mg, I64, "exact::gemv: Mg")
+    if x16.data_ptr() % 16 or wT.data_ptr() % 16:
+        raise ExactError("exact::gemv: x16 and wT must start on a 16-byte boundary")
+    out = torch.empty(N, dtype=I64, device=x16.device) if out is None else _need(out, I64, "exact::gemv: out", N)
+    _lib.call("exact_gemv", _ptr(x16), _ptr(wT), _ptr(Mg), _ptr(out), N, K, _stream())
+    return out
+
+
 @torch.library.custom_op("exact::gemv", mutates_args=())
 def gemv(x16: torch.Tensor, wT: torch.Tensor, Mg: torch.Tensor) -> torch.Tensor:
-    """exact::gemv(x16, wT, Mg) -> int64 (N,) (speed_fair_kaggle.py:698-700); wT / Mg are packed buffers
-    whose output count is carried by Mg: N = Mg.numel() // G rounded to the packed rows."""
-    K = x16.shape[-1]
-    G = K // 128
-    N = Mg.numel() // G
-    lin = PackedLinear(wT, Mg, N, K)
-    return gemv_g128(x16.view(1, K), 15, lin).view(N)
+    """exact::gemv(x16, wT, Mg) -> int64 (N,) (speed_fair_kaggle.py:698-700): the reference's op, same tensors, same
+    result; the output is allocated on x16's device and written by one launch on the current stream."""
+    return gemv_rows(x16, wT, Mg)
 
 
 @gemv.register_fake
 def _gemv_fake(x16, wT, Mg):
-    G = x16.shape[-1] // 128
-    return torch.empty((Mg.numel() // G,), dtype=torch.int64, device=x16.device)
+    return torch.empty((wT.shape[0],), dtype=torch.int64, device=x16.device)
 
 
 def np_to_dev(a, dtype, device):

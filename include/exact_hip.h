@@ -77,6 +77,14 @@ int exact_gemv_g128(const void* x, int32_t abits, const int8_t* wp, const int16_
 int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,
                         int32_t R, int32_t N, int32_t K, void* stream);
 
+/* The reference's exact::gemv on its own tensors, with no repacking: out[n] = sum_g (sum_{k in g} x[k] *
+ * wT[n][k]) * Mg[n][g] for one int16 row x (K,), the row-major int8 weight wT (N, K) (TLinG.wT, each output's
+ * K weights contiguous) and int64 group scales Mg (N, G), G = K / 128; int64 products and sums wrap like the
+ * reference's. out (N,) int64 is written whole. K % 128 != 0 or x / wT not 16-byte aligned (Mg, out 8-byte)
+ * return 2. Replaces the custom op exact::gemv and its kernel gemv_g128_v2
+ * (experiments/speed_fair_kaggle.py:656-702), called by TLinG for one row (:738). */
+int exact_gemv(const int16_t* x, const int8_t* wT, const int64_t* Mg, int64_t* out, int32_t N, int32_t K, void* stream);
+
 /* Exact group-128 GEMM for prefill (any R): same output as exact_gemv_g128. Up to 3 x 15 rows (A16) or
  * 3 x 16 rows (A8) run as row chunks of the GEMV kernel, more rows on the MFMA GEMM kernels (wide scales:
  * int8 x only there; int16 x with wide scales takes exact_gemm_g128_a16, else 2 is returned).

@@ -45,3 +45,6 @@ def test_host_side_validation_rejects_bad_shapes_without_launching():
     assert lib.exact_swiglu_qrow(fake, fake, fake, 7, fake, fake, fake, 1, 64, 0, None, fake, None) == 1   # digits of int8
     assert lib.exact_gemm_g128_digits(fake, fake, fake, None, None, fake, 4, 64, 128, 0, None) == 1    # no colterm
     assert lib.exact_logits_argmax(fake, fake, None, fake, None, 1, 64, 0, None) == 1            # no workspace
+    assert lib.exact_gemv(None, fake, fake, fake, 64, 128, None) == 1                            # exact::gemv: null x
+    assert lib.exact_gemv(fake, fake, fake, fake, 64, 200, None) == 2                            # K % 128
+    assert lib.exact_gemv(fake + 8, fake, fake, fake, 64, 128, None) == 2                        # x not 16-byte aligned

@@ -19,7 +19,9 @@ def test_fake_shapes():
     wp, mp = torch.empty(4 * 2 * 8192, dtype=torch.int8, **M), torch.empty(4 * 2 * 64, dtype=torch.int16, **M)
     t = E.gemm_g128(x16, 15, wp, mp, 200)
     assert t.shape == (5, 200) and t.dtype == torch.int64
-    assert E.gemv(torch.empty(256, dtype=torch.int16, **M), wp, torch.empty(2 * 300, dtype=torch.int64, **M)).shape == (300,)
+    y = E.gemv(torch.empty(256, dtype=torch.int16, **M), torch.empty((300, 256), dtype=torch.int8, **M),
+               torch.empty((300, 2), dtype=torch.int64, **M))
+    assert y.shape == (300,) and y.dtype == torch.int64
     xq, s = E.rmsnorm_qrow(torch.empty((3, 896), dtype=torch.int64, **M), torch.empty(896, dtype=torch.int64, **M), 7)
     assert xq.shape == (3, 896) and xq.dtype == torch.int8 and s.shape == (3,) and s.dtype == torch.int32
     hq, sh = E.swiglu_qrow(torch.empty((2, 2 * 1408), dtype=torch.int64, **M), torch.empty(2, dtype=torch.int32, **M),
