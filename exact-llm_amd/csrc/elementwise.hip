@@ -5,6 +5,8 @@
 #include "abi_util.h"
 #include "row_ops.h"
 
+#include <mutex>
+
 namespace exact {
 
 static const char* g_err = "";
@@ -496,6 +498,56 @@ extern "C" int exact_logits_argmax(int64_t* t, const int32_t* s, int64_t* lg, in
   hipLaunchKernelGGL(k_logits_part, dim3(np, R), dim3(256), 0, st, t, s, lg, part, N, np, clear_t);
   if (ids) hipLaunchKernelGGL(k_argmax_parts, dim3(R), dim3(64), 0, st, part, np, ids);
   return launch_status("logits_argmax");
+}
+
+// ---- exact_logits_argmax without a workspace argument ---------------------------------------------------------
+// The per-slice maxima live in `scratch`, a file-scope device array: each GPU the library runs on holds its own
+// copy (256 KiB) until the process ends. Host code never passes `scratch` itself to a kernel (on the host that
+// name is a stand-in, not a device address): the device address comes from hipGetSymbolAddress, looked up once
+// per device with that device current, on the entry point's first call there, and kept per device.
+#define LA_SCRATCH_ROWS 64
+#define LA_SCRATCH_N (1 << 20)
+#define LA_SCRATCH_WORDS (LA_SCRATCH_ROWS * (LA_SCRATCH_N / LSLICE) * 2)
+static __device__ __align__(256) int64_t scratch[LA_SCRATCH_WORDS];
+
+#define LA_MAX_DEVICES 64
+static std::mutex g_scratch_mu;
+static int64_t* g_scratch_dev[LA_MAX_DEVICES];
+
+static int scratch_for_current_device(int64_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("logits_argmax_noalloc: hipGetDevice", e);
+    return EXACT_E_LAUNCH;
+  }
+  if (dev < 0 || dev >= LA_MAX_DEVICES) return EXACT_E_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("logits_argmax_noalloc: hipGetSymbolAddress(scratch)", e != hipSuccess ? e : hipErrorInvalidSymbol);
+      return EXACT_E_LAUNCH;
+    }
+    g_scratch_dev[dev] = static_cast<int64_t*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return EXACT_OK;
+}
+
+extern "C" int exact_logits_argmax_noalloc(int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int32_t R, int32_t N,
+                                           int32_t clear_t, void* stream) {
+  if (!t || !s || R <= 0 || N <= 0 || (clear_t && lg == t)) return EXACT_E_ARG;
+  if (R > LA_SCRATCH_ROWS || N > LA_SCRATCH_N) return EXACT_E_UNSUPPORTED;
+  int64_t* part = nullptr;
+  const int e = scratch_for_current_device(&part);
+  if (e) return e;
+  const int np = (N + LSLICE - 1) / LSLICE;   // every (row, slice) entry read below is written first by this call
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(k_logits_part, dim3(np, R), dim3(256), 0, st, t, s, lg, part, N, np, clear_t);
+  if (ids) hipLaunchKernelGGL(k_argmax_parts, dim3(R), dim3(64), 0, st, part, np, ids);
+  return launch_status("logits_argmax_noalloc");
 }
 
 extern "C" int exact_advance(int32_t* pos, int32_t R, void* stream) {

@@ -46,6 +46,7 @@ SIGNATURES = {
     "exact_embed": [P, P, P, I32, I32, I32, P],
     "exact_embed_table": [P, P, P, I32, I32, P],
     "exact_logits_argmax": [P, P, P, P, P, I32, I32, I32, P],
+    "exact_logits_argmax_noalloc": [P, P, P, P, I32, I32, I32, P],
     "exact_advance": [P, I32, P],
     "exact_zero": [P, I64, P],
     "exact_sample": [P, I32, I32, U64, P, I64, P, P, P, P],

@@ -296,6 +296,16 @@ int exact_embed_table(const int8_t* wp, const int16_t* mp, int32_t* emb, int32_t
 int exact_logits_argmax(int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int64_t* part, int32_t R,
                         int32_t N, int32_t clear_t, void* stream);
 
+/* exact_logits_argmax with no workspace argument: it allocates nothing (no hipMalloc, hipFree or allocating
+ * library call). No counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid it). The per-slice maxima live in a
+ * library-owned device array of 256 KiB per GPU, held until the process ends, so R <= 64 and N <= 2^20
+ * (else 2 is returned, nothing launched). The device's array is looked up on the first call on each device,
+ * with the stream's device current: make that first call outside a graph capture. Every call on one GPU
+ * shares that GPU's array; calls that overlap on one GPU (different streams, or host threads) race. */
+int exact_logits_argmax_noalloc(int64_t* t, const int32_t* s, int64_t* lg, int32_t* ids, int32_t R, int32_t N,
+                                int32_t clear_t, void* stream);
+
 /* Integer sampler (sample_int, exact_llm.py:256-259) for R logits rows lg (R, V):
  * p = isoftmax_row(rs(lg * tnum, 16)) (Q20), target = (u20 * sum(p)) >> 20 with u20 = splitmix64(seed, step[r]) >> 44,
  * ids[r] = searchsorted(cumsum(p), target, 'right'). tnum = round(2^16 / temperature) (exact_llm.py:249).
