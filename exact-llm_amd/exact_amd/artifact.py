@@ -109,6 +109,8 @@ def load(path, verify=True):
         raise ExactError(f"artifact manifest unreadable: {e}") from None
     if man.get("spec") != SPEC_VERSION or man.get("format") != "Q16":
         raise ExactError(f"artifact spec {man.get('spec')!r} / format {man.get('format')!r} not supported")
+    if set(man.get("files", {})) != set(FILES):
+        raise ExactError(f"artifact manifest lists files {sorted(man.get('files', {}))}, expected {sorted(FILES)}")
     for fname, meta in man["files"].items():
         fp = os.path.join(path, fname)
         if not os.path.exists(fp) or os.path.getsize(fp) != meta["bytes"]:
@@ -120,11 +122,18 @@ def load(path, verify=True):
                       V=a["vocab"], NL=a["layers"], theta=a["rope_theta"], tie=a["tied_head"])
     maps, arrays, tables = {}, {}, {}
     for e in man["arrays"]:
+        if e["file"] not in FILES:      # only the size- and hash-checked files above, never another path
+            raise ExactError(f"array {e.get('name')!r} names file {e['file']!r} outside the artifact")
+        if e["dtype"] not in _DT:
+            raise ExactError(f"array {e.get('name')!r} has dtype {e['dtype']!r}")
         if e["file"] not in maps:
             maps[e["file"]] = np.memmap(os.path.join(path, e["file"]), dtype=np.uint8, mode="r")
         dt = np.dtype(e["dtype"])
         n = int(np.prod(e["shape"])) if e["shape"] else 1
-        raw = maps[e["file"]][e["offset"]:e["offset"] + n * dt.itemsize]
+        off = int(e["offset"])
+        if off < 0 or n < 0 or off + n * dt.itemsize > maps[e["file"]].size:
+            raise ExactError(f"array {e.get('name')!r} runs past the end of {e['file']}")
+        raw = maps[e["file"]][off:off + n * dt.itemsize]
         arr = raw.view(dt).reshape(e["shape"])
         (tables if e["file"] == "tables.int" else arrays)[e["name"]] = arr
     return cfg, man["linear_mode"], arrays, tables

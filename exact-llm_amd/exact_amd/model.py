@@ -11,6 +11,7 @@ sequences launches on the current stream, so a whole decode step can be captured
 """
 import collections
 import hashlib
+import operator
 
 import numpy as np
 import torch
@@ -180,6 +181,16 @@ class Cache:
                         torch.zeros((B, cfg.KV, Smax), dtype=I32, device=device),
                         torch.zeros((B, cfg.KV, Smax, cfg.hd), dtype=I64, device=device)) for _ in range(layers)]
         self.n = [0] * B
+
+
+def _check_slot(slot, cache):
+    """The kernels bound positions, not slots: a slot outside the cache would write keys and values outside it."""
+    try:
+        ok = 0 <= operator.index(slot) < cache.B
+    except TypeError:
+        ok = False
+    if not ok:
+        raise ExactError(f"slot {slot!r} is outside the cache's {cache.B} sequences")
 
 
 class Workspace:
@@ -428,6 +439,7 @@ class TModel:
         if cache is None:
             cache = self.new_cache(B=1)
             slot = 0
+        _check_slot(slot, cache)
         T = len(ids)
         p0 = cache.n[slot]
         if p0 + T > self.Smax:
@@ -437,7 +449,7 @@ class TModel:
         ws.ids.copy_(torch.tensor(ids, dtype=I32))
         ws.slot.fill_(slot)
         ws.pos.copy_(torch.arange(p0, p0 + T, dtype=I32))
-        # the matrix-core attention for prefill chunks of 32 rows or more (hd 128); the row kernel otherwise
+        # the matrix-core attention for prefill chunks of PREFILL_MIN_ROWS rows or more (hd 128); the row kernel otherwise
         ws.seq = (slot, p0 + T) if T >= self.PREFILL_MIN_ROWS and self.cfg.hd == 128 else None
         key = (T, id(cache), slot, p0)
         g = self._graphs.get(key) if graph else None
@@ -466,6 +478,7 @@ class TModel:
         if cache is None:
             cache = self.new_cache(B=1)
             slot = 0
+        _check_slot(slot, cache)
         T = len(ids)
         layout = TraceLayout(self.w, T)
         buf = torch.empty(layout.total, dtype=I64, device=self.dev)

@@ -91,3 +91,28 @@ def test_writer_rejects_non_integer_and_out_of_range(tmp_path):
     bad["emb"] = arr["emb"] * (1 << 30)
     with pytest.raises(ExactError, match="fit"):
         artifact.write(str(tmp_path / "b"), cfg, bad, tab)
+
+
+def test_manifest_that_points_elsewhere_is_rejected(tmp_path):
+    """The loader maps only the hash-checked files, with known dtypes and extents inside each file."""
+    import json
+    _write(tmp_path)
+    mp = os.path.join(str(tmp_path), "manifest.json")
+    good = json.load(open(mp))
+
+    def load_with(edit):
+        man = json.loads(json.dumps(good))
+        edit(man)
+        json.dump(man, open(mp, "w"))
+        return artifact.load(str(tmp_path), verify=False)
+
+    with pytest.raises(ExactError, match="lists files"):
+        load_with(lambda m: m["files"].pop("tables.int"))
+    with pytest.raises(ExactError, match="outside the artifact"):
+        load_with(lambda m: m["arrays"][0].update(file="../manifest.json"))
+    with pytest.raises(ExactError, match="dtype"):
+        load_with(lambda m: m["arrays"][0].update(dtype="<f8"))
+    with pytest.raises(ExactError, match="past the end"):
+        load_with(lambda m: m["arrays"][0].update(offset=good["files"][good["arrays"][0]["file"]]["bytes"]))
+    json.dump(good, open(mp, "w"))
+    artifact.load(str(tmp_path))

@@ -8,6 +8,7 @@ import torch
 import exact_oracle as O
 import helpers
 from exact_amd import synth
+from exact_amd._lib import ExactError
 from exact_amd.model import DeviceWeights, GraphDecoder, TModel
 
 pytestmark = pytest.mark.gpu
@@ -72,18 +73,20 @@ def test_synthetic_prefill_and_decode_match_oracle(name):
 
 
 def test_chunked_prefill_on_matrix_core_attention_matches_oracle():
-    """hd 128: prompt chunks of 32 rows or more take the matrix-core attention (exact_attention_prefill), here a
-    75-token prompt as one chunk and as chunks of 40 + 35 continuing the cache, then greedy decode steps."""
+    """hd 128: prompt chunks of TModel.PREFILL_MIN_ROWS (96) rows or more take the matrix-core attention
+    (exact_attention_prefill), here a 200-token prompt as one chunk and as chunks of 100 + 100, the second
+    continuing the cache (start position 100), then greedy decode steps."""
     cfg = synth.CONFIGS["tiny-hd128"]
     seed = 4
-    om = helpers.oracle_model(cfg, seed, T=96)
-    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=96)
-    ids = helpers.prompt(17, 75, cfg.V)
+    assert TModel.PREFILL_MIN_ROWS <= 100
+    om = helpers.oracle_model(cfg, seed, T=224)
+    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=224)
+    ids = helpers.prompt(17, 200, cfg.V)
     want = om(ids)
     assert np.array_equal(host(tm.forward(ids)), want)
     cache = tm.new_cache(B=1)
-    lg1 = host(tm.forward(ids[:40], cache))
-    lg2 = host(tm.forward(ids[40:], cache))
+    lg1 = host(tm.forward(ids[:100], cache))
+    lg2 = host(tm.forward(ids[100:], cache))
     assert np.array_equal(np.concatenate([lg1, lg2]), want)
     otoks, orows = O.greedy_decode(om, ids, 4)
     tok = int(lg2[-1].argmax())
@@ -120,15 +123,16 @@ def test_batch_decode_and_graph_replay_match_eager():
             assert int(steps[i][1][b]) == otoks[i + 1]
 
 
-@pytest.mark.parametrize("name,T", [("tiny", 12), ("tiny-hd128", 40)])
+@pytest.mark.parametrize("name,T", [("tiny", 12), ("tiny-hd128", 40), ("tiny-hd128", 100)])
 def test_graph_prefill_replays_match_oracle(name, T):
     """Prefill captured as a HIP graph (forward(graph=True)): the first call runs eagerly and captures, later calls of
     the same length, slot and start position replay it with new prompts; every replay equals the oracle, with eager
-    passes and host synchronisations in between, and a second chunk continues the cache."""
+    passes and host synchronisations in between, and a second chunk continues the cache. At hd 128 and 100 rows
+    both chunks run the matrix-core attention inside the captured graph; at 40 rows the row kernel."""
     cfg = synth.CONFIGS[name]
     seed = 8
-    om = helpers.oracle_model(cfg, seed, T=128)
-    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=128, batch=2)
+    om = helpers.oracle_model(cfg, seed, T=256)
+    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=256, batch=2)
     cache = tm.new_cache()
     for rep in range(4):
         ids = helpers.prompt(100 + rep, T, cfg.V)
@@ -143,3 +147,17 @@ def test_graph_prefill_replays_match_oracle(name, T):
         cache.n[0] = 0
         assert np.array_equal(host(tm.forward(other, cache, slot=0)), om(other))
     assert len(tm._graphs) == 2
+
+
+def test_slot_outside_the_cache_is_rejected_before_any_launch():
+    cfg = synth.CONFIGS["tiny"]
+    tm = TModel(DeviceWeights.synthetic(cfg, 2, DEV), Smax=32, batch=2)
+    cache = tm.new_cache()
+    before = [host(t).copy() for t in cache.layers[0]]
+    for bad in (-1, 2, 1.0):
+        with pytest.raises(ExactError, match="outside the cache"):
+            tm.forward([1, 2, 3], cache, slot=bad)
+        with pytest.raises(ExactError, match="outside the cache"):
+            tm.forward_traced([1, 2, 3], cache, slot=bad)
+    assert all(np.array_equal(host(t), b) for t, b in zip(cache.layers[0], before))
+    assert cache.n == [0, 0]

@@ -10,6 +10,7 @@ import exact_oracle as O
 import helpers
 from exact_amd import synth
 from exact_amd import trace as TR
+import trace_verifier as TV
 from exact_amd.model import DeviceWeights, GraphDecoder, TModel
 
 pytestmark = pytest.mark.gpu
@@ -73,15 +74,15 @@ def test_freivalds_verifies_the_gpu_trace_and_rejects_tampers():
     rng = np.random.default_rng(2026)
     lins = {f"L{i}.{n}": L[n] for i, L in enumerate(base.w["layers"]) for n in NAMES}
     lins["head"] = base.w["head"]
-    keys = {n: TR.freivalds_keys(L.w, L.M, rng) for n, L in lins.items()}
+    keys = {n: TV.freivalds_keys(L.w, L.M, rng) for n, L in lins.items()}
     for n in lins:
-        assert TR.freivalds_check(keys[n], rec[n][0], tr[n]), n
+        assert TV.freivalds_check(keys[n], rec[n][0], tr[n]), n
     names = sorted(lins)
     for i in range(20):
         n = names[rng.integers(len(names))]
         bad = tr[n].copy()
         bad[rng.integers(bad.shape[0]), rng.integers(bad.shape[1])] += 1 if i % 2 else -1
-        assert not TR.freivalds_check(keys[n], rec[n][0], bad), n
+        assert not TV.freivalds_check(keys[n], rec[n][0], bad), n
 
 
 def test_graph_decode_trace_commitment_and_logits():

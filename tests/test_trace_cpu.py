@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 from exact_amd import trace as TR
+import trace_verifier as TV
 from exact_amd.ops import ExactError
 
 
@@ -43,12 +44,12 @@ def test_freivalds_keys_are_w_prime_times_r_mod_p():
     K, N = 256, 40
     w = rng.integers(-127, 128, (K, N)).astype(np.int8)
     M = rng.integers(1, 1 << 15, (K // 128, N))
-    keys = TR.freivalds_keys(w, M, np.random.default_rng(1), chunk=16)
+    keys = TV.freivalds_keys(w, M, np.random.default_rng(1), chunk=16)
     for p, r, d in keys:
         for k in (0, 1, 127, 128, 255):
             want = sum(int(w[k, n]) * int(M[k // 128, n]) * int(r[n]) for n in range(N)) % p
             assert int(d[k]) == want
-    ck = TR.freivalds_keys(w, None, np.random.default_rng(1))
+    ck = TV.freivalds_keys(w, None, np.random.default_rng(1))
     for p, r, d in ck:
         assert int(d[3]) == sum(int(w[3, n]) * int(r[n]) for n in range(N)) % p
 
@@ -60,16 +61,16 @@ def test_freivalds_accepts_exact_totals_and_rejects_any_single_change():
     M = rng.integers(8192, 24576, (K // 128, N))
     xq = rng.integers(-32767, 32768, (R, K))
     t = _exact_t(xq, w, M).astype(np.int64)
-    keys = TR.freivalds_keys(w, M, np.random.default_rng(2))
-    assert TR.freivalds_check(keys, xq, t)
+    keys = TV.freivalds_keys(w, M, np.random.default_rng(2))
+    assert TV.freivalds_check(keys, xq, t)
     for i in range(20):
         bad = t.copy()
         bad[rng.integers(R), rng.integers(N)] += 1 if i % 2 else -1
-        assert not TR.freivalds_check(keys, xq, bad)
+        assert not TV.freivalds_check(keys, xq, bad)
     bx = xq.copy()
     bx[1, 200] += 1
-    assert not TR.freivalds_check(keys, bx, t)
-    assert not TR.freivalds_check(keys, xq, t[:, :-1])
+    assert not TV.freivalds_check(keys, bx, t)
+    assert not TV.freivalds_check(keys, xq, t[:, :-1])
 
 
 def test_layout_offsets_and_reference_names():
