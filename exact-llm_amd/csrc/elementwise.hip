@@ -93,7 +93,9 @@ __global__ __launch_bounds__(1024) void k_rmsnorm_qrow(int64_t* __restrict__ x, 
                                                        const int32_t* __restrict__ res_s, const int64_t* __restrict__ g,
                                                        int bits, void* xq, int32_t* s, int D, int clear_t, int8_t* x8) {
   __shared__ RowScratch sc;
-  rmsnorm_qrow_row<EPT>(blockIdx.x, x, res_t, res_s, g, bits, xq, s, D, clear_t, sc, x8);
+  // one block per row: x is updated in place and the residual row cleared (each thread writes only what it read)
+  norm_qrow_row<EPT>(blockIdx.x, blockDim.x, x, res_t, res_s, g, bits, D, nullptr, res_t ? x : nullptr,
+                     (res_t && clear_t) ? res_t : nullptr, s, xq, x8, sc);
 }
 
 // Rows too long for one workgroup are split into slices of QSLICE elements; the producer kernel writes

@@ -15,6 +15,7 @@
 // out[n] = sum_g (sum_{k in g} x[k] * wT[n,k]) * Mg[n,g] for one int16 row.
 #include "exact_common.h"
 #include "abi_util.h"
+#include "row_ops.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -162,17 +163,17 @@ __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t*
   for (int q = 0; q < 4; ++q)
 #pragma unroll
     for (int v = 0; v < VR; ++v) acc[q][v] = 0;
-  if (g0 >= g1) {
-    pro();
-    return;
-  }
   GroupRegs ra, rb;
   if constexpr (__is_same(Pro, NoPrologue)) {
+    if (g0 >= g1) return;
     load_group<ABITS, NT, WIDE>(ra, wp, mp, mh, xrow, valid, tile_index(nb, g0, nbs, G), g0, row, c);
-  } else {   // the first tile in flight while the prologue runs
-    load_scales<WIDE>(ra, mp, mh, tile_index(nb, g0, nbs, G), row);
-    load_tile<NT>(ra, wp, tile_index(nb, g0, nbs, G), row, c);
+  } else {   // the first tile in flight while the prologue runs (one call site: the prologue may be long)
+    if (g0 < g1) {
+      load_scales<WIDE>(ra, mp, mh, tile_index(nb, g0, nbs, G), row);
+      load_tile<NT>(ra, wp, tile_index(nb, g0, nbs, G), row, c);
+    }
     pro();
+    if (g0 >= g1) return;
     load_x<ABITS>(ra, xrow, valid, g0, c);
   }
   int g = g0;
@@ -295,6 +296,54 @@ __global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict_
   int64_t acc[4][VR];
   gemv_groups<ABITS, NT, VR, decltype(quantise), false, WIDE>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c,
                                                               lane, quantise);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = nb * 64 + 16 * q + row;
+#pragma unroll
+    for (int v = 0; v < VR; ++v) {
+      const int r = 4 * c + v;
+      if (r < R && n < N) atomicAdd(reinterpret_cast<unsigned long long*>(t + (size_t)r * N + n), (unsigned long long)acc[q][v]);
+    }
+  }
+}
+
+// GEMV whose int16 input rows are normalised in its own prologue (decode): every block recomputes, for each of its R
+// rows, x = x_in + rs(res_t, 28 - res_s) (res_t optional) and qrow(irms(x, g), 15) over the whole row (three block
+// reductions, exact_llm.py:41-46, 100-106) into LDS while each wave's first weight tile is in flight, then runs the
+// group loop on the LDS row. Block 0 writes x to x_out (another buffer: the other blocks are still reading x_in), the
+// row shifts to s_out and, when xq_out is given, the quantised rows. t += x.W (accumulate). Replaces an
+// exact_rmsnorm_qrow launch + exact_gemv_g128_acc.
+template <bool NT, int VR, int EPT, bool WIDE>
+__global__ __launch_bounds__(256) void k_gemv_g128_norm(const int64_t* __restrict__ x_in, int64_t* __restrict__ x_out,
+                                                        const int64_t* __restrict__ res_t, const int32_t* __restrict__ res_s,
+                                                        const int64_t* __restrict__ gain, const int8_t* __restrict__ wp,
+                                                        const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
+                                                        int64_t* __restrict__ t, int32_t* __restrict__ s_out,
+                                                        int16_t* __restrict__ xq_out, int R, int N, int K, int G, int nsplit) {
+  extern __shared__ __attribute__((aligned(16))) int8_t xlds[];   // R rows of K quantised int16 values
+  __shared__ RowScratch sc;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int task = blockIdx.x * 4 + wave;
+  const int nbs = (N + 63) >> 6;
+  const bool writer = blockIdx.x == 0;
+  int16_t* xl = reinterpret_cast<int16_t*>(xlds);
+  auto norm = [&]() {   // block-wide: every wave of the block runs it, with or without a task
+    for (int r = 0; r < R; ++r)
+      norm_qrow_row<EPT>(r, 256, x_in, res_t, res_s, gain, 15, K, xl + (size_t)r * K, writer ? x_out : nullptr, nullptr,
+                         writer ? s_out : nullptr, writer ? xq_out : nullptr, nullptr, sc);
+    __syncthreads();
+  };
+  // waves without a task run the prologue (its barriers need every wave of the block) through the same call
+  const bool has = task < nbs * nsplit;
+  const int nb = has ? task / nsplit : 0, sp = has ? task - nb * nsplit : 0;
+  const int g0 = has ? (int)(((int64_t)sp * G) / nsplit) : 0;
+  const int g1 = has ? (int)(((int64_t)(sp + 1) * G) / nsplit) : 0;
+  const int row = lane & 15, c = lane >> 4;
+  const int8_t* xrow = reinterpret_cast<const int8_t*>(xl + (size_t)(row < R ? row : 0) * K);
+  int64_t acc[4][VR];
+  gemv_groups<15, NT, VR, decltype(norm), false, WIDE>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane,
+                                                       norm);
+  if (!has) return;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int n = nb * 64 + 16 * q + row;
@@ -626,6 +675,49 @@ extern "C" int exact_gemv(const int16_t* x, const int8_t* wT, const int64_t* Mg,
   hipLaunchKernelGGL((k_gemv_rows<GEMV_NT != 0>), dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0, st, x, wT, Mg, out, N, K,
                      G, nsplit, nsplit > 1 ? 1 : 0);
   return launch_status("gemv");
+}
+
+// rows of one norm-fused GEMV launch (each block runs the row program once per row) and the row width its 256 threads
+// hold in registers (24 values each)
+#define GEMV_NORM_ROWS 2
+#define GEMV_NORM_KMAX (256 * 24)
+
+extern "C" int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, const int64_t* res_t, const int32_t* res_s,
+                                        const int64_t* g, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                                        int64_t* t, int32_t* s_out, int16_t* xq_out, int32_t R, int32_t N, int32_t K,
+                                        void* stream) {
+  if (!x_in || !g || !wp || !mp || !t || R <= 0 || N <= 0 || K <= 0 || (res_t && !res_s)) return EXACT_E_ARG;
+  if (x_out && (x_out == x_in || x_out == res_t)) return EXACT_E_ARG;   // the other blocks still read x_in / res_t
+  if (K % 128 || K > GEMV_NORM_KMAX || R > GEMV_NORM_ROWS) return EXACT_E_UNSUPPORTED;
+  if (reinterpret_cast<uintptr_t>(wp) & 15) return EXACT_E_UNSUPPORTED;
+  const int G = K / 128;
+  const int nsplit = gemv_nsplit(N, G, R, 15);
+  const int64_t tasks = (int64_t)((N + 63) / 64) * nsplit;
+  const size_t lds = (size_t)R * K * 2;
+  dim3 grid((unsigned)((tasks + 3) / 4)), block(256);
+  hipStream_t st = as_stream(stream);
+  const int ept = (K + 255) / 256;
+#define NORM_GO(VR, E)                                                                                                  \
+  do {                                                                                                                  \
+    if (mh)                                                                                                             \
+      hipLaunchKernelGGL((k_gemv_g128_norm<GEMV_NT != 0, VR, E, true>), grid, block, lds, st, x_in, x_out, res_t, res_s, g, \
+                         wp, mp, mh, t, s_out, xq_out, R, N, K, G, nsplit);                                             \
+    else                                                                                                                \
+      hipLaunchKernelGGL((k_gemv_g128_norm<GEMV_NT != 0, VR, E, false>), grid, block, lds, st, x_in, x_out, res_t, res_s,  \
+                         g, wp, mp, mh, t, s_out, xq_out, R, N, K, G, nsplit);                                          \
+  } while (0)
+#define NORM_EPT(VR)                                                                                                    \
+  do {                                                                                                                  \
+    if (ept <= 4) NORM_GO(VR, 4);                                                                                       \
+    else if (ept <= 8) NORM_GO(VR, 8);                                                                                  \
+    else if (ept <= 14) NORM_GO(VR, 14);                                                                                \
+    else if (ept <= 20) NORM_GO(VR, 20);                                                                                \
+    else NORM_GO(VR, 24);                                                                                               \
+  } while (0)
+  if (R == 1) NORM_EPT(1); else NORM_EPT(2);
+#undef NORM_EPT
+#undef NORM_GO
+  return launch_status("gemv_g128_norm_acc");
 }
 
 // LDS of the quantised slices: 4 waves x R rows x gmax groups x 128 values

@@ -23,81 +23,153 @@ struct RowScratch {
   int64_t b[16];
 };
 
-// Row r of: if res_t, x += round_shift(res_t, 28 - res_s[r]) (written back; res_t zeroed when clear_t);
-// then xq, s = qrow(irms(x, g), bits) (exact_llm.py:41-46, 100-106); x8 (optional): xq's digit rows too. The block's threads hold EPT
-// elements each (blockDim.x * EPT >= D); every load of the row is issued before the first use.
+// numpy floor division a // b for any int64 a and b != 0, kept out of line: the lean row program below calls it
+// only when its quotient estimate leaves the range it is exact in.
+static __device__ __attribute__((noinline)) int64_t floordiv_general(int64_t a, int64_t b) {
+  return b > 0 ? floordiv_pos(a, b) : floordiv64(a, b);
+}
+
+// Round-half-up arithmetic shift right by a block-uniform 1 <= n <= 63, with int64 wrap (= shr64 there).
+__device__ __forceinline__ int64_t rsh_pos(int64_t a, int n) {
+  return (int64_t)((uint64_t)a + (1ULL << (n - 1))) >> n;
+}
+
+// bit length of max |v| over values whose largest is vmax and smallest vmin (vmin <= 0 <= vmax)
+__device__ __forceinline__ int bitlen_maxabs(int64_t vmax, int64_t vmin) {
+  const int64_t a = abs64(vmin);
+  return bitlen64(a > vmax ? a : vmax);
+}
+
+// Row r of: x = x_in (+ round_shift(res_t, 28 - res_s[r]) when res_t), then xq, s = qrow(irms(x, g), bits)
+// (exact_llm.py:41-46, 100-106). Outputs, each optional: x_out (x; may be x_in itself when one block owns the row),
+// clear (res_t's row zeroed, likewise), xl (row r's quantised values, int16, LDS or global), xq_out (the quantised
+// row, int16 when bits > 7 else int8), x8 (xq's interleaved digit rows) and s_out. The nt threads of the block hold
+// EPT elements each (element i in thread i % nt). A consumer GEMV runs this in every block, so it is written lean,
+// from bounds the program itself fixes:
+//   k = max(bitlen(max |x|) - 24, 0) leaves |shr(x, k)| <= 2^24, so the squares are int32 products;
+//   den = isqrt(sum / D + 1) << k is within a factor sqrt(D) of every |x|, so y = floor((x << 16) / den) (also
+//   for a wrapped x << 16) has |y| < 2^24: a float64 quotient estimate is off by at most one and one exact int64
+//   remainder test each way corrects it (the general floor division runs when an estimate leaves that range, or
+//   den is outside (0, 2^62]);
+//   the shifts k, 16, 28 - res_s and the qrow shift are uniform over the block, so their branches are too; loads
+//   use clamped indices and mask the values past D, so only the stores are guarded.
 template <int EPT>
-__device__ __forceinline__ void rmsnorm_qrow_row(int r, int64_t* __restrict__ x, int64_t* __restrict__ res_t,
-                                                 const int32_t* __restrict__ res_s, const int64_t* __restrict__ g,
-                                                 int bits, void* xq, int32_t* s, int D, int clear_t, RowScratch& sc,
-                                                 int8_t* x8 = nullptr) {
-  const int tid = threadIdx.x, nt = blockDim.x;
-  int64_t* xr = x + (int64_t)r * D;
-  int64_t* tr = res_t ? res_t + (int64_t)r * D : nullptr;
-  int64_t v[EPT], gv[EPT], rv[EPT];
+__device__ __forceinline__ void norm_qrow_row(int r, int nt, const int64_t* x_in, const int64_t* res_t,
+                                              const int32_t* __restrict__ res_s, const int64_t* __restrict__ g, int bits,
+                                              int D, int16_t* xl, int64_t* x_out, int64_t* clear, int32_t* __restrict__ s_out,
+                                              void* xq_out, int8_t* x8, RowScratch& sc) {
+  const int tid = threadIdx.x;
+  const int64_t* xr = x_in + (int64_t)r * D;
+  const int64_t* tr = res_t ? res_t + (int64_t)r * D : nullptr;
+  int64_t v[EPT], gv[EPT];
+  {
+    int64_t rv[EPT];
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int i = tid + j * nt;
-    v[j] = 0; gv[j] = 0; rv[j] = 0;
-    if (i < D) {
+    for (int j = 0; j < EPT; ++j) {
+      const int i = tid + j * nt < D ? tid + j * nt : D - 1;
       v[j] = xr[i];
       gv[j] = g[i];
-      if (tr) rv[j] = tr[i];
+      rv[j] = tr ? tr[i] : 0;
     }
-  }
-  int m = 0;   // max bit length of |x|
-  const int sh = tr ? 28 - res_s[r] : 0;
+    if (tr) {
+      const int sh = 28 - res_s[r];
+      if (sh > 0) {
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int i = tid + j * nt;
-    if (i < D) {
-      if (tr) {
-        v[j] = (int64_t)((uint64_t)v[j] + (uint64_t)shr64(rv[j], sh));
-        xr[i] = v[j];
-        if (clear_t) tr[i] = 0;
+        for (int j = 0; j < EPT; ++j) v[j] = (int64_t)((uint64_t)v[j] + (uint64_t)rsh_pos(rv[j], sh));
+      } else {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) v[j] = (int64_t)((uint64_t)v[j] + (uint64_t)shl64(rv[j], -sh));
       }
-      const int bl = bitlen64(abs64(v[j]));
-      m = bl > m ? bl : m;
+    }
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const bool in = tid + j * nt < D;
+      v[j] = in ? v[j] : 0;
+      gv[j] = in ? gv[j] : 0;
     }
   }
-  m = block_max_i32(m, sc.a);
-  int k = m - 24;
-  if (k < 0) k = 0;
-  int64_t ss = 0;
+  if (x_out || clear) {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int i = tid + j * nt;
+      if (i < D) {
+        if (x_out) x_out[(int64_t)r * D + i] = v[j];
+        if (clear) clear[(int64_t)r * D + i] = 0;
+      }
+    }
+  }
+  int64_t hi = 0, lo = 0;
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
-    const int64_t xs = shr64(v[j], k);   // elements past D hold 0
-    ss = (int64_t)((uint64_t)ss + (uint64_t)(xs * xs));
+    hi = v[j] > hi ? v[j] : hi;
+    lo = v[j] < lo ? v[j] : lo;
+  }
+  const int m = block_max_i32(bitlen_maxabs(hi, lo), sc.a);   // bit length of max |x|
+  const int k = m > 24 ? m - 24 : 0;
+  int64_t ss = 0;
+  if (k == 0) {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) ss += (int64_t)(int)v[j] * (int)v[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int xs = (int)rsh_pos(v[j], k);   // |xs| <= 2^24
+      ss += (int64_t)xs * xs;
+    }
   }
   ss = block_sum64_1(ss, sc.b);
-  const int64_t ms = floordiv_pos(ss, D) + 1;   // ss >= 0 (a sum of squares; wraps only past 2^63, as numpy)
+  const int64_t ms = floordiv_pos(ss, D) + 1;
   int64_t rt = isqrt64(ms);
   if (rt < 1) rt = 1;
   const int64_t den = shl64(rt, k);
+  const bool fast = den > 0 && den <= (1LL << 62);
   const double rden = 1.0 / (double)den;
-  int m2 = 0;
+  int yq[EPT];
+  bool bad = !fast;
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
-    v[j] = shr64(floordiv_rcp(shl64(v[j], EXACT_F), den, rden) * gv[j], EXACT_F);
-    const int bl = bitlen64(abs64(v[j]));
-    m2 = (tid + j * nt < D && bl > m2) ? bl : m2;
+    const int64_t a = shl64(v[j], EXACT_F);
+    const double qd = __builtin_floor((double)a * rden);
+    bad |= !(__builtin_fabs(qd) < 1073741824.0);
+    int q = (int)qd;
+    const int64_t rem = (int64_t)((uint64_t)a - (uint64_t)(int64_t)q * (uint64_t)den);
+    q += (rem >= den ? 1 : 0) - (rem < 0 ? 1 : 0);
+    yq[j] = q;
   }
-  m2 = block_max_i32(m2, sc.c);
-  int q = m2 - bits;
-  if (q < 0) q = 0;
+  int64_t z[EPT];
+  if (!bad) {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) z[j] = rsh_pos((int64_t)((uint64_t)(int64_t)yq[j] * (uint64_t)gv[j]), EXACT_F);
+  } else {   // not reached at the model shapes; exact for any int64
+#pragma unroll
+    for (int j = 0; j < EPT; ++j)
+      z[j] = rsh_pos((int64_t)((uint64_t)floordiv_general(shl64(v[j], EXACT_F), den) * (uint64_t)gv[j]), EXACT_F);
+  }
+  hi = 0;
+  lo = 0;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {   // gains past D are 0, so z is 0 there
+    hi = z[j] > hi ? z[j] : hi;
+    lo = z[j] < lo ? z[j] : lo;
+  }
+  const int m2 = block_max_i32(bitlen_maxabs(hi, lo), sc.c);
+  const int q = m2 > bits ? m2 - bits : 0;
   const int64_t lim = (1LL << bits) - 1;
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
+    int64_t w = q ? rsh_pos(z[j], q) : z[j];
+    w = w > lim ? lim : (w < -lim ? -lim : w);
     const int i = tid + j * nt;
     if (i < D) {
-      int64_t w = shr64(v[j], q);
-      w = w > lim ? lim : (w < -lim ? -lim : w);
-      if (bits <= 7) store_q<int8_t>(xq, (int64_t)r * D + i, w);
-      else store_q<int16_t>(xq, (int64_t)r * D + i, w);
+      if (xl) xl[i] = (int16_t)w;
+      if (xq_out) {
+        if (bits <= 7) store_q<int8_t>(xq_out, (int64_t)r * D + i, w);
+        else store_q<int16_t>(xq_out, (int64_t)r * D + i, w);
+      }
       if (x8) store_digits(x8, r, D, i, w);
     }
   }
-  if (tid == 0) s[r] = q;
+  if (tid == 0 && s_out) s_out[r] = q;
 }
 
 }  // namespace exact

@@ -203,10 +203,14 @@ class Workspace:
         adt = I16 if abits == 15 else I8
         self.R = R
         self.x, self.xq, self.s = z(R, D), z(R, D, dt=adt), z(R, dt=I32)
-        self.t_qkv, self.qq, self.sq = z(R, nq), z(R, H, hd, dt=I16), z(R, H, dt=I32)
+        # the q|k|v and down totals in one allocation: a decode pass clears both with one range (the o projection's
+        # zero argument) after the norm-fused q|k|v GEMV has read the down totals as its residual
+        self.t_qd = z(R * nq + R * D)
+        self.t_qkv, self.qq, self.sq = self.t_qd[:R * nq].view(R, nq), z(R, H, hd, dt=I16), z(R, H, dt=I32)
+        self.x2 = z(R, D)   # the other residual buffer of decode passes (the norm-fused GEMVs read one, write the other)
         self.att, self.aq, self.sa = z(R, H * hd), z(R, H * hd, dt=adt), z(R, dt=I32)
         self.t_o, self.t_gu, self.hq, self.sh = z(R, D), z(R, 2 * I), z(R, I, dt=adt), z(R, dt=I32)
-        self.t_d, self.t_head = z(R, D), z(R, V)
+        self.t_d, self.t_head = self.t_qd[R * nq:].view(R, D), z(R, V)
         self.logits, self.next_ids = z(R, V), z(R, dt=I32)
         self.s28 = torch.full((R,), 28, dtype=I32, device=device)
         self.part_sw = ops.swiglu_parts(R, max(I, cfg.SI if cfg.moe else 0), device)
@@ -261,6 +265,9 @@ class TModel:
 
     PREFILL_MIN_ROWS = 96   # rows from which prefill attention runs on the matrix cores (the row kernel is faster below)
     QROW_FUSE_ROWS = 2
+    # widest rows whose norm runs inside the consuming GEMVs (every block repeats the row's three reductions; at
+    # 3584-wide rows that costs as much as the separate launch it saves, at 5120 more, at 896 less: 7.0 vs 8.2 us)
+    NORM_FUSE_D = 2048
     EXPERT_GEMM_MIN_PAIRS = 64   # (row, expert) pairs from which the MoE experts run as one grouped GEMM
 
     def _prefill_ws(self, R):
@@ -312,8 +319,13 @@ class TModel:
         # launch at 8 rows
         xfuse = group and R <= self.QROW_FUSE_ROWS
         afuse = xfuse and ws.seq is None and (R == 1 or independent)
-        if xfuse and ws.h is None and c.I > 8192 and not c.moe:
+        # decode rows of dense int16 models: residual + RMSNorm + qrow run inside the GEMVs that consume them (q|k|v,
+        # gate|up, head), which read one residual buffer and write the other
+        nfuse = (afuse and self.abits == 15 and not c.moe and R <= ops.NORM_FUSE_ROWS and D <= self.NORM_FUSE_D
+                 and self.w.head.mode == "group")
+        if xfuse and ws.h is None and (c.I > 8192 or nfuse) and not c.moe:
             ws.h = torch.zeros((R, ws.I), dtype=I64, device=self.dev)
+        x_cur, x_nxt = ws.x, ws.x2
         ops.embed(ws.ids, self.w.emb, ws.x)
         dx = da = dh = None
         if group and ws.dig is not None:
@@ -322,12 +334,21 @@ class TModel:
         res_t, res_s = None, None
         for li, L in enumerate(self.w.layers):
             cache = self._cache.layers[li]
-            ops.rmsnorm_qrow(ws.x, L["g1"], self.abits, res_t, res_s, ws.xq, ws.s, clear=clear, x8=dx)
             if keep:
                 t_qkv, t_o, t_gu, t_d = (slot(f"L{li}.{k}") for k in ("qkv", "o", "gateup", "down"))
             else:
                 t_qkv, t_o, t_gu, t_d = ws.t_qkv, ws.t_o, ws.t_gu, ws.t_d
-            if group:
+            if nfuse:
+                ops.gemv_norm_acc(x_cur, res_t, res_s, L["g1"], L["qkv"], t_qkv, ws.s,
+                                  x_out=x_nxt if res_t is not None else None)
+                if res_t is not None:
+                    x_cur, x_nxt = x_nxt, x_cur
+                s_qkv, b_qkv = ws.s, L["qkv"].bias
+            else:
+                ops.rmsnorm_qrow(ws.x, L["g1"], self.abits, res_t, res_s, ws.xq, ws.s, clear=clear, x8=dx)
+            if nfuse:
+                pass
+            elif group:
                 self._lin(ws.xq, L["qkv"], t_qkv, x8=dx)
                 s_qkv, b_qkv = ws.s, L["qkv"].bias
             else:
@@ -349,11 +370,21 @@ class TModel:
                                           tab.inv, self._prefill_ws(R), ws.obits)
                 else:
                     ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv, ws.obits)
-            if xfuse:
+            if nfuse:   # also clears the down totals the q|k|v GEMV read as its residual (t_qkv and t_d are one range)
+                ops.gemv_qrow_acc(ws.att, ws.obits, H, self.abits, L["o"], t_o, ws.sa, zero=ws.t_qd if clear else None)
+            elif xfuse:
                 ops.gemv_qrow_acc(ws.att, ws.obits, H, self.abits, L["o"], t_o, ws.sa,
                                   zero=t_qkv if afuse and clear else None)   # the q|k|v totals attention left
             else:
                 ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa, x8=da)
+            if nfuse:
+                ops.gemv_norm_acc(x_cur, t_o, ws.sa, L["g2"], L["gateup"], t_gu, ws.s, x_out=x_nxt)
+                x_cur, x_nxt = x_nxt, x_cur
+                ops.swiglu_part(t_gu, ws.s, tab.silu, ws.h, ws.part_sw, clear=clear)
+                ops.gemv_qrow_acc(ws.h, ws.part_sw, -(-c.I // ops.QSLICE), self.abits, L["down"], t_d, ws.sh,
+                                  zero=t_o if clear else None)   # the o totals the gate|up GEMV read
+                res_t, res_s = t_d, ws.sh
+                continue
             if group:
                 if not xfuse:
                     self._lin(ws.aq, L["o"], t_o, x8=da)
@@ -386,8 +417,14 @@ class TModel:
                 ops.swiglu_qrow(ws.t_gu, ws.s28, tab.silu, self.abits, ws.hq, ws.sh, part=ws.part_sw)
                 self._lin_channel(ws.hq, ws.sh, L["down"], ws.t_d)
                 res_t, res_s = ws.t_d, ws.s28
-        ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=clear, x8=dx)
         head = self.w.head
+        if nfuse:
+            t_head = slot("head") if keep else ws.t_head
+            ops.gemv_norm_acc(x_cur, res_t, res_s, self.w.gf, head, t_head, ws.s)
+            ops.logits_argmax(t_head, ws.s, ws.logits if want_logits else None, ws.next_ids, clear=clear,
+                              part=ws.part_lg)
+            return ws
+        ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=clear, x8=dx)
         if head.mode == "group":
             t_head = slot("head") if keep else ws.t_head
             self._lin(ws.xq, head, t_head, x8=dx)

@@ -144,6 +144,34 @@ def gemv_qrow_acc(xs, part, nparts, abits, lin, out, s_out, K=None, zero=None):
     return out
 
 
+NORM_FUSE_ROWS = 2        # rows of one exact_gemv_g128_norm_acc launch
+NORM_FUSE_KMAX = 256 * 24
+
+
+def gemv_norm_acc(x_in, res_t, res_s, g, lin, out, s_out, x_out=None, xq_out=None):
+    """out (R, N) += qrow(irms(x, g), 15) . W in one launch, with x = x_in + rs(res_t, 28 - res_s) (res_t may be None):
+    every block normalises the rows itself; block 0 writes x to x_out (not x_in: the other blocks still read it), the
+    row shifts to s_out and, when given, the int16 rows to xq_out."""
+    R, K = x_in.shape
+    if K != lin.K:
+        raise ExactError(f"gemv_norm_acc: x has K = {K}, linear has K = {lin.K}")
+    _need_packed(lin, "gemv_norm_acc")
+    _need(x_in, I64, "x_in")
+    _need(g, I64, "g", K)
+    _need(out, I64, "out", R * lin.N)
+    _need(s_out, I32, "s_out", R)
+    if res_t is not None:
+        _need(res_t, I64, "res_t", R * K)
+        _need(res_s, I32, "res_s", R)
+    if x_out is not None:
+        _need(x_out, I64, "x_out", R * K)
+    if xq_out is not None:
+        _need(xq_out, I16, "xq_out", R * K)
+    _lib.call("exact_gemv_g128_norm_acc", _ptr(x_in), _ptr(x_out), _ptr(res_t), _ptr(res_s), _ptr(g), _ptr(lin.wp),
+              _ptr(lin.mp), _ptr(lin.mh), _ptr(out), _ptr(s_out), _ptr(xq_out), R, lin.N, K, _stream())
+    return out
+
+
 GEMV_CHUNK_ROWS = {15: 15, 7: 48}   # int8 rows: up to 3 GEMV row chunks in exact_gemm_g128; int16 rows above 15 take
                                     # exact_gemm_g128_a16 (GEMV chunks of 16 with colterm up to 48 rows, digit rows beyond)
 _DIGIT_ROWS = {}                     # device -> int8 workspace of the A16 digit rows

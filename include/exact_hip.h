@@ -85,6 +85,17 @@ int exact_gemv_g128_acc(const void* x, int32_t abits, const int8_t* wp, const in
  * (experiments/speed_fair_kaggle.py:656-702), called by TLinG for one row (:738). */
 int exact_gemv(const int16_t* x, const int8_t* wT, const int64_t* Mg, int64_t* out, int32_t N, int32_t K, void* stream);
 
+/* Residual + RMSNorm + qrow fused into the int16 GEMV that consumes them (decode rows, R <= 2, K <= 6144):
+ * t[r] += qrow(irms(x, g), 15) . W with x = x_in + round_shift(res_t, 28 - res_s[r]) (res_t may be NULL). Every
+ * block normalises the rows itself (exact_llm.py:41-46, 100-106) while its first weight tiles load; block 0 writes
+ * x to x_out (NULL: not written; must not alias x_in or res_t, which the other blocks still read), the row shifts
+ * s_out[r] and, when xq_out is given, the quantised int16 rows. Replaces exact_rmsnorm_qrow + exact_gemv_g128_acc
+ * (IntModel.__call__'s residual add, irms and linear, exact_llm.py:166-169, 177-179; TLinG, speed_fair_kaggle.py:735-738)
+ * with one launch. */
+int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, const int64_t* res_t, const int32_t* res_s,
+                             const int64_t* g, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,
+                             int32_t* s_out, int16_t* xq_out, int32_t R, int32_t N, int32_t K, void* stream);
+
 /* Exact group-128 GEMM for prefill (any R): same output as exact_gemv_g128. Up to 3 x 15 rows (A16) or
  * 3 x 16 rows (A8) run as row chunks of the GEMV kernel, more rows on the MFMA GEMM kernels (wide scales:
  * int8 x only there; int16 x with wide scales takes exact_gemm_g128_a16, else 2 is returned).

@@ -361,3 +361,77 @@ def test_rmsnorm_qrow_row_sizes(D):
     assert np.array_equal(host(xd), x2)
     assert np.array_equal(host(xq), want_q) and np.array_equal(host(sq).reshape(-1), np.asarray(want_s).reshape(-1))
     assert not host(td).any()
+
+
+def _norm_case(kind, R, K, rng_):
+    """Residual rows x, residual totals and shifts for the norm-fused GEMV, from ordinary to the edges of the
+    row program's bounds: x << 16 wrapping int64, rows of zeros and of tiny values, left-shifting residuals."""
+    x = rng_.integers(-(1 << 30), 1 << 30, (R, K))
+    res = rng_.integers(-(1 << 44), 1 << 44, (R, K))
+    rs = rng_.integers(0, 20, R)
+    if kind == "huge":                  # |x| near 2^62: x << 16 wraps, k reaches 38
+        x = rng_.integers(-(1 << 62), 1 << 62, (R, K))
+        res = np.zeros((R, K), np.int64)
+    elif kind == "zeros":
+        x = np.zeros((R, K), np.int64)
+        res = np.zeros((R, K), np.int64)
+    elif kind == "tiny":                # one nonzero element: the largest quotient the row program can meet
+        x = np.zeros((R, K), np.int64)
+        x[:, 7] = rng_.integers(1, 100, R)
+        res = np.zeros((R, K), np.int64)
+    elif kind == "leftshift":           # res_s above 28: the residual is shifted left
+        rs = rng_.integers(29, 40, R)
+        res = rng_.integers(-(1 << 20), 1 << 20, (R, K))
+    return x, res, rs
+
+
+@pytest.mark.parametrize("kind", ["plain", "huge", "zeros", "tiny", "leftshift", "nores"])
+@pytest.mark.parametrize("R,N,K", [(1, 4608, 3584), (2, 1152, 896), (1, 7168, 5120), (2, 640, 2048), (1, 300, 6144)])
+def test_gemv_norm_acc(thr, kind, R, N, K):
+    """exact_gemv_g128_norm_acc: x = x_in + rs(res_t, 28 - res_s), t += qrow(irms(x, g), 15) . W, x_out = x, s_out, xq_out,
+    against the oracle's irms / qrow / group linear; t starts from a running total."""
+    rng_ = np.random.default_rng(R * 1000 + K + len(kind))
+    lin, kw, km = synth_lin(thr, 21, f"norm{K}", N, K)
+    w, M = synth.weights_np(kw, N, K), synth.scales_np(km, N, K)
+    x, res, rs = _norm_case(kind, R, K, rng_)
+    g = rng_.integers(1 << 14, 1 << 17, K)
+    g[::5] = -g[::5]
+    xn = x if kind == "nores" else x + O.round_shift(res, (28 - rs)[:, None])
+    xq, s = O.qrow(O.irms(xn, g), 15)
+    t0 = rng_.integers(-(1 << 50), 1 << 50, (R, N))
+    want = t0 + oracle_t(xq, w, M)
+    td = dev(t0, I64)
+    x_out = torch.full((R, K), 7, dtype=I64, device=DEV)
+    s_out = torch.full((R,), -1, dtype=I32, device=DEV)
+    xq_out = torch.zeros((R, K), dtype=I16, device=DEV)
+    xd = dev(x, I64)
+    ops.gemv_norm_acc(xd, None if kind == "nores" else dev(res, I64), None if kind == "nores" else dev(rs, I32), dev(g, I64),
+                      lin, td, s_out, x_out=x_out, xq_out=xq_out)
+    assert np.array_equal(host(xq_out), xq), kind
+    assert np.array_equal(host(s_out), s[:, 0]), kind
+    assert np.array_equal(host(x_out), xn), kind
+    assert np.array_equal(host(td), want), kind
+    assert np.array_equal(host(xd), x)      # the input rows are left as they were
+
+
+@pytest.mark.parametrize("kind", ["plain", "huge", "zeros", "tiny", "leftshift"])
+@pytest.mark.parametrize("D,bits", [(896, 15), (3584, 15), (5120, 15), (2048, 7), (100, 15)])
+def test_rmsnorm_qrow_edges(kind, D, bits):
+    """The standalone residual + irms + qrow kernel (in place, residual cleared, digit rows) on the same edge rows as
+    the norm-fused GEMV, int16 and int8 quantisation, against the oracle."""
+    R = 2
+    rng_ = np.random.default_rng(D + bits + 17 * len(kind))
+    x, res, rs = _norm_case(kind, R, D, rng_)
+    g = rng_.integers(1 << 14, 1 << 17, D)
+    g[1::7] = -g[1::7]
+    xd, td = dev(x, I64), dev(res, I64)
+    x8 = torch.zeros((2 * R, D), dtype=I8, device=DEV) if bits == 15 else None
+    xq, sq = ops.rmsnorm_qrow(xd, dev(g, I64), bits, td, dev(rs, I32), clear=True, x8=x8)
+    x2 = x + O.round_shift(res, (28 - rs)[:, None])
+    want_q, want_s = O.qrow(O.irms(x2, g), bits)
+    assert np.array_equal(host(xd), x2), kind
+    assert np.array_equal(host(xq), want_q) and np.array_equal(host(sq).reshape(-1), np.asarray(want_s).reshape(-1)), kind
+    assert not host(td).any()
+    if x8 is not None:
+        d8 = host(x8).astype(np.int64)
+        assert np.array_equal(d8[0::2] * 256 + d8[1::2] + 128, want_q), kind
