@@ -375,13 +375,15 @@ def progress(msg):
     print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
-def _median_time(fn, n):
+def _median_time(fn, n, label=None):
     import numpy as np
     ts = []
-    for _ in range(n):
+    for i in range(n):
         t0 = time.perf_counter()
         fn()
         ts.append(time.perf_counter() - t0)
+        if label:
+            progress(f"CPU baseline: {label} run {i + 1}/{n}: {ts[-1]:.2f} s")
     return float(np.median(ts))
 
 
@@ -524,7 +526,7 @@ def cpu_model_c1(full=False):
 
     reps = 3 if full else 1
     if full:
-        kv_s = _median_time(cached_run, reps)
+        kv_s = _median_time(cached_run, reps, "C1 KV-cached 16 + 64")
     else:   # the prompt and 8 steps, the other 55 steps at the median step time
         cache = m.new_cache()
         t0 = time.perf_counter()
@@ -539,7 +541,7 @@ def cpu_model_c1(full=False):
     res = {"cores": os.cpu_count(), "kind": "port", "model_build_s": round(build_s, 1),
            "kv_cached_s": round(kv_s, 2), "kv_cached_tok_s": round(64 / kv_s, 3)}
     if full:
-        ar_s = _median_time(lambda: O.greedy_decode(m, ids, 64, cached=False), reps)
+        ar_s = _median_time(lambda: O.greedy_decode(m, ids, 64, cached=False), reps, "C1 as-reference 16 + 64")
         res.update(as_reference_s=round(ar_s, 2), as_reference_tok_s=round(64 / ar_s, 3),
                    sample="16 + 64 tokens, both variants in full, median of 3")
     else:
