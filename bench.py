@@ -464,14 +464,18 @@ def cpu_baseline(full=False):
     progress("CPU baseline: C2 GEMVs done")
     # C3: the 2048-token prefill GEMMs (A8) and one attention layer
     c3 = {}
-    rows = 2048 if full else 128
     for gname, (K, N) in {"gateup_K3584_N18944": (3584, 18944), "down_K18944_N3584": (18944, 3584)}.items():
         w = exact_c.weights(synth.key(7, gname), synth.thresholds(), N, K)
         M = exact_c.scales(synth.key(8, gname), N, K, synth.M_LO, synth.M_HI)
-        x = rng.integers(-127, 128, (rows, K))
-        t = _median_time(lambda: O.linear_group_t(x, w, M, abits=7, n_chunk=2048), 1) * (2048 / rows)
+        run = lambda rows_: _median_time(lambda: O.linear_group_t(rng.integers(-127, 128, (rows_, K)), w, M, abits=7,
+                                                                   n_chunk=2048), 1)
+        if full:
+            t = run(2048)
+        else:   # a fixed cost per call (the weights' float64 conversion) plus a cost per row: a line through 128 and 256
+            t128, t256 = run(128), run(256)
+            t = t128 + (t256 - t128) * (2048 - 128) / 128
         c3[gname] = {"s": round(t, 2), "GOPS": round(2.0 * 2048 * K * N / t / 1e9, 1)}
-        del w, M, x
+        del w, M
     S, hd, H = 2048, 128, 28
     q = rng.integers(-(1 << 20), 1 << 20, (S, hd))
     k = rng.integers(-(1 << 20), 1 << 20, (S, hd))
@@ -483,7 +487,7 @@ def cpu_baseline(full=False):
     out["C3_prefill"] = c3
     progress("CPU baseline: C3 done")
     c3["sample"] = ("the full 2048 rows, every head" if full else
-                    "128 of the 2048 rows per GEMM x 16, one of the 28 heads x 28 (cost is linear in both)")
+                    "GEMMs at 128 and 256 of the 2048 rows, extrapolated linearly in the rows; one of the 28 heads x 28")
     # C4 / C5: one layer's decode step x layers + head
     for key_, name, ctx in (("C4_qwen2.5-14b_bs1", "qwen2.5-14b", 128), ("C5_qwen1.5-moe-a2.7b_bs1", "qwen1.5-moe-a2.7b", 256)):
         t_l, t_h, nl = cpu_layer_step(name, ctx)

@@ -432,6 +432,7 @@ __device__ __forceinline__ void consume_store(const AttnLDS& L, int nsteps, int 
                                               int H, int h, int d, int half) {
   v16i acc[NB + 2];
   consume<NB>(L, nsteps, ntile, vd, vplane, lane, acc);
+  int b[16];   // bit length of |out| of row r(i) at this lane's dimension
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     uint64_t tot = 0;
@@ -440,7 +441,26 @@ __device__ __forceinline__ void consume_store(const AttnLDS& L, int nsteps, int 
     const int r = 8 * (i >> 2) + 4 * half + (i & 3);
     const int64_t o = shr64((int64_t)tot, 20);
     if (q0 + r < R) out[((int64_t)(q0 + r) * H + h) * AP_HD + d] = o;
-    atomicMax(rowbits + r, bitlen64(abs64(o)));
+    b[i] = bitlen64(abs64(o));
+  }
+  // maxima over the 32 lanes (dimensions) of each half, transposed as they reduce: at the step over lane bit m the
+  // lane keeps the upper or lower half of its values and takes its partner's other half, so after the bits 16, 8, 4,
+  // 2 lane l holds row i = (l>>1&1) + 2 (l>>2&1) + 4 (l>>3&1) + 8 (l>>4&1) over 16 lanes, and bit 1 finishes it:
+  // 16 shuffles and one LDS atomic per row and wave (a per-element atomic cost 7e6 bank conflicts per launch)
+#pragma unroll
+  for (int m = 16, n = 8; m >= 2; m >>= 1, n >>= 1) {
+    const bool up = (lane & m) != 0;
+#pragma unroll
+    for (int j = 0; j < n; ++j) {
+      const int other = __shfl_xor(up ? b[j] : b[j + n], m, 64);
+      const int keep = up ? b[j + n] : b[j];
+      b[j] = other > keep ? other : keep;
+    }
+  }
+  const int other = __shfl_xor(b[0], 1, 64);
+  if ((lane & 1) == 0) {
+    const int i = ((lane >> 1) & 1) + 2 * ((lane >> 2) & 1) + 4 * ((lane >> 3) & 1) + 8 * ((lane >> 4) & 1);
+    atomicMax(rowbits + 8 * (i >> 2) + 4 * half + (i & 3), other > b[0] ? other : b[0]);
   }
 }
 

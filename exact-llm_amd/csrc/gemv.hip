@@ -236,7 +236,9 @@ __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ 
 }
 
 // int64 activations each lane loads per row in the quantising GEMV: a wave's slice holds up to 64 * XQ_LOADS columns
+#ifndef XQ_LOADS
 #define XQ_LOADS 8
+#endif
 
 // GEMV whose int16 / int8 activations are quantised from int64 rows on the fly (qrow, exact_llm.py:41-46): row r's
 // shift is s = max(bitlen(max |x_r|) - abits, 0), with bitlen(max |x_r|) = max_i part[r * nparts + i] as the producer
