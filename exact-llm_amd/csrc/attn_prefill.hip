@@ -24,7 +24,6 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 namespace exact {
 
-int zero_bytes(void* dst, int64_t nbytes, hipStream_t st);
 
 #define AP_HD 128
 #define AP_TN 4608   // exp entries in LDS; the fast path needs the table to be zero from entry AP_TN - 2 on
@@ -55,9 +54,9 @@ __device__ __forceinline__ int sum16(v4i p0, v4i p1) {
 // V digits for the p.v product: vdig[(((kh * 8 + b) * ntile + t) * 2 + half) * hd + d][m] (16 bytes) is balanced
 // base-256 digit b of v[32 t + 8 (m / 4) + 4 half + m % 4][d] (zero from nkeys on): the 16 keys in the order in
 // which a transposed 32x32 MFMA result holds them for lane half `half`, and consecutive dimensions 16 bytes apart
-// (so a wave's loads are contiguous). vbits[kh] = max bit length of |v| over the KV head.
+// (so a wave's loads are contiguous). vpart[kh * ntile + t] = max bit length of |v| over the tile's keys.
 __device__ __forceinline__ void vdigits_tile(const int64_t* __restrict__ v, int sl, int KV, int Smax, int nkeys, int kh, int t,
-                                             int ntile, int8_t* __restrict__ vdig, int32_t* __restrict__ vbits) {
+                                             int ntile, int8_t* __restrict__ vdig, int32_t* __restrict__ vpart, int* red) {
   const int d = threadIdx.x & (AP_HD - 1), half = threadIdx.x >> 7;
   const int64_t cbase = ((int64_t)sl * KV + kh) * Smax;
   v4i pk[8];
@@ -80,18 +79,21 @@ __device__ __forceinline__ void vdigits_tile(const int64_t* __restrict__ v, int 
 #pragma unroll
   for (int b = 0; b < 8; ++b)
     *reinterpret_cast<v4i*>(vdig + (((((int64_t)kh * 8 + b) * ntile + t) * 2 + half) * AP_HD + d) * 16) = pk[b];
-  bl = wave_max_i32(bl);
-  if ((threadIdx.x & 63) == 0) atomicMax(vbits + kh, bl);
+  bl = block_max_i32(bl, red);
+  if (threadIdx.x == 0) vpart[(int64_t)kh * ntile + t] = bl;
 }
 
 // Digits of every cached k of the sequence for the q.k product: kdig[(((kh * 2 + p) * 4 + kb) * kpad + j) * 32 + c]
 // = digit p (0: hi, 1: lo - 128) of k[j][32 kb + c]; ck[kh * kpad + j] = 128 sum_d k[j][d] - 16384 hd and
-// skk[kh * kpad + j] = sk[j] (zeros from nkeys on); skmax[kh] = max sk; tnz[0] = 1 if the exp table T has a
-// nonzero entry from AP_TN - 2 on, else tnz[1] = 1 + the last nonzero index. 8 threads per key.
+// skk[kh * kpad + j] = sk[j] (zeros from nkeys on); kpart[kh * ntile + t] = max sk over the tile's keys. The KV
+// head 0 blocks also scan the exp table T, block t entries 256 t + [0, 256) (+ 8 kpad i): tpart[t] = 2^30 if one
+// of them breaks the form the fast path takes (zero from entry AP_TN - 2 on, T[0] > 0, entries in [0, 2^24] with
+// steps T[i] - T[i + 1] in [0, 2^24)), else 1 + the last nonzero index among them (0 if none). 8 threads per key.
+// Per-block results instead of global atomics: same-line atomics from every block serialise (~20 us here).
 __device__ __forceinline__ void kdigits_tile(const int16_t* __restrict__ kq, const int32_t* __restrict__ sk, int sl, int KV,
                                              int Smax, int nkeys, int kpad, int kh, int t, int8_t* __restrict__ kdig,
-                                             int32_t* __restrict__ ck, int32_t* __restrict__ skk, int32_t* __restrict__ skmax,
-                                             const int32_t* __restrict__ T, int32_t* __restrict__ tnz) {
+                                             int32_t* __restrict__ ck, int32_t* __restrict__ skk, int32_t* __restrict__ kpart,
+                                             const int32_t* __restrict__ T, int32_t* __restrict__ tpart, int* red) {
   const int tid = threadIdx.x;
   const int j = 32 * t + (tid >> 3), c = tid & 7;   // c: 16 dimensions 16 c .. 16 c + 15
   const int64_t row = ((int64_t)sl * KV + kh) * Smax + j;
@@ -117,31 +119,47 @@ __device__ __forceinline__ void kdigits_tile(const int16_t* __restrict__ kq, con
     ck[(int64_t)kh * kpad + j] = j < nkeys ? 128 * sum - 16384 * AP_HD : 0;
     skk[(int64_t)kh * kpad + j] = skv;
   }
-  skv = wave_max_i32(skv);
-  if ((tid & 63) == 0) atomicMax(skmax + kh, skv);
+  const int ntile = kpad / 32;
+  skv = block_max_i32(skv, red);
+  if (tid == 0) kpart[(int64_t)kh * ntile + t] = skv;
   if (kh == 0) {   // the fast path keeps exp entries [0, AP_TN) in LDS; the KV head 0 blocks scan the table
-    int nz = 0, last = 0;
+    int bad = 0, last = 0;
     for (int i = 256 * t + tid; i < EXACT_EXP_N; i += 8 * kpad) {
       const int x = T[i];
-      if (i >= AP_TN - 2) nz |= x != 0;
-      else last = x != 0 ? i + 1 : last;
+      if (i >= AP_TN - 2) {
+        bad |= x != 0;
+      } else {
+        last = x != 0 ? i + 1 : last;
+        const int y = T[i + 1];   // steps in [0, 2^24), entries in [0, 2^24], T[0] > 0
+        bad |= y < 0 || x > (1 << 24) || x < y || x - y >= (1 << 24) || (i == 0 && x == 0);
+      }
     }
-    if (nz) atomicOr(tnz, 1);
-    if (last) atomicMax(tnz + 1, last);
+    const int r = block_max_i32(bad ? 1 << 30 : last, red + 4);
+    if (tid == 0) tpart[t] = r;
   }
 }
 
-// grid (kpad / 32, 2 KV), block 256: blocks with y < KV write V digits, the others k digits (flags zeroed before:
-// vbits[KV], skmax[KV], exp-table tail, exp-table zero index)
+// grid (kpad / 32, 2 KV), block 256: blocks with y < KV write V digits, the others k digits. part: the per-tile
+// partial results, vpart [KV][kpad / 32], kpart [KV][kpad / 32], tpart [kpad / 32], every entry written here.
 __global__ __launch_bounds__(256) void k_attn_digits(const int64_t* __restrict__ v, const int16_t* __restrict__ kq,
                                                      const int32_t* __restrict__ sk, const int32_t* __restrict__ T, int sl, int KV,
                                                      int Smax, int nkeys, int kpad, int8_t* __restrict__ vdig,
                                                      int8_t* __restrict__ kdig, int32_t* __restrict__ ck, int32_t* __restrict__ skk,
-                                                     int32_t* __restrict__ flags) {
+                                                     int32_t* __restrict__ part) {
+  __shared__ int red[8];
+  const int ntile = kpad / 32;
   if ((int)blockIdx.y < KV)
-    vdigits_tile(v, sl, KV, Smax, nkeys, blockIdx.y, blockIdx.x, kpad / 32, vdig, flags);
+    vdigits_tile(v, sl, KV, Smax, nkeys, blockIdx.y, blockIdx.x, ntile, vdig, part, red);
   else
-    kdigits_tile(kq, sk, sl, KV, Smax, nkeys, kpad, blockIdx.y - KV, blockIdx.x, kdig, ck, skk, flags + KV, T, flags + 2 * KV);
+    kdigits_tile(kq, sk, sl, KV, Smax, nkeys, kpad, blockIdx.y - KV, blockIdx.x, kdig, ck, skk, part + (int64_t)KV * ntile, T,
+                 part + (int64_t)2 * KV * ntile, red);
+}
+
+// max of n int32 values, by every lane of a wave (the result is wave-uniform)
+__device__ __forceinline__ int wave_max_of(const int32_t* __restrict__ a, int n) {
+  int m = 0;   // every partial is >= 0
+  for (int i = threadIdx.x & 63; i < n; i += 64) m = a[i] > m ? a[i] : m;
+  return wave_max_i32(m);
 }
 
 // Scores of a tile (keys x queries) from the digit products: HH, HL + LH, LL.
@@ -206,25 +224,31 @@ __device__ __forceinline__ double max_f64(double a, double b) {
   return r;
 }
 
-// unrounded score w (float64, exact) of an element; the score is floor(w + 1/2)
+// unrounded score w (float64, exact) of an element; the score is floor(w + 1/2). SCALE false leaves out the row's
+// factor fscale > 0 (the row maximum of w is the maximum of the unscaled values times fscale, and that product is
+// exact for the same reason w is).
+template <bool SCALE>
 __device__ __forceinline__ double raw_score(int hh, int xx, int llc, double fscale, int skv) {
   const int m = (hh << 8) + xx;
-  return __builtin_ldexp(__builtin_fma((double)m, 256.0, (double)llc) * fscale, skv);
+  const double dot = __builtin_fma((double)m, 256.0, (double)llc);
+  return __builtin_ldexp(SCALE ? dot * fscale : dot, skv);
 }
 
 // lut_exp(mx - sc) for mx - sc = dd >= 0 (exp16 below), given that T is zero from entry tz on (tz <= AP_TN - 2):
 // indices past tz read entry tz (one address for every such lane, so the LDS read broadcasts), which also covers
-// the reference's cut at 40.0. lim = 256 tz.
+// the reference's cut at 40.0. lim = 256 tz. dd = mx - floor(w + 1/2) = ceil((mx - 1/2) - w): w is N 2^-s with
+// an integer |N| < 2^52 and s <= 32, so the difference is exact while below 2^53 2^-s, and a larger one (>= 2^21)
+// clamps to lim either way.
 
-// floor(e 2^20 / es) for 0 <= e <= 2^24, es < 2^53: the estimate e * (2^20 / es) is within 2^-31 of the
-// quotient and the remainder (exact in float64) corrects it by one either way
-__device__ __forceinline__ int pdiv_f64(int e, double es, double res20) {
+// floor(e 2^20 / es) for 0 <= e <= es < 2^40 (es20 = es 2^-20, res20 = 2^20 / es rounded): the estimate
+// e res20 - 2^-30 is below the quotient and within 2^-29 of it, so its floor is the result or one less; the
+// remainder (e 2^20 - q es) 2^-20, exact in one fma (an integer below 2^41 over 2^20), is >= es20 in the second case.
+// For e = 0 the estimate is -2^-30 and the correction brings -1 to 0.
+__device__ __forceinline__ int pdiv_f64(int e, double es20, double res20) {
   const double ed = (double)e;
-  double q = __builtin_floor(ed * res20);
-  const double r = __builtin_fma(-q, es, ed * 1048576.0);
-  q = r < 0.0 ? q - 1.0 : q;
-  q = r >= es ? q + 1.0 : q;
-  return (int)q;
+  const double q = __builtin_floor(__builtin_fma(ed, res20, -0x1p-30));
+  const double r = __builtin_fma(-q, es20, ed);
+  return (int)q + (r >= es20 ? 1 : 0);
 }
 
 // Balanced base-256 digits of p (0 <= p <= 2^20) for 4 keys at once: u = p + 128 + 128 * 256 holds d0 + 128,
@@ -248,7 +272,7 @@ struct FastCtx {
 };
 
 // the 16 unrounded scores of a tile (masked keys AP_NEG)
-template <bool MASK>
+template <bool MASK, bool SCALE = true>
 __device__ __forceinline__ void tile_raw(const QK& c, const FastCtx& f, int j0, const KCol& kc, const v16i& hh, const v16i& xx,
                                          const v16i& ll, double (&wv)[16]) {
 #pragma unroll
@@ -257,28 +281,30 @@ __device__ __forceinline__ void tile_raw(const QK& c, const FastCtx& f, int j0, 
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int i = 4 * g + u;
-      double x = raw_score(hh[i], xx[i], ll[i] + ckv[u] + f.rterm, f.fscale, skv[u]);
+      double x = raw_score<SCALE>(hh[i], xx[i], ll[i] + ckv[u] + f.rterm, f.fscale, skv[u]);
       if (MASK) x = j0 + 8 * g + 4 * c.half + u <= f.mypos ? x : AP_NEG;
       wv[i] = x;
     }
   }
 }
 
+// running maximum of the unscaled scores (times fscale: the row's maximum w)
 template <bool MASK>
 __device__ __forceinline__ double tile_max(const QK& c, const FastCtx& f, int j0, const KCol& kc, const v16i& hh, const v16i& xx,
                                            const v16i& ll, double mw) {
   double wv[16];
-  tile_raw<MASK>(c, f, j0, kc, hh, xx, ll, wv);
+  tile_raw<MASK, false>(c, f, j0, kc, hh, xx, ll, wv);
 #pragma unroll
   for (int i = 0; i < 16; ++i) mw = max_f64(mw, wv[i]);
   return mw;
 }
 
-// exp_lds for the 16 elements of a tile with every LDS read issued before the first use
-__device__ __forceinline__ void exp16(const int32_t* T, double mx, const double (&wv)[16], double lim, int (&e)[16]) {
+// exp_lds for the 16 elements of a tile with every LDS read issued before the first use; mxh = mx - 1/2. The table
+// steps T[i] - T[i + 1] are in [0, 2^24) (checked with the table), so the interpolation product is a 24-bit one.
+__device__ __forceinline__ void exp16(const int32_t* T, double mxh, const double (&wv)[16], double lim, int (&e)[16]) {
   int di[16], a[16], b[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) di[i] = (int)__builtin_fmin(mx - __builtin_floor(wv[i] + 0.5), lim);
+  for (int i = 0; i < 16; ++i) di[i] = (int)__builtin_fmin(__builtin_ceil(mxh - wv[i]), lim);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     a[i] = T[di[i] >> 8];
@@ -286,16 +312,16 @@ __device__ __forceinline__ void exp16(const int32_t* T, double mx, const double 
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) e[i] = a[i] - (((a[i] - b[i]) * (di[i] & 255) + 128) >> 8);
+  for (int i = 0; i < 16; ++i) e[i] = a[i] - (int)((__umul24((unsigned)(a[i] - b[i]), (unsigned)(di[i] & 255)) + 128u) >> 8);
 }
 
 template <bool MASK>
 __device__ __forceinline__ int tile_esum(const QK& c, const FastCtx& f, int j0, const KCol& kc, const v16i& hh, const v16i& xx,
-                                         const v16i& ll, double mx) {
+                                         const v16i& ll, double mxh) {
   double wv[16];
   tile_raw<MASK>(c, f, j0, kc, hh, xx, ll, wv);
   int e[16];
-  exp16(f.T, mx, wv, f.tlim, e);
+  exp16(f.T, mxh, wv, f.tlim, e);
   int part = 0;   // 16 terms <= 2^24
 #pragma unroll
   for (int i = 0; i < 16; ++i) part += e[i];
@@ -304,13 +330,13 @@ __device__ __forceinline__ int tile_esum(const QK& c, const FastCtx& f, int j0, 
 
 template <bool MASK>
 __device__ __forceinline__ void tile_pdig(const QK& c, const FastCtx& f, int j0, const KCol& kc, const v16i& hh, const v16i& xx,
-                                          const v16i& ll, double mx, double esd, double res20, v4i (&pa)[3]) {
+                                          const v16i& ll, double mxh, double es20, double res20, v4i (&pa)[3]) {
   double wv[16];
   tile_raw<MASK>(c, f, j0, kc, hh, xx, ll, wv);
   int p[16];
-  exp16(f.T, mx, wv, f.tlim, p);
+  exp16(f.T, mxh, wv, f.tlim, p);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) p[i] = pdiv_f64(p[i], esd, res20);
+  for (int i = 0; i < 16; ++i) p[i] = pdiv_f64(p[i], es20, res20);
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
         int w0, w1, w2;
@@ -471,14 +497,15 @@ template <int NW>
 __device__ __forceinline__ void passes12_f64(const QK& c, const AttnLDS& L, const FastCtx& f, int ntile, int firstpos, int w,
                                              double& mx, int64_t& es) {
   double mw = AP_NEG;
+  KTile kt;   // the next tile's k digits load while this one is finished (its key terms load behind its products)
+  if (w < ntile) load_ktile(c, 32 * w, kt);
   for (int t = w; t < ntile; t += NW) {
-    KTile kt;
-    KCol kc;
     v16i hh, xx, ll;
-    load_ktile(c, 32 * t, kt);
-    load_kcol(c, 32 * t, kc);
-    __builtin_amdgcn_sched_barrier(0);   // every load of the tile in flight before the first use
+    KCol kc;
     mfma_ktile(c, kt, hh, xx, ll);
+    load_kcol(c, 32 * t, kc);   // before the prefetch: the epilogue's wait then leaves the prefetch in flight
+    if (t + NW < ntile) load_ktile(c, 32 * (t + NW), kt);
+    __builtin_amdgcn_sched_barrier(0);
     mw = 32 * t + 31 <= firstpos ? tile_max<false>(c, f, 32 * t, kc, hh, xx, ll, mw) : tile_max<true>(c, f, 32 * t, kc, hh, xx, ll, mw);
   }
   mw = max_f64(mw, __shfl_xor(mw, 32, 64));
@@ -486,17 +513,18 @@ __device__ __forceinline__ void passes12_f64(const QK& c, const AttnLDS& L, cons
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < NW; ++k) mw = max_f64(mw, L.red_w[k * 32 + c.l32]);
-  mx = __builtin_floor(mw + 0.5);
+  mx = __builtin_floor(mw * f.fscale + 0.5);
+  const double mxh = mx - 0.5;
   int64_t e = 0;
+  if (w < ntile) load_ktile(c, 32 * w, kt);
   for (int t = w; t < ntile; t += NW) {
-    KTile kt;
-    KCol kc;
     v16i hh, xx, ll;
-    load_ktile(c, 32 * t, kt);
-    load_kcol(c, 32 * t, kc);
-    __builtin_amdgcn_sched_barrier(0);
+    KCol kc;
     mfma_ktile(c, kt, hh, xx, ll);
-    e += 32 * t + 31 <= firstpos ? tile_esum<false>(c, f, 32 * t, kc, hh, xx, ll, mx) : tile_esum<true>(c, f, 32 * t, kc, hh, xx, ll, mx);
+    load_kcol(c, 32 * t, kc);   // before the prefetch: the epilogue's wait then leaves the prefetch in flight
+    if (t + NW < ntile) load_ktile(c, 32 * (t + NW), kt);
+    __builtin_amdgcn_sched_barrier(0);
+    e += 32 * t + 31 <= firstpos ? tile_esum<false>(c, f, 32 * t, kc, hh, xx, ll, mxh) : tile_esum<true>(c, f, 32 * t, kc, hh, xx, ll, mxh);
   }
   e += __shfl_xor(e, 32, 64);
   if (c.half == 0) L.red_a[w * 32 + c.l32] = e;
@@ -510,7 +538,7 @@ __device__ __forceinline__ void passes12_f64(const QK& c, const AttnLDS& L, cons
 // tile's k digits and key terms load while this one is finished.
 __device__ __forceinline__ void produce_f64(const QK& c, const AttnLDS& L, const FastCtx& f, int nsteps, int ntile, int firstpos,
                                             int w, int lane, double mx, int64_t es) {
-  const double esd = (double)es, res20 = 1048576.0 / esd;   // 2^20 / es: the reciprocal scaled exactly
+  const double es20 = __builtin_ldexp((double)es, -20), res20 = 1048576.0 / (double)es, mxh = mx - 0.5;
   KTile kt;
   KCol kc;
   if (w < ntile) {
@@ -530,8 +558,8 @@ __device__ __forceinline__ void produce_f64(const QK& c, const AttnLDS& L, const
           load_kcol(c, 32 * (t + AP_PROD), kc);
         }
         __builtin_amdgcn_sched_barrier(0);   // the next tile's loads in flight before this tile's epilogue
-        if (32 * t + 31 <= firstpos) tile_pdig<false>(c, f, 32 * t, cur, hh, xx, ll, mx, esd, res20, pa);
-        else tile_pdig<true>(c, f, 32 * t, cur, hh, xx, ll, mx, esd, res20, pa);
+        if (32 * t + 31 <= firstpos) tile_pdig<false>(c, f, 32 * t, cur, hh, xx, ll, mxh, es20, res20, pa);
+        else tile_pdig<true>(c, f, 32 * t, cur, hh, xx, ll, mxh, es20, res20, pa);
       }
 #pragma unroll
       for (int a = 0; a < 3; ++a) L.Pl[s & 1][w][a][lane] = pa[a];
@@ -626,6 +654,7 @@ __device__ __forceinline__ void produce_i64(const QK& c, const AttnLDS& L, const
 struct Block {
   QK c;
   int h, kh, q0, mypos, firstpos, ntile, sqs, sqv;
+  int tz;      // 1 + the last nonzero index of the exp table (fast path)
   bool fast;
 };
 
@@ -649,16 +678,29 @@ __device__ __forceinline__ bool block_item(int R, int H, int KV, int& h, int& kh
   return true;
 }
 
-// Loads the exp table and the q digits into LDS (ends with a barrier) and fills b. flags: vbits[KV], skmax[KV],
-// exp-table tail nonzero. The float64 decision depends only on the block's rows, so both kernels agree.
+// Loads the exp table and the q digits into LDS (ends with a barrier) and fills b. part: k_attn_digits' per-tile
+// results. The float64 decision depends only on the block's rows, so both kernels agree.
 __device__ __forceinline__ void block_setup(Block& b, int h, int kh, int q0, const int16_t* __restrict__ qq,
                                             const int32_t* __restrict__ sq, const int8_t* __restrict__ kdig,
                                             const int32_t* __restrict__ ck, const int32_t* __restrict__ skk,
-                                            const int32_t* __restrict__ flags, const int32_t* __restrict__ pos,
+                                            const int32_t* __restrict__ part, const int32_t* __restrict__ pos,
                                             const int32_t* __restrict__ Tg, int32_t* T, v4i (*Qd)[64], int R, int H, int KV,
                                             int nkeys, int kpad, int INV) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  for (int i = tid; i < AP_TN; i += blockDim.x) T[i] = Tg[i];
+  {   // exp table into LDS, 16 bytes a lane, every load issued before the first store (blocks of 256 or 512)
+    constexpr int NV = AP_TN / 4, NK = (NV + 255) / 256;
+    v4i r[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      const int i = tid + k * (int)blockDim.x;
+      if (i < NV) r[k] = reinterpret_cast<const v4i*>(Tg)[i];
+    }
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+      const int i = tid + k * (int)blockDim.x;
+      if (i < NV) reinterpret_cast<v4i*>(T)[i] = r[k];
+    }
+  }
   b.h = h;
   b.kh = kh;
   b.q0 = q0;
@@ -692,8 +734,11 @@ __device__ __forceinline__ void block_setup(Block& b, int h, int kh, int q0, con
   }
   b.sqs = sqs + __shfl_xor(sqs, 32, 64);
   b.sqv = sq[(int64_t)qr * H + h];
-  // uniform over the block: every wave sees the same 32 rows
-  b.fast = wave_max_i32(b.sqv) + flags[KV + kh] <= 33 && INV >= 0 && INV < (1 << 14) && flags[2 * KV] == 0;
+  // uniform over the block: every wave sees the same 32 rows and reduces the same partials
+  const int nt = kpad / 32;
+  const int skmax = wave_max_of(part + (int64_t)(KV + kh) * nt, nt), tab = wave_max_of(part + (int64_t)2 * KV * nt, nt);
+  b.tz = tab;
+  b.fast = wave_max_i32(b.sqv) + skmax <= 33 && INV >= 0 && INV < (1 << 14) && tab < (1 << 30);
   __syncthreads();
 }
 
@@ -701,23 +746,23 @@ __device__ __forceinline__ void block_setup(Block& b, int h, int kh, int q0, con
 // int64 (the float64 path stores its exact integer maximum as an int64 too).
 __global__ __launch_bounds__(64 * AP_SW, 3) void k_attn_stats(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
                                                               const int8_t* __restrict__ kdig, const int32_t* __restrict__ ck,
-                                                              const int32_t* __restrict__ skk, const int32_t* __restrict__ flags,
+                                                              const int32_t* __restrict__ skk, const int32_t* __restrict__ part,
                                                               const int32_t* __restrict__ pos, const int32_t* __restrict__ Tg,
                                                               int64_t* __restrict__ st_mx, int64_t* __restrict__ st_es, int R,
                                                               int H, int KV, int nkeys, int kpad, int INV) {
-  __shared__ int32_t T[AP_TN];
+  __shared__ __attribute__((aligned(16))) int32_t T[AP_TN];
   __shared__ v4i Qd[8][64];
   __shared__ double red_w[AP_SW * 32];
   __shared__ int64_t red_a[AP_SW * 32], red_b[AP_SW * 32];
   int h, kh, q0;
   if (!block_item(R, H, KV, h, kh, q0)) return;
   Block b;
-  block_setup(b, h, kh, q0, qq, sq, kdig, ck, skk, flags, pos, Tg, T, Qd, R, H, KV, nkeys, kpad, INV);
+  block_setup(b, h, kh, q0, qq, sq, kdig, ck, skk, part, pos, Tg, T, Qd, R, H, KV, nkeys, kpad, INV);
   const int w = threadIdx.x >> 6;
   AttnLDS L{T, nullptr, red_w, red_a, red_b};
   int64_t mx, es;
   if (b.fast) {
-    const FastCtx f{T, __builtin_ldexp((double)INV, b.sqv - 32), 256.0 * flags[2 * KV + 1], 128 * b.sqs, b.mypos};
+    const FastCtx f{T, __builtin_ldexp((double)INV, b.sqv - 32), 256.0 * b.tz, 128 * b.sqs, b.mypos};
     double m;
     passes12_f64<AP_SW>(b.c, L, f, b.ntile, b.firstpos, w, m, es);
     mx = (int64_t)m;
@@ -737,13 +782,13 @@ __global__ __launch_bounds__(64 * AP_SW, 3) void k_attn_stats(const int16_t* __r
 // and a consumer share each SIMD). The consumers use 4 V digits when every |v| of the KV head is below 2^30, else 8.
 __global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
                                                  const int8_t* __restrict__ kdig, const int32_t* __restrict__ ck,
-                                                 const int32_t* __restrict__ skk, const int32_t* __restrict__ flags,
+                                                 const int32_t* __restrict__ skk, const int32_t* __restrict__ part,
                                                  const int8_t* __restrict__ vdig, const int32_t* __restrict__ pos,
                                                  const int32_t* __restrict__ Tg, const int64_t* __restrict__ st_mx,
                                                  const int64_t* __restrict__ st_es, int64_t* __restrict__ out,
                                                  int32_t* __restrict__ obits, int R, int H, int KV, int nkeys, int kpad,
                                                  int INV) {
-  __shared__ int32_t T[AP_TN];
+  __shared__ __attribute__((aligned(16))) int32_t T[AP_TN];
   __shared__ v4i Pl[2][AP_PROD][3][64];
   __shared__ v4i Qd[8][64];
   __shared__ int rowbits[32];
@@ -752,7 +797,7 @@ __global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int1
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   if (tid < 32) rowbits[tid] = 0;
   Block b;
-  block_setup(b, h, kh, q0, qq, sq, kdig, ck, skk, flags, pos, Tg, T, Qd, R, H, KV, nkeys, kpad, INV);
+  block_setup(b, h, kh, q0, qq, sq, kdig, ck, skk, part, pos, Tg, T, Qd, R, H, KV, nkeys, kpad, INV);
   const QK& c = b.c;
   const int row = q0 + c.l32 < R ? q0 + c.l32 : R - 1;
   const int64_t mx = st_mx[(int64_t)h * R + row], es = st_es[(int64_t)h * R + row];
@@ -762,10 +807,10 @@ __global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int1
   const int8_t* vd = vdig + (int64_t)kh * 8 * AP_HD * kpad + ((int64_t)c.half * AP_HD + 32 * dc + c.l32) * 16;
   const int64_t vplane = (int64_t)AP_HD * kpad;   // one digit plane: kpad / 32 tiles x 2 halves x hd x 16 bytes
   if (w >= AP_PROD) {
-    if (flags[kh] + 2 <= 32) consume_store<4>(L, nsteps, b.ntile, vd, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
+    if (wave_max_of(part + (int64_t)kh * (kpad / 32), kpad / 32) + 2 <= 32) consume_store<4>(L, nsteps, b.ntile, vd, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
     else consume_store<8>(L, nsteps, b.ntile, vd, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
   } else if (b.fast) {
-    const FastCtx f{T, __builtin_ldexp((double)INV, b.sqv - 32), 256.0 * flags[2 * KV + 1], 128 * b.sqs, b.mypos};
+    const FastCtx f{T, __builtin_ldexp((double)INV, b.sqv - 32), 256.0 * b.tz, 128 * b.sqs, b.mypos};
     produce_f64(c, L, f, nsteps, b.ntile, b.firstpos, w, lane, (double)mx, es);
   } else {
     produce_i64(c, L, Tg, 128 * (int64_t)b.sqs, b.sqv, INV, b.mypos, nsteps, b.ntile, w, lane, mx, es);
@@ -775,12 +820,11 @@ __global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int1
 }
 
 // workspace layout (bytes, each part 256-aligned): vdig KV*8*hd*kpad, kdig KV*2*hd*kpad, ck and skk KV*kpad*4
-// each, flags (2 KV + 2) int32: vbits, skmax, exp-table tail, exp-table zero index; row maxima and sums H*R*8 each
+// each, the digit kernel's per-tile results (2 KV + 1) * kpad / 32 int32; row maxima and sums H*R*8 each
 static int64_t al256(int64_t n) { return (n + 255) & ~(int64_t)255; }
-static int64_t al16(int64_t n) { return (n + 15) & ~(int64_t)15; }
 static int64_t ws_bytes(int R, int H, int KV, int kpad) {
   return al256((int64_t)KV * 8 * AP_HD * kpad) + al256((int64_t)KV * 2 * AP_HD * kpad) + 2 * al256((int64_t)KV * kpad * 4) +
-         al256((int64_t)(2 * KV + 2) * 4) + 2 * al256((int64_t)H * R * 8);
+         al256((int64_t)(2 * KV + 1) * (kpad / 32) * 4) + 2 * al256((int64_t)H * R * 8);
 }
 
 }  // namespace exact
@@ -801,23 +845,23 @@ extern "C" int exact_attention_prefill(const int16_t* qq, const int32_t* sq, con
   // per shift class, 3 digit pairs x nkeys products of |.| <= 2^14 stay below 2^31
   if (hd != AP_HD || nkeys > 32768) return EXACT_E_UNSUPPORTED;
   const int kpad = (nkeys + 31) / 32 * 32;
-  if (work_bytes < ws_bytes(R, H, KV, kpad) || (reinterpret_cast<uintptr_t>(work) & 255)) return EXACT_E_ARG;
+  if (work_bytes < ws_bytes(R, H, KV, kpad) || (reinterpret_cast<uintptr_t>(work) & 255) ||
+      (reinterpret_cast<uintptr_t>(exp_t) & 15))
+    return EXACT_E_ARG;
   int8_t* vdig = static_cast<int8_t*>(work);
   int8_t* kdig = vdig + al256((int64_t)KV * 8 * AP_HD * kpad);
   int32_t* ck = reinterpret_cast<int32_t*>(kdig + al256((int64_t)KV * 2 * AP_HD * kpad));
   int32_t* skk = reinterpret_cast<int32_t*>(reinterpret_cast<int8_t*>(ck) + al256((int64_t)KV * kpad * 4));
-  int32_t* flags = reinterpret_cast<int32_t*>(reinterpret_cast<int8_t*>(skk) + al256((int64_t)KV * kpad * 4));
-  int64_t* st_mx = reinterpret_cast<int64_t*>(reinterpret_cast<int8_t*>(flags) + al256((int64_t)(2 * KV + 2) * 4));
+  int32_t* part = reinterpret_cast<int32_t*>(reinterpret_cast<int8_t*>(skk) + al256((int64_t)KV * kpad * 4));
+  int64_t* st_mx = reinterpret_cast<int64_t*>(reinterpret_cast<int8_t*>(part) + al256((int64_t)(2 * KV + 1) * (kpad / 32) * 4));
   int64_t* st_es = reinterpret_cast<int64_t*>(reinterpret_cast<int8_t*>(st_mx) + al256((int64_t)H * R * 8));
   hipStream_t st = as_stream(stream);
-  int e = zero_bytes(flags, al16((int64_t)(2 * KV + 2) * 4), st);
-  if (e) return e;
   hipLaunchKernelGGL(k_attn_digits, dim3(kpad / 32, 2 * KV), dim3(256), 0, st, v, kq, sk, exp_t, slot, KV, Smax, nkeys, kpad,
-                     vdig, kdig, ck, skk, flags);
+                     vdig, kdig, ck, skk, part);
   const dim3 grid(((R + 31) / 32 * H + 7) / 8 * 8);
-  hipLaunchKernelGGL(k_attn_stats, grid, dim3(64 * AP_SW), 0, st, qq, sq, kdig, ck, skk, flags, pos, exp_t, st_mx, st_es, R, H,
+  hipLaunchKernelGGL(k_attn_stats, grid, dim3(64 * AP_SW), 0, st, qq, sq, kdig, ck, skk, part, pos, exp_t, st_mx, st_es, R, H,
                      KV, nkeys, kpad, INV);
-  hipLaunchKernelGGL(k_attn_pv, grid, dim3(64 * (AP_PROD + AP_CONS)), 0, st, qq, sq, kdig, ck, skk, flags, vdig, pos, exp_t, st_mx,
+  hipLaunchKernelGGL(k_attn_pv, grid, dim3(64 * (AP_PROD + AP_CONS)), 0, st, qq, sq, kdig, ck, skk, part, vdig, pos, exp_t, st_mx,
                      st_es, out, obits, R, H, KV, nkeys, kpad, INV);
   return launch_status("attention_prefill");
 }

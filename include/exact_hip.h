@@ -252,7 +252,8 @@ int exact_attention_qkv(const int64_t* t, const int32_t* s, const int64_t* b, co
  * (exact in int32), p.v on balanced int8 digits of p (Q20) and v, summed per digit shift in int32 and
  * combined modulo 2^64 like the reference's int64 product. hd = 128 and nkeys <= 32768 (otherwise
  * EXACT_E_UNSUPPORTED). work: device memory of at least exact_attention_prefill_workspace(R, H, KV, hd, nkeys)
- * bytes, 256-byte aligned (digit copies of the slot's k and v, per-row softmax statistics). */
+ * bytes, 256-byte aligned (digit copies of the slot's k and v, per-row softmax statistics); exp_t 16-byte
+ * aligned. */
 int64_t exact_attention_prefill_workspace(int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t nkeys);
 int exact_attention_prefill(const int16_t* qq, const int32_t* sq, const int16_t* kq, const int32_t* sk,
                             const int64_t* v, int32_t slot, const int32_t* pos, const int32_t* exp_t, int64_t* out,

@@ -120,6 +120,34 @@ def test_prefill_full_size_2048():
     assert np.array_equal(out[rows], oracle_rows(*case, slot, H, KV, rows))
 
 
+@pytest.mark.parametrize("change", ["swap", "steep", "tail"])
+def test_prefill_with_unfit_exp_table_matches_row_kernel(change):
+    """An exp table outside the form the matrix-core path's float64 scores take (non-increasing, entries in
+    [0, 2^24], steps below 2^24, T[0] > 0, zero from entry 4606 on) sends every block to the int64 scores: the
+    result equals the row kernel's, which reads the table as the reference does, on the same table."""
+    H, KV, hd, nkeys, R, slot = 4, 2, 128, 150, 150, 1
+    case = make_case(11, 2, slot, H, KV, hd, 192, nkeys, R, "small")
+    cache, qq, sq, pos = to_dev(*case)
+    t = exp_t().astype(np.int64)
+    if change == "swap":
+        t[[40, 41]] = t[[41, 40]]
+    elif change == "steep":
+        t[0] = (1 << 24) + 3
+    else:   # a nonzero entry past the 4606 entries the fast path keeps in LDS
+        t[4700] = 1
+    T = torch.tensor(t, dtype=I32, device=DEV)
+    out = torch.full((R, H * hd), -7, dtype=I64, device=DEV)
+    obits = torch.full((R, H), -1, dtype=I32, device=DEV)
+    ws = ops.prefill_workspace(R, H, KV, hd, nkeys, DEV)
+    ops.attention_prefill(qq, sq, cache, slot, pos, nkeys, T, out, H, KV, hd, O.inv_sqrt_hd(hd), ws, obits)
+    ref = torch.zeros((R, H * hd), dtype=I64, device=DEV)
+    refbits = torch.zeros((R, H), dtype=I32, device=DEV)
+    ops.attention(qq, sq, cache, torch.full((R,), slot, dtype=I32, device=DEV), pos, T, ref, H, KV, hd,
+                  O.inv_sqrt_hd(hd), refbits)
+    assert np.array_equal(host(out), host(ref))
+    assert np.array_equal(host(obits), host(refbits))
+
+
 @pytest.mark.parametrize("H,KV,hd,R,bias,Smax", [(28, 4, 128, 1, True, 96), (28, 4, 128, 4, False, 96),
                                                  (14, 2, 64, 3, True, 96), (4, 4, 256, 2, True, 96),
                                                  (8, 2, 128, 2, True, 8192)])
