@@ -162,11 +162,21 @@ __device__ __forceinline__ int wave_max_of(const int32_t* __restrict__ a, int n)
   return wave_max_i32(m);
 }
 
+// Raw buffer view of the n bytes at p (n < 2^31): a load's address is a per-lane 32-bit offset plus a wave-uniform
+// scalar offset, so the tile loop spends no vector instructions on 64-bit addresses (loads past n read zeros).
+typedef __amdgpu_buffer_rsrc_t BufRes;
+__device__ __forceinline__ BufRes buf_res(const void* p, int64_t n) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)n, 0x00020000);
+}
+__device__ __forceinline__ v4i buf_load16(BufRes r, int voff, int soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+
 // Scores of a tile (keys x queries) from the digit products: HH, HL + LH, LL.
 struct QK {
-  const int8_t* kd;      // this KV head's k digits
   const int32_t* ckh;    // 128 sum k - 16384 hd per key
   const int32_t* skh;    // sk per key
+  BufRes kdr, ckr, skr;  // buffer views of this KV head's k digits, ckh and skh
   const v4i* qd;         // LDS q digits [kb][hi, lo][lane]: B operand, column = query l32, dimensions 32 kb + 16 half + [0, 16)
   int kpad, l32, half, lane;
 };
@@ -184,16 +194,16 @@ struct KCol {
 __device__ __forceinline__ void load_kcol(const QK& c, int j0, KCol& k) {
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    k.ck[g] = *reinterpret_cast<const v4i*>(c.ckh + j0 + 8 * g + 4 * c.half);
-    k.sk[g] = *reinterpret_cast<const v4i*>(c.skh + j0 + 8 * g + 4 * c.half);
+    k.ck[g] = buf_load16(c.ckr, 16 * c.half, (j0 + 8 * g) * 4);
+    k.sk[g] = buf_load16(c.skr, 16 * c.half, (j0 + 8 * g) * 4);
   }
 }
 
 __device__ __forceinline__ void load_ktile(const QK& c, int j0, KTile& k) {
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
-    k.hi[kb] = *reinterpret_cast<const v4i*>(c.kd + ((int64_t)kb * c.kpad + j0 + c.l32) * 32 + 16 * c.half);
-    k.lo[kb] = *reinterpret_cast<const v4i*>(c.kd + ((int64_t)(4 + kb) * c.kpad + j0 + c.l32) * 32 + 16 * c.half);
+    k.hi[kb] = buf_load16(c.kdr, c.l32 * 32 + 16 * c.half, (kb * c.kpad + j0) * 32);
+    k.lo[kb] = buf_load16(c.kdr, c.l32 * 32 + 16 * c.half, ((4 + kb) * c.kpad + j0) * 32);
   }
 }
 
@@ -375,36 +385,27 @@ struct AttnLDS {
   int64_t* red_b;     // [waves][32]
 };
 
-// Consumer loop of the third pass: iteration s multiplies step s - 1 (the producers fill step s meanwhile).
-// NB = 4 holds the V digits of a whole step and loads the next step's while this one's products run; NB = 8
-// (no registers for that) loads one tile ahead.
+// Consumer loop of the third pass: iteration s multiplies step s - 1 (the producers fill step s meanwhile). V digit
+// plane b of tile t is at vr + voff + b vplane + 4096 t. NB = 4 holds the V digits of a whole step and refills each
+// tile's registers with the next step's tile once its products are issued; NB = 8 (no registers for that) loads one
+// tile ahead.
 template <int NB>
-__device__ __forceinline__ void load_v_step(const int8_t* __restrict__ vd, int64_t vplane, int s, int ntile, v4i (&vb)[AP_PROD][NB]) {
+__device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile, BufRes vr, int voff, int vplane, int lane,
+                                        v16i (&acc)[NB + 2]) {
+  auto load_v = [&](int t, v4i (&vb)[NB]) {
+    t = t < ntile ? t : ntile - 1;   // stays inside the written keys
 #pragma unroll
-  for (int tt = 0; tt < AP_PROD; ++tt) {
-    const int t = AP_PROD * s + tt < ntile ? AP_PROD * s + tt : ntile - 1;   // stays inside the written keys
-#pragma unroll
-    for (int b = 0; b < NB; ++b) vb[tt][b] = *reinterpret_cast<const v4i*>(vd + b * vplane + (int64_t)t * (2 * AP_HD * 16));
-  }
-}
-
-template <int NB>
-__device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile, const int8_t* __restrict__ vd, int64_t vplane,
-                                        int lane, v16i (&acc)[NB + 2]) {
+    for (int b = 0; b < NB; ++b) vb[b] = buf_load16(vr, voff, b * vplane + t * (2 * AP_HD * 16));
+  };
 #pragma unroll
   for (int k = 0; k < NB + 2; ++k) acc[k] = v16i{};
   if constexpr (NB == 4) {
     v4i vb[AP_PROD][NB];
-    load_v_step<NB>(vd, vplane, 0, ntile, vb);
+#pragma unroll
+    for (int tt = 0; tt < AP_PROD; ++tt) load_v(tt, vb[tt]);
     for (int s = 0; s <= nsteps; ++s) {
       if (s >= 1) {
         const int buf = (s - 1) & 1, tiles = min(AP_PROD, ntile - AP_PROD * (s - 1));
-        v4i cur[AP_PROD][NB];
-#pragma unroll
-        for (int tt = 0; tt < AP_PROD; ++tt)
-#pragma unroll
-          for (int b = 0; b < NB; ++b) cur[tt][b] = vb[tt][b];
-        if (s < nsteps) load_v_step<NB>(vd, vplane, s, ntile, vb);
 #pragma unroll
         for (int tt = 0; tt < AP_PROD; ++tt) {
           if (tt < tiles) {
@@ -414,16 +415,16 @@ __device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile,
 #pragma unroll
             for (int a = 0; a < 3; ++a)
 #pragma unroll
-              for (int b = 0; b < NB; ++b) acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pv[a], cur[tt][b], acc[a + b], 0, 0, 0);
+              for (int b = 0; b < NB; ++b) acc[a + b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(pv[a], vb[tt][b], acc[a + b], 0, 0, 0);
           }
+          if (s < nsteps) load_v(AP_PROD * s + tt, vb[tt]);
         }
       }
       __syncthreads();
     }
   } else {
     v4i vb[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) vb[b] = *reinterpret_cast<const v4i*>(vd + b * vplane);
+    load_v(0, vb);
     for (int s = 0; s <= nsteps; ++s) {
       if (s >= 1) {
         const int buf = (s - 1) & 1;
@@ -433,9 +434,7 @@ __device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile,
           v4i pv[3], cur[NB];
 #pragma unroll
           for (int b = 0; b < NB; ++b) cur[b] = vb[b];
-          const int tn = t + 1 < ntile ? t + 1 : t;
-#pragma unroll
-          for (int b = 0; b < NB; ++b) vb[b] = *reinterpret_cast<const v4i*>(vd + b * vplane + (int64_t)tn * (2 * AP_HD * 16));
+          load_v(t + 1, vb);
 #pragma unroll
           for (int a = 0; a < 3; ++a) pv[a] = L.Pl[buf][tt][a][lane];
           __builtin_amdgcn_sched_barrier(0);
@@ -453,11 +452,11 @@ __device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile,
 // consume, then out = shr(sum_s C_s 256^s, 20) (modulo 2^64, as the reference's int64 p . v) for dimension d
 // of the block's rows, and the rows' bit lengths in rowbits. C layout: lane holds rows 8 (i / 4) + 4 half + i % 4.
 template <int NB>
-__device__ __forceinline__ void consume_store(const AttnLDS& L, int nsteps, int ntile, const int8_t* __restrict__ vd,
-                                              int64_t vplane, int lane, int64_t* __restrict__ out, int* rowbits, int q0, int R,
-                                              int H, int h, int d, int half) {
+__device__ __forceinline__ void consume_store(const AttnLDS& L, int nsteps, int ntile, BufRes vr, int voff, int vplane,
+                                              int lane, int64_t* __restrict__ out, int* rowbits, int q0, int R, int H, int h, int d,
+                                              int half) {
   v16i acc[NB + 2];
-  consume<NB>(L, nsteps, ntile, vd, vplane, lane, acc);
+  consume<NB>(L, nsteps, ntile, vr, voff, vplane, lane, acc);
   int b[16];   // bit length of |out| of row r(i) at this lane's dimension
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -710,9 +709,11 @@ __device__ __forceinline__ void block_setup(Block& b, int h, int kh, int q0, con
   c.lane = lane;
   c.qd = &Qd[0][0];
   c.kpad = kpad;
-  c.kd = kdig + (int64_t)kh * 2 * 4 * kpad * 32;
   c.ckh = ck + (int64_t)kh * kpad;
   c.skh = skk + (int64_t)kh * kpad;
+  c.kdr = buf_res(kdig + (int64_t)kh * 2 * 4 * kpad * 32, (int64_t)2 * 4 * kpad * 32);
+  c.ckr = buf_res(c.ckh, (int64_t)kpad * 4);
+  c.skr = buf_res(c.skh, (int64_t)kpad * 4);
   const int qr = q0 + c.l32 < R ? q0 + c.l32 : R - 1;
   const int qlast = q0 + 31 < R ? q0 + 31 : R - 1;
   const int jmax = max(0, min(pos[qlast], nkeys - 1));       // positions increase with the row
@@ -804,11 +805,14 @@ __global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int1
   AttnLDS L{T, Pl, nullptr, nullptr, nullptr};
   const int nsteps = (b.ntile + AP_PROD - 1) / AP_PROD;
   const int dc = w - AP_PROD;   // consumer: dimensions 32 dc + [0, 32)
-  const int8_t* vd = vdig + (int64_t)kh * 8 * AP_HD * kpad + ((int64_t)c.half * AP_HD + 32 * dc + c.l32) * 16;
-  const int64_t vplane = (int64_t)AP_HD * kpad;   // one digit plane: kpad / 32 tiles x 2 halves x hd x 16 bytes
+  const int vplane = AP_HD * kpad;   // one digit plane: kpad / 32 tiles x 2 halves x hd x 16 bytes
+  const BufRes vr = buf_res(vdig + (int64_t)kh * 8 * vplane, (int64_t)8 * vplane);
+  const int voff = (c.half * AP_HD + 32 * dc + c.l32) * 16;
   if (w >= AP_PROD) {
-    if (wave_max_of(part + (int64_t)kh * (kpad / 32), kpad / 32) + 2 <= 32) consume_store<4>(L, nsteps, b.ntile, vd, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
-    else consume_store<8>(L, nsteps, b.ntile, vd, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
+    if (wave_max_of(part + (int64_t)kh * (kpad / 32), kpad / 32) + 2 <= 32)
+      consume_store<4>(L, nsteps, b.ntile, vr, voff, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
+    else
+      consume_store<8>(L, nsteps, b.ntile, vr, voff, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
   } else if (b.fast) {
     const FastCtx f{T, __builtin_ldexp((double)INV, b.sqv - 32), 256.0 * b.tz, 128 * b.sqs, b.mypos};
     produce_f64(c, L, f, nsteps, b.ntile, b.firstpos, w, lane, (double)mx, es);
