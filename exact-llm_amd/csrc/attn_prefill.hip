@@ -134,7 +134,7 @@ __device__ __forceinline__ void kdigits_tile(const int16_t* __restrict__ kq, con
         bad |= y < 0 || x > (1 << 24) || x < y || x - y >= (1 << 24) || (i == 0 && x == 0);
       }
     }
-    const int r = block_max_i32(bad ? 1 << 30 : last, red + 4);
+    const int r = block_max_i32(bad ? 1 << 30 : last, red + 16);
     if (tid == 0) tpart[t] = r;
   }
 }
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void k_attn_digits(const int64_t* __restrict__
                                                      int Smax, int nkeys, int kpad, int8_t* __restrict__ vdig,
                                                      int8_t* __restrict__ kdig, int32_t* __restrict__ ck, int32_t* __restrict__ skk,
                                                      int32_t* __restrict__ part) {
-  __shared__ int red[8];
+  __shared__ int red[32];   // two reductions of 16 entries each
   const int ntile = kpad / 32;
   if ((int)blockIdx.y < KV)
     vdigits_tile(v, sl, KV, Smax, nkeys, blockIdx.y, blockIdx.x, ntile, vdig, part, red);

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void k_swiglu_part(int64_t* __restrict__ t, co
                                                      const int32_t* __restrict__ silu, int32_t* __restrict__ part, int I,
                                                      int nparts, int clear_t, int64_t* __restrict__ hout) {
   constexpr int EPT = QSLICE / 256;
-  __shared__ int red[4];
+  __shared__ int red[16];
   const int r = blockIdx.y, b = blockIdx.x;
   int64_t* tr = t + (int64_t)r * 2 * I;
   const int sh = 28 - s[r];
@@ -377,7 +377,7 @@ extern "C" int exact_irms(const int64_t* x, const int64_t* g, int64_t* y, int32_
 }
 
 #ifndef RMS_MAX_THREADS
-#define RMS_MAX_THREADS 1024
+#define RMS_MAX_THREADS 512      // rows of 2049..4096: 8 waves (3584: 7.5 -> 6.8 us a row in a graph)
 #endif
 #ifndef RMS_LARGE_THREADS
 #define RMS_LARGE_THREADS 768    // rows above 4096: 12 waves (14B decode 196 -> 202 tok/s)

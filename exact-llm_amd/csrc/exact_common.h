@@ -113,52 +113,75 @@ __device__ __forceinline__ int64_t lut16(const int32_t* T, int64_t x, bool sig) 
   return a + shr64((b - a) * fr, 8);
 }
 
-// ---- wave (64-lane) reductions
-__device__ __forceinline__ int64_t wave_max64(int64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    int64_t w = __shfl_xor(v, o, 64);
-    v = w > v ? w : v;
-  }
-  return v;
+// ---- wave (64-lane) reductions, for waves with every lane active. Within each row of 16 lanes four DPP steps
+// (exchange with lane ^ 1, lane ^ 2, the mirrored lane of the 8-lane half row, the mirrored lane of the row) leave
+// the row's result in all 16 lanes; the four row results are then read out of lanes 0, 16, 32, 48 into scalar
+// registers, so the result is wave-uniform. (VALU-rate data movement instead of LDS-crossbar shuffles.)
+template <int CTRL>
+__device__ __forceinline__ int dpp32(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
 }
-__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = (int64_t)((uint64_t)v + (uint64_t)__shfl_xor(v, o, 64));
-  return v;
+template <int CTRL>
+__device__ __forceinline__ int64_t dpp64(int64_t v) {
+  const int lo = dpp32<CTRL>((int)(uint32_t)(uint64_t)v), hi = dpp32<CTRL>((int)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+__device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)v, lane);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)((uint64_t)v >> 32), lane);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int64_t max64(int64_t a, int64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ int64_t wave_max64(int64_t v) {
+  v = max64(v, dpp64<0xB1>(v));
+  v = max64(v, dpp64<0x4E>(v));
+  v = max64(v, dpp64<0x141>(v));
+  v = max64(v, dpp64<0x140>(v));
+  return max64(max64(readlane64(v, 0), readlane64(v, 16)), max64(readlane64(v, 32), readlane64(v, 48)));
+}
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {   // modulo 2^64
+  auto add = [](int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); };
+  v = add(v, dpp64<0xB1>(v));
+  v = add(v, dpp64<0x4E>(v));
+  v = add(v, dpp64<0x141>(v));
+  v = add(v, dpp64<0x140>(v));
+  return add(add(readlane64(v, 0), readlane64(v, 16)), add(readlane64(v, 32), readlane64(v, 48)));
 }
 
 // block reductions for blockDim.x a multiple of 64 (<= 1024); scratch holds >= 16 int64
 __device__ __forceinline__ int64_t block_max64(int64_t v, int64_t* scratch) {
   v = wave_max64(v);
-  int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) scratch[w] = v;
   __syncthreads();
   int64_t r = scratch[0];
-  for (int i = 1; i < nw; ++i) r = scratch[i] > r ? scratch[i] : r;
+#pragma unroll
+  for (int i = 1; i < 16; ++i) r = i < nw && scratch[i] > r ? scratch[i] : r;
   return r;
 }
 __device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t* scratch) {
   v = wave_sum64(v);
-  int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) scratch[w] = v;
   __syncthreads();
   uint64_t r = 0;
-  for (int i = 0; i < nw; ++i) r += (uint64_t)scratch[i];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r += i < nw ? (uint64_t)scratch[i] : 0;
   return (int64_t)r;
 }
 
-// Single-barrier block reductions: each call needs its own scratch array (no barrier protects a reused
+// Single-barrier block reductions: each call needs its own scratch array of 16 (no barrier protects a reused
 // one). bitlen(max |v|) = max bitlen(|v|), so the max reductions of qrow / irms run on 32-bit bit lengths.
 __device__ __forceinline__ int wave_max_i32(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const int w = __shfl_xor(v, o, 64);
-    v = w > v ? w : v;
-  }
-  return v;
+  auto mx = [](int a, int b) { return a > b ? a : b; };
+  v = mx(v, dpp32<0xB1>(v));
+  v = mx(v, dpp32<0x4E>(v));
+  v = mx(v, dpp32<0x141>(v));
+  v = mx(v, dpp32<0x140>(v));
+  return mx(mx(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+            mx(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 __device__ __forceinline__ int block_max_i32(int v, int* scratch) {
   v = wave_max_i32(v);
@@ -166,7 +189,8 @@ __device__ __forceinline__ int block_max_i32(int v, int* scratch) {
   __syncthreads();
   const int nw = blockDim.x >> 6;
   int r = scratch[0];
-  for (int i = 1; i < nw; ++i) r = scratch[i] > r ? scratch[i] : r;
+#pragma unroll
+  for (int i = 1; i < 16; ++i) r = i < nw && scratch[i] > r ? scratch[i] : r;
   return r;
 }
 __device__ __forceinline__ int64_t block_sum64_1(int64_t v, int64_t* scratch) {
@@ -175,7 +199,8 @@ __device__ __forceinline__ int64_t block_sum64_1(int64_t v, int64_t* scratch) {
   __syncthreads();
   const int nw = blockDim.x >> 6;
   uint64_t r = 0;
-  for (int i = 0; i < nw; ++i) r += (uint64_t)scratch[i];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r += i < nw ? (uint64_t)scratch[i] : 0;
   return (int64_t)r;
 }
 

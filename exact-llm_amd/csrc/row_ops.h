@@ -29,6 +29,16 @@ static __device__ __attribute__((noinline)) int64_t floordiv_general(int64_t a, 
   return b > 0 ? floordiv_pos(a, b) : floordiv64(a, b);
 }
 
+// 1 / b in float64 from the hardware reciprocal and two Newton steps (relative error far below 2^-40 for b >= 1);
+// the callers correct every quotient estimate made with it exactly.
+__device__ __forceinline__ double rcp_f64(double b) {
+  double r = __builtin_amdgcn_rcp(b);
+  double e = __builtin_fma(-b, r, 1.0);
+  r = __builtin_fma(r, e, r);
+  e = __builtin_fma(-b, r, 1.0);
+  return __builtin_fma(r, e, r);
+}
+
 // Round-half-up arithmetic shift right by a block-uniform 1 <= n <= 63, with int64 wrap (= shr64 there).
 __device__ __forceinline__ int64_t rsh_pos(int64_t a, int n) {
   return (int64_t)((uint64_t)a + (1ULL << (n - 1))) >> n;
@@ -59,6 +69,7 @@ __device__ __forceinline__ void norm_qrow_row(int r, int nt, const int64_t* x_in
                                               int D, int16_t* xl, int64_t* x_out, int64_t* clear, int32_t* __restrict__ s_out,
                                               void* xq_out, int8_t* x8, RowScratch& sc) {
   const int tid = threadIdx.x;
+  const double rD = rcp_f64((double)D);   // off the critical path: ready before the sum of squares
   const int64_t* xr = x_in + (int64_t)r * D;
   const int64_t* tr = res_t ? res_t + (int64_t)r * D : nullptr;
   int64_t v[EPT], gv[EPT];
@@ -117,13 +128,20 @@ __device__ __forceinline__ void norm_qrow_row(int r, int nt, const int64_t* x_in
       ss += (int64_t)xs * xs;
     }
   }
-  ss = block_sum64_1(ss, sc.b);
-  const int64_t ms = floordiv_pos(ss, D) + 1;
-  int64_t rt = isqrt64(ms);
+  ss = block_sum64_1(ss, sc.b);   // 0 <= ss < 2^62 (squares of at most 2^48, D of at most 2^13)
+  // ms = ss // D + 1 and rt = isqrt(ms): float64 estimates (a reciprocal prepared early, the hardware square root),
+  // each corrected exactly; the scalar chain is short because it sits between two block reductions
+  int64_t qm = (int64_t)((double)ss * rD), rm = ss - qm * D;
+  while (rm < 0) { --qm; rm += D; }
+  while (rm >= D) { ++qm; rm -= D; }
+  const int64_t ms = qm + 1;
+  int64_t rt = (int64_t)__builtin_amdgcn_sqrt((double)ms);
+  while (rt > 0 && rt * rt > ms) --rt;
+  while ((rt + 1) * (rt + 1) <= ms) ++rt;
   if (rt < 1) rt = 1;
   const int64_t den = shl64(rt, k);
   const bool fast = den > 0 && den <= (1LL << 62);
-  const double rden = 1.0 / (double)den;
+  const double rden = rcp_f64((double)den);
   int yq[EPT];
   bool bad = !fast;
 #pragma unroll
