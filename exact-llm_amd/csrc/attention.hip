@@ -237,9 +237,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
   extern __shared__ int64_t sc[];   // Smax entries
   __shared__ int64_t y[3][256];     // q head, new key, new value: shr(t, 28 - s) + b
   __shared__ int32_t qs[256], kn[256];
+  __shared__ __attribute__((aligned(16))) int32_t texp[EXACT_EXP_N + 2];
   __shared__ int32_t shq[2];
-  __shared__ int ored[ATT_THREADS / 64];
-  __shared__ int64_t red[16];
+  __shared__ int ored[16];
+  __shared__ int64_t red[16], red2[16];
   __shared__ int64_t part[ATT_THREADS * 2];
   const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = H / KV, kh = h / grp;
@@ -279,6 +280,18 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
       cs[i][0] = j < hd ? cos_t[(int64_t)p * hd + j] : 0;
       cs[i][1] = j < hd ? sin_t[(int64_t)p * hd + j] : 0;
     }
+  }
+  {   // the exp table into LDS: every piece loaded before the first store, with the loads above
+    constexpr int NV = EXACT_EXP_N / 4, NK = (NV + ATT_THREADS - 1) / ATT_THREADS;
+    v4i te[NK];
+#pragma unroll
+    for (int k = 0; k < NK; ++k)
+      if (tid + k * ATT_THREADS < NV) te[k] = reinterpret_cast<const v4i*>(expt)[tid + k * ATT_THREADS];
+    const int tail = tid < EXACT_EXP_N - 4 * NV ? expt[4 * NV + tid] : 0;
+#pragma unroll
+    for (int k = 0; k < NK; ++k)
+      if (tid + k * ATT_THREADS < NV) reinterpret_cast<v4i*>(texp)[tid + k * ATT_THREADS] = te[k];
+    if (tid < EXACT_EXP_N - 4 * NV) texp[4 * NV + tid] = tail;
   }
   const int sh = 28 - s[r];
   for (int j = tid; j < 3 * hd; j += blockDim.x) {
@@ -369,15 +382,16 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
     sc[p] = val;
     mx = val > mx ? val : mx;
   }
-  mx = block_max64(mx, red);
+  mx = block_max64_1(mx, red);
   int64_t es = 0;
   for (int si = tid; si < S; si += blockDim.x) {
-    const int64_t e = lut_exp(expt, mx - sc[si]);
+    const int64_t e = lut_exp(texp, mx - sc[si]);
     sc[si] = e;
     es += e;
   }
-  es = block_sum64(es, red);
-  for (int si = tid; si < S; si += blockDim.x) sc[si] = floordiv_pos(shl64(sc[si], 20), es);
+  es = block_sum64_1(es, red2);
+  const double res = 1.0 / (double)es;   // one reciprocal; each quotient estimate is corrected exactly
+  for (int si = tid; si < S; si += blockDim.x) sc[si] = floordiv_rcp(shl64(sc[si], 20), es, res);
   __syncthreads();
   int64_t a0 = 0, a1 = 0;
   if (pp < nparts) {
@@ -433,6 +447,7 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
   if (!t || !s || !cos_t || !sin_t || !slot || !pos || !kq || !sk || !v || !exp_t || !out) return EXACT_E_ARG;
   if (R <= 0 || H <= 0 || KV <= 0 || H % KV || hd <= 0 || Smax <= 0) return EXACT_E_ARG;
   if (hd > 256 || hd % 8 || (2 * ATT_THREADS) % hd || Smax > 8192) return EXACT_E_UNSUPPORTED;
+  if (reinterpret_cast<uintptr_t>(exp_t) & 15) return EXACT_E_ARG;   // staged into LDS in 16-byte pieces
   static bool attr_set = false;
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF>),

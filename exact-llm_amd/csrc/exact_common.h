@@ -54,8 +54,10 @@ __device__ __forceinline__ int64_t floordiv64(int64_t a, int64_t b) {
 
 // floor(a / b) for b > 0: a float64 estimate of the quotient, then an exact integer correction of the
 // remainder into [0, b). Exact for every int64 a (the estimate only bounds the number of correction
-// steps: one or two whenever |a / b| < 2^50, which covers every use here).
+// steps: one or two whenever |a / b| < 2^50, which covers every use here). b <= 0 (a softmax sum of an exp table
+// without a positive entry 0, say) gives 0 rather than a correction loop that would not end.
 __device__ __forceinline__ int64_t floordiv_pos(int64_t a, int64_t b) {
+  if (b <= 0) return 0;
   double qd = __builtin_floor((double)a / (double)b);
   qd = qd > 9.2e18 ? 9.2e18 : (qd < -9.2e18 ? -9.2e18 : qd);
   int64_t q = (int64_t)qd;
@@ -68,6 +70,7 @@ __device__ __forceinline__ int64_t floordiv_pos(int64_t a, int64_t b) {
 // floor(a / b) for b > 0 given rb ~ 1 / b (one reciprocal for many divisions by the same b): the estimate is
 // corrected exactly, as in floordiv_pos
 __device__ __forceinline__ int64_t floordiv_rcp(int64_t a, int64_t b, double rb) {
+  if (b <= 0) return 0;   // as floordiv_pos
   double qd = __builtin_floor((double)a * rb);
   qd = qd > 9.2e18 ? 9.2e18 : (qd < -9.2e18 ? -9.2e18 : qd);
   int64_t q = (int64_t)qd;
@@ -173,7 +176,18 @@ __device__ __forceinline__ int64_t block_sum64(int64_t v, int64_t* scratch) {
 }
 
 // Single-barrier block reductions: each call needs its own scratch array of 16 (no barrier protects a reused
-// one). bitlen(max |v|) = max bitlen(|v|), so the max reductions of qrow / irms run on 32-bit bit lengths.
+// one).
+__device__ __forceinline__ int64_t block_max64_1(int64_t v, int64_t* scratch) {
+  v = wave_max64(v);
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const int nw = blockDim.x >> 6;
+  int64_t r = scratch[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) r = i < nw && scratch[i] > r ? scratch[i] : r;
+  return r;
+}
+// bitlen(max |v|) = max bitlen(|v|), so the max reductions of qrow / irms run on 32-bit bit lengths.
 __device__ __forceinline__ int wave_max_i32(int v) {
   auto mx = [](int a, int b) { return a > b ? a : b; };
   v = mx(v, dpp32<0xB1>(v));
