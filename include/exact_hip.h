@@ -240,7 +240,8 @@ int exact_attention(const int16_t* qq, const int32_t* sq, const int16_t* kq, con
  * (slot, position): one row, or rows of different sequences (rows of one sequence in one pass read each
  * other's new keys and take the two launches). Same results, cache contents and obits; the quantised
  * queries stay on chip (no qq / sq) and t is left unchanged. Replaces the per-layer q/k/v epilogue + RoPE +
- * cache write + attention of exact_llm.py:170-176 / speed_fair_kaggle.py:603-624 at decode. */
+ * cache write + attention of exact_llm.py:170-176 / speed_fair_kaggle.py:603-624 at decode. exp_t 16-byte
+ * aligned (staged into LDS). */
 int exact_attention_qkv(const int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
                         const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* kq, int32_t* sk,
                         int64_t* v, const int32_t* exp_t, int64_t* out, int32_t* obits, int32_t R, int32_t H,
