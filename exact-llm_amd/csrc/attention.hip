@@ -8,6 +8,12 @@
 #include "abi_util.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef short s2v __attribute__((ext_vector_type(2)));
+
+// a.lo b.lo + a.hi b.hi of two int16 pairs (v_dot2_i32_i16): exact in int32 for |a|, |b| <= 32767
+__device__ __forceinline__ int dot2(int a, int b) {
+  return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2v, a), __builtin_bit_cast(s2v, b), 0, false);
+}
 
 namespace exact {
 
@@ -237,6 +243,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
   extern __shared__ int64_t sc[];   // Smax entries
   __shared__ int64_t y[3][256];     // q head, new key, new value: shr(t, 28 - s) + b
   __shared__ int32_t qs[256], kn[256];
+  __shared__ __attribute__((aligned(16))) int16_t qs16[256];   // the query head again as int16, pairs for v_dot2
   __shared__ __attribute__((aligned(16))) int32_t texp[EXACT_EXP_N + 2];
   __shared__ int32_t shq[2];
   __shared__ int ored[16];
@@ -327,6 +334,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
       if (j < hd) {
         const int64_t w = shr64(z[i], q);
         dst[j] = (int32_t)(w > 32767 ? 32767 : (w < -32767 ? -32767 : w));
+        if (wave == 0) qs16[j] = (int16_t)dst[j];
       }
     }
     if (lane == 0) shq[wave] = q;
@@ -350,24 +358,18 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
 #pragma unroll
       for (int j8 = 0; j8 < ATT_KPF; ++j8) {
         if (j8 < hd / 8) {
-          const v4i kk = kpre[j8];
+          const v4i kk = kpre[j8], qq = reinterpret_cast<const v4i*>(qs16)[j8];
 #pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const int j = j8 * 8 + 2 * c;
-            dot += (int64_t)(qs[j] * (int32_t)(int16_t)(kk[c] & 0xffff) + qs[j + 1] * (int32_t)(int16_t)(kk[c] >> 16));
-          }
+          for (int c = 0; c < 4; ++c) dot += (int64_t)dot2(qq[c], kk[c]);
         }
       }
       skv = skpre;
     } else {
 #pragma unroll 4
       for (int j8 = 0; j8 < hd / 8; ++j8) {
-        const v4i kk = kr[j8];
+        const v4i kk = kr[j8], qq = reinterpret_cast<const v4i*>(qs16)[j8];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const int j = j8 * 8 + 2 * c;
-          dot += (int64_t)(qs[j] * (int32_t)(int16_t)(kk[c] & 0xffff) + qs[j + 1] * (int32_t)(int16_t)(kk[c] >> 16));
-        }
+        for (int c = 0; c < 4; ++c) dot += (int64_t)dot2(qq[c], kk[c]);
       }
       skv = sk[cbase + si];
     }
@@ -375,12 +377,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
     sc[si] = val;
     mx = val > mx ? val : mx;
   }
-  if (tid == (p % blockDim.x)) {   // the new key, from LDS
-    int64_t dot = 0;
-    for (int j = 0; j < hd; j += 2) dot += (int64_t)(qs[j] * kn[j] + qs[j + 1] * kn[j + 1]);
-    const int64_t val = shr64(dot * INV, 32 - sqv - skn);
-    sc[p] = val;
-    mx = val > mx ? val : mx;
+  if (wave == (int)(p % blockDim.x) >> 6) {   // the new key, from LDS: the wave of thread p % blockDim.x, lanes over dims
+    int64_t part = 0;
+    for (int j = lane; j < hd; j += 64) part += (int64_t)qs[j] * kn[j];   // exact: |q k| < 2^30, 256 of them
+    const int64_t dot = wave_sum64(part);
+    if (tid == (int)(p % blockDim.x)) {   // that thread owns sc[p] in the loops below
+      const int64_t val = shr64(dot * INV, 32 - sqv - skn);
+      sc[p] = val;
+      mx = val > mx ? val : mx;
+    }
   }
   mx = block_max64_1(mx, red);
   int64_t es = 0;
