@@ -148,6 +148,27 @@ def test_prefill_with_unfit_exp_table_matches_row_kernel(change):
     assert np.array_equal(host(obits), host(refbits))
 
 
+def test_attention_with_zero_exp_table_gives_zero_rows():
+    """An exp table of zeros makes every softmax sum 0; numpy's int64 floor division by zero gives 0 (with a
+    warning), so p = 0 and every output is 0. The kernels' divisions return 0 for a non-positive divisor rather
+    than running a correction loop without end: the row kernel and the matrix-core prefill on the same case."""
+    H, KV, hd, nkeys, R, slot = 4, 2, 128, 120, 120, 1
+    case = make_case(5, 2, slot, H, KV, hd, 192, nkeys, R, "small")
+    cache, qq, sq, pos = to_dev(*case)
+    T = torch.zeros(len(exp_t()), dtype=I32, device=DEV)
+    with np.errstate(divide="ignore"):
+        assert (np.array([7], np.int64) << 20) // np.array([0], np.int64) == 0   # the reference's numpy behaviour
+    out = torch.full((R, H * hd), -7, dtype=I64, device=DEV)
+    obits = torch.full((R, H), -1, dtype=I32, device=DEV)
+    ops.attention(qq, sq, cache, torch.full((R,), slot, dtype=I32, device=DEV), pos, T, out, H, KV, hd,
+                  O.inv_sqrt_hd(hd), obits)
+    assert not host(out).any() and not host(obits).any()
+    out2 = torch.full((R, H * hd), -7, dtype=I64, device=DEV)
+    ws = ops.prefill_workspace(R, H, KV, hd, nkeys, DEV)
+    ops.attention_prefill(qq, sq, cache, slot, pos, nkeys, T, out2, H, KV, hd, O.inv_sqrt_hd(hd), ws, obits)
+    assert not host(out2).any() and not host(obits).any()
+
+
 @pytest.mark.parametrize("H,KV,hd,R,bias,Smax", [(28, 4, 128, 1, True, 96), (28, 4, 128, 4, False, 96),
                                                  (14, 2, 64, 3, True, 96), (4, 4, 256, 2, True, 96),
                                                  (8, 2, 128, 2, True, 8192)])
