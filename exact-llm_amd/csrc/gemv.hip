@@ -73,12 +73,13 @@ __device__ __forceinline__ void load_tile(GroupRegs& G_, const int8_t* __restric
     }
 }
 
-// A-operand bytes of group g. xrow: this lane's activation row (any valid row when the lane's row is unused);
-// valid: row < R. xrow may point into LDS (a wave's quantised slice, offset so that group g sits at g * 128).
+// A-operand bytes of group g. xrow: this lane's activation row (any valid row when the lane's row is unused: the
+// lane's A row is zeroed in compute_group, after the data has arrived; zeroing the registers here, while the loads
+// are in flight, made the compiler wait for every outstanding load of the wave, the prefetched tile included).
+// xrow may point into LDS (a wave's quantised slice, offset so that group g sits at g * 128).
 template <int ABITS>
-__device__ __forceinline__ void load_x(GroupRegs& G_, const int8_t* xrow, bool valid, int g, int c) {
+__device__ __forceinline__ void load_x(GroupRegs& G_, const int8_t* xrow, int g, int c) {
   const int kb = g * 128 + 16 * c;
-  const v4i zero = {0, 0, 0, 0};
   if (ABITS == 15) {
     const int16_t* xp = reinterpret_cast<const int16_t*>(xrow) + kb;
 #pragma unroll
@@ -86,14 +87,10 @@ __device__ __forceinline__ void load_x(GroupRegs& G_, const int8_t* xrow, bool v
       G_.xa[2 * h] = *reinterpret_cast<const v4i*>(xp + 64 * h);
       G_.xa[2 * h + 1] = *reinterpret_cast<const v4i*>(xp + 64 * h + 8);
     }
-    if (!valid)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) G_.xa[i] = zero;
   } else {
     const int8_t* xp = xrow + kb;
 #pragma unroll
     for (int h = 0; h < 2; ++h) G_.xa[h] = *reinterpret_cast<const v4i*>(xp + 64 * h);
-    if (!valid) G_.xa[0] = G_.xa[1] = zero;
   }
 }
 
@@ -103,14 +100,16 @@ __device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restri
                                            const int16_t* __restrict__ mh, const int8_t* xrow, bool valid,
                                            size_t tile, int g, int row, int c) {
   load_scales<WIDE>(G_, mp, mh, tile, row);
-  load_x<ABITS>(G_, xrow, valid, g, c);
+  load_x<ABITS>(G_, xrow, g, c);
   load_tile<NT>(G_, wp, tile, row, c);
 }
 
 // CT: int16 rows without the all-ones row; the caller adds 128 colterm (sum_g colsum_g M_g) once instead, so
 // all 16 A rows carry activations.
+// valid: the lane's A row is an activation row (row < R); other rows are zero, except the all-ones row R.
 template <int ABITS, int VR, bool CT = false>
-__device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc)[4][VR], int R, int row, int lane) {
+__device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc)[4][VR], int R, int row, int lane,
+                                              bool valid) {
   const v4i zero = {0, 0, 0, 0};
   const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
   v4i ahi[2], alo[2];
@@ -118,9 +117,12 @@ __device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc
   for (int h = 0; h < 2; ++h) {
     if (ABITS == 15) {
       split_a16(G_.xa[2 * h], G_.xa[2 * h + 1], ahi[h], alo[h]);
-      if (!CT && row == R) alo[h] = ones;   // all-ones row: colsum(W) in the lo pass
+      if (!valid) {
+        ahi[h] = zero;
+        alo[h] = (!CT && row == R) ? ones : zero;   // all-ones row: colsum(W) in the lo pass
+      }
     } else {
-      ahi[h] = G_.xa[h];
+      ahi[h] = valid ? G_.xa[h] : zero;
       alo[h] = zero;
     }
   }
@@ -174,21 +176,21 @@ __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t*
     }
     pro();
     if (g0 >= g1) return;
-    load_x<ABITS>(ra, xrow, valid, g0, c);
+    load_x<ABITS>(ra, xrow, g0, c);
   }
   int g = g0;
   for (; g + 2 < g1; g += 2) {
     load_group<ABITS, NT, WIDE>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
-    compute_group<ABITS, VR, CT>(ra, acc, R, row, lane);
+    compute_group<ABITS, VR, CT>(ra, acc, R, row, lane, valid);
     load_group<ABITS, NT, WIDE>(ra, wp, mp, mh, xrow, valid, tile_index(nb, g + 2, nbs, G), g + 2, row, c);
-    compute_group<ABITS, VR, CT>(rb, acc, R, row, lane);
+    compute_group<ABITS, VR, CT>(rb, acc, R, row, lane, valid);
   }
   if (g + 1 < g1) {
     load_group<ABITS, NT, WIDE>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
-    compute_group<ABITS, VR, CT>(ra, acc, R, row, lane);
-    compute_group<ABITS, VR, CT>(rb, acc, R, row, lane);
+    compute_group<ABITS, VR, CT>(ra, acc, R, row, lane, valid);
+    compute_group<ABITS, VR, CT>(rb, acc, R, row, lane, valid);
   } else {
-    compute_group<ABITS, VR, CT>(ra, acc, R, row, lane);
+    compute_group<ABITS, VR, CT>(ra, acc, R, row, lane, valid);
   }
 }
 
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ 
 // kernel wrote it (attention's per-head bit lengths, or SwiGLU's per-slice ones). Each wave quantises the columns of
 // its own groups into LDS (xs[r][g0 * 128 ...g1 * 128), clipped to +-(2^abits - 1)) and runs the group loop on them;
 // block 0 writes s_out. Replaces a k_quant_rows launch + GEMV pair. t += x.W (accumulate).
-template <int ABITS, bool NT, int VR, bool WIDE>
+template <int ABITS, bool NT, int VR, bool WIDE, int PL>
 __global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict__ xs, int64_t ldx,
                                                       const int32_t* __restrict__ part, int nparts,
                                                       const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
@@ -270,11 +272,16 @@ __global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict_
   auto quantise = [&]() {
     const int64_t lim = (1LL << ABITS) - 1;
     for (int r = 0; r < R; ++r) {
-      const int pv = lane < nparts ? part[(int64_t)r * nparts + lane] : 0;
+      int pw[PL];   // up to 64 PL slice bit lengths, all loads issued before the first use
+#pragma unroll
+      for (int k = 0; k < PL; ++k) pw[k] = lane + 64 * k < nparts ? part[(int64_t)r * nparts + lane + 64 * k] : 0;
       const int64_t* src = xs + (int64_t)r * ldx + (int64_t)g0 * 128;
       int64_t xv[XQ_LOADS];
 #pragma unroll
       for (int j = 0; j < XQ_LOADS; ++j) xv[j] = lane + 64 * j < ncol ? src[lane + 64 * j] : 0;
+      int pv = pw[0];
+#pragma unroll
+      for (int k = 1; k < PL; ++k) pv = pw[k] > pv ? pw[k] : pv;
       const int m = wave_max_i32(pv);
       const int sh = m - ABITS > 0 ? m - ABITS : 0;
       if (blockIdx.x == 0 && wave == 0 && lane == 0) s_out[r] = sh;
@@ -306,6 +313,134 @@ __global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict_
       const int r = 4 * c + v;
       if (r < R && n < N) atomicAdd(reinterpret_cast<unsigned long long*>(t + (size_t)r * N + n), (unsigned long long)acc[q][v]);
     }
+  }
+}
+
+// Operands of group g for one wave of the gate|up GEMV below: slots j = 0, 1 are sub-tiles qb, qb + 1 of the gate
+// tile tg, slots 2, 3 the same sub-tiles of the up tile tu (a sub-tile is the 16 rows at byte 256 q of each 1 KiB
+// chunk of the 8 KiB tile).
+template <bool NT, bool WIDE>
+__device__ __forceinline__ void load_gu_group(GroupRegs& G_, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                              const int16_t* __restrict__ mh, const int8_t* xrow, size_t tg, size_t tu,
+                                              int qb, int g, int row, int c) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const size_t o = (j < 2 ? tg : tu) * 64 + 16 * (qb + (j & 1)) + row;
+    G_.m[j] = mp[o];
+    if constexpr (WIDE) G_.m[j] |= (int)mh[o] << 15;
+  }
+  load_x<15>(G_, xrow, g, c);
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int8_t* base = wp + (j < 2 ? tg : tu) * 8192;
+      const v4i* a = reinterpret_cast<const v4i*>(base + h * 4096 + c * 1024 + (qb + (j & 1)) * 256 + row * 16);
+      G_.b[4 * h + j] = NT ? __builtin_nontemporal_load(a) : *a;
+    }
+}
+
+// Gate|up GEMV with the SwiGLU as its epilogue (decode rows, R <= 4, int16 activations). The linear holds the gate rows
+// [0, I) and the up rows [I, 2I), I a multiple of 64. A pair is 32 gate columns (sub-tiles qb, qb + 1 of a 64-row tile)
+// with the matching up columns; block b owns pairs b * NPB .. + NPB with NPB * KS waves: wave w = (pair p = w % NPB,
+// k part kp = w / NPB) runs the group loop over its share of the groups for the pair's gate and up sub-tiles, so one lane
+// holds a gate total and the up total of the same column. The k parts combine in LDS (no atomics, no zero-filled
+// totals); the kp = 0 waves store h = shr(isilu(shr(g, 28 - s)) * shr(u, 28 - s), F) (exact_llm.py:179, as
+// k_swiglu_part) and the block's bit length of max |h| per row in part[r * gridDim.x + b], which the quantising down
+// GEMV reads. tout (optional, (R, 2I)) receives the gate|up totals. Small blocks (NPB 1, KS 2: 2 I / 32 waves of 64
+// lanes) spread the waves over the CUs better than larger ones (7B bs1 decode: 4-wave blocks of 64 columns 2311 us a
+// step, 2-wave blocks of 32 columns 2194-2218, against 2311 for the GEMV + SwiGLU launches).
+template <bool NT, int VR, int NPB, int KS, bool WIDE>
+__global__ __launch_bounds__(64 * NPB * KS) void k_gemv_gu_swiglu(const int16_t* __restrict__ x, const int8_t* __restrict__ wp,
+                                                             const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
+                                                             const int32_t* __restrict__ s, const int32_t* __restrict__ silu,
+                                                             int64_t* __restrict__ hout, int32_t* __restrict__ part,
+                                                             int64_t* __restrict__ tout, int R, int I, int K, int G) {
+  __shared__ int64_t cmb[KS > 1 ? (KS - 1) * NPB * 4 * VR * 64 : 1];
+  __shared__ int pm[NPB][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int p = wave % NPB, kp = wave / NPB;
+  const int pair = blockIdx.x * NPB + p;   // 32 gate columns: sub-tiles qb, qb + 1 of 64-column tile nb
+  const int nb = pair >> 1, qb = 2 * (pair & 1), nbs = (2 * I) >> 6, ub = I >> 6;
+  const int g0 = (int)(((int64_t)kp * G) / KS), g1 = (int)(((int64_t)(kp + 1) * G) / KS);
+  const int row = lane & 15, c = lane >> 4;
+  const bool valid = row < R;
+  const int8_t* xrow = reinterpret_cast<const int8_t*>(x + (size_t)(valid ? row : 0) * K);
+  int64_t acc[4][VR];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int v = 0; v < VR; ++v) acc[j][v] = 0;
+  if (g0 < g1) {   // two groups in flight, as gemv_groups
+    GroupRegs ra, rb;
+    auto ld = [&](GroupRegs& G_, int g) {
+      load_gu_group<NT, WIDE>(G_, wp, mp, mh, xrow, tile_index(nb, g, nbs, G), tile_index(ub + nb, g, nbs, G), qb, g, row, c);
+    };
+    ld(ra, g0);
+    int g = g0;
+    for (; g + 2 < g1; g += 2) {
+      ld(rb, g + 1);
+      compute_group<15, VR>(ra, acc, R, row, lane, valid);
+      ld(ra, g + 2);
+      compute_group<15, VR>(rb, acc, R, row, lane, valid);
+    }
+    if (g + 1 < g1) {
+      ld(rb, g + 1);
+      compute_group<15, VR>(ra, acc, R, row, lane, valid);
+      compute_group<15, VR>(rb, acc, R, row, lane, valid);
+    } else {
+      compute_group<15, VR>(ra, acc, R, row, lane, valid);
+    }
+  }
+  if constexpr (KS > 1) {
+    if (kp > 0)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < VR; ++v) cmb[((((kp - 1) * NPB + p) * 4 + j) * VR + v) * 64 + lane] = acc[j][v];
+    __syncthreads();
+    if (kp == 0)
+#pragma unroll
+      for (int k = 1; k < KS; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int v = 0; v < VR; ++v) acc[j][v] += cmb[((((k - 1) * NPB + p) * 4 + j) * VR + v) * 64 + lane];
+  }
+  if (kp == 0) {
+    // lane (row, c) holds activation row 4c + v of gate|up column row: rows below R <= 4 sit in the lanes of c = 0
+    int bl[VR];
+#pragma unroll
+    for (int v = 0; v < VR; ++v) {
+      bl[v] = 0;
+      if (c == 0 && v < R) {
+        const int sh = 28 - s[v];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int i = nb * 64 + 16 * (qb + j) + row;
+          const int64_t gt = acc[j][v], ut = acc[2 + j][v];
+          const int64_t hv = shr64(lut16(silu, shr64(gt, sh), false) * shr64(ut, sh), EXACT_F);
+          hout[(size_t)v * I + i] = hv;
+          if (tout) {
+            tout[(size_t)v * 2 * I + i] = gt;
+            tout[(size_t)v * 2 * I + I + i] = ut;
+          }
+          const int b = bitlen64(abs64(hv));
+          bl[v] = b > bl[v] ? b : bl[v];
+        }
+      }
+      bl[v] = wave_max_i32(bl[v]);
+    }
+    if (lane == 0)
+#pragma unroll
+      for (int v = 0; v < VR; ++v) pm[p][v] = bl[v];
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < R) {
+    int a = pm[0][threadIdx.x];
+#pragma unroll
+    for (int q = 1; q < NPB; ++q) a = pm[q][threadIdx.x] > a ? pm[q][threadIdx.x] : a;
+    part[(size_t)threadIdx.x * gridDim.x + blockIdx.x] = a;
   }
 }
 
@@ -724,6 +859,8 @@ extern "C" int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, con
 
 // LDS of the quantised slices: 4 waves x R rows x gmax groups x 128 values
 #define GEMV_XQ_LDS_MAX (64 * 1024)
+// slice bit lengths per row beyond 64 (the SwiGLU GEMV writes one per 32 or 64 columns): up to 64 * XQ_PARTS_WIDE
+#define XQ_PARTS_WIDE 16
 
 extern "C" int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const int32_t* part, int32_t nparts, int32_t abits,
                                         const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int32_t* s_out,
@@ -737,18 +874,23 @@ extern "C" int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const in
   const int nsplit = gemv_nsplit(N, G);
   const int gmax = (G + nsplit - 1) / nsplit;
   const size_t lds = (size_t)4 * R * gmax * 128 * (abits == 15 ? 2 : 1);
-  if (lds > GEMV_XQ_LDS_MAX || gmax * 128 > 64 * XQ_LOADS || nparts > 64) return EXACT_E_UNSUPPORTED;
+  if (lds > GEMV_XQ_LDS_MAX || gmax * 128 > 64 * XQ_LOADS || nparts > 64 * XQ_PARTS_WIDE) return EXACT_E_UNSUPPORTED;
   const int tasks = ((N + 63) / 64) * nsplit;
   dim3 grid((tasks + 3) / 4), block(256);
   hipStream_t st = as_stream(stream);
-#define XQ_GO(AB, VR)                                                                                                  \
+#define XQ_GO_PL(AB, VR, PL)                                                                                           \
   do {                                                                                                                 \
     if (mh)                                                                                                            \
-      hipLaunchKernelGGL((k_gemv_g128_xq<AB, GEMV_NT != 0, VR, true>), grid, block, lds, st, xs, ldx, part, nparts, wp, mp, \
-                         mh, t, s_out, R, N, K, G, nsplit, gmax, zero, zero_n);                                        \
-    else                                                                                                               \
-      hipLaunchKernelGGL((k_gemv_g128_xq<AB, GEMV_NT != 0, VR, false>), grid, block, lds, st, xs, ldx, part, nparts, wp,   \
+      hipLaunchKernelGGL((k_gemv_g128_xq<AB, GEMV_NT != 0, VR, true, PL>), grid, block, lds, st, xs, ldx, part, nparts, wp, \
                          mp, mh, t, s_out, R, N, K, G, nsplit, gmax, zero, zero_n);                                    \
+    else                                                                                                               \
+      hipLaunchKernelGGL((k_gemv_g128_xq<AB, GEMV_NT != 0, VR, false, PL>), grid, block, lds, st, xs, ldx, part, nparts,   \
+                         wp, mp, mh, t, s_out, R, N, K, G, nsplit, gmax, zero, zero_n);                                \
+  } while (0)
+#define XQ_GO(AB, VR)                                                                                                  \
+  do {                                                                                                                 \
+    if (nparts <= 64) XQ_GO_PL(AB, VR, 1);                                                                             \
+    else XQ_GO_PL(AB, VR, XQ_PARTS_WIDE);                                                                              \
   } while (0)
   const int vr = R <= 1 ? 1 : (R <= 2 ? 2 : 4);
   if (abits == 15) {
@@ -757,7 +899,39 @@ extern "C" int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const in
     if (vr == 1) XQ_GO(7, 1); else if (vr == 2) XQ_GO(7, 2); else XQ_GO(7, 4);
   }
 #undef XQ_GO
+#undef XQ_GO_PL
   return launch_status("gemv_g128_qrow_acc");
+}
+
+// The SwiGLU GEMV's blocks: GEMV_GU_NPB pairs of 32 gate columns (one slice bit length per block) x GEMV_GU_KS k parts
+#ifndef GEMV_GU_KS
+#define GEMV_GU_KS 2
+#endif
+#ifndef GEMV_GU_NPB
+#define GEMV_GU_NPB 1
+#endif
+
+extern "C" int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                                      const int32_t* s, const int32_t* silu, int64_t* h, int32_t* part, int64_t* t,
+                                      int32_t R, int32_t I, int32_t K, void* stream) {
+  if (!x || !wp || !mp || !s || !silu || !h || !part || R <= 0 || I <= 0 || K <= 0) return EXACT_E_ARG;
+  if (R > 4 || I % 64 || K % 128) return EXACT_E_UNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(wp) & 15)) return EXACT_E_UNSUPPORTED;
+  const int G = K / 128;
+  dim3 grid((unsigned)(I / (32 * GEMV_GU_NPB))), block(64 * GEMV_GU_NPB * GEMV_GU_KS);
+  hipStream_t st = as_stream(stream);
+#define GU_GO(VR)                                                                                                      \
+  do {                                                                                                                 \
+    if (mh)                                                                                                            \
+      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, GEMV_GU_NPB, GEMV_GU_KS, true>), grid, block, 0, st, x, wp, mp, mh, s, silu, \
+                         h, part, t, R, I, K, G);                                                                      \
+    else                                                                                                               \
+      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, GEMV_GU_NPB, GEMV_GU_KS, false>), grid, block, 0, st, x, wp, mp, mh, s,    \
+                         silu, h, part, t, R, I, K, G);                                                                \
+  } while (0)
+  if (R == 1) GU_GO(1); else if (R == 2) GU_GO(2); else GU_GO(4);
+#undef GU_GO
+  return launch_status("gemv_g128_swiglu");
 }
 
 static int gemm_entry(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,

@@ -29,6 +29,7 @@ SIGNATURES = {
     "exact_gemm_g128_a16_zeroed": [P, P, P, P, P, P, P, I32, I32, I32, P],
     "exact_gemm_g128_digits": [P, P, P, P, P, P, I32, I32, I32, I32, P],
     "exact_gemv_g128_qrow_acc": [P, I64, P, I32, I32, P, P, P, P, P, I32, I32, I32, P, I64, P],
+    "exact_gemv_g128_swiglu": [P, P, P, P, P, P, P, P, P, I32, I32, I32, P],
     "exact_gemv_g128_norm_acc": [P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, P],
     "exact_requant_group": [P, P, P, P, I32, I32, P],
     "exact_requant_channel": [P, P, P, I32, P, P, I32, I32, P],

@@ -213,7 +213,9 @@ class Workspace:
         self.t_d, self.t_head = self.t_qd[R * nq:].view(R, D), z(R, V)
         self.logits, self.next_ids = z(R, V), z(R, dt=I32)
         self.s28 = torch.full((R,), 28, dtype=I32, device=device)
-        self.part_sw = ops.swiglu_parts(R, max(I, cfg.SI if cfg.moe else 0), device)
+        # slice bit lengths of the SwiGLU rows: per 1024 columns (exact_swiglu_qrow) or per 32 or 64
+        # (exact_gemv_g128_swiglu)
+        self.part_sw = z(R * -(-max(I, cfg.SI if cfg.moe else 0) // 32), dt=I32)
         self.part_lg = ops.logits_parts(R, V, device)
         self.obits = z(R, H, dt=I32)
         self.ids, self.slot, self.pos = z(R, dt=I32), z(R, dt=I32), z(R, dt=I32)
@@ -323,7 +325,11 @@ class TModel:
         # gate|up, head), which read one residual buffer and write the other
         nfuse = (afuse and self.abits == 15 and not c.moe and R <= ops.NORM_FUSE_ROWS and D <= self.NORM_FUSE_D
                  and self.w.head.mode == "group")
-        if xfuse and ws.h is None and (c.I > 8192 or nfuse) and not c.moe:
+        # decode rows of dense int16 models whose gate|up GEMV is not the norm-fused one: the SwiGLU runs in the gate|up
+        # GEMV's epilogue (no totals, no atomics, one launch fewer)
+        sfuse = (xfuse and not nfuse and not c.moe and self.abits == 15 and R <= ops.SWIGLU_GEMV_ROWS and c.I % 64 == 0
+                 and c.I // ops.SWIGLU_PART_COLS <= ops.XQ_PARTS_MAX and self.w.layers[0]["gateup"].bias is None)
+        if xfuse and ws.h is None and (c.I > 8192 or nfuse or sfuse) and not c.moe:
             ws.h = torch.zeros((R, ws.I), dtype=I64, device=self.dev)
         x_cur, x_nxt = ws.x, ws.x2
         ops.embed(ws.ids, self.w.emb, ws.x)
@@ -398,7 +404,11 @@ class TModel:
                 self._moe(ws, L, dx, dh)
                 res_t, res_s = None, None
                 continue
-            if group:
+            if sfuse:
+                ops.gemv_swiglu(ws.xq, L["gateup"], ws.s, tab.silu, ws.h, ws.part_sw, t=t_gu if keep else None)
+                ops.gemv_qrow_acc(ws.h, ws.part_sw, c.I // ops.SWIGLU_PART_COLS, self.abits, L["down"], t_d, ws.sh)
+                res_t, res_s = t_d, ws.sh
+            elif group:
                 self._lin(ws.xq, L["gateup"], t_gu, x8=dx)
                 if xfuse and c.I > 8192:   # rows beyond one workgroup: SwiGLU slices, then the down GEMV quantises
                     ops.swiglu_part(t_gu, ws.s, tab.silu, ws.h, ws.part_sw, clear=clear)

@@ -144,6 +144,27 @@ def gemv_qrow_acc(xs, part, nparts, abits, lin, out, s_out, K=None, zero=None):
     return out
 
 
+SWIGLU_GEMV_ROWS = 4      # rows of one exact_gemv_g128_swiglu launch
+SWIGLU_PART_COLS = 32     # columns per slice bit length of exact_gemv_g128_swiglu
+XQ_PARTS_MAX = 1024       # slice bit lengths per row that exact_gemv_g128_qrow_acc takes
+
+
+def gemv_swiglu(xq, lin, s, silu, h, part, t=None):
+    """h (R, I) = SwiGLU of the gate|up totals xq . W (lin: the packed gate|up linear, N = 2I) and part (R, I / 64) = bit
+    lengths of max |h| per SWIGLU_PART_COLS columns, in one launch that keeps the totals in registers; t (optional,
+    (R, 2I)) receives the totals. The down GEMV quantises h: gemv_qrow_acc(h, part, I // SWIGLU_PART_COLS, ...)."""
+    R, K = xq.shape
+    I = lin.N // 2
+    if K != lin.K or lin.N % 2:
+        raise ExactError(f"gemv_swiglu: x has K = {K}, linear is {lin.N} x {lin.K}")
+    _need_packed(lin, "gemv_swiglu")
+    _lib.call("exact_gemv_g128_swiglu", _ptr(_need(xq, I16, "xq", R * K)), _ptr(lin.wp), _ptr(lin.mp), _ptr(lin.mh),
+              _ptr(_need(s, I32, "s", R)), _ptr(silu), _ptr(_need(h, I64, "h", R * I)),
+              _ptr(_need(part, I32, "part", R * (I // SWIGLU_PART_COLS))), _ptr(None if t is None else _need(t, I64, "t", R * 2 * I)), R, I,
+              K, _stream())
+    return h, part
+
+
 NORM_FUSE_ROWS = 2        # rows of one exact_gemv_g128_norm_acc launch
 NORM_FUSE_KMAX = 256 * 24
 

@@ -115,13 +115,25 @@ int exact_gemm_g128_zeroed(const void* x, int32_t abits, const int8_t* wp, const
  * part holds the producer's bit lengths of max |xs| over slices of the row (exact_attention's per-head
  * obits, exact_swiglu_qrow's slice bit lengths); s_out[r] = s. Replaces exact_quant_rows + exact_gemv_g128_acc
  * (qrow, exact_llm.py:41-46; TLinG, speed_fair_kaggle.py:735-738) with one launch. R <= 15 (abits 15) or
- * 16 (abits 7), nparts <= 64; returns 2 when a wave's share of a row exceeds 512 columns (the GEMV's group
+ * 16 (abits 7), nparts <= 1024; returns 2 when a wave's share of a row exceeds 512 columns (the GEMV's group
  * split leaves 4 groups or fewer per wave at the decode shapes) or the slices of a block 64 KiB of LDS.
  * zero (optional): zero_n int64 the launch also clears (a buffer whose readers have finished, e.g. the q|k|v
  * totals exact_attention_qkv leaves in place), so no separate clear is launched. */
 int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const int32_t* part, int32_t nparts, int32_t abits,
                              const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int32_t* s_out,
                              int32_t R, int32_t N, int32_t K, int64_t* zero, int64_t zero_n, void* stream);
+
+/* The gate|up GEMV with the SwiGLU in its epilogue, for decode rows (R <= 4, int16 x): the packed linear (N = 2I)
+ * holds the gate rows [0, I) and the up rows [I, 2I); with t = x . W (never stored unless t is given),
+ * g = rs(t[r][n], 28 - s[r]), u = rs(t[r][I + n], 28 - s[r]) and h[r][n] = round_shift(isilu(g) * u, 16), as
+ * exact_swiglu_qrow with xq NULL; part[r * (I / 32) + b] = bit length of max |h[r][32 b .. 32 b + 32)|, for
+ * exact_gemv_g128_qrow_acc (nparts = I / 32) to quantise. t (optional, (R, 2I)): receives the gate|up totals
+ * (overwritten, for a trace). I % 64 == 0, K % 128 == 0. Replaces exact_gemv_g128_acc + exact_swiglu_qrow
+ * (exact_llm.py:179; TLinG, speed_fair_kaggle.py:735-738; isilu exact_llm.py:118-122) with one launch that adds no
+ * atomics. */
+int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, const int32_t* s,
+                           const int32_t* silu, int64_t* h, int32_t* part, int64_t* t, int32_t R, int32_t I, int32_t K,
+                           void* stream);
 
 /* MoE expert GEMM on the matrix cores, grouped over the chunks exact_moe_dispatch wrote with chunk_rows = 128
  * (int16 x) or 256 (int8 x): for every chunk c < nchunks[0], rows p = chunk_p0[c] .. + chunk_n[c] of the

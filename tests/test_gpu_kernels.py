@@ -296,6 +296,59 @@ def test_swiglu_part_then_qrow_gemv_matches_swiglu_qrow(thr):
     assert not host(td).any()
 
 
+@pytest.mark.parametrize("R,I,K", [(1, 18944, 1792), (2, 4864, 896), (4, 13824, 640), (3, 128, 256), (1, 64, 128)])
+def test_gemv_swiglu_matches_oracle(thr, R, I, K):
+    """The gate|up GEMV with the SwiGLU in its epilogue: h is the oracle's SwiGLU of the gate|up totals, part the bit
+    length of max |h| per 64 columns, t (when given) the totals; h and part feeding gemv_qrow_acc give the oracle's
+    qrow shift and down totals. Row shifts s put row 0's gate values inside the SiLU table's +-16 range (interpolated
+    entries) and the last row's far outside it (saturation)."""
+    from exact_amd.tables import silu_t
+    lin, kw, km = synth_lin(thr, 93, f"gu{I}x{K}", 2 * I, K)
+    xq = rng.integers(-32767, 32768, (R, K))
+    xq[0, :2] = [32767, -32767]
+    if R > 1:
+        xq[1] >>= 9
+    t = oracle_t(xq, synth.weights_np(kw, 2 * I, K), synth.scales_np(km, 2 * I, K))
+    bl = O.bitlen(np.abs(t).max(1))
+    s = 28 - np.maximum(bl - 21, 0)
+    s[-1] = 28 if R > 1 else s[-1]
+    g = O.round_shift(t[:, :I], 28 - s[:, None])
+    u = O.round_shift(t[:, I:], 28 - s[:, None])
+    h_exp = O.round_shift(O.isilu(g) * u, 16)
+    assert (np.abs(g[0]) < (16 << 16)).sum() > I // 4   # the table's interpolated range is exercised
+    h = torch.full((R, I), -5, dtype=I64, device=DEV)
+    pc = ops.SWIGLU_PART_COLS
+    part = torch.full((R * (I // pc),), -1, dtype=I32, device=DEV)
+    td = torch.full((R, 2 * I), 7, dtype=I64, device=DEV) if R == 2 else None
+    ops.gemv_swiglu(dev(xq, I16), lin, dev(s.astype(np.int32), I32), dev(silu_t(), I32), h, part, t=td)
+    assert np.array_equal(host(h), h_exp)
+    part_exp = O.bitlen(np.abs(h_exp).reshape(R, I // pc, pc).max(2)).reshape(-1)
+    assert np.array_equal(host(part), part_exp)
+    if td is not None:
+        assert np.array_equal(host(td), t)
+    if I % 128:
+        return   # a down linear needs whole 128-wide groups
+    D = 192
+    down, kw2, km2 = synth_lin(thr, 94, f"dn{I}", D, I)
+    td2 = torch.zeros((R, D), dtype=I64, device=DEV)
+    sh = torch.full((R,), -1, dtype=I32, device=DEV)
+    ops.gemv_qrow_acc(h, part, I // pc, 15, down, td2, sh)
+    eq, es = O.qrow(h_exp, 15)
+    assert np.array_equal(host(sh), es[:, 0])
+    assert np.array_equal(host(td2), oracle_t(eq, synth.weights_np(kw2, D, I), synth.scales_np(km2, D, I)))
+
+
+def test_gemv_swiglu_refuses_unsupported_shapes(thr):
+    """More than 4 rows, or I not a multiple of 64: 'unsupported' (the model keeps the GEMV + SwiGLU launches then)."""
+    from exact_amd.tables import silu_t
+    lin, _, _ = synth_lin(thr, 95, "gu_bad", 2 * 96, 128)
+    st = dev(silu_t(), I32)
+    for R in (5, 1):   # 5 rows; one row of I = 96
+        with pytest.raises(ops.ExactError, match="unsupported"):
+            ops.gemv_swiglu(dev(np.zeros((R, 128)), I16), lin, dev(np.full(R, 20), I32), st,
+                            torch.zeros((R, 96), dtype=I64, device=DEV), torch.zeros(R * 96, dtype=I32, device=DEV))
+
+
 @pytest.mark.parametrize("R", [20, 33, 47, 60, 100, 300])
 def test_zeroed_gemm_entries_match(thr, R):
     """exact_gemm_g128_zeroed / _a16_zeroed on a zeroed t give the oracle's totals on every path: int8 and int16

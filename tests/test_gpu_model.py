@@ -72,6 +72,39 @@ def test_synthetic_prefill_and_decode_match_oracle(name):
         assert tok == otoks[i]
 
 
+@pytest.mark.parametrize("name", ["tiny", "tiny-hd128"])
+def test_decode_with_swiglu_in_the_gate_up_gemv_matches_oracle(name):
+    """Decode rows whose norms run as launches of their own (the norm-fused GEMVs off, as for hidden sizes above 2048):
+    the gate|up GEMV applies the SwiGLU in its epilogue and the down GEMV quantises its per-64-column bit lengths.
+    Logits and greedy tokens equal the oracle's, eagerly and through the graph; a 2-token prefill takes the same
+    path."""
+    cfg = synth.CONFIGS[name]
+    seed = 5
+    om = helpers.oracle_model(cfg, seed, T=64)
+    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=64)
+    tm.NORM_FUSE_D = 0
+    ids = helpers.prompt(11, 14, cfg.V)
+    otoks, orows = O.greedy_decode(om, ids[:10], 6)
+    cache = tm.new_cache(B=1)
+    lg = host(tm.forward(ids[:8], cache))
+    lg = host(tm.forward(ids[8:10], cache))        # 2 prefill rows: q|k|v epilogue apart, SwiGLU in the GEMV
+    assert np.array_equal(lg[-1], orows[0])
+    tok = int(lg[-1].argmax())
+    for i in range(1, 4):
+        lgi, nid = tm.decode_rows([tok], cache)
+        assert np.array_equal(host(lgi)[0], orows[i]), i
+        tok = int(host(nid)[0])
+        assert tok == otoks[i]
+    gd = GraphDecoder(tm, cache, 1)
+    gd.load([tok])
+    gd.capture()
+    for i in range(4, 6):
+        lgi, nid = gd.step()
+        assert np.array_equal(host(lgi)[0], orows[i]), i
+        tok = int(host(nid)[0])
+        assert tok == otoks[i]
+
+
 def test_chunked_prefill_on_matrix_core_attention_matches_oracle():
     """hd 128: prompt chunks of TModel.PREFILL_MIN_ROWS (96) rows or more take the matrix-core attention
     (exact_attention_prefill), here a 200-token prompt as one chunk and as chunks of 100 + 100, the second
