@@ -319,7 +319,8 @@ __global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict_
 // Operands of group g for one wave of the gate|up GEMV below: slots j = 0, 1 are sub-tiles qb, qb + 1 of the gate
 // tile tg, slots 2, 3 the same sub-tiles of the up tile tu (a sub-tile is the 16 rows at byte 256 q of each 1 KiB
 // chunk of the 8 KiB tile).
-template <bool NT, bool WIDE>
+// scales and weight sub-tiles of one group (X: the activations too, loaded between them)
+template <bool NT, bool WIDE, bool X = true>
 __device__ __forceinline__ void load_gu_group(GroupRegs& G_, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
                                               const int16_t* __restrict__ mh, const int8_t* xrow, size_t tg, size_t tu,
                                               int qb, int g, int row, int c) {
@@ -329,7 +330,7 @@ __device__ __forceinline__ void load_gu_group(GroupRegs& G_, const int8_t* __res
     G_.m[j] = mp[o];
     if constexpr (WIDE) G_.m[j] |= (int)mh[o] << 15;
   }
-  load_x<15>(G_, xrow, g, c);
+  if constexpr (X) load_x<15>(G_, xrow, g, c);
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -350,14 +351,27 @@ __device__ __forceinline__ void load_gu_group(GroupRegs& G_, const int8_t* __res
 // GEMV reads. tout (optional, (R, 2I)) receives the gate|up totals. Small blocks (NPB 1, KS 2: 2 I / 32 waves of 64
 // lanes) spread the waves over the CUs better than larger ones (7B bs1 decode: 4-wave blocks of 64 columns 2311 us a
 // step, 2-wave blocks of 32 columns 2194-2218, against 2311 for the GEMV + SwiGLU launches).
-template <bool NT, int VR, int NPB, int KS, bool WIDE>
+// NE > 0: the input rows are normalised in the kernel's own prologue, as k_gemv_g128_norm (every block runs
+// x = x_in + rs(res_t, 28 - res_s) and qrow(irms(x, gain), 15) for each row into LDS while its first weight tiles load,
+// NE elements per thread; block 0 writes x to x_out and the row shifts to s_out), so one launch replaces
+// exact_rmsnorm_qrow + the gate|up GEMV + the SwiGLU.
+template <bool NT, int VR, int NPB, int KS, bool WIDE, int NE = 0>
 __global__ __launch_bounds__(64 * NPB * KS) void k_gemv_gu_swiglu(const int16_t* __restrict__ x, const int8_t* __restrict__ wp,
                                                              const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
                                                              const int32_t* __restrict__ s, const int32_t* __restrict__ silu,
                                                              int64_t* __restrict__ hout, int32_t* __restrict__ part,
-                                                             int64_t* __restrict__ tout, int R, int I, int K, int G) {
+                                                             int64_t* __restrict__ tout, int R, int I, int K, int G,
+                                                             const int64_t* __restrict__ x_in = nullptr,
+                                                             int64_t* __restrict__ x_out = nullptr,
+                                                             const int64_t* __restrict__ res_t = nullptr,
+                                                             const int32_t* __restrict__ res_s = nullptr,
+                                                             const int64_t* __restrict__ gain = nullptr,
+                                                             int32_t* __restrict__ s_out = nullptr) {
   __shared__ int64_t cmb[KS > 1 ? (KS - 1) * NPB * 4 * VR * 64 : 1];
   __shared__ int pm[NPB][4];
+  extern __shared__ __attribute__((aligned(16))) int8_t xlds[];   // NE > 0: R rows of K int16 values
+  __shared__ RowScratch nsc;
+  __shared__ int32_t s_lds[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int p = wave % NPB, kp = wave / NPB;
   const int pair = blockIdx.x * NPB + p;   // 32 gate columns: sub-tiles qb, qb + 1 of 64-column tile nb
@@ -365,18 +379,33 @@ __global__ __launch_bounds__(64 * NPB * KS) void k_gemv_gu_swiglu(const int16_t*
   const int g0 = (int)(((int64_t)kp * G) / KS), g1 = (int)(((int64_t)(kp + 1) * G) / KS);
   const int row = lane & 15, c = lane >> 4;
   const bool valid = row < R;
-  const int8_t* xrow = reinterpret_cast<const int8_t*>(x + (size_t)(valid ? row : 0) * K);
+  const int8_t* xrow = NE > 0 ? reinterpret_cast<const int8_t*>(reinterpret_cast<const int16_t*>(xlds) + (valid ? row : 0) * K)
+                              : reinterpret_cast<const int8_t*>(x + (size_t)(valid ? row : 0) * K);
   int64_t acc[4][VR];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int v = 0; v < VR; ++v) acc[j][v] = 0;
-  if (g0 < g1) {   // two groups in flight, as gemv_groups
+  if (NE > 0 || g0 < g1) {   // two groups in flight, as gemv_groups
     GroupRegs ra, rb;
     auto ld = [&](GroupRegs& G_, int g) {
       load_gu_group<NT, WIDE>(G_, wp, mp, mh, xrow, tile_index(nb, g, nbs, G), tile_index(ub + nb, g, nbs, G), qb, g, row, c);
     };
-    ld(ra, g0);
+    if constexpr (NE > 0) {   // the first tiles in flight while the block normalises the rows (every wave takes part)
+      if (g0 < g1)
+        load_gu_group<NT, WIDE, false>(ra, wp, mp, mh, xrow, tile_index(nb, g0, nbs, G), tile_index(ub + nb, g0, nbs, G), qb,
+                                       g0, row, c);
+      int16_t* xl = reinterpret_cast<int16_t*>(xlds);
+      for (int r = 0; r < R; ++r)
+        norm_qrow_row<NE>(r, blockDim.x, x_in, res_t, res_s, gain, 15, K, xl + (size_t)r * K, blockIdx.x == 0 ? x_out : nullptr,
+                          nullptr, s_lds, nullptr, nullptr, nsc);
+      __syncthreads();
+      if (blockIdx.x == 0 && (int)threadIdx.x < R) s_out[threadIdx.x] = s_lds[threadIdx.x];
+      if (g0 >= g1) goto combine;
+      load_x<15>(ra, xrow, g0, c);
+    } else {
+      ld(ra, g0);
+    }
     int g = g0;
     for (; g + 2 < g1; g += 2) {
       ld(rb, g + 1);
@@ -392,6 +421,7 @@ __global__ __launch_bounds__(64 * NPB * KS) void k_gemv_gu_swiglu(const int16_t*
       compute_group<15, VR>(ra, acc, R, row, lane, valid);
     }
   }
+combine:
   if constexpr (KS > 1) {
     if (kp > 0)
 #pragma unroll
@@ -414,7 +444,7 @@ __global__ __launch_bounds__(64 * NPB * KS) void k_gemv_gu_swiglu(const int16_t*
     for (int v = 0; v < VR; ++v) {
       bl[v] = 0;
       if (c == 0 && v < R) {
-        const int sh = 28 - s[v];
+        const int sh = 28 - (NE > 0 ? s_lds[v] : s[v]);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int i = nb * 64 + 16 * (qb + j) + row;
@@ -932,6 +962,43 @@ extern "C" int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const 
   if (R == 1) GU_GO(1); else if (R == 2) GU_GO(2); else GU_GO(4);
 #undef GU_GO
   return launch_status("gemv_g128_swiglu");
+}
+
+// rows of one norm-fused SwiGLU GEMV launch and the row width its 128 threads hold (16 values each)
+#define GEMV_NSW_ROWS 2
+#define GEMV_NSW_KMAX (128 * 16)
+
+extern "C" int exact_gemv_g128_norm_swiglu(const int64_t* x_in, int64_t* x_out, const int64_t* res_t, const int32_t* res_s,
+                                           const int64_t* g, const int8_t* wp, const int16_t* mp, const int16_t* mh,
+                                           int32_t* s_out, const int32_t* silu, int64_t* h, int32_t* part, int64_t* t,
+                                           int32_t R, int32_t I, int32_t K, void* stream) {
+  if (!x_in || !g || !wp || !mp || !s_out || !silu || !h || !part || R <= 0 || I <= 0 || K <= 0 || (res_t && !res_s))
+    return EXACT_E_ARG;
+  if (x_out && (x_out == x_in || x_out == res_t)) return EXACT_E_ARG;   // the other blocks still read x_in / res_t
+  if (R > GEMV_NSW_ROWS || I % 64 || K % 128 || K > GEMV_NSW_KMAX) return EXACT_E_UNSUPPORTED;
+  if (GEMV_GU_NPB != 1 || GEMV_GU_KS != 2) return EXACT_E_UNSUPPORTED;   // the prologue's 128 threads hold the row
+  if (reinterpret_cast<uintptr_t>(wp) & 15) return EXACT_E_UNSUPPORTED;
+  const int G = K / 128;
+  dim3 grid((unsigned)(I / 32)), block(128);
+  const size_t lds = (size_t)R * K * 2;
+  hipStream_t st = as_stream(stream);
+  const int ept = (K + 127) / 128;
+#define NSW_GO(VR, E)                                                                                                  \
+  do {                                                                                                                 \
+    if (mh)                                                                                                            \
+      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, 1, 2, true, E>), grid, block, lds, st, nullptr, wp, mp, mh,     \
+                         nullptr, silu, h, part, t, R, I, K, G, x_in, x_out, res_t, res_s, g, s_out);                   \
+    else                                                                                                               \
+      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, 1, 2, false, E>), grid, block, lds, st, nullptr, wp, mp, mh,    \
+                         nullptr, silu, h, part, t, R, I, K, G, x_in, x_out, res_t, res_s, g, s_out);                   \
+  } while (0)
+  if (R == 1) {
+    if (ept <= 8) NSW_GO(1, 8); else NSW_GO(1, 16);
+  } else {
+    if (ept <= 8) NSW_GO(2, 8); else NSW_GO(2, 16);
+  }
+#undef NSW_GO
+  return launch_status("gemv_g128_norm_swiglu");
 }
 
 static int gemm_entry(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,

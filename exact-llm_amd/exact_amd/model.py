@@ -270,6 +270,7 @@ class TModel:
     # widest rows whose norm runs inside the consuming GEMVs (every block repeats the row's three reductions; at
     # 3584-wide rows that costs as much as the separate launch it saves, at 5120 more, at 896 less: 7.0 vs 8.2 us)
     NORM_FUSE_D = 2048
+    NORM_SWIGLU = True   # norm-fused decode: the SwiGLU in the gate|up GEMV's epilogue too
     EXPERT_GEMM_MIN_PAIRS = 64   # (row, expert) pairs from which the MoE experts run as one grouped GEMM
 
     def _prefill_ws(self, R):
@@ -329,6 +330,9 @@ class TModel:
         # GEMV's epilogue (no totals, no atomics, one launch fewer)
         sfuse = (xfuse and not nfuse and not c.moe and self.abits == 15 and R <= ops.SWIGLU_GEMV_ROWS and c.I % 64 == 0
                  and c.I // ops.SWIGLU_PART_COLS <= ops.XQ_PARTS_MAX and self.w.layers[0]["gateup"].bias is None)
+        # norm-fused decode rows whose gate|up GEMV also runs the SwiGLU in its epilogue
+        nsfuse = (nfuse and self.NORM_SWIGLU and R <= ops.SWIGLU_GEMV_ROWS and c.I % 64 == 0 and D <= ops.NORM_SWIGLU_KMAX
+                  and c.I // ops.SWIGLU_PART_COLS <= ops.XQ_PARTS_MAX and self.w.layers[0]["gateup"].bias is None)
         if xfuse and ws.h is None and (c.I > 8192 or nfuse or sfuse) and not c.moe:
             ws.h = torch.zeros((R, ws.I), dtype=I64, device=self.dev)
         x_cur, x_nxt = ws.x, ws.x2
@@ -383,6 +387,14 @@ class TModel:
                                   zero=t_qkv if afuse and clear else None)   # the q|k|v totals attention left
             else:
                 ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa, x8=da)
+            if nfuse and nsfuse:   # norm + gate|up + SwiGLU in one launch
+                ops.gemv_norm_swiglu(x_cur, t_o, ws.sa, L["g2"], L["gateup"], ws.s, tab.silu, ws.h, ws.part_sw,
+                                     x_out=x_nxt, t=t_gu if keep else None)
+                x_cur, x_nxt = x_nxt, x_cur
+                ops.gemv_qrow_acc(ws.h, ws.part_sw, c.I // ops.SWIGLU_PART_COLS, self.abits, L["down"], t_d, ws.sh,
+                                  zero=t_o if clear else None)   # the o totals the gate|up GEMV read
+                res_t, res_s = t_d, ws.sh
+                continue
             if nfuse:
                 ops.gemv_norm_acc(x_cur, t_o, ws.sa, L["g2"], L["gateup"], t_gu, ws.s, x_out=x_nxt)
                 x_cur, x_nxt = x_nxt, x_cur

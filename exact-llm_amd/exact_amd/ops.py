@@ -193,6 +193,34 @@ def gemv_norm_acc(x_in, res_t, res_s, g, lin, out, s_out, x_out=None, xq_out=Non
     return out
 
 
+NORM_SWIGLU_KMAX = 128 * 16   # row width of one exact_gemv_g128_norm_swiglu launch
+
+
+def gemv_norm_swiglu(x_in, res_t, res_s, g, lin, s_out, silu, h, part, x_out=None, t=None):
+    """The gate|up GEMV of gemv_swiglu on rows that it normalises itself (as gemv_norm_acc): x = x_in + rs(res_t,
+    28 - res_s) (res_t may be None), xq = qrow(irms(x, g), 15), h and part = SwiGLU of xq . W and its slice bit lengths,
+    in one launch. Block 0 writes x to x_out (not x_in or res_t) and the row shifts to s_out; t (optional, (R, 2I))
+    receives the gate|up totals."""
+    R, K = x_in.shape
+    I = lin.N // 2
+    if K != lin.K or lin.N % 2:
+        raise ExactError(f"gemv_norm_swiglu: x has K = {K}, linear is {lin.N} x {lin.K}")
+    _need_packed(lin, "gemv_norm_swiglu")
+    _need(x_in, I64, "x_in")
+    _need(g, I64, "g", K)
+    _need(s_out, I32, "s_out", R)
+    if res_t is not None:
+        _need(res_t, I64, "res_t", R * K)
+        _need(res_s, I32, "res_s", R)
+    if x_out is not None:
+        _need(x_out, I64, "x_out", R * K)
+    _lib.call("exact_gemv_g128_norm_swiglu", _ptr(x_in), _ptr(x_out), _ptr(res_t), _ptr(res_s), _ptr(g), _ptr(lin.wp),
+              _ptr(lin.mp), _ptr(lin.mh), _ptr(s_out), _ptr(silu), _ptr(_need(h, I64, "h", R * I)),
+              _ptr(_need(part, I32, "part", R * (I // SWIGLU_PART_COLS))),
+              _ptr(None if t is None else _need(t, I64, "t", R * 2 * I)), R, I, K, _stream())
+    return h, part
+
+
 GEMV_CHUNK_ROWS = {15: 15, 7: 48}   # int8 rows: up to 3 GEMV row chunks in exact_gemm_g128; int16 rows above 15 take
                                     # exact_gemm_g128_a16 (GEMV chunks of 16 with colterm up to 48 rows, digit rows beyond)
 _DIGIT_ROWS = {}                     # device -> int8 workspace of the A16 digit rows

@@ -135,6 +135,17 @@ int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const int16_t* mp
                            const int32_t* silu, int64_t* h, int32_t* part, int64_t* t, int32_t R, int32_t I, int32_t K,
                            void* stream);
 
+/* exact_gemv_g128_swiglu on rows the launch normalises itself, as exact_gemv_g128_norm_acc (decode rows, R <= 2,
+ * K <= 2048): every block computes x = x_in + round_shift(res_t, 28 - res_s[r]) (res_t may be NULL) and
+ * xq, s = qrow(irms(x, g), 15) while its first weight tiles load, then the SwiGLU GEMV on xq with those row shifts.
+ * Block 0 writes x to x_out (NULL: not written; must not alias x_in or res_t) and s to s_out. h, part and t as
+ * exact_gemv_g128_swiglu. Replaces exact_rmsnorm_qrow + exact_gemv_g128_acc + exact_swiglu_qrow
+ * (exact_llm.py:41-46, 100-106, 178-179; speed_fair_kaggle.py:735-738) with one launch. */
+int exact_gemv_g128_norm_swiglu(const int64_t* x_in, int64_t* x_out, const int64_t* res_t, const int32_t* res_s,
+                                const int64_t* g, const int8_t* wp, const int16_t* mp, const int16_t* mh, int32_t* s_out,
+                                const int32_t* silu, int64_t* h, int32_t* part, int64_t* t, int32_t R, int32_t I,
+                                int32_t K, void* stream);
+
 /* MoE expert GEMM on the matrix cores, grouped over the chunks exact_moe_dispatch wrote with chunk_rows = 128
  * (int16 x) or 256 (int8 x): for every chunk c < nchunks[0], rows p = chunk_p0[c] .. + chunk_n[c] of the
  * dispatched pairs, t[p] = x[row_map[p]] . W_e with e = chunk_e[c] (row_map NULL: x row p), expert e's packed

@@ -467,6 +467,73 @@ def test_gemv_norm_acc(thr, kind, R, N, K):
     assert np.array_equal(host(xd), x)      # the input rows are left as they were
 
 
+@pytest.mark.parametrize("kind", ["plain", "huge", "zeros", "tiny", "leftshift", "nores"])
+@pytest.mark.parametrize("R,I,K", [(1, 4864, 896), (2, 4864, 896), (1, 2816, 2048), (2, 640, 1024), (1, 64, 128)])
+def test_gemv_norm_swiglu(thr, kind, R, I, K):
+    """exact_gemv_g128_norm_swiglu: x = x_in + rs(res_t, 28 - res_s), xq, s = qrow(irms(x, g), 15), h = SwiGLU of the
+    gate|up totals xq . W with the row shifts s, part = bit length of max |h| per 32 columns, t = the totals, x_out = x,
+    s_out = s, against the oracle; h and part feed the quantising down GEMV as the unfused path's do."""
+    from exact_amd.tables import silu_t
+    rng_ = np.random.default_rng(R * 1000 + K + I + len(kind))
+    lin, kw, km = synth_lin(thr, 22, f"nsw{I}x{K}", 2 * I, K)
+    w, M = synth.weights_np(kw, 2 * I, K), synth.scales_np(km, 2 * I, K)
+    x, res, rs = _norm_case(kind, R, K, rng_)
+    g = rng_.integers(1 << 14, 1 << 17, K)
+    g[::5] = -g[::5]
+    xn = x if kind == "nores" else x + O.round_shift(res, (28 - rs)[:, None])
+    xq, s = O.qrow(O.irms(xn, g), 15)
+    t = oracle_t(xq, w, M)
+    gg = O.round_shift(t[:, :I], 28 - s)
+    uu = O.round_shift(t[:, I:], 28 - s)
+    h_exp = O.round_shift(O.isilu(gg) * uu, 16)
+    pc = ops.SWIGLU_PART_COLS
+    part_exp = O.bitlen(np.abs(h_exp).reshape(R, I // pc, pc).max(2)).reshape(-1)
+    h = torch.full((R, I), -5, dtype=I64, device=DEV)
+    part = torch.full((R * (I // pc),), -1, dtype=I32, device=DEV)
+    td = torch.full((R, 2 * I), 7, dtype=I64, device=DEV)
+    x_out = torch.full((R, K), 7, dtype=I64, device=DEV)
+    s_out = torch.full((R,), -1, dtype=I32, device=DEV)
+    xd = dev(x, I64)
+    nores = kind == "nores"
+    ops.gemv_norm_swiglu(xd, None if nores else dev(res, I64), None if nores else dev(rs, I32), dev(g, I64), lin, s_out,
+                         dev(silu_t(), I32), h, part, x_out=x_out, t=td)
+    assert np.array_equal(host(s_out), s[:, 0]), kind
+    assert np.array_equal(host(x_out), xn), kind
+    assert np.array_equal(host(td), t), kind
+    assert np.array_equal(host(h), h_exp), kind
+    assert np.array_equal(host(part), part_exp), kind
+    assert np.array_equal(host(xd), x)      # the input rows are left as they were
+    if I % 128:
+        return
+    D = 192
+    down, kw2, km2 = synth_lin(thr, 23, f"nswd{I}", D, I)
+    td2 = torch.zeros((R, D), dtype=I64, device=DEV)
+    sh = torch.full((R,), -1, dtype=I32, device=DEV)
+    ops.gemv_qrow_acc(h, part, I // pc, 15, down, td2, sh)
+    eq, es = O.qrow(h_exp, 15)
+    assert np.array_equal(host(sh), es[:, 0])
+    assert np.array_equal(host(td2), oracle_t(eq, synth.weights_np(kw2, D, I), synth.scales_np(km2, D, I)))
+
+
+def test_gemv_norm_swiglu_refuses_unsupported_shapes(thr):
+    """More than 2 rows, rows wider than 2048, or I not a multiple of 64: 'unsupported'; x_out aliasing x_in: bad
+    argument."""
+    from exact_amd.tables import silu_t
+    st = dev(silu_t(), I32)
+    for R, I, K in ((3, 64, 128), (1, 64, 2176), (1, 96, 128)):
+        lin, _, _ = synth_lin(thr, 24, f"nswbad{R}{I}{K}", 2 * I, K)
+        with pytest.raises(ops.ExactError, match="unsupported"):
+            ops.gemv_norm_swiglu(torch.zeros((R, K), dtype=I64, device=DEV), None, None,
+                                 torch.ones(K, dtype=I64, device=DEV), lin, torch.zeros(R, dtype=I32, device=DEV), st,
+                                 torch.zeros((R, I), dtype=I64, device=DEV), torch.zeros(R * I, dtype=I32, device=DEV))
+    lin, _, _ = synth_lin(thr, 24, "nswalias", 128, 128)
+    xin = torch.zeros((1, 128), dtype=I64, device=DEV)
+    with pytest.raises(ops.ExactError, match="bad argument"):
+        ops.gemv_norm_swiglu(xin, None, None, torch.ones(128, dtype=I64, device=DEV), lin,
+                             torch.zeros(1, dtype=I32, device=DEV), st, torch.zeros((1, 64), dtype=I64, device=DEV),
+                             torch.zeros(64, dtype=I32, device=DEV), x_out=xin)
+
+
 @pytest.mark.parametrize("kind", ["plain", "huge", "zeros", "tiny", "leftshift"])
 @pytest.mark.parametrize("D,bits", [(896, 15), (3584, 15), (5120, 15), (2048, 7), (100, 15)])
 def test_rmsnorm_qrow_edges(kind, D, bits):
