@@ -964,8 +964,14 @@ extern "C" int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const 
   return launch_status("gemv_g128_swiglu");
 }
 
-// rows of one norm-fused SwiGLU GEMV launch and the row width its 128 threads hold (16 values each)
+// rows of one norm-fused SwiGLU GEMV launch, its blocks (NPB pairs as exact_gemv_g128_swiglu, so part has the same
+// slices, x KS k parts) and the row width their threads hold (16 values each)
 #define GEMV_NSW_ROWS 2
+#define GEMV_NSW_NPB GEMV_GU_NPB
+#ifndef GEMV_NSW_KS
+#define GEMV_NSW_KS 4   // 0.5B bs1 decode, A/B: KS 2 0.836-0.855 ms a step, 4 0.823-0.841, 8 0.841-0.859
+#endif
+#define GEMV_NSW_THREADS (64 * GEMV_NSW_NPB * GEMV_NSW_KS)
 #define GEMV_NSW_KMAX (128 * 16)
 
 extern "C" int exact_gemv_g128_norm_swiglu(const int64_t* x_in, int64_t* x_out, const int64_t* res_t, const int32_t* res_s,
@@ -975,22 +981,21 @@ extern "C" int exact_gemv_g128_norm_swiglu(const int64_t* x_in, int64_t* x_out, 
   if (!x_in || !g || !wp || !mp || !s_out || !silu || !h || !part || R <= 0 || I <= 0 || K <= 0 || (res_t && !res_s))
     return EXACT_E_ARG;
   if (x_out && (x_out == x_in || x_out == res_t)) return EXACT_E_ARG;   // the other blocks still read x_in / res_t
-  if (R > GEMV_NSW_ROWS || I % 64 || K % 128 || K > GEMV_NSW_KMAX) return EXACT_E_UNSUPPORTED;
-  if (GEMV_GU_NPB != 1 || GEMV_GU_KS != 2) return EXACT_E_UNSUPPORTED;   // the prologue's 128 threads hold the row
+  if (R > GEMV_NSW_ROWS || I % (32 * GEMV_NSW_NPB) || I % 64 || K % 128 || K > GEMV_NSW_KMAX) return EXACT_E_UNSUPPORTED;
   if (reinterpret_cast<uintptr_t>(wp) & 15) return EXACT_E_UNSUPPORTED;
   const int G = K / 128;
-  dim3 grid((unsigned)(I / 32)), block(128);
+  dim3 grid((unsigned)(I / (32 * GEMV_NSW_NPB))), block(GEMV_NSW_THREADS);
   const size_t lds = (size_t)R * K * 2;
   hipStream_t st = as_stream(stream);
-  const int ept = (K + 127) / 128;
+  const int ept = (K + GEMV_NSW_THREADS - 1) / GEMV_NSW_THREADS;
 #define NSW_GO(VR, E)                                                                                                  \
   do {                                                                                                                 \
     if (mh)                                                                                                            \
-      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, 1, 2, true, E>), grid, block, lds, st, nullptr, wp, mp, mh,     \
-                         nullptr, silu, h, part, t, R, I, K, G, x_in, x_out, res_t, res_s, g, s_out);                   \
+      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, GEMV_NSW_NPB, GEMV_NSW_KS, true, E>), grid, block, lds, st,     \
+                         nullptr, wp, mp, mh, nullptr, silu, h, part, t, R, I, K, G, x_in, x_out, res_t, res_s, g, s_out);   \
     else                                                                                                               \
-      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, 1, 2, false, E>), grid, block, lds, st, nullptr, wp, mp, mh,    \
-                         nullptr, silu, h, part, t, R, I, K, G, x_in, x_out, res_t, res_s, g, s_out);                   \
+      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, GEMV_NSW_NPB, GEMV_NSW_KS, false, E>), grid, block, lds, st,    \
+                         nullptr, wp, mp, mh, nullptr, silu, h, part, t, R, I, K, G, x_in, x_out, res_t, res_s, g, s_out);   \
   } while (0)
   if (R == 1) {
     if (ept <= 8) NSW_GO(1, 8); else NSW_GO(1, 16);
