@@ -221,6 +221,7 @@ class Workspace:
         self.ids, self.slot, self.pos = z(R, dt=I32), z(R, dt=I32), z(R, dt=I32)
         self.seq = None   # (slot, keys) when the rows are one sequence's consecutive positions (prefill)
         self.h = None     # (R, I) SwiGLU values when the gate|up totals must stay intact (trace capture)
+        self.hsh = None   # (R, SI) SwiGLU values of the MoE shared expert (decode rows)
         self.I = I
         # int16 GEMM rows (prefill above 48 rows): the producers also write their rows' int8 digit rows, which the
         # GEMM reads directly (exact_gemm_g128_digits) instead of splitting them in a launch of its own
@@ -271,6 +272,7 @@ class TModel:
     # 3584-wide rows that costs as much as the separate launch it saves, at 5120 more, at 896 less: 7.0 vs 8.2 us)
     NORM_FUSE_D = 2048
     NORM_SWIGLU = True   # norm-fused decode: the SwiGLU in the gate|up GEMV's epilogue too
+    SHARED_SWIGLU = True   # MoE decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue
     EXPERT_GEMM_MIN_PAIRS = 64   # (row, expert) pairs from which the MoE experts run as one grouped GEMM
 
     def _prefill_ws(self, R):
@@ -482,9 +484,17 @@ class TModel:
             ops.gemm_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed, P)
         else:
             ops.gemv_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed)
-        self._lin(ws.xq, L["sgu"], ws.t_sgu, x8=dx)
-        ops.swiglu_qrow(ws.t_sgu, ws.s, tab.silu, self.abits, ws.shq, ws.ssh, clear=True, part=ws.part_sw, x8=dh)
-        self._lin(ws.shq, L["sd"], ws.t_sd, x8=dh)
+        if (self.SHARED_SWIGLU and not grouped and self.abits == 15 and ws.R <= ops.SWIGLU_GEMV_ROWS and c.SI % 64 == 0
+                and c.SI // ops.SWIGLU_PART_COLS <= ops.XQ_PARTS_MAX and L["sgu"].bias is None):
+            # decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue, the down GEMV quantises h
+            if ws.hsh is None:
+                ws.hsh = torch.zeros((ws.R, c.SI), dtype=I64, device=self.dev)
+            ops.gemv_swiglu(ws.xq, L["sgu"], ws.s, tab.silu, ws.hsh, ws.part_sw)
+            ops.gemv_qrow_acc(ws.hsh, ws.part_sw, c.SI // ops.SWIGLU_PART_COLS, self.abits, L["sd"], ws.t_sd, ws.ssh)
+        else:
+            self._lin(ws.xq, L["sgu"], ws.t_sgu, x8=dx)
+            ops.swiglu_qrow(ws.t_sgu, ws.s, tab.silu, self.abits, ws.shq, ws.ssh, clear=True, part=ws.part_sw, x8=dh)
+            self._lin(ws.shq, L["sd"], ws.t_sd, x8=dh)
         ops.moe_combine(ws.x, ws.t_ed, ws.esh, ws.p_sel, ws.disp["pidx"], k, ws.t_sd, ws.ssh, ws.gate, clear=True)
 
     # ---------------------------------------------------------------- reference-shaped API
