@@ -568,6 +568,182 @@ __global__ __launch_bounds__(256) void k_gemv_experts(const void* __restrict__ x
   }
 }
 
+// The routed experts' gate|up GEMV with the SwiGLU as its epilogue (MoE decode, dispatched chunks of at most 4 pairs):
+// block b takes 32 gate columns (and their up columns) of chunk b / (I / 32), KS waves splitting the groups, combined
+// in LDS as in k_gemv_gu_swiglu. Pair p0 + r (r < chunk_n) reads activation row row_map[p0 + r] against expert
+// chunk_e's linear (wp + e w_stride, mp + e m_stride: gate rows [0, I), up rows [I, 2I)) and stores
+// h[p0 + r][n] = shr(isilu(shr(g, 28 - s_pair[p0 + r])) * shr(u, 28 - s_pair[p0 + r]), F) (moe_exact_kaggle.py:461-463,
+// exact_llm.py:179) and part[(p0 + r) (I / 32) + b % (I / 32)] = bit length of max |h| over the 32 columns. Blocks past
+// the dispatched chunks exit.
+template <bool NT, int KS>
+__global__ __launch_bounds__(64 * KS) void k_gemv_experts_swiglu(const int16_t* __restrict__ x, const int32_t* __restrict__ row_map,
+                                                            const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                                            int64_t w_stride, int64_t m_stride,
+                                                            const int32_t* __restrict__ chunk_e,
+                                                            const int32_t* __restrict__ chunk_p0,
+                                                            const int32_t* __restrict__ chunk_n,
+                                                            const int32_t* __restrict__ nchunks,
+                                                            const int32_t* __restrict__ s_pair, const int32_t* __restrict__ silu,
+                                                            int64_t* __restrict__ hout, int32_t* __restrict__ part, int I,
+                                                            int K, int G) {
+  constexpr int VR = 4;
+  __shared__ int64_t cmb[KS > 1 ? (KS - 1) * 4 * VR * 64 : 1];
+  __shared__ int pm[VR];
+  const int lane = threadIdx.x & 63, kp = threadIdx.x >> 6;
+  const int npb = I / 32;
+  const int ch = blockIdx.x / npb, pb = blockIdx.x - ch * npb;
+  if (ch >= nchunks[0]) return;   // uniform over the block: before any barrier
+  const int e = chunk_e[ch], p0 = chunk_p0[ch];
+  const int R = chunk_n[ch] < VR ? chunk_n[ch] : VR;
+  wp += (int64_t)e * w_stride;
+  mp += (int64_t)e * m_stride;
+  const int nb = pb >> 1, qb = 2 * (pb & 1), nbs = (2 * I) >> 6, ub = I >> 6;
+  const int g0 = (int)(((int64_t)kp * G) / KS), g1 = (int)(((int64_t)(kp + 1) * G) / KS);
+  const int row = lane & 15, c = lane >> 4;
+  const bool valid = row < R;
+  const int pr = p0 + (valid ? row : 0);
+  const int8_t* xrow = reinterpret_cast<const int8_t*>(x + (size_t)(row_map ? row_map[pr] : pr) * K);
+  int64_t acc[4][VR];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int v = 0; v < VR; ++v) acc[j][v] = 0;
+  if (g0 < g1) {
+    GroupRegs ra, rb;
+    auto ld = [&](GroupRegs& G_, int g) {
+      load_gu_group<NT, false>(G_, wp, mp, nullptr, xrow, tile_index(nb, g, nbs, G), tile_index(ub + nb, g, nbs, G), qb, g, row,
+                               c);
+    };
+    ld(ra, g0);
+    int g = g0;
+    for (; g + 2 < g1; g += 2) {
+      ld(rb, g + 1);
+      compute_group<15, VR>(ra, acc, R, row, lane, valid);
+      ld(ra, g + 2);
+      compute_group<15, VR>(rb, acc, R, row, lane, valid);
+    }
+    if (g + 1 < g1) {
+      ld(rb, g + 1);
+      compute_group<15, VR>(ra, acc, R, row, lane, valid);
+      compute_group<15, VR>(rb, acc, R, row, lane, valid);
+    } else {
+      compute_group<15, VR>(ra, acc, R, row, lane, valid);
+    }
+  }
+  if constexpr (KS > 1) {
+    if (kp > 0)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < VR; ++v) cmb[(((kp - 1) * 4 + j) * VR + v) * 64 + lane] = acc[j][v];
+    __syncthreads();
+    if (kp == 0)
+#pragma unroll
+      for (int k = 1; k < KS; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int v = 0; v < VR; ++v) acc[j][v] += cmb[(((k - 1) * 4 + j) * VR + v) * 64 + lane];
+  }
+  if (kp == 0) {   // lane (row, c = 0) holds pair r = v's gate and up totals of column row of sub-tiles qb, qb + 1
+#pragma unroll
+    for (int v = 0; v < VR; ++v) {
+      int bl = 0;
+      if (c == 0 && v < R) {
+        const int sh = 28 - s_pair[p0 + v];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int i = nb * 64 + 16 * (qb + j) + row;
+          const int64_t hv = shr64(lut16(silu, shr64(acc[j][v], sh), false) * shr64(acc[2 + j][v], sh), EXACT_F);
+          hout[(size_t)(p0 + v) * I + i] = hv;
+          const int b = bitlen64(abs64(hv));
+          bl = b > bl ? b : bl;
+        }
+      }
+      bl = wave_max_i32(bl);
+      if (lane == 0) pm[v] = bl;
+    }
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < R) part[(size_t)(p0 + threadIdx.x) * npb + pb] = pm[threadIdx.x];
+}
+
+// The routed experts' down GEMV quantising its int64 input rows itself (MoE decode, chunks of at most 4 pairs): task =
+// (chunk, 64-row block, group split) as k_gemv_experts; pair p0 + r's row xs[p0 + r] (ldx apart) is quantised with
+// s = max(bitlen(max |row|) - 15, 0), bitlen(max |row|) = max_i part[(p0 + r) nparts + i] (qrow, exact_llm.py:41-46),
+// into the wave's LDS slice (as k_gemv_g128_xq); t[p0 + r] += q(row) . W_e (64-bit atomics), s_out[p0 + r] = s.
+template <bool NT, int PL>
+__global__ __launch_bounds__(256) void k_gemv_experts_xq(const int64_t* __restrict__ xs, int64_t ldx,
+                                                         const int32_t* __restrict__ part, int nparts,
+                                                         const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                                         int64_t w_stride, int64_t m_stride, const int32_t* __restrict__ chunk_e,
+                                                         const int32_t* __restrict__ chunk_p0, const int32_t* __restrict__ chunk_n,
+                                                         const int32_t* __restrict__ nchunks, int64_t* __restrict__ t,
+                                                         int32_t* __restrict__ s_out, int N, int K, int G, int nsplit, int gmax) {
+  constexpr int VR = 4;
+  extern __shared__ __attribute__((aligned(16))) int8_t xlds[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int task = blockIdx.x * 4 + wave;
+  const int nbs = (N + 63) >> 6;
+  const int per_chunk = nbs * nsplit;
+  const int ch = task / per_chunk;
+  if (ch >= nchunks[0]) return;   // no block-wide barrier below
+  const int rest = task - ch * per_chunk;
+  const int nb = rest / nsplit, sp = rest - nb * nsplit;
+  const int g0 = (int)(((int64_t)sp * G) / nsplit);
+  const int g1 = (int)(((int64_t)(sp + 1) * G) / nsplit);
+  const int e = chunk_e[ch], p0 = chunk_p0[ch];
+  const int R = chunk_n[ch] < VR ? chunk_n[ch] : VR;
+  const int ncol = (g1 - g0) * 128;
+  const int rowb = gmax * 128 * 2;
+  int8_t* mine = xlds + (size_t)wave * VR * rowb;
+  auto quantise = [&]() {
+    const int64_t lim = (1LL << 15) - 1;
+    for (int r = 0; r < R; ++r) {
+      const int p = p0 + r;
+      int pw[PL];
+#pragma unroll
+      for (int k = 0; k < PL; ++k) pw[k] = lane + 64 * k < nparts ? part[(int64_t)p * nparts + lane + 64 * k] : 0;
+      const int64_t* src = xs + (int64_t)p * ldx + (int64_t)g0 * 128;
+      int64_t xv[XQ_LOADS];
+#pragma unroll
+      for (int j = 0; j < XQ_LOADS; ++j) xv[j] = lane + 64 * j < ncol ? src[lane + 64 * j] : 0;
+      int pv = pw[0];
+#pragma unroll
+      for (int k = 1; k < PL; ++k) pv = pw[k] > pv ? pw[k] : pv;
+      const int m = wave_max_i32(pv);
+      const int sh = m - 15 > 0 ? m - 15 : 0;
+      if (nb == 0 && sp == 0 && lane == 0) s_out[p] = sh;
+#pragma unroll
+      for (int j = 0; j < XQ_LOADS; ++j) {
+        const int i = lane + 64 * j;
+        if (i < ncol) {
+          int64_t q = shr64(xv[j], sh);
+          q = q > lim ? lim : (q < -lim ? -lim : q);
+          reinterpret_cast<int16_t*>(mine + (size_t)r * rowb)[i] = (int16_t)q;
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done (wave-private region)
+    __builtin_amdgcn_wave_barrier();
+  };
+  const int row = lane & 15, c = lane >> 4;
+  const int8_t* xrow = mine + (size_t)(row < R ? row : 0) * rowb - (ptrdiff_t)g0 * 128 * 2;
+  int64_t acc[4][VR];
+  gemv_groups<15, NT, VR, decltype(quantise), false, false>(acc, wp + (size_t)e * w_stride, mp + (size_t)e * m_stride, nullptr,
+                                                            xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane, quantise);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = nb * 64 + 16 * q + row;
+#pragma unroll
+    for (int v = 0; v < VR; ++v) {
+      const int r = 4 * c + v;
+      if (r < R && n < N)
+        atomicAdd(reinterpret_cast<unsigned long long*>(t + (size_t)(p0 + r) * N + n), (unsigned long long)acc[q][v]);
+    }
+  }
+}
+
 // The reference's exact::gemv on its own tensors (speed_fair_kaggle.py:686-702): one int16 row x (K,), the
 // row-major int8 weight wT (N, K) and int64 group scales Mg (N, G); out[n] = sum_g (sum_{k in g} x[k] wT[n][k]) Mg[n][g]
 // in int64 (wrapping like the reference's int64 sums). No repacking: lane (row, c) of the MFMA's B operand is
@@ -1056,4 +1232,67 @@ extern "C" int exact_gemv_g128_experts(const void* x, int32_t abits, const int32
     hipLaunchKernelGGL((k_gemv_experts<7, GEMV_NT != 0>), grid, block, 0, as_stream(stream), x, row_map, wp, mp, w_stride,
                        m_stride, chunk_e, chunk_p0, chunk_n, nchunks, t, N, K, G, (int)ns);
   return launch_status("gemv_g128_experts");
+}
+
+// dispatched chunks of at most this many pairs take the fused expert GEMVs below
+#define EXPERT_FUSE_CHUNK 4
+
+static int check_chunks(const int32_t* chunk_e, const int32_t* chunk_p0, const int32_t* chunk_n, const int32_t* nchunks,
+                        int32_t max_chunks, int32_t chunk, int64_t w_stride, int64_t m_stride) {
+  if (!chunk_e || !chunk_p0 || !chunk_n || !nchunks || max_chunks <= 0 || w_stride < 0 || m_stride < 0 || chunk <= 0)
+    return EXACT_E_ARG;
+  if (chunk > EXPERT_FUSE_CHUNK || (w_stride & 15) || (m_stride & 7)) return EXACT_E_UNSUPPORTED;
+  return EXACT_OK;
+}
+
+#ifndef GEMV_EXP_KS
+#define GEMV_EXP_KS 4
+#endif
+
+extern "C" int exact_gemv_g128_experts_swiglu(const int16_t* x, const int32_t* row_map, const int8_t* wp, const int16_t* mp,
+                                              int64_t w_stride, int64_t m_stride, const int32_t* chunk_e,
+                                              const int32_t* chunk_p0, const int32_t* chunk_n, const int32_t* nchunks,
+                                              int32_t max_chunks, int32_t chunk, const int32_t* s_pair,
+                                              const int32_t* silu, int64_t* h, int32_t* part, int32_t I, int32_t K,
+                                              void* stream) {
+  if (!x || !wp || !mp || !s_pair || !silu || !h || !part || I <= 0 || K <= 0) return EXACT_E_ARG;
+  int e = check_chunks(chunk_e, chunk_p0, chunk_n, nchunks, max_chunks, chunk, w_stride, m_stride);
+  if (e) return e;
+  if (I % 64 || K % 128 || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(wp) & 15))
+    return EXACT_E_UNSUPPORTED;
+  const int64_t blocks = (int64_t)max_chunks * (I / 32);
+  if (blocks > (1LL << 30)) return EXACT_E_UNSUPPORTED;
+  hipLaunchKernelGGL((k_gemv_experts_swiglu<GEMV_NT != 0, GEMV_EXP_KS>), dim3((unsigned)blocks), dim3(64 * GEMV_EXP_KS), 0,
+                     as_stream(stream), x, row_map, wp, mp, w_stride, m_stride, chunk_e, chunk_p0, chunk_n, nchunks, s_pair,
+                     silu, h, part, I, K, K / 128);
+  return launch_status("gemv_g128_experts_swiglu");
+}
+
+extern "C" int exact_gemv_g128_experts_qrow_acc(const int64_t* xs, int64_t ldx, const int32_t* part, int32_t nparts,
+                                                const int8_t* wp, const int16_t* mp, int64_t w_stride, int64_t m_stride,
+                                                const int32_t* chunk_e, const int32_t* chunk_p0, const int32_t* chunk_n,
+                                                const int32_t* nchunks, int32_t max_chunks, int32_t chunk, int64_t* t,
+                                                int32_t* s_out, int32_t N, int32_t K, void* stream) {
+  if (!xs || !part || !wp || !mp || !t || !s_out || N <= 0 || K <= 0 || nparts <= 0 || ldx < K) return EXACT_E_ARG;
+  int e = check_chunks(chunk_e, chunk_p0, chunk_n, nchunks, max_chunks, chunk, w_stride, m_stride);
+  if (e) return e;
+  if (K % 128 || (reinterpret_cast<uintptr_t>(wp) & 15)) return EXACT_E_UNSUPPORTED;
+  const int G = K / 128;
+  const int64_t nbs = (N + 63) / 64;
+  int64_t ns = (GEMV_WAVES + (int64_t)max_chunks * nbs - 1) / ((int64_t)max_chunks * nbs);
+  ns = ns < 1 ? 1 : (ns > G ? G : ns);
+  const int gmax = (int)((G + ns - 1) / ns);
+  const size_t lds = (size_t)4 * EXPERT_FUSE_CHUNK * gmax * 128 * 2;
+  if (lds > GEMV_XQ_LDS_MAX || gmax * 128 > 64 * XQ_LOADS || nparts > 64 * XQ_PARTS_WIDE) return EXACT_E_UNSUPPORTED;
+  const int64_t tasks = (int64_t)max_chunks * nbs * ns;
+  if (tasks > (1LL << 30)) return EXACT_E_UNSUPPORTED;
+  dim3 grid((unsigned)((tasks + 3) / 4)), block(256);
+  hipStream_t st = as_stream(stream);
+  if (nparts <= 64)
+    hipLaunchKernelGGL((k_gemv_experts_xq<GEMV_NT != 0, 1>), grid, block, lds, st, xs, ldx, part, nparts, wp, mp, w_stride,
+                       m_stride, chunk_e, chunk_p0, chunk_n, nchunks, t, s_out, N, K, G, (int)ns, gmax);
+  else
+    hipLaunchKernelGGL((k_gemv_experts_xq<GEMV_NT != 0, XQ_PARTS_WIDE>), grid, block, lds, st, xs, ldx, part, nparts, wp, mp,
+                       w_stride, m_stride, chunk_e, chunk_p0, chunk_n, nchunks, t, s_out, N, K, G, (int)ns, gmax);
+  return launch_status("gemv_g128_experts_qrow_acc");
 }

@@ -57,6 +57,8 @@ SIGNATURES = {
     "exact_moe_dispatch": [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P],
     "exact_gemv_g128_experts": [P, I32, P, P, P, I64, I64, P, P, P, P, I32, P, I32, I32, P],
     "exact_gemm_g128_experts": [P, I32, P, P, P, I64, I64, P, P, P, P, P, P, I32, P, I32, I32, I32, P],
+    "exact_gemv_g128_experts_swiglu": [P, P, P, P, I64, I64, P, P, P, P, I32, I32, P, P, P, P, I32, I32, P],
+    "exact_gemv_g128_experts_qrow_acc": [P, I64, P, I32, P, P, I64, I64, P, P, P, P, I32, I32, P, P, I32, I32, P],
     "exact_moe_combine": [P, P, P, P, P, P, P, P, I32, I32, I32, I32, P],
 }
 OTHER = {"exact_version": ([], ctypes.c_int), "exact_last_error": ([], ctypes.c_char_p),

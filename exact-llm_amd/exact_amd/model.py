@@ -222,6 +222,7 @@ class Workspace:
         self.seq = None   # (slot, keys) when the rows are one sequence's consecutive positions (prefill)
         self.h = None     # (R, I) SwiGLU values when the gate|up totals must stay intact (trace capture)
         self.hsh = None   # (R, SI) SwiGLU values of the MoE shared expert (decode rows)
+        self.eh = self.part_eh = None   # the routed experts' SwiGLU values per pair and their slice bit lengths
         self.I = I
         # int16 GEMM rows (prefill above 48 rows): the producers also write their rows' int8 digit rows, which the
         # GEMM reads directly (exact_gemm_g128_digits) instead of splitting them in a launch of its own
@@ -231,7 +232,8 @@ class Workspace:
             self.dig = dict(x=z(2 * R, D, dt=I8), a=z(2 * R, H * hd, dt=I8), h=z(2 * R, hmax, dt=I8))
         if cfg.moe:
             k, P = cfg.topk, R * cfg.topk
-            nch = ops.max_chunks(P, cfg.NE, abits)
+            # chunk arrays for the smallest chunks this workspace may be dispatched with (the fused decode GEMVs' 4 pairs)
+            nch = ops.max_chunks(P, cfg.NE, min(ops.EXPERT_FUSE_CHUNK, ops.chunk_rows(abits)))
             self.gate_col = -(-cfg.NE // 64) * 64
             self.t_rt, self.p_sel, self.e_sel = z(R, self.gate_col + 1), z(R, k), z(R, k, dt=I32)
             self.gate = z(R)
@@ -273,6 +275,7 @@ class TModel:
     NORM_FUSE_D = 2048
     NORM_SWIGLU = True   # norm-fused decode: the SwiGLU in the gate|up GEMV's epilogue too
     SHARED_SWIGLU = True   # MoE decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue
+    EXPERT_SWIGLU = True   # MoE decode rows: the routed experts' SwiGLU and qrow inside their GEMVs
     EXPERT_GEMM_MIN_PAIRS = 64   # (row, expert) pairs from which the MoE experts run as one grouped GEMM
 
     def _prefill_ws(self, R):
@@ -472,18 +475,31 @@ class TModel:
         ops.router_topk(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, clear=True, NE=c.NE, gate_col=ws.gate_col,
                         sig=tab.sig, gate=ws.gate)
         grouped = P >= self.EXPERT_GEMM_MIN_PAIRS   # prefill: experts on the matrix cores, one tile per 128 pairs
-        ops.moe_dispatch(ws.e_sel, ws.s, c.NE, k, ops.EXPERT_CHUNK[self.abits] if grouped else ops.chunk_rows(self.abits),
-                         ws.disp)
-        if grouped:
+        # decode: the SwiGLU in the expert gate|up GEMV's epilogue and the qrow in the expert down GEMV (chunks of 4 pairs)
+        efuse = (self.EXPERT_SWIGLU and not grouped and self.abits == 15 and c.MI % 64 == 0
+                 and c.MI // ops.SWIGLU_PART_COLS <= ops.XQ_PARTS_MAX)
+        chunk = (ops.EXPERT_CHUNK[self.abits] if grouped else
+                 ops.EXPERT_FUSE_CHUNK if efuse else ops.chunk_rows(self.abits))
+        ops.moe_dispatch(ws.e_sel, ws.s, c.NE, k, chunk, ws.disp)
+        if efuse:
+            if ws.eh is None:
+                ws.eh = torch.zeros((P, c.MI), dtype=I64, device=self.dev)
+                ws.part_eh = torch.zeros(P * (c.MI // ops.SWIGLU_PART_COLS), dtype=I32, device=self.dev)
+            ops.gemv_experts_swiglu(ws.xq, ws.disp["pair_row"], L["egu"], ws.disp, ws.disp["s_pair"], tab.silu, ws.eh,
+                                    ws.part_eh)
+            ops.gemv_experts_qrow_acc(ws.eh, ws.part_eh, c.MI // ops.SWIGLU_PART_COLS, L["edown"], ws.disp, ws.t_ed,
+                                      ws.esh)
+        elif grouped:
             ops.gemm_experts(ws.xq, self.abits, ws.disp["pair_row"], L["egu"], ws.disp, ws.t_egu, P)
         else:
             ops.gemv_experts(ws.xq, self.abits, ws.disp["pair_row"], L["egu"], ws.disp, ws.t_egu)
-        ops.swiglu_qrow(ws.t_egu, ws.disp["s_pair"], tab.silu, self.abits, ws.ehq, ws.esh, clear=not grouped,
-                        part=ws.part_esw)
-        if grouped:
-            ops.gemm_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed, P)
-        else:
-            ops.gemv_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed)
+        if not efuse:
+            ops.swiglu_qrow(ws.t_egu, ws.disp["s_pair"], tab.silu, self.abits, ws.ehq, ws.esh, clear=not grouped,
+                            part=ws.part_esw)
+            if grouped:
+                ops.gemm_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed, P)
+            else:
+                ops.gemv_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed)
         if (self.SHARED_SWIGLU and not grouped and self.abits == 15 and ws.R <= ops.SWIGLU_GEMV_ROWS and c.SI % 64 == 0
                 and c.SI // ops.SWIGLU_PART_COLS <= ops.XQ_PARTS_MAX and L["sgu"].bias is None):
             # decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue, the down GEMV quantises h

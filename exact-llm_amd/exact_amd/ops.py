@@ -538,8 +538,9 @@ def chunk_rows(abits):
     return 15 if abits == 15 else 16
 
 
-def max_chunks(P, NE, abits):
-    return min(P, -(-P // chunk_rows(abits)) + NE)
+def max_chunks(P, NE, chunk):
+    """Capacity of moe_dispatch's chunk arrays for P pairs over NE experts in chunks of at most `chunk` pairs."""
+    return min(P, -(-P // chunk) + NE)
 
 
 def router_topk(t, s, expt, k, p_sel, e_sel, clear=False, NE=None, gate_col=-1, sig=None, gate=None):
@@ -553,8 +554,12 @@ def router_topk(t, s, expt, k, p_sel, e_sel, clear=False, NE=None, gate_col=-1, 
 
 
 def moe_dispatch(e_sel, s, NE, k, chunk, out):
-    """out: dict of int32 tensors pidx (P,), pair_row (P,), s_pair (P,), chunk_e/chunk_p0/chunk_n (max chunks,), nchunks (1,)."""
+    """out: dict of int32 tensors pidx (P,), pair_row (P,), s_pair (P,), chunk_e/chunk_p0/chunk_n (max chunks,), nchunks (1,).
+    The chunk arrays must hold max_chunks(P, NE, chunk) entries (the kernel writes every chunk it forms)."""
     R = s.shape[0]
+    need = max_chunks(R * k, NE, chunk)
+    for n in ("chunk_e", "chunk_p0", "chunk_n"):
+        _need(out[n], I32, n, need)
     _lib.call("exact_moe_dispatch", _ptr(_need(e_sel, I32, "e_sel", R * k)), _ptr(_need(s, I32, "s", R)),
               *(_ptr(_need(out[n], I32, n)) for n in ("pidx", "pair_row", "s_pair", "chunk_e", "chunk_p0", "chunk_n",
                                                        "nchunks")), R, NE, k, chunk, _stream())
@@ -570,6 +575,44 @@ def gemv_experts(x, abits, row_map, lin, disp, out):
     _lib.call("exact_gemv_g128_experts", _ptr(x), abits, _ptr(row_map), _ptr(lin.wp), _ptr(lin.mp), lin.w_stride,
               lin.m_stride, _ptr(disp["chunk_e"]), _ptr(disp["chunk_p0"]), _ptr(disp["chunk_n"]), _ptr(disp["nchunks"]),
               disp["chunk_e"].numel(), _ptr(out), lin.N, lin.K, _stream())
+    return out
+
+
+EXPERT_FUSE_CHUNK = 4   # pairs per dispatched chunk that the fused expert GEMVs below take
+
+
+def _chunks(disp):
+    return (_ptr(_need(disp["chunk_e"], I32, "chunk_e")), _ptr(_need(disp["chunk_p0"], I32, "chunk_p0")),
+            _ptr(_need(disp["chunk_n"], I32, "chunk_n")), _ptr(_need(disp["nchunks"], I32, "nchunks", 1)),
+            disp["chunk_e"].numel())
+
+
+def gemv_experts_swiglu(x, row_map, lin, disp, s_pair, silu, h, part, chunk=EXPERT_FUSE_CHUNK):
+    """The routed experts' gate|up GEMV with the SwiGLU in its epilogue (int16 rows; chunks of at most 4 pairs, from
+    moe_dispatch with that chunk): h[p] = SwiGLU of x[row_map[p]] . W_e with shift s_pair[p], part[p * (I / 32) + b] =
+    bit length of max |h[p]| over columns 32 b .. 32 b + 31; gemv_experts_qrow_acc takes them."""
+    I = lin.N // 2
+    P = h.shape[0]
+    _need(x, I16, "x")
+    if x.shape[1] != lin.K or lin.N % 2 or h.shape[1] != I:
+        raise ExactError(f"gemv_experts_swiglu: x {tuple(x.shape)}, h {tuple(h.shape)} against ({lin.N}, {lin.K})")
+    _lib.call("exact_gemv_g128_experts_swiglu", _ptr(x), _ptr(row_map), _ptr(lin.wp), _ptr(lin.mp), lin.w_stride,
+              lin.m_stride, *_chunks(disp), chunk, _ptr(_need(s_pair, I32, "s_pair", P)), _ptr(silu),
+              _ptr(_need(h, I64, "h", P * I)), _ptr(_need(part, I32, "part", P * (I // SWIGLU_PART_COLS))), I, lin.K,
+              _stream())
+    return h, part
+
+
+def gemv_experts_qrow_acc(xs, part, nparts, lin, disp, out, s_out, chunk=EXPERT_FUSE_CHUNK):
+    """out[p] += qrow(xs[p], 15) . W_e for the dispatched chunks (at most 4 pairs each), the shifts from the producer's
+    slice bit lengths part (P, nparts); s_out[p] = the shift."""
+    P, ldx = xs.shape
+    _need(xs, I64, "xs")
+    if ldx < lin.K or out.shape[1] != lin.N:
+        raise ExactError(f"gemv_experts_qrow_acc: xs {tuple(xs.shape)}, out {tuple(out.shape)} against ({lin.N}, {lin.K})")
+    _lib.call("exact_gemv_g128_experts_qrow_acc", _ptr(xs), ldx, _ptr(_need(part, I32, "part", P * nparts)), nparts,
+              _ptr(lin.wp), _ptr(lin.mp), lin.w_stride, lin.m_stride, *_chunks(disp), chunk,
+              _ptr(_need(out, I64, "out", P * lin.N)), _ptr(_need(s_out, I32, "s_out", P)), lin.N, lin.K, _stream())
     return out
 
 

@@ -64,7 +64,7 @@ def test_dispatch_groups_pairs_by_expert(R, NE, k, ch):
     e_sel = np.stack([rng.choice(NE, k, replace=False) for _ in range(R)])
     s = rng.integers(0, 30, R)
     P = R * k
-    nmax = ops.max_chunks(P, NE, 15 if ch == 15 else 7)
+    nmax = ops.max_chunks(P, NE, ch)
     out = {n: torch.full((P,), -1, dtype=I32, device=DEV) for n in ("pidx", "pair_row", "s_pair")}
     out.update({n: torch.full((nmax,), -1, dtype=I32, device=DEV) for n in ("chunk_e", "chunk_p0", "chunk_n")})
     out["nchunks"] = torch.zeros(1, dtype=I32, device=DEV)
@@ -106,7 +106,7 @@ def test_expert_gemv_matches_oracle(abits, R, NE, k, N, K):
     x = rng.integers(-lim, lim + 1, (R, K))
     P = R * k
     disp = {n: torch.zeros((P,), dtype=I32, device=DEV) for n in ("pidx", "pair_row", "s_pair")}
-    nmax = ops.max_chunks(P, NE, abits)
+    nmax = ops.max_chunks(P, NE, ops.chunk_rows(abits))
     disp.update({n: torch.zeros((nmax,), dtype=I32, device=DEV) for n in ("chunk_e", "chunk_p0", "chunk_n")})
     disp["nchunks"] = torch.zeros(1, dtype=I32, device=DEV)
     ops.moe_dispatch(dev(e_sel, I32), torch.zeros(R, dtype=I32, device=DEV), NE, k, ops.chunk_rows(abits), disp)
@@ -140,7 +140,7 @@ def _dispatch(e_sel, NE, k, chunk, abits):
     R = e_sel.shape[0]
     P = R * k
     disp = {n: torch.zeros((P,), dtype=I32, device=DEV) for n in ("pidx", "pair_row", "s_pair")}
-    nmax = ops.max_chunks(P, NE, abits)
+    nmax = ops.max_chunks(P, NE, chunk)
     disp.update({n: torch.zeros((nmax,), dtype=I32, device=DEV) for n in ("chunk_e", "chunk_p0", "chunk_n")})
     disp["nchunks"] = torch.zeros(1, dtype=I32, device=DEV)
     ops.moe_dispatch(dev(e_sel, I32), torch.zeros(R, dtype=I32, device=DEV), NE, k, chunk, disp)
@@ -269,3 +269,56 @@ def test_tiny_moe_batch_graph_decode_matches_oracle():
         toks.append(host(nid).tolist())
     for b in range(B):
         assert [t[b] for t in toks] == want[b][0][:4]
+
+
+@pytest.mark.parametrize("R,NE,k,MI,K,D", [(1, 8, 4, 128, 256, 192), (2, 12, 4, 1408, 2048, 256), (8, 6, 4, 256, 384, 128),
+                                           (3, 5, 2, 128, 128, 64)])
+def test_fused_expert_gemvs_match_oracle(tab, R, NE, k, MI, K, D):
+    """exact_gemv_g128_experts_swiglu + exact_gemv_g128_experts_qrow_acc (dispatched chunks of at most 4 pairs, so
+    experts chosen by many rows split into several chunks): h of every (row, expert) pair is the oracle's SwiGLU of the
+    pair's gate|up totals with the row's shift, part its bit lengths per 32 columns, and the down GEMV quantising h gives
+    the oracle's qrow shift and expert down totals (moe_exact_kaggle.py:461-463)."""
+    rng = np.random.default_rng(R * 100 + MI)
+    thr = dev(synth.thresholds().astype(np.int64), I64).to(I32)
+    gu, dn = ops.ExpertLinears(NE, 2 * MI, K, DEV), ops.ExpertLinears(NE, D, MI, DEV)
+    used = sorted(rng.choice(NE, min(NE, k + 1), replace=False).tolist())
+    e_sel = np.stack([rng.choice(used, k, replace=False) for _ in range(R)])
+    wg, Mg, wd, Md = {}, {}, {}, {}
+    for e in used:
+        for lin, w, M, N, KK, tag in ((gu, wg, Mg, 2 * MI, K, "g"), (dn, wd, Md, D, MI, "d")):
+            wp, mp = lin.part(e)
+            kw, km = synth.key(31, f"{tag}{e}.w"), synth.key(31, f"{tag}{e}.m")
+            ops.synth_linear(wp, mp, N, KK, kw, km, synth.M_LO, synth.M_HI, thr)
+            w[e], M[e] = synth.weights_np(kw, N, KK), synth.scales_np(km, N, KK)
+    x = rng.integers(-32767, 32768, (R, K))
+    x[0, :2] = [32767, -32767]
+    tot = {(r, e): (O.group_acc(x[r:r + 1], wg[e]) * Mg[e][:, None, :]).sum(0)[0] for r in range(R) for e in e_sel[r]}
+    s = np.array([28 - max(int(O.bitlen(max(np.abs(tot[(r, e)]).max() for e in e_sel[r]))) - 21, 0) for r in range(R)])
+    P = R * k
+    disp = {n: torch.zeros((P,), dtype=I32, device=DEV) for n in ("pidx", "pair_row", "s_pair")}
+    nmax = ops.max_chunks(P, NE, ops.EXPERT_FUSE_CHUNK)
+    disp.update({n: torch.zeros((nmax,), dtype=I32, device=DEV) for n in ("chunk_e", "chunk_p0", "chunk_n")})
+    disp["nchunks"] = torch.zeros(1, dtype=I32, device=DEV)
+    ops.moe_dispatch(dev(e_sel, I32), dev(s, I32), NE, k, ops.EXPERT_FUSE_CHUNK, disp)
+    assert host(disp["chunk_n"])[:int(host(disp["nchunks"])[0])].max() <= ops.EXPERT_FUSE_CHUNK
+    pc = ops.SWIGLU_PART_COLS
+    h = torch.full((P, MI), -3, dtype=I64, device=DEV)
+    part = torch.full((P * (MI // pc),), -1, dtype=I32, device=DEV)
+    ops.gemv_experts_swiglu(dev(x, torch.int16), disp["pair_row"], gu, disp, disp["s_pair"], tab.silu, h, part)
+    t = torch.zeros((P, D), dtype=I64, device=DEV)
+    sh = torch.full((P,), -1, dtype=I32, device=DEV)
+    ops.gemv_experts_qrow_acc(h, part, MI // pc, dn, disp, t, sh)
+    gh, gp, gt, gs = host(h), host(part).reshape(P, MI // pc), host(t), host(sh)
+    pidx = host(disp["pidx"])
+    for q in range(P):
+        r, e = q // k, e_sel.reshape(-1)[q]
+        tt = tot[(r, e)]
+        g = O.round_shift(tt[:MI], 28 - int(s[r]))
+        u = O.round_shift(tt[MI:], 28 - int(s[r]))
+        hv = O.round_shift(O.isilu(g) * u, 16)
+        p = pidx[q]
+        assert np.array_equal(gh[p], hv), (q, e)
+        assert np.array_equal(gp[p], O.bitlen(np.abs(hv).reshape(MI // pc, pc).max(1))), (q, e)
+        hq, hs = O.qrow(hv[None, :], 15)
+        assert gs[p] == hs[0, 0], (q, e)
+        assert np.array_equal(gt[p], (O.group_acc(hq, wd[e]) * Md[e][:, None, :]).sum(0)[0]), (q, e)
