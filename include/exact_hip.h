@@ -310,6 +310,28 @@ int exact_gemv_g128_experts(const void* x, int32_t abits, const int32_t* row_map
                             const int32_t* chunk_p0, const int32_t* chunk_n, const int32_t* nchunks,
                             int32_t max_chunks, int64_t* t, int32_t N, int32_t K, void* stream);
 
+/* Decode expert gate|up GEMV with the SwiGLU as its epilogue (int16 rows, chunks of at most 4 pairs, as
+ * exact_moe_dispatch writes them with chunk_rows <= 4; chunk = that size, refused above 4): for every pair p of
+ * every chunk, the expert's gate|up totals of x[row_map[p]] (the 2 I rows at wp + e*w_stride: gate rows [0, I),
+ * up rows [I, 2 I)) and h[p][i] = rs(isilu(rs(g_i, 28 - s_pair[p])) * rs(u_i, 28 - s_pair[p]), 16), the bit length
+ * of max |h| per 32 columns in part[p * (I / 32) + i / 32]. I % 64 == 0. Replaces exact_gemv_g128_experts +
+ * exact_swiglu_qrow for the expert MLP's first half (moe_exact_kaggle.py:461-462; exact_llm.py:179). */
+int exact_gemv_g128_experts_swiglu(const int16_t* x, const int32_t* row_map, const int8_t* wp, const int16_t* mp,
+                                   int64_t w_stride, int64_t m_stride, const int32_t* chunk_e, const int32_t* chunk_p0,
+                                   const int32_t* chunk_n, const int32_t* nchunks, int32_t max_chunks, int32_t chunk,
+                                   const int32_t* s_pair, const int32_t* silu, int64_t* h, int32_t* part, int32_t I,
+                                   int32_t K, void* stream);
+
+/* Decode expert down GEMV on the int64 SwiGLU values xs (row p at xs + p * ldx) quantised in the launch: each pair's
+ * shift s_out[p] = max(max_i part[p * nparts + i] - 15, 0) (qrow, exact_llm.py:41-46) and t[p] += qrow(xs[p]) . W_e
+ * for the dispatched chunks (chunk as exact_gemv_g128_experts_swiglu). Replaces exact_swiglu_qrow's quantisation +
+ * exact_gemv_g128_experts for the expert MLP's second half (moe_exact_kaggle.py:461-462). */
+int exact_gemv_g128_experts_qrow_acc(const int64_t* xs, int64_t ldx, const int32_t* part, int32_t nparts,
+                                     const int8_t* wp, const int16_t* mp, int64_t w_stride, int64_t m_stride,
+                                     const int32_t* chunk_e, const int32_t* chunk_p0, const int32_t* chunk_n,
+                                     const int32_t* nchunks, int32_t max_chunks, int32_t chunk, int64_t* t,
+                                     int32_t* s_out, int32_t N, int32_t K, void* stream);
+
 /* Combination (moe_exact_kaggle.py:463-467): x[r] += sum_j rs(p_sel[r][j] * rs(t_ed[pidx[r*k+j]], 28 - sh_pair), 20)
  *   + rs(gate[r] * rs(t_sd[r], 28 - sh_s[r]), 16)   (shared expert; skipped if t_sd is NULL).
  * clear_t != 0 leaves t_ed and t_sd zeroed. */

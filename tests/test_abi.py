@@ -11,7 +11,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared():
     src = open(os.path.join(ROOT, "include", "exact_hip.h")).read()
-    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(exact_\w+)\(", src, re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t|const char\*)\s+(exact_\w+)\(", src, re.M)))
 
 
 def test_header_declares_entry_points():
@@ -26,6 +26,20 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES or name in _lib.OTHER, name
     assert lib.exact_version() >= 100
+
+
+@pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")
+def test_header_declares_every_exported_entry_point():
+    """The reverse direction: every exact_* symbol the library exports is declared in the header (and bound)."""
+    import shutil
+    import subprocess
+    if not shutil.which("nm"):
+        pytest.skip("nm not available")
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = sorted({ln.split()[-1] for ln in out.splitlines() if ln.split() and ln.split()[-1].startswith("exact_")})
+    names = set(declared())
+    assert [n for n in exported if n not in names] == []
+    assert [n for n in exported if n not in _lib.SIGNATURES and n not in _lib.OTHER] == []
 
 
 @pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH), reason="library not built")

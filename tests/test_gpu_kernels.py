@@ -555,3 +555,18 @@ def test_rmsnorm_qrow_edges(kind, D, bits):
     if x8 is not None:
         d8 = host(x8).astype(np.int64)
         assert np.array_equal(d8[0::2] * 256 + d8[1::2] + 128, want_q), kind
+
+
+@pytest.mark.parametrize("R,N,K", [(1, 10001, 3456), (3, 9600, 3584), (16, 4100, 8192)])
+def test_gemv_large_a8_partial_row_block(thr, R, N, K):
+    """Large int8-row weights (the 1024-thread-block launch) with N not a multiple of 64, so the last row block is
+    partial: overwrite and accumulate modes, bit-exact vs numpy."""
+    lin, kw, km = synth_lin(thr, 73, f"bal{N}", N, K)
+    xq = rng.integers(-127, 128, (R, K))
+    exp = oracle_t(xq, synth.weights_np(kw, N, K), synth.scales_np(km, N, K))
+    t = ops.gemv_g128(dev(xq, I8), 7, lin)
+    assert np.array_equal(host(t), exp)
+    t0 = rng.integers(-(1 << 40), 1 << 40, (R, N))
+    acc = dev(t0, I64)
+    ops.gemv_g128_acc(dev(xq, I8), 7, lin, acc)
+    assert np.array_equal(host(acc), exp + t0)
