@@ -93,6 +93,19 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #ifndef ATT_VPF_LONG_S
 #define ATT_VPF_LONG_S 128
 #endif
+// long caches whose blocks fit one round: twice the threads per block, so each thread walks half the keys of p.V
+#ifndef ATT_WIDE
+#define ATT_WIDE 1
+#endif
+#ifndef ATT_WIDE_THREADS
+#define ATT_WIDE_THREADS 1024
+#endif
+#ifndef ATT_VPF_WIDE
+#define ATT_VPF_WIDE 8
+#endif
+#ifndef ATT_WIDE_BLOCKS
+#define ATT_WIDE_BLOCKS 256
+#endif
 #ifndef ATT_VPF_LONG_BLOCKS
 #define ATT_VPF_LONG_BLOCKS 256
 #endif
@@ -231,8 +244,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
 // Latency: everything that does not depend on the new token (the RoPE row, each thread's first cached key and
 // its first ATT_VPF value pairs) is loaded together with t, so the block waits on memory about once before the
 // exp table.
-template <int VPF>
-__global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
+// KPF: 16-byte chunks of each thread's first cached key loaded with the totals (0: none)
+template <int VPF, int NT = ATT_THREADS, int KPF = ATT_KPF>
+__global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
                                                                const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
                                                                const int64_t* __restrict__ sin_t, const int32_t* __restrict__ slot,
                                                                const int32_t* __restrict__ pos, int16_t* __restrict__ kq,
@@ -248,7 +262,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
   __shared__ int32_t shq[2];
   __shared__ int ored[16];
   __shared__ int64_t red[16], red2[16];
-  __shared__ int64_t part[ATT_THREADS * 2];
+  __shared__ int64_t part[NT * 2];
   const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = H / KV, kh = h / grp;
   const int N = (H + 2 * KV) * hd;
@@ -262,13 +276,13 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
   const int npair = hd >> 1, nparts = blockDim.x / npair;
   const int dp = tid % npair, pp = tid / npair;
   // ---- loads that do not depend on the new token, issued with the totals
-  v4i kpre[ATT_KPF];
+  v4i kpre[KPF > 0 ? KPF : 1];
   int skpre = 0;
-  const bool kp = hd <= 8 * ATT_KPF && tid < p;
+  const bool kp = KPF > 0 && hd <= 8 * KPF && tid < p;
   if (kp) {
     const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + tid) * hd);
 #pragma unroll
-    for (int j8 = 0; j8 < ATT_KPF; ++j8)
+    for (int j8 = 0; j8 < KPF; ++j8)
       if (j8 < hd / 8) kpre[j8] = kr[j8];
     skpre = sk[cbase + tid];
   }
@@ -289,15 +303,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
     }
   }
   {   // the exp table into LDS: every piece loaded before the first store, with the loads above
-    constexpr int NV = EXACT_EXP_N / 4, NK = (NV + ATT_THREADS - 1) / ATT_THREADS;
+    constexpr int NV = EXACT_EXP_N / 4, NK = (NV + NT - 1) / NT;
     v4i te[NK];
 #pragma unroll
     for (int k = 0; k < NK; ++k)
-      if (tid + k * ATT_THREADS < NV) te[k] = reinterpret_cast<const v4i*>(expt)[tid + k * ATT_THREADS];
+      if (tid + k * NT < NV) te[k] = reinterpret_cast<const v4i*>(expt)[tid + k * NT];
     const int tail = tid < EXACT_EXP_N - 4 * NV ? expt[4 * NV + tid] : 0;
 #pragma unroll
     for (int k = 0; k < NK; ++k)
-      if (tid + k * ATT_THREADS < NV) reinterpret_cast<v4i*>(texp)[tid + k * ATT_THREADS] = te[k];
+      if (tid + k * NT < NV) reinterpret_cast<v4i*>(texp)[tid + k * NT] = te[k];
     if (tid < EXACT_EXP_N - 4 * NV) texp[4 * NV + tid] = tail;
   }
   const int sh = 28 - s[r];
@@ -356,7 +370,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention_qkv(const int64_t* __
     int skv;
     if (kp && si == tid) {   // the prefetched first key
 #pragma unroll
-      for (int j8 = 0; j8 < ATT_KPF; ++j8) {
+      for (int j8 = 0; j8 < KPF; ++j8) {
         if (j8 < hd / 8) {
           const v4i kk = kpre[j8], qq = reinterpret_cast<const v4i*>(qs16)[j8];
 #pragma unroll
@@ -462,7 +476,16 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
     attr_set = true;
   }
   const size_t lds = (size_t)Smax * 8;
-  if (Smax > ATT_VPF_LONG_S)
+  if (ATT_WIDE && Smax > ATT_VPF_LONG_S && (int64_t)R * H <= ATT_WIDE_BLOCKS && (2 * ATT_WIDE_THREADS) % hd == 0) {
+    static bool wide_set = false;
+    if (!wide_set) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF_WIDE, ATT_WIDE_THREADS, 0>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
+      wide_set = true;
+    }
+    hipLaunchKernelGGL((k_attention_qkv<ATT_VPF_WIDE, ATT_WIDE_THREADS, 0>), dim3(R, H), dim3(ATT_WIDE_THREADS), lds,
+                       as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
+  } else if (Smax > ATT_VPF_LONG_S)
     hipLaunchKernelGGL(k_attention_qkv<ATT_VPF_LONG>, dim3(R, H), dim3(ATT_THREADS), lds, as_stream(stream), t, s, b, cos_t,
                        sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
   else
