@@ -211,7 +211,7 @@ class Workspace:
         self.att, self.aq, self.sa = z(R, H * hd), z(R, H * hd, dt=adt), z(R, dt=I32)
         self.t_o, self.t_gu, self.hq, self.sh = z(R, D), z(R, 2 * I), z(R, I, dt=adt), z(R, dt=I32)
         self.t_d, self.t_head = self.t_qd[R * nq:].view(R, D), z(R, V)
-        self.logits, self.next_ids = z(R, V), z(R, dt=I32)
+        self.logits = z(R, V)
         self.s28 = torch.full((R,), 28, dtype=I32, device=device)
         # slice bit lengths of the SwiGLU rows: per 1024 columns (exact_swiglu_qrow) or per 32 or 64
         # (exact_gemv_g128_swiglu)
@@ -219,6 +219,9 @@ class Workspace:
         self.part_lg = ops.logits_parts(R, V, device)
         self.obits = z(R, H, dt=I32)
         self.ids, self.slot, self.pos = z(R, dt=I32), z(R, dt=I32), z(R, dt=I32)
+        # the greedy ids are written over the input ids (read once, by the embedding at the start of the pass): the
+        # next decode step consumes them with no copy launch in between
+        self.next_ids = self.ids
         self.seq = None   # (slot, keys) when the rows are one sequence's consecutive positions (prefill)
         self.h = None     # (R, I) SwiGLU values when the gate|up totals must stay intact (trace capture)
         self.hsh = None   # (R, SI) SwiGLU values of the MoE shared expert (decode rows)
@@ -710,8 +713,9 @@ class GraphDecoder:
         torch.cuda.synchronize()
 
     def step(self, feed_argmax=True):
-        """One decode step: returns (logits (B, V) view, next ids view). With feed_argmax the next step
-        consumes the greedy ids directly on the device."""
+        """One decode step: returns (logits (B, V) view, next ids view). The greedy ids land in the step's input
+        ids, so the next step consumes them directly on the device; a caller that chooses other tokens (feed_argmax
+        False, e.g. sampling) loads them with load() before the next step."""
         if max(self.cache.n[:self.B]) >= self.tm.Smax:
             raise ExactError("cache full")
         b = self.nstep % 2
@@ -728,6 +732,5 @@ class GraphDecoder:
         self.nstep += 1
         for r in range(self.B):
             self.cache.n[r] += 1
-        if feed_argmax:
-            self.ws.ids.copy_(self.ws.next_ids)
+        # next_ids is the ids buffer itself, so the greedy ids are already the next step's input
         return self.ws.logits, self.ws.next_ids
