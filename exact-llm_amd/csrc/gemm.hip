@@ -719,12 +719,12 @@ int gemm_mfma(const void* x, int abits, const int8_t* wp, const int16_t* mp, con
 int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int R, int N,
                 int K, hipStream_t st, bool accumulate, const int64_t* colterm);
 
+// int16 rows with colterm: up to A16_GEMV_CHUNKS_MAX x 16 rows as GEMV row chunks (one weight stream per chunk, no
+// all-ones row needed), more rows as interleaved digit rows on the A8 GEMM, which streams the weights once. 7B prefill
+// (ms, graph replays): 32 tokens 5.47 and 48 tokens 7.74 as 2 and 3 chunks, 49 tokens 4.60 on the GEMM.
 #ifndef A16_GEMV_CHUNKS_MAX
-#define A16_GEMV_CHUNKS_MAX 3
+#define A16_GEMV_CHUNKS_MAX 1
 #endif
-
-// int16 rows with colterm: up to 3 x 16 rows as GEMV row chunks (one weight stream per chunk, no all-ones row
-// needed), more rows as interleaved digit rows on the A8 GEMM
 int gemm_a16_digit_rows(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, const int64_t* colterm,
                         int8_t* x8, int64_t* t, int M, int N, int K, hipStream_t st, bool zeroed) {
   if (M <= A16_GEMV_CHUNKS_MAX * 16) {

@@ -227,10 +227,10 @@ class Workspace:
         self.hsh = None   # (R, SI) SwiGLU values of the MoE shared expert (decode rows)
         self.eh = self.part_eh = None   # the routed experts' SwiGLU values per pair and their slice bit lengths
         self.I = I
-        # int16 GEMM rows (prefill above 48 rows): the producers also write their rows' int8 digit rows, which the
+        # int16 GEMM rows (prefill above 16 rows): the producers also write their rows' int8 digit rows, which the
         # GEMM reads directly (exact_gemm_g128_digits) instead of splitting them in a launch of its own
         self.dig = None
-        if abits == 15 and R > ops.GEMV_CHUNK_ROWS[7]:
+        if abits == 15 and R > ops.A16_DIGIT_ROWS:
             hmax = max(I, cfg.SI if cfg.moe else 0)
             self.dig = dict(x=z(2 * R, D, dt=I8), a=z(2 * R, H * hd, dt=I8), h=z(2 * R, hmax, dt=I8))
         if cfg.moe:

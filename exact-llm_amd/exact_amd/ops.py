@@ -222,7 +222,8 @@ def gemv_norm_swiglu(x_in, res_t, res_s, g, lin, s_out, silu, h, part, x_out=Non
 
 
 GEMV_CHUNK_ROWS = {15: 15, 7: 48}   # int8 rows: up to 3 GEMV row chunks in exact_gemm_g128; int16 rows above 15 take
-                                    # exact_gemm_g128_a16 (GEMV chunks of 16 with colterm up to 48 rows, digit rows beyond)
+                                    # exact_gemm_g128_a16 (one GEMV chunk of 16 with colterm, digit rows beyond)
+A16_DIGIT_ROWS = 16                 # int16 rows above this many run on the GEMM as digit rows (exact_gemm_g128_a16)
 _DIGIT_ROWS = {}                     # device -> int8 workspace of the A16 digit rows
 
 
@@ -239,11 +240,11 @@ def colterm(lin):
 
 def gemm_g128(x, abits, lin, out=None, zeroed=False, x8=None):
     """t = x . W for any R; zeroed: out holds zeros, so split paths add into it without a clear launch.
-    x8: the digit rows of the int16 x that its producer wrote (used above GEMV_CHUNK_ROWS[7] rows)."""
+    x8: the digit rows of the int16 x that its producer wrote (used above A16_DIGIT_ROWS rows)."""
     R, K = x.shape
     sfx = "_zeroed" if zeroed and out is not None else ""
     _need_packed(lin, "gemm_g128")
-    if x8 is not None and abits == 15 and R > GEMV_CHUNK_ROWS[7]:
+    if x8 is not None and abits == 15 and R > A16_DIGIT_ROWS:
         if K != lin.K:
             raise ExactError(f"exact_gemm_g128_digits: x has K = {K}, linear has K = {lin.K}")
         if out is None:
