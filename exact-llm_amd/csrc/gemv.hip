@@ -888,7 +888,7 @@ int zero_bytes(void* dst, int64_t nbytes, hipStream_t st) {
 #define GEMV_CUS 256
 #endif
 #ifndef GEMV_CHUNKS_MAX
-#define GEMV_CHUNKS_MAX 3
+#define GEMV_CHUNKS_MAX 1
 #endif
 // Above 4 rows each wave adds 64 x 16 int64 partial totals with atomics, so fewer group splits pay for most shapes.
 // Measured at 8 and 16 rows on the 7B shapes (us, int16 / int8 rows at 16): q|k|v 19.2 -> 11.3 / 17.9 -> 10.1 and
@@ -1188,8 +1188,9 @@ static int gemm_entry(const void* x, int32_t abits, const int8_t* wp, const int1
   if (e) return e;
   const int rmax = abits == 15 ? 15 : 16;
   if (R > GEMV_CHUNKS_MAX * rmax) return gemm_mfma(x, abits, wp, mp, mh, t, R, N, K, as_stream(stream), zeroed);
-  // Up to GEMV_CHUNKS_MAX row chunks: one GEMV per chunk streams the weights once per chunk, which beats the
-  // 128-row GEMM tiles (mostly padding at these R) while the weight passes stay few.
+  // Up to GEMV_CHUNKS_MAX row chunks: one GEMV per chunk streams the weights once per chunk. One chunk beats the
+  // GEMM's 128-row tiles (mostly padding at these R); a second weight pass does not (int8-row 7B prefill, ms: 32 tokens
+  // as 2 chunks 5.79, on the GEMM 4.82; 48 tokens as 3 chunks 8.23, on the GEMM 5.11).
   const size_t xrow = (size_t)K * (abits == 15 ? 2 : 1);
   for (int r0 = 0; r0 < R; r0 += rmax) {
     const int rows = R - r0 < rmax ? R - r0 : rmax;

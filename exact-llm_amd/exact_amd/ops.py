@@ -221,8 +221,8 @@ def gemv_norm_swiglu(x_in, res_t, res_s, g, lin, s_out, silu, h, part, x_out=Non
     return h, part
 
 
-GEMV_CHUNK_ROWS = {15: 15, 7: 48}   # int8 rows: up to 3 GEMV row chunks in exact_gemm_g128; int16 rows above 15 take
-                                    # exact_gemm_g128_a16 (one GEMV chunk of 16 with colterm, digit rows beyond)
+GEMV_CHUNK_ROWS = {15: 15, 7: 16}   # int8 rows: one GEMV row chunk in exact_gemm_g128, the GEMM beyond; int16 rows
+                                    # above 15 take exact_gemm_g128_a16 (one GEMV chunk of 16 with colterm, digit rows beyond)
 A16_DIGIT_ROWS = 16                 # int16 rows above this many run on the GEMM as digit rows (exact_gemm_g128_a16)
 _DIGIT_ROWS = {}                     # device -> int8 workspace of the A16 digit rows
 

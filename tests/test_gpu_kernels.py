@@ -61,9 +61,9 @@ def test_gemv_small_shapes(thr, abits, R, N, K):
 
 
 @pytest.mark.parametrize("abits", [15, 7])
-@pytest.mark.parametrize("R", [16, 37, 46, 49, 130])
+@pytest.mark.parametrize("R", [16, 17, 37, 46, 49, 130])
 def test_gemm_rows(thr, abits, R):
-    """Row chunks of the GEMV kernel (up to 3 chunks of 15 / 16 rows) and the GEMM kernels beyond."""
+    """One row chunk of the GEMV kernel (15 / 16 rows) and the GEMM kernels beyond."""
     N, K = 640, 512
     lin, kw, km = synth_lin(thr, 12, "gemm", N, K)
     lim = (1 << abits) - 1
