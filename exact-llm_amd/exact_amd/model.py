@@ -305,9 +305,10 @@ class TModel:
         return out
 
     # ---------------------------------------------------------------- one pass over R rows
-    def forward_rows(self, ws, want_logits=True, trace=None, independent=False):
+    def forward_rows(self, ws, want_logits=True, trace=None, independent=False, last_only=False):
         """Runs the model on ws.ids with (slot, pos) per row; KV of each row is written into the cache
-        at (slot, pos). Leaves logits in ws.logits and greedy ids in ws.next_ids.
+        at (slot, pos). Leaves logits in ws.logits and greedy ids in ws.next_ids (last_only: of the last row only, the
+        others are left as they were; the final norm, the head and the argmax run on that row alone).
         independent: every row is a different sequence (decode), so no row attends to another row's new key and
         the q/k/v epilogue runs inside the attention launch.
         trace: (TraceLayout, int64 device buffer): every linear's totals t are produced in the buffer's slots
@@ -454,6 +455,24 @@ class TModel:
             ops.logits_argmax(t_head, ws.s, ws.logits if want_logits else None, ws.next_ids, clear=clear,
                               part=ws.part_lg)
             return ws
+        if last_only and R > 1 and not keep:
+            # a prompt's last row only: its final norm, head GEMV and argmax; the other rows' residual totals are
+            # cleared for the next pass that accumulates into them
+            r = slice(R - 1, R)
+            if clear and res_t is not None:
+                ops.zero_(res_t[:R - 1])
+            ops.rmsnorm_qrow(ws.x[r], self.w.gf, self.abits, None if res_t is None else res_t[r],
+                             None if res_s is None else res_s[r], ws.xq[r], ws.s[r], clear=clear)
+            if head.mode == "group":
+                self._lin(ws.xq[r], head, ws.t_head[r])
+                ops.logits_argmax(ws.t_head[r], ws.s[r], ws.logits[r] if want_logits else None, ws.next_ids[r],
+                                  clear=clear, part=ws.part_lg)
+            else:
+                acc = ops.linear_t(ws.xq[r], self.abits, head)
+                ops.requant_channel(acc, ws.s[r], head.M, head.Mbits, head.bias, out=ws.t_head[r])
+                ops.logits_argmax(ws.t_head[r], ws.s28[r], ws.logits[r] if want_logits else None, ws.next_ids[r],
+                                  part=ws.part_lg)
+            return ws
         ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=clear, x8=dx)
         if head.mode == "group":
             t_head = slot("head") if keep else ws.t_head
@@ -539,26 +558,25 @@ class TModel:
         ws.pos.copy_(torch.arange(p0, p0 + T, dtype=I32))
         # the matrix-core attention for prefill chunks of PREFILL_MIN_ROWS rows or more (hd 128); the row kernel otherwise
         ws.seq = (slot, p0 + T) if T >= self.PREFILL_MIN_ROWS and self.cfg.hd == 128 else None
-        key = (T, id(cache), slot, p0)
+        key = (T, id(cache), slot, p0, bool(last_only))
         g = self._graphs.get(key) if graph else None
         try:
             if g is not None:
                 self._graphs.move_to_end(key)
                 g[0].replay()
             else:
-                self.forward_rows(ws)
+                self.forward_rows(ws, last_only=last_only)
                 if graph:   # capture the same pass (capture records, it does not run the kernels again)
                     cg = torch.cuda.CUDAGraph()
                     with torch.cuda.graph(cg):
-                        self.forward_rows(ws)
+                        self.forward_rows(ws, last_only=last_only)
                     self._graphs[key] = (cg, cache)   # the graph holds the cache's buffers
                     while len(self._graphs) > self.PREFILL_GRAPHS:
                         self._graphs.popitem(last=False)
         finally:
             ws.seq = None
         cache.n[slot] = p0 + T
-        out = ws.logits.clone()
-        return out[-1:] if last_only else out
+        return ws.logits[-1:].clone() if last_only else ws.logits.clone()
 
     def forward_traced(self, ids, cache=None, slot=0):
         """forward() that also returns the trace of the pass: {name: (T, n) int64} with the reference's names

@@ -194,3 +194,29 @@ def test_slot_outside_the_cache_is_rejected_before_any_launch():
             tm.forward_traced([1, 2, 3], cache, slot=bad)
     assert all(np.array_equal(host(t), b) for t, b in zip(cache.layers[0], before))
     assert cache.n == [0, 0]
+
+
+@pytest.mark.parametrize("name,abits,T", [("tiny", 15, 20), ("tiny", 15, 40), ("tiny-moe", 15, 24), ("tiny", 7, 30),
+                                          ("tiny-hd128", 15, 100)])
+def test_last_only_prefill_matches_full_prefill(name, abits, T):
+    """forward(last_only=True) computes the final norm, head and argmax for the last row only: its logits equal the
+    full pass's last row, eagerly and as graph replays, and the passes after it on the same workspace (whose residual
+    totals the last-row pass must leave cleared) still equal the oracle-pinned full pass."""
+    cfg = synth.CONFIGS[name]
+    w = DeviceWeights.synthetic(cfg, 5, DEV)
+    tm = TModel(w, Smax=2 * T + 8, abits=abits)
+    ids = helpers.prompt(11, T, cfg.V)
+    full = host(tm.forward(ids, tm.new_cache(B=1)))
+    for graph in (False, True, True):
+        last = host(tm.forward(ids, tm.new_cache(B=1), last_only=True, graph=graph))
+        assert last.shape == (1, cfg.V) and np.array_equal(last[0], full[-1]), graph
+    again = host(tm.forward(ids, tm.new_cache(B=1)))
+    assert np.array_equal(again, full)
+    # a second chunk continuing the cache, last row only, against the same chunk with every row
+    c1, c2 = tm.new_cache(B=1), tm.new_cache(B=1)
+    tm.forward(ids, c1)
+    tm.forward(ids, c2)
+    more = helpers.prompt(12, T, cfg.V)
+    a = host(tm.forward(more, c1))
+    b = host(tm.forward(more, c2, last_only=True))
+    assert np.array_equal(b[0], a[-1])
