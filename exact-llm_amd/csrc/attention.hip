@@ -302,6 +302,22 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
       cs[i][1] = j < hd ? sin_t[(int64_t)p * hd + j] : 0;
     }
   }
+  // the new token's totals (and biases) for the query head, the new key and the new value, loaded before the exp
+  // table's LDS stores, which wait for the table's loads: issued after them, these would wait a round trip more
+  constexpr int TV = (3 * 256 + NT - 1) / NT;   // hd <= 256
+  int64_t tv[TV], bv[TV];
+#pragma unroll
+  for (int i = 0; i < TV; ++i) {
+    const int j = tid + i * NT;
+    tv[i] = bv[i] = 0;
+    if (j < 3 * hd) {
+      const int which = j / hd, jj = j - which * hd;
+      const int base = which == 0 ? h * hd : (which == 1 ? (H + kh) * hd : (H + KV + kh) * hd);
+      tv[i] = t[(int64_t)r * N + base + jj];
+      if (b) bv[i] = b[base + jj];
+    }
+  }
+  const int sh = 28 - s[r];
   {   // the exp table into LDS: every piece loaded before the first store, with the loads above
     constexpr int NV = EXACT_EXP_N / 4, NK = (NV + NT - 1) / NT;
     v4i te[NK];
@@ -314,12 +330,13 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
       if (tid + k * NT < NV) reinterpret_cast<v4i*>(texp)[tid + k * NT] = te[k];
     if (tid < EXACT_EXP_N - 4 * NV) texp[4 * NV + tid] = tail;
   }
-  const int sh = 28 - s[r];
-  for (int j = tid; j < 3 * hd; j += blockDim.x) {
-    const int which = j / hd, jj = j - which * hd;
-    const int base = which == 0 ? h * hd : (which == 1 ? (H + kh) * hd : (H + KV + kh) * hd);
-    const int64_t val = shr64(t[(int64_t)r * N + base + jj], sh);
-    y[which][jj] = b ? val + b[base + jj] : val;
+#pragma unroll
+  for (int i = 0; i < TV; ++i) {
+    const int j = tid + i * NT;
+    if (j < 3 * hd) {
+      const int which = j / hd, jj = j - which * hd;
+      y[which][jj] = shr64(tv[i], sh) + bv[i];
+    }
   }
   __syncthreads();
   if (wave < 2) {   // wave 0: RoPE + qrow of the query head, wave 1: of the new key (k_qkv_rope_cache's steps)
