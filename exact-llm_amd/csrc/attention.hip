@@ -106,6 +106,10 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #ifndef ATT_WIDE_BLOCKS
 #define ATT_WIDE_BLOCKS 256
 #endif
+// short caches (at most 2 ATT_THREADS / 8 positions, hd a multiple of 64): 8 threads per cached key for the scores
+#ifndef ATT_KS8
+#define ATT_KS8 1
+#endif
 #ifndef ATT_VPF_LONG_BLOCKS
 #define ATT_VPF_LONG_BLOCKS 256
 #endif
@@ -244,8 +248,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
 // Latency: everything that does not depend on the new token (the RoPE row, each thread's first cached key and
 // its first ATT_VPF value pairs) is loaded together with t, so the block waits on memory about once before the
 // exp table.
-// KPF: 16-byte chunks of each thread's first cached key loaded with the totals (0: none)
-template <int VPF, int NT = ATT_THREADS, int KPF = ATT_KPF>
+// KPF: 16-byte chunks of each thread's first cached key loaded with the totals (0: none).
+// KS = 8 (caches of at most 2 NT / 8 positions, hd a multiple of 64): the scores of the cached keys are computed by 8
+// threads per key, hd / 8 dimensions each (coalesced 16-byte loads of the key row, a sum over the 8 lanes), NT / 8 keys
+// per pass and at most two passes, all loaded with the totals; KPF is then unused.
+template <int VPF, int NT = ATT_THREADS, int KPF = ATT_KPF, int KS = 1>
 __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
                                                                const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
                                                                const int64_t* __restrict__ sin_t, const int32_t* __restrict__ slot,
@@ -276,9 +283,28 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
   const int npair = hd >> 1, nparts = blockDim.x / npair;
   const int dp = tid % npair, pp = tid / npair;
   // ---- loads that do not depend on the new token, issued with the totals
-  v4i kpre[KPF > 0 ? KPF : 1];
+  v4i kpre[KPF > 0 && KS == 1 ? KPF : 1];
   int skpre = 0;
-  const bool kp = KPF > 0 && hd <= 8 * KPF && tid < p;
+  // KS = 8: thread (key kg = tid / 8, lane kl = tid % 8) holds dims [kl hd / 8, (kl + 1) hd / 8) of keys kg and
+  // kg + NT / 8 (two passes), at most 4 chunks of 16 bytes each
+  v4i ks8[2][4];
+  int sks8[2] = {0, 0};
+  const int kg = tid >> 3, kl = tid & 7;
+  if constexpr (KS == 8) {
+    const int nv = hd >> 6;   // 16-byte chunks per thread and key
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      const int si = kg + ps * (NT / 8);
+      if (si < p) {
+        const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + si) * hd + kl * (hd >> 3));
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (c < nv) ks8[ps][c] = kr[c];
+        sks8[ps] = sk[cbase + si];
+      }
+    }
+  }
+  const bool kp = KS == 1 && KPF > 0 && hd <= 8 * KPF && tid < p;
   if (kp) {
     const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + tid) * hd);
 #pragma unroll
@@ -381,7 +407,35 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
   }
   const int S = p + 1;
   int64_t mx = INT64_MIN;
-  for (int si = tid; si < p; si += blockDim.x) {
+  if constexpr (KS == 8) {
+    const int nv = hd >> 6;
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      const int si = kg + ps * (NT / 8);
+      int64_t dot = 0;
+      if (si < p) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (c < nv) {
+            const v4i kk = ks8[ps][c], qq = reinterpret_cast<const v4i*>(qs16 + kl * (hd >> 3))[c];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dot += (int64_t)dot2(qq[e], kk[e]);
+          }
+        }
+      }
+      // sum over the 8 lanes of the key (lanes 8 kg .. 8 kg + 7): exchange with lane ^ 1, lane ^ 2, then the mirrored
+      // lane of the 8-lane half row; every lane of the key ends with its dot product
+      dot += dpp64<0xB1>(dot);
+      dot += dpp64<0x4E>(dot);
+      dot += dpp64<0x141>(dot);
+      if (si < p) {
+        const int64_t val = shr64(dot * INV, 32 - sqv - sks8[ps]);
+        if (kl == 0) sc[si] = val;
+        mx = val > mx ? val : mx;
+      }
+    }
+  }
+  for (int si = tid; KS == 1 && si < p; si += blockDim.x) {
     const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + si) * hd);
     int64_t dot = 0;
     int skv;
@@ -505,6 +559,9 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
   } else if (Smax > ATT_VPF_LONG_S)
     hipLaunchKernelGGL(k_attention_qkv<ATT_VPF_LONG>, dim3(R, H), dim3(ATT_THREADS), lds, as_stream(stream), t, s, b, cos_t,
                        sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
+  else if (ATT_KS8 && hd % 64 == 0 && Smax <= 2 * (ATT_THREADS / 8))
+    hipLaunchKernelGGL((k_attention_qkv<ATT_VPF, ATT_THREADS, ATT_KPF, 8>), dim3(R, H), dim3(ATT_THREADS), lds,
+                       as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
   else
     hipLaunchKernelGGL(k_attention_qkv<ATT_VPF>, dim3(R, H), dim3(ATT_THREADS), lds, as_stream(stream), t, s, b, cos_t, sin_t,
                        slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
