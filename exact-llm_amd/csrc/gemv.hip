@@ -480,8 +480,10 @@ combine:
 // group loop on the LDS row. Block 0 writes x to x_out (another buffer: the other blocks are still reading x_in), the
 // row shifts to s_out and, when xq_out is given, the quantised rows. t += x.W (accumulate). Replaces an
 // exact_rmsnorm_qrow launch + exact_gemv_g128_acc.
-template <bool NT, int VR, int EPT, bool WIDE>
-__global__ __launch_bounds__(256) void k_gemv_g128_norm(const int64_t* __restrict__ x_in, int64_t* __restrict__ x_out,
+// BW waves per block (4, or 8 for wide rows: one block per CU reads the row once, and the weight tiles of its 8
+// tasks load while it normalises)
+template <bool NT, int VR, int EPT, bool WIDE, int BW = 4>
+__global__ __launch_bounds__(64 * BW) void k_gemv_g128_norm(const int64_t* __restrict__ x_in, int64_t* __restrict__ x_out,
                                                         const int64_t* __restrict__ res_t, const int32_t* __restrict__ res_s,
                                                         const int64_t* __restrict__ gain, const int8_t* __restrict__ wp,
                                                         const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
@@ -490,13 +492,13 @@ __global__ __launch_bounds__(256) void k_gemv_g128_norm(const int64_t* __restric
   extern __shared__ __attribute__((aligned(16))) int8_t xlds[];   // R rows of K quantised int16 values
   __shared__ RowScratch sc;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int task = blockIdx.x * 4 + wave;
+  const int task = blockIdx.x * BW + wave;
   const int nbs = (N + 63) >> 6;
   const bool writer = blockIdx.x == 0;
   int16_t* xl = reinterpret_cast<int16_t*>(xlds);
   auto norm = [&]() {   // block-wide: every wave of the block runs it, with or without a task
     for (int r = 0; r < R; ++r)
-      norm_qrow_row<EPT>(r, 256, x_in, res_t, res_s, gain, 15, K, xl + (size_t)r * K, writer ? x_out : nullptr, nullptr,
+      norm_qrow_row<EPT>(r, 64 * BW, x_in, res_t, res_s, gain, 15, K, xl + (size_t)r * K, writer ? x_out : nullptr, nullptr,
                          writer ? s_out : nullptr, writer ? xq_out : nullptr, nullptr, sc);
     __syncthreads();
   };
@@ -1023,6 +1025,9 @@ extern "C" int exact_gemv(const int16_t* x, const int8_t* wT, const int64_t* Mg,
 // rows of one norm-fused GEMV launch (each block runs the row program once per row) and the row width its 256 threads
 // hold in registers (24 values each)
 #define GEMV_NORM_ROWS 2
+#ifndef GEMV_NORM_BW8_K
+#define GEMV_NORM_BW8_K 2048
+#endif
 #define GEMV_NORM_KMAX (256 * 24)
 
 extern "C" int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, const int64_t* res_t, const int32_t* res_s,
@@ -1037,17 +1042,24 @@ extern "C" int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, con
   const int nsplit = gemv_nsplit(N, G, R, 15);
   const int64_t tasks = (int64_t)((N + 63) / 64) * nsplit;
   const size_t lds = (size_t)R * K * 2;
-  dim3 grid((unsigned)((tasks + 3) / 4)), block(256);
   hipStream_t st = as_stream(stream);
-  const int ept = (K + 255) / 256;
-#define NORM_GO(VR, E)                                                                                                  \
+  // rows wider than GEMV_NORM_BW8_K whose tasks fit one round of 8-wave blocks: 8-wave blocks (see the kernel)
+  const bool bw8 = K > GEMV_NORM_BW8_K && (tasks + 7) / 8 <= GEMV_CUS;
+  const int bw = bw8 ? 8 : 4;
+  dim3 grid((unsigned)((tasks + bw - 1) / bw)), block(64 * bw);
+  const int ept = (K + 64 * bw - 1) / (64 * bw);
+#define NORM_GO_BW(VR, E, BW)                                                                                           \
   do {                                                                                                                  \
     if (mh)                                                                                                             \
-      hipLaunchKernelGGL((k_gemv_g128_norm<GEMV_NT != 0, VR, E, true>), grid, block, lds, st, x_in, x_out, res_t, res_s, g, \
-                         wp, mp, mh, t, s_out, xq_out, R, N, K, G, nsplit);                                             \
-    else                                                                                                                \
-      hipLaunchKernelGGL((k_gemv_g128_norm<GEMV_NT != 0, VR, E, false>), grid, block, lds, st, x_in, x_out, res_t, res_s,  \
+      hipLaunchKernelGGL((k_gemv_g128_norm<GEMV_NT != 0, VR, E, true, BW>), grid, block, lds, st, x_in, x_out, res_t, res_s,\
                          g, wp, mp, mh, t, s_out, xq_out, R, N, K, G, nsplit);                                          \
+    else                                                                                                                \
+      hipLaunchKernelGGL((k_gemv_g128_norm<GEMV_NT != 0, VR, E, false, BW>), grid, block, lds, st, x_in, x_out, res_t,     \
+                         res_s, g, wp, mp, mh, t, s_out, xq_out, R, N, K, G, nsplit);                                   \
+  } while (0)
+#define NORM_GO(VR, E)                                                                                                  \
+  do {                                                                                                                  \
+    if (bw8) NORM_GO_BW(VR, E, 8); else NORM_GO_BW(VR, E, 4);                                                           \
   } while (0)
 #define NORM_EPT(VR)                                                                                                    \
   do {                                                                                                                  \
@@ -1060,6 +1072,7 @@ extern "C" int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, con
   if (R == 1) NORM_EPT(1); else NORM_EPT(2);
 #undef NORM_EPT
 #undef NORM_GO
+#undef NORM_GO_BW
   return launch_status("gemv_g128_norm_acc");
 }
 

@@ -277,6 +277,7 @@ class TModel:
     # 3584-wide rows that costs as much as the separate launch it saves, at 5120 more, at 896 less: 7.0 vs 8.2 us)
     NORM_FUSE_D = 2048
     NORM_SWIGLU = True   # norm-fused decode: the SwiGLU in the gate|up GEMV's epilogue too
+    QKV_NORM = True   # dense decode rows wider than NORM_FUSE_D: the attention norm inside the q|k|v GEMV
     SHARED_SWIGLU = True   # MoE decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue
     EXPERT_SWIGLU = True   # MoE decode rows: the routed experts' SwiGLU and qrow inside their GEMVs
     EXPERT_GEMM_MIN_PAIRS = 64   # (row, expert) pairs from which the MoE experts run as one grouped GEMM
@@ -335,6 +336,11 @@ class TModel:
         # gate|up, head), which read one residual buffer and write the other
         nfuse = (afuse and self.abits == 15 and not c.moe and R <= ops.NORM_FUSE_ROWS and D <= self.NORM_FUSE_D
                  and self.w.head.mode == "group")
+        # wider dense rows: the attention's residual + RMSNorm + qrow inside the q|k|v GEMV only (8-wave blocks, one per
+        # CU, read the row once); the FFN norm stays a launch of its own before the SwiGLU GEMV
+        qfuse = (self.QKV_NORM and group and afuse and not nfuse and self.abits == 15 and not c.moe
+                 and R <= ops.NORM_FUSE_ROWS and D <= ops.NORM_FUSE_KMAX
+                 and (ops.norm_gemv_one_block_per_cu(self.w.layers[0]["qkv"].N, D, R) or D <= ops.GEMV_NORM_BW8_K))
         # decode rows of dense int16 models whose gate|up GEMV is not the norm-fused one: the SwiGLU runs in the gate|up
         # GEMV's epilogue (no totals, no atomics, one launch fewer)
         sfuse = (xfuse and not nfuse and not c.moe and self.abits == 15 and R <= ops.SWIGLU_GEMV_ROWS and c.I % 64 == 0
@@ -357,15 +363,15 @@ class TModel:
                 t_qkv, t_o, t_gu, t_d = (slot(f"L{li}.{k}") for k in ("qkv", "o", "gateup", "down"))
             else:
                 t_qkv, t_o, t_gu, t_d = ws.t_qkv, ws.t_o, ws.t_gu, ws.t_d
-            if nfuse:
+            if nfuse or qfuse:
                 ops.gemv_norm_acc(x_cur, res_t, res_s, L["g1"], L["qkv"], t_qkv, ws.s,
                                   x_out=x_nxt if res_t is not None else None)
                 if res_t is not None:
                     x_cur, x_nxt = x_nxt, x_cur
                 s_qkv, b_qkv = ws.s, L["qkv"].bias
             else:
-                ops.rmsnorm_qrow(ws.x, L["g1"], self.abits, res_t, res_s, ws.xq, ws.s, clear=clear, x8=dx)
-            if nfuse:
+                ops.rmsnorm_qrow(x_cur, L["g1"], self.abits, res_t, res_s, ws.xq, ws.s, clear=clear, x8=dx)
+            if nfuse or qfuse:
                 pass
             elif group:
                 self._lin(ws.xq, L["qkv"], t_qkv, x8=dx)
@@ -391,9 +397,9 @@ class TModel:
                     ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv, ws.obits)
             if nfuse:   # also clears the down totals the q|k|v GEMV read as its residual (t_qkv and t_d are one range)
                 ops.gemv_qrow_acc(ws.att, ws.obits, H, self.abits, L["o"], t_o, ws.sa, zero=ws.t_qd if clear else None)
-            elif xfuse:
+            elif xfuse:   # clears the q|k|v totals attention left (and, q|k|v norm-fused, the down totals it read)
                 ops.gemv_qrow_acc(ws.att, ws.obits, H, self.abits, L["o"], t_o, ws.sa,
-                                  zero=t_qkv if afuse and clear else None)   # the q|k|v totals attention left
+                                  zero=(ws.t_qd if qfuse else t_qkv) if afuse and clear else None)
             else:
                 ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa, x8=da)
             if nfuse and nsfuse:   # norm + gate|up + SwiGLU in one launch
@@ -415,7 +421,7 @@ class TModel:
             if group:
                 if not xfuse:
                     self._lin(ws.aq, L["o"], t_o, x8=da)
-                ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, t_o, ws.sa, ws.xq, ws.s, clear=clear, x8=dx)
+                ops.rmsnorm_qrow(x_cur, L["g2"], self.abits, t_o, ws.sa, ws.xq, ws.s, clear=clear, x8=dx)
             else:
                 self._lin_channel(ws.aq, ws.sa, L["o"], ws.t_o)
                 ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.s28, ws.xq, ws.s)
@@ -461,7 +467,7 @@ class TModel:
             r = slice(R - 1, R)
             if clear and res_t is not None:
                 ops.zero_(res_t[:R - 1])
-            ops.rmsnorm_qrow(ws.x[r], self.w.gf, self.abits, None if res_t is None else res_t[r],
+            ops.rmsnorm_qrow(x_cur[r], self.w.gf, self.abits, None if res_t is None else res_t[r],
                              None if res_s is None else res_s[r], ws.xq[r], ws.s[r], clear=clear)
             if head.mode == "group":
                 self._lin(ws.xq[r], head, ws.t_head[r])
@@ -473,7 +479,7 @@ class TModel:
                 ops.logits_argmax(ws.t_head[r], ws.s28[r], ws.logits[r] if want_logits else None, ws.next_ids[r],
                                   part=ws.part_lg)
             return ws
-        ops.rmsnorm_qrow(ws.x, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=clear, x8=dx)
+        ops.rmsnorm_qrow(x_cur, self.w.gf, self.abits, res_t, res_s, ws.xq, ws.s, clear=clear, x8=dx)
         if head.mode == "group":
             t_head = slot("head") if keep else ws.t_head
             self._lin(ws.xq, head, t_head, x8=dx)

@@ -72,9 +72,11 @@ def test_synthetic_prefill_and_decode_match_oracle(name):
         assert tok == otoks[i]
 
 
+@pytest.mark.parametrize("qkv_norm", [True, False])
 @pytest.mark.parametrize("name", ["tiny", "tiny-hd128"])
-def test_decode_with_swiglu_in_the_gate_up_gemv_matches_oracle(name):
-    """Decode rows whose norms run as launches of their own (the norm-fused GEMVs off, as for hidden sizes above 2048):
+def test_decode_with_swiglu_in_the_gate_up_gemv_matches_oracle(name, qkv_norm):
+    """Decode rows of hidden sizes above 2048 (the fully norm-fused GEMVs off): the attention norm inside the q|k|v GEMV
+    (qkv_norm, the residual alternating between two buffers) or a launch of its own, the FFN norm a launch of its own;
     the gate|up GEMV applies the SwiGLU in its epilogue and the down GEMV quantises its per-64-column bit lengths.
     Logits and greedy tokens equal the oracle's, eagerly and through the graph; a 2-token prefill takes the same
     path."""
@@ -83,6 +85,7 @@ def test_decode_with_swiglu_in_the_gate_up_gemv_matches_oracle(name):
     om = helpers.oracle_model(cfg, seed, T=64)
     tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=64)
     tm.NORM_FUSE_D = 0
+    tm.QKV_NORM = qkv_norm
     ids = helpers.prompt(11, 14, cfg.V)
     otoks, orows = O.greedy_decode(om, ids[:10], 6)
     cache = tm.new_cache(B=1)
