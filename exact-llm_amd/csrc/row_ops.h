@@ -20,7 +20,7 @@ __device__ __forceinline__ void store_digits(int8_t* x8, int64_t r, int64_t K, i
 // their own).
 struct RowScratch {
   int a[16], c[16];
-  int64_t b[16];
+  int64_t b[16], d[16];
 };
 
 // numpy floor division a // b for any int64 a and b != 0, kept out of line: the lean row program below calls it
@@ -115,20 +115,40 @@ __device__ __forceinline__ void norm_qrow_row(int r, int nt, const int64_t* x_in
     hi = v[j] > hi ? v[j] : hi;
     lo = v[j] < lo ? v[j] : lo;
   }
-  const int m = block_max_i32(bitlen_maxabs(hi, lo), sc.a);   // bit length of max |x|
-  const int k = m > 24 ? m - 24 : 0;
-  int64_t ss = 0;
-  if (k == 0) {
+  // the bit length m of max |x| and, for the case m <= 24 (k = 0), the sum of squares, in one reduction: a thread
+  // whose own values exceed 2^24 adds 0 (the sum is then not used), so every partial stays below 2^61
+  const int ml = bitlen_maxabs(hi, lo);
+  uint64_t s0 = 0;
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) ss += (int64_t)(int)v[j] * (int)v[j];
-  } else {
+  for (int j = 0; j < EPT; ++j) s0 += (uint64_t)((int64_t)(int)v[j] * (int)v[j]);
+  int m = wave_max_i32(ml);
+  int64_t ss = wave_sum64(ml <= 24 ? (int64_t)s0 : 0);
+  if ((tid & 63) == 0) {
+    sc.a[tid >> 6] = m;
+    sc.b[tid >> 6] = ss;
+  }
+  __syncthreads();
+  {
+    const int nw = nt >> 6;
+    uint64_t st = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      m = i < nw && sc.a[i] > m ? sc.a[i] : m;
+      st += i < nw ? (uint64_t)sc.b[i] : 0;
+    }
+    ss = (int64_t)st;
+  }
+  const int k = m > 24 ? m - 24 : 0;
+  if (k > 0) {   // block-uniform
+    ss = 0;
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
       const int xs = (int)rsh_pos(v[j], k);   // |xs| <= 2^24
       ss += (int64_t)xs * xs;
     }
+    ss = block_sum64_1(ss, sc.d);
   }
-  ss = block_sum64_1(ss, sc.b);   // 0 <= ss < 2^62 (squares of at most 2^48, D of at most 2^13)
+  // 0 <= ss < 2^62 (squares of at most 2^48, D of at most 2^13)
   // ms = ss // D + 1 and rt = isqrt(ms): float64 estimates (a reciprocal prepared early, the hardware square root),
   // each corrected exactly; the scalar chain is short because it sits between two block reductions
   int64_t qm = (int64_t)((double)ss * rD), rm = ss - qm * D;
