@@ -110,6 +110,11 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #ifndef ATT_KS8
 #define ATT_KS8 1
 #endif
+// ... with ATT_WIDE_THREADS-thread blocks for heads of at least ATT_KS8_WIDE_HD dimensions when the (row, head) blocks
+// fit one round (7B bs1 decode at a 16-token prompt, A/B: 2.114-2.140 -> 2.101-2.126 ms a step; hd 64 at 0.5B: no gain)
+#ifndef ATT_KS8_WIDE_HD
+#define ATT_KS8_WIDE_HD 128
+#endif
 #ifndef ATT_VPF_LONG_BLOCKS
 #define ATT_VPF_LONG_BLOCKS 256
 #endif
@@ -559,6 +564,10 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
   } else if (Smax > ATT_VPF_LONG_S)
     hipLaunchKernelGGL(k_attention_qkv<ATT_VPF_LONG>, dim3(R, H), dim3(ATT_THREADS), lds, as_stream(stream), t, s, b, cos_t,
                        sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
+  else if (ATT_KS8 && ATT_KS8_WIDE_HD && hd % 64 == 0 && hd >= ATT_KS8_WIDE_HD && (2 * ATT_WIDE_THREADS) % hd == 0 &&
+           Smax <= 2 * (ATT_WIDE_THREADS / 8) && (int64_t)R * H <= ATT_WIDE_BLOCKS)
+    hipLaunchKernelGGL((k_attention_qkv<ATT_VPF, ATT_WIDE_THREADS, ATT_KPF, 8>), dim3(R, H), dim3(ATT_WIDE_THREADS), lds,
+                       as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
   else if (ATT_KS8 && hd % 64 == 0 && Smax <= 2 * (ATT_THREADS / 8))
     hipLaunchKernelGGL((k_attention_qkv<ATT_VPF, ATT_THREADS, ATT_KPF, 8>), dim3(R, H), dim3(ATT_THREADS), lds,
                        as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
