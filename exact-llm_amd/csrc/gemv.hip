@@ -881,8 +881,9 @@ int zero_bytes(void* dst, int64_t nbytes, hipStream_t st) {
 #ifndef GEMV_WAVES
 #define GEMV_WAVES 3072
 #endif
-// ... and for decode rows (R <= 4): 7B bs1 decode 2.104-2.122 -> 2.090-2.104 ms a step, 14B 4.174-4.183 -> 4.150-4.156
-// against 3072 (the down GEMV's 148 groups in 74 splits instead of 55); 6144 and 8192 slower, bs8 and 0.5B unchanged
+// ... and for int16 decode rows (R <= 4): 7B bs1 decode 2.104-2.122 -> 2.090-2.104 ms a step, 14B 4.174-4.183 ->
+// 4.150-4.156 against 3072 (the down GEMV's 148 groups in 74 splits instead of 55); 6144 and 8192 slower, bs8 and 0.5B
+// unchanged. int8 rows keep 3072: their large GEMVs then fit one round of 16-wave blocks (down: 56 x 55 tasks)
 #ifndef GEMV_DECODE_WAVES
 #define GEMV_DECODE_WAVES 4096
 #endif
@@ -902,7 +903,7 @@ int zero_bytes(void* dst, int64_t nbytes, hipStream_t st) {
 // o 15.3 -> 11.3 / 13.7 -> 9.7 at 768 waves instead of 3072; gate|up (592 row blocks) 39.9 -> 32.6 at 1536 for int16
 // rows; int8 gate|up and down (148 groups) stay fastest at 3072.
 static int64_t gemv_waves(int64_t nbs, int G, int R, int abits) {
-  if (R <= 4) return GEMV_DECODE_WAVES;
+  if (R <= 4) return abits == 15 ? GEMV_DECODE_WAVES : GEMV_WAVES;
   if (abits == 15) return nbs > 256 ? 1536 : 768;
   return (nbs > 256 || G > 64) ? GEMV_WAVES : 768;
 }
