@@ -296,28 +296,32 @@ __global__ void k_embed(const int32_t* __restrict__ ids, const int32_t* __restri
 // logits = shr(t, 28 - s) over slices of LSLICE columns; each slice's first maximum (value, index)
 // goes to part; k_argmax_parts picks the row's first maximum (exact_llm.py:267: np.argmax)
 #define LSLICE 4096
+#ifndef LOGITS_THREADS
+#define LOGITS_THREADS 1024   // threads of one slice's block (LSLICE / LOGITS_THREADS logits each)
+#endif
 __device__ __forceinline__ void argmax_merge(int64_t& best, int& bidx, int64_t ov, int oi) {
   if (ov > best || (ov == best && oi < bidx)) { best = ov; bidx = oi; }
 }
 
-__global__ __launch_bounds__(256) void k_logits_part(int64_t* t, const int32_t* __restrict__ s, int64_t* lg,
-                                                     int64_t* __restrict__ part, int N, int nparts, int clear_t) {
-  __shared__ int64_t bv[4];
-  __shared__ int bi[4];
+template <int NT>
+__global__ __launch_bounds__(NT) void k_logits_part(int64_t* t, const int32_t* __restrict__ s, int64_t* lg,
+                                                    int64_t* __restrict__ part, int N, int nparts, int clear_t) {
+  __shared__ int64_t bv[NT / 64];
+  __shared__ int bi[NT / 64];
   const int r = blockIdx.y, b = blockIdx.x;
   const int sh = 28 - s[r];
-  constexpr int EPT = LSLICE / 256;
+  constexpr int EPT = LSLICE / NT;
   int64_t tv[EPT];
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
-    const int i = b * LSLICE + j * 256 + threadIdx.x;
+    const int i = b * LSLICE + j * NT + threadIdx.x;
     tv[j] = i < N ? t[(int64_t)r * N + i] : 0;
   }
   int64_t best = INT64_MIN;
   int bidx = 0x7fffffff;
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
-    const int i = b * LSLICE + j * 256 + threadIdx.x;
+    const int i = b * LSLICE + j * NT + threadIdx.x;
     if (i < N) {
       const int64_t v = shr64(tv[j], sh);
       if (clear_t) t[(int64_t)r * N + i] = 0;
@@ -497,7 +501,7 @@ extern "C" int exact_logits_argmax(int64_t* t, const int32_t* s, int64_t* lg, in
   if (!t || !s || !part || R <= 0 || N <= 0 || (clear_t && lg == t)) return EXACT_E_ARG;
   const int np = (N + LSLICE - 1) / LSLICE;
   hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(k_logits_part, dim3(np, R), dim3(256), 0, st, t, s, lg, part, N, np, clear_t);
+  hipLaunchKernelGGL(k_logits_part<LOGITS_THREADS>, dim3(np, R), dim3(LOGITS_THREADS), 0, st, t, s, lg, part, N, np, clear_t);
   if (ids) hipLaunchKernelGGL(k_argmax_parts, dim3(R), dim3(64), 0, st, part, np, ids);
   return launch_status("logits_argmax");
 }
@@ -547,7 +551,7 @@ extern "C" int exact_logits_argmax_noalloc(int64_t* t, const int32_t* s, int64_t
   if (e) return e;
   const int np = (N + LSLICE - 1) / LSLICE;   // every (row, slice) entry read below is written first by this call
   hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(k_logits_part, dim3(np, R), dim3(256), 0, st, t, s, lg, part, N, np, clear_t);
+  hipLaunchKernelGGL(k_logits_part<LOGITS_THREADS>, dim3(np, R), dim3(LOGITS_THREADS), 0, st, t, s, lg, part, N, np, clear_t);
   if (ids) hipLaunchKernelGGL(k_argmax_parts, dim3(R), dim3(64), 0, st, part, np, ids);
   return launch_status("logits_argmax_noalloc");
 }
