@@ -550,6 +550,90 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void k_gemm_a8p(const int8_t* __re
   }
 }
 
+}  // namespace exact
+#include "../_build/gemm_asm.inc"
+namespace exact {
+
+// The A8 GEMM (and A16 as digit-row pairs) with its main loop in generated assembly (gen_gemm_asm.py, which states
+// the schedule and the register map): 256 x 128 tiles (128 x 128 output rows x columns for PAIRS), one K pass, plain
+// stores. This function computes the block's tile, every per-lane copy / read / store offset and the scalar state,
+// and hands them to the asm in pinned registers. Mrows: rows of the A operand (digit rows for PAIRS); tiles past
+// M or N (ragged edges) store under a lane mask; A rows past Mrows read row Mrows - 1 (never stored).
+template <bool PAIRS>
+__global__ __launch_bounds__(512, 1) void k_gemm_asm(const int8_t* __restrict__ xb, const int8_t* __restrict__ wp,
+                                                     const int16_t* __restrict__ mp, int64_t* __restrict__ t,
+                                                     const int64_t* __restrict__ colterm, int Mrows, int N, int K, int G,
+                                                     int nbs, int tiles_m, int tiles_n) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int j = lane & 15, q = lane >> 4;
+  // XCD-aware order as k_gemm_a8p: the blocks of one XCD take consecutive tiles (one column block, its row blocks)
+  const int nblk = tiles_m * tiles_n;
+  const int per_xcd = (nblk + 7) / 8;
+  const int lb = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (lb >= nblk) return;
+  const int bn = lb / tiles_m, bm = lb - bn * tiles_m;
+  const int row0 = bm * 256, nb0 = bn * 2, col0 = nb0 * 64;
+  const int g0 = 0, g1 = G;
+  const int iters = __builtin_amdgcn_readfirstlane((g1 - g0 + 5) / 6);
+  const int phase = __builtin_amdgcn_readfirstlane(6 * iters - (g1 - g0));
+  // copy offsets: A segment i of this wave = rows 8 (4 wave + i) + lane / 8, chunk slot lane % 8 holding the row's
+  // 16-byte chunk (lane % 8) ^ ((row >> 1) & 7)
+  uint32_t vad[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (wave * 4 + i) * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+    const int gr = row0 + r < Mrows ? row0 + r : Mrows - 1;
+    vad[i] = (uint32_t)gr * (uint32_t)K + (uint32_t)(c * 16);
+  }
+  // B: LDS slot 16 cs + j of each 1 KiB chunk holds column 4 j + cs of the packed tile
+  const int vbdma = (4 * (lane & 15) + (lane >> 4)) * 16;
+  int bc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int seg = wave * 2 + i;
+    const int tl = nb0 + (seg >> 3) < nbs ? (seg >> 3) : nbs - 1 - nb0;   // a missing second tile reads the first
+    bc[i] = (nb0 + tl) * 8192 + (seg & 7) * 1024;
+  }
+  const int ncol = (nbs - nb0) * 64;
+  const int vmdma = (2 * lane < ncol ? 2 * lane : ncol - 2) * 2;
+  // LDS read bases (the asm adds stage, sub-tile and k-half offsets as immediates)
+  int vard[4];
+#pragma unroll
+  for (int kh = 0; kh < 2; ++kh) {
+    vard[kh] = wm * 8192 + j * 128 + (((kh * 4 + q) ^ ((j >> 1) & 7)) << 4);
+    vard[2 + kh] = vard[kh] + GEMM_ASM_A_HI;
+  }
+  const int vbrd = GEMM_ASM_B_BASE + wn * 8192 + q * 1024 + j * 16;
+  const int vmrd = GEMM_ASM_M_BASE + wave * 256 + wn * 128 + 8 * j;
+  // outputs: the lane's first row (4 rows, or 2 output rows of digit-row pairs, per 16-row sub-tile) and 4 columns
+  const int Mout = PAIRS ? Mrows / 2 : Mrows;
+  const int orow = PAIRS ? row0 / 2 + wm * 32 + 2 * q : row0 + wm * 64 + 4 * q;
+  const int ocol = col0 + wn * 64 + 4 * j;
+  const int vst = (int)(((uint32_t)orow * (uint32_t)N + (uint32_t)ocol) * 8u);
+  const int full =
+      __builtin_amdgcn_readfirstlane(((PAIRS ? row0 / 2 + 128 <= Mout : row0 + 256 <= Mrows) && col0 + 128 <= N) ? 1 : 0);
+  const __amdgpu_buffer_rsrc_t rA =
+      __builtin_amdgcn_make_buffer_rsrc((void*)xb, (short)0, (int)((uint32_t)Mrows * (uint32_t)K), BUF_DW3);
+  const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc((void*)wp, (short)0, -1, BUF_DW3);
+  const __amdgpu_buffer_rsrc_t rM = __builtin_amdgcn_make_buffer_rsrc((void*)mp, (short)0, -1, BUF_DW3);
+  const __amdgpu_buffer_rsrc_t rT = __builtin_amdgcn_make_buffer_rsrc((void*)t, (short)0, -1, BUF_DW3);
+  const int asoff = g0 * 128, bg = g0 * nbs * 8192, mg = (g0 * nbs + nb0) * 128;
+  const int wavea = wave * 4096, waveb = GEMM_ASM_B_BASE + wave * 2048, wavem = GEMM_ASM_M_BASE + wave * 256;
+  if constexpr (PAIRS) {
+    const __amdgpu_buffer_rsrc_t rCt = __builtin_amdgcn_make_buffer_rsrc((void*)colterm, (short)0, -1, BUF_DW3);
+    const int ctoff = (ocol < N ? ocol : 0) * 8;
+    gemm_asm_main_pairs(g0, g1, iters, phase, full, asoff, bg, bc[0], bc[1], mg, nbs * 8192, nbs * 128, wavea, waveb,
+                        wavem, N * 8, Mout, N, rA, rB, rM, rT, (int)vad[0], (int)vad[1], (int)vad[2], (int)vad[3], vbdma,
+                        vmdma, vard[0], vard[1], vard[2], vard[3], vbrd, vmrd, vst, orow, ocol, rCt, ctoff);
+  } else {
+    gemm_asm_main_a8(g0, g1, iters, phase, full, asoff, bg, bc[0], bc[1], mg, nbs * 8192, nbs * 128, wavea, waveb, wavem,
+                     N * 8, Mout, N, rA, rB, rM, rT, (int)vad[0], (int)vad[1], (int)vad[2], (int)vad[3], vbdma, vmdma,
+                     vard[0], vard[1], vard[2], vard[3], vbrd, vmrd, vst, orow, ocol);
+  }
+}
+
 // int16 rows -> interleaved int8 digit rows: x8[2r] = x[r] >> 8, x8[2r + 1] = (x[r] & 255) - 128.
 // 16 values per thread; K % 16 == 0.
 __global__ __launch_bounds__(256) void k_split_rows_a16(const int16_t* __restrict__ x, int8_t* __restrict__ x8, int64_t M,
@@ -630,6 +714,29 @@ static int gemm_launch(const void* x, const int8_t* wp, const int16_t* mp, int64
 #define GEMM_A8P_CFG 4, 2, 3
 #endif
 
+#ifndef GEMM_ASM
+#define GEMM_ASM 1
+#endif
+
+// M: rows of the A operand (digit rows for PAIRS); one K pass, t fully overwritten
+template <bool PAIRS>
+static int gemm_launch_asm(const int8_t* x, const int8_t* wp, const int16_t* mp, int64_t* t, const int64_t* colterm, int M,
+                           int N, int K, hipStream_t st) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_asm<PAIRS>), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              GEMM_ASM_LDS_BYTES);
+    attr_set = true;
+  }
+  const int G = K / 128, nbs = (N + 63) / 64;
+  const int tiles_m = (M + 255) / 256, tiles_n = (nbs + 1) / 2;
+  const int nblk = tiles_m * tiles_n;
+  const int grid = ((nblk + 7) / 8) * 8;
+  hipLaunchKernelGGL(k_gemm_asm<PAIRS>, dim3(grid), dim3(512), GEMM_ASM_LDS_BYTES, st, x, wp, mp, t, colterm, M, N, K, G,
+                     nbs, tiles_m, tiles_n);
+  return launch_status("gemm_g128");
+}
+
 // M: rows of the A operand (digit rows when PAIRS: the output has M / 2 rows, written through colterm)
 template <int WM, int WN, int S, bool PAIRS, bool WIDE>
 static int gemm_launch_a8p_t(const void* x, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t, int M, int N,
@@ -651,6 +758,10 @@ static int gemm_launch_a8p_t(const void* x, const int8_t* wp, const int16_t* mp,
     while (tiles_m * tiles_n * ksplit < GEMM_SPLIT_TILES && G / (ksplit * 2) >= 8) ksplit *= 2;
   }
   if (ksplit > G) ksplit = G;
+  // one K pass over enough tiles: the assembly main loop (same tiles and outputs; 32-bit offsets into x, W and t)
+  if (GEMM_ASM && ksplit == 1 && !WIDE && WM == 4 && WN == 2 &&
+      (int64_t)(PAIRS ? M / 2 : M) * N * 8 < (1LL << 32) && (int64_t)G * nbs * 8192 < (1LL << 32))
+    return gemm_launch_asm<PAIRS>(reinterpret_cast<const int8_t*>(x), wp, mp, t, colterm, M, N, K, st);
   const int use_atomic = ksplit > 1;
   if (use_atomic && !zeroed) {
     int e = zero_bytes(t, (int64_t)(PAIRS ? M / 2 : M) * N * 8, st);

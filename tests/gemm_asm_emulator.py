@@ -1,0 +1,477 @@
+"""CPU emulator of the prefill GEMM's generated main loop (exact-llm_amd/csrc/gen_gemm_asm.py): test infrastructure.
+
+Runs the generated instruction stream of k_gemm_asm (gemm.hip) for every 256 x 128 tile of a small GEMM: the 8 waves
+of a block in program order between barriers, the block's LDS, the global -> LDS copies and the LDS reads as
+asynchronous operations that complete only at the waits that cover them. Raises Race when
+  * a VGPR is read or written while an LDS read or a load into it is outstanding (a missing or too weak wait),
+  * an LDS read overlaps a copy that has not completed (a missing copy wait or barrier),
+  * a copy targets LDS that another wave still reads (a barrier in the wrong place),
+  * an access leaves its buffer or the LDS allocation;
+and returns the int64 totals, which the tests compare with an int64 matmul of the same operands. The per-lane and
+per-wave inputs are computed as k_gemm_asm computes them (inputs_for). The instruction semantics are those of the
+gfx950 ISA for the few instructions the generator emits (v_mfma_i32_16x16x64_i8 operand layout: lane l holds row / column
+l % 16 and k 16 (l / 16) .. + 15 of A / B, and C rows 4 (l / 16) + v of column l % 16).
+"""
+import re
+import sys
+
+import numpy as np
+
+sys.path.insert(0, __import__("os").path.join(__import__("os").path.dirname(__import__("os").path.dirname(__import__("os").path.abspath(__file__))), "exact-llm_amd", "csrc"))
+import gen_gemm_asm as G  # noqa: E402
+
+LDS_SIZE = 160 * 1024
+CTOFF_REG = 254
+
+
+class Race(Exception):
+    pass
+
+
+def i32(x):
+    return np.asarray(x, dtype=np.int64).astype(np.uint32).view(np.int32)
+
+
+class Block:
+    def __init__(self, lines, mem, inputs_per_wave, M_rows, pairs):
+        self.lines = lines
+        self.labels = {}
+        for k, ln in enumerate(lines):
+            if ln.endswith(":"):
+                self.labels[ln[:-1]] = k
+        self.mem = mem            # name -> np.uint8 array (A, B, M, T, Ct)
+        self.lds = np.zeros(LDS_SIZE, np.uint8)
+        self.pending_dma = []     # (wave, lds_lo, lds_hi) not yet completed
+        self.waves = [Wave(w, self, inputs_per_wave[w]) for w in range(8)]
+
+    def lds_pending_read_overlap(self, lo, hi):
+        for w in self.waves:
+            for op in w.lgkm:
+                if op[2] is not None and op[2][0] < hi and lo < op[2][1]:
+                    raise Race(f"DMA into [{lo},{hi}) while wave {w.id} has an outstanding LDS read of {op[2]}")
+
+    def run(self):
+        while True:
+            states = []
+            for w in self.waves:
+                st = w.run_until_barrier()
+                states.append(st)
+            if all(s == "end" for s in states):
+                break
+            if any(s == "end" for s in states):
+                raise Race("some waves ended while others wait at a barrier")
+        for w in self.waves:
+            if w.lgkm or w.vm:
+                raise Race(f"wave {w.id} ended with outstanding ops")
+
+
+class Wave:
+    def __init__(self, wid, blk, inputs):
+        self.id = wid
+        self.blk = blk
+        self.v = np.zeros((256, 64), np.uint32)
+        self.s = np.zeros(110, np.uint32)
+        self.exec = np.ones(64, bool)
+        self.vcc = np.zeros(64, bool)
+        self.scc = 0
+        self.m0 = 0
+        self.pc = 0
+        self.inputs = inputs
+        self.lgkm = []     # [regs set, data(list of (reg, values)), lds range]
+        self.vm = []       # [kind, payload]
+        self.pending = {}  # vgpr -> count of outstanding writers
+        for name, (reg, val) in inputs["vpin"].items():
+            self.v[reg] = np.asarray(val, np.int64).astype(np.uint32)
+
+    # ---- operands
+    def sval(self, tok):
+        tok = tok.strip()
+        if tok.startswith("%["):
+            val = self.inputs["s"][tok[2:-1]]
+            return np.uint32(np.int64(val) & 0xFFFFFFFF)
+        if tok == "m0":
+            return np.uint32(self.m0)
+        if tok.startswith("s"):
+            return self.s[int(tok[1:])]
+        v = int(tok, 0)
+        return np.uint32(v & 0xFFFFFFFF)
+
+    def vregs(self, tok):
+        tok = tok.strip()
+        m = re.match(r"v\[(\d+):(\d+)\]", tok)
+        if m:
+            return list(range(int(m.group(1)), int(m.group(2)) + 1))
+        m = re.match(r"v(\d+)$", tok)
+        if m:
+            return [int(m.group(1))]
+        raise ValueError(tok)
+
+    def sregs(self, tok):
+        m = re.match(r"s\[(\d+):(\d+)\]", tok.strip())
+        return list(range(int(m.group(1)), int(m.group(2)) + 1))
+
+    def rd(self, regs):
+        for r in regs:
+            if self.pending.get(r, 0):
+                raise Race(f"wave {self.id} pc {self.pc} ({self.blk.lines[self.pc]}): v{r} read while a load into it is outstanding")
+        return self.v[regs]
+
+    def wr(self, regs, vals, mask=None):
+        for r in regs:
+            if self.pending.get(r, 0):
+                raise Race(f"wave {self.id} pc {self.pc}: v{r} written while a load into it is outstanding")
+        m = self.exec if mask is None else mask
+        for k, r in enumerate(regs):
+            self.v[r] = np.where(m, vals[k], self.v[r])
+
+    def vsrc(self, tok):
+        tok = tok.strip()
+        if tok.startswith("v"):
+            return self.rd(self.vregs(tok))[0].astype(np.int64)
+        if tok.startswith("%["):
+            name = tok[2:-1]
+            if name in self.inputs["s"]:
+                return np.full(64, np.int64(self.inputs["s"][name]) & 0xFFFFFFFF, np.int64)
+            raise ValueError(tok)
+        if tok.startswith("s"):
+            return np.full(64, int(self.s[int(tok[1:])]), np.int64)
+        return np.full(64, int(tok, 0) & 0xFFFFFFFF, np.int64)
+
+    # ---- async completion
+    def complete_lgkm(self, keep):
+        while len(self.lgkm) > keep:
+            regs, data, rng = self.lgkm.pop(0)
+            for r, vals in data:
+                self.pending[r] -= 1
+                self.v[r] = vals
+
+    def complete_vm(self, keep):
+        while len(self.vm) > keep:
+            kind, payload = self.vm.pop(0)
+            if kind == "dma":
+                lo, hi, addrs, data = payload
+                self.blk.pending_dma.remove((self.id, lo, hi))
+                self.blk.lds_pending_read_overlap(lo, hi)
+                for lane in range(64):
+                    a = addrs[lane]
+                    self.blk.lds[a:a + len(data[lane])] = data[lane]
+            elif kind == "load":
+                for r, vals in payload:
+                    self.pending[r] -= 1
+                    self.v[r] = vals
+
+    def run_until_barrier(self):
+        lines = self.blk.lines
+        while True:
+            if self.pc >= len(lines):
+                return "end"
+            ln = lines[self.pc]
+            if ln.endswith(":"):
+                self.pc += 1
+                continue
+            op, _, rest = ln.partition(" ")
+            args = [a.strip() for a in re.split(r",(?![^\[]*\])", rest)] if rest else []
+            jump = None
+            if op == "s_barrier":
+                self.pc += 1
+                return "barrier"
+            elif op == "s_nop":
+                pass
+            elif op == "s_waitcnt":
+                mv = re.search(r"vmcnt\((\d+)\)", rest)
+                ml = re.search(r"lgkmcnt\((\d+)\)", rest)
+                if mv:
+                    self.complete_vm(int(mv.group(1)))
+                if ml:
+                    self.complete_lgkm(int(ml.group(1)))
+            elif op in ("s_add_u32", "s_sub_u32", "s_mul_i32", "s_mov_b32"):
+                if op == "s_mov_b32":
+                    val = self.sval(args[1])
+                else:
+                    a, b = int(self.sval(args[1])), int(self.sval(args[2]))
+                    val = {"s_add_u32": a + b, "s_sub_u32": a - b, "s_mul_i32": a * b}[op] & 0xFFFFFFFF
+                    if op == "s_sub_u32":
+                        self.scc = 1 if a < b else 0
+                    if op == "s_add_u32":
+                        self.scc = 1 if a + b > 0xFFFFFFFF else 0
+                if args[0] == "m0":
+                    self.m0 = int(val)
+                else:
+                    self.s[int(args[0][1:])] = np.uint32(val)
+            elif op.startswith("s_cmp_"):
+                a, b = int(self.sval(args[0])), int(self.sval(args[1]))
+                kind = op[6:]
+                self.scc = int({"eq_u32": a == b, "lg_u32": a != b, "lt_u32": a < b, "le_u32": a <= b,
+                                "ge_u32": a >= b, "gt_u32": a > b}[kind])
+            elif op == "s_cbranch_scc0":
+                if self.scc == 0:
+                    jump = args[0]
+            elif op == "s_cbranch_scc1":
+                if self.scc == 1:
+                    jump = args[0]
+            elif op == "s_branch":
+                jump = args[0]
+            elif op == "s_and_b64" and args[0] == "exec":
+                a = self.sregs(args[1]); b = self.sregs(args[2])
+                m = (int(self.s[a[0]]) | (int(self.s[a[1]]) << 32)) & (int(self.s[b[0]]) | (int(self.s[b[1]]) << 32))
+                self.exec = np.array([(m >> l) & 1 for l in range(64)], bool)
+            elif op == "s_mov_b64" and args[0] == "exec":
+                self.exec = np.ones(64, bool)
+            elif op == "v_mov_b64":
+                regs = self.vregs(args[0])
+                self.wr(regs, [np.zeros(64, np.uint32)] * 2)
+            elif op == "v_mov_b32":
+                self.wr(self.vregs(args[0]), [self.vsrc(args[1]).astype(np.uint32)])
+            elif op == "v_and_b32":
+                self.wr(self.vregs(args[0]), [(self.vsrc(args[1]) & self.vsrc(args[2])).astype(np.uint32)])
+            elif op == "v_lshrrev_b32":
+                self.wr(self.vregs(args[0]), [((self.vsrc(args[2]) & 0xFFFFFFFF) >> self.vsrc(args[1])).astype(np.uint32)])
+            elif op == "v_add_u32":
+                self.wr(self.vregs(args[0]), [((self.vsrc(args[1]) + self.vsrc(args[2])) & 0xFFFFFFFF).astype(np.uint32)])
+            elif op == "v_lshl_add_u32":
+                r = ((self.vsrc(args[1]) << self.vsrc(args[2])) + self.vsrc(args[3])) & 0xFFFFFFFF
+                self.wr(self.vregs(args[0]), [r.astype(np.uint32)])
+            elif op == "v_mad_i64_i32":
+                d = self.vregs(args[0])
+                a = i32(self.vsrc(args[2])).astype(np.int64)
+                b = i32(self.vsrc(args[3])).astype(np.int64)
+                c = self.rd(self.vregs(args[4]))
+                c64 = (c[0].astype(np.uint64) | (c[1].astype(np.uint64) << np.uint64(32))).view(np.int64)
+                r = (c64 + a * b).view(np.uint64)
+                self.wr(d, [(r & np.uint64(0xFFFFFFFF)).astype(np.uint32), (r >> np.uint64(32)).astype(np.uint32)])
+            elif op == "v_lshlrev_b64":
+                d = self.vregs(args[0])
+                c = self.rd(self.vregs(args[2]))
+                c64 = c[0].astype(np.uint64) | (c[1].astype(np.uint64) << np.uint64(32))
+                r = c64 << np.uint64(int(args[1]))
+                self.wr(d, [(r & np.uint64(0xFFFFFFFF)).astype(np.uint32), (r >> np.uint64(32)).astype(np.uint32)])
+            elif op == "v_add_co_u32":
+                a, b = self.vsrc(args[2]), self.vsrc(args[3])
+                r = a + b
+                self.vcc = r > 0xFFFFFFFF
+                self.wr(self.vregs(args[0]), [(r & 0xFFFFFFFF).astype(np.uint32)])
+            elif op == "v_addc_co_u32":
+                a, b = self.vsrc(args[2]), self.vsrc(args[3])
+                r = a + b + self.vcc.astype(np.int64)
+                self.vcc = r > 0xFFFFFFFF
+                self.wr(self.vregs(args[0]), [(r & 0xFFFFFFFF).astype(np.uint32)])
+            elif op == "v_cmp_gt_i32":
+                a = i32(self.vsrc(args[1])).astype(np.int64)
+                b = i32(self.vsrc(args[2])).astype(np.int64)
+                res = (a > b) & self.exec
+                m = 0
+                for l in range(64):
+                    if res[l]:
+                        m |= 1 << l
+                d = self.sregs(args[0])
+                self.s[d[0]] = m & 0xFFFFFFFF
+                self.s[d[1]] = m >> 32
+            elif op == "v_mfma_i32_16x16x64_i8":
+                d = self.vregs(args[0])
+                A = self.rd(self.vregs(args[1])).T.copy().view(np.int8).reshape(64, 16)   # lane -> 16 bytes
+                B = self.rd(self.vregs(args[2])).T.copy().view(np.int8).reshape(64, 16)
+                Am = np.zeros((16, 64), np.int64)
+                Bm = np.zeros((64, 16), np.int64)
+                for l in range(64):
+                    Am[l % 16, 16 * (l // 16):16 * (l // 16) + 16] = A[l]
+                    Bm[16 * (l // 16):16 * (l // 16) + 16, l % 16] = B[l]
+                C = Am @ Bm
+                if args[3] != "0":
+                    cin = self.rd(self.vregs(args[3])).view(np.int32).astype(np.int64)   # (4, 64)
+                else:
+                    cin = np.zeros((4, 64), np.int64)
+                out = np.zeros((4, 64), np.int64)
+                for l in range(64):
+                    for vv in range(4):
+                        out[vv, l] = C[4 * (l // 16) + vv, l % 16]
+                out = (out + cin)
+                self.wr(d, [i32(out[vv]).view(np.uint32) for vv in range(4)])
+            elif op in ("ds_read_b128", "ds_read_b64"):
+                d = self.vregs(args[0])
+                addr = self.rd(self.vregs(args[1].split()[0]))[0].astype(np.int64)
+                off = int(re.search(r"offset:(\d+)", rest).group(1))
+                nb = 16 if op == "ds_read_b128" else 8
+                lo, hi = int((addr + off).min()), int((addr + off).max()) + nb
+                if hi > LDS_SIZE or lo < 0 or hi > G.LDS_BYTES:
+                    raise Race(f"LDS read out of range {lo} {hi}")
+                for (w, dlo, dhi) in self.blk.pending_dma:
+                    if dlo < hi and lo < dhi:
+                        raise Race(f"wave {self.id} pc {self.pc}: LDS read [{lo},{hi}) overlaps incomplete DMA of wave {w} [{dlo},{dhi})")
+                data = []
+                raw = np.stack([self.blk.lds[a + off:a + off + nb] for a in addr])   # (64, nb)
+                words = raw.view(np.uint32)   # (64, nb/4)
+                for k, r in enumerate(d):
+                    data.append((r, words[:, k].copy()))
+                    self.pending[r] = self.pending.get(r, 0) + 1
+                self.lgkm.append((set(d), data, (lo, hi)))
+            elif op.startswith("buffer_load") and rest.endswith("lds"):
+                voff = self.rd(self.vregs(args[0]))[0].astype(np.int64)
+                buf = self.inputs["rsrc"][args[1][2:-1]]
+                soff = int(self.sval(args[2].split()[0]))
+                nb = 16 if op == "buffer_load_dwordx4" else 4
+                mem = self.blk.mem[buf]
+                data = []
+                for l in range(64):
+                    a = soff + int(voff[l])
+                    if a + nb > len(mem):
+                        if buf == "A":   # bounds-checked resource: reads zero
+                            data.append(np.zeros(nb, np.uint8))
+                            continue
+                        raise Race(f"wave {self.id} pc {self.pc}: {buf} read out of range {a}")
+                    data.append(mem[a:a + nb].copy())
+                addrs = [self.m0 + nb * l for l in range(64)]
+                lo, hi = self.m0, self.m0 + 64 * nb
+                if hi > G.LDS_BYTES:
+                    raise Race(f"DMA out of range {lo} {hi}")
+                self.blk.lds_pending_read_overlap(lo, hi)
+                self.blk.pending_dma.append((self.id, lo, hi))
+                self.vm.append(("dma", (lo, hi, addrs, data)))
+            elif op == "buffer_load_dwordx4":
+                d = self.vregs(args[0])
+                voff = self.rd(self.vregs(args[1]))[0].astype(np.int64)
+                buf = self.inputs["rsrc"][args[2][2:-1]]
+                mo = re.search(r"offset:(\d+)", rest)
+                off = int(mo.group(1)) if mo else 0
+                mem = self.blk.mem[buf]
+                raw = np.stack([mem[int(a) + off:int(a) + off + 16] for a in voff]).view(np.uint32)
+                payload = []
+                for k, r in enumerate(d):
+                    payload.append((r, raw[:, k].copy()))
+                    self.pending[r] = self.pending.get(r, 0) + 1
+                self.vm.append(("load", payload))
+            elif op.startswith("buffer_store"):
+                regs = self.vregs(args[0])
+                vals = self.rd(regs)
+                voff = self.rd(self.vregs(args[1]))[0].astype(np.int64)
+                buf = self.inputs["rsrc"][args[2][2:-1]]
+                soff = int(self.sval(args[3].split()[0]))
+                mo = re.search(r"offset:(\d+)", rest)
+                off = int(mo.group(1)) if mo else 0
+                mem = self.blk.mem[buf]
+                nb = 4 * len(regs)
+                for l in range(64):
+                    if not self.exec[l]:
+                        continue
+                    a = soff + int(voff[l]) + off
+                    if a < 0 or a + nb > len(mem):
+                        raise Race(f"store out of range lane {l} addr {a}")
+                    mem[a:a + nb] = vals[:, l].astype(np.uint32).view(np.uint8)
+            else:
+                raise NotImplementedError(ln)
+            if jump is not None:
+                self.pc = self.blk.labels[jump]
+            else:
+                self.pc += 1
+
+
+def pack(W, M16, N, K):
+    """packed layout: tile T = g nbs + nb, wp[(T 8 + j) 1024 + l 16 + b] = W[nb 64 + l][g 128 + j 16 + b]"""
+    Gn, nbs = K // 128, (N + 63) // 64
+    Wp = np.zeros((Gn * nbs * 64 * 128,), np.int8)
+    Mp = np.zeros((Gn * nbs * 64,), np.int16)
+    for g in range(Gn):
+        for nb in range(nbs):
+            T = g * nbs + nb
+            for l in range(64):
+                n = nb * 64 + l
+                if n >= N:
+                    continue
+                for j in range(8):
+                    Wp[(T * 8 + j) * 1024 + l * 16:(T * 8 + j) * 1024 + l * 16 + 16] = W[n, g * 128 + j * 16:g * 128 + j * 16 + 16]
+                Mp[T * 64 + l] = M16[g, n]
+    return Wp, Mp
+
+
+def inputs_for(bm, bn, wave, Mrows, N, K, pairs):
+    """transcription of k_gemm_asm's set-up (gemm.hip)"""
+    lane = np.arange(64)
+    Gn, nbs = K // 128, (N + 63) // 64
+    wm, wn = wave >> 1, wave & 1
+    j, q = lane & 15, lane >> 4
+    row0, nb0 = bm * 256, bn * 2
+    col0 = nb0 * 64
+    g0, g1 = 0, Gn
+    iters = (g1 - g0 + 5) // 6
+    phase = 6 * iters - (g1 - g0)
+    vad = []
+    for i in range(4):
+        r = (wave * 4 + i) * 8 + (lane >> 3)
+        c = (lane & 7) ^ ((r >> 1) & 7)
+        gr = np.where(row0 + r < Mrows, row0 + r, Mrows - 1)
+        vad.append(gr * K + c * 16)
+    vbdma = (4 * (lane & 15) + (lane >> 4)) * 16
+    bc = []
+    for i in range(2):
+        seg = wave * 2 + i
+        tl = (seg >> 3) if nb0 + (seg >> 3) < nbs else nbs - 1 - nb0
+        bc.append((nb0 + tl) * 8192 + (seg & 7) * 1024)
+    ncol = (nbs - nb0) * 64
+    vmdma = np.where(2 * lane < ncol, 2 * lane, ncol - 2) * 2
+    vard = [None] * 4
+    for kh in range(2):
+        vard[kh] = wm * 8192 + j * 128 + (((kh * 4 + q) ^ ((j >> 1) & 7)) << 4)
+        vard[2 + kh] = vard[kh] + G.A_STAGE[2]
+    vbrd = G.B_BASE + wn * 8192 + q * 1024 + j * 16
+    vmrd = G.M_BASE + wave * 256 + wn * 128 + 8 * j
+    Mout = Mrows // 2 if pairs else Mrows
+    orow = row0 // 2 + wm * 32 + 2 * q if pairs else row0 + wm * 64 + 4 * q
+    ocol = col0 + wn * 64 + 4 * j
+    vst = ((orow * N + ocol) * 8) & 0xFFFFFFFF
+    full = int(((row0 // 2 + 128 <= Mout) if pairs else (row0 + 256 <= Mrows)) and col0 + 128 <= N)
+    s = dict(g0=g0, g1=g1, iters=iters, phase=phase, full=full, asoff=g0 * 128, bg=g0 * nbs * 8192, bc0=bc[0], bc1=bc[1],
+             mg=(g0 * nbs + nb0) * 128, nbsb=nbs * 8192, nbsm=nbs * 128, wavea=wave * 4096,
+             waveb=G.B_BASE + wave * 2048, wavem=G.M_BASE + wave * 256, n8=N * 8, M=Mout, N=N)
+    vpin = {"vadma0": (G.V_ADMA, vad[0]), "vadma1": (G.V_ADMA + 1, vad[1]), "vadma2": (G.V_ADMA + 2, vad[2]),
+            "vadma3": (G.V_ADMA + 3, vad[3]), "vbdma": (G.V_BDMA, vbdma), "vmdma": (G.V_MDMA, vmdma),
+            "vard0": (G.V_ARD, vard[0]), "vard1": (G.V_ARD + 1, vard[1]), "vard2": (G.V_ARD + 2, vard[2]),
+            "vard3": (G.V_ARD + 3, vard[3]), "vbrd": (G.V_BRD, vbrd), "vmrd": (G.V_MRD, vmrd), "vst": (G.V_ST, vst),
+            "vrow": (G.V_ROW, orow), "vcol": (G.V_COL, ocol)}
+    rsrc = {"rA": "A", "rB": "B", "rM": "M", "rT": "T", "rCt": "Ct"}
+    inp = {"s": s, "vpin": vpin, "rsrc": rsrc}
+    if pairs:   # the asm's one compiler-placed VGPR input; emulated in a register the asm does not use
+        inp["vpin"]["ctoff"] = (CTOFF_REG, np.where(ocol < N, ocol, 0) * 8)
+    return inp
+
+
+def emulate(pairs, K, Mrows, N, seed=1, lines=None):
+    """(totals from the emulated kernel, int64 reference) for a seeded GEMM: int8 rows (A8) or the digit rows of
+    int16 rows (pairs), clipped N(0, 40^2) int8 weights, positive int16 group scales"""
+    rng = np.random.default_rng(seed)
+    Gn, nbs = K // 128, (N + 63) // 64
+    A8 = rng.integers(-127, 128, (Mrows, K)).astype(np.int8)
+    if pairs:
+        X = rng.integers(-32767, 32768, (Mrows // 2, K)).astype(np.int64)
+        A8[0::2] = (X >> 8).astype(np.int8)
+        A8[1::2] = ((X & 255) - 128).astype(np.int8)
+    W = np.clip(np.rint(rng.normal(0, 40, (N, K))), -127, 127).astype(np.int8)
+    M16 = rng.integers(1, 32768, (Gn, N)).astype(np.int16)
+    Wp, Mp = pack(W, M16, N, K)
+    Mout = Mrows // 2 if pairs else Mrows
+    Tmem = np.zeros(Mout * N * 8 + 64, np.uint8)
+    ct = np.zeros(N, np.int64)
+    for g in range(Gn):
+        ct += W[:, g * 128:(g + 1) * 128].astype(np.int64).sum(1) * M16[g].astype(np.int64)
+    mem = {"A": A8.reshape(-1).view(np.uint8).copy(), "B": Wp.view(np.uint8).copy(), "M": Mp.view(np.uint8).copy(),
+           "T": Tmem, "Ct": ct.view(np.uint8).copy()}
+    if lines is None:
+        lines = G.kernel_asm(pairs)
+    lines = [ln.replace("%[ctoff]", f"v{CTOFF_REG}") for ln in lines]
+    for bm in range((Mrows + 255) // 256):
+        for bn in range((nbs + 1) // 2):
+            Block(lines, mem, [inputs_for(bm, bn, w, Mrows, N, K, pairs) for w in range(8)], Mrows, pairs).run()
+    T = Tmem[:Mout * N * 8].view(np.int64).reshape(Mout, N)
+    ref = np.zeros((Mout, N), np.int64)
+    for g in range(Gn):
+        Wg = W[:, g * 128:(g + 1) * 128].astype(np.int64).T
+        acc = (X[:, g * 128:(g + 1) * 128] if pairs else A8[:, g * 128:(g + 1) * 128].astype(np.int64)) @ Wg
+        ref += acc * M16[g].astype(np.int64)[None, :]
+    return T, ref
+
+
+if __name__ == "__main__":
+    pairs = len(sys.argv) > 1 and sys.argv[1] == "pairs"
+    K = int(sys.argv[2]) if len(sys.argv) > 2 else 768
+    Mr = int(sys.argv[3]) if len(sys.argv) > 3 else 256
+    N = int(sys.argv[4]) if len(sys.argv) > 4 else 128
+    T, ref = emulate(pairs, K, Mr, N)
+    print("equal" if np.array_equal(T, ref) else "MISMATCH")
