@@ -209,12 +209,51 @@ def model_decode(args, name="qwen2.5-7b", prompt_len=16, B=1):
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / args.steps
     wbytes = active_bytes(cfg)
-    del tm, gd, cache
+    del gd, cache
+    check = fixture_check(tm, name) if B == 1 else None
+    del tm
     torch.cuda.empty_cache()
-    return {"model": name, "batch": B, "tok_s": round(1000.0 * B / ms, 2), "ms_per_step": round(ms, 4), "abits": 15,
-            "weights_GB_per_step": round(wbytes / 1e9, 3), "GBps": round(wbytes / ms / 1e6, 1),
-            "frac_hbm": round(wbytes / ms / 1e6 / HBM_PEAK_GBPS, 4), "prompt": prompt_len,
-            "prefill_ms_per_sequence": round(prefill_ms, 3), "prefill_eager_ms_per_sequence": round(eager_ms, 3)}
+    res = {"model": name, "batch": B, "tok_s": round(1000.0 * B / ms, 2), "ms_per_step": round(ms, 4), "abits": 15,
+           "weights_GB_per_step": round(wbytes / 1e9, 3), "GBps": round(wbytes / ms / 1e6, 1),
+           "frac_hbm": round(wbytes / ms / 1e6 / HBM_PEAK_GBPS, 4), "prompt": prompt_len,
+           "prefill_ms_per_sequence": round(prefill_ms, 3), "prefill_eager_ms_per_sequence": round(eager_ms, 3)}
+    if check is not None:
+        res["oracle_fixture"] = check
+    return res
+
+
+FIXTURES = {"qwen2.5-7b": "full_c2.json"}   # oracle fixtures of the benchmarked models (the same seed: 11)
+
+
+def fixture_check(tm, name):
+    """Untimed: the benchmarked model (same weights) decodes the fixture's first sequence, prefill then greedy steps in
+    a HIP graph as timed above, and every logits row hash and token is compared with the oracle's
+    (tests/golden/make_full_configs.py)."""
+    import torch
+    from exact_amd.model import GraphDecoder
+    fn = FIXTURES.get(name)
+    path = os.path.join(ROOT, "tests", "golden", fn) if fn else None
+    if not path or not os.path.exists(path):
+        return None
+    import hashlib
+    spec = json.load(open(path))
+    if spec["seed"] != 11 or spec["config"] != name:
+        return None
+    sq = spec["sequences"][0]
+    h = lambda row: hashlib.sha256(row.astype("<i8").tobytes()).hexdigest()[:16]
+    cache = tm.new_cache()
+    row = tm.forward(sq["prompt"], cache, last_only=True, slot=0)[-1].cpu().numpy()
+    ok = h(row) == sq["hashes"][0] and int(row.argmax()) == sq["tokens"][0]
+    gd = GraphDecoder(tm, cache, 1)
+    gd.load([int(row.argmax())])
+    gd.capture()
+    n = min(spec["new_tokens"], tm.Smax - spec["prompt_len"])
+    for i in range(1, n):
+        lg, nid = gd.step()
+        torch.cuda.synchronize()
+        ok = ok and h(lg[0].cpu().numpy()) == sq["hashes"][i] and int(nid[0]) == sq["tokens"][i]
+    del gd, cache
+    return {"fixture": fn, "tokens": n, "equal": bool(ok)}
 
 
 def trace_capture(args, name="qwen2.5-7b", prompt_len=16, steps=32, reps=3):

@@ -748,109 +748,96 @@ __global__ __launch_bounds__(256) void k_gemv_experts_xq(const int64_t* __restri
 
 // The reference's exact::gemv on its own tensors (speed_fair_kaggle.py:686-702): one int16 row x (K,), the
 // row-major int8 weight wT (N, K) and int64 group scales Mg (N, G); out[n] = sum_g (sum_{k in g} x[k] wT[n][k]) Mg[n][g]
-// in int64 (wrapping like the reference's int64 sums). No repacking: lane (row, c) of the MFMA's B operand is
-// 16 consecutive bytes of one weight row, so for sub-tile q and half h a lane loads row nb*64 + 16q + row at
-// k = g*128 + 64h + 16c, and the two halves of a group read each row's 128-byte run in two back-to-back loads.
-// A is the int16 row as digits (hi, lo - 128) in A row 0, with the all-ones row 1 in the lo pass for the colsum.
-struct RowRegs {
-  v4i b[8];
-  v4i xa[4];
-  int64_t m[4];
+// in int64 (wrapping like the reference's int64 sums). No repacking. A wave owns a range of K (4 KiB, or 2 KiB for long
+// rows) and a run of rows; lane l handles the 16-byte chunks l, l + 64, ... of the range, so one load instruction reads
+// 1 KiB of one weight row, and the lanes l / 8 = j of a chunk hold one 128-wide group. The lane's x digits
+// (hi = x >> 8, lo = (x & 255) - 128) stay in registers for all its rows; per chunk three int8 dot products give the
+// lane's part of 256 hi.w + lo.w + 128 sum(w) = x.w (exact_torch.py:101-102), which the lane multiplies by its
+// group's scale (sum_g M_g sum_lanes a = sum_lanes M_g a: the per-group sums need no reduction of their own), and the
+// wave sums the row's int64 partials once. Rows are loaded two ahead of the one being summed. Ranges of one row
+// combine with 64-bit atomics (exact in any order).
+// K ranges of 4 KiB (4 chunks a lane), 2 KiB for rows of 8 KiB and more (7B down, 18944: 19.7 -> 18.6 us a call)
+#define ROWMAJ_LONG_K 8192
+#ifndef ROWMAJ_WAVES
+#define ROWMAJ_WAVES 2048                 // waves to aim for: rows per wave = N x ranges / ROWMAJ_WAVES (1..8)
+#endif
+
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+template <int CH>
+struct RowMajRow {
+  v4i w[CH];
+  int64_t m[CH];
 };
 
-template <bool NT>
-__device__ __forceinline__ void load_rows_group(RowRegs& G_, const int8_t* const (&wr)[4], const int64_t* const (&mr)[4],
-                                                const int16_t* __restrict__ x, int g, int c) {
+template <bool NT, int CH>
+__device__ __forceinline__ void rowmaj_load(RowMajRow<CH>& R_, const int8_t* __restrict__ wT, const int64_t* __restrict__ Mg,
+                                            int n, int K, int G, int kb0, int nck, int lane) {
+  const int8_t* wr = wT + (size_t)n * K + kb0 + 16 * lane;
+  const int64_t* mr = Mg + (size_t)n * G + kb0 / 128 + (lane >> 3);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) G_.m[q] = mr[q][g];
-  const int16_t* xp = x + g * 128 + 16 * c;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    G_.xa[2 * h] = *reinterpret_cast<const v4i*>(xp + 64 * h);
-    G_.xa[2 * h + 1] = *reinterpret_cast<const v4i*>(xp + 64 * h + 8);
-  }
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const v4i* a = reinterpret_cast<const v4i*>(wr[q] + g * 128 + 64 * h);
-      G_.b[4 * h + q] = NT ? __builtin_nontemporal_load(a) : *a;
-    }
-}
-
-__device__ __forceinline__ void compute_rows_group(const RowRegs& G_, int64_t (&acc)[4], int row) {
-  const v4i zero = {0, 0, 0, 0};
-  const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
-  v4i ahi[2], alo[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    split_a16(G_.xa[2 * h], G_.xa[2 * h + 1], ahi[h], alo[h]);
-    if (row != 0) ahi[h] = zero;
-    if (row == 1) alo[h] = ones;
-    else if (row != 0) alo[h] = zero;
-  }
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    v4i chi = zero, clo = zero;
-    chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[0], G_.b[q], chi, 0, 0, 0);
-    chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[1], G_.b[4 + q], chi, 0, 0, 0);
-    clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[0], G_.b[q], clo, 0, 0, 0);
-    clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[1], G_.b[4 + q], clo, 0, 0, 0);
-    // lanes 0..15 hold C row 0 (x) in element 0 and C row 1 (the colsum) in element 1
-    const int a = (chi[0] << 8) + clo[0] + 128 * clo[1];
-    acc[q] += (int64_t)a * G_.m[q];
-  }
-}
-
-template <bool NT>
-__global__ __launch_bounds__(256) void k_gemv_rows(const int16_t* __restrict__ x, const int8_t* __restrict__ wT,
-                                                   const int64_t* __restrict__ Mg, int64_t* __restrict__ out, int N, int K,
-                                                   int G, int nsplit, int out_mode) {
-  const int lane = threadIdx.x & 63;
-  const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int nbs = (N + 63) >> 6;
-  if (task >= nbs * nsplit) return;
-  const int nb = task / nsplit, sp = task - nb * nsplit;
-  const int g0 = (int)(((int64_t)sp * G) / nsplit);
-  const int g1 = (int)(((int64_t)(sp + 1) * G) / nsplit);
-  const int row = lane & 15, c = lane >> 4;
-  const int8_t* wr[4];
-  const int64_t* mr[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    int n = nb * 64 + 16 * q + row;
-    n = n < N ? n : N - 1;   // rows past N load the last row; their results are not stored
-    wr[q] = wT + (size_t)n * K + 16 * c;
-    mr[q] = Mg + (size_t)n * G;
-  }
-  int64_t acc[4] = {0, 0, 0, 0};
-  if (g0 < g1) {
-    RowRegs ra, rb;
-    load_rows_group<NT>(ra, wr, mr, x, g0, c);
-    int g = g0;
-    for (; g + 2 < g1; g += 2) {
-      load_rows_group<NT>(rb, wr, mr, x, g + 1, c);
-      compute_rows_group(ra, acc, row);
-      load_rows_group<NT>(ra, wr, mr, x, g + 2, c);
-      compute_rows_group(rb, acc, row);
-    }
-    if (g + 1 < g1) {
-      load_rows_group<NT>(rb, wr, mr, x, g + 1, c);
-      compute_rows_group(ra, acc, row);
-      compute_rows_group(rb, acc, row);
+  for (int c = 0; c < CH; ++c) {
+    if (lane + 64 * c < nck) {
+      const v4i* p = reinterpret_cast<const v4i*>(wr + 1024 * c);
+      R_.w[c] = NT ? __builtin_nontemporal_load(p) : *p;
+      R_.m[c] = mr[8 * c];
     } else {
-      compute_rows_group(ra, acc, row);
+      R_.w[c] = v4i{0, 0, 0, 0};
+      R_.m[c] = 0;
     }
   }
-  if (c != 0) return;
+}
+
+template <bool NT, int CH>
+__global__ __launch_bounds__(256) void k_gemv_rowmajor(const int16_t* __restrict__ x, const int8_t* __restrict__ wT,
+                                                       const int64_t* __restrict__ Mg, int64_t* __restrict__ out, int N,
+                                                       int K, int G, int nranges, int rpw, int out_mode) {
+  const int lane = threadIdx.x & 63;
+  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nrb = (N + rpw - 1) / rpw;
+  if (wid >= nrb * nranges) return;
+  const int rb = wid / nranges, kr = wid - rb * nranges;
+  const int kb0 = kr * CH * 1024;
+  const int nck = ((K - kb0 < CH * 1024 ? K - kb0 : CH * 1024)) / 16;   // 16-byte chunks in the range
+  const int n0 = rb * rpw, n1 = n0 + rpw < N ? n0 + rpw : N;
+  // the lane's x digits, one 16-byte chunk of k per slot
+  v4i xh[CH], xl[CH];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int n = nb * 64 + 16 * q + row;
-    if (n < N) {
+  for (int c = 0; c < CH; ++c) {
+    const v4i zero = {0, 0, 0, 0};
+    if (lane + 64 * c < nck) {
+      const v4i* xp = reinterpret_cast<const v4i*>(x + kb0 + 16 * (lane + 64 * c));
+      split_a16(xp[0], xp[1], xh[c], xl[c]);
+    } else {
+      xh[c] = zero;
+      xl[c] = zero;
+    }
+  }
+  RowMajRow<CH> ra, rb_;
+  rowmaj_load<NT, CH>(ra, wT, Mg, n0, K, G, kb0, nck, lane);
+  if (n0 + 1 < n1) rowmaj_load<NT, CH>(rb_, wT, Mg, n0 + 1, K, G, kb0, nck, lane);
+  for (int n = n0; n < n1; ++n) {
+    int64_t part = 0;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      int sh = 0, sl = 0, s1 = 0;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        sh = dot4(ra.w[c][d], xh[c][d], sh);
+        sl = dot4(ra.w[c][d], xl[c][d], sl);
+        s1 = dot4(ra.w[c][d], 0x01010101, s1);
+      }
+      part += (int64_t)((sh << 8) + sl + (s1 << 7)) * ra.m[c];   // zero past the range (m = 0)
+    }
+    ra = rb_;
+    if (n + 2 < n1) rowmaj_load<NT, CH>(rb_, wT, Mg, n + 2, K, G, kb0, nck, lane);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) part += __shfl_xor(part, o, 64);
+    if (lane == 0) {
       if (out_mode)
-        atomicAdd(reinterpret_cast<unsigned long long*>(out + n), (unsigned long long)acc[q]);
+        atomicAdd(reinterpret_cast<unsigned long long*>(out + n), (unsigned long long)part);
       else
-        out[n] = acc[q];
+        out[n] = part;
     }
   }
 }
@@ -891,13 +878,26 @@ int zero_bytes(void* dst, int64_t nbytes, hipStream_t st) {
 #define GEMV_NT 1
 #endif
 // prefill rows up to this many GEMV row chunks run as chunked GEMVs rather than as the GEMM
-// compute units of one MI355X (8 XCDs x 32)
+// compute units of one MI355X (8 XCDs x 32): the fallback when the device cannot be queried
 #ifndef GEMV_CUS
 #define GEMV_CUS 256
 #endif
+// compute units of the current device (cached per device)
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return GEMV_CUS;
+  if (cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = GEMV_CUS;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
 #ifndef GEMV_CHUNKS_MAX
 #define GEMV_CHUNKS_MAX 1
 #endif
+#define WIDE_A16_CHUNKS_MAX 3
 // Above 4 rows each wave adds 64 x 16 int64 partial totals with atomics, so fewer group splits pay for most shapes.
 // Measured at 8 and 16 rows on the 7B shapes (us, int16 / int8 rows at 16): q|k|v 19.2 -> 11.3 / 17.9 -> 10.1 and
 // o 15.3 -> 11.3 / 13.7 -> 9.7 at 768 waves instead of 3072; gate|up (592 row blocks) 39.9 -> 32.6 at 1536 for int16
@@ -937,7 +937,7 @@ int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, c
   // 37888x3584 24.3 -> 22.8 us, 3584x18944 13.7 -> 13.3 us; smaller weights and the 152064-row head
   // (two rounds) run faster with 256-thread blocks, and int16 activations need more than the 128 VGPRs
   // a 1024-thread block leaves each wave.
-  const bool wide = abits == 7 && (int64_t)N * K >= (32LL << 20) && (tasks + 15) / 16 <= GEMV_CUS;
+  const bool wide = abits == 7 && (int64_t)N * K >= (32LL << 20) && (tasks + 15) / 16 <= device_cus();
   const int bw = wide ? 16 : 4;
   dim3 grid((tasks + bw - 1) / bw), block(64 * bw);
 #define GEMV_GO(AB, VR, BW)                                                                                          \
@@ -1015,16 +1015,23 @@ extern "C" int exact_gemv(const int16_t* x, const int8_t* wT, const int64_t* Mg,
       (reinterpret_cast<uintptr_t>(Mg) & 7) || (reinterpret_cast<uintptr_t>(out) & 7))
     return EXACT_E_UNSUPPORTED;
   const int G = K / 128;
-  const int nsplit = gemv_nsplit(N, G, 1, 15);
-  const int64_t tasks = (int64_t)((N + 63) / 64) * nsplit;
-  if (tasks > (1LL << 30)) return EXACT_E_UNSUPPORTED;
+  const int ch = K >= ROWMAJ_LONG_K ? 2 : 4;
+  const int nranges = (K + ch * 1024 - 1) / (ch * 1024);
+  int64_t rpw = (int64_t)N * nranges / ROWMAJ_WAVES;
+  rpw = rpw < 1 ? 1 : (rpw > 8 ? 8 : rpw);
+  const int64_t waves = (((int64_t)N + rpw - 1) / rpw) * nranges;
+  if (waves > (1LL << 30)) return EXACT_E_UNSUPPORTED;
   hipStream_t st = as_stream(stream);
-  if (nsplit > 1) {
+  if (nranges > 1) {
     int e = zero_bytes(out, (int64_t)N * 8, st);
     if (e) return e;
   }
-  hipLaunchKernelGGL((k_gemv_rows<GEMV_NT != 0>), dim3((unsigned)((tasks + 3) / 4)), dim3(256), 0, st, x, wT, Mg, out, N, K,
-                     G, nsplit, nsplit > 1 ? 1 : 0);
+  if (ch == 2)
+    hipLaunchKernelGGL((k_gemv_rowmajor<GEMV_NT != 0, 2>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, wT, Mg,
+                       out, N, K, G, nranges, (int)rpw, nranges > 1 ? 1 : 0);
+  else
+    hipLaunchKernelGGL((k_gemv_rowmajor<GEMV_NT != 0, 4>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, wT, Mg,
+                       out, N, K, G, nranges, (int)rpw, nranges > 1 ? 1 : 0);
   return launch_status("gemv");
 }
 
@@ -1035,6 +1042,18 @@ extern "C" int exact_gemv(const int16_t* x, const int8_t* wT, const int64_t* Mg,
 #define GEMV_NORM_BW8_K 2048
 #endif
 #define GEMV_NORM_KMAX (256 * 24)
+
+// waves per block of exact_gemv_g128_norm_acc: 8 for rows wider than GEMV_NORM_BW8_K whose group-split tasks fit one
+// round of 8-wave blocks on `cus` compute units (each CU then normalises the row once), else 4
+static int norm_block_waves(int R, int N, int K, int cus) {
+  const int64_t tasks = (int64_t)((N + 63) / 64) * gemv_nsplit(N, K / 128, R, 15);
+  return K > GEMV_NORM_BW8_K && (tasks + 7) / 8 <= cus ? 8 : 4;
+}
+
+extern "C" int exact_gemv_g128_norm_acc_blockwaves(int32_t R, int32_t N, int32_t K, int32_t cus) {
+  if (R <= 0 || N <= 0 || K <= 0 || K % 128) return 0;
+  return norm_block_waves(R, N, K, cus > 0 ? cus : device_cus());
+}
 
 extern "C" int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, const int64_t* res_t, const int32_t* res_s,
                                         const int64_t* g, const int8_t* wp, const int16_t* mp, const int16_t* mh,
@@ -1050,7 +1069,7 @@ extern "C" int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, con
   const size_t lds = (size_t)R * K * 2;
   hipStream_t st = as_stream(stream);
   // rows wider than GEMV_NORM_BW8_K whose tasks fit one round of 8-wave blocks: 8-wave blocks (see the kernel)
-  const bool bw8 = K > GEMV_NORM_BW8_K && (tasks + 7) / 8 <= GEMV_CUS;
+  const bool bw8 = norm_block_waves(R, N, K, device_cus()) == 8;
   const int bw = bw8 ? 8 : 4;
   dim3 grid((unsigned)((tasks + bw - 1) / bw)), block(64 * bw);
   const int ept = (K + 64 * bw - 1) / (64 * bw);
@@ -1135,6 +1154,9 @@ extern "C" int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const in
 #ifndef GEMV_GU_NPB
 #define GEMV_GU_NPB 1
 #endif
+// the slice bit lengths (part) are one per block, and every caller (the down GEMV's qrow, ops.SWIGLU_PART_COLS)
+// reads them as one per 32 gate columns: that holds only with one pair of 32 columns a block
+static_assert(GEMV_GU_NPB == 1, "part holds one slice bit length per 32 gate columns");
 
 extern "C" int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh,
                                       const int32_t* s, const int32_t* silu, int64_t* h, int32_t* part, int64_t* t,
@@ -1206,7 +1228,10 @@ static int gemm_entry(const void* x, int32_t abits, const int8_t* wp, const int1
   int e = check_linear(x, abits, wp, mp, t, R, N, K);
   if (e) return e;
   const int rmax = abits == 15 ? 15 : 16;
-  if (R > GEMV_CHUNKS_MAX * rmax) return gemm_mfma(x, abits, wp, mp, mh, t, R, N, K, as_stream(stream), zeroed);
+  // int16 rows with wide scales have no MFMA kernel behind this entry (the digit-row entry exact_gemm_g128_a16 is
+  // theirs): they keep the GEMV row chunks up to WIDE_A16_CHUNKS_MAX x 15 rows, and above that gemm_mfma refuses them
+  const int chunks_max = (abits == 15 && mh) ? WIDE_A16_CHUNKS_MAX : GEMV_CHUNKS_MAX;
+  if (R > chunks_max * rmax) return gemm_mfma(x, abits, wp, mp, mh, t, R, N, K, as_stream(stream), zeroed);
   // Up to GEMV_CHUNKS_MAX row chunks: one GEMV per chunk streams the weights once per chunk. One chunk beats the
   // GEMM's 128-row tiles (mostly padding at these R); a second weight pass does not (int8-row 7B prefill, ms: 32 tokens
   // as 2 chunks 5.79, on the GEMM 4.82; 48 tokens as 3 chunks 8.23, on the GEMM 5.11).

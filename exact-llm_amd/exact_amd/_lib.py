@@ -31,6 +31,7 @@ SIGNATURES = {
     "exact_gemv_g128_qrow_acc": [P, I64, P, I32, I32, P, P, P, P, P, I32, I32, I32, P, I64, P],
     "exact_gemv_g128_swiglu": [P, P, P, P, P, P, P, P, P, I32, I32, I32, P],
     "exact_gemv_g128_norm_acc": [P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, P],
+    "exact_gemv_g128_norm_acc_blockwaves": [I32, I32, I32, I32],
     "exact_gemv_g128_norm_swiglu": [P, P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, P],
     "exact_requant_group": [P, P, P, P, I32, I32, P],
     "exact_requant_channel": [P, P, P, I32, P, P, I32, I32, P],

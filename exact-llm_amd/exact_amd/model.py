@@ -340,7 +340,7 @@ class TModel:
         # CU, read the row once); the FFN norm stays a launch of its own before the SwiGLU GEMV
         qfuse = (self.QKV_NORM and group and afuse and not nfuse and self.abits == 15 and not c.moe
                  and R <= ops.NORM_FUSE_ROWS and D <= ops.NORM_FUSE_KMAX
-                 and (ops.norm_gemv_one_block_per_cu(self.w.layers[0]["qkv"].N, D, R) or D <= ops.GEMV_NORM_BW8_K))
+                 and (ops.norm_gemv_one_block_per_cu(self.w.layers[0]["qkv"].N, D, R) or D <= self.NORM_FUSE_D))
         # decode rows of dense int16 models whose gate|up GEMV is not the norm-fused one: the SwiGLU runs in the gate|up
         # GEMV's epilogue (no totals, no atomics, one launch fewer)
         sfuse = (xfuse and not nfuse and not c.moe and self.abits == 15 and R <= ops.SWIGLU_GEMV_ROWS and c.I % 64 == 0
@@ -736,10 +736,11 @@ class GraphDecoder:
             self.graph = g
         torch.cuda.synchronize()
 
-    def step(self, feed_argmax=True):
+    def step(self):
         """One decode step: returns (logits (B, V) view, next ids view). The greedy ids land in the step's input
-        ids, so the next step consumes them directly on the device; a caller that chooses other tokens (feed_argmax
-        False, e.g. sampling) loads them with load() before the next step."""
+        ids, so the next step consumes them directly on the device; a caller that chooses other tokens (sampling, say)
+        loads them with load() before the next step. Both views alias the decoder's own buffers: the next step, and
+        for the ids also load(), overwrite them (clone what must outlive that)."""
         if max(self.cache.n[:self.B]) >= self.tm.Smax:
             raise ExactError("cache full")
         b = self.nstep % 2

@@ -169,20 +169,15 @@ NORM_FUSE_ROWS = 2        # rows of one exact_gemv_g128_norm_acc launch
 NORM_FUSE_KMAX = 256 * 24
 
 
-GEMV_DECODE_WAVES, GEMV_CUS, GEMV_NORM_BW8_K = 4096, 256, 2048   # as gemv.hip
-
-
-def norm_gemv_one_block_per_cu(N, K, R=1):
-    """True when exact_gemv_g128_norm_acc runs its 8-wave blocks, one per CU (rows wider than GEMV_NORM_BW8_K whose
-    group-split tasks fit one round): then each CU normalises the row once. With more tasks every one of its 4-wave
-    blocks normalises the row (at 14B's q|k|v, hundreds of blocks of 5120-wide rows: 5.33 against 4.20 ms a decode step).
-    The launch takes at most NORM_FUSE_ROWS rows; its task count follows gemv.hip's split for such rows: ceil(N / 64)
-    row blocks x min(G, ceil(4096 / row blocks)) group ranges."""
-    if K <= GEMV_NORM_BW8_K or R > NORM_FUSE_ROWS:
+def norm_gemv_one_block_per_cu(N, K, R=1, cus=0):
+    """True when exact_gemv_g128_norm_acc runs its 8-wave blocks, one per CU (rows wider than 2048 whose group-split
+    tasks fit one round): then each CU normalises the row once. With more tasks every one of its 4-wave blocks
+    normalises the row (at 14B's q|k|v, hundreds of blocks of 5120-wide rows: 5.33 against 4.20 ms a decode step).
+    The launch takes at most NORM_FUSE_ROWS rows; the split is the library's own (exact_gemv_g128_norm_acc_blockwaves),
+    on `cus` compute units (0: the current device's)."""
+    if R > NORM_FUSE_ROWS:
         return False
-    nbs, G = -(-N // 64), K // 128
-    tasks = nbs * max(1, min(G, -(-GEMV_DECODE_WAVES // nbs)))
-    return -(-tasks // 8) <= GEMV_CUS
+    return _lib.load().exact_gemv_g128_norm_acc_blockwaves(int(R), int(N), int(K), int(cus)) == 8
 
 
 def gemv_norm_acc(x_in, res_t, res_s, g, lin, out, s_out, x_out=None, xq_out=None):

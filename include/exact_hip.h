@@ -96,9 +96,16 @@ int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, const int64_t*
                              const int64_t* g, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,
                              int32_t* s_out, int16_t* xq_out, int32_t R, int32_t N, int32_t K, void* stream);
 
-/* Exact group-128 GEMM for prefill (any R): same output as exact_gemv_g128. Up to 3 x 15 rows (A16) or
- * 3 x 16 rows (A8) run as row chunks of the GEMV kernel, more rows on the MFMA GEMM kernels (wide scales:
- * int8 x only there; int16 x with wide scales takes exact_gemm_g128_a16, else 2 is returned).
+/* Waves per block that exact_gemv_g128_norm_acc launches for R rows of an N x K linear on cus compute units (cus <= 0:
+ * the current device's): 8 when the rows are wider than 2048 and the group-split tasks fit one round of 8-wave blocks
+ * (each CU then normalises the rows once), else 4; 0 for sizes the launch refuses. A host-side query (no launch), so
+ * a caller choosing between the fused norm and a separate norm launch reads the kernel's own split. No counterpart in
+ * the reference. */
+int exact_gemv_g128_norm_acc_blockwaves(int32_t R, int32_t N, int32_t K, int32_t cus);
+
+/* Exact group-128 GEMM for prefill (any R): same output as exact_gemv_g128. Up to 15 rows (A16) or 16 rows (A8)
+ * run on the GEMV kernel, more rows on the MFMA GEMM kernels. Wide scales (mh != NULL): int8 rows at any R; int16
+ * rows run as GEMV row chunks of 15 up to 45 rows, and above that 2 is returned (exact_gemm_g128_a16 covers them).
  * Replaces TLinG's R > 1 fp64 bmm branch (speed_fair_kaggle.py:739-742) and TLin._acc's
  * torch._int_mm A16/A8 passes (exact_torch.py:94-119). */
 int exact_gemm_g128(const void* x, int32_t abits, const int8_t* wp, const int16_t* mp, const int16_t* mh, int64_t* t,

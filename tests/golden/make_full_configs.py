@@ -8,6 +8,7 @@ tests/golden/full_<name>.json: the prompts, the greedy tokens, and the conforman
 int64 row, first 16 hex digits; exact_llm.py:22) of every logits row that produced a token.
 
   c1  Qwen2.5-0.5B shape, 16-token prompt, 64 greedy tokens, bs1
+  c2  Qwen2.5-7B shape (the decode benchmark's model: the same seed), 16-token prompt, 24 greedy tokens, bs1 and bs2
   c4  Qwen2.5-14B shape, 128-token prompt, 48 greedy tokens, bs1 and bs8 (8 prompts)
   c5  Qwen1.5-MoE-A2.7B shape, 256-token prompt, 32 greedy tokens, bs1
 """
@@ -28,6 +29,7 @@ from exact_amd import synth  # noqa: E402
 
 RUNS = {
     "c1": dict(cfg="qwen2.5-0.5b", seed=101, prompt=16, new=64, batch=1),
+    "c2": dict(cfg="qwen2.5-7b", seed=11, prompt=16, new=24, batch=2),
     "c4": dict(cfg="qwen2.5-14b", seed=104, prompt=128, new=48, batch=8),
     "c5": dict(cfg="qwen1.5-moe-a2.7b", seed=105, prompt=256, new=32, batch=1),
 }

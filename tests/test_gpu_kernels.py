@@ -237,10 +237,25 @@ def test_wide_group_scales(abits, R, N, K, mbits):
     assert np.array_equal(host(t), oracle_t(xq, w, M)), (R, abits)
 
 
+@pytest.mark.parametrize("R", [15, 16, 45])
+def test_wide_scales_a16_generic_gemm_entry_row_chunks(R):
+    """The generic GEMM entry (the one INTEGRATION.md binds for TLinG's R > 1 branch) with int16 rows and wide scales
+    runs GEMV row chunks of 15 up to 3 x 15 rows and equals the int64 sum."""
+    K, N = 1408, 500
+    w = rng.integers(-127, 128, (K, N)).astype(np.int8)
+    M = rng.integers(1 << 15, 1 << 21, (K // 128, N))
+    lin = ops.pack_group_linear(w, M, DEV)
+    assert lin.mh is not None
+    xq = rng.integers(-32767, 32768, (R, K))
+    t = torch.zeros((R, N), dtype=I64, device=DEV)
+    ops._linear("exact_gemm_g128", dev(xq, I16), 15, lin, t)
+    assert np.array_equal(host(t), oracle_t(xq, w, M))
+
+
 def test_wide_scales_a16_generic_gemm_entry_is_refused():
-    """The generic GEMM entry with int16 rows above the GEMV sizes runs the legacy A16 kernel, which takes int16 scales
-    only: with a high plane it returns 'unsupported' (the digit-row entry, which ops uses, covers it)."""
-    K, N, R = 256, 64, 60
+    """The generic GEMM entry with int16 rows above 3 x 15 has no wide-scale kernel: it returns 'unsupported' (the
+    digit-row entry, which ops uses, covers it)."""
+    K, N, R = 256, 64, 46
     lin = ops.pack_group_linear(rng.integers(-127, 128, (K, N)).astype(np.int8), rng.integers(1 << 15, 1 << 20, (2, N)), DEV)
     x = dev(rng.integers(-100, 100, (R, K)), I16)
     with pytest.raises(ops.ExactError, match="unsupported"):
