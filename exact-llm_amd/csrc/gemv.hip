@@ -38,6 +38,10 @@ __device__ __forceinline__ void split_a16(v4i p0, v4i p1, v4i& hi, v4i& lo) {
   lo[3] = __builtin_amdgcn_perm(p1[3], p1[2], 0x06040200u) ^ 0x80808080;
 }
 
+#ifndef GEMV_A8_SELECT
+#define GEMV_A8_SELECT 0
+#endif
+
 // Per-group operands of one wave: the 8 KiB weight tile (8 x 16 B per lane), the A-operand bytes of
 // the x rows (A8: 2 x 16 B, A16: 4 x 16 B raw int16) and the four int16 scales of the lane's columns.
 struct GroupRegs {
@@ -122,7 +126,11 @@ __device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc
         alo[h] = (!CT && row == R) ? ones : zero;   // all-ones row: colsum(W) in the lo pass
       }
     } else {
+#if GEMV_A8_SELECT
       ahi[h] = valid ? G_.xa[h] : zero;
+#else
+      ahi[h] = G_.xa[h];   // A row i feeds only C row i: the rows of unused lanes are never stored
+#endif
       alo[h] = zero;
     }
   }
