@@ -15,7 +15,8 @@
 // (cheaper than a round trip of int64 scores through HBM): max, then sum of exp, then p and p.v. The scores
 // are computed transposed (keys x queries), so each lane holds one query row and 16 keys of a tile: the
 // layout the p.v product takes p in, without a transpose. The V digits are stored with the keys of every
-// 32-key group permuted to match (kdig/vdig below). Head dimension 128.
+// 32-key group permuted to match (kdig/vdig below). Head dimension HD = 64 or 128 (a template parameter): the q.k
+// products run over HD / 32 blocks of 32 dimensions and the p.v consumers take 32 dimensions each.
 #include "exact_common.h"
 #include "abi_util.h"
 
@@ -25,7 +26,6 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 namespace exact {
 
 
-#define AP_HD 128
 #define AP_TN 4608   // exp entries in LDS; the fast path needs the table to be zero from entry AP_TN - 2 on
 
 // int16 -> (hi, lo - 128) int8 digits of 16 values held in two 16-byte chunks
@@ -55,9 +55,12 @@ __device__ __forceinline__ int sum16(v4i p0, v4i p1) {
 // base-256 digit b of v[32 t + 8 (m / 4) + 4 half + m % 4][d] (zero from nkeys on): the 16 keys in the order in
 // which a transposed 32x32 MFMA result holds them for lane half `half`, and consecutive dimensions 16 bytes apart
 // (so a wave's loads are contiguous). vpart[kh * ntile + t] = max bit length of |v| over the tile's keys.
+// 2 HD threads work (the rest of the block only joins the reduction).
+template <int HD>
 __device__ __forceinline__ void vdigits_tile(const int64_t* __restrict__ v, int sl, int KV, int Smax, int nkeys, int kh, int t,
                                              int ntile, int8_t* __restrict__ vdig, int32_t* __restrict__ vpart, int* red) {
-  const int d = threadIdx.x & (AP_HD - 1), half = threadIdx.x >> 7;
+  const int d = threadIdx.x & (HD - 1), half = (threadIdx.x / HD) & 1;
+  const bool act = threadIdx.x < 2 * HD;
   const int64_t cbase = ((int64_t)sl * KV + kh) * Smax;
   v4i pk[8];
 #pragma unroll
@@ -66,7 +69,7 @@ __device__ __forceinline__ void vdigits_tile(const int64_t* __restrict__ v, int 
 #pragma unroll
   for (int m = 0; m < 16; ++m) {
     const int key = 32 * t + 8 * (m >> 2) + 4 * half + (m & 3);
-    int64_t x = key < nkeys ? v[(cbase + key) * AP_HD + d] : 0;
+    int64_t x = act && key < nkeys ? v[(cbase + key) * HD + d] : 0;
     const int b0 = bitlen64(abs64(x));
     bl = b0 > bl ? b0 : bl;
 #pragma unroll
@@ -76,30 +79,35 @@ __device__ __forceinline__ void vdigits_tile(const int64_t* __restrict__ v, int 
       x = (x - dg) >> 8;
     }
   }
+  if (act)
 #pragma unroll
-  for (int b = 0; b < 8; ++b)
-    *reinterpret_cast<v4i*>(vdig + (((((int64_t)kh * 8 + b) * ntile + t) * 2 + half) * AP_HD + d) * 16) = pk[b];
+    for (int b = 0; b < 8; ++b)
+      *reinterpret_cast<v4i*>(vdig + (((((int64_t)kh * 8 + b) * ntile + t) * 2 + half) * HD + d) * 16) = pk[b];
   bl = block_max_i32(bl, red);
   if (threadIdx.x == 0) vpart[(int64_t)kh * ntile + t] = bl;
 }
 
-// Digits of every cached k of the sequence for the q.k product: kdig[(((kh * 2 + p) * 4 + kb) * kpad + j) * 32 + c]
+// Digits of every cached k of the sequence for the q.k product: kdig[(((kh * 2 + p) * HD / 32 + kb) * kpad + j) * 32 + c]
 // = digit p (0: hi, 1: lo - 128) of k[j][32 kb + c]; ck[kh * kpad + j] = 128 sum_d k[j][d] - 16384 hd and
 // skk[kh * kpad + j] = sk[j] (zeros from nkeys on); kpart[kh * ntile + t] = max sk over the tile's keys. The KV
 // head 0 blocks also scan the exp table T, block t entries 256 t + [0, 256) (+ 8 kpad i): tpart[t] = 2^30 if one
 // of them breaks the form the fast path takes (zero from entry AP_TN - 2 on, T[0] > 0, entries in [0, 2^24] with
-// steps T[i] - T[i + 1] in [0, 2^24)), else 1 + the last nonzero index among them (0 if none). 8 threads per key.
+// steps T[i] - T[i + 1] in [0, 2^24)), else 1 + the last nonzero index among them (0 if none). HD / 16 threads per
+// key (16 dimensions each); the other threads of the block join the reductions and the table scan.
 // Per-block results instead of global atomics: same-line atomics from every block serialise (~20 us here).
+template <int HD>
 __device__ __forceinline__ void kdigits_tile(const int16_t* __restrict__ kq, const int32_t* __restrict__ sk, int sl, int KV,
                                              int Smax, int nkeys, int kpad, int kh, int t, int8_t* __restrict__ kdig,
                                              int32_t* __restrict__ ck, int32_t* __restrict__ skk, int32_t* __restrict__ kpart,
                                              const int32_t* __restrict__ T, int32_t* __restrict__ tpart, int* red) {
+  constexpr int TPK = HD / 16, KB = HD / 32;       // threads per key, 32-dimension blocks
   const int tid = threadIdx.x;
-  const int j = 32 * t + (tid >> 3), c = tid & 7;   // c: 16 dimensions 16 c .. 16 c + 15
+  const bool act = tid < 32 * TPK;
+  const int j = 32 * t + tid / TPK, c = tid % TPK;   // c: 16 dimensions 16 c .. 16 c + 15
   const int64_t row = ((int64_t)sl * KV + kh) * Smax + j;
   v4i p0 = {}, p1 = {};
-  if (j < nkeys) {
-    const v4i* src = reinterpret_cast<const v4i*>(kq + row * AP_HD + 16 * c);
+  if (act && j < nkeys) {
+    const v4i* src = reinterpret_cast<const v4i*>(kq + row * HD + 16 * c);
     p0 = src[0];
     p1 = src[1];
   }
@@ -107,16 +115,17 @@ __device__ __forceinline__ void kdigits_tile(const int16_t* __restrict__ kq, con
   split_digits(p0, p1, hi, lo);
   if (j >= nkeys) lo = v4i{};
   const int kb = c >> 1, half = c & 1;
-  *reinterpret_cast<v4i*>(kdig + ((((int64_t)kh * 2 + 0) * 4 + kb) * kpad + j) * 32 + 16 * half) = hi;
-  *reinterpret_cast<v4i*>(kdig + ((((int64_t)kh * 2 + 1) * 4 + kb) * kpad + j) * 32 + 16 * half) = lo;
+  if (act) {
+    *reinterpret_cast<v4i*>(kdig + ((((int64_t)kh * 2 + 0) * KB + kb) * kpad + j) * 32 + 16 * half) = hi;
+    *reinterpret_cast<v4i*>(kdig + ((((int64_t)kh * 2 + 1) * KB + kb) * kpad + j) * 32 + 16 * half) = lo;
+  }
   int sum = sum16(p0, p1);
-  sum += __shfl_xor(sum, 1, 64);
-  sum += __shfl_xor(sum, 2, 64);
-  sum += __shfl_xor(sum, 4, 64);
+#pragma unroll
+  for (int o = 1; o < TPK; o <<= 1) sum += __shfl_xor(sum, o, 64);
   int skv = 0;
-  if (c == 0) {
+  if (act && c == 0) {
     skv = j < nkeys ? sk[row] : 0;
-    ck[(int64_t)kh * kpad + j] = j < nkeys ? 128 * sum - 16384 * AP_HD : 0;
+    ck[(int64_t)kh * kpad + j] = j < nkeys ? 128 * sum - 16384 * HD : 0;
     skk[(int64_t)kh * kpad + j] = skv;
   }
   const int ntile = kpad / 32;
@@ -141,6 +150,7 @@ __device__ __forceinline__ void kdigits_tile(const int16_t* __restrict__ kq, con
 
 // grid (kpad / 32, 2 KV), block 256: blocks with y < KV write V digits, the others k digits. part: the per-tile
 // partial results, vpart [KV][kpad / 32], kpart [KV][kpad / 32], tpart [kpad / 32], every entry written here.
+template <int HD>
 __global__ __launch_bounds__(256) void k_attn_digits(const int64_t* __restrict__ v, const int16_t* __restrict__ kq,
                                                      const int32_t* __restrict__ sk, const int32_t* __restrict__ T, int sl, int KV,
                                                      int Smax, int nkeys, int kpad, int8_t* __restrict__ vdig,
@@ -149,9 +159,9 @@ __global__ __launch_bounds__(256) void k_attn_digits(const int64_t* __restrict__
   __shared__ int red[32];   // two reductions of 16 entries each
   const int ntile = kpad / 32;
   if ((int)blockIdx.y < KV)
-    vdigits_tile(v, sl, KV, Smax, nkeys, blockIdx.y, blockIdx.x, ntile, vdig, part, red);
+    vdigits_tile<HD>(v, sl, KV, Smax, nkeys, blockIdx.y, blockIdx.x, ntile, vdig, part, red);
   else
-    kdigits_tile(kq, sk, sl, KV, Smax, nkeys, kpad, blockIdx.y - KV, blockIdx.x, kdig, ck, skk, part + (int64_t)KV * ntile, T,
+    kdigits_tile<HD>(kq, sk, sl, KV, Smax, nkeys, kpad, blockIdx.y - KV, blockIdx.x, kdig, ck, skk, part + (int64_t)KV * ntile, T,
                  part + (int64_t)2 * KV * ntile, red);
 }
 
@@ -178,12 +188,14 @@ struct QK {
   const int32_t* skh;    // sk per key
   BufRes kdr, ckr, skr;  // buffer views of this KV head's k digits, ckh and skh
   const v4i* qd;         // LDS q digits [kb][hi, lo][lane]: B operand, column = query l32, dimensions 32 kb + 16 half + [0, 16)
+  // (kb < HD / 32; the callers pass HD as a template parameter)
   int kpad, l32, half, lane;
 };
 
 // k digits of one 32-key tile: A operand, row = key l32
+template <int HD>
 struct KTile {
-  v4i hi[4], lo[4];
+  v4i hi[HD / 32], lo[HD / 32];
 };
 
 // per-key terms of the 16 keys a lane holds in a tile (keys j0 + 8 g + 4 half + [0, 4))
@@ -199,20 +211,22 @@ __device__ __forceinline__ void load_kcol(const QK& c, int j0, KCol& k) {
   }
 }
 
-__device__ __forceinline__ void load_ktile(const QK& c, int j0, KTile& k) {
+template <int HD>
+__device__ __forceinline__ void load_ktile(const QK& c, int j0, KTile<HD>& k) {
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
+  for (int kb = 0; kb < HD / 32; ++kb) {
     k.hi[kb] = buf_load16(c.kdr, c.l32 * 32 + 16 * c.half, (kb * c.kpad + j0) * 32);
-    k.lo[kb] = buf_load16(c.kdr, c.l32 * 32 + 16 * c.half, ((4 + kb) * c.kpad + j0) * 32);
+    k.lo[kb] = buf_load16(c.kdr, c.l32 * 32 + 16 * c.half, ((HD / 32 + kb) * c.kpad + j0) * 32);
   }
 }
 
-__device__ __forceinline__ void mfma_ktile(const QK& c, const KTile& k, v16i& hh, v16i& xx, v16i& ll) {
+template <int HD>
+__device__ __forceinline__ void mfma_ktile(const QK& c, const KTile<HD>& k, v16i& hh, v16i& xx, v16i& ll) {
   hh = v16i{};
   xx = v16i{};
   ll = v16i{};
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
+  for (int kb = 0; kb < HD / 32; ++kb) {
     const v4i qh = c.qd[(2 * kb) * 64 + c.lane], ql = c.qd[(2 * kb + 1) * 64 + c.lane];
     hh = __builtin_amdgcn_mfma_i32_32x32x32_i8(k.hi[kb], qh, hh, 0, 0, 0);
     xx = __builtin_amdgcn_mfma_i32_32x32x32_i8(k.hi[kb], ql, xx, 0, 0, 0);
@@ -373,8 +387,7 @@ __device__ __forceinline__ void scores_i64(const QK& c, int j0, const v16i& hh, 
   }
 }
 
-#define AP_PROD 4      // the p.v kernel: waves 0..3 produce p digits, waves 4..7 multiply them into V
-#define AP_CONS 4
+#define AP_PROD 4      // the p.v kernel: waves 0..3 produce p digits, the HD / 32 waves after them multiply them into V
 #define AP_SW 4        // waves of the statistics kernel
 
 struct AttnLDS {
@@ -386,16 +399,16 @@ struct AttnLDS {
 };
 
 // Consumer loop of the third pass: iteration s multiplies step s - 1 (the producers fill step s meanwhile). V digit
-// plane b of tile t is at vr + voff + b vplane + 4096 t. NB = 4 holds the V digits of a whole step and refills each
+// plane b of tile t is at vr + voff + b vplane + 32 HD t. NB = 4 holds the V digits of a whole step and refills each
 // tile's registers with the next step's tile once its products are issued; NB = 8 (no registers for that) loads one
 // tile ahead.
-template <int NB>
+template <int HD, int NB>
 __device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile, BufRes vr, int voff, int vplane, int lane,
                                         v16i (&acc)[NB + 2]) {
   auto load_v = [&](int t, v4i (&vb)[NB]) {
     t = t < ntile ? t : ntile - 1;   // stays inside the written keys
 #pragma unroll
-    for (int b = 0; b < NB; ++b) vb[b] = buf_load16(vr, voff, b * vplane + t * (2 * AP_HD * 16));
+    for (int b = 0; b < NB; ++b) vb[b] = buf_load16(vr, voff, b * vplane + t * (2 * HD * 16));
   };
 #pragma unroll
   for (int k = 0; k < NB + 2; ++k) acc[k] = v16i{};
@@ -451,12 +464,12 @@ __device__ __forceinline__ void consume(const AttnLDS& L, int nsteps, int ntile,
 
 // consume, then out = shr(sum_s C_s 256^s, 20) (modulo 2^64, as the reference's int64 p . v) for dimension d
 // of the block's rows, and the rows' bit lengths in rowbits. C layout: lane holds rows 8 (i / 4) + 4 half + i % 4.
-template <int NB>
+template <int HD, int NB>
 __device__ __forceinline__ void consume_store(const AttnLDS& L, int nsteps, int ntile, BufRes vr, int voff, int vplane,
                                               int lane, int64_t* __restrict__ out, int* rowbits, int q0, int R, int H, int h, int d,
                                               int half) {
   v16i acc[NB + 2];
-  consume<NB>(L, nsteps, ntile, vr, voff, vplane, lane, acc);
+  consume<HD, NB>(L, nsteps, ntile, vr, voff, vplane, lane, acc);
   int b[16];   // bit length of |out| of row r(i) at this lane's dimension
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -465,7 +478,7 @@ __device__ __forceinline__ void consume_store(const AttnLDS& L, int nsteps, int 
     for (int k = 0; k < NB + 2; ++k) tot += (uint64_t)shl64((int64_t)acc[k][i], 8 * k);
     const int r = 8 * (i >> 2) + 4 * half + (i & 3);
     const int64_t o = shr64((int64_t)tot, 20);
-    if (q0 + r < R) out[((int64_t)(q0 + r) * H + h) * AP_HD + d] = o;
+    if (q0 + r < R) out[((int64_t)(q0 + r) * H + h) * HD + d] = o;
     b[i] = bitlen64(abs64(o));
   }
   // maxima over the 32 lanes (dimensions) of each half, transposed as they reduce: at the step over lane bit m the
@@ -492,11 +505,11 @@ __device__ __forceinline__ void consume_store(const AttnLDS& L, int nsteps, int 
 // Passes 1 and 2 for the float64 path: wave w of NW takes tiles w, w + NW, ...; the row maximum score and the
 // row sum of exp. The per-key terms come in with each group of 4 keys (the statistics kernel runs 4 waves per
 // SIMD, which hide the loads).
-template <int NW>
+template <int HD, int NW>
 __device__ __forceinline__ void passes12_f64(const QK& c, const AttnLDS& L, const FastCtx& f, int ntile, int firstpos, int w,
                                              double& mx, int64_t& es) {
   double mw = AP_NEG;
-  KTile kt;   // the next tile's k digits load while this one is finished (its key terms load behind its products)
+  KTile<HD> kt;   // the next tile's k digits load while this one is finished (its key terms load behind its products)
   if (w < ntile) load_ktile(c, 32 * w, kt);
   for (int t = w; t < ntile; t += NW) {
     v16i hh, xx, ll;
@@ -535,10 +548,11 @@ __device__ __forceinline__ void passes12_f64(const QK& c, const AttnLDS& L, cons
 
 // Producer loop of the third pass (float64 path): iteration s turns tile AP_PROD s + w into p digits; the next
 // tile's k digits and key terms load while this one is finished.
+template <int HD>
 __device__ __forceinline__ void produce_f64(const QK& c, const AttnLDS& L, const FastCtx& f, int nsteps, int ntile, int firstpos,
                                             int w, int lane, double mx, int64_t es) {
   const double es20 = __builtin_ldexp((double)es, -20), res20 = 1048576.0 / (double)es, mxh = mx - 0.5;
-  KTile kt;
+  KTile<HD> kt;
   KCol kc;
   if (w < ntile) {
     load_ktile(c, 32 * w, kt);
@@ -568,13 +582,13 @@ __device__ __forceinline__ void produce_f64(const QK& c, const AttnLDS& L, const
 }
 
 // The int64 path (any shifts, any exp table): shr64 and lut_exp as the reference, exp table in global memory.
-template <int NW>
+template <int HD, int NW>
 __device__ __forceinline__ void passes12_i64(const QK& c, const AttnLDS& L, const int32_t* __restrict__ Tg, int64_t rterm, int sqv,
                                              int INV, int mypos, int ntile, int w, int64_t& mx, int64_t& es) {
   auto valid = [&](int t, int i) { return 32 * t + 8 * (i >> 2) + 4 * c.half + (i & 3) <= mypos; };
   int64_t m = INT64_MIN;
   for (int t = w; t < ntile; t += NW) {
-    KTile kt;
+    KTile<HD> kt;
     v16i hh, xx, ll;
     int64_t sc[16];
     load_ktile(c, 32 * t, kt);
@@ -595,7 +609,7 @@ __device__ __forceinline__ void passes12_i64(const QK& c, const AttnLDS& L, cons
   mx = m;
   int64_t e = 0;
   for (int t = w; t < ntile; t += NW) {
-    KTile kt;
+    KTile<HD> kt;
     v16i hh, xx, ll;
     int64_t sc[16];
     load_ktile(c, 32 * t, kt);
@@ -613,6 +627,7 @@ __device__ __forceinline__ void passes12_i64(const QK& c, const AttnLDS& L, cons
   for (int k = 0; k < NW; ++k) es += L.red_b[k * 32 + c.l32];
 }
 
+template <int HD>
 __device__ __forceinline__ void produce_i64(const QK& c, const AttnLDS& L, const int32_t* __restrict__ Tg, int64_t rterm, int sqv,
                                             int INV, int mypos, int nsteps, int ntile, int w, int lane, int64_t mx, int64_t es) {
   const double res = 1.0 / (double)es;
@@ -621,7 +636,7 @@ __device__ __forceinline__ void produce_i64(const QK& c, const AttnLDS& L, const
     if (s < nsteps) {
       v4i pa[3] = {v4i{}, v4i{}, v4i{}};
       if (t < ntile) {
-        KTile kt;
+        KTile<HD> kt;
         v16i hh, xx, ll;
         int64_t sc[16];
         load_ktile(c, 32 * t, kt);
@@ -679,6 +694,7 @@ __device__ __forceinline__ bool block_item(int R, int H, int KV, int& h, int& kh
 
 // Loads the exp table and the q digits into LDS (ends with a barrier) and fills b. part: k_attn_digits' per-tile
 // results. The float64 decision depends only on the block's rows, so both kernels agree.
+template <int HD>
 __device__ __forceinline__ void block_setup(Block& b, int h, int kh, int q0, const int16_t* __restrict__ qq,
                                             const int32_t* __restrict__ sq, const int8_t* __restrict__ kdig,
                                             const int32_t* __restrict__ ck, const int32_t* __restrict__ skk,
@@ -711,7 +727,7 @@ __device__ __forceinline__ void block_setup(Block& b, int h, int kh, int q0, con
   c.kpad = kpad;
   c.ckh = ck + (int64_t)kh * kpad;
   c.skh = skk + (int64_t)kh * kpad;
-  c.kdr = buf_res(kdig + (int64_t)kh * 2 * 4 * kpad * 32, (int64_t)2 * 4 * kpad * 32);
+  c.kdr = buf_res(kdig + (int64_t)kh * 2 * HD * kpad, (int64_t)2 * HD * kpad);   // 2 digits x HD / 32 blocks x kpad x 32
   c.ckr = buf_res(c.ckh, (int64_t)kpad * 4);
   c.skr = buf_res(c.skh, (int64_t)kpad * 4);
   const int qr = q0 + c.l32 < R ? q0 + c.l32 : R - 1;
@@ -721,9 +737,9 @@ __device__ __forceinline__ void block_setup(Block& b, int h, int kh, int q0, con
   b.mypos = max(0, min(pos[qr], nkeys - 1));
   b.ntile = jmax / 32 + 1;
   int sqs = 0;
-  const v4i* qp = reinterpret_cast<const v4i*>(qq + ((int64_t)qr * H + h) * AP_HD);
+  const v4i* qp = reinterpret_cast<const v4i*>(qq + ((int64_t)qr * H + h) * HD);
 #pragma unroll
-  for (int kb = 0; kb < 4; ++kb) {
+  for (int kb = 0; kb < HD / 32; ++kb) {
     const v4i a0 = qp[(32 * kb + 16 * c.half) / 8], a1 = qp[(32 * kb + 16 * c.half) / 8 + 1];
     v4i qh, ql;
     split_digits(a0, a1, qh, ql);
@@ -745,6 +761,7 @@ __device__ __forceinline__ void block_setup(Block& b, int h, int kh, int q0, con
 
 // Passes 1 and 2 (row maximum score, row sum of exp). grid as k_attn_pv, block 64 AP_SW. st_mx / st_es: [H][R]
 // int64 (the float64 path stores its exact integer maximum as an int64 too).
+template <int HD>
 __global__ __launch_bounds__(64 * AP_SW, 3) void k_attn_stats(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
                                                               const int8_t* __restrict__ kdig, const int32_t* __restrict__ ck,
                                                               const int32_t* __restrict__ skk, const int32_t* __restrict__ part,
@@ -752,23 +769,23 @@ __global__ __launch_bounds__(64 * AP_SW, 3) void k_attn_stats(const int16_t* __r
                                                               int64_t* __restrict__ st_mx, int64_t* __restrict__ st_es, int R,
                                                               int H, int KV, int nkeys, int kpad, int INV) {
   __shared__ __attribute__((aligned(16))) int32_t T[AP_TN];
-  __shared__ v4i Qd[8][64];
+  __shared__ v4i Qd[HD / 16][64];
   __shared__ double red_w[AP_SW * 32];
   __shared__ int64_t red_a[AP_SW * 32], red_b[AP_SW * 32];
   int h, kh, q0;
   if (!block_item(R, H, KV, h, kh, q0)) return;
   Block b;
-  block_setup(b, h, kh, q0, qq, sq, kdig, ck, skk, part, pos, Tg, T, Qd, R, H, KV, nkeys, kpad, INV);
+  block_setup<HD>(b, h, kh, q0, qq, sq, kdig, ck, skk, part, pos, Tg, T, Qd, R, H, KV, nkeys, kpad, INV);
   const int w = threadIdx.x >> 6;
   AttnLDS L{T, nullptr, red_w, red_a, red_b};
   int64_t mx, es;
   if (b.fast) {
     const FastCtx f{T, __builtin_ldexp((double)INV, b.sqv - 32), 256.0 * b.tz, 128 * b.sqs, b.mypos};
     double m;
-    passes12_f64<AP_SW>(b.c, L, f, b.ntile, b.firstpos, w, m, es);
+    passes12_f64<HD, AP_SW>(b.c, L, f, b.ntile, b.firstpos, w, m, es);
     mx = (int64_t)m;
   } else {
-    passes12_i64<AP_SW>(b.c, L, Tg, 128 * (int64_t)b.sqs, b.sqv, INV, b.mypos, b.ntile, w, mx, es);
+    passes12_i64<HD, AP_SW>(b.c, L, Tg, 128 * (int64_t)b.sqs, b.sqv, INV, b.mypos, b.ntile, w, mx, es);
   }
   const int row = q0 + b.c.l32;
   if (w == 0 && b.c.half == 0 && row < R) {
@@ -779,9 +796,11 @@ __global__ __launch_bounds__(64 * AP_SW, 3) void k_attn_stats(const int16_t* __r
 
 // Pass 3. grid ceil(R / 32) H rounded up to a multiple of 8, block 512 (8 waves): 32 query rows of one head per
 // block, heaviest tiles first. In steps of 4 key tiles of 32, waves 0..3 turn tile 4 s + w into p digits (LDS,
-// double-buffered) while waves 4..7 multiply the previous step's p into V, each for 32 dimensions (a producer
-// and a consumer share each SIMD). The consumers use 4 V digits when every |v| of the KV head is below 2^30, else 8.
-__global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
+// double-buffered) while the HD / 32 waves after them multiply the previous step's p into V, each for 32 dimensions
+// (at HD 128 a producer and a consumer share each SIMD). The consumers use 4 V digits when every |v| of the KV head
+// is below 2^30, else 8.
+template <int HD>
+__global__ __launch_bounds__(64 * (AP_PROD + HD / 32)) void k_attn_pv(const int16_t* __restrict__ qq, const int32_t* __restrict__ sq,
                                                  const int8_t* __restrict__ kdig, const int32_t* __restrict__ ck,
                                                  const int32_t* __restrict__ skk, const int32_t* __restrict__ part,
                                                  const int8_t* __restrict__ vdig, const int32_t* __restrict__ pos,
@@ -791,33 +810,33 @@ __global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int1
                                                  int INV) {
   __shared__ __attribute__((aligned(16))) int32_t T[AP_TN];
   __shared__ v4i Pl[2][AP_PROD][3][64];
-  __shared__ v4i Qd[8][64];
+  __shared__ v4i Qd[HD / 16][64];
   __shared__ int rowbits[32];
   int h, kh, q0;
   if (!block_item(R, H, KV, h, kh, q0)) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   if (tid < 32) rowbits[tid] = 0;
   Block b;
-  block_setup(b, h, kh, q0, qq, sq, kdig, ck, skk, part, pos, Tg, T, Qd, R, H, KV, nkeys, kpad, INV);
+  block_setup<HD>(b, h, kh, q0, qq, sq, kdig, ck, skk, part, pos, Tg, T, Qd, R, H, KV, nkeys, kpad, INV);
   const QK& c = b.c;
   const int row = q0 + c.l32 < R ? q0 + c.l32 : R - 1;
   const int64_t mx = st_mx[(int64_t)h * R + row], es = st_es[(int64_t)h * R + row];
   AttnLDS L{T, Pl, nullptr, nullptr, nullptr};
   const int nsteps = (b.ntile + AP_PROD - 1) / AP_PROD;
   const int dc = w - AP_PROD;   // consumer: dimensions 32 dc + [0, 32)
-  const int vplane = AP_HD * kpad;   // one digit plane: kpad / 32 tiles x 2 halves x hd x 16 bytes
+  const int vplane = HD * kpad;   // one digit plane: kpad / 32 tiles x 2 halves x hd x 16 bytes
   const BufRes vr = buf_res(vdig + (int64_t)kh * 8 * vplane, (int64_t)8 * vplane);
-  const int voff = (c.half * AP_HD + 32 * dc + c.l32) * 16;
+  const int voff = (c.half * HD + 32 * dc + c.l32) * 16;
   if (w >= AP_PROD) {
     if (wave_max_of(part + (int64_t)kh * (kpad / 32), kpad / 32) + 2 <= 32)
-      consume_store<4>(L, nsteps, b.ntile, vr, voff, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
+      consume_store<HD, 4>(L, nsteps, b.ntile, vr, voff, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
     else
-      consume_store<8>(L, nsteps, b.ntile, vr, voff, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
+      consume_store<HD, 8>(L, nsteps, b.ntile, vr, voff, vplane, lane, out, rowbits, q0, R, H, h, 32 * dc + c.l32, c.half);
   } else if (b.fast) {
     const FastCtx f{T, __builtin_ldexp((double)INV, b.sqv - 32), 256.0 * b.tz, 128 * b.sqs, b.mypos};
-    produce_f64(c, L, f, nsteps, b.ntile, b.firstpos, w, lane, (double)mx, es);
+    produce_f64<HD>(c, L, f, nsteps, b.ntile, b.firstpos, w, lane, (double)mx, es);
   } else {
-    produce_i64(c, L, Tg, 128 * (int64_t)b.sqs, b.sqv, INV, b.mypos, nsteps, b.ntile, w, lane, mx, es);
+    produce_i64<HD>(c, L, Tg, 128 * (int64_t)b.sqs, b.sqv, INV, b.mypos, nsteps, b.ntile, w, lane, mx, es);
   }
   __syncthreads();
   if (obits && tid < 32 && q0 + tid < R) obits[(int64_t)(q0 + tid) * H + h] = rowbits[tid];
@@ -826,8 +845,8 @@ __global__ __launch_bounds__(64 * (AP_PROD + AP_CONS)) void k_attn_pv(const int1
 // workspace layout (bytes, each part 256-aligned): vdig KV*8*hd*kpad, kdig KV*2*hd*kpad, ck and skk KV*kpad*4
 // each, the digit kernel's per-tile results (2 KV + 1) * kpad / 32 int32; row maxima and sums H*R*8 each
 static int64_t al256(int64_t n) { return (n + 255) & ~(int64_t)255; }
-static int64_t ws_bytes(int R, int H, int KV, int kpad) {
-  return al256((int64_t)KV * 8 * AP_HD * kpad) + al256((int64_t)KV * 2 * AP_HD * kpad) + 2 * al256((int64_t)KV * kpad * 4) +
+static int64_t ws_bytes(int R, int H, int KV, int hd, int kpad) {
+  return al256((int64_t)KV * 8 * hd * kpad) + al256((int64_t)KV * 2 * hd * kpad) + 2 * al256((int64_t)KV * kpad * 4) +
          al256((int64_t)(2 * KV + 1) * (kpad / 32) * 4) + 2 * al256((int64_t)H * R * 8);
 }
 
@@ -836,8 +855,8 @@ static int64_t ws_bytes(int R, int H, int KV, int kpad) {
 using namespace exact;
 
 extern "C" int64_t exact_attention_prefill_workspace(int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t nkeys) {
-  if (R <= 0 || H <= 0 || KV <= 0 || hd != AP_HD || nkeys <= 0) return -1;
-  return ws_bytes(R, H, KV, (nkeys + 31) / 32 * 32);
+  if (R <= 0 || H <= 0 || KV <= 0 || (hd != 64 && hd != 128) || nkeys <= 0) return -1;
+  return ws_bytes(R, H, KV, hd, (nkeys + 31) / 32 * 32);
 }
 
 extern "C" int exact_attention_prefill(const int16_t* qq, const int32_t* sq, const int16_t* kq, const int32_t* sk,
@@ -847,25 +866,33 @@ extern "C" int exact_attention_prefill(const int16_t* qq, const int32_t* sq, con
   if (!qq || !sq || !kq || !sk || !v || !pos || !exp_t || !out || !work) return EXACT_E_ARG;
   if (R <= 0 || H <= 0 || KV <= 0 || H % KV || slot < 0 || Smax <= 0 || nkeys <= 0 || nkeys > Smax) return EXACT_E_ARG;
   // per shift class, 3 digit pairs x nkeys products of |.| <= 2^14 stay below 2^31
-  if (hd != AP_HD || nkeys > 32768) return EXACT_E_UNSUPPORTED;
+  if ((hd != 64 && hd != 128) || nkeys > 32768) return EXACT_E_UNSUPPORTED;
   const int kpad = (nkeys + 31) / 32 * 32;
-  if (work_bytes < ws_bytes(R, H, KV, kpad) || (reinterpret_cast<uintptr_t>(work) & 255) ||
+  if (work_bytes < ws_bytes(R, H, KV, hd, kpad) || (reinterpret_cast<uintptr_t>(work) & 255) ||
       (reinterpret_cast<uintptr_t>(exp_t) & 15))
     return EXACT_E_ARG;
   int8_t* vdig = static_cast<int8_t*>(work);
-  int8_t* kdig = vdig + al256((int64_t)KV * 8 * AP_HD * kpad);
-  int32_t* ck = reinterpret_cast<int32_t*>(kdig + al256((int64_t)KV * 2 * AP_HD * kpad));
+  int8_t* kdig = vdig + al256((int64_t)KV * 8 * hd * kpad);
+  int32_t* ck = reinterpret_cast<int32_t*>(kdig + al256((int64_t)KV * 2 * hd * kpad));
   int32_t* skk = reinterpret_cast<int32_t*>(reinterpret_cast<int8_t*>(ck) + al256((int64_t)KV * kpad * 4));
   int32_t* part = reinterpret_cast<int32_t*>(reinterpret_cast<int8_t*>(skk) + al256((int64_t)KV * kpad * 4));
   int64_t* st_mx = reinterpret_cast<int64_t*>(reinterpret_cast<int8_t*>(part) + al256((int64_t)(2 * KV + 1) * (kpad / 32) * 4));
   int64_t* st_es = reinterpret_cast<int64_t*>(reinterpret_cast<int8_t*>(st_mx) + al256((int64_t)H * R * 8));
   hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(k_attn_digits, dim3(kpad / 32, 2 * KV), dim3(256), 0, st, v, kq, sk, exp_t, slot, KV, Smax, nkeys, kpad,
-                     vdig, kdig, ck, skk, part);
   const dim3 grid(((R + 31) / 32 * H + 7) / 8 * 8);
-  hipLaunchKernelGGL(k_attn_stats, grid, dim3(64 * AP_SW), 0, st, qq, sq, kdig, ck, skk, part, pos, exp_t, st_mx, st_es, R, H,
-                     KV, nkeys, kpad, INV);
-  hipLaunchKernelGGL(k_attn_pv, grid, dim3(64 * (AP_PROD + AP_CONS)), 0, st, qq, sq, kdig, ck, skk, part, vdig, pos, exp_t, st_mx,
-                     st_es, out, obits, R, H, KV, nkeys, kpad, INV);
+#define AP_GO(HD)                                                                                                      \
+  do {                                                                                                                 \
+    hipLaunchKernelGGL(k_attn_digits<HD>, dim3(kpad / 32, 2 * KV), dim3(256), 0, st, v, kq, sk, exp_t, slot, KV, Smax,   \
+                       nkeys, kpad, vdig, kdig, ck, skk, part);                                                        \
+    hipLaunchKernelGGL(k_attn_stats<HD>, grid, dim3(64 * AP_SW), 0, st, qq, sq, kdig, ck, skk, part, pos, exp_t, st_mx,  \
+                       st_es, R, H, KV, nkeys, kpad, INV);                                                             \
+    hipLaunchKernelGGL(k_attn_pv<HD>, grid, dim3(64 * (AP_PROD + HD / 32)), 0, st, qq, sq, kdig, ck, skk, part, vdig,    \
+                       pos, exp_t, st_mx, st_es, out, obits, R, H, KV, nkeys, kpad, INV);                              \
+  } while (0)
+  if (hd == 64)
+    AP_GO(64);
+  else
+    AP_GO(128);
+#undef AP_GO
   return launch_status("attention_prefill");
 }

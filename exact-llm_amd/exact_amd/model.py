@@ -271,7 +271,9 @@ class TModel:
     def new_cache(self, B=None):
         return Cache(self.cfg, self.batch if B is None else B, self.Smax, self.dev, self.nl)
 
-    PREFILL_MIN_ROWS = 96   # rows from which prefill attention runs on the matrix cores (the row kernel is faster below)
+    # rows from which prefill attention runs on the matrix cores, per head dimension (the row kernel is faster below:
+    # at hd 64, 14 q heads, 128 rows take 21.5 us there and 19.1 us in the row kernel, 256 rows 26.5 and 41.2 us)
+    PREFILL_MIN_ROWS = {64: 160, 128: 96}
     QROW_FUSE_ROWS = 2
     # widest rows whose norm runs inside the consuming GEMVs (every block repeats the row's three reductions; at
     # 3584-wide rows that costs as much as the separate launch it saves, at 5120 more, at 896 less: 7.0 vs 8.2 us)
@@ -562,8 +564,8 @@ class TModel:
         ws.ids.copy_(torch.tensor(ids, dtype=I32))
         ws.slot.fill_(slot)
         ws.pos.copy_(torch.arange(p0, p0 + T, dtype=I32))
-        # the matrix-core attention for prefill chunks of PREFILL_MIN_ROWS rows or more (hd 128); the row kernel otherwise
-        ws.seq = (slot, p0 + T) if T >= self.PREFILL_MIN_ROWS and self.cfg.hd == 128 else None
+        # the matrix-core attention for prefill chunks of PREFILL_MIN_ROWS[hd] rows or more (hd 64, 128); the row kernel otherwise
+        ws.seq = (slot, p0 + T) if T >= self.PREFILL_MIN_ROWS.get(self.cfg.hd, 1 << 30) else None
         key = (T, id(cache), slot, p0, bool(last_only))
         g = self._graphs.get(key) if graph else None
         try:
@@ -602,7 +604,7 @@ class TModel:
         ws.ids.copy_(torch.tensor(ids, dtype=I32))
         ws.slot.fill_(slot)
         ws.pos.copy_(torch.arange(p0, p0 + T, dtype=I32))
-        ws.seq = (slot, p0 + T) if T >= self.PREFILL_MIN_ROWS and self.cfg.hd == 128 else None
+        ws.seq = (slot, p0 + T) if T >= self.PREFILL_MIN_ROWS.get(self.cfg.hd, 1 << 30) else None
         try:
             self.forward_rows(ws, trace=(layout, buf))
         finally:

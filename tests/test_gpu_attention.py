@@ -88,6 +88,22 @@ def test_prefill_matches_oracle(H, KV, nkeys, R, vmag, shifts):
     assert np.array_equal(obits, obits_of(want, H))
 
 
+@pytest.mark.parametrize("H,KV,nkeys,R,vmag,shifts", [(14, 2, 300, 300, "small", 4), (14, 2, 290, 257, "large", 4),
+                                                      (4, 2, 1, 1, "small", 4), (4, 1, 100, 37, "large", 4),
+                                                      (2, 2, 64, 64, "wrap", 4), (4, 2, 150, 150, "small", 22),
+                                                      (4, 2, 120, 120, "small", (18, 18))])
+def test_prefill_hd64_matches_oracle(H, KV, nkeys, R, vmag, shifts):
+    """head dimension 64 (the 0.5B shape: 14 q heads over 2 KV heads) on the matrix-core prefill: two 32-dimension
+    blocks per q.k product and two p.v consumer waves; bit-exact against the oracle, obits too"""
+    hd, Smax, slot = 64, 320, 1
+    case = make_case(nkeys * 5 + R, 2, slot, H, KV, hd, Smax, nkeys, R, vmag, shifts)
+    cache, qq, sq, pos = to_dev(*case)
+    out, obits = run_prefill(cache, qq, sq, pos, slot, nkeys, H, KV, hd)
+    want = oracle_rows(*case, slot, H, KV, np.arange(R))
+    assert np.array_equal(out, want)
+    assert np.array_equal(obits, obits_of(want, H))
+
+
 @pytest.mark.parametrize("R,nkeys", [(3, 50), (17, 17), (70, 100)])   # 70 x 4 heads: the blocks run in several rounds
 def test_row_attention_matches_oracle(R, nkeys):
     H, KV, hd, Smax, slot = 4, 2, 128, max(64, nkeys), 1
@@ -103,10 +119,11 @@ def test_row_attention_matches_oracle(R, nkeys):
     assert np.array_equal(host(obits), obits_of(want, H))
 
 
-def test_prefill_full_size_2048():
-    """Attention prefill at the 7B shape (28 q heads, 4 KV heads, hd 128, 2048 tokens): every row equal to the
-    row kernel's result, and 24 rows (first, last and random) equal to the oracle."""
-    H, KV, hd, S, slot = 28, 4, 128, 2048, 0
+@pytest.mark.parametrize("H,KV,hd", [(28, 4, 128), (14, 2, 64)])
+def test_prefill_full_size_2048(H, KV, hd):
+    """Attention prefill at the 7B shape (28 q heads, 4 KV heads, hd 128) and the 0.5B shape (14, 2, hd 64), 2048
+    tokens: every row equal to the row kernel's result, and 24 rows (first, last and random) equal to the oracle."""
+    S, slot = 2048, 0
     case = make_case(2048, 1, slot, H, KV, hd, S, S, S, "small")
     cache, qq, sq, pos = to_dev(*case)
     out, obits = run_prefill(cache, qq, sq, pos, slot, S, H, KV, hd)
@@ -120,12 +137,13 @@ def test_prefill_full_size_2048():
     assert np.array_equal(out[rows], oracle_rows(*case, slot, H, KV, rows))
 
 
+@pytest.mark.parametrize("hd", [128, 64])
 @pytest.mark.parametrize("change", ["swap", "steep", "tail"])
-def test_prefill_with_unfit_exp_table_matches_row_kernel(change):
+def test_prefill_with_unfit_exp_table_matches_row_kernel(change, hd):
     """An exp table outside the form the matrix-core path's float64 scores take (non-increasing, entries in
     [0, 2^24], steps below 2^24, T[0] > 0, zero from entry 4606 on) sends every block to the int64 scores: the
     result equals the row kernel's, which reads the table as the reference does, on the same table."""
-    H, KV, hd, nkeys, R, slot = 4, 2, 128, 150, 150, 1
+    H, KV, nkeys, R, slot = 4, 2, 150, 150, 1
     case = make_case(11, 2, slot, H, KV, hd, 192, nkeys, R, "small")
     cache, qq, sq, pos = to_dev(*case)
     t = exp_t().astype(np.int64)

@@ -7,7 +7,7 @@ import torch
 
 import exact_oracle as O
 import helpers
-from exact_amd import synth
+from exact_amd import ops, synth
 from exact_amd._lib import ExactError
 from exact_amd.model import DeviceWeights, GraphDecoder, TModel
 
@@ -108,22 +108,28 @@ def test_decode_with_swiglu_in_the_gate_up_gemv_matches_oracle(name, qkv_norm):
         assert tok == otoks[i]
 
 
-def test_chunked_prefill_on_matrix_core_attention_matches_oracle():
-    """hd 128: prompt chunks of TModel.PREFILL_MIN_ROWS (96) rows or more take the matrix-core attention
-    (exact_attention_prefill), here a 200-token prompt as one chunk and as chunks of 100 + 100, the second
-    continuing the cache (start position 100), then greedy decode steps."""
-    cfg = synth.CONFIGS["tiny-hd128"]
+@pytest.mark.parametrize("name", ["tiny-hd128", "tiny"])
+def test_chunked_prefill_on_matrix_core_attention_matches_oracle(name, monkeypatch):
+    """hd 128 and hd 64: prompt chunks of TModel.PREFILL_MIN_ROWS[hd] rows or more take the matrix-core attention
+    (exact_attention_prefill), here a prompt of 2 c tokens (c = that threshold + 4) as one chunk and as chunks of
+    c + c, the second continuing the cache (start position c), then greedy decode steps."""
+    cfg = synth.CONFIGS[name]
+    c = TModel.PREFILL_MIN_ROWS[cfg.hd] + 4
+    calls = []
+    real = ops.attention_prefill
+    monkeypatch.setattr(ops, "attention_prefill", lambda *a, **k: calls.append(a[5]) or real(*a, **k))
     seed = 4
-    assert TModel.PREFILL_MIN_ROWS <= 100
-    om = helpers.oracle_model(cfg, seed, T=224)
-    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=224)
-    ids = helpers.prompt(17, 200, cfg.V)
+    om = helpers.oracle_model(cfg, seed, T=2 * c + 24)
+    tm = TModel(DeviceWeights.synthetic(cfg, seed, DEV), Smax=2 * c + 24)
+    ids = helpers.prompt(17, 2 * c, cfg.V)
     want = om(ids)
     assert np.array_equal(host(tm.forward(ids)), want)
     cache = tm.new_cache(B=1)
-    lg1 = host(tm.forward(ids[:100], cache))
-    lg2 = host(tm.forward(ids[100:], cache))
+    lg1 = host(tm.forward(ids[:c], cache))
+    lg2 = host(tm.forward(ids[c:], cache))
     assert np.array_equal(np.concatenate([lg1, lg2]), want)
+    # every layer of the three passes ran the matrix-core attention, over 2 c, c and 2 c keys
+    assert calls == [2 * c] * cfg.NL + [c] * cfg.NL + [2 * c] * cfg.NL
     otoks, orows = O.greedy_decode(om, ids, 4)
     tok = int(lg2[-1].argmax())
     assert tok == otoks[0]
