@@ -473,9 +473,9 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
     mx = val > mx ? val : mx;
   }
   if (wave == (int)(p % blockDim.x) >> 6) {   // the new key, from LDS: the wave of thread p % blockDim.x, lanes over dims
-    int64_t part = 0;
-    for (int j = lane; j < hd; j += 64) part += (int64_t)qs[j] * kn[j];   // exact: |q k| < 2^30, 256 of them
-    const int64_t dot = wave_sum64(part);
+    int64_t psum = 0;
+    for (int j = lane; j < hd; j += 64) psum += (int64_t)qs[j] * kn[j];   // exact: |q k| < 2^30, 256 of them
+    const int64_t dot = wave_sum64(psum);
     if (tid == (int)(p % blockDim.x)) {   // that thread owns sc[p] in the loops below
       const int64_t val = shr64(dot * INV, 32 - sqv - skn);
       sc[p] = val;

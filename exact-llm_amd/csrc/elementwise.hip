@@ -47,11 +47,11 @@ __global__ void k_qrow(const int64_t* __restrict__ x, int bits, void* xq, int32_
   qrow_store(buf, K, bits, xq, s, r, red);
 }
 
-// irms of the row in buf (in place): exact_llm.py:100-106
-__device__ void irms_inplace(int64_t* buf, const int64_t* __restrict__ g, int D, int64_t* red) {
+// irms of one row, in place: exact_llm.py:100-106
+__device__ void irms_inplace(int64_t* row, const int64_t* __restrict__ g, int D, int64_t* red) {
   int64_t m = 0;
   for (int i = threadIdx.x; i < D; i += blockDim.x) {
-    const int64_t a = abs64(buf[i]);
+    const int64_t a = abs64(row[i]);
     m = a > m ? a : m;
   }
   m = block_max64(m, red);
@@ -59,7 +59,7 @@ __device__ void irms_inplace(int64_t* buf, const int64_t* __restrict__ g, int D,
   if (k < 0) k = 0;
   int64_t ss = 0;
   for (int i = threadIdx.x; i < D; i += blockDim.x) {
-    const int64_t xs = shr64(buf[i], k);
+    const int64_t xs = shr64(row[i], k);
     ss = (int64_t)((uint64_t)ss + (uint64_t)(xs * xs));
   }
   ss = block_sum64(ss, red);
@@ -68,8 +68,8 @@ __device__ void irms_inplace(int64_t* buf, const int64_t* __restrict__ g, int D,
   if (rt < 1) rt = 1;
   const int64_t den = shl64(rt, k);
   for (int i = threadIdx.x; i < D; i += blockDim.x) {
-    const int64_t y = floordiv_pos(shl64(buf[i], EXACT_F), den);
-    buf[i] = shr64(y * g[i], EXACT_F);
+    const int64_t y = floordiv_pos(shl64(row[i], EXACT_F), den);
+    row[i] = shr64(y * g[i], EXACT_F);
   }
   __syncthreads();
 }
