@@ -25,8 +25,11 @@ HBM_PEAK_GBPS = 8000.0
 # gate|up launch: 37888*3584 int8 weights + 37888*28*2 scale bytes + 3584 x bytes + 37888*8 output bytes
 GATEUP_BYTES = 37888 * 3584 + 37888 * 28 * 2 + 3584 + 37888 * 8
 # HBM bytes per gate|up launch from FETCH_SIZE / WRITE_SIZE counter runs, each scaled by the same counter on a
-# 512 MiB device copy (profiles/gemv_gateup_7b_traffic.md)
-GATEUP_TRAFFIC_BYTES = 139_850_000
+# 512 MiB device copy (profiles/gemv_gateup_7b_traffic.md): 138,023,202 read + 1,818,624 written
+GATEUP_TRAFFIC_BYTES = 139_841_826
+# HBM bytes of one 7B bs1 decode step (the headline's unit of work), measured the same way over the step's 174
+# launches (profiles/decode_7b_bs1_step.md): 7,326.1 MB read + 124.9 MB written
+STEP_TRAFFIC_BYTES = 7_451_100_000
 INT8_PEAK_TOPS = 5000.0
 
 
@@ -315,8 +318,9 @@ def trace_capture(args, name="qwen2.5-7b", prompt_len=16, steps=32, reps=3):
 
 
 def attention_prefill(args, S=2048, H=28, KV=4, hd=128):
-    """Exact integer causal attention of one 2048-token prefill layer (28 q / 4 kv heads, hd 128) from the
-    KV cache: algorithmic ops 2*(S(S+1)/2)*hd*H for q.k and the same for p.v."""
+    """Exact integer causal attention of one 2048-token prefill layer (by default the 7B's 28 q / 4 kv heads of
+    hd 128) from the KV cache, on the matrix cores and on the row kernel: algorithmic ops 2*(S(S+1)/2)*hd*H for q.k
+    and the same for p.v."""
     import torch
     from exact_amd import ops
     from exact_amd.tables import DeviceTables
@@ -671,6 +675,8 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="also copy 512 MiB on the device three times (calibrates the HBM traffic counters)")
     ap.add_argument("--cpu-only", action="store_true", help="only the CPU baseline (no GPU work); prints its JSON")
+    ap.add_argument("--no-headline", action="store_true",
+                    help="skip the 7B decode headline (for profiling the other parts); prints their JSON without a value")
     args = ap.parse_args()
     if args.cpu_only:
         print(json.dumps(cpu_baseline(full=args.cpu_full)), flush=True)
@@ -694,8 +700,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     # the headline: full-model Qwen2.5-7B-shape decode, batch 1, int16 activations (the spec), timed over --steps steps
-    mdl = model_decode(args)
-    progress(f"7B decode {mdl['tok_s']} tok/s")
+    mdl = None if args.no_headline else model_decode(args)
+    if mdl is not None:
+        progress(f"7B decode {mdl['tok_s']} tok/s")
     r = None if args.no_gemv else gemv_pass(args)
     progress("GEMV pass done")
     op = None if args.no_gemv else gemv_op_pass(args)
@@ -714,8 +721,15 @@ def main():
                 progress(f"{k} {models[k]['tok_s']} tok/s")
         trc = None if args.no_trace else trace_capture(args)
     att = None if args.no_prefill else attention_prefill(args)
+    att64 = None if args.no_prefill else attention_prefill(args, H=14, KV=2, hd=64)   # the 0.5B's heads
     progress("prefill GEMM / attention / trace done")
     cpu = None if args.no_cpu else cpu_baseline(full=args.cpu_full)
+    if mdl is None:   # a profiling run of the other parts: no headline value
+        print(json.dumps({"metric": METRIC, "value": None, "headline": "skipped (--no-headline)", "gemv_c2": r,
+                          "exact_gemv_op": op, "prefill_gemm": pre, "attention_prefill": att,
+                          "attention_prefill_hd64": att64, "model_configs": models,
+                          "trace_capture": trc, "cpu_baseline": cpu}, default=str), flush=True)
+        return
     wbytes = mdl["weights_GB_per_step"] * 1e9
     step_gbps = wbytes / (mdl["ms_per_step"] * 1e-3) / 1e9
     line = {
@@ -730,7 +744,7 @@ def main():
                    "batch": 1, "abits": 15, "prompt": mdl["prompt"], "weights_GB_per_step": mdl["weights_GB_per_step"],
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(step_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(step_gbps / HBM_PEAK_GBPS, 4), "traffic": STEP_TRAFFIC_BYTES,
                      "algorithmic_bytes": int(wbytes), "unit_of_work": "one decode step (embedding to greedy token, one "
                                                                        "graph replay): int8 weights + int16 scales read"},
         "model_decode": mdl,
@@ -739,6 +753,7 @@ def main():
         "prefill_TOPS": (round(min(v["TOPS"] for k, v in pre.items() if not k.endswith("_a16")), 2) if pre else None),
         "prefill_TOPS_a16": (round(min(v["TOPS"] for k, v in pre.items() if k.endswith("_a16")), 2) if pre else None),
         "attention_prefill": att,
+        "attention_prefill_hd64": att64,
         "trace_capture": trc,
         "exact_gemv_op": op,
         "cpu_baseline": None if cpu is None else dict(
