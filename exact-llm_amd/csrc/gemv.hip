@@ -762,10 +762,17 @@ __global__ __launch_bounds__(256) void k_gemv_experts_xq(const int64_t* __restri
 // (hi = x >> 8, lo = (x & 255) - 128) stay in registers for all its rows; per chunk three int8 dot products give the
 // lane's part of 256 hi.w + lo.w + 128 sum(w) = x.w (exact_torch.py:101-102), which the lane multiplies by its
 // group's scale (sum_g M_g sum_lanes a = sum_lanes M_g a: the per-group sums need no reduction of their own), and the
-// wave sums the row's int64 partials once. Rows are loaded two ahead of the one being summed. Ranges of one row
-// combine with 64-bit atomics (exact in any order).
+// wave sums the row's int64 partials once. Rows are loaded two ahead of the one being summed, into two register sets
+// used in turn; the row loop is unrolled whole (RPW rows a wave, a template parameter) and no load sits behind a
+// branch, so each row waits only for its own loads. (A row loop with a back edge made the compiler copy the loaded
+// registers at the latch, which waits for every outstanding load: one memory round trip a row.) Lanes past the
+// range's end load its last chunk and weigh it 0 (their x digits and their all-ones pattern are zero); rows past the
+// block's end load its last row again and store nothing. Ranges of one row combine with 64-bit atomics (exact in any
+// order).
 // K ranges of 4 KiB (4 chunks a lane), 2 KiB for rows of 8 KiB and more (7B down, 18944: 19.7 -> 18.6 us a call)
+#ifndef ROWMAJ_LONG_K
 #define ROWMAJ_LONG_K 8192
+#endif
 #ifndef ROWMAJ_WAVES
 #define ROWMAJ_WAVES 2048                 // waves to aim for: rows per wave = N x ranges / ROWMAJ_WAVES (1..8)
 #endif
@@ -781,38 +788,37 @@ struct RowMajRow {
 template <bool NT, int CH>
 __device__ __forceinline__ void rowmaj_load(RowMajRow<CH>& R_, const int8_t* __restrict__ wT, const int64_t* __restrict__ Mg,
                                             int n, int K, int G, int kb0, int nck, int lane) {
-  const int8_t* wr = wT + (size_t)n * K + kb0 + 16 * lane;
-  const int64_t* mr = Mg + (size_t)n * G + kb0 / 128 + (lane >> 3);
+  const int8_t* wr = wT + (size_t)n * K + kb0;
+  const int64_t* mr = Mg + (size_t)n * G + kb0 / 128;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    if (lane + 64 * c < nck) {
-      const v4i* p = reinterpret_cast<const v4i*>(wr + 1024 * c);
-      R_.w[c] = NT ? __builtin_nontemporal_load(p) : *p;
-      R_.m[c] = mr[8 * c];
-    } else {
-      R_.w[c] = v4i{0, 0, 0, 0};
-      R_.m[c] = 0;
-    }
+    const int ci = lane + 64 * c < nck ? lane + 64 * c : nck - 1;   // chunk index inside the range
+    const v4i* p = reinterpret_cast<const v4i*>(wr + 16 * ci);
+    R_.w[c] = NT ? __builtin_nontemporal_load(p) : *p;
+    R_.m[c] = mr[ci >> 3];
   }
 }
 
-template <bool NT, int CH>
+template <bool NT, int CH, int RPW>
 __global__ __launch_bounds__(256) void k_gemv_rowmajor(const int16_t* __restrict__ x, const int8_t* __restrict__ wT,
                                                        const int64_t* __restrict__ Mg, int64_t* __restrict__ out, int N,
-                                                       int K, int G, int nranges, int rpw, int out_mode) {
+                                                       int K, int G, int nranges, int out_mode) {
+  constexpr int rpw = RPW;
   const int lane = threadIdx.x & 63;
-  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int wid = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));   // rows and range: scalar
   const int nrb = (N + rpw - 1) / rpw;
   if (wid >= nrb * nranges) return;
   const int rb = wid / nranges, kr = wid - rb * nranges;
   const int kb0 = kr * CH * 1024;
   const int nck = ((K - kb0 < CH * 1024 ? K - kb0 : CH * 1024)) / 16;   // 16-byte chunks in the range
   const int n0 = rb * rpw, n1 = n0 + rpw < N ? n0 + rpw : N;
-  // the lane's x digits, one 16-byte chunk of k per slot
+  // the lane's x digits, one 16-byte chunk of k per slot, and its all-ones pattern (zero past the range)
   v4i xh[CH], xl[CH];
+  int ones[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const v4i zero = {0, 0, 0, 0};
+    ones[c] = lane + 64 * c < nck ? 0x01010101 : 0;
     if (lane + 64 * c < nck) {
       const v4i* xp = reinterpret_cast<const v4i*>(x + kb0 + 16 * (lane + 64 * c));
       split_a16(xp[0], xp[1], xh[c], xl[c]);
@@ -821,31 +827,33 @@ __global__ __launch_bounds__(256) void k_gemv_rowmajor(const int16_t* __restrict
       xl[c] = zero;
     }
   }
-  RowMajRow<CH> ra, rb_;
-  rowmaj_load<NT, CH>(ra, wT, Mg, n0, K, G, kb0, nck, lane);
-  if (n0 + 1 < n1) rowmaj_load<NT, CH>(rb_, wT, Mg, n0 + 1, K, G, kb0, nck, lane);
-  for (int n = n0; n < n1; ++n) {
+  auto row = [&](int r) { return n0 + r < n1 ? n0 + r : n1 - 1; };   // past the block's end: its last row again
+  RowMajRow<CH> rr[2];
+  rowmaj_load<NT, CH>(rr[0], wT, Mg, row(0), K, G, kb0, nck, lane);
+  if (RPW > 1) rowmaj_load<NT, CH>(rr[1], wT, Mg, row(1), K, G, kb0, nck, lane);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    RowMajRow<CH>& cur = rr[r & 1];
     int64_t part = 0;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
       int sh = 0, sl = 0, s1 = 0;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        sh = dot4(ra.w[c][d], xh[c][d], sh);
-        sl = dot4(ra.w[c][d], xl[c][d], sl);
-        s1 = dot4(ra.w[c][d], 0x01010101, s1);
+        sh = dot4(cur.w[c][d], xh[c][d], sh);
+        sl = dot4(cur.w[c][d], xl[c][d], sl);
+        s1 = dot4(cur.w[c][d], ones[c], s1);
       }
-      part += (int64_t)((sh << 8) + sl + (s1 << 7)) * ra.m[c];   // zero past the range (m = 0)
+      part += (int64_t)((sh << 8) + sl + (s1 << 7)) * cur.m[c];   // a = 0 past the range
     }
-    ra = rb_;
-    if (n + 2 < n1) rowmaj_load<NT, CH>(rb_, wT, Mg, n + 2, K, G, kb0, nck, lane);
+    if (r + 2 < RPW) rowmaj_load<NT, CH>(cur, wT, Mg, row(r + 2), K, G, kb0, nck, lane);
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) part += __shfl_xor(part, o, 64);
-    if (lane == 0) {
+    if (lane == 0 && n0 + r < n1) {
       if (out_mode)
-        atomicAdd(reinterpret_cast<unsigned long long*>(out + n), (unsigned long long)part);
+        atomicAdd(reinterpret_cast<unsigned long long*>(out + n0 + r), (unsigned long long)part);
       else
-        out[n] = part;
+        out[n0 + r] = part;
     }
   }
 }
@@ -1025,8 +1033,8 @@ extern "C" int exact_gemv(const int16_t* x, const int8_t* wT, const int64_t* Mg,
   const int G = K / 128;
   const int ch = K >= ROWMAJ_LONG_K ? 2 : 4;
   const int nranges = (K + ch * 1024 - 1) / (ch * 1024);
-  int64_t rpw = (int64_t)N * nranges / ROWMAJ_WAVES;
-  rpw = rpw < 1 ? 1 : (rpw > 8 ? 8 : rpw);
+  const int64_t rq = (int64_t)N * nranges / ROWMAJ_WAVES;
+  const int rpw = rq >= 8 ? 8 : (rq >= 4 ? 4 : (rq >= 2 ? 2 : 1));   // rows per wave: a power of two up to 8
   const int64_t waves = (((int64_t)N + rpw - 1) / rpw) * nranges;
   if (waves > (1LL << 30)) return EXACT_E_UNSUPPORTED;
   hipStream_t st = as_stream(stream);
@@ -1034,12 +1042,16 @@ extern "C" int exact_gemv(const int16_t* x, const int8_t* wT, const int64_t* Mg,
     int e = zero_bytes(out, (int64_t)N * 8, st);
     if (e) return e;
   }
-  if (ch == 2)
-    hipLaunchKernelGGL((k_gemv_rowmajor<GEMV_NT != 0, 2>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, wT, Mg,
-                       out, N, K, G, nranges, (int)rpw, nranges > 1 ? 1 : 0);
-  else
-    hipLaunchKernelGGL((k_gemv_rowmajor<GEMV_NT != 0, 4>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, x, wT, Mg,
-                       out, N, K, G, nranges, (int)rpw, nranges > 1 ? 1 : 0);
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  const int mode = nranges > 1 ? 1 : 0;
+#define ROWMAJ_GO(C, P) hipLaunchKernelGGL((k_gemv_rowmajor<GEMV_NT != 0, C, P>), grid, dim3(256), 0, st, x, wT, Mg, out, N, K, \
+                                           G, nranges, mode)
+  if (ch == 2) {
+    if (rpw == 8) ROWMAJ_GO(2, 8); else if (rpw == 4) ROWMAJ_GO(2, 4); else if (rpw == 2) ROWMAJ_GO(2, 2); else ROWMAJ_GO(2, 1);
+  } else {
+    if (rpw == 8) ROWMAJ_GO(4, 8); else if (rpw == 4) ROWMAJ_GO(4, 4); else if (rpw == 2) ROWMAJ_GO(4, 2); else ROWMAJ_GO(4, 1);
+  }
+#undef ROWMAJ_GO
   return launch_status("gemv");
 }
 
