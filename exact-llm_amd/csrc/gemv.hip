@@ -157,7 +157,13 @@ __device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc
 
 // The group loop of one wave over groups [g0, g1) of row block nb. The next group's loads are issued
 // before the current group's matrix-core work and every load is unconditional inside the loop, so
-// each wave keeps two tiles (16 KiB) in flight.
+// each wave keeps two tiles (16 KiB) in flight. With one row per lane (VR = 1) a scheduling fence keeps the next group's
+// loads ahead of this group's products: without it the compiler, aiming at an occupancy a 16-wave block cannot use,
+// sinks them below the products and each group waits for its own loads (A8 7B pass 1.394-1.436 -> 1.359-1.402 ms).
+// At VR = 4 the second register set does not fit the 128 registers of a 1024-thread block (bs8 gate|up 27.5 -> 40 us).
+#ifndef GEMV_SCHED_FENCE
+#define GEMV_SCHED_FENCE 1
+#endif
 // pro: run after the first group's weight tile is in flight and before its activations are read (the
 // quantising GEMV fills its LDS slice there).
 struct NoPrologue {
@@ -189,8 +195,10 @@ __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t*
   int g = g0;
   for (; g + 2 < g1; g += 2) {
     load_group<ABITS, NT, WIDE>(rb, wp, mp, mh, xrow, valid, tile_index(nb, g + 1, nbs, G), g + 1, row, c);
+    if (GEMV_SCHED_FENCE && VR == 1) __builtin_amdgcn_sched_barrier(0);
     compute_group<ABITS, VR, CT>(ra, acc, R, row, lane, valid);
     load_group<ABITS, NT, WIDE>(ra, wp, mp, mh, xrow, valid, tile_index(nb, g + 2, nbs, G), g + 2, row, c);
+    if (GEMV_SCHED_FENCE && VR == 1) __builtin_amdgcn_sched_barrier(0);
     compute_group<ABITS, VR, CT>(rb, acc, R, row, lane, valid);
   }
   if (g + 1 < g1) {
