@@ -634,47 +634,107 @@ def step_hash(prev, lg_row):
     return hashlib.sha256(prev.encode() + np.ascontiguousarray(lg_row, np.int64).tobytes()).hexdigest()[:16]
 
 
+class _RowPipe:
+    """Each decode step's logits row (and its sampled id) copied to pinned host memory behind the step on the same
+    stream, two slots in turn: the host hashes step t while the device runs step t + 1. Stream order makes each copy
+    read the decoder's buffers before the next step overwrites them."""
+
+    def __init__(self, V):
+        self.rows = [torch.empty(V, dtype=I64, pin_memory=True) for _ in range(2)]
+        self.ids = [torch.empty(1, dtype=I32, pin_memory=True) for _ in range(2)]
+        self.ev = [torch.cuda.Event(), torch.cuda.Event()]
+
+    def push(self, t, lg_row, ids):
+        k = t % 2
+        self.rows[k].copy_(lg_row, non_blocking=True)
+        self.ids[k].copy_(ids, non_blocking=True)
+        self.ev[k].record()
+
+    def pop(self, t):
+        """(logits row, sampled id) of step t, once its copies have landed"""
+        k = t % 2
+        self.ev[k].synchronize()
+        return self.rows[k].numpy(), int(self.ids[k][0])
+
+
 def generate(tm, prompt_ids, n, seed, temp):
     """Sampled generation with a receipt (exact_llm.generate, exact_llm.py:262-268): the integer sampler runs on
-    the device; each step's logits row comes to the host only for the receipt hash. Uses the KV cache (the
-    reference re-runs the whole sequence per step; the logits are identical by causality).
+    the device and its token stays there as the next step's input (one HIP-graph replay a step); each step's logits
+    row comes to the host only for the receipt hash, copied behind the step and hashed while the next step runs.
+    Uses the KV cache (the reference re-runs the whole sequence per step; the logits are identical by causality).
     Returns (receipt dict, greedy tokens)."""
     tnum = ops.temp_num(temp)
     cache = tm.new_cache(B=1)
-    dev = tm.dev
-    step = torch.zeros(1, dtype=I32, device=dev)
-    ids = torch.zeros(1, dtype=I32, device=dev)
+    step = torch.zeros(1, dtype=I32, device=tm.dev)
     chain, toks, greedy = "start", [], []
     lg = tm.forward(list(prompt_ids), cache, last_only=True)
+    pipe = _RowPipe(lg.shape[1])
+    gd, ids = None, torch.zeros(1, dtype=I32, device=tm.dev)
+    if n > 1:
+        gd = GraphDecoder(tm, cache, 1)
+        gd.load([0])
+        ids = gd.ws.ids            # the sampled token is the next step's input, on the device
     for t in range(n):
+        if t > 0:
+            lg, _ = gd.step()       # consumes ids; its greedy ids are overwritten by the sample below
         step.fill_(t)
         ops.sample(lg, seed, step, tnum, tm.tab.exp, ids)
-        row = lg[0].cpu().numpy()
-        tok = int(ids.cpu()[0])
-        chain = step_hash(chain, row)
-        toks.append(tok)
-        greedy.append(int(row.argmax()))
-        if t + 1 < n:
-            lg, _ = tm.decode_rows([tok], cache)
+        pipe.push(t, lg[0], ids)
+        if t == 0 and gd is not None:
+            gd.capture()            # captured after the first sample: its warm-up step restores ids and positions
+        if t > 0:
+            row, tok = pipe.pop(t - 1)
+            chain = step_hash(chain, row)
+            toks.append(tok)
+            greedy.append(int(row.argmax()))
+    row, tok = pipe.pop(n - 1)
+    chain = step_hash(chain, row)
+    toks.append(tok)
+    greedy.append(int(row.argmax()))
     return dict(prompt=list(prompt_ids), seed=seed, temp=temp, tokens=toks, chain=chain), greedy
 
 
 def verify(tm, receipt):
-    """Recompute a receipt (exact_llm.verify, exact_llm.py:269-276): (ok, first bad position, "chain" or None)."""
+    """Recompute a receipt (exact_llm.verify, exact_llm.py:269-276): (ok, first bad position, "chain" or None). The
+    receipt's own tokens feed the steps (from the device); each step's sample is compared on the host one step
+    behind, and the work queued past a mismatch is discarded."""
     tnum = ops.temp_num(receipt["temp"])
+    rec = list(receipt["tokens"])
+    n = len(rec)
     cache = tm.new_cache(B=1)
     step = torch.zeros(1, dtype=I32, device=tm.dev)
-    ids = torch.zeros(1, dtype=I32, device=tm.dev)
+    samp = torch.zeros(1, dtype=I32, device=tm.dev)
     chain = "start"
     lg = tm.forward(list(receipt["prompt"]), cache, last_only=True)
-    for t, rec in enumerate(receipt["tokens"]):
+    if n == 0:
+        return chain == receipt["chain"], (None if chain == receipt["chain"] else "chain")
+    pipe = _RowPipe(lg.shape[1])
+    gd = None
+    if n > 1:
+        rec_dev = torch.tensor(rec, dtype=I32).to(tm.dev)
+        gd = GraphDecoder(tm, cache, 1)
+        gd.load([rec[0]])
+        gd.capture()
+
+    def check(t):
+        row, tok = pipe.pop(t)
+        return step_hash(chain, row), tok == rec[t]
+
+    for t in range(n):
+        if t > 0:
+            gd.ws.ids.copy_(rec_dev[t - 1:t])
+            lg, _ = gd.step()
         step.fill_(t)
-        ops.sample(lg, receipt["seed"], step, tnum, tm.tab.exp, ids)
-        chain = step_hash(chain, lg[0].cpu().numpy())
-        if int(ids.cpu()[0]) != rec:
-            return False, t
-        if t + 1 < len(receipt["tokens"]):
-            lg, _ = tm.decode_rows([rec], cache)
+        ops.sample(lg, receipt["seed"], step, tnum, tm.tab.exp, samp)
+        pipe.push(t, lg[0], samp)
+        if t > 0:
+            chain, ok = check(t - 1)
+            if not ok:
+                torch.cuda.current_stream().synchronize()
+                return False, t - 1
+    chain, ok = check(n - 1)
+    if not ok:
+        return False, n - 1
     return chain == receipt["chain"], (None if chain == receipt["chain"] else "chain")
 
 

@@ -52,3 +52,22 @@ def test_generate_receipt_matches_oracle_and_verifies():
     bad = dict(rec, tokens=list(rec["tokens"]))
     bad["tokens"][5] = (bad["tokens"][5] + 1) % cfg.V
     assert verify(tm, bad) == (False, 5)
+    # the host checks each step one step behind the device: the first and last positions and the chain itself
+    for pos in (0, 11):
+        bad = dict(rec, tokens=list(rec["tokens"]))
+        bad["tokens"][pos] = (bad["tokens"][pos] + 1) % cfg.V
+        assert verify(tm, bad) == (False, pos)
+    assert verify(tm, dict(rec, chain="0" * 16)) == (False, "chain")
+
+
+@pytest.mark.parametrize("n", [1, 2])
+def test_short_generations_match_oracle(n):
+    """one token (no decode step) and two (one captured step) through the pipelined receipt path"""
+    cfg = synth.CONFIGS["tiny"]
+    om = helpers.oracle_model(cfg, 6, T=32)
+    tm = TModel(DeviceWeights.synthetic(cfg, 6, DEV), Smax=32)
+    prompt = helpers.prompt(3, 5, cfg.V)
+    rec, greedy = generate(tm, prompt, n, seed=7, temp=0.9)
+    orec, ogreedy, _ = O.generate(om, prompt, n, seed=7, temp=0.9)
+    assert rec["tokens"] == orec["tokens"] and rec["chain"] == orec["chain"] and greedy == ogreedy
+    assert verify(tm, rec) == (True, None)
