@@ -186,7 +186,9 @@ __device__ __forceinline__ v4i buf_load16(BufRes r, int voff, int soff) {
 struct QK {
   const int32_t* ckh;    // 128 sum k - 16384 hd per key
   const int32_t* skh;    // sk per key
-  BufRes kdr, ckr, skr;  // buffer views of this KV head's k digits, ckh and skh
+  BufRes kdr;            // buffer view of this KV head's k digits
+  BufRes kcr;            // one view from ckh to the end of skh (the key terms a wave loads one dword a lane)
+  int kcoff;             // the lane's dword in it: ck of key l (l < 32), sk of key l - 32
   const v4i* qd;         // LDS q digits [kb][hi, lo][lane]: B operand, column = query l32, dimensions 32 kb + 16 half + [0, 16)
   // (kb < HD / 32; the callers pass HD as a template parameter)
   int kpad, l32, half, lane;
@@ -203,11 +205,20 @@ struct KCol {
   v4i ck[4], sk[4];
 };
 
-__device__ __forceinline__ void load_kcol(const QK& c, int j0, KCol& k) {
+// The key terms of a tile at one dword a lane (lanes 0..31 ck of keys j0 + l, 32..63 sk of keys j0 + l - 32), put
+// into the lane's own 16 keys through the wave's 256-byte LDS slot: 256 bytes of loads a tile instead of the 8 KiB
+// that 16-byte loads of the lane's own keys take (the two half-waves hold different keys, so every lane of a half
+// loads the same bytes).
+__device__ __forceinline__ int load_kterm(const QK& c, int j0) {
+  return __builtin_amdgcn_raw_buffer_load_b32(c.kcr, c.kcoff, j0 * 4, 0);
+}
+__device__ __forceinline__ void kterm_col(int32_t* slot, int kw, const QK& c, KCol& k) {
+  slot[c.lane] = kw;
+  __builtin_amdgcn_wave_barrier();   // the wave's own LDS write, read back by its other lanes (LDS is in order per wave)
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    k.ck[g] = buf_load16(c.ckr, 16 * c.half, (j0 + 8 * g) * 4);
-    k.sk[g] = buf_load16(c.skr, 16 * c.half, (j0 + 8 * g) * 4);
+    k.ck[g] = *reinterpret_cast<const v4i*>(slot + 8 * g + 4 * c.half);
+    k.sk[g] = *reinterpret_cast<const v4i*>(slot + 32 + 8 * g + 4 * c.half);
   }
 }
 
@@ -393,6 +404,7 @@ __device__ __forceinline__ void scores_i64(const QK& c, int j0, const v16i& hh, 
 struct AttnLDS {
   int32_t* T;
   v4i (*Pl)[AP_PROD][3][64];
+  int32_t* kcl;       // [waves][64]: each wave's key-term slot
   double* red_w;      // [waves][32]
   int64_t* red_a;     // [waves][32]
   int64_t* red_b;     // [waves][32]
@@ -509,14 +521,22 @@ template <int HD, int NW>
 __device__ __forceinline__ void passes12_f64(const QK& c, const AttnLDS& L, const FastCtx& f, int ntile, int firstpos, int w,
                                              double& mx, int64_t& es) {
   double mw = AP_NEG;
-  KTile<HD> kt;   // the next tile's k digits load while this one is finished (its key terms load behind its products)
-  if (w < ntile) load_ktile(c, 32 * w, kt);
+  int32_t* slot = L.kcl + 64 * w;
+  KTile<HD> kt;   // the next tile's k digits and key terms load while this one is finished
+  int kw = 0;
+  if (w < ntile) {
+    load_ktile(c, 32 * w, kt);
+    kw = load_kterm(c, 32 * w);
+  }
   for (int t = w; t < ntile; t += NW) {
     v16i hh, xx, ll;
     KCol kc;
+    kterm_col(slot, kw, c, kc);   // LDS round trip under the products
     mfma_ktile(c, kt, hh, xx, ll);
-    load_kcol(c, 32 * t, kc);   // before the prefetch: the epilogue's wait then leaves the prefetch in flight
-    if (t + NW < ntile) load_ktile(c, 32 * (t + NW), kt);
+    if (t + NW < ntile) {
+      load_ktile(c, 32 * (t + NW), kt);
+      kw = load_kterm(c, 32 * (t + NW));
+    }
     __builtin_amdgcn_sched_barrier(0);
     mw = 32 * t + 31 <= firstpos ? tile_max<false>(c, f, 32 * t, kc, hh, xx, ll, mw) : tile_max<true>(c, f, 32 * t, kc, hh, xx, ll, mw);
   }
@@ -528,13 +548,19 @@ __device__ __forceinline__ void passes12_f64(const QK& c, const AttnLDS& L, cons
   mx = __builtin_floor(mw * f.fscale + 0.5);
   const double mxh = mx - 0.5;
   int64_t e = 0;
-  if (w < ntile) load_ktile(c, 32 * w, kt);
+  if (w < ntile) {
+    load_ktile(c, 32 * w, kt);
+    kw = load_kterm(c, 32 * w);
+  }
   for (int t = w; t < ntile; t += NW) {
     v16i hh, xx, ll;
     KCol kc;
+    kterm_col(slot, kw, c, kc);
     mfma_ktile(c, kt, hh, xx, ll);
-    load_kcol(c, 32 * t, kc);   // before the prefetch: the epilogue's wait then leaves the prefetch in flight
-    if (t + NW < ntile) load_ktile(c, 32 * (t + NW), kt);
+    if (t + NW < ntile) {
+      load_ktile(c, 32 * (t + NW), kt);
+      kw = load_kterm(c, 32 * (t + NW));
+    }
     __builtin_amdgcn_sched_barrier(0);
     e += 32 * t + 31 <= firstpos ? tile_esum<false>(c, f, 32 * t, kc, hh, xx, ll, mxh) : tile_esum<true>(c, f, 32 * t, kc, hh, xx, ll, mxh);
   }
@@ -553,10 +579,11 @@ __device__ __forceinline__ void produce_f64(const QK& c, const AttnLDS& L, const
                                             int w, int lane, double mx, int64_t es) {
   const double es20 = __builtin_ldexp((double)es, -20), res20 = 1048576.0 / (double)es, mxh = mx - 0.5;
   KTile<HD> kt;
-  KCol kc;
+  int kw = 0;
+  int32_t* slot = L.kcl + 64 * w;
   if (w < ntile) {
     load_ktile(c, 32 * w, kt);
-    load_kcol(c, 32 * w, kc);
+    kw = load_kterm(c, 32 * w);
   }
   for (int s = 0; s <= nsteps; ++s) {
     const int t = AP_PROD * s + w;
@@ -564,11 +591,12 @@ __device__ __forceinline__ void produce_f64(const QK& c, const AttnLDS& L, const
       v4i pa[3] = {v4i{}, v4i{}, v4i{}};
       if (t < ntile) {
         v16i hh, xx, ll;
+        KCol cur;
+        kterm_col(slot, kw, c, cur);   // LDS round trip under the products
         mfma_ktile(c, kt, hh, xx, ll);
-        const KCol cur = kc;
         if (t + AP_PROD < ntile) {
           load_ktile(c, 32 * (t + AP_PROD), kt);
-          load_kcol(c, 32 * (t + AP_PROD), kc);
+          kw = load_kterm(c, 32 * (t + AP_PROD));
         }
         __builtin_amdgcn_sched_barrier(0);   // the next tile's loads in flight before this tile's epilogue
         if (32 * t + 31 <= firstpos) tile_pdig<false>(c, f, 32 * t, cur, hh, xx, ll, mxh, es20, res20, pa);
@@ -728,8 +756,11 @@ __device__ __forceinline__ void block_setup(Block& b, int h, int kh, int q0, con
   c.ckh = ck + (int64_t)kh * kpad;
   c.skh = skk + (int64_t)kh * kpad;
   c.kdr = buf_res(kdig + (int64_t)kh * 2 * HD * kpad, (int64_t)2 * HD * kpad);   // 2 digits x HD / 32 blocks x kpad x 32
-  c.ckr = buf_res(c.ckh, (int64_t)kpad * 4);
-  c.skr = buf_res(c.skh, (int64_t)kpad * 4);
+  {
+    const int64_t d = reinterpret_cast<const char*>(c.skh) - reinterpret_cast<const char*>(c.ckh);   // > 0, < 2^31
+    c.kcr = buf_res(c.ckh, d + (int64_t)kpad * 4);
+    c.kcoff = lane < 32 ? 4 * lane : (int)d + 4 * (lane - 32);
+  }
   const int qr = q0 + c.l32 < R ? q0 + c.l32 : R - 1;
   const int qlast = q0 + 31 < R ? q0 + 31 : R - 1;
   const int jmax = max(0, min(pos[qlast], nkeys - 1));       // positions increase with the row
@@ -772,12 +803,13 @@ __global__ __launch_bounds__(64 * AP_SW, 3) void k_attn_stats(const int16_t* __r
   __shared__ v4i Qd[HD / 16][64];
   __shared__ double red_w[AP_SW * 32];
   __shared__ int64_t red_a[AP_SW * 32], red_b[AP_SW * 32];
+  __shared__ __attribute__((aligned(16))) int32_t kcl[AP_SW * 64];
   int h, kh, q0;
   if (!block_item(R, H, KV, h, kh, q0)) return;
   Block b;
   block_setup<HD>(b, h, kh, q0, qq, sq, kdig, ck, skk, part, pos, Tg, T, Qd, R, H, KV, nkeys, kpad, INV);
   const int w = threadIdx.x >> 6;
-  AttnLDS L{T, nullptr, red_w, red_a, red_b};
+  AttnLDS L{T, nullptr, kcl, red_w, red_a, red_b};
   int64_t mx, es;
   if (b.fast) {
     const FastCtx f{T, __builtin_ldexp((double)INV, b.sqv - 32), 256.0 * b.tz, 128 * b.sqs, b.mypos};
@@ -812,6 +844,7 @@ __global__ __launch_bounds__(64 * (AP_PROD + HD / 32)) void k_attn_pv(const int1
   __shared__ v4i Pl[2][AP_PROD][3][64];
   __shared__ v4i Qd[HD / 16][64];
   __shared__ int rowbits[32];
+  __shared__ __attribute__((aligned(16))) int32_t kcl[AP_PROD * 64];
   int h, kh, q0;
   if (!block_item(R, H, KV, h, kh, q0)) return;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -821,7 +854,7 @@ __global__ __launch_bounds__(64 * (AP_PROD + HD / 32)) void k_attn_pv(const int1
   const QK& c = b.c;
   const int row = q0 + c.l32 < R ? q0 + c.l32 : R - 1;
   const int64_t mx = st_mx[(int64_t)h * R + row], es = st_es[(int64_t)h * R + row];
-  AttnLDS L{T, Pl, nullptr, nullptr, nullptr};
+  AttnLDS L{T, Pl, kcl, nullptr, nullptr, nullptr};
   const int nsteps = (b.ntile + AP_PROD - 1) / AP_PROD;
   const int dc = w - AP_PROD;   // consumer: dimensions 32 dc + [0, 32)
   const int vplane = HD * kpad;   // one digit plane: kpad / 32 tiles x 2 halves x hd x 16 bytes
