@@ -330,10 +330,14 @@ class Wave:
                 d = self.vregs(args[0])
                 voff = self.rd(self.vregs(args[1]))[0].astype(np.int64)
                 buf = self.inputs["rsrc"][args[2][2:-1]]
+                soff = int(self.sval(args[3].split()[0]))
                 mo = re.search(r"offset:(\d+)", rest)
                 off = int(mo.group(1)) if mo else 0
                 mem = self.blk.mem[buf]
-                raw = np.stack([mem[int(a) + off:int(a) + off + 16] for a in voff]).view(np.uint32)
+                for a in voff:
+                    if int(a) + soff + off < 0 or int(a) + soff + off + 16 > len(mem):
+                        raise Race(f"wave {self.id} pc {self.pc}: {buf} load out of range {int(a) + soff + off}")
+                raw = np.stack([mem[int(a) + soff + off:int(a) + soff + off + 16] for a in voff]).view(np.uint32)
                 payload = []
                 for k, r in enumerate(d):
                     payload.append((r, raw[:, k].copy()))

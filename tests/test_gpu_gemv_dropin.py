@@ -35,10 +35,11 @@ def closed_form(x, wT, Mg):
 
 
 @pytest.mark.parametrize("N,K", [(1, 128), (63, 256), (65, 384), (300, 1280), (4608, 3584), (1000, 18944),
-                                 (18949, 3584), (2053, 8192), (9001, 1152)])
+                                 (18949, 3584), (2053, 8192), (9001, 1152), (3584, 18944), (2049, 4224)])
 def test_ragged_shapes_and_wrapping_scales(N, K):
     """Shapes that give a wave 1, 2, 4 and 8 rows (the last row block ragged: 18949 = 8 * 2368 + 5), K ranges of 4 KiB
-    and 2 KiB (K >= 8192), and ranges whose last chunk is partly or barely used (3584, 1152)."""
+    and 2 KiB (K >= 8192), and ranges whose last chunk is partly or barely used (3584, 1152); rows of several ranges
+    combine with 64-bit atomics (the 7B down shape 3584 x 18944: 10 ranges; 2049 x 4224: the second range 128 bytes)."""
     rng = np.random.default_rng(N * 7 + K)
     x = rng.integers(-32768, 32768, K).astype(np.int16)
     wT = rng.integers(-128, 128, (N, K)).astype(np.int8)

@@ -90,6 +90,20 @@ def test_prefill_gemm_full_shapes(thr, name, N, K):
         assert np.array_equal(t[:, cols], oracle_t(xq, w[:, cols], Mg[:, cols])), (name, abits, "cols")
 
 
+@pytest.mark.parametrize("M_,N,K", [(2048, 8192, 384), (2000, 8000, 1664), (1024, 36864, 768)])
+def test_multi_round_gemm_whole_output(thr, M_, N, K):
+    """A8 GEMMs of more 256 x 128 tiles than CUs (blocks in several rounds), every output against numpy: 512 tiles
+    of 3 groups, 504 tiles of 13 groups with a ragged last row block and column tile, 1152 tiles of 6."""
+    lin, kw, km = synth_lin(thr, 73, f"ps{N}", N, K)
+    w = synth.weights_np(kw, N, K)
+    Mg = synth.scales_np(km, N, K)
+    xq = rng.integers(-127, 128, (M_, K))
+    print(f"multi-round GEMM {M_} x {N} x {K}", flush=True)
+    t = host(ops.gemm_g128(dev(xq, I8), 7, lin))
+    for c0 in range(0, N, 2048):
+        assert np.array_equal(t[:, c0:c0 + 2048], oracle_t(xq, w[:, c0:c0 + 2048], Mg[:, c0:c0 + 2048])), (M_, N, K, c0)
+
+
 @pytest.mark.parametrize("name,N,K", [("q", 3584, 3584), ("kv", 512, 3584), ("gate", 18944, 3584), ("down", 3584, 18944)])
 @pytest.mark.parametrize("R", [1, 2, 8])
 def test_gemv_7b_shapes(thr, name, N, K, R):
