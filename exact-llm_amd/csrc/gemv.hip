@@ -357,7 +357,7 @@ __device__ __forceinline__ void load_gu_group(GroupRegs& G_, const int8_t* __res
     }
 }
 
-// Gate|up GEMV with the SwiGLU as its epilogue (decode rows, R <= 4, int16 activations). The linear holds the gate rows
+// Gate|up GEMV with the SwiGLU as its epilogue (decode rows, R <= 8, int16 activations). The linear holds the gate rows
 // [0, I) and the up rows [I, 2I), I a multiple of 64. A pair is 32 gate columns (sub-tiles qb, qb + 1 of a 64-row tile)
 // with the matching up columns; block b owns pairs b * NPB .. + NPB with NPB * KS waves: wave w = (pair p = w % NPB,
 // k part kp = w / NPB) runs the group loop over its share of the groups for the pair's gate and up sub-tiles, so one lane
@@ -384,10 +384,10 @@ __global__ __launch_bounds__(64 * NPB * KS) void k_gemv_gu_swiglu(const int16_t*
                                                              const int64_t* __restrict__ gain = nullptr,
                                                              int32_t* __restrict__ s_out = nullptr) {
   __shared__ int64_t cmb[KS > 1 ? (KS - 1) * NPB * 4 * VR * 64 : 1];
-  __shared__ int pm[NPB][4];
+  __shared__ int pm[NPB][8];
   extern __shared__ __attribute__((aligned(16))) int8_t xlds[];   // NE > 0: R rows of K int16 values
   __shared__ RowScratch nsc;
-  __shared__ int32_t s_lds[4];
+  __shared__ int32_t s_lds[8];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int p = wave % NPB, kp = wave / NPB;
   const int pair = blockIdx.x * NPB + p;   // 32 gate columns: sub-tiles qb, qb + 1 of 64-column tile nb
@@ -454,32 +454,38 @@ combine:
           for (int v = 0; v < VR; ++v) acc[j][v] += cmb[((((k - 1) * NPB + p) * 4 + j) * VR + v) * 64 + lane];
   }
   if (kp == 0) {
-    // lane (row, c) holds activation row 4c + v of gate|up column row: rows below R <= 4 sit in the lanes of c = 0
+    // lane (row, c) holds activation row r = 4c + v of gate|up column row: rows below R <= 8 sit in the lanes of
+    // c = 0 and 1; each row's bit length is the maximum over its 16 lanes
     int bl[VR];
 #pragma unroll
     for (int v = 0; v < VR; ++v) {
+      const int r = 4 * c + v;
       bl[v] = 0;
-      if (c == 0 && v < R) {
-        const int sh = 28 - (NE > 0 ? s_lds[v] : s[v]);
+      if (c < 2 && r < R) {
+        const int sh = 28 - (NE > 0 ? s_lds[r] : s[r]);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int i = nb * 64 + 16 * (qb + j) + row;
           const int64_t gt = acc[j][v], ut = acc[2 + j][v];
           const int64_t hv = shr64(lut16(silu, shr64(gt, sh), false) * shr64(ut, sh), EXACT_F);
-          hout[(size_t)v * I + i] = hv;
+          hout[(size_t)r * I + i] = hv;
           if (tout) {
-            tout[(size_t)v * 2 * I + i] = gt;
-            tout[(size_t)v * 2 * I + I + i] = ut;
+            tout[(size_t)r * 2 * I + i] = gt;
+            tout[(size_t)r * 2 * I + I + i] = ut;
           }
           const int b = bitlen64(abs64(hv));
           bl[v] = b > bl[v] ? b : bl[v];
         }
       }
-      bl[v] = wave_max_i32(bl[v]);
-    }
-    if (lane == 0)
 #pragma unroll
-      for (int v = 0; v < VR; ++v) pm[p][v] = bl[v];
+      for (int o = 1; o < 16; o <<= 1) {
+        const int other = __shfl_xor(bl[v], o, 64);
+        bl[v] = other > bl[v] ? other : bl[v];
+      }
+    }
+    if (row == 0 && c < 2)
+#pragma unroll
+      for (int v = 0; v < VR; ++v) pm[p][4 * c + v] = bl[v];
   }
   __syncthreads();
   if ((int)threadIdx.x < R) {
@@ -1190,7 +1196,7 @@ extern "C" int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const 
                                       const int32_t* s, const int32_t* silu, int64_t* h, int32_t* part, int64_t* t,
                                       int32_t R, int32_t I, int32_t K, void* stream) {
   if (!x || !wp || !mp || !s || !silu || !h || !part || R <= 0 || I <= 0 || K <= 0) return EXACT_E_ARG;
-  if (R > 4 || I % 64 || K % 128) return EXACT_E_UNSUPPORTED;
+  if (R > 8 || I % 64 || K % 128) return EXACT_E_UNSUPPORTED;
   if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(wp) & 15)) return EXACT_E_UNSUPPORTED;
   const int G = K / 128;
   dim3 grid((unsigned)(I / (32 * GEMV_GU_NPB))), block(64 * GEMV_GU_NPB * GEMV_GU_KS);

@@ -279,6 +279,7 @@ class TModel:
     # 3584-wide rows that costs as much as the separate launch it saves, at 5120 more, at 896 less: 7.0 vs 8.2 us)
     NORM_FUSE_D = 2048
     NORM_SWIGLU = True   # norm-fused decode: the SwiGLU in the gate|up GEMV's epilogue too
+    BATCH_SWIGLU = True   # decode rows above QROW_FUSE_ROWS: the SwiGLU in the gate|up GEMV's epilogue, then a qrow launch
     QKV_NORM = True   # dense decode rows wider than NORM_FUSE_D: the attention norm inside the q|k|v GEMV
     SHARED_SWIGLU = True   # MoE decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue
     EXPERT_SWIGLU = True   # MoE decode rows: the routed experts' SwiGLU and qrow inside their GEMVs
@@ -350,7 +351,11 @@ class TModel:
         # norm-fused decode rows whose gate|up GEMV also runs the SwiGLU in its epilogue
         nsfuse = (nfuse and self.NORM_SWIGLU and R <= ops.SWIGLU_GEMV_ROWS and c.I % 64 == 0 and D <= ops.NORM_SWIGLU_KMAX
                   and c.I // ops.SWIGLU_PART_COLS <= ops.XQ_PARTS_MAX and self.w.layers[0]["gateup"].bias is None)
-        if xfuse and ws.h is None and (c.I > 8192 or nfuse or sfuse) and not c.moe:
+        # decode rows above QROW_FUSE_ROWS (bs8): the SwiGLU in the gate|up GEMV's epilogue as well, then one qrow launch
+        # over its slice bit lengths before the down GEMV (no gate|up totals, no SwiGLU launch)
+        sqfuse = (self.BATCH_SWIGLU and group and not xfuse and not c.moe and self.abits == 15 and R <= ops.SWIGLU_GEMV_MAX_ROWS
+                  and c.I % 64 == 0 and self.w.layers[0]["gateup"].bias is None)
+        if ws.h is None and not c.moe and ((xfuse and (c.I > 8192 or nfuse or sfuse)) or sqfuse):
             ws.h = torch.zeros((R, ws.I), dtype=I64, device=self.dev)
         x_cur, x_nxt = ws.x, ws.x2
         ops.embed(ws.ids, self.w.emb, ws.x)
@@ -436,6 +441,11 @@ class TModel:
             if sfuse:
                 ops.gemv_swiglu(ws.xq, L["gateup"], ws.s, tab.silu, ws.h, ws.part_sw, t=t_gu if keep else None)
                 ops.gemv_qrow_acc(ws.h, ws.part_sw, c.I // ops.SWIGLU_PART_COLS, self.abits, L["down"], t_d, ws.sh)
+                res_t, res_s = t_d, ws.sh
+            elif sqfuse:
+                ops.gemv_swiglu(ws.xq, L["gateup"], ws.s, tab.silu, ws.h, ws.part_sw, t=t_gu if keep else None)
+                ops.quant_rows(ws.h, ws.part_sw, c.I // ops.SWIGLU_PART_COLS, self.abits, ws.hq, ws.sh, x8=dh)
+                self._lin(ws.hq, L["down"], t_d, x8=dh)
                 res_t, res_s = t_d, ws.sh
             elif group:
                 self._lin(ws.xq, L["gateup"], t_gu, x8=dx)

@@ -144,7 +144,8 @@ def gemv_qrow_acc(xs, part, nparts, abits, lin, out, s_out, K=None, zero=None):
     return out
 
 
-SWIGLU_GEMV_ROWS = 4      # rows of one exact_gemv_g128_swiglu launch
+SWIGLU_GEMV_ROWS = 4      # rows of one exact_gemv_g128_swiglu launch whose h the quantising down GEMV reads
+SWIGLU_GEMV_MAX_ROWS = 8  # rows exact_gemv_g128_swiglu takes
 SWIGLU_PART_COLS = 32     # columns per slice bit length of exact_gemv_g128_swiglu
 XQ_PARTS_MAX = 1024       # slice bit lengths per row that exact_gemv_g128_qrow_acc takes
 

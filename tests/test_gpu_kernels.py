@@ -325,12 +325,14 @@ def test_swiglu_part_then_qrow_gemv_matches_swiglu_qrow(thr):
     assert not host(td).any()
 
 
-@pytest.mark.parametrize("R,I,K", [(1, 18944, 1792), (2, 4864, 896), (4, 13824, 640), (3, 128, 256), (1, 64, 128)])
+@pytest.mark.parametrize("R,I,K", [(1, 18944, 1792), (2, 4864, 896), (4, 13824, 640), (3, 128, 256), (1, 64, 128),
+                                   (8, 1280, 384), (5, 128, 256), (7, 192, 128)])
 def test_gemv_swiglu_matches_oracle(thr, R, I, K):
     """The gate|up GEMV with the SwiGLU in its epilogue: h is the oracle's SwiGLU of the gate|up totals, part the bit
-    length of max |h| per 64 columns, t (when given) the totals; h and part feeding gemv_qrow_acc give the oracle's
+    length of max |h| per 32 columns, t (when given) the totals; h and part feeding gemv_qrow_acc give the oracle's
     qrow shift and down totals. Row shifts s put row 0's gate values inside the SiLU table's +-16 range (interpolated
-    entries) and the last row's far outside it (saturation)."""
+    entries) and the last row's far outside it (saturation). Rows 4 to 7 (R > 4) sit in the second 16-lane group of
+    the matrix-core layout, each with its own bit lengths."""
     from exact_amd.tables import silu_t
     lin, kw, km = synth_lin(thr, 93, f"gu{I}x{K}", 2 * I, K)
     xq = rng.integers(-32767, 32768, (R, K))
@@ -368,11 +370,11 @@ def test_gemv_swiglu_matches_oracle(thr, R, I, K):
 
 
 def test_gemv_swiglu_refuses_unsupported_shapes(thr):
-    """More than 4 rows, or I not a multiple of 64: 'unsupported' (the model keeps the GEMV + SwiGLU launches then)."""
+    """More than 8 rows, or I not a multiple of 64: 'unsupported' (the model keeps the GEMV + SwiGLU launches then)."""
     from exact_amd.tables import silu_t
     lin, _, _ = synth_lin(thr, 95, "gu_bad", 2 * 96, 128)
     st = dev(silu_t(), I32)
-    for R in (5, 1):   # 5 rows; one row of I = 96
+    for R in (9, 1):   # 9 rows; one row of I = 96
         with pytest.raises(ops.ExactError, match="unsupported"):
             ops.gemv_swiglu(dev(np.zeros((R, 128)), I16), lin, dev(np.full(R, 20), I32), st,
                             torch.zeros((R, 96), dtype=I64, device=DEV), torch.zeros(R * 96, dtype=I32, device=DEV))
