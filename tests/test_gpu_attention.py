@@ -119,6 +119,24 @@ def test_row_attention_matches_oracle(R, nkeys):
     assert np.array_equal(host(obits), obits_of(want, H))
 
 
+@pytest.mark.parametrize("R,H,KV,hd,nkeys", [(80, 4, 2, 64, 300), (40, 8, 2, 128, 257), (65, 4, 1, 256, 70),
+                                             (33, 8, 4, 128, 520)])
+def test_row_attention_many_blocks_matches_oracle(R, H, KV, hd, nkeys):
+    """More (row, head) blocks than one round (the batch-decode path, no prefetch), at hd 64, 128 and 256, over caches
+    of 70 to 520 positions with rows at consecutive positions."""
+    Smax, slot = nkeys + 8, 0
+    case = make_case(R * 7 + nkeys, 1, slot, H, KV, hd, Smax, nkeys, R, "large")
+    cache, qq, sq, pos = to_dev(*case)
+    print(f"many-block attention R={R} H={H} hd={hd} nkeys={nkeys}", flush=True)
+    out = torch.full((R, H * hd), -7, dtype=I64, device=DEV)
+    obits = torch.zeros((R, H), dtype=I32, device=DEV)
+    ops.attention(qq, sq, cache, torch.full((R,), slot, dtype=I32, device=DEV), pos,
+                  torch.tensor(exp_t(), dtype=I32, device=DEV), out, H, KV, hd, O.inv_sqrt_hd(hd), obits)
+    want = oracle_rows(*case, slot, H, KV, np.arange(R))
+    assert np.array_equal(host(out), want)
+    assert np.array_equal(host(obits), obits_of(want, H))
+
+
 @pytest.mark.parametrize("H,KV,hd", [(28, 4, 128), (14, 2, 64)])
 def test_prefill_full_size_2048(H, KV, hd):
     """Attention prefill at the 7B shape (28 q heads, 4 KV heads, hd 128) and the 0.5B shape (14, 2, hd 64), 2048
