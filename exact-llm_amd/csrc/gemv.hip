@@ -1123,6 +1123,7 @@ extern "C" int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, con
 #define NORM_EPT(VR)                                                                                                    \
   do {                                                                                                                  \
     if (ept <= 4) NORM_GO(VR, 4);                                                                                       \
+    else if (ept == 7 && bw8) NORM_GO_BW(VR, 7, 8);   /* 3584-wide rows over 512 threads: no padded slots */            \
     else if (ept <= 8) NORM_GO(VR, 8);                                                                                  \
     else if (ept <= 14) NORM_GO(VR, 14);                                                                                \
     else if (ept <= 20) NORM_GO(VR, 20);                                                                                \
