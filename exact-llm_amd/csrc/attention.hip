@@ -112,6 +112,11 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #endif
 // ... with ATT_WIDE_THREADS-thread blocks for heads of at least ATT_KS8_WIDE_HD dimensions when the (row, head) blocks
 // fit one round (7B bs1 decode at a 16-token prompt, A/B: 2.114-2.140 -> 2.101-2.126 ms a step; hd 64 at 0.5B: no gain)
+// ... also for caches of ATT_VPF_LONG_S to 2 ATT_WIDE_THREADS / 8 positions (14B bs1 at a 128-token prompt, A/B:
+// 4.399-4.434 -> 4.367-4.400 ms a step; 7B at 150 tokens 2.183-2.203 -> 2.170-2.189)
+#ifndef ATT_KS8_LONG
+#define ATT_KS8_LONG 1
+#endif
 #ifndef ATT_KS8_WIDE_HD
 #define ATT_KS8_WIDE_HD 128
 #endif
@@ -557,7 +562,12 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
     attr_set = true;
   }
   const size_t lds = (size_t)Smax * 8;
-  if (ATT_WIDE && Smax > ATT_VPF_LONG_S && (int64_t)R * H <= ATT_WIDE_BLOCKS && (2 * ATT_WIDE_THREADS) % hd == 0) {
+  // caches of up to 2 ATT_WIDE_THREADS / 8 positions whose blocks fit one round: 8 threads per cached key (below), also
+  // past ATT_VPF_LONG_S when ATT_KS8_LONG
+  const bool ks8_wide = ATT_KS8 && ATT_KS8_WIDE_HD && hd % 64 == 0 && hd >= ATT_KS8_WIDE_HD && (2 * ATT_WIDE_THREADS) % hd == 0 &&
+                        Smax <= 2 * (ATT_WIDE_THREADS / 8) && (int64_t)R * H <= ATT_WIDE_BLOCKS &&
+                        (Smax <= ATT_VPF_LONG_S || ATT_KS8_LONG);
+  if (ATT_WIDE && !ks8_wide && Smax > ATT_VPF_LONG_S && (int64_t)R * H <= ATT_WIDE_BLOCKS && (2 * ATT_WIDE_THREADS) % hd == 0) {
     static bool wide_set = false;
     if (!wide_set) {
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF_WIDE, ATT_WIDE_THREADS, 0>),
@@ -566,11 +576,10 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
     }
     hipLaunchKernelGGL((k_attention_qkv<ATT_VPF_WIDE, ATT_WIDE_THREADS, 0>), dim3(R, H), dim3(ATT_WIDE_THREADS), lds,
                        as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
-  } else if (Smax > ATT_VPF_LONG_S)
+  } else if (Smax > ATT_VPF_LONG_S && !ks8_wide)
     hipLaunchKernelGGL(k_attention_qkv<ATT_VPF_LONG>, dim3(R, H), dim3(ATT_THREADS), lds, as_stream(stream), t, s, b, cos_t,
                        sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
-  else if (ATT_KS8 && ATT_KS8_WIDE_HD && hd % 64 == 0 && hd >= ATT_KS8_WIDE_HD && (2 * ATT_WIDE_THREADS) % hd == 0 &&
-           Smax <= 2 * (ATT_WIDE_THREADS / 8) && (int64_t)R * H <= ATT_WIDE_BLOCKS)
+  else if (ks8_wide)
     hipLaunchKernelGGL((k_attention_qkv<ATT_VPF, ATT_WIDE_THREADS, ATT_KPF, 8>), dim3(R, H), dim3(ATT_WIDE_THREADS), lds,
                        as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
   else if (ATT_KS8 && hd % 64 == 0 && Smax <= 2 * (ATT_THREADS / 8) && hd < ATT_KS8_WIDE_HD)
