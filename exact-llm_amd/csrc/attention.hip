@@ -117,6 +117,9 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #ifndef ATT_KS8_LONG
 #define ATT_KS8_LONG 1
 #endif
+#ifndef ATT_KS8_LONG4
+#define ATT_KS8_LONG4 1
+#endif
 #ifndef ATT_KS8_WIDE_HD
 #define ATT_KS8_WIDE_HD 128
 #endif
@@ -264,10 +267,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
 // its first ATT_VPF value pairs) is loaded together with t, so the block waits on memory about once before the
 // exp table.
 // KPF: 16-byte chunks of each thread's first cached key loaded with the totals (0: none).
-// KS = 8 (caches of at most 2 NT / 8 positions, hd a multiple of 64): the scores of the cached keys are computed by 8
+// KS = 8 (caches of at most KP NT / 8 positions, hd a multiple of 64): the scores of the cached keys are computed by 8
 // threads per key, hd / 8 dimensions each (coalesced 16-byte loads of the key row, a sum over the 8 lanes), NT / 8 keys
-// per pass and at most two passes, all loaded with the totals; KPF is then unused.
-template <int VPF, int NT = ATT_THREADS, int KPF = ATT_KPF, int KS = 1>
+// per pass and at most KP passes, all loaded with the totals; KPF is then unused.
+template <int VPF, int NT = ATT_THREADS, int KPF = ATT_KPF, int KS = 1, int KP = 2>
 __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
                                                                const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
                                                                const int64_t* __restrict__ sin_t, const int32_t* __restrict__ slot,
@@ -300,20 +303,23 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
   // ---- loads that do not depend on the new token, issued with the totals
   v4i kpre[KPF > 0 && KS == 1 ? KPF : 1];
   int skpre = 0;
-  // KS = 8: thread (key kg = tid / 8, lane kl = tid % 8) holds dims [kl hd / 8, (kl + 1) hd / 8) of keys kg and
-  // kg + NT / 8 (two passes), at most 4 chunks of 16 bytes each
-  v4i ks8[2][4];
-  int sks8[2] = {0, 0};
+  // KS = 8: thread (key kg = tid / 8, lane kl = tid % 8) holds dims [kl hd / 8, (kl + 1) hd / 8) of keys kg,
+  // kg + NT / 8, ... (KP passes), at most 4 chunks of 16 bytes each
+  constexpr int NVC = KP > 2 ? 2 : 4;   // chunks a thread holds per key (the 4-pass variant runs at hd 128 only)
+  v4i ks8[KP][NVC];
+  int sks8[KP];
+#pragma unroll
+  for (int ps = 0; ps < KP; ++ps) sks8[ps] = 0;
   const int kg = tid >> 3, kl = tid & 7;
   if constexpr (KS == 8) {
     const int nv = hd >> 6;   // 16-byte chunks per thread and key
 #pragma unroll
-    for (int ps = 0; ps < 2; ++ps) {
+    for (int ps = 0; ps < KP; ++ps) {
       const int si = kg + ps * (NT / 8);
       if (si < p) {
         const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + si) * hd + kl * (hd >> 3));
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < NVC; ++c)
           if (c < nv) ks8[ps][c] = kr[c];
         sks8[ps] = sk[cbase + si];
       }
@@ -425,12 +431,12 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
   if constexpr (KS == 8) {
     const int nv = hd >> 6;
 #pragma unroll
-    for (int ps = 0; ps < 2; ++ps) {
+    for (int ps = 0; ps < KP; ++ps) {
       const int si = kg + ps * (NT / 8);
       int64_t dot = 0;
       if (si < p) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < NVC; ++c) {
           if (c < nv) {
             const v4i kk = ks8[ps][c], qq = reinterpret_cast<const v4i*>(qs16 + kl * (hd >> 3))[c];
 #pragma unroll
@@ -567,7 +573,19 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
   const bool ks8_wide = ATT_KS8 && ATT_KS8_WIDE_HD && hd % 64 == 0 && hd >= ATT_KS8_WIDE_HD && (2 * ATT_WIDE_THREADS) % hd == 0 &&
                         Smax <= 2 * (ATT_WIDE_THREADS / 8) && (int64_t)R * H <= ATT_WIDE_BLOCKS &&
                         (Smax <= ATT_VPF_LONG_S || ATT_KS8_LONG);
-  if (ATT_WIDE && !ks8_wide && Smax > ATT_VPF_LONG_S && (int64_t)R * H <= ATT_WIDE_BLOCKS && (2 * ATT_WIDE_THREADS) % hd == 0) {
+  // ... and of up to 4 ATT_WIDE_THREADS / 8 positions at hd 128 in four passes
+  const bool ks8_wide4 = !ks8_wide && ATT_KS8 && ATT_KS8_LONG4 && hd == 128 && ATT_KS8_WIDE_HD && hd >= ATT_KS8_WIDE_HD &&
+                         Smax <= 4 * (ATT_WIDE_THREADS / 8) && (int64_t)R * H <= ATT_WIDE_BLOCKS;
+  if (ks8_wide4) {
+    static bool w4_set = false;
+    if (!w4_set) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF, ATT_WIDE_THREADS, ATT_KPF, 8, 4>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
+      w4_set = true;
+    }
+    hipLaunchKernelGGL((k_attention_qkv<ATT_VPF, ATT_WIDE_THREADS, ATT_KPF, 8, 4>), dim3(R, H), dim3(ATT_WIDE_THREADS), lds,
+                       as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
+  } else if (ATT_WIDE && !ks8_wide && Smax > ATT_VPF_LONG_S && (int64_t)R * H <= ATT_WIDE_BLOCKS && (2 * ATT_WIDE_THREADS) % hd == 0) {
     static bool wide_set = false;
     if (!wide_set) {
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF_WIDE, ATT_WIDE_THREADS, 0>),

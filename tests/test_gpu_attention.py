@@ -209,7 +209,8 @@ def test_attention_with_zero_exp_table_gives_zero_rows():
                                                  (14, 2, 64, 3, True, 96), (4, 4, 256, 2, True, 96),
                                                  (8, 2, 128, 2, True, 8192), (16, 16, 128, 1, False, 300),
                                                  (40, 8, 128, 1, True, 200), (14, 2, 64, 2, True, 300),
-                                                 (4, 4, 256, 1, True, 400), (28, 4, 128, 10, True, 96)])
+                                                 (4, 4, 256, 1, True, 400), (28, 4, 128, 10, True, 96),
+                                                 (28, 4, 128, 3, True, 500)])
 def test_fused_qkv_attention_matches_two_launches(H, KV, hd, R, bias, Smax):
     """exact_attention_qkv against exact_qkv_rope_cache + exact_attention (both oracle-pinned above and in the
     model tests): outputs, obits and every cache entry equal; rows in different slots at positions 0, Smax - 1 and
