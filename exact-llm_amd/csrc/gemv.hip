@@ -111,11 +111,36 @@ __device__ __forceinline__ void load_group(GroupRegs& G_, const int8_t* __restri
 // CT: int16 rows without the all-ones row; the caller adds 128 colterm (sum_g colsum_g M_g) once instead, so
 // all 16 A rows carry activations.
 // valid: the lane's A row is an activation row (row < R); other rows are zero, except the all-ones row R.
+// One int16 row (VR = 1, so R = 1): its hi digits, lo digits and (without CT) the all-ones row are A rows 0, 1 and 2 of
+// one MFMA chain, so their products land in C rows 0, 1 and 2, the same lane's three values: half the matrix-core work
+// of the two chains below and no lane exchange for the column sums.
+#ifndef GEMV_R1_PACK
+#define GEMV_R1_PACK 1
+#endif
 template <int ABITS, int VR, bool CT = false>
 __device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc)[4][VR], int R, int row, int lane,
                                               bool valid) {
   const v4i zero = {0, 0, 0, 0};
   const v4i ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+  if constexpr (ABITS == 15 && VR == 1 && GEMV_R1_PACK) {
+    v4i a[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      v4i hi, lo;
+      split_a16(G_.xa[2 * h], G_.xa[2 * h + 1], hi, lo);
+      a[h] = row == 0 ? hi : (row == 1 ? lo : ((!CT && row == 2) ? ones : zero));
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      v4i cc = zero;
+      cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0], G_.b[q], cc, 0, 0, 0);
+      cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[1], G_.b[4 + q], cc, 0, 0, 0);
+      // lanes 0..15 hold C rows 0, 1, 2 of their column in cc[0..2]; the other lanes' rows are never stored
+      const int av = (cc[0] << 8) + cc[1] + (CT ? 0 : 128 * cc[2]);
+      acc[q][0] += (int64_t)av * (int64_t)G_.m[q];
+    }
+    return;
+  }
   v4i ahi[2], alo[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
