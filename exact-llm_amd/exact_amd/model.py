@@ -281,6 +281,7 @@ class TModel:
     NORM_SWIGLU = True   # norm-fused decode: the SwiGLU in the gate|up GEMV's epilogue too
     BATCH_SWIGLU = True   # decode rows above QROW_FUSE_ROWS: the SwiGLU in the gate|up GEMV's epilogue, then a qrow launch
     QKV_NORM = True   # dense decode rows wider than NORM_FUSE_D: the attention norm inside the q|k|v GEMV
+    MOE_NORM = True   # MoE decode rows: the attention norm inside the q|k|v GEMV, the expert norm inside the router GEMV
     SHARED_SWIGLU = True   # MoE decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue
     EXPERT_SWIGLU = True   # MoE decode rows: the routed experts' SwiGLU and qrow inside their GEMVs
     EXPERT_GEMM_MIN_PAIRS = 64   # (row, expert) pairs from which the MoE experts run as one grouped GEMM
@@ -341,9 +342,12 @@ class TModel:
                  and self.w.head.mode == "group")
         # wider dense rows: the attention's residual + RMSNorm + qrow inside the q|k|v GEMV only (8-wave blocks, one per
         # CU, read the row once); the FFN norm stays a launch of its own before the SwiGLU GEMV
-        qfuse = (self.QKV_NORM and group and afuse and not nfuse and self.abits == 15 and not c.moe
+        qfuse = (self.QKV_NORM and group and afuse and not nfuse and self.abits == 15 and (self.MOE_NORM or not c.moe)
                  and R <= ops.NORM_FUSE_ROWS and D <= ops.NORM_FUSE_KMAX
                  and (ops.norm_gemv_one_block_per_cu(self.w.layers[0]["qkv"].N, D, R) or D <= self.NORM_FUSE_D))
+        # MoE decode rows: the residual + RMSNorm + qrow before the experts inside the router GEMV, which also writes the
+        # quantised row the experts read (one launch instead of the norm and the router GEMV)
+        rfuse = (self.MOE_NORM and c.moe and qfuse and self.w.layers[0]["router"].bias is None)
         # decode rows of dense int16 models whose gate|up GEMV is not the norm-fused one: the SwiGLU runs in the gate|up
         # GEMV's epilogue (no totals, no atomics, one launch fewer)
         sfuse = (xfuse and not nfuse and not c.moe and self.abits == 15 and R <= ops.SWIGLU_GEMV_ROWS and c.I % 64 == 0
@@ -428,14 +432,18 @@ class TModel:
             if group:
                 if not xfuse:
                     self._lin(ws.aq, L["o"], t_o, x8=da)
-                ops.rmsnorm_qrow(x_cur, L["g2"], self.abits, t_o, ws.sa, ws.xq, ws.s, clear=clear, x8=dx)
+                if rfuse:   # x_out: the other blocks still read x_cur; t_o is cleared by the shared expert's down GEMV
+                    ops.gemv_norm_acc(x_cur, t_o, ws.sa, L["g2"], L["router"], ws.t_rt, ws.s, x_out=x_nxt, xq_out=ws.xq)
+                    x_cur, x_nxt = x_nxt, x_cur
+                else:
+                    ops.rmsnorm_qrow(x_cur, L["g2"], self.abits, t_o, ws.sa, ws.xq, ws.s, clear=clear, x8=dx)
             else:
                 self._lin_channel(ws.aq, ws.sa, L["o"], ws.t_o)
                 ops.rmsnorm_qrow(ws.x, L["g2"], self.abits, ws.t_o, ws.s28, ws.xq, ws.s)
             if c.moe:
                 if not group:
                     raise ExactError("MoE layers need group-128 linears")
-                self._moe(ws, L, dx, dh)
+                self._moe(ws, L, dx, dh, x=x_cur, routed=rfuse, zero=t_o if rfuse and clear else None)
                 res_t, res_s = None, None
                 continue
             if sfuse:
@@ -504,14 +512,17 @@ class TModel:
             ops.logits_argmax(ws.t_head, ws.s28, ws.logits if want_logits else None, ws.next_ids, part=ws.part_lg)
         return ws
 
-    def _moe(self, ws, L, dx=None, dh=None):
-        """MoE block on m = ws.xq (scale ws.s), added into ws.x (MoEInt.moe, moe_exact_kaggle.py:454-467):
+    def _moe(self, ws, L, dx=None, dh=None, x=None, routed=False, zero=None):
+        """MoE block on m = ws.xq (scale ws.s), added into x (ws.x when None) (MoEInt.moe, moe_exact_kaggle.py:454-467):
         router (with the shared-expert gate logit in the same GEMV) -> isoftmax -> stable top-k -> experts grouped
         into chunks -> SwiGLU per (row, expert) pair -> combination weighted by the Q20 probabilities, plus the
-        isig-gated shared expert."""
+        isig-gated shared expert. routed: the router totals ws.t_rt are already there (the norm-fused router GEMV);
+        zero: an int64 tensor to clear on the way (the shared expert's down GEMV clears it, or a launch of its own)."""
         c, tab, k = self.cfg, self.tab, self.cfg.topk
         P = ws.R * k
-        self._lin(ws.xq, L["router"], ws.t_rt, x8=dx)
+        x = ws.x if x is None else x
+        if not routed:
+            self._lin(ws.xq, L["router"], ws.t_rt, x8=dx)
         ops.router_topk(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, clear=True, NE=c.NE, gate_col=ws.gate_col,
                         sig=tab.sig, gate=ws.gate)
         grouped = P >= self.EXPERT_GEMM_MIN_PAIRS   # prefill: experts on the matrix cores, one tile per 128 pairs
@@ -546,12 +557,15 @@ class TModel:
             if ws.hsh is None:
                 ws.hsh = torch.zeros((ws.R, c.SI), dtype=I64, device=self.dev)
             ops.gemv_swiglu(ws.xq, L["sgu"], ws.s, tab.silu, ws.hsh, ws.part_sw)
-            ops.gemv_qrow_acc(ws.hsh, ws.part_sw, c.SI // ops.SWIGLU_PART_COLS, self.abits, L["sd"], ws.t_sd, ws.ssh)
+            ops.gemv_qrow_acc(ws.hsh, ws.part_sw, c.SI // ops.SWIGLU_PART_COLS, self.abits, L["sd"], ws.t_sd, ws.ssh,
+                              zero=zero)
         else:
             self._lin(ws.xq, L["sgu"], ws.t_sgu, x8=dx)
             ops.swiglu_qrow(ws.t_sgu, ws.s, tab.silu, self.abits, ws.shq, ws.ssh, clear=True, part=ws.part_sw, x8=dh)
             self._lin(ws.shq, L["sd"], ws.t_sd, x8=dh)
-        ops.moe_combine(ws.x, ws.t_ed, ws.esh, ws.p_sel, ws.disp["pidx"], k, ws.t_sd, ws.ssh, ws.gate, clear=True)
+            if zero is not None:
+                ops.zero_(zero)
+        ops.moe_combine(x, ws.t_ed, ws.esh, ws.p_sel, ws.disp["pidx"], k, ws.t_sd, ws.ssh, ws.gate, clear=True)
 
     # ---------------------------------------------------------------- reference-shaped API
     PREFILL_GRAPHS = 8   # captured prefill passes kept (least recently used dropped)
