@@ -171,7 +171,7 @@ NORM_FUSE_KMAX = 256 * 24
 
 
 def norm_gemv_one_block_per_cu(N, K, R=1, cus=0):
-    """True when exact_gemv_g128_norm_acc runs its 8-wave blocks, one per CU (rows wider than 2048 whose group-split
+    """True when exact_gemv_g128_norm_acc runs its 8-wave blocks, one per CU (rows wider than 1024 whose group-split
     tasks fit one round): then each CU normalises the row once. With more tasks every one of its 4-wave blocks
     normalises the row (at 14B's q|k|v, hundreds of blocks of 5120-wide rows: 5.33 against 4.20 ms a decode step).
     The launch takes at most NORM_FUSE_ROWS rows; the split is the library's own (exact_gemv_g128_norm_acc_blockwaves),

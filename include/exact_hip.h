@@ -97,7 +97,7 @@ int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, const int64_t*
                              int32_t* s_out, int16_t* xq_out, int32_t R, int32_t N, int32_t K, void* stream);
 
 /* Waves per block that exact_gemv_g128_norm_acc launches for R rows of an N x K linear on cus compute units (cus <= 0:
- * the current device's): 8 when the rows are wider than 2048 and the group-split tasks fit one round of 8-wave blocks
+ * the current device's): 8 when the rows are wider than 1024 and the group-split tasks fit one round of 8-wave blocks
  * (each CU then normalises the rows once), else 4; 0 for sizes the launch refuses. A host-side query (no launch), so
  * a caller choosing between the fused norm and a separate norm launch reads the kernel's own split. No counterpart in
  * the reference. */
