@@ -570,11 +570,11 @@ extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int
   const size_t lds = (size_t)Smax * 8;
   // caches of up to 2 ATT_WIDE_THREADS / 8 positions whose blocks fit one round: 8 threads per cached key (below), also
   // past ATT_VPF_LONG_S when ATT_KS8_LONG
-  const bool ks8_wide = ATT_KS8 && ATT_KS8_WIDE_HD && hd % 64 == 0 && hd >= ATT_KS8_WIDE_HD && (2 * ATT_WIDE_THREADS) % hd == 0 &&
+  const bool ks8_wide = ATT_KS8 != 0 && ATT_KS8_WIDE_HD != 0 && hd % 64 == 0 && hd >= ATT_KS8_WIDE_HD && (2 * ATT_WIDE_THREADS) % hd == 0 &&
                         Smax <= 2 * (ATT_WIDE_THREADS / 8) && (int64_t)R * H <= ATT_WIDE_BLOCKS &&
                         (Smax <= ATT_VPF_LONG_S || ATT_KS8_LONG);
   // ... and of up to 4 ATT_WIDE_THREADS / 8 positions at hd 128 in four passes
-  const bool ks8_wide4 = !ks8_wide && ATT_KS8 && ATT_KS8_LONG4 && hd == 128 && ATT_KS8_WIDE_HD && hd >= ATT_KS8_WIDE_HD &&
+  const bool ks8_wide4 = !ks8_wide && ATT_KS8 != 0 && ATT_KS8_LONG4 != 0 && hd == 128 && hd >= ATT_KS8_WIDE_HD &&
                          Smax <= 4 * (ATT_WIDE_THREADS / 8) && (int64_t)R * H <= ATT_WIDE_BLOCKS;
   if (ks8_wide4) {
     static bool w4_set = false;

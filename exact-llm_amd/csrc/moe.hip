@@ -11,6 +11,10 @@
 #include "exact_common.h"
 #include "abi_util.h"
 
+#ifndef MOE_WAVE_PATHS
+#define MOE_WAVE_PATHS 1   // routers of at most 64 experts and at most 64 pairs: one-wave kernels
+#endif
+
 namespace exact {
 
 // One block per row of t (row stride ld). The probabilities stay in LDS for the rank computation:
@@ -54,6 +58,76 @@ __global__ void k_router_topk(int64_t* __restrict__ t, int ld, const int32_t* __
       e_sel[(int64_t)r * k + rank] = i;
     }
   }
+}
+
+// Routers of at most 64 experts (decode rows): one wave per row, expert i in lane i. The same steps as k_router_topk
+// with wave reductions, and the rank of lane i from the other lanes' probabilities read as scalars, one per step.
+__global__ __launch_bounds__(64) void k_router_topk_w(int64_t* __restrict__ t, int ld, const int32_t* __restrict__ s,
+                                                      const int32_t* __restrict__ T, int64_t* __restrict__ p_sel,
+                                                      int32_t* __restrict__ e_sel, int gate_col, const int32_t* __restrict__ sig_t,
+                                                      int64_t* __restrict__ gate, int NE, int k, int clear_t) {
+  const int r = blockIdx.x, lane = threadIdx.x;
+  const int sh = 28 - s[r];
+  int64_t* tr = t + (int64_t)r * ld;
+  if (gate_col >= 0 && lane == 0) {
+    gate[r] = lut16(sig_t, shr64(tr[gate_col], sh), true);
+    if (clear_t) tr[gate_col] = 0;
+  }
+  const bool in = lane < NE;
+  const int64_t y = in ? shr64(tr[in ? lane : 0], sh) : INT64_MIN;
+  if (in && clear_t) tr[lane] = 0;
+  const int64_t mx = wave_max64(y);
+  const int64_t e = in ? lut_exp(T, mx - y) : 0;
+  const int64_t es = wave_sum64(e);
+  const int64_t p = in ? floordiv_pos(shl64(e, 20), es) : -1;   // probabilities are >= 0: lanes past NE rank last
+  int rank = 0;
+  for (int j = 0; j < NE; ++j) {
+    const int64_t pj = readlane64(p, j);
+    rank += (pj > p) || (pj == p && j < lane);
+  }
+  if (in && rank < k) {
+    p_sel[(int64_t)r * k + rank] = p;
+    e_sel[(int64_t)r * k + rank] = lane;
+  }
+}
+
+// At most 64 pairs (decode rows): one wave, pair q in lane q. Its place in the stable order by (expert, q) counts the
+// pairs before it; a pair whose index inside its expert is a multiple of CH starts a chunk, and the chunk's index
+// counts the starts placed before it, which orders the chunks by expert and then position, as k_moe_dispatch does.
+__global__ __launch_bounds__(64) void k_moe_dispatch_w(const int32_t* __restrict__ e_sel, const int32_t* __restrict__ s,
+                                                       int32_t* __restrict__ pidx, int32_t* __restrict__ pair_row,
+                                                       int32_t* __restrict__ s_pair, int32_t* __restrict__ chunk_e,
+                                                       int32_t* __restrict__ chunk_p0, int32_t* __restrict__ chunk_n,
+                                                       int32_t* __restrict__ nchunks, int P, int k, int CH) {
+  const int lane = threadIdx.x;
+  const bool in = lane < P;
+  const int e = in ? e_sel[lane] : 0x7fffffff;
+  int pos = 0, first = 0, cnt = 0;
+  for (int j = 0; j < P; ++j) {
+    const int ej = __builtin_amdgcn_readlane(e, j);
+    pos += (ej < e) || (ej == e && j < lane);
+    first += ej < e;
+    cnt += ej == e;
+  }
+  const int idx = pos - first;   // place inside the expert's pairs
+  const bool start = in && idx % CH == 0;
+  const uint64_t starts = __ballot(start);
+  int cidx = 0;
+  for (int j = 0; j < P; ++j) {
+    const int pj = __builtin_amdgcn_readlane(pos, j);
+    cidx += (int)((starts >> j) & 1) & (pj < pos ? 1 : 0);
+  }
+  if (in) {
+    pidx[lane] = pos;
+    pair_row[pos] = lane / k;
+    s_pair[pos] = s[lane / k];
+  }
+  if (start) {
+    chunk_e[cidx] = e;
+    chunk_p0[cidx] = pos;
+    chunk_n[cidx] = cnt - idx < CH ? cnt - idx : CH;
+  }
+  if (lane == 0) nchunks[0] = __popcll(starts);
 }
 
 // One block of 16 waves. Pair q = r * k + j. Wave w owns experts e = w, w + 16, ...: it walks the pairs 64 at a
@@ -193,6 +267,11 @@ extern "C" int exact_router_topk(int64_t* t, int32_t ld, const int32_t* s, const
   if (!t || !s || !exp_t || !p_sel || !e_sel || R <= 0 || NE <= 0 || k <= 0 || k > NE || ld < NE) return EXACT_E_ARG;
   if (gate_col >= 0 && (gate_col >= ld || (gate_col < NE) || !sig_t || !gate)) return EXACT_E_ARG;
   if (NE > 4096) return EXACT_E_UNSUPPORTED;
+  if (MOE_WAVE_PATHS && NE <= 64) {
+    hipLaunchKernelGGL(k_router_topk_w, dim3(R), dim3(64), 0, as_stream(stream), t, ld, s, exp_t, p_sel, e_sel, gate_col, sig_t,
+                       gate, NE, k, clear_t);
+    return launch_status("router_topk");
+  }
   hipLaunchKernelGGL(k_router_topk, dim3(R), dim3(256), NE * sizeof(int64_t), as_stream(stream), t, ld, s, exp_t, p_sel, e_sel,
                      gate_col, sig_t, gate, NE, k, clear_t);
   return launch_status("router_topk");
@@ -204,6 +283,11 @@ extern "C" int exact_moe_dispatch(const int32_t* e_sel, const int32_t* s, int32_
   if (!e_sel || !s || !pidx || !pair_row || !s_pair || !chunk_e || !chunk_p0 || !chunk_n || !nchunks) return EXACT_E_ARG;
   if (R <= 0 || NE <= 0 || k <= 0 || k > NE || chunk_rows <= 0) return EXACT_E_ARG;
   const int64_t P = (int64_t)R * k;
+  if (MOE_WAVE_PATHS && P <= 64) {
+    hipLaunchKernelGGL(k_moe_dispatch_w, dim3(1), dim3(64), 0, as_stream(stream), e_sel, s, pidx, pair_row, s_pair, chunk_e,
+                       chunk_p0, chunk_n, nchunks, (int)P, k, chunk_rows);
+    return launch_status("moe_dispatch");
+  }
   if (P + 3LL * NE + R > 16384) return EXACT_E_UNSUPPORTED;   // 64 KiB of LDS
   hipLaunchKernelGGL(k_moe_dispatch, dim3(1), dim3(1024), (size_t)(P + 3 * NE + R) * sizeof(int32_t), as_stream(stream), e_sel,
                      s, pidx, pair_row, s_pair, chunk_e, chunk_p0, chunk_n, nchunks, (int)P, NE, k, chunk_rows);

@@ -29,8 +29,9 @@ def tab():
     return DeviceTables(DEV, 16, 64, 1e4)
 
 
-@pytest.mark.parametrize("R,NE,k", [(1, 60, 4), (8, 60, 4), (37, 6, 2), (5, 64, 8)])
+@pytest.mark.parametrize("R,NE,k", [(1, 60, 4), (8, 60, 4), (37, 6, 2), (5, 64, 8), (3, 100, 6)])
 def test_router_topk_matches_oracle(tab, R, NE, k):
+    """Routers of up to 64 experts run one wave per row, wider ones a block (100 experts)."""
     rng = np.random.default_rng(R * 100 + NE)
     t = rng.integers(-(1 << 40), 1 << 40, (R, NE))
     # ties: copies of one logit inside a row, so equal probabilities must resolve to the lower index
@@ -58,8 +59,9 @@ def test_router_topk_matches_oracle(tab, R, NE, k):
 
 
 @pytest.mark.parametrize("R,NE,k,ch", [(1, 60, 4, 15), (8, 60, 4, 15), (256, 60, 4, 15), (40, 6, 2, 16), (2048, 4, 2, 15),
-                                      (100, 130, 8, 16), (2048, 60, 4, 128), (333, 60, 4, 256)])
+                                      (100, 130, 8, 16), (2048, 60, 4, 128), (333, 60, 4, 256), (16, 4, 2, 3), (32, 2, 2, 5)])
 def test_dispatch_groups_pairs_by_expert(R, NE, k, ch):
+    """Up to 64 pairs run one wave (experts with several chunks at 16 x 2 and 32 x 2 pairs), more a block of 16."""
     rng = np.random.default_rng(R + NE)
     e_sel = np.stack([rng.choice(NE, k, replace=False) for _ in range(R)])
     s = rng.integers(0, 30, R)
