@@ -62,11 +62,11 @@ __global__ void k_router_topk(int64_t* __restrict__ t, int ld, const int32_t* __
 
 // Routers of at most 64 experts (decode rows): one wave per row, expert i in lane i. The same steps as k_router_topk
 // with wave reductions, and the rank of lane i from the other lanes' probabilities read as scalars, one per step.
-__global__ __launch_bounds__(64) void k_router_topk_w(int64_t* __restrict__ t, int ld, const int32_t* __restrict__ s,
-                                                      const int32_t* __restrict__ T, int64_t* __restrict__ p_sel,
-                                                      int32_t* __restrict__ e_sel, int gate_col, const int32_t* __restrict__ sig_t,
-                                                      int64_t* __restrict__ gate, int NE, int k, int clear_t) {
-  const int r = blockIdx.x, lane = threadIdx.x;
+// Returns the lane's rank (k or more when not selected).
+__device__ __forceinline__ int route_row_w(int64_t* __restrict__ t, int ld, const int32_t* __restrict__ s,
+                                           const int32_t* __restrict__ T, int64_t* __restrict__ p_sel,
+                                           int32_t* __restrict__ e_sel, int gate_col, const int32_t* __restrict__ sig_t,
+                                           int64_t* __restrict__ gate, int NE, int k, int clear_t, int r, int lane) {
   const int sh = 28 - s[r];
   int64_t* tr = t + (int64_t)r * ld;
   if (gate_col >= 0 && lane == 0) {
@@ -85,23 +85,31 @@ __global__ __launch_bounds__(64) void k_router_topk_w(int64_t* __restrict__ t, i
     const int64_t pj = readlane64(p, j);
     rank += (pj > p) || (pj == p && j < lane);
   }
-  if (in && rank < k) {
+  if (!in) rank = k;
+  if (rank < k) {
     p_sel[(int64_t)r * k + rank] = p;
     e_sel[(int64_t)r * k + rank] = lane;
   }
+  return rank;
 }
 
-// At most 64 pairs (decode rows): one wave, pair q in lane q. Its place in the stable order by (expert, q) counts the
-// pairs before it; a pair whose index inside its expert is a multiple of CH starts a chunk, and the chunk's index
-// counts the starts placed before it, which orders the chunks by expert and then position, as k_moe_dispatch does.
-__global__ __launch_bounds__(64) void k_moe_dispatch_w(const int32_t* __restrict__ e_sel, const int32_t* __restrict__ s,
-                                                       int32_t* __restrict__ pidx, int32_t* __restrict__ pair_row,
-                                                       int32_t* __restrict__ s_pair, int32_t* __restrict__ chunk_e,
-                                                       int32_t* __restrict__ chunk_p0, int32_t* __restrict__ chunk_n,
-                                                       int32_t* __restrict__ nchunks, int P, int k, int CH) {
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(64) void k_router_topk_w(int64_t* __restrict__ t, int ld, const int32_t* __restrict__ s,
+                                                      const int32_t* __restrict__ T, int64_t* __restrict__ p_sel,
+                                                      int32_t* __restrict__ e_sel, int gate_col, const int32_t* __restrict__ sig_t,
+                                                      int64_t* __restrict__ gate, int NE, int k, int clear_t) {
+  route_row_w(t, ld, s, T, p_sel, e_sel, gate_col, sig_t, gate, NE, k, clear_t, blockIdx.x, threadIdx.x);
+}
+
+// At most 64 pairs (decode rows): one wave, pair q in lane q (expert e, e past the pairs for lanes >= P). Its place in
+// the stable order by (expert, q) counts the pairs before it; a pair whose index inside its expert is a multiple of CH
+// starts a chunk, and the chunk's index counts the starts placed before it, which orders the chunks by expert and then
+// position, as k_moe_dispatch does.
+__device__ __forceinline__ void dispatch_w(int e, const int32_t* __restrict__ s, int32_t* __restrict__ pidx,
+                                           int32_t* __restrict__ pair_row, int32_t* __restrict__ s_pair,
+                                           int32_t* __restrict__ chunk_e, int32_t* __restrict__ chunk_p0,
+                                           int32_t* __restrict__ chunk_n, int32_t* __restrict__ nchunks, int P, int k, int CH,
+                                           int lane) {
   const bool in = lane < P;
-  const int e = in ? e_sel[lane] : 0x7fffffff;
   int pos = 0, first = 0, cnt = 0;
   for (int j = 0; j < P; ++j) {
     const int ej = __builtin_amdgcn_readlane(e, j);
@@ -128,6 +136,37 @@ __global__ __launch_bounds__(64) void k_moe_dispatch_w(const int32_t* __restrict
     chunk_n[cidx] = cnt - idx < CH ? cnt - idx : CH;
   }
   if (lane == 0) nchunks[0] = __popcll(starts);
+}
+
+__global__ __launch_bounds__(64) void k_moe_dispatch_w(const int32_t* __restrict__ e_sel, const int32_t* __restrict__ s,
+                                                       int32_t* __restrict__ pidx, int32_t* __restrict__ pair_row,
+                                                       int32_t* __restrict__ s_pair, int32_t* __restrict__ chunk_e,
+                                                       int32_t* __restrict__ chunk_p0, int32_t* __restrict__ chunk_n,
+                                                       int32_t* __restrict__ nchunks, int P, int k, int CH) {
+  const int lane = threadIdx.x;
+  const int e = lane < P ? e_sel[lane] : 0x7fffffff;
+  dispatch_w(e, s, pidx, pair_row, s_pair, chunk_e, chunk_p0, chunk_n, nchunks, P, k, CH, lane);
+}
+
+// Decode rows (at most 64 experts, at most 64 pairs): the top-k of every row, then the dispatch of their pairs, in one
+// wave; the selected experts reach the dispatch through LDS (pair r k + rank of row r is the lane of that rank).
+__global__ __launch_bounds__(64) void k_moe_route_w(int64_t* __restrict__ t, int ld, const int32_t* __restrict__ s,
+                                                    const int32_t* __restrict__ T, int64_t* __restrict__ p_sel,
+                                                    int32_t* __restrict__ e_sel, int gate_col, const int32_t* __restrict__ sig_t,
+                                                    int64_t* __restrict__ gate, int NE, int k, int clear_t, int R,
+                                                    int32_t* __restrict__ pidx, int32_t* __restrict__ pair_row,
+                                                    int32_t* __restrict__ s_pair, int32_t* __restrict__ chunk_e,
+                                                    int32_t* __restrict__ chunk_p0, int32_t* __restrict__ chunk_n,
+                                                    int32_t* __restrict__ nchunks, int CH) {
+  __shared__ int32_t es[64];
+  const int lane = threadIdx.x;
+  for (int r = 0; r < R; ++r) {
+    const int rank = route_row_w(t, ld, s, T, p_sel, e_sel, gate_col, sig_t, gate, NE, k, clear_t, r, lane);
+    if (rank < k) es[r * k + rank] = lane;
+  }
+  __syncthreads();
+  const int P = R * k;
+  dispatch_w(lane < P ? es[lane] : 0x7fffffff, s, pidx, pair_row, s_pair, chunk_e, chunk_p0, chunk_n, nchunks, P, k, CH, lane);
 }
 
 // One block of 16 waves. Pair q = r * k + j. Wave w owns experts e = w, w + 16, ...: it walks the pairs 64 at a
@@ -292,6 +331,19 @@ extern "C" int exact_moe_dispatch(const int32_t* e_sel, const int32_t* s, int32_
   hipLaunchKernelGGL(k_moe_dispatch, dim3(1), dim3(1024), (size_t)(P + 3 * NE + R) * sizeof(int32_t), as_stream(stream), e_sel,
                      s, pidx, pair_row, s_pair, chunk_e, chunk_p0, chunk_n, nchunks, (int)P, NE, k, chunk_rows);
   return launch_status("moe_dispatch");
+}
+
+extern "C" int exact_moe_route(int64_t* t, int32_t ld, const int32_t* s, const int32_t* exp_t, int64_t* p_sel, int32_t* e_sel,
+                               int32_t gate_col, const int32_t* sig_t, int64_t* gate, int32_t R, int32_t NE, int32_t k,
+                               int32_t clear_t, int32_t* pidx, int32_t* pair_row, int32_t* s_pair, int32_t* chunk_e,
+                               int32_t* chunk_p0, int32_t* chunk_n, int32_t* nchunks, int32_t chunk_rows, void* stream) {
+  if (!t || !s || !exp_t || !p_sel || !e_sel || R <= 0 || NE <= 0 || k <= 0 || k > NE || ld < NE) return EXACT_E_ARG;
+  if (gate_col >= 0 && (gate_col >= ld || (gate_col < NE) || !sig_t || !gate)) return EXACT_E_ARG;
+  if (!pidx || !pair_row || !s_pair || !chunk_e || !chunk_p0 || !chunk_n || !nchunks || chunk_rows <= 0) return EXACT_E_ARG;
+  if (NE > 64 || (int64_t)R * k > 64) return EXACT_E_UNSUPPORTED;   // one wave: an expert a lane, a pair a lane
+  hipLaunchKernelGGL(k_moe_route_w, dim3(1), dim3(64), 0, as_stream(stream), t, ld, s, exp_t, p_sel, e_sel, gate_col, sig_t,
+                     gate, NE, k, clear_t, R, pidx, pair_row, s_pair, chunk_e, chunk_p0, chunk_n, nchunks, chunk_rows);
+  return launch_status("moe_route");
 }
 
 extern "C" int exact_moe_combine(int64_t* x, int64_t* t_ed, const int32_t* sh_pair, const int64_t* p_sel, const int32_t* pidx,

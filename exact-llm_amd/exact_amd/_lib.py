@@ -56,6 +56,7 @@ SIGNATURES = {
     "exact_sample": [P, I32, I32, U64, P, I64, P, P, P, P],
     "exact_router_topk": [P, I32, P, P, P, P, I32, P, P, I32, I32, I32, I32, P],
     "exact_moe_dispatch": [P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, P],
+    "exact_moe_route": [P, I32, P, P, P, P, I32, P, P, I32, I32, I32, I32, P, P, P, P, P, P, P, I32, P],
     "exact_gemv_g128_experts": [P, I32, P, P, P, I64, I64, P, P, P, P, I32, P, I32, I32, P],
     "exact_gemm_g128_experts": [P, I32, P, P, P, I64, I64, P, P, P, P, P, P, I32, P, I32, I32, I32, P],
     "exact_gemv_g128_experts_swiglu": [P, P, P, P, I64, I64, P, P, P, P, I32, I32, P, P, P, P, I32, I32, P],

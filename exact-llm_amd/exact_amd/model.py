@@ -282,6 +282,7 @@ class TModel:
     BATCH_SWIGLU = True   # decode rows above QROW_FUSE_ROWS: the SwiGLU in the gate|up GEMV's epilogue, then a qrow launch
     QKV_NORM = True   # dense decode rows wider than NORM_FUSE_D: the attention norm inside the q|k|v GEMV
     MOE_NORM = True   # MoE decode rows: the attention norm inside the q|k|v GEMV, the expert norm inside the router GEMV
+    MOE_ROUTE = True   # MoE decode rows: top-k routing and dispatch in one launch
     SHARED_SWIGLU = True   # MoE decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue
     EXPERT_SWIGLU = True   # MoE decode rows: the routed experts' SwiGLU and qrow inside their GEMVs
     EXPERT_GEMM_MIN_PAIRS = 64   # (row, expert) pairs from which the MoE experts run as one grouped GEMM
@@ -523,15 +524,19 @@ class TModel:
         x = ws.x if x is None else x
         if not routed:
             self._lin(ws.xq, L["router"], ws.t_rt, x8=dx)
-        ops.router_topk(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, clear=True, NE=c.NE, gate_col=ws.gate_col,
-                        sig=tab.sig, gate=ws.gate)
         grouped = P >= self.EXPERT_GEMM_MIN_PAIRS   # prefill: experts on the matrix cores, one tile per 128 pairs
         # decode: the SwiGLU in the expert gate|up GEMV's epilogue and the qrow in the expert down GEMV (chunks of 4 pairs)
         efuse = (self.EXPERT_SWIGLU and not grouped and self.abits == 15 and c.MI % 64 == 0
                  and c.MI // ops.SWIGLU_PART_COLS <= ops.XQ_PARTS_MAX)
         chunk = (ops.EXPERT_CHUNK[self.abits] if grouped else
                  ops.EXPERT_FUSE_CHUNK if efuse else ops.chunk_rows(self.abits))
-        ops.moe_dispatch(ws.e_sel, ws.s, c.NE, k, chunk, ws.disp)
+        if self.MOE_ROUTE and c.NE <= ops.ROUTE_MAX and P <= ops.ROUTE_MAX:   # top-k and dispatch in one wave
+            ops.moe_route(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, chunk, ws.disp, clear=True, NE=c.NE,
+                          gate_col=ws.gate_col, sig=tab.sig, gate=ws.gate)
+        else:
+            ops.router_topk(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, clear=True, NE=c.NE, gate_col=ws.gate_col,
+                            sig=tab.sig, gate=ws.gate)
+            ops.moe_dispatch(ws.e_sel, ws.s, c.NE, k, chunk, ws.disp)
         if efuse:
             if ws.eh is None:
                 ws.eh = torch.zeros((P, c.MI), dtype=I64, device=self.dev)

@@ -579,6 +579,24 @@ def moe_dispatch(e_sel, s, NE, k, chunk, out):
     return out
 
 
+ROUTE_MAX = 64   # experts and (row, expert) pairs of one moe_route launch
+
+
+def moe_route(t, s, expt, k, p_sel, e_sel, chunk, out, clear=False, NE=None, gate_col=-1, sig=None, gate=None):
+    """router_topk then moe_dispatch in one launch (decode rows: at most ROUTE_MAX experts and pairs)."""
+    R, ld = t.shape
+    NE = ld if NE is None else NE
+    need = max_chunks(R * k, NE, chunk)
+    for n in ("chunk_e", "chunk_p0", "chunk_n"):
+        _need(out[n], I32, n, need)
+    _lib.call("exact_moe_route", _ptr(_need(t, I64, "t")), ld, _ptr(_need(s, I32, "s", R)), _ptr(expt),
+              _ptr(_need(p_sel, I64, "p_sel", R * k)), _ptr(_need(e_sel, I32, "e_sel", R * k)), gate_col, _ptr(sig),
+              _ptr(gate), R, NE, k, int(clear),
+              *(_ptr(_need(out[n], I32, n)) for n in ("pidx", "pair_row", "s_pair", "chunk_e", "chunk_p0", "chunk_n",
+                                                       "nchunks")), chunk, _stream())
+    return p_sel, e_sel, out
+
+
 def gemv_experts(x, abits, row_map, lin, disp, out):
     """out[p] += x[row_map[p]] . W_{expert of p} for the dispatched chunks (row_map None: x row p)."""
     _need(x, I16 if abits == 15 else I8, "x")

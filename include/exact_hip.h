@@ -309,6 +309,15 @@ int exact_moe_dispatch(const int32_t* e_sel, const int32_t* s, int32_t* pidx, in
                        int32_t* chunk_e, int32_t* chunk_p0, int32_t* chunk_n, int32_t* nchunks, int32_t R,
                        int32_t NE, int32_t k, int32_t chunk_rows, void* stream);
 
+/* Decode rows: exact_router_topk followed by exact_moe_dispatch in one launch (one wave), with the same arguments and
+ * outputs as the two. No counterpart in the reference (its router and its per-expert loop are separate steps,
+ * moe_exact_kaggle.py:456-463); for routers of at most 64 experts and at most 64 (row, expert) pairs, otherwise
+ * EXACT_E_UNSUPPORTED (call the two entry points). */
+int exact_moe_route(int64_t* t, int32_t ld, const int32_t* s, const int32_t* exp_t, int64_t* p_sel, int32_t* e_sel,
+                    int32_t gate_col, const int32_t* sig_t, int64_t* gate, int32_t R, int32_t NE, int32_t k, int32_t clear_t,
+                    int32_t* pidx, int32_t* pair_row, int32_t* s_pair, int32_t* chunk_e, int32_t* chunk_p0, int32_t* chunk_n,
+                    int32_t* nchunks, int32_t chunk_rows, void* stream);
+
 /* Expert GEMV: for every chunk, t[p] += x[row_map ? row_map[p] : p] . W_e for its pairs p, with expert e's
  * packed linear at wp + e*w_stride, mp + e*m_stride (bytes / int16 elements). chunk_n <= 15 (abits 15) or
  * 16 (abits 7). The per-expert gate/up and down linears of MoEInt.moe (moe_exact_kaggle.py:461-462). */

@@ -90,6 +90,65 @@ def test_dispatch_groups_pairs_by_expert(R, NE, k, ch):
     assert (covered == 1).all()
 
 
+@pytest.mark.parametrize("R,NE,k,ch", [(1, 60, 4, 4), (2, 60, 4, 15), (16, 4, 2, 3), (8, 64, 8, 5), (3, 7, 2, 1)])
+def test_moe_route_matches_topk_and_dispatch(tab, R, NE, k, ch):
+    """exact_moe_route (top-k and dispatch of decode rows in one wave): the oracle's top-k (ties to the lower expert),
+    the gate and the cleared totals, the dispatch's stable grouping and chunks, and every output equal to
+    exact_router_topk + exact_moe_dispatch; more than 64 experts or pairs are refused."""
+    rng = np.random.default_rng(R * 7 + NE)
+    t = rng.integers(-(1 << 40), 1 << 40, (R, NE))
+    t[:, NE // 2] = t[:, 1]                              # ties inside a row
+    if R > 1:
+        t[1] = t[1, 0]                                   # an all-equal row
+    s = rng.integers(0, 20, R)
+    gcol = -(-NE // 64) * 64
+    tfull = np.zeros((R, gcol + 1), np.int64)
+    tfull[:, :NE], tfull[:, gcol] = t, rng.integers(-(1 << 44), 1 << 44, R)
+    P, nmax = R * k, ops.max_chunks(R * k, NE, ch)
+
+    def run(fused):
+        td = dev(tfull, I64)
+        p_sel, e_sel = torch.zeros((R, k), dtype=I64, device=DEV), torch.zeros((R, k), dtype=I32, device=DEV)
+        gate = torch.zeros(R, dtype=I64, device=DEV)
+        out = {n: torch.full((P,), -1, dtype=I32, device=DEV) for n in ("pidx", "pair_row", "s_pair")}
+        out.update({n: torch.full((nmax,), -1, dtype=I32, device=DEV) for n in ("chunk_e", "chunk_p0", "chunk_n")})
+        out["nchunks"] = torch.zeros(1, dtype=I32, device=DEV)
+        if fused:
+            ops.moe_route(td, dev(s, I32), tab.exp, k, p_sel, e_sel, ch, out, clear=True, NE=NE, gate_col=gcol,
+                          sig=tab.sig, gate=gate)
+        else:
+            ops.router_topk(td, dev(s, I32), tab.exp, k, p_sel, e_sel, clear=True, NE=NE, gate_col=gcol, sig=tab.sig,
+                            gate=gate)
+            ops.moe_dispatch(e_sel, dev(s, I32), NE, k, ch, out)
+        return {"td": host(td), "p_sel": host(p_sel), "e_sel": host(e_sel), "gate": host(gate),
+                **{n: host(v) for n, v in out.items()}}
+
+    got, sep = run(True), run(False)
+    for n in got:
+        assert np.array_equal(got[n], sep[n]), n
+    p = O.isoftmax(O.round_shift(t, (28 - s)[:, None]), np.ones((R, NE), bool))
+    sel = np.argsort(-p, axis=-1, kind="stable")[:, :k]
+    assert np.array_equal(got["e_sel"], sel) and np.array_equal(got["p_sel"], np.take_along_axis(p, sel, -1))
+    assert not got["td"].any()
+    q = np.arange(P)
+    order = np.lexsort((q, sel.reshape(-1)))
+    assert np.array_equal(got["pidx"][order], q)
+    n = int(got["nchunks"][0])
+    covered = np.zeros(P, int)
+    for c in range(n):
+        e, p0, cnt = got["chunk_e"][c], got["chunk_p0"][c], got["chunk_n"][c]
+        assert 1 <= cnt <= ch and (sel.reshape(-1)[order[p0:p0 + cnt]] == e).all()
+        covered[p0:p0 + cnt] += 1
+    assert (covered == 1).all()
+    if NE == 64:
+        bad = torch.zeros((1, 65), dtype=I64, device=DEV)
+        with pytest.raises(ops.ExactError, match="unsupported"):
+            ops.moe_route(bad, dev(s[:1], I32), tab.exp, k, torch.zeros(k, dtype=I64, device=DEV),
+                          torch.zeros(k, dtype=I32, device=DEV), ch,
+                          {nm: torch.zeros(64, dtype=I32, device=DEV) for nm in
+                           ("pidx", "pair_row", "s_pair", "chunk_e", "chunk_p0", "chunk_n", "nchunks")}, NE=65)
+
+
 @pytest.mark.parametrize("abits", [15, 7])
 @pytest.mark.parametrize("R,NE,k,N,K", [(1, 60, 4, 2816, 2048), (8, 60, 4, 2048, 1408), (50, 6, 2, 384, 256)])
 def test_expert_gemv_matches_oracle(abits, R, NE, k, N, K):
