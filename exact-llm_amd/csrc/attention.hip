@@ -128,6 +128,10 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #ifndef ATT_VPF_NARROW
 #define ATT_VPF_NARROW 8
 #endif
+// most blocks per (row, head) that exact_attention_qkv_split gives the p.V of a short cache
+#ifndef ATT_DS
+#define ATT_DS 4
+#endif
 #ifndef ATT_VPF_LONG_BLOCKS
 #define ATT_VPF_LONG_BLOCKS 256
 #endif
@@ -270,7 +274,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
 // KS = 8 (caches of at most KP NT / 8 positions, hd a multiple of 64): the scores of the cached keys are computed by 8
 // threads per key, hd / 8 dimensions each (coalesced 16-byte loads of the key row, a sum over the 8 lanes), NT / 8 keys
 // per pass and at most KP passes, all loaded with the totals; KPF is then unused.
-template <int VPF, int NT = ATT_THREADS, int KPF = ATT_KPF, int KS = 1, int KP = 2>
+// DS > 1: DS blocks per (row, head) (blockIdx.z = slice), each with the whole softmax and the p.V of hd / DS
+// dimensions, so each thread's share of the value rows is loaded with the keys, at the start; needs hd / (2 DS) a
+// power of two of at most 64. obits gets obn (a multiple of DS) entries per head, each block the max of its slice.
+template <int VPF, int NT = ATT_THREADS, int KPF = ATT_KPF, int KS = 1, int KP = 2, int DS = 1>
 __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
                                                                const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
                                                                const int64_t* __restrict__ sin_t, const int32_t* __restrict__ slot,
@@ -278,7 +285,7 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
                                                                int32_t* __restrict__ sk, int64_t* __restrict__ v,
                                                                const int32_t* __restrict__ expt, int64_t* __restrict__ out,
                                                                int32_t* __restrict__ obits, int H, int KV, int hd, int Smax,
-                                                               int INV) {
+                                                               int INV, int obn) {
   extern __shared__ int64_t sc[];   // Smax entries
   __shared__ int64_t y[3][256];     // q head, new key, new value: shr(t, 28 - s) + b
   __shared__ int32_t qs[256], kn[256];
@@ -288,18 +295,20 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
   __shared__ int ored[16];
   __shared__ int64_t red[16], red2[16];
   __shared__ int64_t part[NT * 2];
-  const int r = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = blockIdx.x, h = blockIdx.y, ds = DS > 1 ? (int)blockIdx.z : 0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = H / KV, kh = h / grp;
   const int N = (H + 2 * KV) * hd;
   const int p = pos[r], sl = slot[r];
+  const int hds = hd / DS;   // this block's output dimensions [ds hds, (ds + 1) hds)
   if (p < 0 || p >= Smax) {   // the host keeps positions inside the cache; write nothing there
-    for (int d = tid; d < hd; d += blockDim.x) out[((int64_t)r * H + h) * hd + d] = 0;
-    if (obits && tid == 0) obits[(int64_t)r * H + h] = 0;
+    for (int d = tid; d < hds; d += blockDim.x) out[((int64_t)r * H + h) * hd + ds * hds + d] = 0;
+    if (obits && tid < obn / DS) obits[((int64_t)r * H + h) * obn + ds * (obn / DS) + tid] = 0;
     return;
   }
   const int64_t cbase = ((int64_t)sl * KV + kh) * Smax;
-  const int npair = hd >> 1, nparts = blockDim.x / npair;
-  const int dp = tid % npair, pp = tid / npair;
+  const int npair = hds >> 1, nparts = blockDim.x / npair;   // value pairs of the slice, threads per pair
+  const int dp = ds * npair + tid % npair, pp = tid / npair;
   // ---- loads that do not depend on the new token, issued with the totals
   v4i kpre[KPF > 0 && KS == 1 ? KPF : 1];
   int skpre = 0;
@@ -419,7 +428,7 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
   }
   __syncthreads();
   const int sqv = shq[0], skn = shq[1];
-  if (h % grp == 0) {   // one block per KV head writes the new position
+  if (h % grp == 0 && ds == 0) {   // one block per KV head writes the new position
     for (int j = tid; j < hd; j += blockDim.x) {
       kq[(cbase + p) * hd + j] = (int16_t)kn[j];
       v[(cbase + p) * hd + j] = y[2][j];
@@ -529,21 +538,42 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
       a1 = (int64_t)((uint64_t)a1 + (uint64_t)(pr * y[2][2 * dp + 1]));
     }
   }
-  part[2 * tid] = a0;
-  part[2 * tid + 1] = a1;
-  __syncthreads();
   int m = 0;
-  if (tid < hd) {
-    const int d = tid;
-    uint64_t tot = 0;
-    for (int k = 0; k < nparts; ++k) tot += (uint64_t)part[2 * (k * npair + (d >> 1)) + (d & 1)];
-    const int64_t o = shr64((int64_t)tot, 20);
-    out[((int64_t)r * H + h) * hd + d] = o;
-    m = bitlen64(abs64(o));
+  if constexpr (DS == 1) {
+    part[2 * tid] = a0;
+    part[2 * tid + 1] = a1;
+    __syncthreads();
+    if (tid < hd) {
+      const int d = tid;
+      uint64_t tot = 0;
+      for (int k = 0; k < nparts; ++k) tot += (uint64_t)part[2 * (k * npair + (d >> 1)) + (d & 1)];
+      const int64_t o = shr64((int64_t)tot, 20);
+      out[((int64_t)r * H + h) * hd + d] = o;
+      m = bitlen64(abs64(o));
+    }
+  } else {
+    // lanes l, l ^ npair, l ^ 2 npair ... of a wave hold the same pair: fold them (sums modulo 2^64), then the waves
+    for (int o = npair; o < 64; o <<= 1) {
+      a0 = (int64_t)((uint64_t)a0 + (uint64_t)__shfl_xor((long long)a0, o));
+      a1 = (int64_t)((uint64_t)a1 + (uint64_t)__shfl_xor((long long)a1, o));
+    }
+    if (lane < npair) {
+      part[wave * hds + 2 * lane] = a0;
+      part[wave * hds + 2 * lane + 1] = a1;
+    }
+    __syncthreads();
+    if (tid < hds) {
+      uint64_t tot = 0;
+#pragma unroll
+      for (int w = 0; w < NT / 64; ++w) tot += (uint64_t)part[w * hds + tid];
+      const int64_t o = shr64((int64_t)tot, 20);
+      out[((int64_t)r * H + h) * hd + ds * hds + tid] = o;
+      m = bitlen64(abs64(o));
+    }
   }
   if (obits) {
     m = block_max_i32(m, ored);
-    if (tid == 0) obits[(int64_t)r * H + h] = m;
+    if (tid < obn / DS) obits[((int64_t)r * H + h) * obn + ds * (obn / DS) + tid] = m;
   }
 }
 
@@ -551,65 +581,98 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
 
 using namespace exact;
 
+// one launch of a k_attention_qkv variant; the scores take Smax * 8 bytes of LDS, up to 64 KiB beside the static arrays
+template <int VPF, int NT, int KPF = ATT_KPF, int KS = 1, int KP = 2, int DS = 1>
+static void att_qkv_go(int R, int H, size_t lds, hipStream_t st, const int64_t* t, const int32_t* s, const int64_t* b,
+                       const int64_t* cos_t, const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* kq,
+                       int32_t* sk, int64_t* v, const int32_t* exp_t, int64_t* out, int32_t* obits, int KV, int hd, int Smax,
+                       int INV, int obn) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<VPF, NT, KPF, KS, KP, DS>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_attention_qkv<VPF, NT, KPF, KS, KP, DS>), dim3(R, H, DS), dim3(NT), lds, st, t, s, b, cos_t, sin_t,
+                     slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV, obn);
+}
+
+// blocks per (row, head) for the short-cache paths: the largest power of two up to ATT_DS that divides obn, keeps
+// the launch in one round of ATT_WIDE_BLOCKS blocks and leaves a power of two of at most 64 value pairs a block
+static int att_qkv_ds(int obn, int64_t blocks, int hd) {
+  for (int ds = ATT_DS; ds > 1; ds >>= 1) {
+    const int np = hd / (2 * ds);
+    if (obn % ds == 0 && blocks * ds <= ATT_WIDE_BLOCKS && hd % (2 * ds) == 0 && np <= 64 && (np & (np - 1)) == 0)
+      return ds;
+  }
+  return 1;
+}
+
+extern "C" int exact_attention_qkv_split(const int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
+                                         const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* kq,
+                                         int32_t* sk, int64_t* v, const int32_t* exp_t, int64_t* out, int32_t* obits,
+                                         int32_t obn, int32_t R, int32_t H, int32_t KV, int32_t hd, int32_t Smax, int32_t INV,
+                                         void* stream) {
+  if (!t || !s || !cos_t || !sin_t || !slot || !pos || !kq || !sk || !v || !exp_t || !out) return EXACT_E_ARG;
+  if (R <= 0 || H <= 0 || KV <= 0 || H % KV || hd <= 0 || Smax <= 0) return EXACT_E_ARG;
+  if (obn != 1 && obn != 2 && obn != 4) return EXACT_E_ARG;
+  if (hd > 256 || hd % 8 || (2 * ATT_THREADS) % hd || Smax > 8192) return EXACT_E_UNSUPPORTED;
+  if (reinterpret_cast<uintptr_t>(exp_t) & 15) return EXACT_E_ARG;   // staged into LDS in 16-byte pieces
+  const size_t lds = (size_t)Smax * 8;
+  const hipStream_t st = as_stream(stream);
+  const int64_t blocks = (int64_t)R * H;
+#define ATT_QKV_ARGS R, H, lds, st, t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, KV, hd, Smax, INV, obn
+  // caches of up to 2 ATT_WIDE_THREADS / 8 positions whose blocks fit one round: 8 threads per cached key (below), also
+  // past ATT_VPF_LONG_S when ATT_KS8_LONG
+  const bool ks8_wide = ATT_KS8 != 0 && ATT_KS8_WIDE_HD != 0 && hd % 64 == 0 && hd >= ATT_KS8_WIDE_HD && (2 * ATT_WIDE_THREADS) % hd == 0 &&
+                        Smax <= 2 * (ATT_WIDE_THREADS / 8) && blocks <= ATT_WIDE_BLOCKS &&
+                        (Smax <= ATT_VPF_LONG_S || ATT_KS8_LONG);
+  // ... and of up to 4 ATT_WIDE_THREADS / 8 positions at hd 128 in four passes
+  const bool ks8_wide4 = !ks8_wide && ATT_KS8 != 0 && ATT_KS8_LONG4 != 0 && hd == 128 && hd >= ATT_KS8_WIDE_HD &&
+                         Smax <= 4 * (ATT_WIDE_THREADS / 8) && blocks <= ATT_WIDE_BLOCKS;
+  const bool ks8_narrow = ATT_KS8 && hd % 64 == 0 && Smax <= 2 * (ATT_THREADS / 8);
+  const int ds = ks8_wide || ks8_wide4 || (ks8_narrow && hd < ATT_KS8_WIDE_HD) ? att_qkv_ds(obn, blocks, hd) : 1;
+  if (ks8_wide4) {
+    // value prefetch: 2 ATT_WIDE_THREADS DS / hd threads per pair cover the up to 512 positions in VPF steps
+    if (ds == 4)
+      att_qkv_go<8, ATT_WIDE_THREADS, ATT_KPF, 8, 4, 4>(ATT_QKV_ARGS);
+    else if (ds == 2)
+      att_qkv_go<8, ATT_WIDE_THREADS, ATT_KPF, 8, 4, 2>(ATT_QKV_ARGS);
+    else
+      att_qkv_go<ATT_VPF, ATT_WIDE_THREADS, ATT_KPF, 8, 4>(ATT_QKV_ARGS);
+  } else if (ATT_WIDE && !ks8_wide && Smax > ATT_VPF_LONG_S && blocks <= ATT_WIDE_BLOCKS && (2 * ATT_WIDE_THREADS) % hd == 0) {
+    att_qkv_go<ATT_VPF_WIDE, ATT_WIDE_THREADS, 0>(ATT_QKV_ARGS);
+  } else if (Smax > ATT_VPF_LONG_S && !ks8_wide) {
+    att_qkv_go<ATT_VPF_LONG, ATT_THREADS>(ATT_QKV_ARGS);
+  } else if (ks8_wide) {
+    if (ds == 4)
+      att_qkv_go<4, ATT_WIDE_THREADS, ATT_KPF, 8, 2, 4>(ATT_QKV_ARGS);
+    else if (ds == 2)
+      att_qkv_go<8, ATT_WIDE_THREADS, ATT_KPF, 8, 2, 2>(ATT_QKV_ARGS);
+    else
+      att_qkv_go<ATT_VPF, ATT_WIDE_THREADS, ATT_KPF, 8>(ATT_QKV_ARGS);
+  } else if (ks8_narrow && hd < ATT_KS8_WIDE_HD) {
+    if (ds == 4)
+      att_qkv_go<2, ATT_THREADS, ATT_KPF, 8, 2, 4>(ATT_QKV_ARGS);
+    else if (ds == 2)
+      att_qkv_go<4, ATT_THREADS, ATT_KPF, 8, 2, 2>(ATT_QKV_ARGS);
+    else
+      att_qkv_go<ATT_VPF_NARROW, ATT_THREADS, ATT_KPF, 8>(ATT_QKV_ARGS);
+  } else if (ks8_narrow) {
+    att_qkv_go<ATT_VPF, ATT_THREADS, ATT_KPF, 8>(ATT_QKV_ARGS);
+  } else {
+    att_qkv_go<ATT_VPF, ATT_THREADS>(ATT_QKV_ARGS);
+  }
+#undef ATT_QKV_ARGS
+  return launch_status("attention_qkv");
+}
+
 extern "C" int exact_attention_qkv(const int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
                                    const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* kq, int32_t* sk,
                                    int64_t* v, const int32_t* exp_t, int64_t* out, int32_t* obits, int32_t R, int32_t H,
                                    int32_t KV, int32_t hd, int32_t Smax, int32_t INV, void* stream) {
-  if (!t || !s || !cos_t || !sin_t || !slot || !pos || !kq || !sk || !v || !exp_t || !out) return EXACT_E_ARG;
-  if (R <= 0 || H <= 0 || KV <= 0 || H % KV || hd <= 0 || Smax <= 0) return EXACT_E_ARG;
-  if (hd > 256 || hd % 8 || (2 * ATT_THREADS) % hd || Smax > 8192) return EXACT_E_UNSUPPORTED;
-  if (reinterpret_cast<uintptr_t>(exp_t) & 15) return EXACT_E_ARG;   // staged into LDS in 16-byte pieces
-  static bool attr_set = false;
-  if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF_LONG>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
-    attr_set = true;
-  }
-  const size_t lds = (size_t)Smax * 8;
-  // caches of up to 2 ATT_WIDE_THREADS / 8 positions whose blocks fit one round: 8 threads per cached key (below), also
-  // past ATT_VPF_LONG_S when ATT_KS8_LONG
-  const bool ks8_wide = ATT_KS8 != 0 && ATT_KS8_WIDE_HD != 0 && hd % 64 == 0 && hd >= ATT_KS8_WIDE_HD && (2 * ATT_WIDE_THREADS) % hd == 0 &&
-                        Smax <= 2 * (ATT_WIDE_THREADS / 8) && (int64_t)R * H <= ATT_WIDE_BLOCKS &&
-                        (Smax <= ATT_VPF_LONG_S || ATT_KS8_LONG);
-  // ... and of up to 4 ATT_WIDE_THREADS / 8 positions at hd 128 in four passes
-  const bool ks8_wide4 = !ks8_wide && ATT_KS8 != 0 && ATT_KS8_LONG4 != 0 && hd == 128 && hd >= ATT_KS8_WIDE_HD &&
-                         Smax <= 4 * (ATT_WIDE_THREADS / 8) && (int64_t)R * H <= ATT_WIDE_BLOCKS;
-  if (ks8_wide4) {
-    static bool w4_set = false;
-    if (!w4_set) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF, ATT_WIDE_THREADS, ATT_KPF, 8, 4>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
-      w4_set = true;
-    }
-    hipLaunchKernelGGL((k_attention_qkv<ATT_VPF, ATT_WIDE_THREADS, ATT_KPF, 8, 4>), dim3(R, H), dim3(ATT_WIDE_THREADS), lds,
-                       as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
-  } else if (ATT_WIDE && !ks8_wide && Smax > ATT_VPF_LONG_S && (int64_t)R * H <= ATT_WIDE_BLOCKS && (2 * ATT_WIDE_THREADS) % hd == 0) {
-    static bool wide_set = false;
-    if (!wide_set) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<ATT_VPF_WIDE, ATT_WIDE_THREADS, 0>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
-      wide_set = true;
-    }
-    hipLaunchKernelGGL((k_attention_qkv<ATT_VPF_WIDE, ATT_WIDE_THREADS, 0>), dim3(R, H), dim3(ATT_WIDE_THREADS), lds,
-                       as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
-  } else if (Smax > ATT_VPF_LONG_S && !ks8_wide)
-    hipLaunchKernelGGL(k_attention_qkv<ATT_VPF_LONG>, dim3(R, H), dim3(ATT_THREADS), lds, as_stream(stream), t, s, b, cos_t,
-                       sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
-  else if (ks8_wide)
-    hipLaunchKernelGGL((k_attention_qkv<ATT_VPF, ATT_WIDE_THREADS, ATT_KPF, 8>), dim3(R, H), dim3(ATT_WIDE_THREADS), lds,
-                       as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
-  else if (ATT_KS8 && hd % 64 == 0 && Smax <= 2 * (ATT_THREADS / 8) && hd < ATT_KS8_WIDE_HD)
-    hipLaunchKernelGGL((k_attention_qkv<ATT_VPF_NARROW, ATT_THREADS, ATT_KPF, 8>), dim3(R, H), dim3(ATT_THREADS), lds,
-                       as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
-  else if (ATT_KS8 && hd % 64 == 0 && Smax <= 2 * (ATT_THREADS / 8))
-    hipLaunchKernelGGL((k_attention_qkv<ATT_VPF, ATT_THREADS, ATT_KPF, 8>), dim3(R, H), dim3(ATT_THREADS), lds,
-                       as_stream(stream), t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
-  else
-    hipLaunchKernelGGL(k_attention_qkv<ATT_VPF>, dim3(R, H), dim3(ATT_THREADS), lds, as_stream(stream), t, s, b, cos_t, sin_t,
-                       slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV);
-  return launch_status("attention_qkv");
+  return exact_attention_qkv_split(t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, 1, R, H, KV, hd, Smax,
+                                   INV, stream);
 }
 
 extern "C" int exact_qkv_rope_cache(int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,

@@ -1194,6 +1194,7 @@ extern "C" int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const in
 #define XQ_GO(AB, VR)                                                                                                  \
   do {                                                                                                                 \
     if (nparts <= 64) XQ_GO_PL(AB, VR, 1);                                                                             \
+    else if (nparts <= 256) XQ_GO_PL(AB, VR, 4);                                                                       \
     else XQ_GO_PL(AB, VR, XQ_PARTS_WIDE);                                                                              \
   } while (0)
   const int vr = R <= 1 ? 1 : (R <= 2 ? 2 : 4);

@@ -46,6 +46,7 @@ SIGNATURES = {
     "exact_qkv_rope_cache": [P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
     "exact_attention": [P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
     "exact_attention_qkv": [P, P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, P],
+    "exact_attention_qkv_split": [P, P, P, P, P, P, P, P, P, P, P, P, P, I32, I32, I32, I32, I32, I32, I32, P],
     "exact_attention_prefill": [P, P, P, P, P, I32, P, P, P, P, P, I64, I32, I32, I32, I32, I32, I32, I32, P],
     "exact_embed": [P, P, P, I32, I32, I32, P],
     "exact_embed_table": [P, P, P, I32, I32, P],

@@ -217,7 +217,7 @@ class Workspace:
         # (exact_gemv_g128_swiglu)
         self.part_sw = z(R * -(-max(I, cfg.SI if cfg.moe else 0) // 32), dt=I32)
         self.part_lg = ops.logits_parts(R, V, device)
-        self.obits = z(R, H, dt=I32)
+        self.obits = z(R, H * ops.ATT_SPLIT_MAX, dt=I32)   # per-head bit lengths, up to ATT_SPLIT_MAX a head
         self.ids, self.slot, self.pos = z(R, dt=I32), z(R, dt=I32), z(R, dt=I32)
         # the greedy ids are written over the input ids (read once, by the embedding at the start of the pass): the
         # next decode step consumes them with no copy launch in between
@@ -283,6 +283,7 @@ class TModel:
     QKV_NORM = True   # dense decode rows wider than NORM_FUSE_D: the attention norm inside the q|k|v GEMV
     MOE_NORM = True   # MoE decode rows: the attention norm inside the q|k|v GEMV, the expert norm inside the router GEMV
     MOE_ROUTE = True   # MoE decode rows: top-k routing and dispatch in one launch
+    ATT_SPLIT = 4   # decode attention with the q|k|v epilogue: bit lengths a head, so its p.V may run in that many blocks
     SHARED_SWIGLU = True   # MoE decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue
     EXPERT_SWIGLU = True   # MoE decode rows: the routed experts' SwiGLU and qrow inside their GEMVs
     EXPERT_GEMM_MIN_PAIRS = 64   # (row, expert) pairs from which the MoE experts run as one grouped GEMM
@@ -396,9 +397,11 @@ class TModel:
                     ws.t_qkv[:, off:off + lin.N].copy_(y)
                     off += lin.N
                 s_qkv, b_qkv = ws.s28, None
+            nob = H   # bit lengths per row that attention leaves in ws.obits
             if afuse:
                 ops.attention_qkv(t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache, tab.exp, ws.att, H, KV, hd,
-                                  tab.inv, ws.obits)
+                                  tab.inv, ws.obits, obn=self.ATT_SPLIT)
+                nob = H * self.ATT_SPLIT
             else:
                 ops.qkv_rope_cache(t_qkv if group else ws.t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache,
                                    ws.qq, ws.sq, H, KV, hd, clear=clear)
@@ -408,12 +411,12 @@ class TModel:
                 else:
                     ops.attention(ws.qq, ws.sq, cache, ws.slot, ws.pos, tab.exp, ws.att, H, KV, hd, tab.inv, ws.obits)
             if nfuse:   # also clears the down totals the q|k|v GEMV read as its residual (t_qkv and t_d are one range)
-                ops.gemv_qrow_acc(ws.att, ws.obits, H, self.abits, L["o"], t_o, ws.sa, zero=ws.t_qd if clear else None)
+                ops.gemv_qrow_acc(ws.att, ws.obits, nob, self.abits, L["o"], t_o, ws.sa, zero=ws.t_qd if clear else None)
             elif xfuse:   # clears the q|k|v totals attention left (and, q|k|v norm-fused, the down totals it read)
-                ops.gemv_qrow_acc(ws.att, ws.obits, H, self.abits, L["o"], t_o, ws.sa,
+                ops.gemv_qrow_acc(ws.att, ws.obits, nob, self.abits, L["o"], t_o, ws.sa,
                                   zero=(ws.t_qd if qfuse else t_qkv) if afuse and clear else None)
             else:
-                ops.quant_rows(ws.att, ws.obits, H, self.abits, ws.aq, ws.sa, x8=da)
+                ops.quant_rows(ws.att, ws.obits, nob, self.abits, ws.aq, ws.sa, x8=da)
             if nfuse and nsfuse:   # norm + gate|up + SwiGLU in one launch
                 ops.gemv_norm_swiglu(x_cur, t_o, ws.sa, L["g2"], L["gateup"], ws.s, tab.silu, ws.h, ws.part_sw,
                                      x_out=x_nxt, t=t_gu if keep else None)

@@ -449,17 +449,25 @@ def attention(qq, sq, cache, slot, pos, expt, out, H, KV, hd, inv, obits=None):
     return out
 
 
-def attention_qkv(t, s, b, cos_t, sin_t, slot, pos, cache, expt, out, H, KV, hd, inv, obits=None):
-    """qkv_rope_cache + attention in one launch for rows that each own their (slot, position); t unchanged."""
+ATT_SPLIT_MAX = 4   # bit lengths a head that attention_qkv may write (blocks a head's p.V may take)
+
+
+def attention_qkv(t, s, b, cos_t, sin_t, slot, pos, cache, expt, out, H, KV, hd, inv, obits=None, obn=1):
+    """qkv_rope_cache + attention in one launch for rows that each own their (slot, position); t unchanged.
+    obits (optional) gets obn entries per head (1, 2 or ATT_SPLIT_MAX; their max is the head's bit length): with obn > 1
+    the library may split each head's p.V over obn blocks, one output slice each."""
     R = t.shape[0]
     kq, sk, v = cache
     _need(t, I64, "t", R * (H + 2 * KV) * hd)
     _need(out, I64, "out", R * H * hd)
     if obits is not None:
-        _need(obits, I32, "obits", R * H)
-    _lib.call("exact_attention_qkv", _ptr(t), _ptr(_need(s, I32, "s", R)), _ptr(b), _ptr(cos_t), _ptr(sin_t), _ptr(slot),
-              _ptr(pos), _ptr(kq), _ptr(sk), _ptr(v), _ptr(expt), _ptr(out), _ptr(obits), R, H, KV, hd, kq.shape[2], inv,
-              _stream())
+        _need(obits, I32, "obits", R * H * obn)
+    args = (_ptr(t), _ptr(_need(s, I32, "s", R)), _ptr(b), _ptr(cos_t), _ptr(sin_t), _ptr(slot), _ptr(pos), _ptr(kq),
+            _ptr(sk), _ptr(v), _ptr(expt), _ptr(out), _ptr(obits))
+    if obn == 1:
+        _lib.call("exact_attention_qkv", *args, R, H, KV, hd, kq.shape[2], inv, _stream())
+    else:
+        _lib.call("exact_attention_qkv_split", *args, obn, R, H, KV, hd, kq.shape[2], inv, _stream())
     return out
 
 

@@ -277,6 +277,17 @@ int exact_attention_qkv(const int64_t* t, const int32_t* s, const int64_t* b, co
                         int64_t* v, const int32_t* exp_t, int64_t* out, int32_t* obits, int32_t R, int32_t H,
                         int32_t KV, int32_t hd, int32_t Smax, int32_t INV, void* stream);
 
+/* exact_attention_qkv with obn (1, 2 or 4) obits entries per head: obits[(r H + h) obn + i], whose max is the
+ * head's bit length (exact_quant_rows / exact_gemv_g128_qrow_acc take them with nparts = H obn). With obn > 1
+ * the launch may split each head's p.V over up to obn blocks that each write a slice of the head's dimensions
+ * and the bit length of that slice (short caches, while the blocks fit one round). Results identical to
+ * exact_attention_qkv; obn = 1 is that entry point. No counterpart in the reference, whose attention
+ * (exact_llm.py:170-176) returns the whole output and leaves its row maximum to qrow (exact_llm.py:41-46). */
+int exact_attention_qkv_split(const int64_t* t, const int32_t* s, const int64_t* b, const int64_t* cos_t,
+                              const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* kq, int32_t* sk,
+                              int64_t* v, const int32_t* exp_t, int64_t* out, int32_t* obits, int32_t obn, int32_t R,
+                              int32_t H, int32_t KV, int32_t hd, int32_t Smax, int32_t INV, void* stream);
+
 /* The same attention for the prefill of one sequence on the matrix cores: R query rows of cache slot `slot`
  * at increasing positions pos[r] (< nkeys), against keys 0..pos[r]; results identical to exact_attention
  * (exact_llm.py:170-176; exact_torch.py:162-166). q.k runs on int8 digit products of the int16 q and k

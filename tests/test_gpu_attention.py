@@ -210,11 +210,14 @@ def test_attention_with_zero_exp_table_gives_zero_rows():
                                                  (8, 2, 128, 2, True, 8192), (16, 16, 128, 1, False, 300),
                                                  (40, 8, 128, 1, True, 200), (14, 2, 64, 2, True, 300),
                                                  (4, 4, 256, 1, True, 400), (28, 4, 128, 10, True, 96),
-                                                 (28, 4, 128, 3, True, 500)])
-def test_fused_qkv_attention_matches_two_launches(H, KV, hd, R, bias, Smax):
-    """exact_attention_qkv against exact_qkv_rope_cache + exact_attention (both oracle-pinned above and in the
-    model tests): outputs, obits and every cache entry equal; rows in different slots at positions 0, Smax - 1 and
-    in between; the totals t are left unchanged."""
+                                                 (28, 4, 128, 3, True, 500), (16, 16, 128, 2, True, 512)])
+@pytest.mark.parametrize("obn", [1, 2, 4])
+def test_fused_qkv_attention_matches_two_launches(H, KV, hd, R, bias, Smax, obn):
+    """exact_attention_qkv (obn = 1) and exact_attention_qkv_split (obn = 2, 4: each head's p.V over up to obn
+    blocks) against exact_qkv_rope_cache + exact_attention (both oracle-pinned above and in the model tests):
+    outputs and every cache entry equal; the max of a head's obn bit lengths is its obits, and entry i bounds the
+    bit length of the head's i-th slice of hd / obn dimensions; rows in different slots at positions 0, Smax - 1
+    and in between; the totals t are left unchanged."""
     from exact_amd.tables import host_tables
     rng = np.random.default_rng(H + R + hd)
     B = R + 2
@@ -243,12 +246,15 @@ def test_fused_qkv_attention_matches_two_launches(H, KV, hd, R, bias, Smax):
     out_a = torch.full((R, H * hd), -7, dtype=I64, device=DEV)
     out_b = torch.full((R, H * hd), -9, dtype=I64, device=DEV)
     ob_a = torch.full((R, H), -1, dtype=I32, device=DEV)
-    ob_b = torch.full((R, H), -2, dtype=I32, device=DEV)
+    ob_b = torch.full((R, H * obn), -2, dtype=I32, device=DEV)
     ops.qkv_rope_cache(t_a, s_d, b_d, cos, sin, slot_d, pos_d, c_a, qq, sq, clear=False, **args)
     ops.attention(qq, sq, c_a, slot_d, pos_d, expt, out_a, inv=inv, obits=ob_a, **args)
-    ops.attention_qkv(t_b, s_d, b_d, cos, sin, slot_d, pos_d, c_b, expt, out_b, inv=inv, obits=ob_b, **args)
+    ops.attention_qkv(t_b, s_d, b_d, cos, sin, slot_d, pos_d, c_b, expt, out_b, inv=inv, obits=ob_b, obn=obn, **args)
     assert np.array_equal(host(out_b), host(out_a))
-    assert np.array_equal(host(ob_b), host(ob_a))
+    ob = host(ob_b).reshape(R, H, obn)
+    assert np.array_equal(ob.max(-1), host(ob_a))
+    slice_bits = np.vectorize(lambda m: int(m).bit_length())(np.abs(host(out_a)).reshape(R, H, obn, -1).max(-1))
+    assert (ob >= slice_bits).all()
     for x, y in zip(c_b, c_a):
         assert np.array_equal(host(x), host(y))
     assert np.array_equal(host(t_b), t)
