@@ -132,6 +132,15 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #ifndef ATT_DS
 #define ATT_DS 4
 #endif
+// launches whose (row, head) blocks run in several rounds (batched decode): the 8-threads-per-key path up to
+// 4 ATT_THREADS / 8 cached positions (14B bs8 at a 135-token context, in isolation: 19.6 -> 11.5 us, against 13.7 us
+// for exact_qkv_rope_cache + exact_attention), ATT_MR_VPF value pairs prefetched (1 to 8: level)
+#ifndef ATT_KS8_MR
+#define ATT_KS8_MR 1
+#endif
+#ifndef ATT_MR_VPF
+#define ATT_MR_VPF 4
+#endif
 #ifndef ATT_VPF_LONG_BLOCKS
 #define ATT_VPF_LONG_BLOCKS 256
 #endif
@@ -277,7 +286,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attention(const int16_t* __rest
 // DS > 1: DS blocks per (row, head) (blockIdx.z = slice), each with the whole softmax and the p.V of hd / DS
 // dimensions, so each thread's share of the value rows is loaded with the keys, at the start; needs hd / (2 DS) a
 // power of two of at most 64. obits gets obn (a multiple of DS) entries per head, each block the max of its slice.
-template <int VPF, int NT = ATT_THREADS, int KPF = ATT_KPF, int KS = 1, int KP = 2, int DS = 1>
+// GT: exp table lookups from global memory (cached), not staged into LDS: 41 KiB less LDS a block, for launches whose
+// blocks run in several rounds
+template <int VPF, int NT = ATT_THREADS, int KPF = ATT_KPF, int KS = 1, int KP = 2, int DS = 1, bool GT = false>
 __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
                                                                const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
                                                                const int64_t* __restrict__ sin_t, const int32_t* __restrict__ slot,
@@ -374,7 +385,7 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
     }
   }
   const int sh = 28 - s[r];
-  {   // the exp table into LDS: every piece loaded before the first store, with the loads above
+  if constexpr (!GT) {   // the exp table into LDS: every piece loaded before the first store, with the loads above
     constexpr int NV = EXACT_EXP_N / 4, NK = (NV + NT - 1) / NT;
     v4i te[NK];
 #pragma unroll
@@ -505,7 +516,7 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
   mx = block_max64_1(mx, red);
   int64_t es = 0;
   for (int si = tid; si < S; si += blockDim.x) {
-    const int64_t e = lut_exp(texp, mx - sc[si]);
+    const int64_t e = lut_exp(GT ? expt : texp, mx - sc[si]);
     sc[si] = e;
     es += e;
   }
@@ -582,18 +593,18 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
 using namespace exact;
 
 // one launch of a k_attention_qkv variant; the scores take Smax * 8 bytes of LDS, up to 64 KiB beside the static arrays
-template <int VPF, int NT, int KPF = ATT_KPF, int KS = 1, int KP = 2, int DS = 1>
+template <int VPF, int NT, int KPF = ATT_KPF, int KS = 1, int KP = 2, int DS = 1, bool GT = false>
 static void att_qkv_go(int R, int H, size_t lds, hipStream_t st, const int64_t* t, const int32_t* s, const int64_t* b,
                        const int64_t* cos_t, const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* kq,
                        int32_t* sk, int64_t* v, const int32_t* exp_t, int64_t* out, int32_t* obits, int KV, int hd, int Smax,
                        int INV, int obn) {
   static bool attr_set = false;
   if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<VPF, NT, KPF, KS, KP, DS>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_qkv<VPF, NT, KPF, KS, KP, DS, GT>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, 8192 * 8);
     attr_set = true;
   }
-  hipLaunchKernelGGL((k_attention_qkv<VPF, NT, KPF, KS, KP, DS>), dim3(R, H, DS), dim3(NT), lds, st, t, s, b, cos_t, sin_t,
+  hipLaunchKernelGGL((k_attention_qkv<VPF, NT, KPF, KS, KP, DS, GT>), dim3(R, H, DS), dim3(NT), lds, st, t, s, b, cos_t, sin_t,
                      slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV, obn);
 }
 
@@ -631,8 +642,18 @@ extern "C" int exact_attention_qkv_split(const int64_t* t, const int32_t* s, con
   const bool ks8_wide4 = !ks8_wide && ATT_KS8 != 0 && ATT_KS8_LONG4 != 0 && hd == 128 && hd >= ATT_KS8_WIDE_HD &&
                          Smax <= 4 * (ATT_WIDE_THREADS / 8) && blocks <= ATT_WIDE_BLOCKS;
   const bool ks8_narrow = ATT_KS8 && hd % 64 == 0 && Smax <= 2 * (ATT_THREADS / 8);
+  // blocks in several rounds (batched decode) over caches of up to 4 ATT_THREADS / 8 positions: ATT_THREADS-thread
+  // blocks, 8 threads per cached key in two or four passes, exp table lookups from global memory (the LDS it would
+  // take leaves room for more blocks per CU)
+  const bool ks8_mr = ATT_KS8 && ATT_KS8_MR && blocks > ATT_WIDE_BLOCKS && hd % 64 == 0 && hd <= 128 &&
+                      Smax <= 4 * (ATT_THREADS / 8);
   const int ds = ks8_wide || ks8_wide4 || (ks8_narrow && hd < ATT_KS8_WIDE_HD) ? att_qkv_ds(obn, blocks, hd) : 1;
-  if (ks8_wide4) {
+  if (ks8_mr) {
+    if (Smax <= 2 * (ATT_THREADS / 8))
+      att_qkv_go<ATT_MR_VPF, ATT_THREADS, ATT_KPF, 8, 2, 1, true>(ATT_QKV_ARGS);
+    else
+      att_qkv_go<ATT_MR_VPF, ATT_THREADS, ATT_KPF, 8, 4, 1, true>(ATT_QKV_ARGS);
+  } else if (ks8_wide4) {
     // value prefetch: 2 ATT_WIDE_THREADS DS / hd threads per pair cover the up to 512 positions in VPF steps
     if (ds == 4)
       att_qkv_go<8, ATT_WIDE_THREADS, ATT_KPF, 8, 4, 4>(ATT_QKV_ARGS);

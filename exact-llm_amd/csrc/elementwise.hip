@@ -192,9 +192,12 @@ __global__ __launch_bounds__(1024) void k_swiglu_qrow_row(int64_t* __restrict__ 
 // grid (slices, R): xq[r][i] = clip(shr(src[r * ld + i], s_r), +-(2^bits - 1)), s_r from the slice maxima
 __global__ __launch_bounds__(256) void k_quant_rows(int64_t* __restrict__ src, int64_t ld, const int32_t* __restrict__ part,
                                                     int nparts, int bits, void* xq, int32_t* __restrict__ s, int K,
-                                                    int clear, int8_t* x8) {
+                                                    int clear, int8_t* x8, int64_t* __restrict__ zero, int64_t zero_n) {
   __shared__ int qs;
   const int r = blockIdx.y, b = blockIdx.x;
+  for (int64_t i = ((int64_t)r * gridDim.x + b) * blockDim.x + threadIdx.x; i < zero_n;
+       i += (int64_t)gridDim.x * gridDim.y * blockDim.x)
+    zero[i] = 0;
   if (threadIdx.x < 64) {
     int m = 0;
     for (int i = threadIdx.x; i < nparts; i += 64) {
@@ -441,18 +444,22 @@ extern "C" int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* si
   const int np = (I + QSLICE - 1) / QSLICE;
   hipLaunchKernelGGL(k_swiglu_part, dim3(np, R), dim3(256), 0, st, t, s, silu_t, part, I, np, clear_t, h);
   if (h)
-    hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, h, (int64_t)I, part, np, bits, xq, sq, I, 0, x8);
+    hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, h, (int64_t)I, part, np, bits, xq, sq, I, 0, x8, nullptr,
+                       (int64_t)0);
   else
-    hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, t, (int64_t)2 * I, part, np, bits, xq, sq, I, clear_t, x8);
+    hipLaunchKernelGGL(k_quant_rows, dim3(np, R), dim3(256), 0, st, t, (int64_t)2 * I, part, np, bits, xq, sq, I, clear_t, x8,
+                       nullptr, (int64_t)0);
   return launch_status("swiglu_qrow");
 }
 
 extern "C" int exact_quant_rows(int64_t* src, int64_t ld, const int32_t* part, int32_t nparts, int32_t bits, void* xq,
-                                int32_t* s, int32_t R, int32_t K, int32_t clear, int8_t* x8, void* stream) {
+                                int32_t* s, int32_t R, int32_t K, int32_t clear, int8_t* x8, int64_t* zero, int64_t zero_n,
+                                void* stream) {
   if (!src || !part || !xq || !s || R <= 0 || K <= 0 || ld < K || nparts <= 0 || bits < 1 || bits > 15) return EXACT_E_ARG;
   if (x8 && bits < 8) return EXACT_E_ARG;
+  if (zero_n < 0 || (zero_n > 0 && !zero)) return EXACT_E_ARG;
   hipLaunchKernelGGL(k_quant_rows, dim3((K + QSLICE - 1) / QSLICE, R), dim3(256), 0, as_stream(stream), src, ld, part, nparts,
-                     bits, xq, s, K, clear, x8);
+                     bits, xq, s, K, clear, x8, zero, zero_n);
   return launch_status("quant_rows");
 }
 

@@ -39,7 +39,7 @@ SIGNATURES = {
     "exact_irms": [P, P, P, I32, I32, P],
     "exact_rmsnorm_qrow": [P, P, P, P, I32, P, P, I32, I32, I32, P, P],
     "exact_swiglu_qrow": [P, P, P, I32, P, P, P, I32, I32, I32, P, P, P],
-    "exact_quant_rows": [P, I64, P, I32, I32, P, P, I32, I32, I32, P, P],
+    "exact_quant_rows": [P, I64, P, I32, I32, P, P, I32, I32, I32, P, P, I64, P],
     "exact_isilu": [P, P, P, I64, P],
     "exact_isig": [P, P, P, I64, P],
     "exact_isoftmax": [P, P, P, P, I32, I32, P],

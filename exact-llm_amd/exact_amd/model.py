@@ -283,6 +283,7 @@ class TModel:
     QKV_NORM = True   # dense decode rows wider than NORM_FUSE_D: the attention norm inside the q|k|v GEMV
     MOE_NORM = True   # MoE decode rows: the attention norm inside the q|k|v GEMV, the expert norm inside the router GEMV
     MOE_ROUTE = True   # MoE decode rows: top-k routing and dispatch in one launch
+    BATCH_ATTN = True   # batched decode rows: the q|k|v epilogue inside the attention launch
     ATT_SPLIT = 4   # decode attention with the q|k|v epilogue: bit lengths a head, so its p.V may run in that many blocks
     SHARED_SWIGLU = True   # MoE decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue
     EXPERT_SWIGLU = True   # MoE decode rows: the routed experts' SwiGLU and qrow inside their GEMVs
@@ -338,6 +339,10 @@ class TModel:
         # launch at 8 rows
         xfuse = group and R <= self.QROW_FUSE_ROWS
         afuse = xfuse and ws.seq is None and (R == 1 or independent)
+        # batched decode rows (each its own sequence): the q|k|v epilogue inside the attention launch as well, whose
+        # totals the attention output's qrow launch then clears (caches of up to 256 positions: 8 threads per key)
+        bfuse = (self.BATCH_ATTN and group and not xfuse and ws.seq is None and independent and hd % 64 == 0 and hd <= 128
+                 and self.Smax <= 256)
         # decode rows of dense int16 models: residual + RMSNorm + qrow run inside the GEMVs that consume them (q|k|v,
         # gate|up, head), which read one residual buffer and write the other
         nfuse = (afuse and self.abits == 15 and not c.moe and R <= ops.NORM_FUSE_ROWS and D <= self.NORM_FUSE_D
@@ -398,7 +403,7 @@ class TModel:
                     off += lin.N
                 s_qkv, b_qkv = ws.s28, None
             nob = H   # bit lengths per row that attention leaves in ws.obits
-            if afuse:
+            if afuse or bfuse:
                 ops.attention_qkv(t_qkv, s_qkv, b_qkv, tab.cos, tab.sin, ws.slot, ws.pos, cache, tab.exp, ws.att, H, KV, hd,
                                   tab.inv, ws.obits, obn=self.ATT_SPLIT)
                 nob = H * self.ATT_SPLIT
@@ -416,7 +421,7 @@ class TModel:
                 ops.gemv_qrow_acc(ws.att, ws.obits, nob, self.abits, L["o"], t_o, ws.sa,
                                   zero=(ws.t_qd if qfuse else t_qkv) if afuse and clear else None)
             else:
-                ops.quant_rows(ws.att, ws.obits, nob, self.abits, ws.aq, ws.sa, x8=da)
+                ops.quant_rows(ws.att, ws.obits, nob, self.abits, ws.aq, ws.sa, x8=da, zero=t_qkv if bfuse and clear else None)
             if nfuse and nsfuse:   # norm + gate|up + SwiGLU in one launch
                 ops.gemv_norm_swiglu(x_cur, t_o, ws.sa, L["g2"], L["gateup"], ws.s, tab.silu, ws.h, ws.part_sw,
                                      x_out=x_nxt, t=t_gu if keep else None)

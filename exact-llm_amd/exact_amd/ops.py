@@ -400,13 +400,14 @@ def swiglu_qrow(t, s, silu, bits=15, xq=None, sq=None, clear=False, part=None, h
     return xq, sq
 
 
-def quant_rows(src, part, nparts, bits, xq, s, K=None, clear=False, x8=None):
+def quant_rows(src, part, nparts, bits, xq, s, K=None, clear=False, x8=None, zero=None):
     """qrow of src rows (first K columns) given per-slice bit lengths of max |src| part (R, nparts) int32.
-    x8: (2R, K) int8, also receives xq's digit rows."""
+    x8: (2R, K) int8, also receives xq's digit rows. zero: an int64 tensor the launch also clears."""
     R, ld = src.shape
     K = ld if K is None else K
     _lib.call("exact_quant_rows", _ptr(_need(src, I64, "src")), ld, _ptr(_need(part, I32, "part", R * nparts)), nparts, bits,
-              _ptr(xq), _ptr(_need(s, I32, "s", R)), R, K, int(clear), _digits(x8, R, K), _stream())
+              _ptr(xq), _ptr(_need(s, I32, "s", R)), R, K, int(clear), _digits(x8, R, K),
+              _ptr(None if zero is None else _need(zero, I64, "zero")), 0 if zero is None else zero.numel(), _stream())
     return xq, s
 
 

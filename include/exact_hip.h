@@ -230,9 +230,12 @@ int exact_swiglu_qrow(int64_t* t, const int32_t* s, const int32_t* silu_t, int32
 /* qrow with the row maximum supplied in parts (a producer kernel wrote part[r * nparts + i] =
  * bitlen(max |src| over its slice i of row r)): s = max(max_i part - bits, 0), xq = clip(rs(src, s))
  * (exact_llm.py:41-46; bitlen of the row max = max of the slice bit lengths). src rows are ld apart;
- * clear != 0 leaves src zeroed. x8 (optional, bits >= 8): xq's digit rows too, as exact_rmsnorm_qrow. */
+ * clear != 0 leaves src zeroed. x8 (optional, bits >= 8): xq's digit rows too, as exact_rmsnorm_qrow.
+ * zero (optional): zero_n int64 the launch also clears (a buffer whose readers have finished, e.g. the q|k|v
+ * totals exact_attention_qkv leaves in place). */
 int exact_quant_rows(int64_t* src, int64_t ld, const int32_t* part, int32_t nparts, int32_t bits, void* xq,
-                     int32_t* s, int32_t R, int32_t K, int32_t clear, int8_t* x8, void* stream);
+                     int32_t* s, int32_t R, int32_t K, int32_t clear, int8_t* x8, int64_t* zero, int64_t zero_n,
+                     void* stream);
 
 /* Elementwise LUT nonlinearities on int64 arrays (isilu exact_llm.py:118-122; isig moe_exact_kaggle.py:420-424). */
 int exact_isilu(const int64_t* x, const int32_t* silu_t, int64_t* y, int64_t n, void* stream);

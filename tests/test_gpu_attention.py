@@ -210,7 +210,8 @@ def test_attention_with_zero_exp_table_gives_zero_rows():
                                                  (8, 2, 128, 2, True, 8192), (16, 16, 128, 1, False, 300),
                                                  (40, 8, 128, 1, True, 200), (14, 2, 64, 2, True, 300),
                                                  (4, 4, 256, 1, True, 400), (28, 4, 128, 10, True, 96),
-                                                 (28, 4, 128, 3, True, 500), (16, 16, 128, 2, True, 512)])
+                                                 (28, 4, 128, 3, True, 500), (16, 16, 128, 2, True, 512),
+                                                 (40, 8, 128, 8, True, 200), (14, 2, 64, 20, False, 256)])
 @pytest.mark.parametrize("obn", [1, 2, 4])
 def test_fused_qkv_attention_matches_two_launches(H, KV, hd, R, bias, Smax, obn):
     """exact_attention_qkv (obn = 1) and exact_attention_qkv_split (obn = 2, 4: each head's p.V over up to obn
