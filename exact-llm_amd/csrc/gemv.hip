@@ -388,7 +388,7 @@ __device__ __forceinline__ void load_gu_group(GroupRegs& G_, const int8_t* __res
 // k part kp = w / NPB) runs the group loop over its share of the groups for the pair's gate and up sub-tiles, so one lane
 // holds a gate total and the up total of the same column. The k parts combine in LDS (no atomics, no zero-filled
 // totals); the kp = 0 waves store h = shr(isilu(shr(g, 28 - s)) * shr(u, 28 - s), F) (exact_llm.py:179, as
-// k_swiglu_part) and the block's bit length of max |h| per row in part[r * gridDim.x + b], which the quantising down
+// k_swiglu_part) and each pair's bit length of max |h| per row in part[r * I / 32 + pair], which the quantising down
 // GEMV reads. tout (optional, (R, 2I)) receives the gate|up totals. Small blocks (NPB 1, KS 2: 2 I / 32 waves of 64
 // lanes) spread the waves over the CUs better than larger ones (7B bs1 decode: 4-wave blocks of 64 columns 2311 us a
 // step, 2-wave blocks of 32 columns 2194-2218, against 2311 for the GEMV + SwiGLU launches).
@@ -513,11 +513,9 @@ combine:
       for (int v = 0; v < VR; ++v) pm[p][4 * c + v] = bl[v];
   }
   __syncthreads();
-  if ((int)threadIdx.x < R) {
-    int a = pm[0][threadIdx.x];
-#pragma unroll
-    for (int q = 1; q < NPB; ++q) a = pm[q][threadIdx.x] > a ? pm[q][threadIdx.x] : a;
-    part[(size_t)threadIdx.x * gridDim.x + blockIdx.x] = a;
+  if ((int)threadIdx.x < R * NPB) {   // one bit length per pair (32 columns) and row, whatever NPB
+    const int r = threadIdx.x / NPB, q = threadIdx.x - r * NPB;
+    part[(size_t)r * gridDim.x * NPB + blockIdx.x * NPB + q] = pm[q][r];
   }
 }
 
@@ -1102,11 +1100,35 @@ extern "C" int exact_gemv(const int16_t* x, const int8_t* wT, const int64_t* Mg,
 #endif
 #define GEMV_NORM_KMAX (256 * 24)
 
-// waves per block of exact_gemv_g128_norm_acc: 8 for rows wider than GEMV_NORM_BW8_K whose group-split tasks fit one
-// round of 8-wave blocks on `cus` compute units (each CU then normalises the row once), else 4
+// rows wider than GEMV_NORM_BW8_K whose group-split tasks do not fit one round of 8-wave blocks: the split capped so
+// that they do, when that leaves at least GEMV_NORM_FIT_MIN splits (0: never)
+#ifndef GEMV_NORM_FIT_MIN
+#define GEMV_NORM_FIT_MIN 8
+#endif
+
+// group split and waves per block of exact_gemv_g128_norm_acc on `cus` compute units: 8-wave blocks, one per CU (each
+// CU then normalises the row once), for rows wider than GEMV_NORM_BW8_K whose tasks fit one round or are capped to;
+// else 4-wave blocks, every block normalising the row
+static int norm_split(int R, int N, int K, int cus, int* bw) {
+  const int64_t nbs = (N + 63) / 64;
+  const int ns = gemv_nsplit(N, K / 128, R, 15);
+  *bw = 4;
+  if (K <= GEMV_NORM_BW8_K) return ns;
+  if ((nbs * ns + 7) / 8 <= cus) {
+    *bw = 8;
+    return ns;
+  }
+  const int64_t cap = (int64_t)cus * 8 / nbs;
+  if (GEMV_NORM_FIT_MIN > 0 && cap >= GEMV_NORM_FIT_MIN) {
+    *bw = 8;
+    return (int)cap;
+  }
+  return ns;
+}
 static int norm_block_waves(int R, int N, int K, int cus) {
-  const int64_t tasks = (int64_t)((N + 63) / 64) * gemv_nsplit(N, K / 128, R, 15);
-  return K > GEMV_NORM_BW8_K && (tasks + 7) / 8 <= cus ? 8 : 4;
+  int bw;
+  (void)norm_split(R, N, K, cus, &bw);
+  return bw;
 }
 
 extern "C" int exact_gemv_g128_norm_acc_blockwaves(int32_t R, int32_t N, int32_t K, int32_t cus) {
@@ -1123,13 +1145,12 @@ extern "C" int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, con
   if (K % 128 || K > GEMV_NORM_KMAX || R > GEMV_NORM_ROWS) return EXACT_E_UNSUPPORTED;
   if (reinterpret_cast<uintptr_t>(wp) & 15) return EXACT_E_UNSUPPORTED;
   const int G = K / 128;
-  const int nsplit = gemv_nsplit(N, G, R, 15);
+  int bw;
+  const int nsplit = norm_split(R, N, K, device_cus(), &bw);   // 8-wave blocks: see the kernel
+  const bool bw8 = bw == 8;
   const int64_t tasks = (int64_t)((N + 63) / 64) * nsplit;
   const size_t lds = (size_t)R * K * 2;
   hipStream_t st = as_stream(stream);
-  // rows wider than GEMV_NORM_BW8_K whose tasks fit one round of 8-wave blocks: 8-wave blocks (see the kernel)
-  const bool bw8 = norm_block_waves(R, N, K, device_cus()) == 8;
-  const int bw = bw8 ? 8 : 4;
   dim3 grid((unsigned)((tasks + bw - 1) / bw)), block(64 * bw);
   const int ept = (K + 64 * bw - 1) / (64 * bw);
 #define NORM_GO_BW(VR, E, BW)                                                                                           \
@@ -1251,6 +1272,7 @@ extern "C" int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const 
 #endif
 #define GEMV_NSW_THREADS (64 * GEMV_NSW_NPB * GEMV_NSW_KS)
 #define GEMV_NSW_KMAX (128 * 16)
+#define GEMV_NSW_WIDE_KMAX (128 * 64)   // wider rows (up to this): 8-wave blocks, see the launcher
 
 extern "C" int exact_gemv_g128_norm_swiglu(const int64_t* x_in, int64_t* x_out, const int64_t* res_t, const int32_t* res_s,
                                            const int64_t* g, const int8_t* wp, const int16_t* mp, const int16_t* mh,
@@ -1259,9 +1281,45 @@ extern "C" int exact_gemv_g128_norm_swiglu(const int64_t* x_in, int64_t* x_out, 
   if (!x_in || !g || !wp || !mp || !s_out || !silu || !h || !part || R <= 0 || I <= 0 || K <= 0 || (res_t && !res_s))
     return EXACT_E_ARG;
   if (x_out && (x_out == x_in || x_out == res_t)) return EXACT_E_ARG;   // the other blocks still read x_in / res_t
-  if (R > GEMV_NSW_ROWS || I % (32 * GEMV_NSW_NPB) || I % 64 || K % 128 || K > GEMV_NSW_KMAX) return EXACT_E_UNSUPPORTED;
+  if (R > GEMV_NSW_ROWS || I % 64 || K % 128 || K > GEMV_NSW_WIDE_KMAX) return EXACT_E_UNSUPPORTED;
   if (reinterpret_cast<uintptr_t>(wp) & 15) return EXACT_E_UNSUPPORTED;
   const int G = K / 128;
+  if (K > GEMV_NSW_KMAX) {
+    // wide rows: 8-wave blocks, each normalising the rows once, as many as the CUs take in one round: pairs of 32 gate
+    // columns x k parts 2 x 4 when I / 64 blocks fit (14B, I = 13824: 216 blocks; A/B 4.15 -> 3.91 ms a decode step),
+    // else 4 x 2 (7B, I = 18944: 148 blocks; 2.10 -> 1.99 ms; as 2 x 4, 296 blocks: 2.27)
+    if (I % 128 && I / 64 > device_cus()) return EXACT_E_UNSUPPORTED;
+    const bool np2 = I / 64 <= device_cus();
+    dim3 gridw((unsigned)(I / (np2 ? 64 : 128))), blockw(512);
+    const size_t ldsw = (size_t)R * K * 2;
+    hipStream_t stw = as_stream(stream);
+    const int eptw = (K + 511) / 512;
+#define NSWW_GO2(VR, E, NPBW, KSW)                                                                                     \
+  do {                                                                                                                 \
+    if (mh)                                                                                                            \
+      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, NPBW, KSW, true, E>), gridw, blockw, ldsw, stw, nullptr, wp,  \
+                         mp, mh, nullptr, silu, h, part, t, R, I, K, G, x_in, x_out, res_t, res_s, g, s_out);           \
+    else                                                                                                               \
+      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, NPBW, KSW, false, E>), gridw, blockw, ldsw, stw, nullptr, wp, \
+                         mp, mh, nullptr, silu, h, part, t, R, I, K, G, x_in, x_out, res_t, res_s, g, s_out);           \
+  } while (0)
+#define NSWW_GO(VR, E)                                                                                                 \
+  do {                                                                                                                 \
+    if (np2) NSWW_GO2(VR, E, 2, 4); else NSWW_GO2(VR, E, 4, 2);                                                        \
+  } while (0)
+#define NSWW_EPT(VR)                                                                                                   \
+  do {                                                                                                                 \
+    if (eptw <= 7) NSWW_GO(VR, 7);                                                                                     \
+    else if (eptw <= 10) NSWW_GO(VR, 10);                                                                              \
+    else NSWW_GO(VR, 16);                                                                                              \
+  } while (0)
+    if (R == 1) NSWW_EPT(1); else NSWW_EPT(2);
+#undef NSWW_EPT
+#undef NSWW_GO
+#undef NSWW_GO2
+    return launch_status("gemv_g128_norm_swiglu");
+  }
+  if (I % (32 * GEMV_NSW_NPB)) return EXACT_E_UNSUPPORTED;
   dim3 grid((unsigned)(I / (32 * GEMV_NSW_NPB))), block(GEMV_NSW_THREADS);
   const size_t lds = (size_t)R * K * 2;
   hipStream_t st = as_stream(stream);

@@ -283,6 +283,7 @@ class TModel:
     QKV_NORM = True   # dense decode rows wider than NORM_FUSE_D: the attention norm inside the q|k|v GEMV
     MOE_NORM = True   # MoE decode rows: the attention norm inside the q|k|v GEMV, the expert norm inside the router GEMV
     MOE_ROUTE = True   # MoE decode rows: top-k routing and dispatch in one launch
+    FFN_NORM = True   # decode rows with the attention norm in the q|k|v GEMV: the FFN norm in the SwiGLU GEMV too
     BATCH_ATTN = True   # batched decode rows: the q|k|v epilogue inside the attention launch
     ATT_SPLIT = 4   # decode attention with the q|k|v epilogue: bit lengths a head, so its p.V may run in that many blocks
     SHARED_SWIGLU = True   # MoE decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue
@@ -366,6 +367,10 @@ class TModel:
         # over its slice bit lengths before the down GEMV (no gate|up totals, no SwiGLU launch)
         sqfuse = (self.BATCH_SWIGLU and group and not xfuse and not c.moe and self.abits == 15 and R <= ops.SWIGLU_GEMV_MAX_ROWS
                   and c.I % 64 == 0 and self.w.layers[0]["gateup"].bias is None)
+        # ... and with the attention norm inside the q|k|v GEMV, the FFN norm inside the SwiGLU GEMV (8-wave blocks, about
+        # one per CU)
+        fsfuse = (self.FFN_NORM and sfuse and qfuse and D > ops.NORM_SWIGLU_KMAX and D <= ops.NORM_SWIGLU_WIDE_KMAX
+                  and c.I % 128 == 0)
         if ws.h is None and not c.moe and ((xfuse and (c.I > 8192 or nfuse or sfuse)) or sqfuse):
             ws.h = torch.zeros((R, ws.I), dtype=I64, device=self.dev)
         x_cur, x_nxt = ws.x, ws.x2
@@ -444,6 +449,8 @@ class TModel:
                 if rfuse:   # x_out: the other blocks still read x_cur; t_o is cleared by the shared expert's down GEMV
                     ops.gemv_norm_acc(x_cur, t_o, ws.sa, L["g2"], L["router"], ws.t_rt, ws.s, x_out=x_nxt, xq_out=ws.xq)
                     x_cur, x_nxt = x_nxt, x_cur
+                elif fsfuse:
+                    pass
                 else:
                     ops.rmsnorm_qrow(x_cur, L["g2"], self.abits, t_o, ws.sa, ws.xq, ws.s, clear=clear, x8=dx)
             else:
@@ -455,7 +462,14 @@ class TModel:
                 self._moe(ws, L, dx, dh, x=x_cur, routed=rfuse, zero=t_o if rfuse and clear else None)
                 res_t, res_s = None, None
                 continue
-            if sfuse:
+            if fsfuse:   # the down GEMV clears the o totals the norm read
+                ops.gemv_norm_swiglu(x_cur, t_o, ws.sa, L["g2"], L["gateup"], ws.s, tab.silu, ws.h, ws.part_sw,
+                                     x_out=x_nxt, t=t_gu if keep else None)
+                x_cur, x_nxt = x_nxt, x_cur
+                ops.gemv_qrow_acc(ws.h, ws.part_sw, c.I // ops.SWIGLU_PART_COLS, self.abits, L["down"], t_d, ws.sh,
+                                  zero=t_o if clear else None)
+                res_t, res_s = t_d, ws.sh
+            elif sfuse:
                 ops.gemv_swiglu(ws.xq, L["gateup"], ws.s, tab.silu, ws.h, ws.part_sw, t=t_gu if keep else None)
                 ops.gemv_qrow_acc(ws.h, ws.part_sw, c.I // ops.SWIGLU_PART_COLS, self.abits, L["down"], t_d, ws.sh)
                 res_t, res_s = t_d, ws.sh

@@ -205,7 +205,8 @@ def gemv_norm_acc(x_in, res_t, res_s, g, lin, out, s_out, x_out=None, xq_out=Non
     return out
 
 
-NORM_SWIGLU_KMAX = 128 * 16   # row width of one exact_gemv_g128_norm_swiglu launch
+NORM_SWIGLU_KMAX = 128 * 16   # row width of one exact_gemv_g128_norm_swiglu launch with 4-wave blocks
+NORM_SWIGLU_WIDE_KMAX = 128 * 64   # ... and with 8-wave blocks (I a multiple of 128)
 
 
 def gemv_norm_swiglu(x_in, res_t, res_s, g, lin, s_out, silu, h, part, x_out=None, t=None):

@@ -97,8 +97,8 @@ int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, const int64_t*
                              int32_t* s_out, int16_t* xq_out, int32_t R, int32_t N, int32_t K, void* stream);
 
 /* Waves per block that exact_gemv_g128_norm_acc launches for R rows of an N x K linear on cus compute units (cus <= 0:
- * the current device's): 8 when the rows are wider than 1024 and the group-split tasks fit one round of 8-wave blocks
- * (each CU then normalises the rows once), else 4; 0 for sizes the launch refuses. A host-side query (no launch), so
+ * the current device's): 8 when the rows are wider than 1024 and the group-split tasks fit one round of 8-wave blocks,
+ * or do with the split capped at no fewer than 8 parts (each CU then normalises the rows once), else 4; 0 for sizes the launch refuses. A host-side query (no launch), so
  * a caller choosing between the fused norm and a separate norm launch reads the kernel's own split. No counterpart in
  * the reference. */
 int exact_gemv_g128_norm_acc_blockwaves(int32_t R, int32_t N, int32_t K, int32_t cus);
@@ -143,7 +143,7 @@ int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const int16_t* mp
                            void* stream);
 
 /* exact_gemv_g128_swiglu on rows the launch normalises itself, as exact_gemv_g128_norm_acc (decode rows, R <= 2,
- * K <= 2048): every block computes x = x_in + round_shift(res_t, 28 - res_s[r]) (res_t may be NULL) and
+ * K <= 8192; above 2048 I a multiple of 128 or I / 64 at most the CU count): every block computes x = x_in + round_shift(res_t, 28 - res_s[r]) (res_t may be NULL) and
  * xq, s = qrow(irms(x, g), 15) while its first weight tiles load, then the SwiGLU GEMV on xq with those row shifts.
  * Block 0 writes x to x_out (NULL: not written; must not alias x_in or res_t) and s to s_out. h, part and t as
  * exact_gemv_g128_swiglu. Replaces exact_rmsnorm_qrow + exact_gemv_g128_acc + exact_swiglu_qrow

@@ -500,11 +500,13 @@ def test_gemv_norm_acc(thr, kind, R, N, K):
 
 
 @pytest.mark.parametrize("kind", ["plain", "huge", "zeros", "tiny", "leftshift", "nores"])
-@pytest.mark.parametrize("R,I,K", [(1, 4864, 896), (2, 4864, 896), (1, 2816, 2048), (2, 640, 1024), (1, 64, 128)])
+@pytest.mark.parametrize("R,I,K", [(1, 4864, 896), (2, 4864, 896), (1, 2816, 2048), (2, 640, 1024), (1, 64, 128),
+                                   (1, 18944, 3584), (2, 13824, 5120), (1, 192, 2176)])
 def test_gemv_norm_swiglu(thr, kind, R, I, K):
     """exact_gemv_g128_norm_swiglu: x = x_in + rs(res_t, 28 - res_s), xq, s = qrow(irms(x, g), 15), h = SwiGLU of the
     gate|up totals xq . W with the row shifts s, part = bit length of max |h| per 32 columns, t = the totals, x_out = x,
-    s_out = s, against the oracle; h and part feed the quantising down GEMV as the unfused path's do."""
+    s_out = s, against the oracle; h and part feed the quantising down GEMV as the unfused path's do. Rows wider than
+    2048 run 8-wave blocks: 4 pairs x 2 k parts (the 7B's I = 18944) or 2 x 4 (the 14B's 13824, and I = 192)."""
     from exact_amd.tables import silu_t
     rng_ = np.random.default_rng(R * 1000 + K + I + len(kind))
     lin, kw, km = synth_lin(thr, 22, f"nsw{I}x{K}", 2 * I, K)
@@ -548,11 +550,11 @@ def test_gemv_norm_swiglu(thr, kind, R, I, K):
 
 
 def test_gemv_norm_swiglu_refuses_unsupported_shapes(thr):
-    """More than 2 rows, rows wider than 2048, or I not a multiple of 64: 'unsupported'; x_out aliasing x_in: bad
+    """More than 2 rows, rows wider than 8192, or I not a multiple of 64: 'unsupported'; x_out aliasing x_in: bad
     argument."""
     from exact_amd.tables import silu_t
     st = dev(silu_t(), I32)
-    for R, I, K in ((3, 64, 128), (1, 64, 2176), (1, 96, 128)):
+    for R, I, K in ((3, 64, 128), (1, 64, 8320), (1, 96, 128)):
         lin, _, _ = synth_lin(thr, 24, f"nswbad{R}{I}{K}", 2 * I, K)
         with pytest.raises(ops.ExactError, match="unsupported"):
             ops.gemv_norm_swiglu(torch.zeros((R, K), dtype=I64, device=DEV), None, None,
