@@ -133,8 +133,10 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #define ATT_DS 4
 #endif
 // launches whose (row, head) blocks run in several rounds (batched decode): the 8-threads-per-key path up to
-// 4 ATT_THREADS / 8 cached positions (14B bs8 at a 135-token context, in isolation: 19.6 -> 11.5 us, against 13.7 us
-// for exact_qkv_rope_cache + exact_attention), ATT_MR_VPF value pairs prefetched (1 to 8: level)
+// 4 ATT_THREADS / 8 cached positions (14B bs8 at a 135-token context, warm caches: 19.6 -> 11.5 us, against 13.7 us
+// for exact_qkv_rope_cache + exact_attention), the exp table read from global memory (ATT_MR_GT; cold caches, 48
+// layers' KV in turn: 17.0 us against 25.6 with the table staged into LDS) and ATT_MR_VPF value pairs prefetched
+// (cold: 4 18.1 us, 8 17.0, 12 22.8, 16 20.6; 14B bs8 decode 5.32-5.33 -> 5.27-5.29 ms a step with 8 against 4)
 #ifndef ATT_KS8_MR
 #define ATT_KS8_MR 1
 #endif
@@ -143,7 +145,10 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #define ATT_GT1 1
 #endif
 #ifndef ATT_MR_VPF
-#define ATT_MR_VPF 4
+#define ATT_MR_VPF 8
+#endif
+#ifndef ATT_MR_GT
+#define ATT_MR_GT 1
 #endif
 #ifndef ATT_VPF_LONG_BLOCKS
 #define ATT_VPF_LONG_BLOCKS 256
@@ -654,9 +659,9 @@ extern "C" int exact_attention_qkv_split(const int64_t* t, const int32_t* s, con
   const int ds = ks8_wide || ks8_wide4 || (ks8_narrow && hd < ATT_KS8_WIDE_HD) ? att_qkv_ds(obn, blocks, hd) : 1;
   if (ks8_mr) {
     if (Smax <= 2 * (ATT_THREADS / 8))
-      att_qkv_go<ATT_MR_VPF, ATT_THREADS, ATT_KPF, 8, 2, 1, true>(ATT_QKV_ARGS);
+      att_qkv_go<ATT_MR_VPF, ATT_THREADS, ATT_KPF, 8, 2, 1, ATT_MR_GT != 0>(ATT_QKV_ARGS);
     else
-      att_qkv_go<ATT_MR_VPF, ATT_THREADS, ATT_KPF, 8, 4, 1, true>(ATT_QKV_ARGS);
+      att_qkv_go<ATT_MR_VPF, ATT_THREADS, ATT_KPF, 8, 4, 1, ATT_MR_GT != 0>(ATT_QKV_ARGS);
   } else if (ks8_wide4) {
     // value prefetch: 2 ATT_WIDE_THREADS DS / hd threads per pair cover the up to 512 positions in VPF steps
     if (ds == 4)
