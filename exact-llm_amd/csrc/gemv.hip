@@ -1099,6 +1099,9 @@ extern "C" int exact_gemv(const int16_t* x, const int8_t* wT, const int64_t* Mg,
 #define GEMV_NORM_BW8_K 1024   // rows wider than this (MoE q|k|v 6144 x 2048, A/B: 1.98-2.00 -> 1.95-1.97 ms a step)
 #endif
 #define GEMV_NORM_KMAX (256 * 24)
+#ifndef GEMV_NORM_EPT10
+#define GEMV_NORM_EPT10 1
+#endif
 
 // rows wider than GEMV_NORM_BW8_K whose group-split tasks do not fit one round of 8-wave blocks: the split capped so
 // that they do, when that leaves at least GEMV_NORM_FIT_MIN splits (0: never)
@@ -1170,6 +1173,7 @@ extern "C" int exact_gemv_g128_norm_acc(const int64_t* x_in, int64_t* x_out, con
   do {                                                                                                                  \
     if (ept <= 4) NORM_GO(VR, 4);                                                                                       \
     else if (ept == 7 && bw8) NORM_GO_BW(VR, 7, 8);   /* 3584-wide rows over 512 threads: no padded slots */            \
+    else if (ept == 10 && bw8 && GEMV_NORM_EPT10) NORM_GO_BW(VR, 10, 8);   /* 5120-wide rows likewise */                   \
     else if (ept <= 8) NORM_GO(VR, 8);                                                                                  \
     else if (ept <= 14) NORM_GO(VR, 14);                                                                                \
     else if (ept <= 20) NORM_GO(VR, 20);                                                                                \

@@ -471,7 +471,7 @@ def _norm_case(kind, R, K, rng_):
 
 @pytest.mark.parametrize("kind", ["plain", "huge", "zeros", "tiny", "leftshift", "nores"])
 @pytest.mark.parametrize("R,N,K", [(1, 4608, 3584), (2, 1152, 896), (1, 7168, 5120), (2, 640, 2048), (1, 300, 6144), (2, 4608, 3584),
-                                   (1, 6144, 2048)])
+                                   (1, 6144, 2048), (2, 7168, 5120)])
 def test_gemv_norm_acc(thr, kind, R, N, K):
     """exact_gemv_g128_norm_acc: x = x_in + rs(res_t, 28 - res_s), t += qrow(irms(x, g), 15) . W, x_out = x, s_out, xq_out,
     against the oracle's irms / qrow / group linear; t starts from a running total."""
