@@ -1277,6 +1277,11 @@ extern "C" int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const 
 #define GEMV_NSW_THREADS (64 * GEMV_NSW_NPB * GEMV_NSW_KS)
 #define GEMV_NSW_KMAX (128 * 16)
 #define GEMV_NSW_WIDE_KMAX (128 * 64)   // wider rows (up to this): 8-wave blocks, see the launcher
+// rows of up to 4 values a thread (the 0.5B's 896 over 256 threads) hold 4, not 8 with padded slots: 0.5B bs1
+// decode 0.771-0.773 -> 0.749-0.750 ms a step
+#ifndef GEMV_NSW_EPT4
+#define GEMV_NSW_EPT4 1
+#endif
 
 extern "C" int exact_gemv_g128_norm_swiglu(const int64_t* x_in, int64_t* x_out, const int64_t* res_t, const int32_t* res_s,
                                            const int64_t* g, const int8_t* wp, const int16_t* mp, const int16_t* mh,
@@ -1338,9 +1343,9 @@ extern "C" int exact_gemv_g128_norm_swiglu(const int64_t* x_in, int64_t* x_out, 
                          nullptr, wp, mp, mh, nullptr, silu, h, part, t, R, I, K, G, x_in, x_out, res_t, res_s, g, s_out);   \
   } while (0)
   if (R == 1) {
-    if (ept <= 8) NSW_GO(1, 8); else NSW_GO(1, 16);
+    if (ept <= 4 && GEMV_NSW_EPT4) NSW_GO(1, 4); else if (ept <= 8) NSW_GO(1, 8); else NSW_GO(1, 16);
   } else {
-    if (ept <= 8) NSW_GO(2, 8); else NSW_GO(2, 16);
+    if (ept <= 4 && GEMV_NSW_EPT4) NSW_GO(2, 4); else if (ept <= 8) NSW_GO(2, 8); else NSW_GO(2, 16);
   }
 #undef NSW_GO
   return launch_status("gemv_g128_norm_swiglu");
