@@ -816,6 +816,13 @@ __global__ __launch_bounds__(256) void k_gemv_experts_xq(const int64_t* __restri
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+#ifndef ROWMAJ_DPP
+#define ROWMAJ_DPP 1
+#endif
+#ifndef ROWMAJ_BR
+#define ROWMAJ_BR 1
+#endif
+
 template <int CH>
 struct RowMajRow {
   v4i w[CH];
@@ -836,15 +843,20 @@ __device__ __forceinline__ void rowmaj_load(RowMajRow<CH>& R_, const int8_t* __r
   }
 }
 
-template <bool NT, int CH, int RPW>
-__global__ __launch_bounds__(256) void k_gemv_rowmajor(const int16_t* __restrict__ x, const int8_t* __restrict__ wT,
-                                                       const int64_t* __restrict__ Mg, int64_t* __restrict__ out, int N,
-                                                       int K, int G, int nranges, int out_mode) {
+// BR: one block per row block with one wave per K range (blockDim = 64 nranges, at most ROWMAJ_BR_MAX): the ranges'
+// row totals are added in LDS and stored once (no atomics, no clearing launch before)
+#define ROWMAJ_BR_MAX 16
+template <bool NT, int CH, int RPW, bool BR = false>
+__global__ __launch_bounds__(BR ? 64 * ROWMAJ_BR_MAX : 256) void k_gemv_rowmajor(
+    const int16_t* __restrict__ x, const int8_t* __restrict__ wT, const int64_t* __restrict__ Mg, int64_t* __restrict__ out,
+    int N, int K, int G, int nranges, int out_mode) {
   constexpr int rpw = RPW;
+  __shared__ int64_t red[BR ? ROWMAJ_BR_MAX : 1][RPW];
   const int lane = threadIdx.x & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));   // rows and range: scalar
+  const int wid = __builtin_amdgcn_readfirstlane(BR ? (int)blockIdx.x * nranges + (int)(threadIdx.x >> 6)
+                                                    : (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));   // rows and range: scalar
   const int nrb = (N + rpw - 1) / rpw;
-  if (wid >= nrb * nranges) return;
+  if (!BR && wid >= nrb * nranges) return;
   const int rb = wid / nranges, kr = wid - rb * nranges;
   const int kb0 = kr * CH * 1024;
   const int nck = ((K - kb0 < CH * 1024 ? K - kb0 : CH * 1024)) / 16;   // 16-byte chunks in the range
@@ -884,13 +896,27 @@ __global__ __launch_bounds__(256) void k_gemv_rowmajor(const int16_t* __restrict
       part += (int64_t)((sh << 8) + sl + (s1 << 7)) * cur.m[c];   // a = 0 past the range
     }
     if (r + 2 < RPW) rowmaj_load<NT, CH>(cur, wT, Mg, row(r + 2), K, G, kb0, nck, lane);
+    if (ROWMAJ_DPP) {
+      part = wave_sum64(part);   // row-level data movement and four reads of lanes, not six LDS-crossbar exchanges
+    } else {
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) part += __shfl_xor(part, o, 64);
-    if (lane == 0 && n0 + r < n1) {
+      for (int o = 1; o < 64; o <<= 1) part += __shfl_xor(part, o, 64);
+    }
+    if constexpr (BR) {
+      if (lane == 0) red[kr][r] = part;
+    } else if (lane == 0 && n0 + r < n1) {
       if (out_mode)
         atomicAdd(reinterpret_cast<unsigned long long*>(out + n0 + r), (unsigned long long)part);
       else
         out[n0 + r] = part;
+    }
+  }
+  if constexpr (BR) {
+    __syncthreads();
+    if (kr == 0 && lane < RPW && n0 + lane < n1) {
+      uint64_t tot = 0;
+      for (int k = 0; k < nranges; ++k) tot += (uint64_t)red[k][lane];
+      out[n0 + lane] = (int64_t)tot;
     }
   }
 }
@@ -1075,14 +1101,22 @@ extern "C" int exact_gemv(const int16_t* x, const int8_t* wT, const int64_t* Mg,
   const int64_t waves = (((int64_t)N + rpw - 1) / rpw) * nranges;
   if (waves > (1LL << 30)) return EXACT_E_UNSUPPORTED;
   hipStream_t st = as_stream(stream);
-  if (nranges > 1) {
+  // several K ranges: one block per row block, its waves the ranges (ROWMAJ_BR), else atomics into a cleared output
+  const bool br = ROWMAJ_BR && nranges > 1 && nranges <= ROWMAJ_BR_MAX;
+  if (nranges > 1 && !br) {
     int e = zero_bytes(out, (int64_t)N * 8, st);
     if (e) return e;
   }
-  const dim3 grid((unsigned)((waves + 3) / 4));
+  const dim3 grid((unsigned)(br ? (N + rpw - 1) / rpw : (waves + 3) / 4)), block(br ? 64 * nranges : 256);
   const int mode = nranges > 1 ? 1 : 0;
-#define ROWMAJ_GO(C, P) hipLaunchKernelGGL((k_gemv_rowmajor<GEMV_NT != 0, C, P>), grid, dim3(256), 0, st, x, wT, Mg, out, N, K, \
-                                           G, nranges, mode)
+#define ROWMAJ_GO(C, P)                                                                                                \
+  do {                                                                                                                 \
+    if (br)                                                                                                            \
+      hipLaunchKernelGGL((k_gemv_rowmajor<GEMV_NT != 0, C, P, true>), grid, block, 0, st, x, wT, Mg, out, N, K, G, nranges, \
+                         mode);                                                                                        \
+    else                                                                                                               \
+      hipLaunchKernelGGL((k_gemv_rowmajor<GEMV_NT != 0, C, P>), grid, block, 0, st, x, wT, Mg, out, N, K, G, nranges, mode); \
+  } while (0)
   if (ch == 2) {
     if (rpw == 8) ROWMAJ_GO(2, 8); else if (rpw == 4) ROWMAJ_GO(2, 4); else if (rpw == 2) ROWMAJ_GO(2, 2); else ROWMAJ_GO(2, 1);
   } else {
