@@ -1267,16 +1267,18 @@ extern "C" int exact_gemv_g128_qrow_acc(const int64_t* xs, int64_t ldx, const in
   return launch_status("gemv_g128_qrow_acc");
 }
 
-// The SwiGLU GEMV's blocks: GEMV_GU_NPB pairs of 32 gate columns (one slice bit length per block) x GEMV_GU_KS k parts
+// The SwiGLU GEMV's blocks: GEMV_GU_NPB pairs of 32 gate columns x GEMV_GU_KS k parts (rows above 2), GEMV_GU_KS1
+// k parts for one or two rows (the MoE shared expert's 11264 x 2048 at bs1: 4 parts of 4 groups, 1.725-1.740 ->
+// 1.704-1.723 ms a step; at 8 rows 4 parts cost the 14B 1%)
 #ifndef GEMV_GU_KS
 #define GEMV_GU_KS 2
+#endif
+#ifndef GEMV_GU_KS1
+#define GEMV_GU_KS1 4
 #endif
 #ifndef GEMV_GU_NPB
 #define GEMV_GU_NPB 1
 #endif
-// the slice bit lengths (part) are one per block, and every caller (the down GEMV's qrow, ops.SWIGLU_PART_COLS)
-// reads them as one per 32 gate columns: that holds only with one pair of 32 columns a block
-static_assert(GEMV_GU_NPB == 1, "part holds one slice bit length per 32 gate columns");
 
 extern "C" int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const int16_t* mp, const int16_t* mh,
                                       const int32_t* s, const int32_t* silu, int64_t* h, int32_t* part, int64_t* t,
@@ -1285,18 +1287,19 @@ extern "C" int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const 
   if (R > 8 || I % 64 || K % 128) return EXACT_E_UNSUPPORTED;
   if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(wp) & 15)) return EXACT_E_UNSUPPORTED;
   const int G = K / 128;
-  dim3 grid((unsigned)(I / (32 * GEMV_GU_NPB))), block(64 * GEMV_GU_NPB * GEMV_GU_KS);
+  const int ks = R <= 2 ? GEMV_GU_KS1 : GEMV_GU_KS;
+  dim3 grid((unsigned)(I / (32 * GEMV_GU_NPB))), block(64 * GEMV_GU_NPB * ks);
   hipStream_t st = as_stream(stream);
-#define GU_GO(VR)                                                                                                      \
+#define GU_GO(VR, KS)                                                                                                  \
   do {                                                                                                                 \
     if (mh)                                                                                                            \
-      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, GEMV_GU_NPB, GEMV_GU_KS, true>), grid, block, 0, st, x, wp, mp, mh, s, silu, \
-                         h, part, t, R, I, K, G);                                                                      \
+      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, GEMV_GU_NPB, KS, true>), grid, block, 0, st, x, wp, mp, mh, s,  \
+                         silu, h, part, t, R, I, K, G);                                                                \
     else                                                                                                               \
-      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, GEMV_GU_NPB, GEMV_GU_KS, false>), grid, block, 0, st, x, wp, mp, mh, s,    \
+      hipLaunchKernelGGL((k_gemv_gu_swiglu<GEMV_NT != 0, VR, GEMV_GU_NPB, KS, false>), grid, block, 0, st, x, wp, mp, mh, s, \
                          silu, h, part, t, R, I, K, G);                                                                \
   } while (0)
-  if (R == 1) GU_GO(1); else if (R == 2) GU_GO(2); else GU_GO(4);
+  if (R == 1) GU_GO(1, GEMV_GU_KS1); else if (R == 2) GU_GO(2, GEMV_GU_KS1); else GU_GO(4, GEMV_GU_KS);
 #undef GU_GO
   return launch_status("gemv_g128_swiglu");
 }
