@@ -288,19 +288,17 @@ __global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ 
 // kernel wrote it (attention's per-head bit lengths, or SwiGLU's per-slice ones). Each wave quantises the columns of
 // its own groups into LDS (xs[r][g0 * 128 ...g1 * 128), clipped to +-(2^abits - 1)) and runs the group loop on them;
 // block 0 writes s_out. Replaces a k_quant_rows launch + GEMV pair. t += x.W (accumulate).
+// block bid of the launch (the kernel below, or a launch that runs it beside another GEMV)
 template <int ABITS, bool NT, int VR, bool WIDE, int PL>
-__global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict__ xs, int64_t ldx,
-                                                      const int32_t* __restrict__ part, int nparts,
-                                                      const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
-                                                      const int16_t* __restrict__ mh, int64_t* __restrict__ t,
-                                                      int32_t* __restrict__ s_out, int R, int N, int K, int G, int nsplit,
-                                                      int gmax, int64_t* __restrict__ zero, int64_t zero_n) {
+__device__ __forceinline__ void g128_xq_body(const int64_t* __restrict__ xs, int64_t ldx, const int32_t* __restrict__ part,
+                                             int nparts, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                             const int16_t* __restrict__ mh, int64_t* __restrict__ t,
+                                             int32_t* __restrict__ s_out, int R, int N, int K, int G, int nsplit, int gmax,
+                                             int bid) {
   extern __shared__ __attribute__((aligned(16))) int8_t xlds[];
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += (int64_t)gridDim.x * blockDim.x)
-    zero[i] = 0;
   constexpr int EB = ABITS == 15 ? 2 : 1;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int task = blockIdx.x * 4 + wave;
+  const int task = bid * 4 + wave;
   const int nbs = (N + 63) >> 6;
   if (task >= nbs * nsplit) return;   // no block-wide barrier below
   const int nb = task / nsplit, sp = task - nb * nsplit;
@@ -325,7 +323,7 @@ __global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict_
       for (int k = 1; k < PL; ++k) pv = pw[k] > pv ? pw[k] : pv;
       const int m = wave_max_i32(pv);
       const int sh = m - ABITS > 0 ? m - ABITS : 0;
-      if (blockIdx.x == 0 && wave == 0 && lane == 0) s_out[r] = sh;
+      if (bid == 0 && wave == 0 && lane == 0) s_out[r] = sh;
 #pragma unroll
       for (int j = 0; j < XQ_LOADS; ++j) {
         const int i = lane + 64 * j;
@@ -355,6 +353,18 @@ __global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict_
       if (r < R && n < N) atomicAdd(reinterpret_cast<unsigned long long*>(t + (size_t)r * N + n), (unsigned long long)acc[q][v]);
     }
   }
+}
+
+template <int ABITS, bool NT, int VR, bool WIDE, int PL>
+__global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict__ xs, int64_t ldx,
+                                                      const int32_t* __restrict__ part, int nparts,
+                                                      const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                                      const int16_t* __restrict__ mh, int64_t* __restrict__ t,
+                                                      int32_t* __restrict__ s_out, int R, int N, int K, int G, int nsplit,
+                                                      int gmax, int64_t* __restrict__ zero, int64_t zero_n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += (int64_t)gridDim.x * blockDim.x)
+    zero[i] = 0;
+  g128_xq_body<ABITS, NT, VR, WIDE, PL>(xs, ldx, part, nparts, wp, mp, mh, t, s_out, R, N, K, G, nsplit, gmax, blockIdx.x);
 }
 
 // Operands of group g for one wave of the gate|up GEMV below: slots j = 0, 1 are sub-tiles qb, qb + 1 of the gate
@@ -396,18 +406,16 @@ __device__ __forceinline__ void load_gu_group(GroupRegs& G_, const int8_t* __res
 // x = x_in + rs(res_t, 28 - res_s) and qrow(irms(x, gain), 15) for each row into LDS while its first weight tiles load,
 // NE elements per thread; block 0 writes x to x_out and the row shifts to s_out), so one launch replaces
 // exact_rmsnorm_qrow + the gate|up GEMV + the SwiGLU.
-template <bool NT, int VR, int NPB, int KS, bool WIDE, int NE = 0>
-__global__ __launch_bounds__(64 * NPB * KS) void k_gemv_gu_swiglu(const int16_t* __restrict__ x, const int8_t* __restrict__ wp,
-                                                             const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
-                                                             const int32_t* __restrict__ s, const int32_t* __restrict__ silu,
-                                                             int64_t* __restrict__ hout, int32_t* __restrict__ part,
-                                                             int64_t* __restrict__ tout, int R, int I, int K, int G,
-                                                             const int64_t* __restrict__ x_in = nullptr,
-                                                             int64_t* __restrict__ x_out = nullptr,
-                                                             const int64_t* __restrict__ res_t = nullptr,
-                                                             const int32_t* __restrict__ res_s = nullptr,
-                                                             const int64_t* __restrict__ gain = nullptr,
-                                                             int32_t* __restrict__ s_out = nullptr) {
+template <bool NT, int VR, int NPB, int KS, bool WIDE, int NE>
+__device__ __forceinline__ void gu_swiglu_body(const int16_t* __restrict__ x, const int8_t* __restrict__ wp,
+                                               const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
+                                               const int32_t* __restrict__ s, const int32_t* __restrict__ silu,
+                                               int64_t* __restrict__ hout, int32_t* __restrict__ part,
+                                               int64_t* __restrict__ tout, int R, int I, int K, int G,
+                                               const int64_t* __restrict__ x_in, int64_t* __restrict__ x_out,
+                                               const int64_t* __restrict__ res_t, const int32_t* __restrict__ res_s,
+                                               const int64_t* __restrict__ gain, int32_t* __restrict__ s_out, int bid,
+                                               int nblk) {
   __shared__ int64_t cmb[KS > 1 ? (KS - 1) * NPB * 4 * VR * 64 : 1];
   __shared__ int pm[NPB][8];
   extern __shared__ __attribute__((aligned(16))) int8_t xlds[];   // NE > 0: R rows of K int16 values
@@ -415,7 +423,7 @@ __global__ __launch_bounds__(64 * NPB * KS) void k_gemv_gu_swiglu(const int16_t*
   __shared__ int32_t s_lds[8];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int p = wave % NPB, kp = wave / NPB;
-  const int pair = blockIdx.x * NPB + p;   // 32 gate columns: sub-tiles qb, qb + 1 of 64-column tile nb
+  const int pair = bid * NPB + p;   // 32 gate columns: sub-tiles qb, qb + 1 of 64-column tile nb
   const int nb = pair >> 1, qb = 2 * (pair & 1), nbs = (2 * I) >> 6, ub = I >> 6;
   const int g0 = (int)(((int64_t)kp * G) / KS), g1 = (int)(((int64_t)(kp + 1) * G) / KS);
   const int row = lane & 15, c = lane >> 4;
@@ -438,10 +446,10 @@ __global__ __launch_bounds__(64 * NPB * KS) void k_gemv_gu_swiglu(const int16_t*
                                        g0, row, c);
       int16_t* xl = reinterpret_cast<int16_t*>(xlds);
       for (int r = 0; r < R; ++r)
-        norm_qrow_row<NE>(r, blockDim.x, x_in, res_t, res_s, gain, 15, K, xl + (size_t)r * K, blockIdx.x == 0 ? x_out : nullptr,
+        norm_qrow_row<NE>(r, blockDim.x, x_in, res_t, res_s, gain, 15, K, xl + (size_t)r * K, bid == 0 ? x_out : nullptr,
                           nullptr, s_lds, nullptr, nullptr, nsc);
       __syncthreads();
-      if (blockIdx.x == 0 && (int)threadIdx.x < R) s_out[threadIdx.x] = s_lds[threadIdx.x];
+      if (bid == 0 && (int)threadIdx.x < R) s_out[threadIdx.x] = s_lds[threadIdx.x];
       if (g0 >= g1) goto combine;
       load_x<15>(ra, xrow, g0, c);
     } else {
@@ -515,8 +523,24 @@ combine:
   __syncthreads();
   if ((int)threadIdx.x < R * NPB) {   // one bit length per pair (32 columns) and row, whatever NPB
     const int r = threadIdx.x / NPB, q = threadIdx.x - r * NPB;
-    part[(size_t)r * gridDim.x * NPB + blockIdx.x * NPB + q] = pm[q][r];
+    part[(size_t)r * nblk * NPB + bid * NPB + q] = pm[q][r];
   }
+}
+
+template <bool NT, int VR, int NPB, int KS, bool WIDE, int NE = 0>
+__global__ __launch_bounds__(64 * NPB * KS) void k_gemv_gu_swiglu(const int16_t* __restrict__ x, const int8_t* __restrict__ wp,
+                                                             const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
+                                                             const int32_t* __restrict__ s, const int32_t* __restrict__ silu,
+                                                             int64_t* __restrict__ hout, int32_t* __restrict__ part,
+                                                             int64_t* __restrict__ tout, int R, int I, int K, int G,
+                                                             const int64_t* __restrict__ x_in = nullptr,
+                                                             int64_t* __restrict__ x_out = nullptr,
+                                                             const int64_t* __restrict__ res_t = nullptr,
+                                                             const int32_t* __restrict__ res_s = nullptr,
+                                                             const int64_t* __restrict__ gain = nullptr,
+                                                             int32_t* __restrict__ s_out = nullptr) {
+  gu_swiglu_body<NT, VR, NPB, KS, WIDE, NE>(x, wp, mp, mh, s, silu, hout, part, tout, R, I, K, G, x_in, x_out, res_t, res_s,
+                                            gain, s_out, blockIdx.x, gridDim.x);
 }
 
 // GEMV whose int16 input rows are normalised in its own prologue (decode): every block recomputes, for each of its R
@@ -623,22 +647,19 @@ __global__ __launch_bounds__(256) void k_gemv_experts(const void* __restrict__ x
 // exact_llm.py:179) and part[(p0 + r) (I / 32) + b % (I / 32)] = bit length of max |h| over the 32 columns. Blocks past
 // the dispatched chunks exit.
 template <bool NT, int KS>
-__global__ __launch_bounds__(64 * KS) void k_gemv_experts_swiglu(const int16_t* __restrict__ x, const int32_t* __restrict__ row_map,
-                                                            const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
-                                                            int64_t w_stride, int64_t m_stride,
-                                                            const int32_t* __restrict__ chunk_e,
-                                                            const int32_t* __restrict__ chunk_p0,
-                                                            const int32_t* __restrict__ chunk_n,
-                                                            const int32_t* __restrict__ nchunks,
-                                                            const int32_t* __restrict__ s_pair, const int32_t* __restrict__ silu,
-                                                            int64_t* __restrict__ hout, int32_t* __restrict__ part, int I,
-                                                            int K, int G) {
+__device__ __forceinline__ void experts_swiglu_body(const int16_t* __restrict__ x, const int32_t* __restrict__ row_map,
+                                                    const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                                    int64_t w_stride, int64_t m_stride, const int32_t* __restrict__ chunk_e,
+                                                    const int32_t* __restrict__ chunk_p0, const int32_t* __restrict__ chunk_n,
+                                                    const int32_t* __restrict__ nchunks, const int32_t* __restrict__ s_pair,
+                                                    const int32_t* __restrict__ silu, int64_t* __restrict__ hout,
+                                                    int32_t* __restrict__ part, int I, int K, int G, int bid) {
   constexpr int VR = 4;
   __shared__ int64_t cmb[KS > 1 ? (KS - 1) * 4 * VR * 64 : 1];
   __shared__ int pm[VR];
   const int lane = threadIdx.x & 63, kp = threadIdx.x >> 6;
   const int npb = I / 32;
-  const int ch = blockIdx.x / npb, pb = blockIdx.x - ch * npb;
+  const int ch = bid / npb, pb = bid - ch * npb;
   if (ch >= nchunks[0]) return;   // uniform over the block: before any barrier
   const int e = chunk_e[ch], p0 = chunk_p0[ch];
   const int R = chunk_n[ch] < VR ? chunk_n[ch] : VR;
@@ -715,22 +736,37 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_experts_swiglu(const int16_t* 
   if ((int)threadIdx.x < R) part[(size_t)(p0 + threadIdx.x) * npb + pb] = pm[threadIdx.x];
 }
 
+template <bool NT, int KS>
+__global__ __launch_bounds__(64 * KS) void k_gemv_experts_swiglu(const int16_t* __restrict__ x, const int32_t* __restrict__ row_map,
+                                                            const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                                            int64_t w_stride, int64_t m_stride,
+                                                            const int32_t* __restrict__ chunk_e,
+                                                            const int32_t* __restrict__ chunk_p0,
+                                                            const int32_t* __restrict__ chunk_n,
+                                                            const int32_t* __restrict__ nchunks,
+                                                            const int32_t* __restrict__ s_pair, const int32_t* __restrict__ silu,
+                                                            int64_t* __restrict__ hout, int32_t* __restrict__ part, int I,
+                                                            int K, int G) {
+  experts_swiglu_body<NT, KS>(x, row_map, wp, mp, w_stride, m_stride, chunk_e, chunk_p0, chunk_n, nchunks, s_pair, silu, hout,
+                              part, I, K, G, blockIdx.x);
+}
+
 // The routed experts' down GEMV quantising its int64 input rows itself (MoE decode, chunks of at most 4 pairs): task =
 // (chunk, 64-row block, group split) as k_gemv_experts; pair p0 + r's row xs[p0 + r] (ldx apart) is quantised with
 // s = max(bitlen(max |row|) - 15, 0), bitlen(max |row|) = max_i part[(p0 + r) nparts + i] (qrow, exact_llm.py:41-46),
 // into the wave's LDS slice (as k_gemv_g128_xq); t[p0 + r] += q(row) . W_e (64-bit atomics), s_out[p0 + r] = s.
 template <bool NT, int PL>
-__global__ __launch_bounds__(256) void k_gemv_experts_xq(const int64_t* __restrict__ xs, int64_t ldx,
-                                                         const int32_t* __restrict__ part, int nparts,
-                                                         const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
-                                                         int64_t w_stride, int64_t m_stride, const int32_t* __restrict__ chunk_e,
-                                                         const int32_t* __restrict__ chunk_p0, const int32_t* __restrict__ chunk_n,
-                                                         const int32_t* __restrict__ nchunks, int64_t* __restrict__ t,
-                                                         int32_t* __restrict__ s_out, int N, int K, int G, int nsplit, int gmax) {
+__device__ __forceinline__ void experts_xq_body(const int64_t* __restrict__ xs, int64_t ldx, const int32_t* __restrict__ part,
+                                                int nparts, const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                                int64_t w_stride, int64_t m_stride, const int32_t* __restrict__ chunk_e,
+                                                const int32_t* __restrict__ chunk_p0, const int32_t* __restrict__ chunk_n,
+                                                const int32_t* __restrict__ nchunks, int64_t* __restrict__ t,
+                                                int32_t* __restrict__ s_out, int N, int K, int G, int nsplit, int gmax,
+                                                int bid) {
   constexpr int VR = 4;
   extern __shared__ __attribute__((aligned(16))) int8_t xlds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int task = blockIdx.x * 4 + wave;
+  const int task = bid * 4 + wave;
   const int nbs = (N + 63) >> 6;
   const int per_chunk = nbs * nsplit;
   const int ch = task / per_chunk;
@@ -789,6 +825,18 @@ __global__ __launch_bounds__(256) void k_gemv_experts_xq(const int64_t* __restri
         atomicAdd(reinterpret_cast<unsigned long long*>(t + (size_t)(p0 + r) * N + n), (unsigned long long)acc[q][v]);
     }
   }
+}
+
+template <bool NT, int PL>
+__global__ __launch_bounds__(256) void k_gemv_experts_xq(const int64_t* __restrict__ xs, int64_t ldx,
+                                                         const int32_t* __restrict__ part, int nparts,
+                                                         const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
+                                                         int64_t w_stride, int64_t m_stride, const int32_t* __restrict__ chunk_e,
+                                                         const int32_t* __restrict__ chunk_p0, const int32_t* __restrict__ chunk_n,
+                                                         const int32_t* __restrict__ nchunks, int64_t* __restrict__ t,
+                                                         int32_t* __restrict__ s_out, int N, int K, int G, int nsplit, int gmax) {
+  experts_xq_body<NT, PL>(xs, ldx, part, nparts, wp, mp, w_stride, m_stride, chunk_e, chunk_p0, chunk_n, nchunks, t, s_out, N, K,
+                          G, nsplit, gmax, blockIdx.x);
 }
 
 // The reference's exact::gemv on its own tensors (speed_fair_kaggle.py:686-702): one int16 row x (K,), the
@@ -1050,6 +1098,57 @@ int gemv_launch(const void* x, int abits, const int8_t* wp, const int16_t* mp, c
   }
 #undef GEMV_GO
   return launch_status("gemv_g128");
+}
+
+// MoE decode: the routed experts' SwiGLU GEMV and the shared expert's (R rows of the same activations) in one launch:
+// blocks below B1 are k_gemv_experts_swiglu's, the others k_gemv_gu_swiglu's (both 4 waves a block)
+template <bool NT, int VR, bool WIDE>
+__global__ __launch_bounds__(256) void k_moe_swiglu_pair(const int16_t* __restrict__ x, const int32_t* __restrict__ row_map,
+                                                         const int8_t* __restrict__ ewp, const int16_t* __restrict__ emp,
+                                                         int64_t w_stride, int64_t m_stride,
+                                                         const int32_t* __restrict__ chunk_e,
+                                                         const int32_t* __restrict__ chunk_p0,
+                                                         const int32_t* __restrict__ chunk_n,
+                                                         const int32_t* __restrict__ nchunks,
+                                                         const int32_t* __restrict__ s_pair, const int32_t* __restrict__ silu,
+                                                         int64_t* __restrict__ eh, int32_t* __restrict__ epart, int EI,
+                                                         const int8_t* __restrict__ swp, const int16_t* __restrict__ smp,
+                                                         const int16_t* __restrict__ smh, const int32_t* __restrict__ s,
+                                                         int64_t* __restrict__ sh, int32_t* __restrict__ spart, int R, int SI,
+                                                         int K, int B1, int B2) {
+  if ((int)blockIdx.x < B1)
+    experts_swiglu_body<NT, 4>(x, row_map, ewp, emp, w_stride, m_stride, chunk_e, chunk_p0, chunk_n, nchunks, s_pair, silu,
+                               eh, epart, EI, K, K / 128, blockIdx.x);
+  else
+    gu_swiglu_body<NT, VR, 1, 4, WIDE, 0>(x, swp, smp, smh, s, silu, sh, spart, nullptr, R, SI, K, K / 128, nullptr, nullptr,
+                                           nullptr, nullptr, nullptr, nullptr, (int)blockIdx.x - B1, B2);
+}
+
+// ... and the two down GEMVs that quantise those SwiGLU rows: blocks below B1 are k_gemv_experts_xq's, the others
+// k_gemv_g128_xq's; every block also clears its share of zero
+template <bool NT, int VR, bool WIDE, int PLE, int PLS>
+__global__ __launch_bounds__(256) void k_moe_qrow_pair(const int64_t* __restrict__ exs, int64_t eldx,
+                                                       const int32_t* __restrict__ epart, int enparts,
+                                                       const int8_t* __restrict__ ewp, const int16_t* __restrict__ emp,
+                                                       int64_t w_stride, int64_t m_stride, const int32_t* __restrict__ chunk_e,
+                                                       const int32_t* __restrict__ chunk_p0,
+                                                       const int32_t* __restrict__ chunk_n,
+                                                       const int32_t* __restrict__ nchunks, int64_t* __restrict__ et,
+                                                       int32_t* __restrict__ es_out, int EN, int EK, int ensplit, int egmax,
+                                                       const int64_t* __restrict__ sxs, int64_t sldx,
+                                                       const int32_t* __restrict__ spart, int snparts,
+                                                       const int8_t* __restrict__ swp, const int16_t* __restrict__ smp,
+                                                       const int16_t* __restrict__ smh, int64_t* __restrict__ st,
+                                                       int32_t* __restrict__ ss_out, int R, int SN, int SK, int snsplit,
+                                                       int sgmax, int64_t* __restrict__ zero, int64_t zero_n, int B1) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += (int64_t)gridDim.x * blockDim.x)
+    zero[i] = 0;
+  if ((int)blockIdx.x < B1)
+    experts_xq_body<NT, PLE>(exs, eldx, epart, enparts, ewp, emp, w_stride, m_stride, chunk_e, chunk_p0, chunk_n, nchunks, et,
+                             es_out, EN, EK, EK / 128, ensplit, egmax, blockIdx.x);
+  else
+    g128_xq_body<15, NT, VR, WIDE, PLS>(sxs, sldx, spart, snparts, swp, smp, smh, st, ss_out, R, SN, SK, SK / 128, snsplit,
+                                        sgmax, (int)blockIdx.x - B1);
 }
 
 static int check_linear(const void* x, int abits, const int8_t* wp, const int16_t* mp, int64_t* t, int R, int N, int K) {
@@ -1505,4 +1604,96 @@ extern "C" int exact_gemv_g128_experts_qrow_acc(const int64_t* xs, int64_t ldx, 
     hipLaunchKernelGGL((k_gemv_experts_xq<GEMV_NT != 0, XQ_PARTS_WIDE>), grid, block, lds, st, xs, ldx, part, nparts, wp, mp,
                        w_stride, m_stride, chunk_e, chunk_p0, chunk_n, nchunks, t, s_out, N, K, G, (int)ns, gmax);
   return launch_status("gemv_g128_experts_qrow_acc");
+}
+
+extern "C" int exact_moe_swiglu_pair(const int16_t* x, const int32_t* row_map, const int8_t* ewp, const int16_t* emp,
+                                     int64_t w_stride, int64_t m_stride, const int32_t* chunk_e, const int32_t* chunk_p0,
+                                     const int32_t* chunk_n, const int32_t* nchunks, int32_t max_chunks, int32_t chunk,
+                                     const int32_t* s_pair, const int32_t* silu, int64_t* eh, int32_t* epart, int32_t EI,
+                                     const int8_t* swp, const int16_t* smp, const int16_t* smh, const int32_t* s, int64_t* sh,
+                                     int32_t* spart, int32_t R, int32_t SI, int32_t K, void* stream) {
+  if (!x || !ewp || !emp || !s_pair || !silu || !eh || !epart || !swp || !smp || !s || !sh || !spart) return EXACT_E_ARG;
+  if (EI <= 0 || SI <= 0 || K <= 0 || R <= 0) return EXACT_E_ARG;
+  int e = check_chunks(chunk_e, chunk_p0, chunk_n, nchunks, max_chunks, chunk, w_stride, m_stride);
+  if (e) return e;
+  if (R > 2 || EI % 64 || SI % 64 || K % 128 || GEMV_EXP_KS != 4 || GEMV_GU_KS1 != 4 || GEMV_GU_NPB != 1)
+    return EXACT_E_UNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(ewp) & 15) || (reinterpret_cast<uintptr_t>(swp) & 15))
+    return EXACT_E_UNSUPPORTED;
+  const int64_t B1 = (int64_t)max_chunks * (EI / 32), B2 = SI / 32;
+  if (B1 + B2 > (1LL << 30)) return EXACT_E_UNSUPPORTED;
+  hipStream_t st = as_stream(stream);
+#define PAIR_GO(VR, W)                                                                                                 \
+  hipLaunchKernelGGL((k_moe_swiglu_pair<GEMV_NT != 0, VR, W>), dim3((unsigned)(B1 + B2)), dim3(256), 0, st, x, row_map, ewp, \
+                     emp, w_stride, m_stride, chunk_e, chunk_p0, chunk_n, nchunks, s_pair, silu, eh, epart, EI, swp, smp,  \
+                     smh, s, sh, spart, R, SI, K, (int)B1, (int)B2)
+  if (smh) {
+    if (R == 1) PAIR_GO(1, true); else PAIR_GO(2, true);
+  } else {
+    if (R == 1) PAIR_GO(1, false); else PAIR_GO(2, false);
+  }
+#undef PAIR_GO
+  return launch_status("moe_swiglu_pair");
+}
+
+extern "C" int exact_moe_qrow_pair(const int64_t* exs, int64_t eldx, const int32_t* epart, int32_t enparts, const int8_t* ewp,
+                                   const int16_t* emp, int64_t w_stride, int64_t m_stride, const int32_t* chunk_e,
+                                   const int32_t* chunk_p0, const int32_t* chunk_n, const int32_t* nchunks, int32_t max_chunks,
+                                   int32_t chunk, int64_t* et, int32_t* es_out, int32_t EN, int32_t EK, const int64_t* sxs,
+                                   int64_t sldx, const int32_t* spart, int32_t snparts, const int8_t* swp, const int16_t* smp,
+                                   const int16_t* smh, int64_t* st, int32_t* ss_out, int32_t R, int32_t SN, int32_t SK,
+                                   int64_t* zero, int64_t zero_n, void* stream) {
+  if (!exs || !epart || !ewp || !emp || !et || !es_out || !sxs || !spart || !swp || !smp || !st || !ss_out) return EXACT_E_ARG;
+  if (EN <= 0 || EK <= 0 || SN <= 0 || SK <= 0 || R <= 0 || enparts <= 0 || snparts <= 0 || eldx < EK || sldx < SK)
+    return EXACT_E_ARG;
+  if (zero_n < 0 || (zero_n > 0 && !zero)) return EXACT_E_ARG;
+  int e = check_chunks(chunk_e, chunk_p0, chunk_n, nchunks, max_chunks, chunk, w_stride, m_stride);
+  if (e) return e;
+  if (R > 2 || EK % 128 || SK % 128 || (reinterpret_cast<uintptr_t>(ewp) & 15) || (reinterpret_cast<uintptr_t>(swp) & 15))
+    return EXACT_E_UNSUPPORTED;
+  // the routed experts' split, as exact_gemv_g128_experts_qrow_acc
+  const int EG = EK / 128;
+  const int64_t enbs = (EN + 63) / 64;
+  int64_t ens = (GEMV_WAVES + (int64_t)max_chunks * enbs - 1) / ((int64_t)max_chunks * enbs);
+  ens = ens < 1 ? 1 : (ens > EG ? EG : ens);
+  const int egmax = (int)((EG + ens - 1) / ens);
+  const size_t elds = (size_t)4 * EXPERT_FUSE_CHUNK * egmax * 128 * 2;
+  const int64_t etasks = (int64_t)max_chunks * enbs * ens;
+  // the shared expert's, as exact_gemv_g128_qrow_acc
+  const int SG = SK / 128;
+  const int sns = gemv_nsplit(SN, SG);
+  const int sgmax = (SG + sns - 1) / sns;
+  const size_t slds = (size_t)4 * R * sgmax * 128 * 2;
+  const int64_t stasks = (int64_t)((SN + 63) / 64) * sns;
+  if (elds > GEMV_XQ_LDS_MAX || slds > GEMV_XQ_LDS_MAX || egmax * 128 > 64 * XQ_LOADS || sgmax * 128 > 64 * XQ_LOADS ||
+      enparts > 64 * XQ_PARTS_WIDE || snparts > 64 * XQ_PARTS_WIDE)
+    return EXACT_E_UNSUPPORTED;
+  const int64_t B1 = (etasks + 3) / 4, B2 = (stasks + 3) / 4;
+  if (B1 + B2 > (1LL << 30)) return EXACT_E_UNSUPPORTED;
+  const size_t lds = elds > slds ? elds : slds;
+  hipStream_t sm = as_stream(stream);
+#define QP_GO(VR, W, PLE, PLS)                                                                                         \
+  hipLaunchKernelGGL((k_moe_qrow_pair<GEMV_NT != 0, VR, W, PLE, PLS>), dim3((unsigned)(B1 + B2)), dim3(256), lds, sm, exs,  \
+                     eldx, epart, enparts, ewp, emp, w_stride, m_stride, chunk_e, chunk_p0, chunk_n, nchunks, et, es_out, EN, \
+                     EK, (int)ens, egmax, sxs, sldx, spart, snparts, swp, smp, smh, st, ss_out, R, SN, SK, sns, sgmax, zero,  \
+                     zero_n, (int)B1)
+#define QP_PLS(VR, W, PLE)                                                                                             \
+  do {                                                                                                                 \
+    if (snparts <= 64) QP_GO(VR, W, PLE, 1);                                                                           \
+    else if (snparts <= 256) QP_GO(VR, W, PLE, 4);                                                                     \
+    else QP_GO(VR, W, PLE, XQ_PARTS_WIDE);                                                                             \
+  } while (0)
+#define QP_PLE(VR, W)                                                                                                  \
+  do {                                                                                                                 \
+    if (enparts <= 64) QP_PLS(VR, W, 1); else QP_PLS(VR, W, XQ_PARTS_WIDE);                                            \
+  } while (0)
+  if (smh) {
+    if (R == 1) QP_PLE(1, true); else QP_PLE(2, true);
+  } else {
+    if (R == 1) QP_PLE(1, false); else QP_PLE(2, false);
+  }
+#undef QP_PLE
+#undef QP_PLS
+#undef QP_GO
+  return launch_status("moe_qrow_pair");
 }

@@ -62,6 +62,9 @@ SIGNATURES = {
     "exact_gemm_g128_experts": [P, I32, P, P, P, I64, I64, P, P, P, P, P, P, I32, P, I32, I32, I32, P],
     "exact_gemv_g128_experts_swiglu": [P, P, P, P, I64, I64, P, P, P, P, I32, I32, P, P, P, P, I32, I32, P],
     "exact_gemv_g128_experts_qrow_acc": [P, I64, P, I32, P, P, I64, I64, P, P, P, P, I32, I32, P, P, I32, I32, P],
+    "exact_moe_swiglu_pair": [P, P, P, P, I64, I64, P, P, P, P, I32, I32, P, P, P, P, I32, P, P, P, P, P, P, I32, I32, I32, P],
+    "exact_moe_qrow_pair": [P, I64, P, I32, P, P, I64, I64, P, P, P, P, I32, I32, P, P, I32, I32, P, I64, P, I32, P, P, P, P, P,
+                            I32, I32, I32, P, I64, P],
     "exact_moe_combine": [P, P, P, P, P, P, P, P, I32, I32, I32, I32, P],
 }
 OTHER = {"exact_version": ([], ctypes.c_int), "exact_last_error": ([], ctypes.c_char_p),

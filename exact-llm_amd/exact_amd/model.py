@@ -283,6 +283,7 @@ class TModel:
     QKV_NORM = True   # dense decode rows wider than NORM_FUSE_D: the attention norm inside the q|k|v GEMV
     MOE_NORM = True   # MoE decode rows: the attention norm inside the q|k|v GEMV, the expert norm inside the router GEMV
     MOE_ROUTE = True   # MoE decode rows: top-k routing and dispatch in one launch
+    MOE_PAIR = True   # MoE decode rows: the routed and shared experts' GEMVs paired in one launch each (up, down)
     FFN_NORM = True   # decode rows with the attention norm in the q|k|v GEMV: the FFN norm in the SwiGLU GEMV too
     BATCH_ATTN = True   # batched decode rows: the q|k|v epilogue inside the attention launch
     ATT_SPLIT = 4   # decode attention with the q|k|v epilogue: bit lengths a head, so its p.V may run in that many blocks
@@ -559,10 +560,22 @@ class TModel:
             ops.router_topk(ws.t_rt, ws.s, tab.exp, k, ws.p_sel, ws.e_sel, clear=True, NE=c.NE, gate_col=ws.gate_col,
                             sig=tab.sig, gate=ws.gate)
             ops.moe_dispatch(ws.e_sel, ws.s, c.NE, k, chunk, ws.disp)
+        sfuse = (self.SHARED_SWIGLU and not grouped and self.abits == 15 and ws.R <= ops.SWIGLU_GEMV_ROWS and c.SI % 64 == 0
+                 and c.SI // ops.SWIGLU_PART_COLS <= ops.XQ_PARTS_MAX and L["sgu"].bias is None)
+        if efuse and ws.eh is None:
+            ws.eh = torch.zeros((P, c.MI), dtype=I64, device=self.dev)
+            ws.part_eh = torch.zeros(P * (c.MI // ops.SWIGLU_PART_COLS), dtype=I32, device=self.dev)
+        if sfuse and ws.hsh is None:
+            ws.hsh = torch.zeros((ws.R, c.SI), dtype=I64, device=self.dev)
+        if efuse and sfuse and self.MOE_PAIR and ws.R <= 2:
+            # decode rows: the routed and the shared experts' SwiGLU GEMVs in one launch, their down GEMVs in another
+            ops.moe_swiglu_pair(ws.xq, ws.disp["pair_row"], L["egu"], ws.disp, ws.disp["s_pair"], tab.silu, ws.eh,
+                                ws.part_eh, L["sgu"], ws.s, ws.hsh, ws.part_sw)
+            ops.moe_qrow_pair(ws.eh, ws.part_eh, c.MI // ops.SWIGLU_PART_COLS, L["edown"], ws.disp, ws.t_ed, ws.esh,
+                              ws.hsh, ws.part_sw, c.SI // ops.SWIGLU_PART_COLS, L["sd"], ws.t_sd, ws.ssh, zero=zero)
+            ops.moe_combine(x, ws.t_ed, ws.esh, ws.p_sel, ws.disp["pidx"], k, ws.t_sd, ws.ssh, ws.gate, clear=True)
+            return
         if efuse:
-            if ws.eh is None:
-                ws.eh = torch.zeros((P, c.MI), dtype=I64, device=self.dev)
-                ws.part_eh = torch.zeros(P * (c.MI // ops.SWIGLU_PART_COLS), dtype=I32, device=self.dev)
             ops.gemv_experts_swiglu(ws.xq, ws.disp["pair_row"], L["egu"], ws.disp, ws.disp["s_pair"], tab.silu, ws.eh,
                                     ws.part_eh)
             ops.gemv_experts_qrow_acc(ws.eh, ws.part_eh, c.MI // ops.SWIGLU_PART_COLS, L["edown"], ws.disp, ws.t_ed,
@@ -578,11 +591,8 @@ class TModel:
                 ops.gemm_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed, P)
             else:
                 ops.gemv_experts(ws.ehq, self.abits, None, L["edown"], ws.disp, ws.t_ed)
-        if (self.SHARED_SWIGLU and not grouped and self.abits == 15 and ws.R <= ops.SWIGLU_GEMV_ROWS and c.SI % 64 == 0
-                and c.SI // ops.SWIGLU_PART_COLS <= ops.XQ_PARTS_MAX and L["sgu"].bias is None):
+        if sfuse:
             # decode rows: the shared expert's SwiGLU in its gate|up GEMV's epilogue, the down GEMV quantises h
-            if ws.hsh is None:
-                ws.hsh = torch.zeros((ws.R, c.SI), dtype=I64, device=self.dev)
             ops.gemv_swiglu(ws.xq, L["sgu"], ws.s, tab.silu, ws.hsh, ws.part_sw)
             ops.gemv_qrow_acc(ws.hsh, ws.part_sw, c.SI // ops.SWIGLU_PART_COLS, self.abits, L["sd"], ws.t_sd, ws.ssh,
                               zero=zero)

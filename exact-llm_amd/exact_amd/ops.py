@@ -657,6 +657,45 @@ def gemv_experts_qrow_acc(xs, part, nparts, lin, disp, out, s_out, chunk=EXPERT_
     return out
 
 
+def moe_swiglu_pair(x, row_map, elin, disp, s_pair, silu, eh, epart, slin, s, sh, spart, chunk=EXPERT_FUSE_CHUNK):
+    """gemv_experts_swiglu(x, row_map, elin, disp, s_pair, silu, eh, epart) and gemv_swiglu(x, slin, s, silu, sh, spart)
+    (the shared expert, R <= 2 rows of x) in one launch."""
+    R, K = x.shape
+    EI, SI = elin.N // 2, slin.N // 2
+    P = eh.shape[0]
+    _need(x, I16, "x")
+    if elin.K != K or slin.K != K or elin.N % 2 or slin.N % 2 or eh.shape[1] != EI:
+        raise ExactError(f"moe_swiglu_pair: x {tuple(x.shape)} against ({elin.N}, {elin.K}) and ({slin.N}, {slin.K})")
+    _need_packed(slin, "moe_swiglu_pair")
+    _lib.call("exact_moe_swiglu_pair", _ptr(x), _ptr(row_map), _ptr(elin.wp), _ptr(elin.mp), elin.w_stride, elin.m_stride,
+              *_chunks(disp), chunk, _ptr(_need(s_pair, I32, "s_pair", P)), _ptr(silu), _ptr(_need(eh, I64, "eh", P * EI)),
+              _ptr(_need(epart, I32, "epart", P * (EI // SWIGLU_PART_COLS))), EI, _ptr(slin.wp), _ptr(slin.mp),
+              _ptr(slin.mh), _ptr(_need(s, I32, "s", R)), _ptr(_need(sh, I64, "sh", R * SI)),
+              _ptr(_need(spart, I32, "spart", R * (SI // SWIGLU_PART_COLS))), R, SI, K, _stream())
+    return eh, sh
+
+
+def moe_qrow_pair(exs, epart, enparts, elin, disp, et, es_out, sxs, spart, snparts, slin, st, ss_out, zero=None,
+                  chunk=EXPERT_FUSE_CHUNK):
+    """gemv_experts_qrow_acc(exs, epart, enparts, elin, disp, et, es_out) and gemv_qrow_acc(sxs, spart, snparts, 15, slin,
+    st, ss_out, zero=zero) (the shared expert's down GEMV, R <= 2 rows) in one launch."""
+    P, eldx = exs.shape
+    R, sldx = sxs.shape
+    _need(exs, I64, "exs")
+    _need(sxs, I64, "sxs")
+    if eldx < elin.K or et.shape[1] != elin.N or sldx < slin.K:
+        raise ExactError(f"moe_qrow_pair: xs {tuple(exs.shape)} / {tuple(sxs.shape)} against ({elin.N}, {elin.K}) and "
+                         f"({slin.N}, {slin.K})")
+    _need_packed(slin, "moe_qrow_pair")
+    _lib.call("exact_moe_qrow_pair", _ptr(exs), eldx, _ptr(_need(epart, I32, "epart", P * enparts)), enparts, _ptr(elin.wp),
+              _ptr(elin.mp), elin.w_stride, elin.m_stride, *_chunks(disp), chunk, _ptr(_need(et, I64, "et", P * elin.N)),
+              _ptr(_need(es_out, I32, "es_out", P)), elin.N, elin.K, _ptr(sxs), sldx,
+              _ptr(_need(spart, I32, "spart", R * snparts)), snparts, _ptr(slin.wp), _ptr(slin.mp), _ptr(slin.mh),
+              _ptr(_need(st, I64, "st", R * slin.N)), _ptr(_need(ss_out, I32, "ss_out", R)), R, slin.N, slin.K,
+              _ptr(zero), 0 if zero is None else _need(zero, I64, "zero").numel(), _stream())
+    return et, st
+
+
 EXPERT_CHUNK = {15: 128, 7: 256}   # pairs per dispatched chunk for gemm_experts: one 256-row matrix-core tile
 _EXPERT_ROWS = {}                   # device -> int8 workspace of the gathered (digit) rows
 

@@ -362,6 +362,28 @@ int exact_gemv_g128_experts_qrow_acc(const int64_t* xs, int64_t ldx, const int32
                                      const int32_t* nchunks, int32_t max_chunks, int32_t chunk, int64_t* t,
                                      int32_t* s_out, int32_t N, int32_t K, void* stream);
 
+/* MoE decode (R <= 2 rows): exact_gemv_g128_experts_swiglu (the routed experts, expert linears ewp/emp of I = EI) and
+ * exact_gemv_g128_swiglu on the same rows x (the shared expert, swp/smp/smh of I = SI, row shifts s) in one launch:
+ * eh/epart and sh/spart as those two entries write them; K is both linears' K. No counterpart in the reference, whose
+ * MoE layer runs the experts and the shared expert one after the other (MoEInt.moe, moe_exact_kaggle.py:454-467). */
+int exact_moe_swiglu_pair(const int16_t* x, const int32_t* row_map, const int8_t* ewp, const int16_t* emp,
+                          int64_t w_stride, int64_t m_stride, const int32_t* chunk_e, const int32_t* chunk_p0,
+                          const int32_t* chunk_n, const int32_t* nchunks, int32_t max_chunks, int32_t chunk,
+                          const int32_t* s_pair, const int32_t* silu, int64_t* eh, int32_t* epart, int32_t EI,
+                          const int8_t* swp, const int16_t* smp, const int16_t* smh, const int32_t* s, int64_t* sh,
+                          int32_t* spart, int32_t R, int32_t SI, int32_t K, void* stream);
+
+/* ... and exact_gemv_g128_experts_qrow_acc (routed experts: exs, epart, ... et, es_out, EN x EK) with
+ * exact_gemv_g128_qrow_acc at abits 15 (the shared expert's down GEMV: sxs, spart, ... st, ss_out, SN x SK, R <= 2
+ * rows, clearing zero_n int64 of zero) in one launch. No counterpart in the reference, as above. */
+int exact_moe_qrow_pair(const int64_t* exs, int64_t eldx, const int32_t* epart, int32_t enparts, const int8_t* ewp,
+                        const int16_t* emp, int64_t w_stride, int64_t m_stride, const int32_t* chunk_e,
+                        const int32_t* chunk_p0, const int32_t* chunk_n, const int32_t* nchunks, int32_t max_chunks,
+                        int32_t chunk, int64_t* et, int32_t* es_out, int32_t EN, int32_t EK, const int64_t* sxs,
+                        int64_t sldx, const int32_t* spart, int32_t snparts, const int8_t* swp, const int16_t* smp,
+                        const int16_t* smh, int64_t* st, int32_t* ss_out, int32_t R, int32_t SN, int32_t SK,
+                        int64_t* zero, int64_t zero_n, void* stream);
+
 /* Combination (moe_exact_kaggle.py:463-467): x[r] += sum_j rs(p_sel[r][j] * rs(t_ed[pidx[r*k+j]], 28 - sh_pair), 20)
  *   + rs(gate[r] * rs(t_sd[r], 28 - sh_s[r]), 16)   (shared expert; skipped if t_sd is NULL).
  * clear_t != 0 leaves t_ed and t_sd zeroed. */

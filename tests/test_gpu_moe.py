@@ -383,3 +383,59 @@ def test_fused_expert_gemvs_match_oracle(tab, R, NE, k, MI, K, D):
         hq, hs = O.qrow(hv[None, :], 15)
         assert gs[p] == hs[0, 0], (q, e)
         assert np.array_equal(gt[p], (O.group_acc(hq, wd[e]) * Md[e][:, None, :]).sum(0)[0]), (q, e)
+
+
+@pytest.mark.parametrize("R,NE,k,MI,SI,K,D", [(1, 60, 4, 1408, 5632, 2048, 2048), (2, 8, 4, 128, 512, 256, 192),
+                                              (1, 6, 2, 256, 384, 384, 128)])
+def test_moe_pairs_match_the_separate_launches(tab, R, NE, k, MI, SI, K, D):
+    """exact_moe_swiglu_pair = exact_gemv_g128_experts_swiglu + exact_gemv_g128_swiglu (the shared expert on the same
+    rows) and exact_moe_qrow_pair = exact_gemv_g128_experts_qrow_acc + exact_gemv_g128_qrow_acc (with its clearing
+    range): every output equal to the separate launches' (those are pinned against the oracle above and in the
+    whole-model tests), at the Qwen1.5-MoE-A2.7B shapes and smaller ones."""
+    from exact_amd.ops import PackedLinear
+    rng = np.random.default_rng(R * 1000 + MI + SI)
+    thr = dev(synth.thresholds().astype(np.int64), I64).to(I32)
+    gu, dn = ops.ExpertLinears(NE, 2 * MI, K, DEV), ops.ExpertLinears(NE, D, MI, DEV)
+    used = sorted(rng.choice(NE, min(NE, k + 1), replace=False).tolist())
+    for e in used:
+        for lin, N, KK, tag in ((gu, 2 * MI, K, "g"), (dn, D, MI, "d")):
+            wp, mp = lin.part(e)
+            ops.synth_linear(wp, mp, N, KK, synth.key(41, f"{tag}{e}.w"), synth.key(41, f"{tag}{e}.m"), synth.M_LO, synth.M_HI,
+                             thr)
+
+    def packed(N, KK, tag):
+        wp, mp = PackedLinear.alloc(N, KK, DEV)
+        ops.synth_linear(wp, mp, N, KK, synth.key(43, tag + ".w"), synth.key(43, tag + ".m"), synth.M_LO, synth.M_HI, thr)
+        return PackedLinear(wp, mp, N, KK)
+    sgu, sdn = packed(2 * SI, K, "sgu"), packed(D, SI, "sd")
+    e_sel = np.stack([rng.choice(used, k, replace=False) for _ in range(R)])
+    x = dev(rng.integers(-32767, 32768, (R, K)), torch.int16)
+    s = dev(rng.integers(0, 8, R), I32)
+    P = R * k
+    disp = {n: torch.zeros((P,), dtype=I32, device=DEV) for n in ("pidx", "pair_row", "s_pair")}
+    nmax = ops.max_chunks(P, NE, ops.EXPERT_FUSE_CHUNK)
+    disp.update({n: torch.zeros((nmax,), dtype=I32, device=DEV) for n in ("chunk_e", "chunk_p0", "chunk_n")})
+    disp["nchunks"] = torch.zeros(1, dtype=I32, device=DEV)
+    ops.moe_dispatch(dev(e_sel, I32), s, NE, k, ops.EXPERT_FUSE_CHUNK, disp)
+    pc = ops.SWIGLU_PART_COLS
+    outs = []
+    for paired in (False, True):
+        eh = torch.full((P, MI), -3, dtype=I64, device=DEV)
+        ep = torch.full((P * (MI // pc),), -1, dtype=I32, device=DEV)
+        sh = torch.full((R, SI), -5, dtype=I64, device=DEV)
+        sp = torch.full((R * (SI // pc),), -1, dtype=I32, device=DEV)
+        et, st = torch.zeros((P, D), dtype=I64, device=DEV), torch.zeros((R, D), dtype=I64, device=DEV)
+        es, ss = torch.full((P,), -1, dtype=I32, device=DEV), torch.full((R,), -1, dtype=I32, device=DEV)
+        zero = torch.full((333,), 9, dtype=I64, device=DEV)
+        if paired:
+            ops.moe_swiglu_pair(x, disp["pair_row"], gu, disp, disp["s_pair"], tab.silu, eh, ep, sgu, s, sh, sp)
+            ops.moe_qrow_pair(eh, ep, MI // pc, dn, disp, et, es, sh, sp, SI // pc, sdn, st, ss, zero=zero)
+        else:
+            ops.gemv_experts_swiglu(x, disp["pair_row"], gu, disp, disp["s_pair"], tab.silu, eh, ep)
+            ops.gemv_swiglu(x, sgu, s, tab.silu, sh, sp)
+            ops.gemv_experts_qrow_acc(eh, ep, MI // pc, dn, disp, et, es)
+            ops.gemv_qrow_acc(sh, sp, SI // pc, 15, sdn, st, ss, zero=zero)
+        outs.append([host(v) for v in (eh, ep, sh, sp, et, es, st, ss, zero)])
+    for a, b, name in zip(outs[0], outs[1], ("eh", "epart", "sh", "spart", "et", "es", "st", "ss", "zero")):
+        assert np.array_equal(a, b), name
+    assert not outs[1][8].any()
