@@ -1408,7 +1408,8 @@ extern "C" int exact_gemv_g128_swiglu(const int16_t* x, const int8_t* wp, const 
 #define GEMV_NSW_ROWS 2
 #define GEMV_NSW_NPB GEMV_GU_NPB
 #ifndef GEMV_NSW_KS
-#define GEMV_NSW_KS 4   // 0.5B bs1 decode, A/B: KS 2 0.836-0.855 ms a step, 4 0.823-0.841, 8 0.841-0.859
+#define GEMV_NSW_KS 8   // 0.5B bs1 decode (2 values a thread of its 896-wide rows), A/B: KS 2 0.768-0.779 ms a step,
+                        // 4 0.744-0.753, 7 0.737-0.747, 8 0.736-0.745
 #endif
 #define GEMV_NSW_THREADS (64 * GEMV_NSW_NPB * GEMV_NSW_KS)
 #define GEMV_NSW_KMAX (128 * 16)
@@ -1479,9 +1480,9 @@ extern "C" int exact_gemv_g128_norm_swiglu(const int64_t* x_in, int64_t* x_out, 
                          nullptr, wp, mp, mh, nullptr, silu, h, part, t, R, I, K, G, x_in, x_out, res_t, res_s, g, s_out);   \
   } while (0)
   if (R == 1) {
-    if (ept <= 4 && GEMV_NSW_EPT4) NSW_GO(1, 4); else if (ept <= 8) NSW_GO(1, 8); else NSW_GO(1, 16);
+    if (ept <= 2) NSW_GO(1, 2); else if (ept <= 4 && GEMV_NSW_EPT4) NSW_GO(1, 4); else if (ept <= 8) NSW_GO(1, 8); else NSW_GO(1, 16);
   } else {
-    if (ept <= 4 && GEMV_NSW_EPT4) NSW_GO(2, 4); else if (ept <= 8) NSW_GO(2, 8); else NSW_GO(2, 16);
+    if (ept <= 2) NSW_GO(2, 2); else if (ept <= 4 && GEMV_NSW_EPT4) NSW_GO(2, 4); else if (ept <= 8) NSW_GO(2, 8); else NSW_GO(2, 16);
   }
 #undef NSW_GO
   return launch_status("gemv_g128_norm_swiglu");
