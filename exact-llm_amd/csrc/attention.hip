@@ -147,6 +147,17 @@ __global__ void k_qkv_rope_cache(int64_t* __restrict__ t, const int32_t* __restr
 #ifndef ATT_MR_VPF
 #define ATT_MR_VPF 8
 #endif
+#ifndef ATT_GQA
+#define ATT_GQA 1
+#endif
+#ifndef ATT_GQA_NT
+#define ATT_GQA_NT 512
+#endif
+// ... for caches longer than this (14B bs8, cold caches of 48 layers in turn: at 256 positions 23.2 against 25.1 us
+// a launch, at 148 positions 18.8 against 17.1, decode 5.37 against 5.28 ms a step; 1024-thread blocks: slower still)
+#ifndef ATT_GQA_MIN_S
+#define ATT_GQA_MIN_S 192
+#endif
 #ifndef ATT_MR_GT
 #define ATT_MR_GT 1
 #endif
@@ -597,6 +608,285 @@ __global__ __launch_bounds__(NT) void k_attention_qkv(const int64_t* __restrict_
   }
 }
 
+// Batched decode whose (row, head) blocks would take several rounds: one block per (row r, KV head kh, dimension slice
+// ds) for all HB = H / KV query heads of the group, so the group's cached keys and values are loaded once. The
+// arithmetic per head is k_attention_qkv's (8 threads per cached key, exp table read from global memory, the p.V of
+// hd / DS dimensions): the same shifts, rounding, RoPE, quantisation, products and sums, so the results are equal.
+// hd <= 128 (a multiple of 64); caches of at most KP NT / 8 positions; hd / (2 DS) a power of two of at most 64.
+template <int VPF, int NT, int KP, int DS, int HB>
+__global__ __launch_bounds__(NT) void k_attention_gqa(const int64_t* __restrict__ t, const int32_t* __restrict__ s,
+                                                      const int64_t* __restrict__ b, const int64_t* __restrict__ cos_t,
+                                                      const int64_t* __restrict__ sin_t, const int32_t* __restrict__ slot,
+                                                      const int32_t* __restrict__ pos, int16_t* __restrict__ kq,
+                                                      int32_t* __restrict__ sk, int64_t* __restrict__ v,
+                                                      const int32_t* __restrict__ expt, int64_t* __restrict__ out,
+                                                      int32_t* __restrict__ obits, int H, int KV, int hd, int Smax, int INV,
+                                                      int obn) {
+  constexpr int NW = NT / 64;
+  extern __shared__ int64_t sc[];   // HB x Smax scores, then exponentials, then probabilities
+  __shared__ int64_t y[HB + 2][128];   // the group's query heads, the new key, the new value: shr(t, 28 - s) + b
+  __shared__ int32_t kn[128];
+  __shared__ __attribute__((aligned(16))) int16_t qs16[HB][128];
+  __shared__ int32_t shq[HB + 1];
+  __shared__ int64_t red[NW][HB], red2[NW][HB];
+  __shared__ int64_t part[NW][HB][128 / DS];
+  __shared__ int bl[HB][128 / DS];
+  const int r = blockIdx.x, kh = blockIdx.y, ds = DS > 1 ? (int)blockIdx.z : 0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h0 = kh * HB;
+  const int N = (H + 2 * KV) * hd;
+  const int p = pos[r], sl = slot[r];
+  const int hds = hd / DS;
+  if (p < 0 || p >= Smax) {   // the host keeps positions inside the cache; write nothing there
+    for (int i = tid; i < HB * hds; i += NT) out[((int64_t)r * H + h0 + i / hds) * hd + ds * hds + i % hds] = 0;
+    if (obits && tid < HB * (obn / DS))
+      obits[((int64_t)r * H + h0 + tid / (obn / DS)) * obn + ds * (obn / DS) + tid % (obn / DS)] = 0;
+    return;
+  }
+  const int64_t cbase = ((int64_t)sl * KV + kh) * Smax;
+  const int npair = hds >> 1, nparts = NT / npair;
+  const int dp = ds * npair + tid % npair, pp = tid / npair;
+  // keys: thread (kg = tid / 8, kl = tid % 8) holds dims [kl hd / 8, (kl + 1) hd / 8) of keys kg, kg + NT / 8, ...
+  v4i ks8[KP][2];
+  int sks8[KP];
+  const int kg = tid >> 3, kl = tid & 7, nv = hd >> 6;
+#pragma unroll
+  for (int ps = 0; ps < KP; ++ps) {
+    sks8[ps] = 0;
+    const int si = kg + ps * (NT / 8);
+    if (si < p) {
+      const v4i* kr = reinterpret_cast<const v4i*>(kq + (cbase + si) * hd + kl * (hd >> 3));
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        if (c < nv) ks8[ps][c] = kr[c];
+      sks8[ps] = sk[cbase + si];
+    }
+  }
+  v4i vpre[VPF];
+  const int64_t* vb = v + cbase * hd + 2 * dp;
+#pragma unroll
+  for (int i = 0; i < VPF; ++i) {
+    const int si = pp + i * nparts;
+    if (si < p) vpre[i] = *reinterpret_cast<const v4i*>(vb + (int64_t)si * hd);
+  }
+  int64_t cs[2][2];
+  if (wave <= HB) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = lane + 64 * i;
+      cs[i][0] = j < hd ? cos_t[(int64_t)p * hd + j] : 0;
+      cs[i][1] = j < hd ? sin_t[(int64_t)p * hd + j] : 0;
+    }
+  }
+  constexpr int TV = ((HB + 2) * 128 + NT - 1) / NT;
+  int64_t tv[TV], bv[TV];
+#pragma unroll
+  for (int i = 0; i < TV; ++i) {
+    const int j = tid + i * NT;
+    tv[i] = bv[i] = 0;
+    if (j < (HB + 2) * hd) {
+      const int which = j / hd, jj = j - which * hd;
+      const int base = which < HB ? (h0 + which) * hd : (which == HB ? (H + kh) * hd : (H + KV + kh) * hd);
+      tv[i] = t[(int64_t)r * N + base + jj];
+      if (b) bv[i] = b[base + jj];
+    }
+  }
+  const int sh = 28 - s[r];
+#pragma unroll
+  for (int i = 0; i < TV; ++i) {
+    const int j = tid + i * NT;
+    if (j < (HB + 2) * hd) {
+      const int which = j / hd, jj = j - which * hd;
+      y[which][jj] = shr64(tv[i], sh) + bv[i];
+    }
+  }
+  __syncthreads();
+  if (wave <= HB) {   // waves 0 .. HB - 1: RoPE + qrow of the query heads, wave HB: of the new key
+    const int half = hd >> 1;
+    const int64_t* yy = y[wave];
+    int64_t z[2];
+    int64_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = lane + 64 * i;
+      z[i] = 0;
+      if (j < hd) {
+        const int64_t rot = j < half ? -yy[j + half] : yy[j - half];
+        z[i] = shr64(yy[j] * cs[i][0] + rot * cs[i][1], EXACT_F);
+        const int64_t a = abs64(z[i]);
+        m = a > m ? a : m;
+      }
+    }
+    m = wave_max64(m);
+    int q = bitlen64(m) - 15;
+    if (q < 0) q = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = lane + 64 * i;
+      if (j < hd) {
+        const int64_t w = shr64(z[i], q);
+        const int32_t wc = (int32_t)(w > 32767 ? 32767 : (w < -32767 ? -32767 : w));
+        if (wave < HB) qs16[wave][j] = (int16_t)wc;
+        else kn[j] = wc;
+      }
+    }
+    if (lane == 0) shq[wave] = q;
+  }
+  __syncthreads();
+  const int skn = shq[HB];
+  if (ds == 0) {   // one block per (row, KV head) writes the new position
+    for (int j = tid; j < hd; j += NT) {
+      kq[(cbase + p) * hd + j] = (int16_t)kn[j];
+      v[(cbase + p) * hd + j] = y[HB + 1][j];
+    }
+    if (tid == 0) sk[cbase + p] = skn;
+  }
+  const int S = p + 1;
+  int64_t mx[HB];
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) mx[hb] = INT64_MIN;
+#pragma unroll
+  for (int ps = 0; ps < KP; ++ps) {
+    const int si = kg + ps * (NT / 8);
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      int64_t dot = 0;
+      if (si < p) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          if (c < nv) {
+            const v4i kk = ks8[ps][c], qq = reinterpret_cast<const v4i*>(qs16[hb] + kl * (hd >> 3))[c];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dot += (int64_t)dot2(qq[e], kk[e]);
+          }
+        }
+      }
+      dot += dpp64<0xB1>(dot);
+      dot += dpp64<0x4E>(dot);
+      dot += dpp64<0x141>(dot);
+      if (si < p) {
+        const int64_t val = shr64(dot * INV, 32 - shq[hb] - sks8[ps]);
+        if (kl == 0) sc[hb * Smax + si] = val;
+        mx[hb] = val > mx[hb] ? val : mx[hb];
+      }
+    }
+  }
+  if (wave == (int)(p % NT) >> 6) {   // the new key, from LDS: the wave of thread p % NT, lanes over dims
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      int64_t psum = 0;
+      for (int j = lane; j < hd; j += 64) psum += (int64_t)qs16[hb][j] * kn[j];
+      const int64_t dot = wave_sum64(psum);
+      if (tid == (int)(p % NT)) {   // that thread owns sc[hb][p] in the loops below
+        const int64_t val = shr64(dot * INV, 32 - shq[hb] - skn);
+        sc[hb * Smax + p] = val;
+        mx[hb] = val > mx[hb] ? val : mx[hb];
+      }
+    }
+  }
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    const int64_t m = wave_max64(mx[hb]);
+    if (lane == 0) red[wave][hb] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    int64_t m = red[0][hb];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) m = red[w][hb] > m ? red[w][hb] : m;
+    mx[hb] = m;
+  }
+  int64_t es[HB];
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) es[hb] = 0;
+  for (int si = tid; si < S; si += NT) {
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      const int64_t e = lut_exp(expt, mx[hb] - sc[hb * Smax + si]);
+      sc[hb * Smax + si] = e;
+      es[hb] += e;
+    }
+  }
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    const int64_t e = wave_sum64(es[hb]);
+    if (lane == 0) red2[wave][hb] = e;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    uint64_t e = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) e += (uint64_t)red2[w][hb];
+    es[hb] = (int64_t)e;
+  }
+  for (int si = tid; si < S; si += NT) {
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      const double res = 1.0 / (double)es[hb];   // one reciprocal per head; each quotient estimate is corrected exactly
+      sc[hb * Smax + si] = floordiv_rcp(shl64(sc[hb * Smax + si], 20), es[hb], res);
+    }
+  }
+  __syncthreads();
+  int64_t a0[HB], a1[HB];
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) a0[hb] = a1[hb] = 0;
+  auto madd = [&](const v4i vv, int si) {
+    const int64_t lo = ((int64_t)vv[1] << 32) | (uint32_t)vv[0], hi = ((int64_t)vv[3] << 32) | (uint32_t)vv[2];
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      const int64_t pr = sc[hb * Smax + si];
+      a0[hb] = (int64_t)((uint64_t)a0[hb] + (uint64_t)(pr * lo));
+      a1[hb] = (int64_t)((uint64_t)a1[hb] + (uint64_t)(pr * hi));
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < VPF; ++i) {
+    const int si = pp + i * nparts;
+    if (si < p) madd(vpre[i], si);
+  }
+  for (int si = pp + VPF * nparts; si < p; si += nparts) madd(*reinterpret_cast<const v4i*>(vb + (int64_t)si * hd), si);
+  if (pp == p % nparts) {   // the new value, from LDS
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      const int64_t pr = sc[hb * Smax + p];
+      a0[hb] = (int64_t)((uint64_t)a0[hb] + (uint64_t)(pr * y[HB + 1][2 * dp]));
+      a1[hb] = (int64_t)((uint64_t)a1[hb] + (uint64_t)(pr * y[HB + 1][2 * dp + 1]));
+    }
+  }
+  // lanes l, l ^ npair, ... of a wave hold the same pair: fold them (sums modulo 2^64), then the waves
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb) {
+    for (int o = npair; o < 64; o <<= 1) {
+      a0[hb] = (int64_t)((uint64_t)a0[hb] + (uint64_t)__shfl_xor((long long)a0[hb], o));
+      a1[hb] = (int64_t)((uint64_t)a1[hb] + (uint64_t)__shfl_xor((long long)a1[hb], o));
+    }
+    if (lane < npair) {
+      part[wave][hb][2 * lane] = a0[hb];
+      part[wave][hb][2 * lane + 1] = a1[hb];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < HB * hds; i += NT) {
+    const int hb = i / hds, dl = i - hb * hds;
+    uint64_t tot = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tot += (uint64_t)part[w][hb][dl];
+    const int64_t o = shr64((int64_t)tot, 20);
+    out[((int64_t)r * H + h0 + hb) * hd + ds * hds + dl] = o;
+    bl[hb][dl] = bitlen64(abs64(o));
+  }
+  if (obits) {
+    __syncthreads();
+    if (tid < HB) {
+      int m = 0;
+      for (int dl = 0; dl < hds; ++dl) m = bl[tid][dl] > m ? bl[tid][dl] : m;
+      for (int i = 0; i < obn / DS; ++i) obits[((int64_t)r * H + h0 + tid) * obn + ds * (obn / DS) + i] = m;
+    }
+  }
+}
+
 }  // namespace exact
 
 using namespace exact;
@@ -615,6 +905,38 @@ static void att_qkv_go(int R, int H, size_t lds, hipStream_t st, const int64_t* 
   }
   hipLaunchKernelGGL((k_attention_qkv<VPF, NT, KPF, KS, KP, DS, GT>), dim3(R, H, DS), dim3(NT), lds, st, t, s, b, cos_t, sin_t,
                      slot, pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV, obn);
+}
+
+// one k_attention_gqa launch: dimension slices ds (4, 2 or 1) of the (row, KV head) blocks
+template <int DS, int HB>
+static void att_gqa_go1(int R, int H, size_t, hipStream_t st, const int64_t* t, const int32_t* s, const int64_t* b,
+                        const int64_t* cos_t, const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* kq,
+                        int32_t* sk, int64_t* v, const int32_t* exp_t, int64_t* out, int32_t* obits, int KV, int hd, int Smax,
+                        int INV, int obn) {
+  constexpr int NT = ATT_GQA_NT, KP = 2048 / NT;       // 256 cached positions in KP passes of NT / 8 keys
+  constexpr int NP = NT * 2 * DS / 128;                 // threads per value pair at hd 128
+  constexpr int VPF = (256 + NP - 1) / NP < 16 ? (256 + NP - 1) / NP : 16;
+  static bool attr_set = false;
+  const size_t lds = (size_t)HB * Smax * 8;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k_attention_gqa<VPF, NT, KP, DS, HB>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 8 * 256 * 8);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_attention_gqa<VPF, NT, KP, DS, HB>), dim3(R, KV, DS), dim3(NT), lds, st, t, s, b, cos_t, sin_t, slot,
+                     pos, kq, sk, v, exp_t, out, obits, H, KV, hd, Smax, INV, obn);
+}
+template <int HB>
+static void att_gqa_go(int ds, int R, int H, size_t lds, hipStream_t st, const int64_t* t, const int32_t* s, const int64_t* b,
+                       const int64_t* cos_t, const int64_t* sin_t, const int32_t* slot, const int32_t* pos, int16_t* kq,
+                       int32_t* sk, int64_t* v, const int32_t* exp_t, int64_t* out, int32_t* obits, int KV, int hd, int Smax,
+                       int INV, int obn) {
+  if (ds == 4)
+    att_gqa_go1<4, HB>(R, H, lds, st, t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, KV, hd, Smax, INV, obn);
+  else if (ds == 2)
+    att_gqa_go1<2, HB>(R, H, lds, st, t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, KV, hd, Smax, INV, obn);
+  else
+    att_gqa_go1<1, HB>(R, H, lds, st, t, s, b, cos_t, sin_t, slot, pos, kq, sk, v, exp_t, out, obits, KV, hd, Smax, INV, obn);
 }
 
 // blocks per (row, head) for the short-cache paths: the largest power of two up to ATT_DS that divides obn, keeps
@@ -657,7 +979,18 @@ extern "C" int exact_attention_qkv_split(const int64_t* t, const int32_t* s, con
   const bool ks8_mr = ATT_KS8 && ATT_KS8_MR && blocks > ATT_WIDE_BLOCKS && hd % 64 == 0 && hd <= 128 &&
                       Smax <= 4 * (ATT_THREADS / 8);
   const int ds = ks8_wide || ks8_wide4 || (ks8_narrow && hd < ATT_KS8_WIDE_HD) ? att_qkv_ds(obn, blocks, hd) : 1;
-  if (ks8_mr) {
+  // ... and, for query groups of 4, 5, 7 or 8 heads over caches of at most 256 positions, one block per (row, KV
+  // head, dimension slice) for the whole group
+  const int grp = H / KV;
+  const bool gqa = ATT_GQA && blocks > ATT_WIDE_BLOCKS && hd % 64 == 0 && hd <= 128 && Smax > ATT_GQA_MIN_S && Smax <= 256 &&
+                   (grp == 4 || grp == 5 || grp == 7 || grp == 8);
+  if (gqa) {
+    const int gds = att_qkv_ds(obn, (int64_t)R * KV, hd);
+    if (grp == 4) att_gqa_go<4>(gds, ATT_QKV_ARGS);
+    else if (grp == 5) att_gqa_go<5>(gds, ATT_QKV_ARGS);
+    else if (grp == 7) att_gqa_go<7>(gds, ATT_QKV_ARGS);
+    else att_gqa_go<8>(gds, ATT_QKV_ARGS);
+  } else if (ks8_mr) {
     if (Smax <= 2 * (ATT_THREADS / 8))
       att_qkv_go<ATT_MR_VPF, ATT_THREADS, ATT_KPF, 8, 2, 1, ATT_MR_GT != 0>(ATT_QKV_ARGS);
     else
