@@ -190,16 +190,24 @@ __device__ __forceinline__ void compute_group(const GroupRegs& G_, int64_t (&acc
 #define GEMV_SCHED_FENCE 1
 #endif
 // pro: run after the first group's weight tile is in flight and before its activations are read (the
-// quantising GEMV fills its LDS slice there).
+// quantising GEMV fills its LDS slice there). pre: issues the prologue's own global loads before that tile's, so
+// that their first use waits for them alone (loads complete in issue order: issued after the tile, they made the
+// prologue wait for the tile's HBM latency first). The first tile is loaded without a branch (a wave without groups
+// loads a valid one and never uses it): a branch around it would make the wait counts after the join assume the
+// path without it.
+#ifndef GEMV_PRE_FIRST
+#define GEMV_PRE_FIRST 1
+#endif
 struct NoPrologue {
   __device__ void operator()() const {}
 };
 
-template <int ABITS, bool NT, int VR, typename Pro = NoPrologue, bool CT = false, bool WIDE = false>
+template <int ABITS, bool NT, int VR, typename Pro = NoPrologue, bool CT = false, bool WIDE = false,
+          typename Pre = NoPrologue>
 __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t* __restrict__ wp,
                                             const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
                                             const int8_t* xrow, bool valid, int R, int nb, int nbs, int G,
-                                            int g0, int g1, int row, int c, int lane, Pro pro = Pro()) {
+                                            int g0, int g1, int row, int c, int lane, Pro pro = Pro(), Pre pre = Pre()) {
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -209,9 +217,19 @@ __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t*
     if (g0 >= g1) return;
     load_group<ABITS, NT, WIDE>(ra, wp, mp, mh, xrow, valid, tile_index(nb, g0, nbs, G), g0, row, c);
   } else {   // the first tile in flight while the prologue runs (one call site: the prologue may be long)
-    if (g0 < g1) {
-      load_scales<WIDE>(ra, mp, mh, tile_index(nb, g0, nbs, G), row);
-      load_tile<NT>(ra, wp, tile_index(nb, g0, nbs, G), row, c);
+    if (GEMV_PRE_FIRST) {
+      pre();
+      __builtin_amdgcn_sched_barrier(0);
+      const int gl = g0 < G ? g0 : G - 1;
+      load_scales<WIDE>(ra, mp, mh, tile_index(nb, gl, nbs, G), row);
+      load_tile<NT>(ra, wp, tile_index(nb, gl, nbs, G), row, c);
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      if (g0 < g1) {
+        load_scales<WIDE>(ra, mp, mh, tile_index(nb, g0, nbs, G), row);
+        load_tile<NT>(ra, wp, tile_index(nb, g0, nbs, G), row, c);
+      }
+      pre();
     }
     pro();
     if (g0 >= g1) return;
@@ -307,33 +325,42 @@ __device__ __forceinline__ void g128_xq_body(const int64_t* __restrict__ xs, int
   const int ncol = (g1 - g0) * 128;
   const int rowb = gmax * 128 * EB;                       // LDS bytes per row of a wave's slice
   int8_t* mine = xlds + (size_t)wave * R * rowb;
-  // quantise this wave's columns of every row: the row's slice bit lengths and its values are loaded together
-  auto quantise = [&]() {
+  // quantise this wave's columns of every row: the row's slice bit lengths and its values are loaded together (row 0's
+  // before the first weight tile)
+  int pw[PL];   // up to 64 PL slice bit lengths, all loads issued before the first use
+  int64_t xv[XQ_LOADS];
+  auto ldrow = [&](int r) {
+#pragma unroll
+    for (int k = 0; k < PL; ++k) pw[k] = lane + 64 * k < nparts ? part[(int64_t)r * nparts + lane + 64 * k] : 0;
+    const int64_t* src = xs + (int64_t)r * ldx + (int64_t)g0 * 128;
+#pragma unroll
+    for (int j = 0; j < XQ_LOADS; ++j) xv[j] = lane + 64 * j < ncol ? src[lane + 64 * j] : 0;
+  };
+  auto qrow = [&](int r) {
     const int64_t lim = (1LL << ABITS) - 1;
-    for (int r = 0; r < R; ++r) {
-      int pw[PL];   // up to 64 PL slice bit lengths, all loads issued before the first use
+    int pv = pw[0];
 #pragma unroll
-      for (int k = 0; k < PL; ++k) pw[k] = lane + 64 * k < nparts ? part[(int64_t)r * nparts + lane + 64 * k] : 0;
-      const int64_t* src = xs + (int64_t)r * ldx + (int64_t)g0 * 128;
-      int64_t xv[XQ_LOADS];
+    for (int k = 1; k < PL; ++k) pv = pw[k] > pv ? pw[k] : pv;
+    const int m = wave_max_i32(pv);
+    const int sh = m - ABITS > 0 ? m - ABITS : 0;
+    if (bid == 0 && wave == 0 && lane == 0) s_out[r] = sh;
 #pragma unroll
-      for (int j = 0; j < XQ_LOADS; ++j) xv[j] = lane + 64 * j < ncol ? src[lane + 64 * j] : 0;
-      int pv = pw[0];
-#pragma unroll
-      for (int k = 1; k < PL; ++k) pv = pw[k] > pv ? pw[k] : pv;
-      const int m = wave_max_i32(pv);
-      const int sh = m - ABITS > 0 ? m - ABITS : 0;
-      if (bid == 0 && wave == 0 && lane == 0) s_out[r] = sh;
-#pragma unroll
-      for (int j = 0; j < XQ_LOADS; ++j) {
-        const int i = lane + 64 * j;
-        if (i < ncol) {
-          int64_t q = shr64(xv[j], sh);
-          q = q > lim ? lim : (q < -lim ? -lim : q);
-          if (ABITS == 15) reinterpret_cast<int16_t*>(mine + (size_t)r * rowb)[i] = (int16_t)q;
-          else mine[(size_t)r * rowb + i] = (int8_t)q;
-        }
+    for (int j = 0; j < XQ_LOADS; ++j) {
+      const int i = lane + 64 * j;
+      if (i < ncol) {
+        int64_t q = shr64(xv[j], sh);
+        q = q > lim ? lim : (q < -lim ? -lim : q);
+        if (ABITS == 15) reinterpret_cast<int16_t*>(mine + (size_t)r * rowb)[i] = (int16_t)q;
+        else mine[(size_t)r * rowb + i] = (int8_t)q;
       }
+    }
+  };
+  auto first = [&]() { ldrow(0); };   // R >= 1 (the host entries refuse R <= 0)
+  auto quantise = [&]() {
+    qrow(0);
+    for (int r = 1; r < R; ++r) {
+      ldrow(r);
+      qrow(r);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done (wave-private region)
     __builtin_amdgcn_wave_barrier();
@@ -342,8 +369,8 @@ __device__ __forceinline__ void g128_xq_body(const int64_t* __restrict__ xs, int
   // group g's columns sit at (g - g0) * 128 of the slice: offset the row base back by g0 * 128 elements
   const int8_t* xrow = mine + (size_t)(row < R ? row : 0) * rowb - (ptrdiff_t)g0 * 128 * EB;
   int64_t acc[4][VR];
-  gemv_groups<ABITS, NT, VR, decltype(quantise), false, WIDE>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c,
-                                                              lane, quantise);
+  gemv_groups<ABITS, NT, VR, decltype(quantise), false, WIDE, decltype(first)>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G,
+                                                                              g0, g1, row, c, lane, quantise, first);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int n = nb * 64 + 16 * q + row;
@@ -441,11 +468,25 @@ __device__ __forceinline__ void gu_swiglu_body(const int16_t* __restrict__ x, co
       load_gu_group<NT, WIDE>(G_, wp, mp, mh, xrow, tile_index(nb, g, nbs, G), tile_index(ub + nb, g, nbs, G), qb, g, row, c);
     };
     if constexpr (NE > 0) {   // the first tiles in flight while the block normalises the rows (every wave takes part)
-      if (g0 < g1)
+      // (row 0's norm inputs are loaded first, as gemv_groups' pre)
+      int16_t* xl = reinterpret_cast<int16_t*>(xlds);
+      int r0 = 0;
+      if (GEMV_PRE_FIRST) {
+        NormIn<NE> in0;
+        norm_load<NE>(in0, 0, blockDim.x, x_in, res_t, res_s, gain, K);
+        __builtin_amdgcn_sched_barrier(0);
+        const int gl = g0 < G ? g0 : G - 1;
+        load_gu_group<NT, WIDE, false>(ra, wp, mp, mh, xrow, tile_index(nb, gl, nbs, G), tile_index(ub + nb, gl, nbs, G), qb,
+                                       gl, row, c);
+        __builtin_amdgcn_sched_barrier(0);
+        norm_qrow_in<NE>(in0, 0, blockDim.x, res_t, 15, K, xl, bid == 0 ? x_out : nullptr, nullptr, s_lds, nullptr, nullptr,
+                         nsc);
+        r0 = 1;
+      } else if (g0 < g1) {
         load_gu_group<NT, WIDE, false>(ra, wp, mp, mh, xrow, tile_index(nb, g0, nbs, G), tile_index(ub + nb, g0, nbs, G), qb,
                                        g0, row, c);
-      int16_t* xl = reinterpret_cast<int16_t*>(xlds);
-      for (int r = 0; r < R; ++r)
+      }
+      for (int r = r0; r < R; ++r)
         norm_qrow_row<NE>(r, blockDim.x, x_in, res_t, res_s, gain, 15, K, xl + (size_t)r * K, bid == 0 ? x_out : nullptr,
                           nullptr, s_lds, nullptr, nullptr, nsc);
       __syncthreads();
@@ -565,8 +606,12 @@ __global__ __launch_bounds__(64 * BW) void k_gemv_g128_norm(const int64_t* __res
   const int nbs = (N + 63) >> 6;
   const bool writer = blockIdx.x == 0;
   int16_t* xl = reinterpret_cast<int16_t*>(xlds);
+  NormIn<EPT> in0;   // row 0's inputs, loaded before the first weight tile
+  auto first = [&]() { norm_load<EPT>(in0, 0, 64 * BW, x_in, res_t, res_s, gain, K); };
   auto norm = [&]() {   // block-wide: every wave of the block runs it, with or without a task
-    for (int r = 0; r < R; ++r)
+    norm_qrow_in<EPT>(in0, 0, 64 * BW, res_t, 15, K, xl, writer ? x_out : nullptr, nullptr, writer ? s_out : nullptr,
+                      writer ? xq_out : nullptr, nullptr, sc);
+    for (int r = 1; r < R; ++r)
       norm_qrow_row<EPT>(r, 64 * BW, x_in, res_t, res_s, gain, 15, K, xl + (size_t)r * K, writer ? x_out : nullptr, nullptr,
                          writer ? s_out : nullptr, writer ? xq_out : nullptr, nullptr, sc);
     __syncthreads();
@@ -579,8 +624,8 @@ __global__ __launch_bounds__(64 * BW) void k_gemv_g128_norm(const int64_t* __res
   const int row = lane & 15, c = lane >> 4;
   const int8_t* xrow = reinterpret_cast<const int8_t*>(xl + (size_t)(row < R ? row : 0) * K);
   int64_t acc[4][VR];
-  gemv_groups<15, NT, VR, decltype(norm), false, WIDE>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane,
-                                                       norm);
+  gemv_groups<15, NT, VR, decltype(norm), false, WIDE, decltype(first)>(acc, wp, mp, mh, xrow, row < R, R, nb, nbs, G, g0, g1,
+                                                                        row, c, lane, norm, first);
   if (!has) return;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -780,32 +825,43 @@ __device__ __forceinline__ void experts_xq_body(const int64_t* __restrict__ xs, 
   const int ncol = (g1 - g0) * 128;
   const int rowb = gmax * 128 * 2;
   int8_t* mine = xlds + (size_t)wave * VR * rowb;
-  auto quantise = [&]() {
+  int pw[PL];
+  int64_t xv[XQ_LOADS];
+  auto ldrow = [&](int r) {
+    const int p = p0 + r;
+#pragma unroll
+    for (int k = 0; k < PL; ++k) pw[k] = lane + 64 * k < nparts ? part[(int64_t)p * nparts + lane + 64 * k] : 0;
+    const int64_t* src = xs + (int64_t)p * ldx + (int64_t)g0 * 128;
+#pragma unroll
+    for (int j = 0; j < XQ_LOADS; ++j) xv[j] = lane + 64 * j < ncol ? src[lane + 64 * j] : 0;
+  };
+  auto qrow = [&](int r) {
     const int64_t lim = (1LL << 15) - 1;
-    for (int r = 0; r < R; ++r) {
-      const int p = p0 + r;
-      int pw[PL];
+    const int p = p0 + r;
+    int pv = pw[0];
 #pragma unroll
-      for (int k = 0; k < PL; ++k) pw[k] = lane + 64 * k < nparts ? part[(int64_t)p * nparts + lane + 64 * k] : 0;
-      const int64_t* src = xs + (int64_t)p * ldx + (int64_t)g0 * 128;
-      int64_t xv[XQ_LOADS];
+    for (int k = 1; k < PL; ++k) pv = pw[k] > pv ? pw[k] : pv;
+    const int m = wave_max_i32(pv);
+    const int sh = m - 15 > 0 ? m - 15 : 0;
+    if (nb == 0 && sp == 0 && lane == 0) s_out[p] = sh;
 #pragma unroll
-      for (int j = 0; j < XQ_LOADS; ++j) xv[j] = lane + 64 * j < ncol ? src[lane + 64 * j] : 0;
-      int pv = pw[0];
-#pragma unroll
-      for (int k = 1; k < PL; ++k) pv = pw[k] > pv ? pw[k] : pv;
-      const int m = wave_max_i32(pv);
-      const int sh = m - 15 > 0 ? m - 15 : 0;
-      if (nb == 0 && sp == 0 && lane == 0) s_out[p] = sh;
-#pragma unroll
-      for (int j = 0; j < XQ_LOADS; ++j) {
-        const int i = lane + 64 * j;
-        if (i < ncol) {
-          int64_t q = shr64(xv[j], sh);
-          q = q > lim ? lim : (q < -lim ? -lim : q);
-          reinterpret_cast<int16_t*>(mine + (size_t)r * rowb)[i] = (int16_t)q;
-        }
+    for (int j = 0; j < XQ_LOADS; ++j) {
+      const int i = lane + 64 * j;
+      if (i < ncol) {
+        int64_t q = shr64(xv[j], sh);
+        q = q > lim ? lim : (q < -lim ? -lim : q);
+        reinterpret_cast<int16_t*>(mine + (size_t)r * rowb)[i] = (int16_t)q;
       }
+    }
+  };
+  auto first = [&]() {   // row 0's loads ahead of the first weight tile
+    if (R > 0) ldrow(0);
+  };
+  auto quantise = [&]() {
+    if (R > 0) qrow(0);
+    for (int r = 1; r < R; ++r) {
+      ldrow(r);
+      qrow(r);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done (wave-private region)
     __builtin_amdgcn_wave_barrier();
@@ -813,8 +869,10 @@ __device__ __forceinline__ void experts_xq_body(const int64_t* __restrict__ xs, 
   const int row = lane & 15, c = lane >> 4;
   const int8_t* xrow = mine + (size_t)(row < R ? row : 0) * rowb - (ptrdiff_t)g0 * 128 * 2;
   int64_t acc[4][VR];
-  gemv_groups<15, NT, VR, decltype(quantise), false, false>(acc, wp + (size_t)e * w_stride, mp + (size_t)e * m_stride, nullptr,
-                                                            xrow, row < R, R, nb, nbs, G, g0, g1, row, c, lane, quantise);
+  gemv_groups<15, NT, VR, decltype(quantise), false, false, decltype(first)>(acc, wp + (size_t)e * w_stride,
+                                                                             mp + (size_t)e * m_stride, nullptr, xrow, row < R,
+                                                                             R, nb, nbs, G, g0, g1, row, c, lane, quantise,
+                                                                             first);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int n = nb * 64 + 16 * q + row;

@@ -63,27 +63,43 @@ __device__ __forceinline__ int bitlen_maxabs(int64_t vmax, int64_t vmin) {
 //   den is outside (0, 2^62]);
 //   the shifts k, 16, 28 - res_s and the qrow shift are uniform over the block, so their branches are too; loads
 //   use clamped indices and mask the values past D, so only the stores are guarded.
+// The global loads of one row's pass (x_in, res_t and the gains, clamped indices), kept apart so that a consumer GEMV
+// can issue them before its first weight tile: the pass's first use then waits for these loads only.
 template <int EPT>
-__device__ __forceinline__ void norm_qrow_row(int r, int nt, const int64_t* x_in, const int64_t* res_t,
-                                              const int32_t* __restrict__ res_s, const int64_t* __restrict__ g, int bits,
-                                              int D, int16_t* xl, int64_t* x_out, int64_t* clear, int32_t* __restrict__ s_out,
-                                              void* xq_out, int8_t* x8, RowScratch& sc) {
+struct NormIn {
+  int64_t v[EPT], gv[EPT], rv[EPT];
+  int rs;   // res_s[r] when res_t is given
+};
+
+template <int EPT>
+__device__ __forceinline__ void norm_load(NormIn<EPT>& in, int r, int nt, const int64_t* x_in, const int64_t* res_t,
+                                          const int32_t* __restrict__ res_s, const int64_t* __restrict__ g, int D) {
   const int tid = threadIdx.x;
-  const double rD = rcp_f64((double)D);   // off the critical path: ready before the sum of squares
   const int64_t* xr = x_in + (int64_t)r * D;
   const int64_t* tr = res_t ? res_t + (int64_t)r * D : nullptr;
-  int64_t v[EPT], gv[EPT];
-  {
-    int64_t rv[EPT];
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) {
-      const int i = tid + j * nt < D ? tid + j * nt : D - 1;
-      v[j] = xr[i];
-      gv[j] = g[i];
-      rv[j] = tr ? tr[i] : 0;
-    }
-    if (tr) {
-      const int sh = 28 - res_s[r];
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tid + j * nt < D ? tid + j * nt : D - 1;
+    in.v[j] = xr[i];
+    in.gv[j] = g[i];
+    in.rv[j] = tr ? tr[i] : 0;
+  }
+  in.rs = tr ? res_s[r] : 0;
+}
+
+template <int EPT>
+__device__ __forceinline__ void norm_qrow_in(NormIn<EPT>& in, int r, int nt, const int64_t* res_t, int bits, int D,
+                                             int16_t* xl,
+                                             int64_t* x_out, int64_t* clear, int32_t* __restrict__ s_out, void* xq_out,
+                                             int8_t* x8, RowScratch& sc) {
+  const int tid = threadIdx.x;
+  const double rD = rcp_f64((double)D);   // off the critical path: ready before the sum of squares
+  int64_t (&v)[EPT] = in.v;
+  int64_t (&gv)[EPT] = in.gv;
+  {
+    const int64_t (&rv)[EPT] = in.rv;
+    if (res_t) {
+      const int sh = 28 - in.rs;
       if (sh > 0) {
 #pragma unroll
         for (int j = 0; j < EPT; ++j) v[j] = (int64_t)((uint64_t)v[j] + (uint64_t)rsh_pos(rv[j], sh));
@@ -94,9 +110,9 @@ __device__ __forceinline__ void norm_qrow_row(int r, int nt, const int64_t* x_in
     }
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
-      const bool in = tid + j * nt < D;
-      v[j] = in ? v[j] : 0;
-      gv[j] = in ? gv[j] : 0;
+      const bool inside = tid + j * nt < D;
+      v[j] = inside ? v[j] : 0;
+      gv[j] = inside ? gv[j] : 0;
     }
   }
   if (x_out || clear) {
@@ -208,6 +224,16 @@ __device__ __forceinline__ void norm_qrow_row(int r, int nt, const int64_t* x_in
     }
   }
   if (tid == 0 && s_out) s_out[r] = q;
+}
+
+template <int EPT>
+__device__ __forceinline__ void norm_qrow_row(int r, int nt, const int64_t* x_in, const int64_t* res_t,
+                                              const int32_t* __restrict__ res_s, const int64_t* __restrict__ g, int bits,
+                                              int D, int16_t* xl, int64_t* x_out, int64_t* clear, int32_t* __restrict__ s_out,
+                                              void* xq_out, int8_t* x8, RowScratch& sc) {
+  NormIn<EPT> in;
+  norm_load<EPT>(in, r, nt, x_in, res_t, res_s, g, D);
+  norm_qrow_in<EPT>(in, r, nt, res_t, bits, D, xl, x_out, clear, s_out, xq_out, x8, sc);
 }
 
 }  // namespace exact
