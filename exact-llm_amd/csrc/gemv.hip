@@ -383,7 +383,9 @@ __device__ __forceinline__ void g128_xq_body(const int64_t* __restrict__ xs, int
 }
 
 template <int ABITS, bool NT, int VR, bool WIDE, int PL>
-__global__ __launch_bounds__(256) void k_gemv_g128_xq(const int64_t* __restrict__ xs, int64_t ldx,
+// one row (VR = 1): 3 waves a SIMD (at most 168 registers), which the row 0 loads ahead of the first tile had cost
+// (down 3584 x 18944 at 2 waves: 14.9 -> 16.3 us)
+__global__ __launch_bounds__(256, VR == 1 ? 3 : 1) void k_gemv_g128_xq(const int64_t* __restrict__ xs, int64_t ldx,
                                                       const int32_t* __restrict__ part, int nparts,
                                                       const int8_t* __restrict__ wp, const int16_t* __restrict__ mp,
                                                       const int16_t* __restrict__ mh, int64_t* __restrict__ t,
