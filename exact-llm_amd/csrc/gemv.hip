@@ -259,7 +259,8 @@ __device__ __forceinline__ void gemv_groups(int64_t (&acc)[4][VR], const int8_t*
 // CT (int16 rows): colterm[n] = sum_g colsum_g M_g given, 128 colterm added by the first split of each row block,
 // so R may be 16.
 template <int ABITS, bool NT, int VR, int BW, bool CT = false, bool WIDE = false>
-__global__ __launch_bounds__(64 * BW) void k_gemv_g128(const void* __restrict__ xv, const int8_t* __restrict__ wp,
+// int16 rows, one row, 4-wave blocks (the lm_head): 3 waves a SIMD (at most 168 registers; 172 otherwise)
+__global__ __launch_bounds__(64 * BW, (ABITS == 15 && VR == 1 && BW == 4) ? 3 : 1) void k_gemv_g128(const void* __restrict__ xv, const int8_t* __restrict__ wp,
                                                        const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
                                                        int64_t* __restrict__ t, int R, int N, int K, int G, int nsplit,
                                                        int out_mode, const int64_t* __restrict__ colterm) {
