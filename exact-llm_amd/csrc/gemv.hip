@@ -595,8 +595,9 @@ __global__ __launch_bounds__(64 * NPB * KS) void k_gemv_gu_swiglu(const int16_t*
 // exact_rmsnorm_qrow launch + exact_gemv_g128_acc.
 // BW waves per block (4, or 8 for wide rows: one block per CU reads the row once, and the weight tiles of its 8
 // tasks load while it normalises)
+// (one row, 4-wave blocks, up to 8 values a thread: 3 waves a SIMD, at most 168 registers; 172 otherwise)
 template <bool NT, int VR, int EPT, bool WIDE, int BW = 4>
-__global__ __launch_bounds__(64 * BW) void k_gemv_g128_norm(const int64_t* __restrict__ x_in, int64_t* __restrict__ x_out,
+__global__ __launch_bounds__(64 * BW, (VR == 1 && BW == 4 && EPT <= 8) ? 3 : 1) void k_gemv_g128_norm(const int64_t* __restrict__ x_in, int64_t* __restrict__ x_out,
                                                         const int64_t* __restrict__ res_t, const int32_t* __restrict__ res_s,
                                                         const int64_t* __restrict__ gain, const int8_t* __restrict__ wp,
                                                         const int16_t* __restrict__ mp, const int16_t* __restrict__ mh,
