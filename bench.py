@@ -28,8 +28,8 @@ GATEUP_BYTES = 37888 * 3584 + 37888 * 28 * 2 + 3584 + 37888 * 8
 # 512 MiB device copy (profiles/gemv_gateup_7b_traffic.md): 137,998,602 read + 1,818,624 written
 GATEUP_TRAFFIC_BYTES = 139_822_021
 # HBM bytes of one 7B bs1 decode step (the headline's unit of work), measured the same way over the step's 146
-# launches (profiles/decode_7b_bs1_step.md): 7,284.0 MB read + 124.2 MB written
-STEP_TRAFFIC_BYTES = 7_408_200_000
+# launches (profiles/decode_7b_bs1_step.md): 7,284.5 MB read + 124.4 MB written
+STEP_TRAFFIC_BYTES = 7_408_900_000
 INT8_PEAK_TOPS = 5000.0
 
 
